@@ -1,0 +1,204 @@
+"""ctypes mirror of the argument structs declared in include/gs3d_hip.h.
+
+The field order and types must match the C header exactly; a CPU test
+compiles the header and compares every offset with the ones below.
+"""
+
+import ctypes
+
+c_float_p = ctypes.POINTER(ctypes.c_float)
+c_int32_p = ctypes.POINTER(ctypes.c_int32)
+
+ABI_VERSION = 1
+
+GS3D_OK = 0
+GS3D_ERR_ARGUMENT = -1
+GS3D_ERR_LAUNCH = -2
+GS3D_ERR_UNSUPPORTED = -3
+GS3D_ERR_SCRATCH = -4
+GS3D_ERR_OVERFLOW = -5
+
+STATUS_NAMES = {
+    GS3D_ERR_ARGUMENT: "invalid argument",
+    GS3D_ERR_LAUNCH: "kernel launch failed",
+    GS3D_ERR_UNSUPPORTED: "unsupported configuration",
+    GS3D_ERR_SCRATCH: "scratch buffer too small",
+    GS3D_ERR_OVERFLOW: "pair count exceeds int32 offsets",
+}
+
+_P = ctypes.c_void_p
+
+
+class ProjectArgs(ctypes.Structure):
+    _fields_ = [
+        ("n", ctypes.c_int32),
+        ("views", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("height", ctypes.c_int32),
+        ("near_plane", ctypes.c_float),
+        ("far_plane", ctypes.c_float),
+        ("radius_clip", ctypes.c_float),
+        ("means", _P),
+        ("quats", _P),
+        ("scales", _P),
+        ("opacities", _P),
+        ("view", _P),
+        ("projection", _P),
+        ("intrinsics", _P),
+        ("centers", _P),
+        ("conics", _P),
+        ("radii", _P),
+        ("tiles", _P),
+        ("depths", _P),
+        ("sh", _P),
+        ("sh_view_stride", ctypes.c_int64),
+        ("sh_rows", ctypes.c_int32),
+        ("sh_degree", ctypes.c_int32),
+        ("camera_centers", _P),
+        ("colors", _P),
+        ("means2d", _P),
+        ("meta_opacities", _P),
+        ("meta_conics", _P),
+    ]
+
+
+class ProjectBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("n", ctypes.c_int32),
+        ("views", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("height", ctypes.c_int32),
+        ("means", _P),
+        ("quats", _P),
+        ("scales", _P),
+        ("opacities", _P),
+        ("view", _P),
+        ("projection", _P),
+        ("intrinsics", _P),
+        ("radii", _P),
+        ("grad_centers", _P),
+        ("grad_centers_stride", ctypes.c_int64),
+        ("grad_conics", _P),
+        ("grad_conics_stride", ctypes.c_int64),
+        ("grad_means", _P),
+        ("grad_quats", _P),
+        ("grad_scales", _P),
+        ("grad_opacities", _P),
+        ("grad_view", _P),
+        ("grad_projection", _P),
+        ("sh", _P),
+        ("sh_view_stride", ctypes.c_int64),
+        ("sh_rows", ctypes.c_int32),
+        ("sh_degree", ctypes.c_int32),
+        ("camera_centers", _P),
+        ("grad_colors", _P),
+        ("grad_colors_stride", ctypes.c_int64),
+        ("grad_sh", _P),
+        ("grad_camera_centers", _P),
+    ]
+
+
+class EmitArgs(ctypes.Structure):
+    _fields_ = [
+        ("n", ctypes.c_int32),
+        ("views", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("height", ctypes.c_int32),
+        ("centers", _P),
+        ("radii", _P),
+        ("depths", _P),
+        ("offsets", _P),
+        ("keys", _P),
+        ("values", _P),
+    ]
+
+
+class RenderArgs(ctypes.Structure):
+    _fields_ = [
+        ("width", ctypes.c_int32),
+        ("height", ctypes.c_int32),
+        ("views", ctypes.c_int32),
+        ("n", ctypes.c_int32),
+        ("ranges", _P),
+        ("ids", _P),
+        ("centers", _P),
+        ("conics", _P),
+        ("features", _P),
+        ("feat_channels", ctypes.c_int32),
+        ("feat_stride", ctypes.c_int64),
+        ("feat_view_stride", ctypes.c_int64),
+        ("extra", _P),
+        ("extra_channels", ctypes.c_int32),
+        ("extra_stride", ctypes.c_int64),
+        ("extra_view_stride", ctypes.c_int64),
+        ("one_tail", ctypes.c_int32),
+        ("background", _P),
+        ("background_view_stride", ctypes.c_int64),
+        ("image", _P),
+        ("final_t", _P),
+        ("contributors", _P),
+    ]
+
+
+class RenderBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", RenderArgs),
+        ("upstream", _P),
+        ("grad_centers", _P),
+        ("grad_centers_stride", ctypes.c_int64),
+        ("grad_conics", _P),
+        ("grad_conics_stride", ctypes.c_int64),
+        ("abs_centers", _P),
+        ("abs_stride", ctypes.c_int64),
+        ("grad_features", _P),
+        ("grad_feat_stride", ctypes.c_int64),
+        ("grad_feat_view_stride", ctypes.c_int64),
+        ("grad_extra", _P),
+        ("grad_extra_stride", ctypes.c_int64),
+        ("grad_extra_view_stride", ctypes.c_int64),
+    ]
+
+
+STRUCTS = {
+    "gs3d_project_args": ProjectArgs,
+    "gs3d_project_bwd_args": ProjectBwdArgs,
+    "gs3d_emit_args": EmitArgs,
+    "gs3d_render_args": RenderArgs,
+    "gs3d_render_bwd_args": RenderBwdArgs,
+}
+
+# Exported functions: name -> (restype, argtypes).  void* carries device
+# pointers and the hipStream_t.
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+
+FUNCTIONS = {
+    "gs3d_abi_version": (ctypes.c_int, []),
+    "gs3d_last_error": (ctypes.c_char_p, []),
+    "gs3d_camera_prepare": (
+        ctypes.c_int,
+        [_P, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P],
+    ),
+    "gs3d_camera_backward": (
+        ctypes.c_int,
+        [_P, _P, _I32, _I32, _P, _P, _I32, _P, _P],
+    ),
+    "gs3d_project_fwd": (ctypes.c_int, [ctypes.POINTER(ProjectArgs), _P]),
+    "gs3d_project_bwd": (ctypes.c_int, [ctypes.POINTER(ProjectBwdArgs), _P]),
+    "gs3d_sh_fwd": (ctypes.c_int, [_P, _I32, _P, _P, _I32, _I32, _P, _P, _P]),
+    "gs3d_sh_bwd": (
+        ctypes.c_int,
+        [_P, _I32, _P, _P, _P, _P, _I32, _I32, _P, _P, _P],
+    ),
+    "gs3d_metadata": (ctypes.c_int, [_P, _P, _P, _I64, _P, _P, _P, _P]),
+    "gs3d_scan_scratch_bytes": (_SZ, [_I64]),
+    "gs3d_scan_i32": (ctypes.c_int, [_P, _I64, _P, _P, _P, _SZ, _P]),
+    "gs3d_emit_scratch_bytes": (_SZ, [_I64]),
+    "gs3d_emit_keys": (ctypes.c_int, [ctypes.POINTER(EmitArgs), _P, _SZ, _P]),
+    "gs3d_sort_scratch_bytes": (_SZ, [_I64]),
+    "gs3d_sort_pairs_u64": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),
+    "gs3d_tile_ranges": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
+    "gs3d_render_fwd": (ctypes.c_int, [ctypes.POINTER(RenderArgs), _P]),
+    "gs3d_render_bwd": (ctypes.c_int, [ctypes.POINTER(RenderBwdArgs), _P]),
+}

@@ -1,0 +1,282 @@
+/*
+ * gs3d_hip.h — C ABI of the MI355X (gfx950) original-3DGS rasterizer.
+ *
+ * Every entry point is stateless and reentrant: it takes raw device pointers,
+ * element counts, scalar parameters, a hipStream_t (passed as void*) and, where
+ * it needs temporary device memory, a caller-provided scratch buffer whose size
+ * is returned by the matching *_scratch_bytes query.  No entry point allocates
+ * device memory, retains a pointer after it returns, or synchronises the
+ * stream.  All launches go to the given stream in submission order.
+ *
+ * Return value: GS3D_OK (0) or a negative status.  Invalid arguments are
+ * detected on the host before anything is launched.
+ *
+ * Each declaration names the reference launch it replaces (paths relative to
+ * the dsl_splat package of YukiNagato/dsl_splat).  Multi-view launches
+ * ("views" > 1) are equivalent to one reference launch per view; views are
+ * stored back to back with the strides given in the argument structs.
+ *
+ * Layouts: float32 row-major; matrices (4,4)/(3,3) row-major per view; all
+ * per-view Gaussian arrays are (views, N, ...) contiguous unless a stride
+ * argument says otherwise.
+ */
+#ifndef GS3D_HIP_H
+#define GS3D_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    GS3D_OK = 0,
+    GS3D_ERR_ARGUMENT = -1,   /* bad pointer/size/stride combination */
+    GS3D_ERR_LAUNCH = -2,     /* hipGetLastError after a launch */
+    GS3D_ERR_UNSUPPORTED = -3,/* channel count or degree outside what was built */
+    GS3D_ERR_SCRATCH = -4,    /* scratch buffer smaller than *_scratch_bytes */
+    GS3D_ERR_OVERFLOW = -5    /* a count that would not fit int32 offsets */
+};
+
+/* ABI revision; bumped whenever a struct layout or signature changes. */
+int gs3d_abi_version(void);
+
+/* Last HIP error string seen by this thread (for diagnostics). */
+const char* gs3d_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Camera preparation.
+ * Replaces splatting/camera_kernels.py:11-66 (prepare_kernel), launched from
+ * splatting/cameras.py:45-63.  Per camera i: error code (0 ok, 2 non-finite K
+ * or fx,fy<=0, 1 skew/non-pinhole K, 3 singular view with with_centers);
+ * full projection rows (count,4,4); with_centers: view inverse (count,4,4) and
+ * camera centre inverse[0:3,3] (count,3).
+ * ---------------------------------------------------------------------- */
+int gs3d_camera_prepare(const float* views, const float* Ks, int32_t count,
+                        int32_t width, int32_t height, int32_t with_centers,
+                        float* full, float* inverse, float* centers,
+                        int32_t* errors, void* stream);
+
+/* Replaces splatting/camera_kernels.py:69-106 (backward_kernel), launched from
+ * splatting/cameras.py:98-114.  grad_full and/or grad_centers may be NULL.
+ * Writes grad_views (count,4,4) (overwritten, not accumulated). */
+int gs3d_camera_backward(const float* Ks, const float* grad_full,
+                         int32_t width, int32_t height, const float* inverse,
+                         const float* grad_centers, int32_t count,
+                         float* grad_views, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Projection forward (+ optional fused SH colour and training metadata).
+ * Replaces gs3d/projection.py:89-164 (project, launched at :331-353); with
+ * sh != NULL also primitives/sh.py:44-79 (evaluate, launched from
+ * primitives/spherical_harmonics.py:218-233 with radii masking); with
+ * means2d != NULL also splatting/metadata.py:12-31 (_prepare, :296-311).
+ * Culled rows get radii = tiles = 0 and zeros in centers/conics/depths.
+ * ---------------------------------------------------------------------- */
+typedef struct gs3d_project_args {
+    int32_t n;            /* Gaussians */
+    int32_t views;        /* cameras handled by this launch */
+    int32_t width, height;
+    float near_plane, far_plane, radius_clip;
+    const float* means;       /* (N,3) */
+    const float* quats;       /* (N,4) wxyz, already normalised */
+    const float* scales;      /* (N,3) activated */
+    const float* opacities;   /* (N,) activated */
+    const float* view;        /* (views,4,4) world->camera */
+    const float* projection;  /* (views,4,4) from gs3d_camera_prepare */
+    const float* intrinsics;  /* (views,3,3) */
+    float* centers;           /* (views,N,2) pixel centres */
+    float* conics;            /* (views,N,4) inverse cov (a,b,c) + opacity */
+    int32_t* radii;           /* (views,N) */
+    int32_t* tiles;           /* (views,N) touched 16x16 tiles */
+    float* depths;            /* (views,N) camera-space z */
+    /* fused SH (sh == NULL disables) */
+    const float* sh;          /* (N,K,3), or per view with sh_view_stride */
+    int64_t sh_view_stride;   /* floats between views; 0 = shared by all views */
+    int32_t sh_rows;          /* K (row count of each Gaussian's block) */
+    int32_t sh_degree;        /* 0..3; (deg+1)^2 <= K */
+    const float* camera_centers; /* (views,3); required when sh_degree > 0 */
+    float* colors;            /* (views,N,3) */
+    /* fused metadata (means2d == NULL disables) */
+    float* means2d;           /* (views,N,2) */
+    float* meta_opacities;    /* (views,N) */
+    float* meta_conics;       /* (views,N,3) */
+} gs3d_project_args;
+
+int gs3d_project_fwd(const gs3d_project_args* args, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Projection backward (+ optional fused SH backward).
+ * Replaces gs3d/projection.py:213-285 (project_backward, launched at
+ * :393-422) and, with sh != NULL, primitives/sh.py:82-138 (backward, launched
+ * from primitives/spherical_harmonics.py:256-273) followed by the Torch
+ * "means - camera centre" VJP of gs3d/api.py:160-164.
+ * Per-Gaussian outputs are dense, summed over views and overwritten (culled
+ * rows give zeros).  grad_view/grad_projection/grad_camera_centers are
+ * accumulated with atomics: the caller zeroes them.  Any output may be NULL.
+ * ---------------------------------------------------------------------- */
+typedef struct gs3d_project_bwd_args {
+    int32_t n, views, width, height;
+    const float* means;
+    const float* quats;
+    const float* scales;
+    const float* opacities;
+    const float* view;        /* (views,4,4) */
+    const float* projection;  /* (views,4,4) */
+    const float* intrinsics;  /* (views,3,3) */
+    const int32_t* radii;     /* (views,N) */
+    const float* grad_centers;   /* (views,N,*) rows of grad_centers_stride floats */
+    int64_t grad_centers_stride;
+    const float* grad_conics;    /* (views,N,*) rows of grad_conics_stride floats (a,b,c,opacity) */
+    int64_t grad_conics_stride;
+    float* grad_means;        /* (N,3) */
+    float* grad_quats;        /* (N,4) */
+    float* grad_scales;       /* (N,3) */
+    float* grad_opacities;    /* (N,) */
+    float* grad_view;         /* (views,4,4) accumulated */
+    float* grad_projection;   /* (views,4,4) accumulated */
+    /* fused SH backward (sh == NULL disables) */
+    const float* sh;
+    int64_t sh_view_stride;   /* 0 = shared coefficients; grads then summed over views */
+    int32_t sh_rows, sh_degree;
+    const float* camera_centers;  /* (views,3) */
+    const float* grad_colors;     /* (views,N,*) rows of grad_colors_stride floats */
+    int64_t grad_colors_stride;
+    float* grad_sh;               /* like sh (dense, rows beyond (deg+1)^2 are zero) */
+    float* grad_camera_centers;   /* (views,3) accumulated */
+} gs3d_project_bwd_args;
+
+int gs3d_project_bwd(const gs3d_project_bwd_args* args, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Standalone SH0-3 (primitives/sh.py:44-138 through
+ * primitives/spherical_harmonics.py:198-281).  radii may be NULL (no mask).
+ * coefficients (N,K,3) with row stride K*3, directions (N,3).
+ * active (N,3) uint8 clamp mask may be NULL.
+ * ---------------------------------------------------------------------- */
+int gs3d_sh_fwd(const float* coefficients, int32_t rows, const float* directions,
+                const int32_t* radii, int32_t n, int32_t degree,
+                float* colors, uint8_t* active, void* stream);
+/* grad_coefficients (N,K,3) fully written (zeros beyond (deg+1)^2), may be
+ * NULL; grad_directions (N,3) may be NULL. */
+int gs3d_sh_bwd(const float* coefficients, int32_t rows, const float* directions,
+                const int32_t* radii, const uint8_t* active, const float* upstream,
+                int32_t n, int32_t degree, float* grad_coefficients,
+                float* grad_directions, void* stream);
+
+/* Standalone metadata pass, splatting/metadata.py:12-31 (_prepare). */
+int gs3d_metadata(const int32_t* radii, const float* centers, const float* conics,
+                  int64_t n, float* means2d, float* opacities, float* meta_conics,
+                  void* stream);
+
+/* ------------------------------------------------------------------------
+ * Inclusive int32 prefix sum: primitives/tiling.py:57-64 (scan_counts,
+ * wp.utils.array_scan).  total (device int64, may be NULL) receives the sum
+ * computed in 64 bits; offsets overflow is reported through *total > INT32_MAX.
+ * ---------------------------------------------------------------------- */
+size_t gs3d_scan_scratch_bytes(int64_t n);
+int gs3d_scan_i32(const int32_t* counts, int64_t n, int32_t* offsets,
+                  int64_t* total, void* scratch, size_t scratch_bytes,
+                  void* stream);
+
+/* ------------------------------------------------------------------------
+ * Tile-pair emission: splatting/binning.py:16-37 (duplicate, launched at
+ * :192-215).  The (views*N) rows are one flat array; row r belongs to view
+ * r / n and emits key ((view*tiles_per_view + y*gx + x) << 32) | bits(depth)
+ * and value (r % n) at offsets[r-1] + k (row-major over its tile rectangle).
+ * ---------------------------------------------------------------------- */
+typedef struct gs3d_emit_args {
+    int32_t n, views, width, height;
+    const float* centers;     /* (views,N,2) */
+    const int32_t* radii;     /* (views,N) */
+    const float* depths;      /* (views,N) */
+    const int32_t* offsets;   /* (views*N) inclusive scan of tiles */
+    uint64_t* keys;           /* (M) */
+    int32_t* values;          /* (M) */
+} gs3d_emit_args;
+
+size_t gs3d_emit_scratch_bytes(int64_t rows);
+int gs3d_emit_keys(const gs3d_emit_args* args, void* scratch, size_t scratch_bytes,
+                   void* stream);
+
+/* ------------------------------------------------------------------------
+ * Stable LSD radix sort of (uint64 key, int32 value) pairs over key bits
+ * [0, end_bit): primitives/tiling.py:67-86 (sort_tile_pairs ->
+ * wp.utils.radix_sort_pairs).  keys/values hold 2*count elements: the first
+ * count are the input and, on return, the sorted output (the second half is
+ * the ping-pong buffer, as in the reference).
+ * ---------------------------------------------------------------------- */
+size_t gs3d_sort_scratch_bytes(int64_t count);
+int gs3d_sort_pairs_u64(uint64_t* keys, int32_t* values, int64_t count,
+                        int32_t end_bit, void* scratch, size_t scratch_bytes,
+                        void* stream);
+
+/* Per-tile [first, last) ranges of sorted keys: primitives/tiling.py:39-54
+ * (identify_ranges, launched at :87-100).  ranges (tile_count,2) must be
+ * zero-initialised by the caller; tile id 0xFFFFFFFF is ignored. */
+int gs3d_tile_ranges(const uint64_t* sorted_keys, int64_t count, int32_t* ranges,
+                     int64_t tile_count, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Forward alpha blending on 16x16 tiles: gs3d/render.py:36-208 (render,
+ * launched at :359-406).  The blended channel vector of Gaussian g in view v
+ * is [features (feat_channels) | extra (extra_channels) | 1.0 if one_tail],
+ * D' channels in all; background covers the feature channels only (the rest
+ * are zero), as gs3d/autograd.py:41-50 builds it.
+ * image is written channel-last (views,H,W,D').
+ * ---------------------------------------------------------------------- */
+typedef struct gs3d_render_args {
+    int32_t width, height, views;
+    int32_t n;                 /* Gaussians per view (rows of centers/conics) */
+    const int32_t* ranges;     /* (views*tiles,2), indices into ids */
+    const int32_t* ids;        /* sorted Gaussian indices (per-view row index) */
+    const float* centers;      /* (views,N,2) */
+    const float* conics;       /* (views,N,4) */
+    const float* features;     /* rows of feat_stride floats */
+    int32_t feat_channels;
+    int64_t feat_stride;       /* floats between rows */
+    int64_t feat_view_stride;  /* floats between views (0 = shared) */
+    const float* extra;        /* may be NULL when extra_channels == 0 */
+    int32_t extra_channels;
+    int64_t extra_stride, extra_view_stride;
+    int32_t one_tail;          /* 1 appends the constant alpha channel */
+    const float* background;   /* (views, feat_channels) rows, may be NULL */
+    int64_t background_view_stride;
+    float* image;              /* (views,H,W,D') */
+    float* final_t;            /* (views,H,W) */
+    int32_t* contributors;     /* (views,H,W) */
+} gs3d_render_args;
+
+int gs3d_render_fwd(const gs3d_render_args* args, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Reverse traversal of the blend: gs3d/render.py:211-356 (backward, launched
+ * at :409-463) with constant_tail = one_tail.  Gradients are accumulated with
+ * atomics (the caller zeroes them); a wavefront reduces its 64 pixels'
+ * contributions to one Gaussian before the atomic.  grad_features and
+ * grad_extra honour their view strides (0 = summed over views).  Any
+ * gradient pointer may be NULL except grad_centers/grad_conics.
+ * ---------------------------------------------------------------------- */
+typedef struct gs3d_render_bwd_args {
+    gs3d_render_args fwd;        /* same inputs; image unused */
+    const float* upstream;       /* (views,H,W,D') channel-last dL/dimage */
+    float* grad_centers;         /* (views,N,*) rows of grad_centers_stride */
+    int64_t grad_centers_stride;
+    float* grad_conics;          /* (views,N,*) rows of grad_conics_stride */
+    int64_t grad_conics_stride;
+    float* abs_centers;          /* (views,N,*) or NULL; rows of abs_stride */
+    int64_t abs_stride;
+    float* grad_features;        /* rows of grad_feat_stride, view stride below */
+    int64_t grad_feat_stride, grad_feat_view_stride;
+    float* grad_extra;
+    int64_t grad_extra_stride, grad_extra_view_stride;
+} gs3d_render_bwd_args;
+
+int gs3d_render_bwd(const gs3d_render_bwd_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GS3D_HIP_H */

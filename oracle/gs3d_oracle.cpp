@@ -1,0 +1,1130 @@
+// gs3d_oracle.cpp — CPU restatement of the original-3DGS (gs3d) path of
+// YukiNagato/dsl_splat, used ONLY as the checker for the HIP kernels.
+//
+// TEST INFRASTRUCTURE.  Only tests/, __graft_entry__.smoke() and bench.py's
+// cpu_baseline leg load this library.  The product (dsl_splat_amd) never
+// links, imports or calls it.
+//
+// Every function follows the reference kernel it names, operation by
+// operation, in float32 with contraction off (built with -ffp-contract=off);
+// fmaf appears exactly where the reference calls fused_multiply_add / fmaf.
+// The projection forward and its VJP are templates so that a float64
+// instantiation can be checked against finite differences.
+//
+// Choices the reference leaves to the CUDA compiler (Warp's default fuse_fp in
+// project/duplicate/render) are fixed here and documented at each site:
+//   * projection scalar arithmetic: no contraction;
+//   * blending: the power/colour contractions in blend_power()/blend_accum();
+//   * exp: gs_expf() below, a fixed-sequence Cody-Waite + Taylor routine.
+// The HIP kernels implement the same choices, so integer outputs and the
+// forward image are bit-exact between the two; reductions whose order the
+// GPU does not fix (atomics) are compared with a tolerance.
+//
+// Parity pins (tests/test_oracle_*.py): closed forms for camera rows,
+// projection special cases, SH0 and the blend of a single Gaussian; a NumPy
+// brute-force renderer; numpy.lexsort / searchsorted for scan, keys, sort and
+// ranges; float64 central differences for the projection, SH and blend VJPs;
+// known-answer checks of the three custom adjoints.
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <numeric>
+#include <vector>
+
+#include <omp.h>
+
+#include "gs3d_hip.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// exp used by blending (gs3d/render.py:96, :287 call wp.exp).  Fixed sequence:
+// x = k*ln2 + r with k = rint(x*log2 e), r by two-constant Cody-Waite
+// reduction (ln2_hi has 15 significant bits so k*ln2_hi is exact), then the
+// degree-7 Taylor polynomial of exp(r) on |r| <= ln2/2 in Horner form, scaled
+// by 2^k.  Below -86 the result is flushed to 0 (it is < 2^-124, far below the
+// 1/255 blending threshold and keeps every intermediate normal).
+// ---------------------------------------------------------------------------
+inline float gs_expf(float x) {
+    if (x < -86.0f) return 0.0f;
+    const float k = rintf(x * 1.44269502e+00f);
+    float r = fmaf(k, -6.93145752e-01f, x);
+    r = fmaf(k, -1.42860677e-06f, r);
+    float p = 1.98412701e-04f;            // 1/5040
+    p = fmaf(p, r, 1.38888892e-03f);      // 1/720
+    p = fmaf(p, r, 8.33333377e-03f);      // 1/120
+    p = fmaf(p, r, 4.16666679e-02f);      // 1/24
+    p = fmaf(p, r, 1.66666672e-01f);      // 1/6
+    p = fmaf(p, r, 5.00000000e-01f);      // 1/2
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)k);
+}
+
+// ---------------------------------------------------------------------------
+// Small fixed-size math in a scalar template T (float for the oracle,
+// double for finite-difference checks).
+// ---------------------------------------------------------------------------
+template <class T> inline T fma_(T a, T b, T c) { return std::fma(a, b, c); }
+template <> inline float fma_<float>(float a, float b, float c) { return fmaf(a, b, c); }
+
+template <class T> struct M3 { T m[3][3]; };
+template <class T> struct M4 { T m[4][4]; };
+
+template <class T> M3<T> transpose(const M3<T>& a) {
+    M3<T> r;
+    for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 3; ++j) r.m[i][j] = a.m[j][i];
+    return r;
+}
+
+// splatting/math.py:31-41 reference_matmul: fma(a[r,2], b[2,c],
+// fma(a[r,0], b[0,c], a[r,1]*b[1,c])).
+template <class T> M3<T> ref_matmul(const M3<T>& a, const M3<T>& b) {
+    M3<T> r;
+    for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 3; ++j)
+            r.m[i][j] = fma_(a.m[i][2], b.m[2][j], fma_(a.m[i][0], b.m[0][j], a.m[i][1] * b.m[1][j]));
+    return r;
+}
+
+// splatting/math.py:44-47 point_row: fma(M[r,2], z, fma(M[r,0], x, M[r,1]*y)) + M[r,3].
+template <class T> T point_row(const M4<T>& m, int r, const T p[3]) {
+    T xy = fma_(m.m[r][0], p[0], m.m[r][1] * p[1]);
+    return fma_(m.m[r][2], p[2], xy) + m.m[r][3];
+}
+
+// primitives/math.py:33-45 glm_rotation (rounded products where __fmul_rn /
+// __fadd_rn / __fsub_rn are used, fmaf elsewhere).
+template <class T> M3<T> glm_rotation(const T q[4]) {
+    const T r = q[0], x = q[1], y = q[2], z = q[3];
+    const T yy = y * y, zz = z * z;
+    const T rz = r * z, xz = x * z, rx = r * x;
+    const T d0 = yy + zz, d1 = fma_(x, x, zz), d2 = fma_(x, x, yy);
+    M3<T> R;
+    R.m[0][0] = T(1) - (d0 + d0);
+    R.m[0][1] = T(2) * fma_(x, y, rz);
+    R.m[0][2] = T(2) * fma_(-r, y, xz);
+    R.m[1][0] = T(2) * fma_(x, y, -rz);
+    R.m[1][1] = T(1) - (d1 + d1);
+    R.m[1][2] = T(2) * fma_(y, z, rx);
+    R.m[2][0] = T(2) * fma_(r, y, xz);
+    R.m[2][1] = T(2) * fma_(y, z, -rx);
+    R.m[2][2] = T(1) - (d2 + d2);
+    return R;
+}
+
+template <class T> T clampv(T v, T lo, T hi) { return std::min(std::max(v, lo), hi); }
+
+template <class T> M4<T> load44(const float* p) {
+    M4<T> m;
+    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) m.m[i][j] = T(p[4 * i + j]);
+    return m;
+}
+
+// ---------------------------------------------------------------------------
+// Projection forward, gs3d/projection.py:37-86 (screen_covariance) and
+// splatting/geometry.py:22-123.
+// ---------------------------------------------------------------------------
+template <class T> struct CovState {
+    // Intermediates kept for the VJP.
+    T t[3];          // clamped camera point (geometry.py:33-39)
+    T pos[3];        // unclamped camera point
+    M3<T> R, M, Sigma, J, W, Tm, X, cov2;
+    T limx, limy;
+};
+
+template <class T>
+void screen_covariance(const T pos[3], const T q[4], const T s[3], const M4<T>& V,
+                       int width, int height, T fx, T fy, CovState<T>& st, T cov[3]) {
+    // projection.py:48-52 limits, clamp_point geometry.py:33-39.
+    const T limx = T(1.3) * T(width) / (T(2) * fx);
+    const T limy = T(1.3) * T(height) / (T(2) * fy);
+    st.limx = limx;
+    st.limy = limy;
+    for (int i = 0; i < 3; ++i) st.pos[i] = pos[i];
+    st.t[0] = clampv(pos[0] / pos[2], -limx, limx) * pos[2];
+    st.t[1] = clampv(pos[1] / pos[2], -limy, limy) * pos[2];
+    st.t[2] = pos[2];
+    st.R = glm_rotation(q);
+    M3<T> S{};
+    for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 3; ++j) S.m[i][j] = T(0);
+    S.m[0][0] = s[0];
+    S.m[1][1] = s[1];
+    S.m[2][2] = s[2];
+    st.M = ref_matmul(S, st.R);
+    st.Sigma = ref_matmul(transpose(st.M), st.M);
+    const T* t = st.t;
+    M3<T> J{};
+    J.m[0][0] = fx / t[2]; J.m[0][1] = T(0); J.m[0][2] = T(0);
+    J.m[1][0] = T(0); J.m[1][1] = fy / t[2]; J.m[1][2] = T(0);
+    J.m[2][0] = -(fx * t[0]) / (t[2] * t[2]);
+    J.m[2][1] = -(fy * t[1]) / (t[2] * t[2]);
+    J.m[2][2] = T(0);
+    st.J = J;
+    M3<T> W;
+    for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 3; ++j) W.m[i][j] = V.m[j][i];
+    st.W = W;
+    st.Tm = ref_matmul(W, J);
+    st.X = ref_matmul(transpose(st.Tm), transpose(st.Sigma));
+    st.cov2 = ref_matmul(st.X, st.Tm);
+    cov[0] = st.cov2.m[0][0] + T(0.3);
+    cov[1] = st.cov2.m[1][0];
+    cov[2] = st.cov2.m[1][1] + T(0.3);
+}
+
+// splatting/geometry.py:54-58 invert_covariance.
+template <class T> void invert_covariance(const T cov[3], T out[3]) {
+    const T a = cov[0], b = cov[1], c = cov[2];
+    const T inv = T(1) / (a * c - b * b);
+    out[0] = c * inv;
+    out[1] = -b * inv;
+    out[2] = a * inv;
+}
+
+// splatting/geometry.py:106-123 pixel_center: fp32 perspective divide, fp64
+// viewport transform, rounded once to fp32.
+template <class T> void pixel_center(const T mean[3], const M4<T>& P, int width, int height,
+                                     T out[2], T clip[4], T* inv_w_out) {
+    for (int r = 0; r < 4; ++r) clip[r] = point_row(P, r, mean);
+    const T inv_w = T(1) / (clip[3] + T(0.0000001));
+    *inv_w_out = inv_w;
+    const double ndc_x = double(clip[0] * inv_w);
+    const double ndc_y = double(clip[1] * inv_w);
+    out[0] = T(((ndc_x + 1.0) * double(width) - 1.0) * 0.5);
+    out[1] = T(((ndc_y + 1.0) * double(height) - 1.0) * 0.5);
+}
+
+// splatting/geometry.py:22-30 tile_bounds (CUDA getRect truncation).
+inline void tile_bounds(const float c[2], int radius, int gx, int gy, int b[4]) {
+    auto trunc_clamp = [](float v, int hi) {
+        int i = (int)v;
+        return std::min(std::max(i, 0), hi);
+    };
+    const float r = (float)radius;
+    b[0] = trunc_clamp((c[0] - r) / 16.0f, gx);
+    b[1] = trunc_clamp((c[1] - r) / 16.0f, gy);
+    b[2] = trunc_clamp(((c[0] + r) + 16.0f - 1.0f) / 16.0f, gx);
+    b[3] = trunc_clamp(((c[1] + r) + 16.0f - 1.0f) / 16.0f, gy);
+}
+
+// gs3d/projection.py:89-164 project, one Gaussian in one view.
+struct ProjOut {
+    float center[2], conic[4];
+    int radius, tiles;
+    float depth;
+};
+
+bool project_one(const float* mean, const float* quat, const float* scale, float opacity,
+                 const float* view, const float* proj, const float* K, int width, int height,
+                 float near_plane, float far_plane, float radius_clip, ProjOut& o) {
+    o = ProjOut{};
+    const M4<float> V = load44<float>(view);
+    float t4[4];
+    for (int r = 0; r < 4; ++r) t4[r] = point_row(V, r, mean);
+    if (t4[2] <= near_plane || t4[2] >= far_plane) return false;
+    CovState<float> st;
+    float cov[3];
+    screen_covariance<float>(t4, quat, scale, V, width, height, K[0], K[4], st, cov);
+    const float a = cov[0], b = cov[1], c = cov[2];
+    const float det = a * c - b * b;
+    if (det == 0.0f) return false;
+    const float mid = 0.5f * (a + c);
+    const int radius = (int)ceilf(3.0f * sqrtf(mid + sqrtf(std::max(0.1f, mid * mid - det))));
+    if ((float)radius <= radius_clip) return false;
+    float center[2], clip[4], inv_w;
+    pixel_center<float>(mean, load44<float>(proj), width, height, center, clip, &inv_w);
+    int bnd[4];
+    tile_bounds(center, radius, (width + 15) / 16, (height + 15) / 16, bnd);
+    const int count = (bnd[2] - bnd[0]) * (bnd[3] - bnd[1]);
+    if (count == 0) return false;
+    float inv[3];
+    invert_covariance<float>(cov, inv);
+    o.center[0] = center[0];
+    o.center[1] = center[1];
+    o.conic[0] = inv[0];
+    o.conic[1] = inv[1];
+    o.conic[2] = inv[2];
+    o.conic[3] = opacity;
+    o.radius = radius;
+    o.tiles = count;
+    o.depth = t4[2];
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// SH, primitives/sh.py:7-79 (basis, evaluate).  Constants are the float32
+// roundings of the reference literals; products evaluate left to right.
+// ---------------------------------------------------------------------------
+inline float sh_basis(const float u[3], int k) {
+    const float x = u[0], y = u[1], z = u[2];
+    switch (k) {
+    case 0: return 0.28209479177387814f;
+    case 1: return -0.4886025119029199f * y;
+    case 2: return 0.4886025119029199f * z;
+    case 3: return -0.4886025119029199f * x;
+    case 4: return 1.0925484305920792f * x * y;
+    case 5: return -1.0925484305920792f * y * z;
+    case 6: return 0.31539156525252005f * (2.0f * z * z - x * x - y * y);
+    case 7: return -1.0925484305920792f * x * z;
+    case 8: return 0.5462742152960396f * (x * x - y * y);
+    case 9: return -0.5900435899266435f * y * (3.0f * x * x - y * y);
+    case 10: return 2.890611442640554f * x * y * z;
+    case 11: return -0.4570457994644658f * y * (4.0f * z * z - x * x - y * y);
+    case 12: return 0.3731763325901154f * z * (2.0f * z * z - 3.0f * x * x - 3.0f * y * y);
+    case 13: return -0.4570457994644658f * x * (4.0f * z * z - x * x - y * y);
+    case 14: return 1.445305721320277f * z * (x * x - y * y);
+    default: return -0.5900435899266435f * x * (x * x - 3.0f * y * y);
+    }
+}
+
+// Gradient of sh_basis w.r.t. the unit direction (what wp.grad(basis)
+// returns at primitives/sh.py:127), derived from the polynomials above.
+inline void sh_basis_grad(const float u[3], int k, float g[3]) {
+    const float x = u[0], y = u[1], z = u[2];
+    g[0] = g[1] = g[2] = 0.0f;
+    const float C1 = 0.4886025119029199f, C4 = 1.0925484305920792f, C6 = 0.31539156525252005f,
+                C8 = 0.5462742152960396f, C9 = 0.5900435899266435f, C10 = 2.890611442640554f,
+                C11 = 0.4570457994644658f, C12 = 0.3731763325901154f, C14 = 1.445305721320277f;
+    switch (k) {
+    case 0: break;
+    case 1: g[1] = -C1; break;
+    case 2: g[2] = C1; break;
+    case 3: g[0] = -C1; break;
+    case 4: g[0] = C4 * y; g[1] = C4 * x; break;
+    case 5: g[1] = -C4 * z; g[2] = -C4 * y; break;
+    case 6: g[0] = C6 * (-2.0f * x); g[1] = C6 * (-2.0f * y); g[2] = C6 * (4.0f * z); break;
+    case 7: g[0] = -C4 * z; g[2] = -C4 * x; break;
+    case 8: g[0] = C8 * (2.0f * x); g[1] = C8 * (-2.0f * y); break;
+    case 9:  // -C9 * y * (3x^2 - y^2) = -C9 (3x^2 y - y^3)
+        g[0] = -C9 * (6.0f * x * y);
+        g[1] = -C9 * (3.0f * x * x - 3.0f * y * y);
+        break;
+    case 10: g[0] = C10 * y * z; g[1] = C10 * x * z; g[2] = C10 * x * y; break;
+    case 11:  // -C11 * y * (4z^2 - x^2 - y^2)
+        g[0] = -C11 * (-2.0f * x * y);
+        g[1] = -C11 * (4.0f * z * z - x * x - 3.0f * y * y);
+        g[2] = -C11 * (8.0f * y * z);
+        break;
+    case 12:  // C12 * z * (2z^2 - 3x^2 - 3y^2)
+        g[0] = C12 * (-6.0f * x * z);
+        g[1] = C12 * (-6.0f * y * z);
+        g[2] = C12 * (6.0f * z * z - 3.0f * x * x - 3.0f * y * y);
+        break;
+    case 13:  // -C11 * x * (4z^2 - x^2 - y^2)
+        g[0] = -C11 * (4.0f * z * z - 3.0f * x * x - y * y);
+        g[1] = -C11 * (-2.0f * x * y);
+        g[2] = -C11 * (8.0f * x * z);
+        break;
+    case 14:  // C14 * z * (x^2 - y^2)
+        g[0] = C14 * (2.0f * x * z);
+        g[1] = C14 * (-2.0f * y * z);
+        g[2] = C14 * (x * x - y * y);
+        break;
+    default:  // -C9 * x * (x^2 - 3y^2)
+        g[0] = -C9 * (3.0f * x * x - 3.0f * y * y);
+        g[1] = -C9 * (-6.0f * x * y);
+        break;
+    }
+}
+
+// wp.length (dot without contraction, then sqrt) and the guarded divide of
+// primitives/sh.py:67, :113-114.
+inline float length3(const float d[3]) { return sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]); }
+
+// primitives/sh.py:58-77 for one row: returns the pre-clamp value in raw.
+inline void sh_eval(const float* coef, const float dir[3], int degree, bool visible,
+                    float color[3], float raw[3]) {
+    float value[3] = {0.0f, 0.0f, 0.0f};
+    if (visible) {
+        float unit[3] = {0.0f, 0.0f, 0.0f};
+        if (degree > 0) {
+            const float len = std::max(length3(dir), 1.0e-12f);
+            for (int i = 0; i < 3; ++i) unit[i] = dir[i] / len;
+        }
+        const int count = (degree + 1) * (degree + 1);
+        for (int k = 0; k < count; ++k) {
+            const float b = sh_basis(unit, k);
+            for (int ch = 0; ch < 3; ++ch) value[ch] = value[ch] + b * coef[3 * k + ch];
+        }
+        for (int ch = 0; ch < 3; ++ch) value[ch] = value[ch] + 0.5f;
+    }
+    for (int ch = 0; ch < 3; ++ch) {
+        raw[ch] = value[ch];
+        color[ch] = std::max(value[ch], 0.0f);
+    }
+}
+
+// primitives/sh.py:100-136 for one row.  active[ch] is the saved clamp mask.
+inline void sh_backward_row(const float* coef, const float dir[3], int degree, bool visible,
+                            const bool active[3], const float upstream[3], float* grad_coef,
+                            int rows, float grad_dir[3]) {
+    grad_dir[0] = grad_dir[1] = grad_dir[2] = 0.0f;
+    if (grad_coef)
+        for (int i = 0; i < rows * 3; ++i) grad_coef[i] = 0.0f;
+    if (!visible) return;
+    float cg[3];
+    for (int ch = 0; ch < 3; ++ch) cg[ch] = active[ch] ? upstream[ch] : 0.0f;
+    float unit[3] = {0.0f, 0.0f, 0.0f}, length = 1.0f;
+    if (degree > 0) {
+        length = length3(dir);
+        const float l = std::max(length, 1.0e-12f);
+        for (int i = 0; i < 3; ++i) unit[i] = dir[i] / l;
+    }
+    float ug[3] = {0.0f, 0.0f, 0.0f};
+    const int count = (degree + 1) * (degree + 1);
+    for (int k = 0; k < count; ++k) {
+        const float b = sh_basis(unit, k);
+        if (grad_coef)
+            for (int ch = 0; ch < 3; ++ch) grad_coef[3 * k + ch] = b * cg[ch];
+        float bg[3];
+        sh_basis_grad(unit, k, bg);
+        const float d = coef[3 * k] * cg[0] + coef[3 * k + 1] * cg[1] + coef[3 * k + 2] * cg[2];
+        for (int i = 0; i < 3; ++i) ug[i] = ug[i] + d * bg[i];
+    }
+    if (degree > 0) {
+        const float l = std::max(length, 1.0e-12f);
+        for (int i = 0; i < 3; ++i) grad_dir[i] = ug[i] / l;
+        if (length >= 1.0e-12f) {
+            const float dot = unit[0] * ug[0] + unit[1] * ug[1] + unit[2] * ug[2];
+            const float f = dot / length;
+            for (int i = 0; i < 3; ++i) grad_dir[i] = grad_dir[i] - unit[i] * f;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Projection VJP: the reverse pass of gs3d/projection.py:198-210
+// (projection_loss) as wp.grad evaluates it, with the custom adjoints of
+// splatting/geometry.py:42-51 (clamp), :61-71 (inverse covariance) and
+// splatting/math.py:13-28 (rotation); fmaf adjoint of primitives/math.py:16.
+// ---------------------------------------------------------------------------
+template <class T> struct ProjGrad {
+    T mean[3], quat[4], scale[3], opacity;
+    T view[4][4], proj[4][4];
+};
+
+// dC = A*B; given gC, accumulate gA += gC*B^T, gB += A^T*gC.
+template <class T> void matmul_vjp(const M3<T>& A, const M3<T>& B, const M3<T>& gC, M3<T>& gA, M3<T>& gB) {
+    for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 3; ++j) {
+            T sa = T(0), sb = T(0);
+            for (int k = 0; k < 3; ++k) {
+                sa += gC.m[i][k] * B.m[j][k];
+                sb += A.m[k][i] * gC.m[k][j];
+            }
+            gA.m[i][j] += sa;
+            gB.m[i][j] += sb;
+        }
+}
+
+template <class T> M3<T> zero3() {
+    M3<T> z;
+    for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 3; ++j) z.m[i][j] = T(0);
+    return z;
+}
+
+template <class T>
+void projection_vjp(const T mean[3], const T q[4], const T s[3], T opacity, const M4<T>& V,
+                    const M4<T>& P, int width, int height, T fx, T fy, const T gc[2],
+                    const T gk[4], ProjGrad<T>& g) {
+    std::memset(&g, 0, sizeof(g));
+    // Forward recomputation.
+    T pos[3];
+    for (int r = 0; r < 3; ++r) pos[r] = point_row(V, r, mean);
+    CovState<T> st;
+    T cov[3];
+    screen_covariance<T>(pos, q, s, V, width, height, fx, fy, st, cov);
+    // conic = invert_covariance(cov) + opacity.
+    g.opacity = gk[3];
+    {
+        // splatting/geometry.py:61-71 adj_invert_covariance.
+        const T a = cov[0], b = cov[1], c = cov[2];
+        const T det = a * c - b * b;
+        const T factor = T(1) / (det * det + T(0.0000001));
+        const T x = gk[0], y = gk[1], z = gk[2];
+        const T ga = factor * (-c * c * x + b * c * y + (det - a * c) * z);
+        const T gb = factor * (T(2) * b * c * x - (det + T(2) * b * b) * y + T(2) * a * b * z);
+        const T gcv = factor * (-a * a * z + a * b * y + (det - a * c) * x);
+        // cov = (cov2[0,0]+0.3, cov2[1,0], cov2[1,1]+0.3)
+        M3<T> gcov2 = zero3<T>();
+        gcov2.m[0][0] = ga;
+        gcov2.m[1][0] = gb;
+        gcov2.m[1][1] = gcv;
+        // cov2 = X * Tm ; X = Tm^T * Sigma^T
+        M3<T> gX = zero3<T>(), gTm = zero3<T>();
+        matmul_vjp(st.X, st.Tm, gcov2, gX, gTm);
+        M3<T> gTmT = zero3<T>(), gSigmaT = zero3<T>();
+        matmul_vjp(transpose(st.Tm), transpose(st.Sigma), gX, gTmT, gSigmaT);
+        gTm = [&] {
+            M3<T> r = gTm;
+            for (int i = 0; i < 3; ++i)
+                for (int j = 0; j < 3; ++j) r.m[i][j] += gTmT.m[j][i];
+            return r;
+        }();
+        M3<T> gSigma = transpose(gSigmaT);
+        // Tm = W * J
+        M3<T> gW = zero3<T>(), gJ = zero3<T>();
+        matmul_vjp(st.W, st.J, gTm, gW, gJ);
+        // Sigma = M^T * M
+        M3<T> gMT = zero3<T>(), gM = zero3<T>();
+        matmul_vjp(transpose(st.M), st.M, gSigma, gMT, gM);
+        for (int i = 0; i < 3; ++i)
+            for (int j = 0; j < 3; ++j) gM.m[i][j] += gMT.m[j][i];
+        // M = S * R (S diagonal)
+        M3<T> gR;
+        for (int i = 0; i < 3; ++i) {
+            T acc = T(0);
+            for (int j = 0; j < 3; ++j) {
+                acc += gM.m[i][j] * st.R.m[i][j];
+                gR.m[i][j] = s[i] * gM.m[i][j];
+            }
+            g.scale[i] = acc;
+        }
+        // splatting/math.py:13-28 adj_reference_rotation.
+        {
+            const T r = q[0], x = q[1], y = q[2], z = q[3];
+            const auto& G = gR.m;
+            g.quat[0] = T(2) * (z * (G[0][1] - G[1][0]) + y * (G[2][0] - G[0][2]) + x * (G[1][2] - G[2][1]));
+            g.quat[1] = T(2) * (y * (G[0][1] + G[1][0]) + z * (G[0][2] + G[2][0]) + r * (G[1][2] - G[2][1])) -
+                        T(4) * x * (G[1][1] + G[2][2]);
+            g.quat[2] = T(2) * (x * (G[0][1] + G[1][0]) + r * (G[2][0] - G[0][2]) + z * (G[1][2] + G[2][1])) -
+                        T(4) * y * (G[0][0] + G[2][2]);
+            g.quat[3] = T(2) * (r * (G[0][1] - G[1][0]) + x * (G[0][2] + G[2][0]) + y * (G[1][2] + G[2][1])) -
+                        T(4) * z * (G[0][0] + G[1][1]);
+        }
+        // W[i][j] = V[j][i]
+        for (int i = 0; i < 3; ++i)
+            for (int j = 0; j < 3; ++j) g.view[j][i] += gW.m[i][j];
+        // J entries depend on the clamped point t.
+        const T* t = st.t;
+        T gt[3];
+        const T tz2 = t[2] * t[2];
+        gt[0] = gJ.m[2][0] * (-fx / tz2);
+        gt[1] = gJ.m[2][1] * (-fy / tz2);
+        gt[2] = gJ.m[0][0] * (-fx / tz2) + gJ.m[1][1] * (-fy / tz2) +
+                gJ.m[2][0] * (T(2) * fx * t[0] / (tz2 * t[2])) +
+                gJ.m[2][1] * (T(2) * fy * t[1] / (tz2 * t[2]));
+        // splatting/geometry.py:42-51 adj_clamp_point.
+        const T xr = pos[0] / pos[2], yr = pos[1] / pos[2];
+        T gpos[3];
+        gpos[0] = gt[0] * T(xr >= -st.limx && xr <= st.limx ? 1 : 0);
+        gpos[1] = gt[1] * T(yr >= -st.limy && yr <= st.limy ? 1 : 0);
+        gpos[2] = gt[2];
+        // pos = V * [mean, 1] (rows 0..2)
+        for (int r = 0; r < 3; ++r) {
+            for (int c = 0; c < 3; ++c) {
+                g.mean[c] += gpos[r] * V.m[r][c];
+                g.view[r][c] += gpos[r] * mean[c];
+            }
+            g.view[r][3] += gpos[r];
+        }
+    }
+    // Centre path, splatting/geometry.py:106-123.
+    {
+        T clip[4];
+        for (int r = 0; r < 4; ++r) clip[r] = point_row(P, r, mean);
+        const T inv_w = T(1) / (clip[3] + T(0.0000001));
+        const T gnx = gc[0] * (T(0.5) * T(width));
+        const T gny = gc[1] * (T(0.5) * T(height));
+        T gclip[4];
+        gclip[0] = gnx * inv_w;
+        gclip[1] = gny * inv_w;
+        gclip[2] = T(0);
+        const T ginv = gnx * clip[0] + gny * clip[1];
+        gclip[3] = -ginv * inv_w * inv_w;
+        for (int r = 0; r < 4; ++r) {
+            for (int c = 0; c < 3; ++c) {
+                g.mean[c] += gclip[r] * P.m[r][c];
+                g.proj[r][c] += gclip[r] * mean[c];
+            }
+            g.proj[r][3] += gclip[r];
+        }
+    }
+}
+
+// Differentiable scalar projection_loss (gs3d/projection.py:198-210), used
+// only by the float64 finite-difference tests.
+template <class T>
+T projection_loss(const T mean[3], const T q[4], const T s[3], T opacity, const M4<T>& V,
+                  const M4<T>& P, int width, int height, T fx, T fy, const T gc[2], const T gk[4]) {
+    T pos[3];
+    for (int r = 0; r < 3; ++r) pos[r] = point_row(V, r, mean);
+    CovState<T> st;
+    T cov[3], inv[3];
+    screen_covariance<T>(pos, q, s, V, width, height, fx, fy, st, cov);
+    invert_covariance<T>(cov, inv);
+    T clip[4];
+    for (int r = 0; r < 4; ++r) clip[r] = point_row(P, r, mean);
+    const T inv_w = T(1) / (clip[3] + T(0.0000001));
+    const T cx = ((clip[0] * inv_w + T(1)) * T(width) - T(1)) * T(0.5);
+    const T cy = ((clip[1] * inv_w + T(1)) * T(height) - T(1)) * T(0.5);
+    return cx * gc[0] + cy * gc[1] + inv[0] * gk[0] + inv[1] * gk[1] + inv[2] * gk[2] + opacity * gk[3];
+}
+
+// ---------------------------------------------------------------------------
+// Blending helpers shared by forward and backward (gs3d/render.py:85-108,
+// :276-290).  The reference leaves contraction to the CUDA compiler; the
+// fixed choice here is
+//   power = fma(-0.5, fma(c0*dx, dx, (c2*dy)*dy), -((c1*dx)*dy))
+//   colour = fma(f, alpha*T, colour)
+// ---------------------------------------------------------------------------
+inline float blend_power(const float conic[4], float dx, float dy) {
+    const float q = fmaf(conic[0] * dx, dx, (conic[2] * dy) * dy);
+    return fmaf(-0.5f, q, -((conic[1] * dx) * dy));
+}
+
+int g_threads = 1;
+
+// Accumulation shared between threads (render backward, camera gradients).
+inline void acc(float* p, float v) {
+#pragma omp atomic
+    *p += v;
+}
+
+}  // namespace
+
+extern "C" {
+
+int oracle_abi_version(void) { return 1; }
+
+// Threads used by the per-Gaussian and per-pixel loops.  With 1 thread every
+// accumulation happens in a fixed order (deterministic results).
+int oracle_set_threads(int n) {
+    g_threads = n < 1 ? 1 : n;
+    return g_threads;
+}
+
+// ---------------------------------------------------------------------------
+// splatting/camera_kernels.py:11-66 prepare_kernel (no contraction).
+// ---------------------------------------------------------------------------
+int oracle_camera_prepare(const float* views, const float* Ks, int32_t count, int32_t width,
+                          int32_t height, int32_t with_centers, float* full, float* inverse,
+                          float* centers, int32_t* errors) {
+    for (int i = 0; i < count; ++i) {
+        const float* K = Ks + 9 * i;
+        const float* V = views + 16 * i;
+        bool finite = true;
+        for (int e = 0; e < 9; ++e) finite = finite && std::isfinite(K[e]);
+        int error = 0;
+        if (!finite || K[0] <= 0.0f || K[4] <= 0.0f)
+            error = 2;
+        else if (K[1] != 0.0f || K[3] != 0.0f || K[6] != 0.0f || K[7] != 0.0f || K[8] != 1.0f)
+            error = 1;
+        errors[i] = error;
+        if (error) continue;
+        const float px = 2.0f * K[0] / (float)width;
+        const float py = 2.0f * K[4] / (float)height;
+        const float cx = 2.0f * K[2] / (float)width - 1.0f;
+        const float cy = 2.0f * K[5] / (float)height - 1.0f;
+        float* F = full + 16 * i;
+        for (int col = 0; col < 4; ++col) {
+            F[col] = px * V[col] + cx * V[8 + col];
+            F[4 + col] = py * V[4 + col] + cy * V[8 + col];
+            F[8 + col] = V[8 + col];
+            F[12 + col] = V[8 + col];
+        }
+        if (with_centers) {
+            // wp.determinant / wp.inverse: cofactor expansion (adjugate / det).
+            const float* m = V;
+            float inv[16];
+            inv[0] = m[5] * m[10] * m[15] - m[5] * m[11] * m[14] - m[9] * m[6] * m[15] + m[9] * m[7] * m[14] +
+                     m[13] * m[6] * m[11] - m[13] * m[7] * m[10];
+            inv[4] = -m[4] * m[10] * m[15] + m[4] * m[11] * m[14] + m[8] * m[6] * m[15] - m[8] * m[7] * m[14] -
+                     m[12] * m[6] * m[11] + m[12] * m[7] * m[10];
+            inv[8] = m[4] * m[9] * m[15] - m[4] * m[11] * m[13] - m[8] * m[5] * m[15] + m[8] * m[7] * m[13] +
+                     m[12] * m[5] * m[11] - m[12] * m[7] * m[9];
+            inv[12] = -m[4] * m[9] * m[14] + m[4] * m[10] * m[13] + m[8] * m[5] * m[14] - m[8] * m[6] * m[13] -
+                      m[12] * m[5] * m[10] + m[12] * m[6] * m[9];
+            inv[1] = -m[1] * m[10] * m[15] + m[1] * m[11] * m[14] + m[9] * m[2] * m[15] - m[9] * m[3] * m[14] -
+                     m[13] * m[2] * m[11] + m[13] * m[3] * m[10];
+            inv[5] = m[0] * m[10] * m[15] - m[0] * m[11] * m[14] - m[8] * m[2] * m[15] + m[8] * m[3] * m[14] +
+                     m[12] * m[2] * m[11] - m[12] * m[3] * m[10];
+            inv[9] = -m[0] * m[9] * m[15] + m[0] * m[11] * m[13] + m[8] * m[1] * m[15] - m[8] * m[3] * m[13] -
+                     m[12] * m[1] * m[11] + m[12] * m[3] * m[9];
+            inv[13] = m[0] * m[9] * m[14] - m[0] * m[10] * m[13] - m[8] * m[1] * m[14] + m[8] * m[2] * m[13] +
+                      m[12] * m[1] * m[10] - m[12] * m[2] * m[9];
+            inv[2] = m[1] * m[6] * m[15] - m[1] * m[7] * m[14] - m[5] * m[2] * m[15] + m[5] * m[3] * m[14] +
+                     m[13] * m[2] * m[7] - m[13] * m[3] * m[6];
+            inv[6] = -m[0] * m[6] * m[15] + m[0] * m[7] * m[14] + m[4] * m[2] * m[15] - m[4] * m[3] * m[14] -
+                     m[12] * m[2] * m[7] + m[12] * m[3] * m[6];
+            inv[10] = m[0] * m[5] * m[15] - m[0] * m[7] * m[13] - m[4] * m[1] * m[15] + m[4] * m[3] * m[13] +
+                      m[12] * m[1] * m[7] - m[12] * m[3] * m[5];
+            inv[14] = -m[0] * m[5] * m[14] + m[0] * m[6] * m[13] + m[4] * m[1] * m[14] - m[4] * m[2] * m[13] -
+                      m[12] * m[1] * m[6] + m[12] * m[2] * m[5];
+            inv[3] = -m[1] * m[6] * m[11] + m[1] * m[7] * m[10] + m[5] * m[2] * m[11] - m[5] * m[3] * m[10] -
+                     m[9] * m[2] * m[7] + m[9] * m[3] * m[6];
+            inv[7] = m[0] * m[6] * m[11] - m[0] * m[7] * m[10] - m[4] * m[2] * m[11] + m[4] * m[3] * m[10] +
+                     m[8] * m[2] * m[7] - m[8] * m[3] * m[6];
+            inv[11] = -m[0] * m[5] * m[11] + m[0] * m[7] * m[9] + m[4] * m[1] * m[11] - m[4] * m[3] * m[9] -
+                      m[8] * m[1] * m[7] + m[8] * m[3] * m[5];
+            inv[15] = m[0] * m[5] * m[10] - m[0] * m[6] * m[9] - m[4] * m[1] * m[10] + m[4] * m[2] * m[9] +
+                      m[8] * m[1] * m[6] - m[8] * m[2] * m[5];
+            const float det = m[0] * inv[0] + m[1] * inv[4] + m[2] * inv[8] + m[3] * inv[12];
+            if (det == 0.0f) {
+                errors[i] = 3;
+                continue;
+            }
+            const float rdet = 1.0f / det;
+            for (int e = 0; e < 16; ++e) inverse[16 * i + e] = inv[e] * rdet;
+            for (int r = 0; r < 3; ++r) centers[3 * i + r] = inverse[16 * i + 4 * r + 3];
+        }
+    }
+    return 0;
+}
+
+// splatting/camera_kernels.py:69-106 backward_kernel.
+int oracle_camera_backward(const float* Ks, const float* grad_full, int32_t width, int32_t height,
+                           const float* inverse, const float* grad_centers, int32_t count,
+                           float* grad_views) {
+    for (int i = 0; i < count; ++i) {
+        const float* K = Ks + 9 * i;
+        const float px = 2.0f * K[0] / (float)width;
+        const float py = 2.0f * K[4] / (float)height;
+        const float cx = 2.0f * K[2] / (float)width - 1.0f;
+        const float cy = 2.0f * K[5] / (float)height - 1.0f;
+        const float* G = grad_full ? grad_full + 16 * i : nullptr;
+        for (int row = 0; row < 4; ++row)
+            for (int col = 0; col < 4; ++col) {
+                float value = 0.0f;
+                if (G) {
+                    if (row == 0)
+                        value = px * G[col];
+                    else if (row == 1)
+                        value = py * G[4 + col];
+                    else if (row == 2)
+                        value = (cx * G[col] + cy * G[4 + col]) + G[8 + col] + G[12 + col];
+                }
+                if (grad_centers) {
+                    const float* inv = inverse + 16 * i;
+                    float vjp = 0.0f;
+                    for (int k = 0; k < 3; ++k) vjp += inv[4 * k + row] * grad_centers[3 * i + k];
+                    value -= vjp * inv[4 * col + 3];
+                }
+                grad_views[16 * i + 4 * row + col] = value;
+            }
+    }
+    return 0;
+}
+
+// gs3d/projection.py:89-164 (+ primitives/sh.py:44-79, splatting/metadata.py:12-31).
+int oracle_project_fwd(const gs3d_project_args* a) {
+    const int64_t n = a->n;
+    for (int v = 0; v < a->views; ++v) {
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+        for (int64_t i = 0; i < n; ++i) {
+            const int64_t row = v * n + i;
+            ProjOut o;
+            const bool vis = project_one(a->means + 3 * i, a->quats + 4 * i, a->scales + 3 * i, a->opacities[i],
+                                         a->view + 16 * v, a->projection + 16 * v, a->intrinsics + 9 * v, a->width,
+                                         a->height, a->near_plane, a->far_plane, a->radius_clip, o);
+            a->centers[2 * row] = o.center[0];
+            a->centers[2 * row + 1] = o.center[1];
+            for (int k = 0; k < 4; ++k) a->conics[4 * row + k] = o.conic[k];
+            a->radii[row] = o.radius;
+            a->tiles[row] = o.tiles;
+            a->depths[row] = o.depth;
+            if (a->sh) {
+                const float* coef = a->sh + v * a->sh_view_stride + (int64_t)3 * a->sh_rows * i;
+                float dir[3] = {0.0f, 0.0f, 0.0f};
+                if (a->sh_degree > 0)
+                    for (int k = 0; k < 3; ++k) dir[k] = a->means[3 * i + k] - a->camera_centers[3 * v + k];
+                float color[3], raw[3];
+                sh_eval(coef, dir, a->sh_degree, vis, color, raw);
+                for (int k = 0; k < 3; ++k) a->colors[3 * row + k] = color[k];
+            }
+            if (a->means2d) {
+                a->means2d[2 * row] = vis ? o.center[0] : 0.0f;
+                a->means2d[2 * row + 1] = vis ? o.center[1] : 0.0f;
+                a->meta_opacities[row] = vis ? o.conic[3] : 0.0f;
+                for (int k = 0; k < 3; ++k) a->meta_conics[3 * row + k] = vis ? o.conic[k] : 0.0f;
+            }
+        }
+    }
+    return 0;
+}
+
+// primitives/sh.py:44-79 standalone.
+int oracle_sh_fwd(const float* coefficients, int32_t rows, const float* directions, const int32_t* radii,
+                  int32_t n, int32_t degree, float* colors, uint8_t* active) {
+    for (int64_t i = 0; i < n; ++i) {
+        const bool vis = radii ? radii[i] > 0 : true;
+        float color[3], raw[3];
+        sh_eval(coefficients + (int64_t)3 * rows * i, directions + 3 * i, degree, vis, color, raw);
+        for (int k = 0; k < 3; ++k) {
+            colors[3 * i + k] = color[k];
+            if (active) active[3 * i + k] = (vis && raw[k] >= 0.0f) ? 1 : 0;
+        }
+    }
+    return 0;
+}
+
+// primitives/sh.py:82-138 standalone.
+int oracle_sh_bwd(const float* coefficients, int32_t rows, const float* directions, const int32_t* radii,
+                  const uint8_t* active, const float* upstream, int32_t n, int32_t degree,
+                  float* grad_coefficients, float* grad_directions) {
+    for (int64_t i = 0; i < n; ++i) {
+        const bool vis = radii ? radii[i] > 0 : true;
+        const bool act[3] = {active[3 * i] != 0, active[3 * i + 1] != 0, active[3 * i + 2] != 0};
+        float gd[3];
+        sh_backward_row(coefficients + (int64_t)3 * rows * i, directions + 3 * i, degree, vis, act, upstream + 3 * i,
+                        grad_coefficients ? grad_coefficients + (int64_t)3 * rows * i : nullptr, rows, gd);
+        if (grad_directions)
+            for (int k = 0; k < 3; ++k) grad_directions[3 * i + k] = gd[k];
+    }
+    return 0;
+}
+
+// gs3d/projection.py:213-285 (+ primitives/sh.py:82-138 and the
+// means - centre VJP of gs3d/api.py:160-164).  Sequential accumulation.
+int oracle_project_bwd(const gs3d_project_bwd_args* a) {
+    const int64_t n = a->n;
+    const int K = a->sh_rows;
+    if (a->grad_sh) {
+        const int64_t per = a->sh_view_stride ? a->sh_view_stride * a->views : (int64_t)3 * K * n;
+        std::fill(a->grad_sh, a->grad_sh + per, 0.0f);
+    }
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int64_t i = 0; i < n; ++i) {
+        float gco[3 * 64];
+        double gm[3] = {0, 0, 0}, gq[4] = {0, 0, 0, 0}, gs[3] = {0, 0, 0}, go = 0;
+        for (int v = 0; v < a->views; ++v) {
+            const int64_t row = v * n + i;
+            if (a->radii[row] > 0) {
+                const M4<float> V = load44<float>(a->view + 16 * v);
+                const M4<float> P = load44<float>(a->projection + 16 * v);
+                const float* gcp = a->grad_centers + row * a->grad_centers_stride;
+                const float* gkp = a->grad_conics + row * a->grad_conics_stride;
+                const float gc[2] = {gcp[0], gcp[1]};
+                const float gk[4] = {gkp[0], gkp[1], gkp[2], gkp[3]};
+                ProjGrad<float> g;
+                projection_vjp<float>(a->means + 3 * i, a->quats + 4 * i, a->scales + 3 * i, a->opacities[i], V, P,
+                                      a->width, a->height, a->intrinsics[9 * v], a->intrinsics[9 * v + 4], gc, gk, g);
+                for (int k = 0; k < 3; ++k) gm[k] += g.mean[k];
+                for (int k = 0; k < 4; ++k) gq[k] += g.quat[k];
+                for (int k = 0; k < 3; ++k) gs[k] += g.scale[k];
+                go += g.opacity;
+                if (a->grad_view)
+                    for (int r = 0; r < 4; ++r)
+                        for (int c = 0; c < 4; ++c) acc(&a->grad_view[16 * v + 4 * r + c], g.view[r][c]);
+                if (a->grad_projection)
+                    for (int r = 0; r < 4; ++r)
+                        for (int c = 0; c < 4; ++c) acc(&a->grad_projection[16 * v + 4 * r + c], g.proj[r][c]);
+            }
+            if (a->sh) {
+                const float* coef = a->sh + v * a->sh_view_stride + (int64_t)3 * K * i;
+                const bool vis = a->radii[row] > 0;
+                float dir[3] = {0.0f, 0.0f, 0.0f};
+                if (a->sh_degree > 0)
+                    for (int k = 0; k < 3; ++k) dir[k] = a->means[3 * i + k] - a->camera_centers[3 * v + k];
+                float color[3], raw[3];
+                sh_eval(coef, dir, a->sh_degree, vis, color, raw);
+                const bool act[3] = {vis && raw[0] >= 0.0f, vis && raw[1] >= 0.0f, vis && raw[2] >= 0.0f};
+                const float* gcol = a->grad_colors + row * a->grad_colors_stride;
+                const float up[3] = {gcol[0], gcol[1], gcol[2]};
+                float gd[3];
+                sh_backward_row(coef, dir, a->sh_degree, vis, act, up, gco, K, gd);
+                if (a->grad_sh) {
+                    float* dst = a->grad_sh + v * a->sh_view_stride + (int64_t)3 * K * i;
+                    for (int e = 0; e < 3 * K; ++e) dst[e] += gco[e];
+                }
+                if (a->sh_degree > 0) {
+                    for (int k = 0; k < 3; ++k) gm[k] += gd[k];
+                    if (a->grad_camera_centers)
+                        for (int k = 0; k < 3; ++k) acc(&a->grad_camera_centers[3 * v + k], -gd[k]);
+                }
+            }
+        }
+        if (a->grad_means)
+            for (int k = 0; k < 3; ++k) a->grad_means[3 * i + k] = (float)gm[k];
+        if (a->grad_quats)
+            for (int k = 0; k < 4; ++k) a->grad_quats[4 * i + k] = (float)gq[k];
+        if (a->grad_scales)
+            for (int k = 0; k < 3; ++k) a->grad_scales[3 * i + k] = (float)gs[k];
+        if (a->grad_opacities) a->grad_opacities[i] = (float)go;
+    }
+    return 0;
+}
+
+// float64 instantiations for finite-difference tests of the VJP.
+double oracle_projection_loss_f64(const double* mean, const double* quat, const double* scale, double opacity,
+                                  const double* view, const double* proj, int32_t width, int32_t height, double fx,
+                                  double fy, const double* gc, const double* gk) {
+    M4<double> V, P;
+    for (int i = 0; i < 16; ++i) {
+        V.m[i / 4][i % 4] = view[i];
+        P.m[i / 4][i % 4] = proj[i];
+    }
+    return projection_loss<double>(mean, quat, scale, opacity, V, P, width, height, fx, fy, gc, gk);
+}
+
+int oracle_projection_vjp_f64(const double* mean, const double* quat, const double* scale, double opacity,
+                              const double* view, const double* proj, int32_t width, int32_t height, double fx,
+                              double fy, const double* gc, const double* gk, double* out /* 3+4+3+1+16+16 */) {
+    M4<double> V, P;
+    for (int i = 0; i < 16; ++i) {
+        V.m[i / 4][i % 4] = view[i];
+        P.m[i / 4][i % 4] = proj[i];
+    }
+    ProjGrad<double> g;
+    projection_vjp<double>(mean, quat, scale, opacity, V, P, width, height, fx, fy, gc, gk, g);
+    int o = 0;
+    for (int k = 0; k < 3; ++k) out[o++] = g.mean[k];
+    for (int k = 0; k < 4; ++k) out[o++] = g.quat[k];
+    for (int k = 0; k < 3; ++k) out[o++] = g.scale[k];
+    out[o++] = g.opacity;
+    for (int r = 0; r < 4; ++r)
+        for (int c = 0; c < 4; ++c) out[o++] = g.view[r][c];
+    for (int r = 0; r < 4; ++r)
+        for (int c = 0; c < 4; ++c) out[o++] = g.proj[r][c];
+    return 0;
+}
+
+// Forward intermediates for the custom-adjoint known-answer tests.
+float oracle_expf(float x) { return gs_expf(x); }
+
+int oracle_glm_rotation(const float* q, float* out) {
+    M3<float> R = glm_rotation<float>(q);
+    for (int i = 0; i < 9; ++i) out[i] = R.m[i / 3][i % 3];
+    return 0;
+}
+
+// SH basis / gradient access for tests.
+float oracle_sh_basis(const float* u, int32_t k) { return sh_basis(u, k); }
+int oracle_sh_basis_grad(const float* u, int32_t k, float* g) {
+    sh_basis_grad(u, k, g);
+    return 0;
+}
+
+// primitives/tiling.py:57-64 scan_counts (inclusive), 64-bit total.
+int oracle_scan_i32(const int32_t* counts, int64_t n, int32_t* offsets, int64_t* total) {
+    int64_t s = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        s += counts[i];
+        offsets[i] = (int32_t)s;
+    }
+    if (total) *total = s;
+    return 0;
+}
+
+// splatting/binning.py:16-37 duplicate + primitives/tiling.py:32-36 sort_key.
+int oracle_emit_keys(const gs3d_emit_args* a) {
+    const int gx = (a->width + 15) / 16, gy = (a->height + 15) / 16;
+    const int64_t tiles_per_view = (int64_t)gx * gy;
+    const int64_t rows = (int64_t)a->n * a->views;
+    for (int64_t r = 0; r < rows; ++r) {
+        if (a->radii[r] <= 0) continue;
+        const int64_t v = r / a->n;
+        int b[4];
+        tile_bounds(a->centers + 2 * r, a->radii[r], gx, gy, b);
+        int64_t off = r > 0 ? a->offsets[r - 1] : 0;
+        uint32_t bits;
+        std::memcpy(&bits, a->depths + r, 4);
+        for (int y = b[1]; y < b[3]; ++y)
+            for (int x = b[0]; x < b[2]; ++x) {
+                const uint64_t tile = (uint64_t)(uint32_t)(v * tiles_per_view + y * gx + x);
+                a->keys[off] = (tile << 32) | (uint64_t)bits;
+                a->values[off] = (int32_t)(r % a->n);
+                ++off;
+            }
+    }
+    return 0;
+}
+
+// primitives/tiling.py:67-86: stable sort on key bits [0, end_bit).
+int oracle_sort_pairs_u64(uint64_t* keys, int32_t* values, int64_t count, int32_t end_bit) {
+    const uint64_t mask = end_bit >= 64 ? ~0ull : ((1ull << end_bit) - 1ull);
+    std::vector<int64_t> idx(count);
+    std::iota(idx.begin(), idx.end(), 0);
+    std::stable_sort(idx.begin(), idx.end(),
+                     [&](int64_t x, int64_t y) { return (keys[x] & mask) < (keys[y] & mask); });
+    std::vector<uint64_t> k2(count);
+    std::vector<int32_t> v2(count);
+    for (int64_t i = 0; i < count; ++i) {
+        k2[i] = keys[idx[i]];
+        v2[i] = values[idx[i]];
+    }
+    std::copy(k2.begin(), k2.end(), keys);
+    std::copy(v2.begin(), v2.end(), values);
+    return 0;
+}
+
+// primitives/tiling.py:39-54 identify_ranges.
+int oracle_tile_ranges(const uint64_t* keys, int64_t count, int32_t* ranges, int64_t tile_count) {
+    (void)tile_count;
+    for (int64_t i = 0; i < count; ++i) {
+        const uint32_t cur = (uint32_t)(keys[i] >> 32);
+        if (i == 0) {
+            if (cur != 0xFFFFFFFFu) ranges[2 * (int64_t)cur] = 0;
+        } else {
+            const uint32_t prev = (uint32_t)(keys[i - 1] >> 32);
+            if (cur != prev) {
+                if (prev != 0xFFFFFFFFu) ranges[2 * (int64_t)prev + 1] = (int32_t)i;
+                if (cur != 0xFFFFFFFFu) ranges[2 * (int64_t)cur] = (int32_t)i;
+            }
+        }
+        if (i == count - 1 && cur != 0xFFFFFFFFu) ranges[2 * (int64_t)cur + 1] = (int32_t)count;
+    }
+    return 0;
+}
+
+// Assemble the blended vector of one Gaussian (gs3d/autograd.py:41-46).
+static inline void gather_features(const gs3d_render_args* a, int v, int64_t g, float* out) {
+    int c = 0;
+    const float* f = a->features + v * a->feat_view_stride + g * a->feat_stride;
+    for (int k = 0; k < a->feat_channels; ++k) out[c++] = f[k];
+    if (a->extra_channels) {
+        const float* e = a->extra + v * a->extra_view_stride + g * a->extra_stride;
+        for (int k = 0; k < a->extra_channels; ++k) out[c++] = e[k];
+    }
+    if (a->one_tail) out[c++] = 1.0f;
+}
+
+static inline int total_channels(const gs3d_render_args* a) {
+    return a->feat_channels + a->extra_channels + (a->one_tail ? 1 : 0);
+}
+
+// gs3d/render.py:36-126 forward, one pixel at a time.
+int oracle_render_fwd(const gs3d_render_args* a) {
+    const int W = a->width, H = a->height;
+    const int gx = (W + 15) / 16, gy = (H + 15) / 16;
+    const int D = total_channels(a);
+    std::vector<float> bg(D);
+    for (int v = 0; v < a->views; ++v) {
+        for (int k = 0; k < D; ++k)
+            bg[k] = (a->background && k < a->feat_channels) ? a->background[v * a->background_view_stride + k] : 0.0f;
+#pragma omp parallel for schedule(dynamic, 4) num_threads(g_threads)
+        for (int y = 0; y < H; ++y) {
+            std::vector<float> color(D), f(D);
+            for (int x = 0; x < W; ++x) {
+                const int64_t tile = (int64_t)v * gx * gy + (y / 16) * gx + (x / 16);
+                const int first = a->ranges[2 * tile], last = a->ranges[2 * tile + 1];
+                float T = 1.0f;
+                std::fill(color.begin(), color.end(), 0.0f);
+                int contributor = 0, last_contributor = 0;
+                for (int idx = first; idx < last; ++idx) {
+                    contributor += 1;
+                    const int64_t g = a->ids[idx];
+                    const int64_t row = (int64_t)v * a->n + g;
+                    const float dx = a->centers[2 * row] - (float)x;
+                    const float dy = a->centers[2 * row + 1] - (float)y;
+                    const float* conic = a->conics + 4 * row;
+                    const float power = blend_power(conic, dx, dy);
+                    if (!(power <= 0.0f)) continue;
+                    const float alpha = std::min(0.99f, conic[3] * gs_expf(power));
+                    if (!(alpha >= 1.0f / 255.0f)) continue;
+                    const float next_t = T * (1.0f - alpha);
+                    if (next_t < 0.0001f) break;
+                    gather_features(a, v, g, f.data());
+                    const float w = alpha * T;
+                    for (int k = 0; k < D; ++k) color[k] = fmaf(f[k], w, color[k]);
+                    T = next_t;
+                    last_contributor = contributor;
+                }
+                const int64_t pix = ((int64_t)v * H + y) * W + x;
+                for (int k = 0; k < D; ++k) a->image[pix * D + k] = fmaf(T, bg[k], color[k]);
+                a->final_t[pix] = T;
+                a->contributors[pix] = last_contributor;
+            }
+        }
+    }
+    return 0;
+}
+
+// gs3d/render.py:211-356 backward, sequential accumulation per pixel in
+// tile-then-row-major order (the GPU sums the same terms in another order).
+int oracle_render_bwd(const gs3d_render_bwd_args* b) {
+    const gs3d_render_args* a = &b->fwd;
+    const int W = a->width, H = a->height;
+    const int gx = (W + 15) / 16, gy = (H + 15) / 16;
+    const int D = total_channels(a);
+    const int Dg = D - (a->one_tail ? 1 : 0);
+    std::vector<float> bg(D);
+    for (int v = 0; v < a->views; ++v) {
+        for (int k = 0; k < D; ++k)
+            bg[k] = (a->background && k < a->feat_channels) ? a->background[v * a->background_view_stride + k] : 0.0f;
+#pragma omp parallel for schedule(dynamic, 4) num_threads(g_threads)
+        for (int y = 0; y < H; ++y) {
+            std::vector<float> grad(D), accum(D), last_color(D), f(D);
+            for (int x = 0; x < W; ++x) {
+                const int64_t tile = (int64_t)v * gx * gy + (y / 16) * gx + (x / 16);
+                const int first = a->ranges[2 * tile], last = a->ranges[2 * tile + 1];
+                const int64_t pix = ((int64_t)v * H + y) * W + x;
+                const float final_T = a->final_t[pix];
+                float T = final_T;
+                const int last_contributor = a->contributors[pix];
+                float bg_grad = 0.0f;
+                for (int k = 0; k < D; ++k) {
+                    grad[k] = b->upstream[pix * D + k];
+                    bg_grad += bg[k] * grad[k];
+                    accum[k] = 0.0f;
+                    last_color[k] = 0.0f;
+                }
+                float last_alpha = 0.0f;
+                int contributor = last - first;
+                for (int idx = last - 1; idx >= first; --idx) {
+                    contributor -= 1;
+                    if (!(contributor < last_contributor)) continue;
+                    const int64_t g = a->ids[idx];
+                    const int64_t row = (int64_t)v * a->n + g;
+                    const float dx = a->centers[2 * row] - (float)x;
+                    const float dy = a->centers[2 * row + 1] - (float)y;
+                    const float* conic = a->conics + 4 * row;
+                    const float power = blend_power(conic, dx, dy);
+                    if (!(power <= 0.0f)) continue;
+                    const float G = gs_expf(power);
+                    const float alpha = std::min(0.99f, conic[3] * G);
+                    if (!(alpha >= 1.0f / 255.0f)) continue;
+                    T = T / (1.0f - alpha);
+                    gather_features(a, v, g, f.data());
+                    float grad_alpha = 0.0f;
+                    for (int k = 0; k < D; ++k) {
+                        accum[k] = last_alpha * last_color[k] + (1.0f - last_alpha) * accum[k];
+                        last_color[k] = f[k];
+                        grad_alpha += (f[k] - accum[k]) * grad[k];
+                        if (k < Dg) {
+                            const float gv = alpha * T * grad[k];
+                            if (k < a->feat_channels) {
+                                if (b->grad_features)
+                                    acc(&b->grad_features[v * b->grad_feat_view_stride + g * b->grad_feat_stride + k],
+                                        gv);
+                            } else if (b->grad_extra) {
+                                acc(&b->grad_extra[v * b->grad_extra_view_stride + g * b->grad_extra_stride +
+                                                   (k - a->feat_channels)],
+                                    gv);
+                            }
+                        }
+                    }
+                    grad_alpha = grad_alpha * T + (-final_T / (1.0f - alpha)) * bg_grad;
+                    last_alpha = alpha;
+                    const float gvv = conic[3] * grad_alpha;
+                    const float gdx = G * dx, gdy = G * dy;
+                    const float dcx = gvv * (-gdx * conic[0] - gdy * conic[1]);
+                    const float dcy = gvv * (-gdy * conic[2] - gdx * conic[1]);
+                    float* gc = b->grad_centers + row * b->grad_centers_stride;
+                    acc(&gc[0], dcx);
+                    acc(&gc[1], dcy);
+                    if (b->abs_centers) {
+                        float* ab = b->abs_centers + row * b->abs_stride;
+                        acc(&ab[0], std::fabs(dcx));
+                        acc(&ab[1], std::fabs(dcy));
+                    }
+                    float* gk = b->grad_conics + row * b->grad_conics_stride;
+                    acc(&gk[0], -0.5f * gdx * dx * gvv);
+                    acc(&gk[1], -gdx * dy * gvv);
+                    acc(&gk[2], -0.5f * gdy * dy * gvv);
+                    acc(&gk[3], G * grad_alpha);
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+}  // extern "C"
