@@ -1,0 +1,121 @@
+// Shared device helpers for the gfx950 gs3d kernels.
+//
+// Everything is compiled with -ffp-contract=off: a multiply followed by an
+// add stays two roundings unless the code calls fmaf explicitly.  The
+// projection, key and blend arithmetic below therefore reproduces a fixed
+// operation sequence (integer outputs and the forward image are bit-exact
+// against the CPU restatement that follows the same sequence).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gs3d_hip.h"
+
+#define GS3D_DEV __device__ __forceinline__
+
+namespace gs3d {
+
+// Host side: record and translate a launch error (defined in abi.hip).
+int launch_status(const char* where);
+void set_error(const char* message);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline unsigned blocks_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
+
+// ---------------------------------------------------------------------------
+// Branch-exact min/max/clamp: the C++ std::min/std::max selection rule
+// (first operand unless the comparison picks the second), so NaN handling is
+// the same on the host and the device.
+// ---------------------------------------------------------------------------
+GS3D_DEV float sel_max(float a, float b) { return (a < b) ? b : a; }
+GS3D_DEV float sel_min(float a, float b) { return (b < a) ? b : a; }
+GS3D_DEV float sel_clamp(float v, float lo, float hi) { return sel_min(sel_max(v, lo), hi); }
+
+// ---------------------------------------------------------------------------
+// exp for blending.  x = k ln2 + r, k = rint(x log2 e), two-constant
+// Cody-Waite reduction (the high part of ln2 has 15 significant bits, so
+// k*ln2_hi is exact for |k| < 512), degree-7 Taylor polynomial of e^r on
+// |r| <= ln2/2 in Horner form, exact scaling by 2^k.  Inputs below -86 give 0
+// (the result would be < 2^-124, three orders below the 1/255 threshold),
+// which also keeps every intermediate normal.
+// ---------------------------------------------------------------------------
+GS3D_DEV float blend_exp(float x) {
+    if (x < -86.0f) return 0.0f;
+    const float k = __builtin_rintf(x * 1.44269502e+00f);
+    float r = __builtin_fmaf(k, -6.93145752e-01f, x);
+    r = __builtin_fmaf(k, -1.42860677e-06f, r);
+    float p = 1.98412701e-04f;
+    p = __builtin_fmaf(p, r, 1.38888892e-03f);
+    p = __builtin_fmaf(p, r, 8.33333377e-03f);
+    p = __builtin_fmaf(p, r, 4.16666679e-02f);
+    p = __builtin_fmaf(p, r, 1.66666672e-01f);
+    p = __builtin_fmaf(p, r, 5.00000000e-01f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)k);
+}
+
+// Gaussian exponent of the blend (gs3d/render.py:87-94 with the contraction
+// fixed as fma(-0.5, fma(a dx, dx, (c dy) dy), -((b dx) dy))).
+GS3D_DEV float blend_power(float a, float b, float c, float dx, float dy) {
+    const float q = __builtin_fmaf(a * dx, dx, (c * dy) * dy);
+    return __builtin_fmaf(-0.5f, q, -((b * dx) * dy));
+}
+
+// ---------------------------------------------------------------------------
+// Wavefront (64-lane) reductions with DPP.  Within each row of 16 lanes a
+// butterfly (quad_perm swaps, then row rotations by 4 and 8) leaves the row
+// sum in every lane of the row; row_bcast15/row_bcast31 then fold the four
+// row sums into lane 63.
+// ---------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+GS3D_DEV float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+}
+
+GS3D_DEV float row_sum16(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x124>(v);  // row_ror:4
+    v += dpp_f<0x128>(v);  // row_ror:8
+    return v;
+}
+
+// Full wave sum; valid in lane 63.  All 64 lanes must be active.
+GS3D_DEV float wave_sum_to_lane63(float v) {
+    v = row_sum16(v);
+    v += dpp_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_f<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// Wave sum broadcast as a wave-uniform value.
+GS3D_DEV float wave_sum(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(v)), 63));
+}
+
+GS3D_DEV int lane_id() { return __lane_id(); }
+
+// ---------------------------------------------------------------------------
+// Tile rectangle of a projected Gaussian, splatting/geometry.py:22-30
+// (truncating conversions, then clamping to the tile grid).
+// ---------------------------------------------------------------------------
+GS3D_DEV int trunc_clamp(float v, int hi) {
+    int i = (int)v;
+    i = i < 0 ? 0 : i;
+    return i > hi ? hi : i;
+}
+
+GS3D_DEV int4 tile_rect(float cx, float cy, int radius, int gx, int gy) {
+    const float r = (float)radius;
+    int4 b;
+    b.x = trunc_clamp((cx - r) / 16.0f, gx);
+    b.y = trunc_clamp((cy - r) / 16.0f, gy);
+    b.z = trunc_clamp(((cx + r) + 16.0f - 1.0f) / 16.0f, gx);
+    b.w = trunc_clamp(((cy + r) + 16.0f - 1.0f) / 16.0f, gy);
+    return b;
+}
+
+}  // namespace gs3d

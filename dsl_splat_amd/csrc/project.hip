@@ -1,0 +1,945 @@
+// EWA projection, SH0-3 colour and training metadata (forward), and the
+// projection / SH VJP (backward), one thread per Gaussian looping over views.
+//
+// Forward: gs3d/projection.py:37-164 (screen_covariance + project),
+// splatting/geometry.py:22-123, splatting/math.py:8-47, primitives/math.py
+// :14-45, primitives/sh.py:7-79 (basis + evaluate), splatting/metadata.py
+// :12-31 (_prepare).  Backward: gs3d/projection.py:198-285 (projection_loss
+// reverse pass) with the custom adjoints of splatting/geometry.py:42-51, :61-71
+// and splatting/math.py:13-28, primitives/sh.py:82-138, and the Torch
+// "means - camera centre" VJP of gs3d/api.py:160-164.
+//
+// HBM layout: Gaussians are read once per launch (means/quats/scales/opacity
+// rows plus the SH block) and every view's outputs are written as contiguous
+// (views, N, ...) rows.  SH blocks (N, K, 3) are staged through LDS so that
+// global loads and stores are fully coalesced; each thread then reads its
+// row from LDS with an odd row pitch (conflict-free).
+#include "common.hpp"
+
+namespace gs3d {
+
+constexpr int kProjBlock = 128;
+
+struct M3 {
+    float m[3][3];
+};
+
+GS3D_DEV M3 transpose3(const M3& a) {
+    M3 r;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) r.m[i][j] = a.m[j][i];
+    return r;
+}
+
+// splatting/math.py:31-41: fma(a[r,2], b[2,c], fma(a[r,0], b[0,c], a[r,1]*b[1,c])).
+GS3D_DEV M3 ref_matmul(const M3& a, const M3& b) {
+    M3 r;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+            r.m[i][j] = __builtin_fmaf(a.m[i][2], b.m[2][j], __builtin_fmaf(a.m[i][0], b.m[0][j], a.m[i][1] * b.m[1][j]));
+    return r;
+}
+
+// splatting/math.py:44-47.
+GS3D_DEV float point_row(const float* M, int r, const float* p) {
+    const float xy = __builtin_fmaf(M[4 * r + 0], p[0], M[4 * r + 1] * p[1]);
+    return __builtin_fmaf(M[4 * r + 2], p[2], xy) + M[4 * r + 3];
+}
+
+// primitives/math.py:33-45.
+GS3D_DEV M3 glm_rotation(const float* q) {
+    const float r = q[0], x = q[1], y = q[2], z = q[3];
+    const float yy = y * y, zz = z * z;
+    const float rz = r * z, xz = x * z, rx = r * x;
+    const float d0 = yy + zz, d1 = __builtin_fmaf(x, x, zz), d2 = __builtin_fmaf(x, x, yy);
+    M3 R;
+    R.m[0][0] = 1.0f - (d0 + d0);
+    R.m[0][1] = 2.0f * __builtin_fmaf(x, y, rz);
+    R.m[0][2] = 2.0f * __builtin_fmaf(-r, y, xz);
+    R.m[1][0] = 2.0f * __builtin_fmaf(x, y, -rz);
+    R.m[1][1] = 1.0f - (d1 + d1);
+    R.m[1][2] = 2.0f * __builtin_fmaf(y, z, rx);
+    R.m[2][0] = 2.0f * __builtin_fmaf(r, y, xz);
+    R.m[2][1] = 2.0f * __builtin_fmaf(y, z, -rx);
+    R.m[2][2] = 1.0f - (d2 + d2);
+    return R;
+}
+
+struct CovParts {
+    float t[3];
+    float limx, limy;
+    M3 R, M, Sigma, J, W, Tm, X;
+};
+
+// gs3d/projection.py:37-86.
+GS3D_DEV void screen_covariance(const float* pos, const float* q, const float* s, const float* V, int width,
+                                int height, float fx, float fy, CovParts& st, float* cov) {
+    st.limx = 1.3f * (float)width / (2.0f * fx);
+    st.limy = 1.3f * (float)height / (2.0f * fy);
+    st.t[0] = sel_clamp(pos[0] / pos[2], -st.limx, st.limx) * pos[2];
+    st.t[1] = sel_clamp(pos[1] / pos[2], -st.limy, st.limy) * pos[2];
+    st.t[2] = pos[2];
+    st.R = glm_rotation(q);
+    M3 S;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) S.m[i][j] = 0.0f;
+    S.m[0][0] = s[0];
+    S.m[1][1] = s[1];
+    S.m[2][2] = s[2];
+    st.M = ref_matmul(S, st.R);
+    st.Sigma = ref_matmul(transpose3(st.M), st.M);
+    const float* t = st.t;
+    st.J.m[0][0] = fx / t[2];
+    st.J.m[0][1] = 0.0f;
+    st.J.m[0][2] = 0.0f;
+    st.J.m[1][0] = 0.0f;
+    st.J.m[1][1] = fy / t[2];
+    st.J.m[1][2] = 0.0f;
+    st.J.m[2][0] = -(fx * t[0]) / (t[2] * t[2]);
+    st.J.m[2][1] = -(fy * t[1]) / (t[2] * t[2]);
+    st.J.m[2][2] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) st.W.m[i][j] = V[4 * j + i];
+    st.Tm = ref_matmul(st.W, st.J);
+    st.X = ref_matmul(transpose3(st.Tm), transpose3(st.Sigma));
+    const M3 cov2 = ref_matmul(st.X, st.Tm);
+    cov[0] = cov2.m[0][0] + 0.3f;
+    cov[1] = cov2.m[1][0];
+    cov[2] = cov2.m[1][1] + 0.3f;
+}
+
+// splatting/geometry.py:106-123: fp32 divide, fp64 viewport, one rounding.
+GS3D_DEV void pixel_center(const float* mean, const float* P, int width, int height, float* out) {
+    float clip[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) clip[r] = point_row(P, r, mean);
+    const float inv_w = 1.0f / (clip[3] + 0.0000001f);
+    const double nx = (double)(clip[0] * inv_w);
+    const double ny = (double)(clip[1] * inv_w);
+    out[0] = (float)(((nx + 1.0) * (double)width - 1.0) * 0.5);
+    out[1] = (float)(((ny + 1.0) * (double)height - 1.0) * 0.5);
+}
+
+struct Footprint {
+    float center[2];
+    float conic[3];
+    int radius, tiles;
+    float depth;
+};
+
+// gs3d/projection.py:113-162 for one (Gaussian, view); false when culled.
+GS3D_DEV bool project_one(const float* mean, const float* q, const float* s, const float* V, const float* P,
+                          float fx, float fy, int width, int height, float near_plane, float far_plane,
+                          float radius_clip, Footprint& f) {
+    float t4[3];
+#pragma unroll
+    for (int r = 0; r < 3; ++r) t4[r] = point_row(V, r, mean);
+    if (t4[2] <= near_plane || t4[2] >= far_plane) return false;
+    CovParts st;
+    float cov[3];
+    screen_covariance(t4, q, s, V, width, height, fx, fy, st, cov);
+    const float a = cov[0], b = cov[1], c = cov[2];
+    const float det = a * c - b * b;
+    if (det == 0.0f) return false;
+    const float mid = 0.5f * (a + c);
+    const int radius = (int)__builtin_ceilf(3.0f * __builtin_sqrtf(mid + __builtin_sqrtf(sel_max(0.1f, mid * mid - det))));
+    if ((float)radius <= radius_clip) return false;
+    float center[2];
+    pixel_center(mean, P, width, height, center);
+    const int4 rect = tile_rect(center[0], center[1], radius, (width + 15) / 16, (height + 15) / 16);
+    const int count = (rect.z - rect.x) * (rect.w - rect.y);
+    if (count == 0) return false;
+    const float inv = 1.0f / (a * c - b * b);
+    f.center[0] = center[0];
+    f.center[1] = center[1];
+    f.conic[0] = c * inv;
+    f.conic[1] = -b * inv;
+    f.conic[2] = a * inv;
+    f.radius = radius;
+    f.tiles = count;
+    f.depth = t4[2];
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// SH basis (primitives/sh.py:7-41) with float32 constants, left-to-right
+// products, and its analytic gradient.
+// ---------------------------------------------------------------------------
+GS3D_DEV float sh_basis(const float* u, int k) {
+    const float x = u[0], y = u[1], z = u[2];
+    switch (k) {
+    case 0: return 0.28209479177387814f;
+    case 1: return -0.4886025119029199f * y;
+    case 2: return 0.4886025119029199f * z;
+    case 3: return -0.4886025119029199f * x;
+    case 4: return 1.0925484305920792f * x * y;
+    case 5: return -1.0925484305920792f * y * z;
+    case 6: return 0.31539156525252005f * (2.0f * z * z - x * x - y * y);
+    case 7: return -1.0925484305920792f * x * z;
+    case 8: return 0.5462742152960396f * (x * x - y * y);
+    case 9: return -0.5900435899266435f * y * (3.0f * x * x - y * y);
+    case 10: return 2.890611442640554f * x * y * z;
+    case 11: return -0.4570457994644658f * y * (4.0f * z * z - x * x - y * y);
+    case 12: return 0.3731763325901154f * z * (2.0f * z * z - 3.0f * x * x - 3.0f * y * y);
+    case 13: return -0.4570457994644658f * x * (4.0f * z * z - x * x - y * y);
+    case 14: return 1.445305721320277f * z * (x * x - y * y);
+    default: return -0.5900435899266435f * x * (x * x - 3.0f * y * y);
+    }
+}
+
+GS3D_DEV void sh_basis_grad(const float* u, int k, float* g) {
+    const float x = u[0], y = u[1], z = u[2];
+    const float C1 = 0.4886025119029199f, C4 = 1.0925484305920792f, C6 = 0.31539156525252005f,
+                C8 = 0.5462742152960396f, C9 = 0.5900435899266435f, C10 = 2.890611442640554f,
+                C11 = 0.4570457994644658f, C12 = 0.3731763325901154f, C14 = 1.445305721320277f;
+    g[0] = g[1] = g[2] = 0.0f;
+    switch (k) {
+    case 0: break;
+    case 1: g[1] = -C1; break;
+    case 2: g[2] = C1; break;
+    case 3: g[0] = -C1; break;
+    case 4: g[0] = C4 * y; g[1] = C4 * x; break;
+    case 5: g[1] = -C4 * z; g[2] = -C4 * y; break;
+    case 6: g[0] = C6 * (-2.0f * x); g[1] = C6 * (-2.0f * y); g[2] = C6 * (4.0f * z); break;
+    case 7: g[0] = -C4 * z; g[2] = -C4 * x; break;
+    case 8: g[0] = C8 * (2.0f * x); g[1] = C8 * (-2.0f * y); break;
+    case 9: g[0] = -C9 * (6.0f * x * y); g[1] = -C9 * (3.0f * x * x - 3.0f * y * y); break;
+    case 10: g[0] = C10 * y * z; g[1] = C10 * x * z; g[2] = C10 * x * y; break;
+    case 11:
+        g[0] = -C11 * (-2.0f * x * y);
+        g[1] = -C11 * (4.0f * z * z - x * x - 3.0f * y * y);
+        g[2] = -C11 * (8.0f * y * z);
+        break;
+    case 12:
+        g[0] = C12 * (-6.0f * x * z);
+        g[1] = C12 * (-6.0f * y * z);
+        g[2] = C12 * (6.0f * z * z - 3.0f * x * x - 3.0f * y * y);
+        break;
+    case 13:
+        g[0] = -C11 * (4.0f * z * z - 3.0f * x * x - y * y);
+        g[1] = -C11 * (-2.0f * x * y);
+        g[2] = -C11 * (8.0f * x * z);
+        break;
+    case 14: g[0] = C14 * (2.0f * x * z); g[1] = C14 * (-2.0f * y * z); g[2] = C14 * (x * x - y * y); break;
+    default: g[0] = -C9 * (3.0f * x * x - 3.0f * y * y); g[1] = -C9 * (-6.0f * x * y); break;
+    }
+}
+
+GS3D_DEV float length3(const float* d) { return __builtin_sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]); }
+
+// primitives/sh.py:58-77 for one row; raw receives the pre-clamp value.
+template <int DEG>
+GS3D_DEV void sh_eval(const float* coef, const float* dir, bool visible, float* color, float* raw) {
+    float value[3] = {0.0f, 0.0f, 0.0f};
+    if (visible) {
+        float unit[3] = {0.0f, 0.0f, 0.0f};
+        if (DEG > 0) {
+            const float len = sel_max(length3(dir), 1.0e-12f);
+#pragma unroll
+            for (int i = 0; i < 3; ++i) unit[i] = dir[i] / len;
+        }
+#pragma unroll
+        for (int k = 0; k < (DEG + 1) * (DEG + 1); ++k) {
+            const float b = sh_basis(unit, k);
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) value[ch] = value[ch] + b * coef[3 * k + ch];
+        }
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) value[ch] = value[ch] + 0.5f;
+    }
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch) {
+        raw[ch] = value[ch];
+        color[ch] = sel_max(value[ch], 0.0f);
+    }
+}
+
+// primitives/sh.py:100-136 for one row.  grad_coef receives (DEG+1)^2 * 3
+// values (added to it when ACC, which lets views accumulate in place).
+template <int DEG, bool ACC>
+GS3D_DEV void sh_backward(const float* coef, const float* dir, bool visible, const bool* active, const float* up,
+                          float* grad_coef, float* grad_dir) {
+    constexpr int KC = (DEG + 1) * (DEG + 1);
+    grad_dir[0] = grad_dir[1] = grad_dir[2] = 0.0f;
+    if (!ACC) {
+#pragma unroll
+        for (int e = 0; e < 3 * KC; ++e) grad_coef[e] = 0.0f;
+    }
+    if (!visible) return;
+    float cg[3];
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch) cg[ch] = active[ch] ? up[ch] : 0.0f;
+    float unit[3] = {0.0f, 0.0f, 0.0f}, length = 1.0f;
+    if (DEG > 0) {
+        length = length3(dir);
+        const float l = sel_max(length, 1.0e-12f);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) unit[i] = dir[i] / l;
+    }
+    float ug[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+        const float b = sh_basis(unit, k);
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) {
+            if (ACC)
+                grad_coef[3 * k + ch] += b * cg[ch];
+            else
+                grad_coef[3 * k + ch] = b * cg[ch];
+        }
+        if (DEG > 0) {
+            float bg[3];
+            sh_basis_grad(unit, k, bg);
+            const float d = coef[3 * k] * cg[0] + coef[3 * k + 1] * cg[1] + coef[3 * k + 2] * cg[2];
+#pragma unroll
+            for (int i = 0; i < 3; ++i) ug[i] = ug[i] + d * bg[i];
+        }
+    }
+    if (DEG > 0) {
+        const float l = sel_max(length, 1.0e-12f);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) grad_dir[i] = ug[i] / l;
+        if (length >= 1.0e-12f) {
+            const float f = (unit[0] * ug[0] + unit[1] * ug[1] + unit[2] * ug[2]) / length;
+#pragma unroll
+            for (int i = 0; i < 3; ++i) grad_dir[i] = grad_dir[i] - unit[i] * f;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// LDS staging of SH blocks.  Rows of `row_floats` contiguous floats (only
+// the first `need` are kept) for `count` Gaussians; LDS rows have an odd
+// pitch so the per-thread row reads are bank-conflict free.
+// ---------------------------------------------------------------------------
+template <int B>
+GS3D_DEV void stage_rows_in(const float* __restrict__ src, int count, int row_floats, int need, float* lds, int pad) {
+    if ((row_floats & 3) == 0 && ((reinterpret_cast<uintptr_t>(src) & 15) == 0)) {
+        const int rf4 = row_floats >> 2;
+        const int total = count * rf4;
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+        int g = threadIdx.x / rf4, c = threadIdx.x - g * rf4;
+        const int sg = B / rf4, sc = B - sg * rf4;
+        for (int idx = threadIdx.x; idx < total; idx += B) {
+            if (4 * c < need) {
+                const float4 v = s4[idx];
+                float* dst = lds + g * pad + 4 * c;
+                dst[0] = v.x;
+                if (4 * c + 1 < need) dst[1] = v.y;
+                if (4 * c + 2 < need) dst[2] = v.z;
+                if (4 * c + 3 < need) dst[3] = v.w;
+            }
+            g += sg;
+            c += sc;
+            if (c >= rf4) {
+                c -= rf4;
+                g += 1;
+            }
+        }
+        return;
+    }
+    const int total = count * row_floats;
+    int g = threadIdx.x / row_floats, c = threadIdx.x - g * row_floats;
+    const int sg = B / row_floats, sc = B - sg * row_floats;
+    for (int idx = threadIdx.x; idx < total; idx += B) {
+        if (c < need) lds[g * pad + c] = src[idx];
+        g += sg;
+        c += sc;
+        if (c >= row_floats) {
+            c -= row_floats;
+            g += 1;
+        }
+    }
+}
+
+// Inverse of stage_rows_in: write rows to global, zero beyond `need`.
+template <int B>
+GS3D_DEV void stage_rows_out(float* __restrict__ dst, int count, int row_floats, int need, const float* lds, int pad) {
+    const int total = count * row_floats;
+    int g = threadIdx.x / row_floats, c = threadIdx.x - g * row_floats;
+    const int sg = B / row_floats, sc = B - sg * row_floats;
+    for (int idx = threadIdx.x; idx < total; idx += B) {
+        dst[idx] = c < need ? lds[g * pad + c] : 0.0f;
+        g += sg;
+        c += sc;
+        if (c >= row_floats) {
+            c -= row_floats;
+            g += 1;
+        }
+    }
+}
+
+template <int DEG>
+struct ShLayout {
+    static constexpr int need = DEG >= 0 ? 3 * (DEG + 1) * (DEG + 1) : 0;
+    static constexpr int pad = need | 1;
+    static constexpr int lds = DEG >= 0 ? kProjBlock * pad : 1;
+    static constexpr int regs = need > 0 ? need : 1;
+};
+
+// ---------------------------------------------------------------------------
+// Forward.  DEG < 0: no SH evaluation in this launch.
+// ---------------------------------------------------------------------------
+template <int DEG, bool META>
+__global__ __launch_bounds__(kProjBlock) void project_fwd_kernel(gs3d_project_args a) {
+    using L = ShLayout<DEG>;
+    __shared__ float s_sh[L::lds];
+    const int n = a.n;
+    const int64_t base = (int64_t)blockIdx.x * kProjBlock;
+    const int64_t i = base + threadIdx.x;
+    const bool valid = i < n;
+    float mean[3] = {0, 0, 0}, q[4] = {1, 0, 0, 0}, s[3] = {1, 1, 1}, opac = 0.0f;
+    if (valid) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
+        const float4 qq = reinterpret_cast<const float4*>(a.quats)[i];
+        q[0] = qq.x;
+        q[1] = qq.y;
+        q[2] = qq.z;
+        q[3] = qq.w;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
+        opac = a.opacities[i];
+    }
+    float coef[L::regs];
+    const int count = (int)min((int64_t)kProjBlock, (int64_t)n - base);
+    for (int v = 0; v < a.views; ++v) {
+        if constexpr (DEG >= 0) {
+            if (v == 0 || a.sh_view_stride != 0) {
+                __syncthreads();
+                const int rf = a.sh_rows * 3;
+                stage_rows_in<kProjBlock>(a.sh + v * a.sh_view_stride + base * rf, count, rf, L::need, s_sh, L::pad);
+                __syncthreads();
+#pragma unroll
+                for (int e = 0; e < L::need; ++e) coef[e] = s_sh[threadIdx.x * L::pad + e];
+            }
+        }
+        if (!valid) continue;
+        const float* V = a.view + 16 * v;
+        const float* P = a.projection + 16 * v;
+        const float fx = a.intrinsics[9 * v], fy = a.intrinsics[9 * v + 4];
+        Footprint f;
+        const bool vis = project_one(mean, q, s, V, P, fx, fy, a.width, a.height, a.near_plane, a.far_plane,
+                                     a.radius_clip, f);
+        const int64_t row = (int64_t)v * n + i;
+        if (!vis) f = Footprint{{0.0f, 0.0f}, {0.0f, 0.0f, 0.0f}, 0, 0, 0.0f};
+        reinterpret_cast<float2*>(a.centers)[row] = make_float2(f.center[0], f.center[1]);
+        reinterpret_cast<float4*>(a.conics)[row] =
+            make_float4(f.conic[0], f.conic[1], f.conic[2], vis ? opac : 0.0f);
+        a.radii[row] = f.radius;
+        a.tiles[row] = f.tiles;
+        a.depths[row] = f.depth;
+        if constexpr (DEG >= 0) {
+            float dir[3] = {0.0f, 0.0f, 0.0f};
+            if (DEG > 0) {
+#pragma unroll
+                for (int k = 0; k < 3; ++k) dir[k] = mean[k] - a.camera_centers[3 * v + k];
+            }
+            float color[3], raw[3];
+            sh_eval<DEG >= 0 ? DEG : 0>(coef, dir, vis, color, raw);
+#pragma unroll
+            for (int k = 0; k < 3; ++k) a.colors[3 * row + k] = color[k];
+        }
+        if constexpr (META) {
+            reinterpret_cast<float2*>(a.means2d)[row] = make_float2(f.center[0], f.center[1]);
+            a.meta_opacities[row] = vis ? opac : 0.0f;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) a.meta_conics[3 * row + k] = f.conic[k];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward.  Persistent grid-stride loop over blocks of Gaussians; camera
+// gradients (view rows 0-2, projection rows 0,1,3 and SH camera centres) are
+// reduced per wavefront with DPP each iteration into wave-private LDS
+// accumulators, and summed over the block once at the end (one atomic per
+// block and entry).
+// ---------------------------------------------------------------------------
+constexpr int kCamEntries = 12 + 12 + 3;  // view rows 0-2, proj rows 0,1,3, centre
+constexpr int kMaxViewsCamLds = 16;
+
+struct VJP {
+    float mean[3], quat[4], scale[3], opacity;
+    float view[3][4];   // rows 0..2
+    float proj[3][4];   // rows 0, 1, 3
+};
+
+// C = A*B: gA += gC B^T, gB += A^T gC.
+GS3D_DEV void matmul_vjp(const M3& A, const M3& B, const M3& gC, M3& gA, M3& gB) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                sa += gC.m[i][k] * B.m[j][k];
+                sb += A.m[k][i] * gC.m[k][j];
+            }
+            gA.m[i][j] += sa;
+            gB.m[i][j] += sb;
+        }
+}
+
+GS3D_DEV M3 zero3() {
+    M3 z;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) z.m[i][j] = 0.0f;
+    return z;
+}
+
+GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, const float* V, const float* P,
+                             int width, int height, float fx, float fy, const float* gc, const float* gk, VJP& g) {
+    float pos[3];
+#pragma unroll
+    for (int r = 0; r < 3; ++r) pos[r] = point_row(V, r, mean);
+    CovParts st;
+    float cov[3];
+    screen_covariance(pos, q, s, V, width, height, fx, fy, st, cov);
+    g.opacity = gk[3];
+    // splatting/geometry.py:61-71.
+    const float a = cov[0], b = cov[1], c = cov[2];
+    const float det = a * c - b * b;
+    const float factor = 1.0f / (det * det + 0.0000001f);
+    const float x = gk[0], y = gk[1], z = gk[2];
+    M3 gcov2 = zero3();
+    gcov2.m[0][0] = factor * (-c * c * x + b * c * y + (det - a * c) * z);
+    gcov2.m[1][0] = factor * (2.0f * b * c * x - (det + 2.0f * b * b) * y + 2.0f * a * b * z);
+    gcov2.m[1][1] = factor * (-a * a * z + a * b * y + (det - a * c) * x);
+    M3 gX = zero3(), gTm = zero3();
+    matmul_vjp(st.X, st.Tm, gcov2, gX, gTm);
+    M3 gTmT = zero3(), gSigmaT = zero3();
+    matmul_vjp(transpose3(st.Tm), transpose3(st.Sigma), gX, gTmT, gSigmaT);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) gTm.m[i][j] += gTmT.m[j][i];
+    const M3 gSigma = transpose3(gSigmaT);
+    M3 gW = zero3(), gJ = zero3();
+    matmul_vjp(st.W, st.J, gTm, gW, gJ);
+    M3 gMT = zero3(), gM = zero3();
+    matmul_vjp(transpose3(st.M), st.M, gSigma, gMT, gM);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) gM.m[i][j] += gMT.m[j][i];
+    M3 gR;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            acc += gM.m[i][j] * st.R.m[i][j];
+            gR.m[i][j] = s[i] * gM.m[i][j];
+        }
+        g.scale[i] = acc;
+    }
+    {   // splatting/math.py:13-28.
+        const float r = q[0], qx = q[1], qy = q[2], qz = q[3];
+        const auto& G = gR.m;
+        g.quat[0] = 2.0f * (qz * (G[0][1] - G[1][0]) + qy * (G[2][0] - G[0][2]) + qx * (G[1][2] - G[2][1]));
+        g.quat[1] = 2.0f * (qy * (G[0][1] + G[1][0]) + qz * (G[0][2] + G[2][0]) + r * (G[1][2] - G[2][1])) -
+                    4.0f * qx * (G[1][1] + G[2][2]);
+        g.quat[2] = 2.0f * (qx * (G[0][1] + G[1][0]) + r * (G[2][0] - G[0][2]) + qz * (G[1][2] + G[2][1])) -
+                    4.0f * qy * (G[0][0] + G[2][2]);
+        g.quat[3] = 2.0f * (r * (G[0][1] - G[1][0]) + qx * (G[0][2] + G[2][0]) + qy * (G[1][2] + G[2][1])) -
+                    4.0f * qz * (G[0][0] + G[1][1]);
+    }
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) g.view[r][cc] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) g.view[j][i] += gW.m[i][j];
+    const float* t = st.t;
+    const float tz2 = t[2] * t[2];
+    float gt[3];
+    gt[0] = gJ.m[2][0] * (-fx / tz2);
+    gt[1] = gJ.m[2][1] * (-fy / tz2);
+    gt[2] = gJ.m[0][0] * (-fx / tz2) + gJ.m[1][1] * (-fy / tz2) + gJ.m[2][0] * (2.0f * fx * t[0] / (tz2 * t[2])) +
+            gJ.m[2][1] * (2.0f * fy * t[1] / (tz2 * t[2]));
+    // splatting/geometry.py:42-51: saturated x/y are constants.
+    const float xr = pos[0] / pos[2], yr = pos[1] / pos[2];
+    float gpos[3];
+    gpos[0] = (xr >= -st.limx && xr <= st.limx) ? gt[0] : 0.0f;
+    gpos[1] = (yr >= -st.limy && yr <= st.limy) ? gt[1] : 0.0f;
+    gpos[2] = gt[2];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) g.mean[k] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+#pragma unroll
+        for (int cc = 0; cc < 3; ++cc) {
+            g.mean[cc] += gpos[r] * V[4 * r + cc];
+            g.view[r][cc] += gpos[r] * mean[cc];
+        }
+        g.view[r][3] += gpos[r];
+    }
+    // Centre path.
+    float clip[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) clip[r] = point_row(P, r, mean);
+    const float inv_w = 1.0f / (clip[3] + 0.0000001f);
+    const float gnx = gc[0] * (0.5f * (float)width);
+    const float gny = gc[1] * (0.5f * (float)height);
+    const float gclip[3] = {gnx * inv_w, gny * inv_w, -(gnx * clip[0] + gny * clip[1]) * inv_w * inv_w};
+    const int prow[3] = {0, 1, 3};
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+#pragma unroll
+        for (int cc = 0; cc < 3; ++cc) {
+            g.mean[cc] += gclip[r] * P[4 * prow[r] + cc];
+            g.proj[r][cc] = gclip[r] * mean[cc];
+        }
+        g.proj[r][3] = gclip[r];
+    }
+}
+
+template <int DEG>
+__global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bwd_args a, int want_camera) {
+    using L = ShLayout<DEG>;
+    __shared__ float s_sh[L::lds];
+    // Wave-private camera accumulators: [wave][view][entry].
+    __shared__ float s_cam[kProjBlock / 64][kMaxViewsCamLds][kCamEntries];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = a.n;
+    const int views = a.views;
+    if (want_camera) {
+        for (int e = threadIdx.x; e < (kProjBlock / 64) * kMaxViewsCamLds * kCamEntries; e += kProjBlock)
+            (&s_cam[0][0][0])[e] = 0.0f;
+    }
+    const int rf = a.sh_rows * 3;
+    for (int64_t base = (int64_t)blockIdx.x * kProjBlock; base < n; base += (int64_t)gridDim.x * kProjBlock) {
+        const int64_t i = base + threadIdx.x;
+        const bool valid = i < n;
+        const int count = (int)min((int64_t)kProjBlock, (int64_t)n - base);
+        float mean[3] = {0, 0, 0}, q[4] = {1, 0, 0, 0}, s[3] = {1, 1, 1};
+        if (valid) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
+            const float4 qq = reinterpret_cast<const float4*>(a.quats)[i];
+            q[0] = qq.x;
+            q[1] = qq.y;
+            q[2] = qq.z;
+            q[3] = qq.w;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
+        }
+        float gm[3] = {0, 0, 0}, gq[4] = {0, 0, 0, 0}, gs[3] = {0, 0, 0}, go = 0.0f;
+        float coef[L::regs];
+        float gco[L::regs];
+#pragma unroll
+        for (int e = 0; e < L::regs; ++e) gco[e] = 0.0f;
+        for (int v = 0; v < views; ++v) {
+            if constexpr (DEG >= 0) {
+                if (v == 0 || a.sh_view_stride != 0) {
+                    __syncthreads();
+                    stage_rows_in<kProjBlock>(a.sh + v * a.sh_view_stride + base * rf, count, rf, L::need, s_sh,
+                                              L::pad);
+                    __syncthreads();
+#pragma unroll
+                    for (int e = 0; e < L::need; ++e) coef[e] = s_sh[threadIdx.x * L::pad + e];
+                }
+            }
+            const int64_t row = (int64_t)v * n + i;
+            const bool vis = valid && a.radii[row] > 0;
+            VJP g;
+            float cam[kCamEntries];
+#pragma unroll
+            for (int e = 0; e < kCamEntries; ++e) cam[e] = 0.0f;
+            if (vis) {
+                const float* gcp = a.grad_centers + row * a.grad_centers_stride;
+                const float* gkp = a.grad_conics + row * a.grad_conics_stride;
+                const float gc[2] = {gcp[0], gcp[1]};
+                const float gk[4] = {gkp[0], gkp[1], gkp[2], gkp[3]};
+                projection_vjp(mean, q, s, a.view + 16 * v, a.projection + 16 * v, a.width, a.height,
+                               a.intrinsics[9 * v], a.intrinsics[9 * v + 4], gc, gk, g);
+#pragma unroll
+                for (int k = 0; k < 3; ++k) gm[k] += g.mean[k];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) gq[k] += g.quat[k];
+#pragma unroll
+                for (int k = 0; k < 3; ++k) gs[k] += g.scale[k];
+                go += g.opacity;
+#pragma unroll
+                for (int r = 0; r < 3; ++r)
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) {
+                        cam[4 * r + cc] = g.view[r][cc];
+                        cam[12 + 4 * r + cc] = g.proj[r][cc];
+                    }
+            }
+            if constexpr (DEG >= 0) {
+                if (valid) {
+                    float dir[3] = {0.0f, 0.0f, 0.0f};
+                    if (DEG > 0) {
+#pragma unroll
+                        for (int k = 0; k < 3; ++k) dir[k] = mean[k] - a.camera_centers[3 * v + k];
+                    }
+                    float color[3], raw[3];
+                    sh_eval<DEG>(coef, dir, vis, color, raw);
+                    const bool act[3] = {vis && raw[0] >= 0.0f, vis && raw[1] >= 0.0f, vis && raw[2] >= 0.0f};
+                    const float* gcol = a.grad_colors + row * a.grad_colors_stride;
+                    const float up[3] = {gcol[0], gcol[1], gcol[2]};
+                    float gd[3];
+                    sh_backward<DEG, true>(coef, dir, vis, act, up, gco, gd);
+                    if (DEG > 0) {
+#pragma unroll
+                        for (int k = 0; k < 3; ++k) {
+                            gm[k] += gd[k];
+                            cam[24 + k] = -gd[k];
+                        }
+                    }
+                }
+                if (a.sh_view_stride != 0 && a.grad_sh) {
+                    // Per-view coefficients: write this view's gradient block.
+                    __syncthreads();
+#pragma unroll
+                    for (int e = 0; e < L::need; ++e) s_sh[threadIdx.x * L::pad + e] = gco[e];
+                    __syncthreads();
+                    stage_rows_out<kProjBlock>(a.grad_sh + v * a.sh_view_stride + base * rf, count, rf, L::need, s_sh,
+                                               L::pad);
+#pragma unroll
+                    for (int e = 0; e < L::regs; ++e) gco[e] = 0.0f;
+                }
+            }
+            if (want_camera && v < kMaxViewsCamLds) {
+#pragma unroll
+                for (int e = 0; e < kCamEntries; ++e) {
+                    const float sum = wave_sum_to_lane63(cam[e]);
+                    if (lane == 63) s_cam[wave][v][e] += sum;
+                }
+            }
+        }
+        if (valid) {
+            if (a.grad_means)
+#pragma unroll
+                for (int k = 0; k < 3; ++k) a.grad_means[3 * i + k] = gm[k];
+            if (a.grad_quats)
+                reinterpret_cast<float4*>(a.grad_quats)[i] = make_float4(gq[0], gq[1], gq[2], gq[3]);
+            if (a.grad_scales)
+#pragma unroll
+                for (int k = 0; k < 3; ++k) a.grad_scales[3 * i + k] = gs[k];
+            if (a.grad_opacities) a.grad_opacities[i] = go;
+        }
+        if constexpr (DEG >= 0) {
+            if (a.sh_view_stride == 0 && a.grad_sh) {
+                __syncthreads();
+#pragma unroll
+                for (int e = 0; e < L::need; ++e) s_sh[threadIdx.x * L::pad + e] = gco[e];
+                __syncthreads();
+                stage_rows_out<kProjBlock>(a.grad_sh + base * rf, count, rf, L::need, s_sh, L::pad);
+            }
+        }
+    }
+    if (want_camera) {
+        __syncthreads();
+        const int total = views * kCamEntries;
+        for (int e = threadIdx.x; e < total; e += kProjBlock) {
+            const int v = e / kCamEntries, k = e - v * kCamEntries;
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kProjBlock / 64; ++w) sum += s_cam[w][v][k];
+            if (k < 12) {
+                if (a.grad_view) atomicAdd(a.grad_view + 16 * v + k, sum);
+            } else if (k < 24) {
+                const int r = (k - 12) >> 2, c = (k - 12) & 3;
+                const int prow = r == 2 ? 3 : r;
+                if (a.grad_projection) atomicAdd(a.grad_projection + 16 * v + 4 * prow + c, sum);
+            } else if (a.grad_camera_centers) {
+                atomicAdd(a.grad_camera_centers + 3 * v + (k - 24), sum);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Standalone SH and metadata kernels (used by the staged ops API).
+// ---------------------------------------------------------------------------
+template <int DEG>
+__global__ void sh_fwd_kernel(const float* __restrict__ coefficients, int rows, const float* __restrict__ dirs,
+                              const int32_t* __restrict__ radii, int n, float* __restrict__ colors,
+                              uint8_t* __restrict__ active) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    constexpr int KC = (DEG + 1) * (DEG + 1);
+    float coef[3 * KC];
+    for (int e = 0; e < 3 * KC; ++e) coef[e] = coefficients[i * rows * 3 + e];
+    const float dir[3] = {dirs[3 * i], dirs[3 * i + 1], dirs[3 * i + 2]};
+    const bool vis = radii ? radii[i] > 0 : true;
+    float color[3], raw[3];
+    sh_eval<DEG>(coef, dir, vis, color, raw);
+    for (int k = 0; k < 3; ++k) {
+        colors[3 * i + k] = color[k];
+        if (active) active[3 * i + k] = (vis && raw[k] >= 0.0f) ? 1 : 0;
+    }
+}
+
+template <int DEG>
+__global__ void sh_bwd_kernel(const float* __restrict__ coefficients, int rows, const float* __restrict__ dirs,
+                              const int32_t* __restrict__ radii, const uint8_t* __restrict__ active,
+                              const float* __restrict__ upstream, int n, float* __restrict__ grad_coefficients,
+                              float* __restrict__ grad_dirs) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    constexpr int KC = (DEG + 1) * (DEG + 1);
+    float coef[3 * KC], gco[3 * KC], gd[3];
+    for (int e = 0; e < 3 * KC; ++e) coef[e] = coefficients[i * rows * 3 + e];
+    const float dir[3] = {dirs[3 * i], dirs[3 * i + 1], dirs[3 * i + 2]};
+    const bool vis = radii ? radii[i] > 0 : true;
+    const bool act[3] = {active[3 * i] != 0, active[3 * i + 1] != 0, active[3 * i + 2] != 0};
+    const float up[3] = {upstream[3 * i], upstream[3 * i + 1], upstream[3 * i + 2]};
+    sh_backward<DEG, false>(coef, dir, vis, act, up, gco, gd);
+    if (grad_coefficients)
+        for (int e = 0; e < rows * 3; ++e) grad_coefficients[i * rows * 3 + e] = e < 3 * KC ? gco[e] : 0.0f;
+    if (grad_dirs)
+        for (int k = 0; k < 3; ++k) grad_dirs[3 * i + k] = gd[k];
+}
+
+__global__ void metadata_kernel(const int32_t* __restrict__ radii, const float* __restrict__ centers,
+                                const float* __restrict__ conics, int64_t n, float* __restrict__ means2d,
+                                float* __restrict__ opacities, float* __restrict__ meta_conics) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const bool vis = radii[i] > 0;
+    const float2 c = vis ? reinterpret_cast<const float2*>(centers)[i] : make_float2(0.0f, 0.0f);
+    const float4 k = vis ? reinterpret_cast<const float4*>(conics)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    reinterpret_cast<float2*>(means2d)[i] = c;
+    opacities[i] = k.w;
+    meta_conics[3 * i] = k.x;
+    meta_conics[3 * i + 1] = k.y;
+    meta_conics[3 * i + 2] = k.z;
+}
+
+template <int DEG>
+int launch_project_fwd(const gs3d_project_args& a, hipStream_t stream) {
+    const dim3 grid(blocks_for(a.n, kProjBlock));
+    if (a.means2d)
+        hipLaunchKernelGGL((project_fwd_kernel<DEG, true>), grid, dim3(kProjBlock), 0, stream, a);
+    else
+        hipLaunchKernelGGL((project_fwd_kernel<DEG, false>), grid, dim3(kProjBlock), 0, stream, a);
+    return launch_status("gs3d_project_fwd");
+}
+
+template <int DEG>
+int launch_project_bwd(const gs3d_project_bwd_args& a, int want_camera, hipStream_t stream) {
+    int device = 0, cus = 256;
+    if (hipGetDevice(&device) == hipSuccess) {
+        int value = 0;
+        if (hipDeviceGetAttribute(&value, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && value > 0)
+            cus = value;
+    }
+    const int64_t needed = blocks_for(a.n, kProjBlock);
+    const int64_t persistent = (int64_t)cus * 8;
+    const dim3 grid((unsigned)(needed < persistent ? needed : persistent));
+    hipLaunchKernelGGL((project_bwd_kernel<DEG>), grid, dim3(kProjBlock), 0, stream, a, want_camera);
+    return launch_status("gs3d_project_bwd");
+}
+
+}  // namespace gs3d
+
+extern "C" int gs3d_project_fwd(const gs3d_project_args* args, void* stream) {
+    if (!args) return GS3D_ERR_ARGUMENT;
+    const gs3d_project_args& a = *args;
+    if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0) return GS3D_ERR_ARGUMENT;
+    if (a.n == 0 || a.views == 0) return GS3D_OK;
+    if (!a.means || !a.quats || !a.scales || !a.opacities || !a.view || !a.projection || !a.intrinsics ||
+        !a.centers || !a.conics || !a.radii || !a.tiles || !a.depths)
+        return GS3D_ERR_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(a.quats) & 15) || (reinterpret_cast<uintptr_t>(a.conics) & 15) ||
+        (reinterpret_cast<uintptr_t>(a.centers) & 7) || (a.means2d && (reinterpret_cast<uintptr_t>(a.means2d) & 7)))
+        return GS3D_ERR_ARGUMENT;
+    if (a.means2d && (!a.meta_opacities || !a.meta_conics)) return GS3D_ERR_ARGUMENT;
+    hipStream_t s = gs3d::as_stream(stream);
+    if (!a.sh) return gs3d::launch_project_fwd<-1>(a, s);
+    if (a.sh_degree < 0 || a.sh_degree > 3 || a.sh_rows < (a.sh_degree + 1) * (a.sh_degree + 1) || !a.colors ||
+        (a.sh_degree > 0 && !a.camera_centers))
+        return GS3D_ERR_ARGUMENT;
+    switch (a.sh_degree) {
+    case 0: return gs3d::launch_project_fwd<0>(a, s);
+    case 1: return gs3d::launch_project_fwd<1>(a, s);
+    case 2: return gs3d::launch_project_fwd<2>(a, s);
+    default: return gs3d::launch_project_fwd<3>(a, s);
+    }
+}
+
+extern "C" int gs3d_project_bwd(const gs3d_project_bwd_args* args, void* stream) {
+    if (!args) return GS3D_ERR_ARGUMENT;
+    const gs3d_project_bwd_args& a = *args;
+    if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0) return GS3D_ERR_ARGUMENT;
+    if (a.n == 0 || a.views == 0) return GS3D_OK;
+    if (!a.means || !a.quats || !a.scales || !a.opacities || !a.view || !a.projection || !a.intrinsics ||
+        !a.radii || !a.grad_centers || !a.grad_conics || a.grad_centers_stride < 2 || a.grad_conics_stride < 4)
+        return GS3D_ERR_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(a.quats) & 15) || (a.grad_quats && (reinterpret_cast<uintptr_t>(a.grad_quats) & 15)))
+        return GS3D_ERR_ARGUMENT;
+    const int want_camera = (a.grad_view || a.grad_projection || (a.sh && a.grad_camera_centers)) ? 1 : 0;
+    if (want_camera && a.views > gs3d::kMaxViewsCamLds) return GS3D_ERR_UNSUPPORTED;
+    hipStream_t s = gs3d::as_stream(stream);
+    if (!a.sh) return gs3d::launch_project_bwd<-1>(a, want_camera, s);
+    if (a.sh_degree < 0 || a.sh_degree > 3 || a.sh_rows < (a.sh_degree + 1) * (a.sh_degree + 1) || !a.grad_colors ||
+        a.grad_colors_stride < 3 || (a.sh_degree > 0 && !a.camera_centers))
+        return GS3D_ERR_ARGUMENT;
+    switch (a.sh_degree) {
+    case 0: return gs3d::launch_project_bwd<0>(a, want_camera, s);
+    case 1: return gs3d::launch_project_bwd<1>(a, want_camera, s);
+    case 2: return gs3d::launch_project_bwd<2>(a, want_camera, s);
+    default: return gs3d::launch_project_bwd<3>(a, want_camera, s);
+    }
+}
+
+extern "C" int gs3d_sh_fwd(const float* coefficients, int32_t rows, const float* directions, const int32_t* radii,
+                           int32_t n, int32_t degree, float* colors, uint8_t* active, void* stream) {
+    if (n < 0 || degree < 0 || degree > 3 || rows < (degree + 1) * (degree + 1)) return GS3D_ERR_ARGUMENT;
+    if (n == 0) return GS3D_OK;
+    if (!coefficients || !directions || !colors) return GS3D_ERR_ARGUMENT;
+    const dim3 grid(gs3d::blocks_for(n, 256)), block(256);
+    hipStream_t s = gs3d::as_stream(stream);
+    switch (degree) {
+    case 0: hipLaunchKernelGGL(gs3d::sh_fwd_kernel<0>, grid, block, 0, s, coefficients, rows, directions, radii, n, colors, active); break;
+    case 1: hipLaunchKernelGGL(gs3d::sh_fwd_kernel<1>, grid, block, 0, s, coefficients, rows, directions, radii, n, colors, active); break;
+    case 2: hipLaunchKernelGGL(gs3d::sh_fwd_kernel<2>, grid, block, 0, s, coefficients, rows, directions, radii, n, colors, active); break;
+    default: hipLaunchKernelGGL(gs3d::sh_fwd_kernel<3>, grid, block, 0, s, coefficients, rows, directions, radii, n, colors, active); break;
+    }
+    return gs3d::launch_status("gs3d_sh_fwd");
+}
+
+extern "C" int gs3d_sh_bwd(const float* coefficients, int32_t rows, const float* directions, const int32_t* radii,
+                           const uint8_t* active, const float* upstream, int32_t n, int32_t degree,
+                           float* grad_coefficients, float* grad_directions, void* stream) {
+    if (n < 0 || degree < 0 || degree > 3 || rows < (degree + 1) * (degree + 1)) return GS3D_ERR_ARGUMENT;
+    if (n == 0) return GS3D_OK;
+    if (!coefficients || !directions || !active || !upstream) return GS3D_ERR_ARGUMENT;
+    const dim3 grid(gs3d::blocks_for(n, 256)), block(256);
+    hipStream_t s = gs3d::as_stream(stream);
+    switch (degree) {
+    case 0: hipLaunchKernelGGL(gs3d::sh_bwd_kernel<0>, grid, block, 0, s, coefficients, rows, directions, radii, active, upstream, n, grad_coefficients, grad_directions); break;
+    case 1: hipLaunchKernelGGL(gs3d::sh_bwd_kernel<1>, grid, block, 0, s, coefficients, rows, directions, radii, active, upstream, n, grad_coefficients, grad_directions); break;
+    case 2: hipLaunchKernelGGL(gs3d::sh_bwd_kernel<2>, grid, block, 0, s, coefficients, rows, directions, radii, active, upstream, n, grad_coefficients, grad_directions); break;
+    default: hipLaunchKernelGGL(gs3d::sh_bwd_kernel<3>, grid, block, 0, s, coefficients, rows, directions, radii, active, upstream, n, grad_coefficients, grad_directions); break;
+    }
+    return gs3d::launch_status("gs3d_sh_bwd");
+}
+
+extern "C" int gs3d_metadata(const int32_t* radii, const float* centers, const float* conics, int64_t n,
+                             float* means2d, float* opacities, float* meta_conics, void* stream) {
+    if (n < 0) return GS3D_ERR_ARGUMENT;
+    if (n == 0) return GS3D_OK;
+    if (!radii || !centers || !conics || !means2d || !opacities || !meta_conics) return GS3D_ERR_ARGUMENT;
+    hipLaunchKernelGGL(gs3d::metadata_kernel, dim3(gs3d::blocks_for(n, 256)), dim3(256), 0, gs3d::as_stream(stream),
+                       radii, centers, conics, n, means2d, opacities, meta_conics);
+    return gs3d::launch_status("gs3d_metadata");
+}

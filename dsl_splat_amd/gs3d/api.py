@@ -1,0 +1,188 @@
+"""Original 3DGS API with OpenCV cameras (gs3d/api.py:25-265 of the reference).
+
+Same signature, defaults, validation errors, outputs and ``meta`` keys.  Per
+Gaussian batch the host issues: one camera launch, one fused projection
+(+SH +metadata) launch for all cameras, one scan, ONE host synchronisation
+(camera status codes and the pair count together), emission, one radix sort
+over all cameras' pairs, ranges, and one blend launch for all cameras.
+"""
+
+from dataclasses import dataclass, field
+import math
+from numbers import Integral
+from typing import Any, Sequence
+
+import torch
+from torch import Tensor
+
+from .autograd import Frame, Rasterize
+from .projection import project_views
+from ..cameras import validate_camera_options
+from ..inputs import batch_item, normalize_inputs
+from ..primitives.tiling import scan_device
+from ..splatting.binning import emit_and_sort, require_radius_mode, validate_tile_mode
+from ..splatting.cameras import launch_prepare, raise_camera_errors
+from ..statistics import StatisticsRequest
+from ..training import prepare_training_metadata
+
+BACKEND = "gs3d-hip"
+
+
+@dataclass(slots=True)
+class RasterizationResult:
+    """Channel-last views of frame-owned images and training metadata."""
+
+    features: Tensor
+    alpha: Tensor
+    meta: dict[str, Any]
+    statistics: dict[str, Tensor] = field(default_factory=dict)
+
+    @property
+    def radii(self) -> Tensor:
+        return self.meta["radii"]
+
+    @property
+    def means2d(self) -> Tensor:
+        return self.meta["means2d"]
+
+    @property
+    def extra_features(self) -> Tensor | None:
+        return self.meta.get("render_extra_signals")
+
+
+@torch.no_grad()
+def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height, near, far, radius_clip,
+                   sh, sh_degree, background) -> Frame:
+    """Camera rows, fused projection, scan, one synchronisation, binning."""
+    with_centers = sh_degree is not None and sh_degree > 0
+    full, inverse, centers, errors = launch_prepare(viewmats, Ks, width, height, with_centers)
+    state = project_views(
+        means, quats, scales, opacities, viewmats, full, Ks, width, height, near, far, radius_clip,
+        sh=sh if sh_degree is not None else None, sh_degree=sh_degree or 0,
+        camera_centers=centers if with_centers else None, metadata=True,
+    )
+    offsets, total = scan_device(state.tile_counts)
+    host = torch.cat([errors.to(torch.int64), total]).cpu().tolist()
+    raise_camera_errors(host[:-1])
+    count = int(host[-1]) if len(offsets) else 0
+    if count > 2**31 - 1:
+        raise OverflowError(f"{count} tile pairs exceed the int32 offsets of the binning stage")
+    bins = emit_and_sort(state.centers, state.radii, state.depths, offsets, count, width, height)
+    return Frame(
+        width, height, Ks.detach(), full, inverse if with_centers else None, centers if with_centers else None,
+        state, bins["ranges"], bins["point_list"], count, sh_degree, background,
+    )
+
+
+def rasterize(
+    means: Tensor,
+    quats: Tensor,
+    scales: Tensor,
+    opacities: Tensor,
+    viewmats: Tensor,
+    Ks: Tensor,
+    width: int,
+    height: int,
+    *,
+    features: Tensor | None = None,
+    sh_coeffs: Tensor | None = None,
+    sh_degree: int | None = None,
+    backgrounds: Tensor | None = None,
+    extra_features: Tensor | None = None,
+    near_plane: float = 0.2,
+    far_plane: float = math.inf,
+    radius_clip: float = 0.0,
+    packed: bool = False,
+    absgrad: bool = False,
+    statistics: Sequence[StatisticsRequest] = (),
+    tile_mode: str = "radius",
+) -> RasterizationResult:
+    """Render original 3DGS with centre-Z sorting.
+
+    Scales/opacities are activated; wxyz quaternions are normalized. Gaussian
+    batch dimensions and per-view features/SH follow the reference layouts.
+    Pixel centers are (x+0.5, y+0.5) in the supplied K coordinate system;
+    returned means2d uses integer pixel centres (K projection minus 0.5),
+    with culled rows set to zero.  The default centre-depth cutoff z > 0.2
+    matches original CUDA; the 0.3 covariance dilation is fixed.
+    K/background gradients, depth output and higher derivatives are
+    unsupported.
+    """
+    validate_tile_mode(tile_mode)
+    validate_camera_options(width, height, near_plane, far_plane, radius_clip)
+    if (features is None) == (sh_coeffs is None):
+        raise ValueError("provide exactly one of features or sh_coeffs")
+    if sh_coeffs is not None:
+        if not isinstance(sh_coeffs, Tensor) or sh_coeffs.ndim < 3:
+            raise ValueError("sh_coeffs must have shape (...,N,K,3) or (...,C,N,K,3)")
+        if sh_degree is None:
+            sh_degree = min(3, math.isqrt(sh_coeffs.shape[-2]) - 1)
+    elif sh_degree is not None:
+        raise ValueError("sh_degree requires sh_coeffs")
+    if sh_degree is not None and (
+        isinstance(sh_degree, bool) or not isinstance(sh_degree, Integral) or sh_degree not in range(4)
+    ):
+        raise ValueError("sh_degree must be an integer in [0,3]")
+    layout = normalize_inputs(
+        means, quats, scales, opacities, features if sh_coeffs is None else sh_coeffs, viewmats, Ks,
+        backgrounds, extra_features, None, sh_degree,
+    )
+    require_radius_mode(tile_mode)
+    if statistics:
+        raise NotImplementedError("contribution statistics are not implemented in the HIP rasterizer yet")
+    frames: list[Frame] = []
+    dense: dict[str, list[Tensor]] = {n: [] for n in ("radii", "means2d", "opacities", "tiles_per_gauss", "conics")}
+    for b in range(layout.batch_count):
+        colors = layout.colors.values[b]
+        frame = _prepare_frame(
+            layout.means[b], layout.quats[b], layout.scales[b], layout.opacities[b],
+            batch_item(layout.viewmats, b), batch_item(layout.Ks, b), width, height, near_plane, far_plane,
+            radius_clip, colors if sh_degree is not None else None, sh_degree,
+            None if layout.backgrounds is None else batch_item(layout.backgrounds, b),
+        )
+        frames.append(frame)
+        st = frame.state
+        dense["radii"].append(st.radii[..., None].expand(-1, -1, 2))
+        dense["means2d"].append(st.means2d)
+        dense["opacities"].append(st.opacities)
+        dense["tiles_per_gauss"].append(st.tile_counts)
+        dense["conics"].append(st.meta_conics)
+    geometry = {
+        name: (rows[0] if len(rows) == 1 else torch.stack(rows)).reshape(
+            (layout.batch_count, layout.cameras, layout.n) + tuple(rows[0].shape[2:])
+        )
+        for name, rows in dense.items()
+    }
+    training = prepare_training_metadata(geometry, layout, packed=packed, absgrad=absgrad)
+    meta = training.values
+    meta.update(
+        width=width,
+        height=height,
+        tile_size=16,
+        tile_width=(width + 15) // 16,
+        tile_height=(height + 15) // 16,
+        n_cameras=layout.cameras,
+        packed=packed,
+        backend=BACKEND,
+        with_eval3d=False,
+        supports_means2d_grad=True,
+        screen_gradient_mode="projected_mean",
+        tile_mode=tile_mode,
+    )
+    images = []
+    grad_enabled = torch.is_grad_enabled()
+    for b, frame in enumerate(frames):
+        screen = None if training.screen is None else batch_item(training.screen, b)
+        targets = training.absolute_targets[b * layout.cameras:(b + 1) * layout.cameras]
+        extras = None if layout.extras is None else layout.extras.values[b]
+        image = Rasterize.apply(
+            layout.means[b], layout.quats[b], layout.scales[b], layout.opacities[b], layout.colors.values[b],
+            extras, batch_item(layout.viewmats, b), screen, frame, targets, grad_enabled,
+        )
+        images.append(image)
+    shape = layout.batch_dims + (layout.cameras, height, width)
+    images = (images[0] if len(images) == 1 else torch.stack(images)).reshape(shape + (images[0].shape[-1],))
+    channels = layout.colors.channels
+    if layout.extras is not None:
+        meta["render_extra_signals"] = images[..., channels:-1]
+    return RasterizationResult(images[..., :channels], images[..., -1:], meta, {})

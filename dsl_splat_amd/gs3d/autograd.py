@@ -1,0 +1,132 @@
+"""Original-3DGS blending boundary and its projection/SH/camera VJPs.
+
+Mirrors gs3d/autograd.py:17-171 of the reference, with one Function per
+Gaussian batch covering all of its cameras (the reference applies one per
+view).  Forward blends the already projected and sorted frame; backward runs
+the blend VJP, writes the absolute screen gradients, then one fused
+projection + SH VJP over all views and the camera VJP:
+
+    viewmats.grad = d(view) + camera_backward(d(full projection), d(centres))
+
+which is what the reference's separate camera/projection/SH autograd nodes
+sum to.  Gradients of means2d are the blend's centre gradients
+(screen_gradient_mode "projected_mean").
+"""
+
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+from torch import Tensor
+from torch.autograd.function import once_differentiable
+
+from . import projection, render
+from ..runtime.gradients import AbsGradientTarget
+from ..splatting.cameras import camera_backward
+
+
+@dataclass(slots=True)
+class Frame:
+    """Forward state of one Gaussian batch (all C cameras)."""
+
+    width: int
+    height: int
+    Ks: Tensor                 # (C,3,3) detached
+    full: Tensor               # (C,4,4) projection rows
+    inverse: Tensor | None     # (C,4,4) view inverse (SH only)
+    camera_centers: Tensor | None
+    state: projection.ProjectedViews
+    ranges: Tensor             # (C*T, 2)
+    ids: Tensor                # (M,)
+    pair_count: int
+    sh_degree: int | None
+    background: Tensor | None  # (C, D) or None
+
+
+class Rasterize(torch.autograd.Function):
+    @staticmethod
+    def forward(
+        ctx: Any,
+        means: Tensor,
+        quats: Tensor,
+        scales: Tensor,
+        opacities: Tensor,
+        colors: Tensor,
+        extra_features: Tensor | None,
+        viewmats: Tensor,
+        screen: Tensor | None,
+        frame: Frame,
+        absolute: list[AbsGradientTarget | None] | None,
+        grad_enabled: bool,
+    ) -> Tensor:
+        st = frame.state
+        blended = st.colors if frame.sh_degree is not None else colors
+        output = render.render_views(
+            frame.ranges, frame.ids, st.centers, st.conics, blended, frame.width, frame.height,
+            extra=extra_features, background=frame.background, one_tail=True,
+        )
+        if grad_enabled and any(ctx.needs_input_grad[:8]):
+            ctx.save_for_backward(means, quats, scales, opacities, colors, extra_features, viewmats,
+                                  output.transmittance, output.contributors)
+            ctx.frame = frame
+            ctx.absolute = absolute
+        ctx.set_materialize_grads(False)
+        return output.features
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, gradient: Tensor | None) -> tuple[Tensor | None, ...]:
+        none = (None,) * 11
+        if gradient is None:
+            return none
+        means, quats, scales, opacities, colors, extra, viewmats, final_t, contributors = ctx.saved_tensors
+        frame: Frame = ctx.frame
+        st = frame.state
+        needs = ctx.needs_input_grad
+        sh = frame.sh_degree is not None
+        blended = st.colors if sh else colors
+        absgrad = ctx.absolute is not None and any(t is not None for t in ctx.absolute)
+        record, grad_blended, grad_extra = render.backward_views(
+            frame.ranges, frame.ids, st.centers, st.conics, blended, final_t, contributors, gradient,
+            frame.width, frame.height, extra=extra, background=frame.background, one_tail=True,
+            absgrad=absgrad, need_features=sh or needs[4], need_extra=needs[5],
+        )
+        if absgrad:
+            for c, target in enumerate(ctx.absolute):
+                if target is not None:
+                    target.write(record[c, :, 6:8])
+        grad_centers = record[..., 0:2]
+        grad_conics = record[..., 2:6]
+        proj_needs = (needs[0], needs[1], needs[2], needs[3], needs[6], needs[6])
+        want_sh = sh and (needs[4] or (frame.sh_degree > 0 and (needs[0] or needs[6])))
+        grads = dict(means=None, quats=None, scales=None, opacities=None, view=None, projection=None, sh=None,
+                     camera_centers=None)
+        if any(proj_needs) or want_sh:
+            grads = projection.backward_views(
+                means, quats, scales, opacities, viewmats.detach(), frame.full, frame.Ks, frame.width,
+                frame.height, st.radii, grad_centers, grad_conics, proj_needs,
+                sh=colors if sh else None, sh_degree=frame.sh_degree or 0, camera_centers=frame.camera_centers,
+                grad_colors=grad_blended if sh else None, need_sh=sh and needs[4],
+                need_centers=sh and (frame.sh_degree or 0) > 0 and needs[6],
+            )
+        grad_view = None
+        if needs[6]:
+            grad_view = camera_backward(frame.Ks, grads["projection"], frame.width, frame.height,
+                                        frame.inverse if frame.inverse is not None else frame.full,
+                                        grads["camera_centers"])
+            if grads["view"] is not None:
+                grad_view = grad_view + grads["view"]
+            grad_view = grad_view.reshape(viewmats.shape)
+        return (
+            grads["means"] if needs[0] else None,
+            grads["quats"] if needs[1] else None,
+            grads["scales"] if needs[2] else None,
+            grads["opacities"] if needs[3] else None,
+            (grads["sh"] if sh else grad_blended) if needs[4] else None,
+            grad_extra if needs[5] else None,
+            grad_view,
+            grad_centers if needs[7] else None,
+            None,
+            None,
+            None,
+        )

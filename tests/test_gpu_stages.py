@@ -1,0 +1,239 @@
+"""Stage-by-stage parity of the HIP kernels with the CPU oracle.
+
+Integer stages (radii, tile counts, offsets, sorted keys/values, ranges,
+contributors) are compared bit-exactly; the forward float stages follow the
+same operation sequence as the oracle and are compared bit-exactly too;
+gradients (atomically accumulated in another order) within
+rtol 1e-4 / atol 1e-5 relative to the gradient scale.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle_pipeline import compare
+from dsl_splat_amd import synthetic
+from dsl_splat_amd.gs3d import projection as gproj
+from dsl_splat_amd.gs3d import render as grender
+from dsl_splat_amd.primitives import tiling
+from dsl_splat_amd.splatting import binning, cameras
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _say(*args):
+    print(*args, flush=True)
+
+
+SCENES = {
+    "small_rgb": dict(name="small", n=4000, width=128, height=96, seed=1),
+    "sh3_4view": dict(name="sh3_1080p_4view", n=6000, width=160, height=96, seed=2),
+    "sh3_720p": dict(name="sh3_720p", n=5000, width=200, height=120, seed=3),
+}
+
+
+def _scene(key):
+    cfg = dict(SCENES[key])
+    name = cfg.pop("name")
+    return synthetic.make_scene(name, **cfg).to(DEV)
+
+
+def _project(scene, sh_degree=None):
+    quats = torch.nn.functional.normalize(scene.quats, dim=-1)
+    with_centers = sh_degree is not None and sh_degree > 0
+    full, inverse, centers, errors = cameras.launch_prepare(scene.viewmats, scene.Ks, scene.width, scene.height,
+                                                            with_centers)
+    state = gproj.project_views(
+        scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks, scene.width,
+        scene.height, 0.2, float("inf"), 0.0, sh=scene.sh_coeffs if sh_degree is not None else None,
+        sh_degree=sh_degree or 0, camera_centers=centers if with_centers else None, metadata=True)
+    return quats, full, inverse, centers, errors, state
+
+
+def test_camera_prepare_bit_exact():
+    scene = _scene("sh3_4view")
+    _say("camera_prepare sh3_4view")
+    full, inverse, centers, errors = cameras.launch_prepare(scene.viewmats, scene.Ks, scene.width, scene.height, True)
+    torch.cuda.synchronize()
+    of, oi, oc, oe = oracle.camera_prepare(_np(scene.viewmats), _np(scene.Ks), scene.width, scene.height, True)
+    np.testing.assert_array_equal(_np(errors), oe)
+    np.testing.assert_array_equal(_np(full), of)
+    np.testing.assert_array_equal(_np(inverse), oi)
+    np.testing.assert_array_equal(_np(centers), oc)
+    bad = scene.Ks.clone()
+    bad[0, 0, 1] = 0.5
+    bad[1, 1, 1] = -2.0
+    _, _, _, e2 = cameras.launch_prepare(scene.viewmats, bad, scene.width, scene.height, True)
+    assert _np(e2).tolist() == [1, 2, 0, 0]
+
+
+@pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3), ("sh3_720p", 0), ("sh3_720p", 1),
+                                        ("sh3_720p", 2), ("sh3_720p", 3)])
+def test_projection_forward_bit_exact(key, degree):
+    scene = _scene(key)
+    _say(f"projection fwd {key} degree={degree}")
+    quats, full, inverse, centers, errors, st = _project(scene, degree)
+    torch.cuda.synchronize()
+    ref = oracle.project_fwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+                             _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height,
+                             sh=_np(scene.sh_coeffs) if degree is not None else None, sh_degree=degree or 0,
+                             camera_centers=_np(centers) if degree else None, metadata=True)
+    for name, got in (("radii", st.radii), ("tiles", st.tile_counts), ("centers", st.centers),
+                      ("conics", st.conics), ("depths", st.depths), ("means2d", st.means2d),
+                      ("meta_opacities", st.opacities), ("meta_conics", st.meta_conics)):
+        np.testing.assert_array_equal(_np(got), ref[name], err_msg=name)
+    if degree is not None:
+        np.testing.assert_array_equal(_np(st.colors), ref["colors"], err_msg="colors")
+    assert (_np(st.radii) > 0).mean() > 0.3
+
+
+def test_per_view_sh_projection():
+    scene = _scene("sh3_4view")
+    per_view = torch.randn((4,) + tuple(scene.sh_coeffs.shape), device=DEV) * 0.3
+    scene.sh_coeffs = per_view
+    _say("projection fwd per-view SH")
+    quats, full, inverse, centers, errors, st = _project(scene, 2)
+    ref = oracle.project_fwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+                             _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height,
+                             sh=_np(per_view), sh_degree=2, camera_centers=_np(centers))
+    np.testing.assert_array_equal(_np(st.colors), ref["colors"])
+
+
+@pytest.mark.parametrize("n", [1, 1000, 4096, 4097, 300_001, 5_000_000])
+def test_scan_bit_exact(n):
+    _say(f"scan n={n}")
+    g = torch.Generator().manual_seed(n)
+    counts = torch.randint(0, 50, (n,), generator=g, dtype=torch.int32)
+    offsets, total = tiling.scan_device(counts.to(DEV))
+    ref = np.cumsum(counts.numpy().astype(np.int64))
+    np.testing.assert_array_equal(_np(offsets).astype(np.int64), ref)
+    assert int(total.item()) == int(ref[-1])
+
+
+@pytest.mark.parametrize("count,end_bit", [(1, 45), (5, 41), (4095, 40), (4096, 45), (70_001, 47), (3_000_000, 45)])
+def test_radix_sort_stable_bit_exact(count, end_bit):
+    _say(f"sort count={count} end_bit={end_bit}")
+    rng = np.random.default_rng(count)
+    hi = rng.integers(0, 1 << (end_bit - 32), size=count, dtype=np.uint64)
+    lo = rng.integers(0, 1 << 10, size=count, dtype=np.uint64) << np.uint64(20)  # many ties
+    keys = (hi << np.uint64(32)) | lo
+    vals = rng.integers(0, 1 << 30, size=count).astype(np.int32)
+    k = torch.empty(2 * count, dtype=torch.int64, device=DEV)
+    v = torch.empty(2 * count, dtype=torch.int32, device=DEV)
+    k[:count] = torch.from_numpy(keys.view(np.int64)).to(DEV)
+    v[:count] = torch.from_numpy(vals).to(DEV)
+    tiling.sort_pairs(k, v, count, end_bit)
+    order = np.argsort(keys, kind="stable")
+    np.testing.assert_array_equal(_np(k[:count]).view(np.uint64), keys[order])
+    np.testing.assert_array_equal(_np(v[:count]), vals[order])
+
+
+@pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3)])
+def test_binning_bit_exact(key, degree):
+    scene = _scene(key)
+    _say(f"binning {key}")
+    quats, full, inverse, centers, errors, st = _project(scene, degree)
+    offsets, count = tiling.scan_counts(st.tile_counts)
+    bins = binning.emit_and_sort(st.centers, st.radii, st.depths, offsets, count, scene.width, scene.height)
+    ro, rtotal = oracle.scan_i32(_np(st.tile_counts).ravel())
+    assert rtotal == count
+    np.testing.assert_array_equal(_np(offsets), ro)
+    keys, vals = oracle.emit_keys(_np(st.centers), _np(st.radii), _np(st.depths), ro, rtotal, scene.width,
+                                  scene.height)
+    views = scene.viewmats.shape[0]
+    T = views * ((scene.width + 15) // 16) * ((scene.height + 15) // 16)
+    sk, sv = oracle.sort_pairs(keys, vals, 32 + int(T).bit_length())
+    np.testing.assert_array_equal(_np(bins["point_list_keys"]).view(np.uint64), sk)
+    np.testing.assert_array_equal(_np(bins["point_list"]), sv)
+    np.testing.assert_array_equal(_np(bins["ranges"]), oracle.tile_ranges(sk, T))
+
+
+def _frame(scene, degree):
+    quats, full, inverse, centers, errors, st = _project(scene, degree)
+    offsets, count = tiling.scan_counts(st.tile_counts)
+    bins = binning.emit_and_sort(st.centers, st.radii, st.depths, offsets, count, scene.width, scene.height)
+    return quats, full, inverse, centers, st, bins
+
+
+@pytest.mark.parametrize("key,degree,extra,bg", [("small_rgb", None, False, True), ("sh3_4view", 3, False, False),
+                                                 ("small_rgb", None, True, True)])
+def test_render_forward_bit_exact(key, degree, extra, bg):
+    scene = _scene(key)
+    _say(f"render fwd {key} extra={extra} bg={bg}")
+    quats, full, inverse, centers, st, bins = _frame(scene, degree)
+    views = scene.viewmats.shape[0]
+    feats = st.colors if degree is not None else scene.features
+    ex = torch.randn((st.radii.shape[1], 2), device=DEV) if extra else None
+    background = torch.rand((views, 3), device=DEV) if bg else None
+    out = grender.render_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats, scene.width,
+                               scene.height, extra=ex, background=background)
+    img, ft, ct = oracle.render_fwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]),
+                                    _np(st.centers), _np(st.conics), _np(feats), extra=None if ex is None else _np(ex),
+                                    background=None if background is None else _np(background))
+    np.testing.assert_array_equal(_np(out.contributors), ct)
+    np.testing.assert_array_equal(_np(out.transmittance), ft)
+    np.testing.assert_array_equal(_np(out.features), img)
+    assert ct.max() > 0
+
+
+@pytest.mark.parametrize("key,degree,absgrad", [("small_rgb", None, True), ("sh3_4view", 3, False)])
+def test_render_backward_parity(key, degree, absgrad):
+    scene = _scene(key)
+    _say(f"render bwd {key}")
+    quats, full, inverse, centers, st, bins = _frame(scene, degree)
+    views = scene.viewmats.shape[0]
+    feats = st.colors if degree is not None else scene.features
+    background = torch.rand((views, 3), device=DEV)
+    out = grender.render_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats, scene.width,
+                               scene.height, background=background)
+    up = torch.randn(out.features.shape, device=DEV)
+    record, gf, _ = grender.backward_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats,
+                                           out.transmittance, out.contributors, up, scene.width, scene.height,
+                                           background=background, absgrad=absgrad)
+    ref = oracle.render_bwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]), _np(st.centers),
+                            _np(st.conics), _np(feats), _np(out.transmittance), _np(out.contributors), _np(up),
+                            background=_np(background), absgrad=absgrad)
+    rec = _np(record)
+    for name, got, want in (("centers", rec[..., 0:2], ref["centers"]), ("conics", rec[..., 2:6], ref["conics"]),
+                            ("features", _np(gf), ref["features"])):
+        compare(name, got, want, rtol=1e-4, atol=1e-5 * max(1.0, np.abs(want).max()))
+    if absgrad:
+        compare("abs", rec[..., 6:8], ref["abs"], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(ref["abs"]).max()))
+
+
+@pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3), ("sh3_720p", 1)])
+def test_projection_backward_parity(key, degree):
+    scene = _scene(key)
+    _say(f"projection bwd {key} degree={degree}")
+    quats, full, inverse, centers, errors, st = _project(scene, degree)
+    views, n = st.radii.shape
+    g = torch.Generator().manual_seed(5)
+    gc = torch.randn((views, n, 2), generator=g).to(DEV)
+    gk = torch.randn((views, n, 4), generator=g).to(DEV) * 0.1
+    gcol = torch.randn((views, n, 3), generator=g).to(DEV) if degree is not None else None
+    res = gproj.backward_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks,
+                               scene.width, scene.height, st.radii, gc, gk, (True,) * 6,
+                               sh=scene.sh_coeffs if degree is not None else None, sh_degree=degree or 0,
+                               camera_centers=centers if degree else None, grad_colors=gcol,
+                               need_sh=degree is not None, need_centers=bool(degree))
+    ref = oracle.project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+                             _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height, _np(st.radii),
+                             _np(gc), _np(gk), sh=_np(scene.sh_coeffs) if degree is not None else None,
+                             sh_degree=degree or 0, camera_centers=_np(centers) if degree else None,
+                             grad_colors=None if gcol is None else _np(gcol))
+    for name in ("means", "quats", "scales", "opacities"):
+        compare(name, _np(res[name]), ref[name], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(ref[name]).max()))
+    for name in ("view", "projection"):
+        compare(name, _np(res[name]), ref[name], rtol=1e-3, atol=1e-4 * max(1.0, np.abs(ref[name]).max()))
+    if degree is not None:
+        compare("sh", _np(res["sh"]), ref["sh"], rtol=1e-4, atol=1e-6)
+    if degree:
+        compare("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], rtol=1e-3,
+                atol=1e-4 * max(1.0, np.abs(ref["camera_centers"]).max()))
