@@ -5,6 +5,8 @@ Use ``dsl_splat_amd.gs3d.rasterize`` (method API) or
 reference package root, importing this package loads no other method.
 """
 
+import importlib
+
 from .cameras import PinholeCamera
 
 __all__ = ["PinholeCamera", "gs3d"]
@@ -12,7 +14,5 @@ __all__ = ["PinholeCamera", "gs3d"]
 
 def __getattr__(name):
     if name == "gs3d":
-        from . import gs3d
-
-        return gs3d
+        return importlib.import_module(f"{__name__}.gs3d")
     raise AttributeError(name)

@@ -284,7 +284,8 @@ int launch_bwd(const gs3d_render_bwd_args& b, unsigned blocks, hipStream_t s) {
 inline int check_render_args(const gs3d_render_args& a) {
     if (a.width <= 0 || a.height <= 0 || a.views < 0 || a.n < 0) return GS3D_ERR_ARGUMENT;
     if (a.feat_channels < 0 || a.extra_channels < 0 || (a.extra_channels > 0 && !a.extra)) return GS3D_ERR_ARGUMENT;
-    if (a.views > 0 && (!a.ranges || !a.centers || !a.conics || (a.feat_channels > 0 && !a.features)))
+    if (a.views > 0 && !a.ranges) return GS3D_ERR_ARGUMENT;
+    if (a.views > 0 && a.n > 0 && (!a.centers || !a.conics || (a.feat_channels > 0 && !a.features)))
         return GS3D_ERR_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(a.centers) & 7) || (reinterpret_cast<uintptr_t>(a.conics) & 15))
         return GS3D_ERR_ARGUMENT;

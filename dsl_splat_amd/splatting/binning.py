@@ -33,19 +33,18 @@ def require_radius_mode(mode) -> None:
         )
 
 
+def tile_count(width: int, height: int, views: int = 1) -> int:
+    return views * ((width + 15) // 16) * ((height + 15) // 16)
+
+
 @torch.no_grad()
-def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, count: int, width: int,
-                  height: int) -> TileBins:
-    """Emit keys for (views, N) rows given inclusive offsets and their total,
-    then sort them and extract per-(view, tile) ranges."""
+def emit_keys(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, count: int, width: int,
+              height: int) -> tuple[Tensor, Tensor]:
+    """Keys/ids (2*count storage each) of the (views, N) rows' tile pairs."""
     device = radii.device
-    centers = centers.reshape(-1, radii.shape[-1], 2) if centers.ndim == 2 else centers
     views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
-    gx, gy = (width + 15) // 16, (height + 15) // 16
-    tiles = views * gx * gy
     keys = torch.empty(2 * count, dtype=torch.int64, device=device)
     ids = torch.empty(2 * count, dtype=torch.int32, device=device)
-    ranges = torch.zeros((tiles, 2), dtype=torch.int32, device=device)
     if count:
         a = abi.EmitArgs()
         a.n, a.views, a.width, a.height = n, views, width, height
@@ -55,6 +54,19 @@ def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tenso
         a.keys, a.values = native.ptr(keys), native.ptr(ids)
         scratch = _scratch(native.query("gs3d_emit_scratch_bytes", views * n), device)
         native.call("gs3d_emit_keys", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
+    return keys, ids
+
+
+@torch.no_grad()
+def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, count: int, width: int,
+                  height: int) -> TileBins:
+    """Emit keys for (views, N) rows given inclusive offsets and their total,
+    then sort them and extract per-(view, tile) ranges."""
+    views = 1 if radii.ndim == 1 else radii.shape[0]
+    tiles = tile_count(width, height, views)
+    keys, ids = emit_keys(centers, radii, depths, offsets, count, width, height)
+    ranges = torch.zeros((tiles, 2), dtype=torch.int32, device=radii.device)
+    if count:
         sort_pairs(keys, ids, count, 32 + int(tiles).bit_length())
         identify_ranges(keys[:count], ranges)
     return dict(point_list=ids[:count], ranges=ranges, point_list_keys=keys[:count], point_offsets=offsets)

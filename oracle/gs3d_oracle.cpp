@@ -34,6 +34,7 @@
 #include <vector>
 
 #include <omp.h>
+#include <parallel/algorithm>
 
 #include "gs3d_hip.h"
 
@@ -937,18 +938,29 @@ int oracle_emit_keys(const gs3d_emit_args* a) {
     return 0;
 }
 
-// primitives/tiling.py:67-86: stable sort on key bits [0, end_bit).
+// primitives/tiling.py:67-86: stable sort on key bits [0, end_bit).  Sorting
+// (masked key, input position) pairs, which are all distinct, gives exactly
+// the stable order; the parallel sort then needs no stability of its own.
 int oracle_sort_pairs_u64(uint64_t* keys, int32_t* values, int64_t count, int32_t end_bit) {
     const uint64_t mask = end_bit >= 64 ? ~0ull : ((1ull << end_bit) - 1ull);
-    std::vector<int64_t> idx(count);
-    std::iota(idx.begin(), idx.end(), 0);
-    std::stable_sort(idx.begin(), idx.end(),
-                     [&](int64_t x, int64_t y) { return (keys[x] & mask) < (keys[y] & mask); });
+    struct Item {
+        uint64_t key;
+        int64_t pos;
+        bool operator<(const Item& o) const { return key < o.key || (key == o.key && pos < o.pos); }
+    };
+    std::vector<Item> items(count);
+    for (int64_t i = 0; i < count; ++i) items[i] = Item{keys[i] & mask, i};
+    if (g_threads > 1) {
+        omp_set_num_threads(g_threads);
+        __gnu_parallel::sort(items.begin(), items.end());
+    } else {
+        std::sort(items.begin(), items.end());
+    }
     std::vector<uint64_t> k2(count);
     std::vector<int32_t> v2(count);
     for (int64_t i = 0; i < count; ++i) {
-        k2[i] = keys[idx[i]];
-        v2[i] = values[idx[i]];
+        k2[i] = keys[items[i].pos];
+        v2[i] = values[items[i].pos];
     }
     std::copy(k2.begin(), k2.end(), keys);
     std::copy(v2.begin(), v2.end(), values);

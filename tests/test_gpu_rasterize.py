@@ -1,0 +1,204 @@
+"""End-to-end parity of the public entry points with the oracle pipeline.
+
+gs3d.rasterize / gs3d.gsplat.rasterization / gs3d.ops run forward and
+backward on the GPU for a loss sum(image * W) over every blended channel
+(features, extra channels, alpha); the oracle composes the same stages on
+the GPU-normalised quaternions.  Forward images and metadata are bit-exact;
+gradients are within rtol 1e-4 / atol 1e-5 of the gradient scale (atomic
+accumulation order differs).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_pipeline
+from oracle_pipeline import compare
+from dsl_splat_amd import gs3d, synthetic
+from dsl_splat_amd.cameras import PinholeCamera
+from dsl_splat_amd.gs3d import gsplat, ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+CASES = {
+    "small_rgb_bg": dict(name="small", n=3000, width=96, height=80, seed=11, background=True),
+    "sh3_4view": dict(name="sh3_1080p_4view", n=8000, width=160, height=96, seed=12),
+    "sh3_720p_absgrad": dict(name="sh3_720p", n=6000, width=192, height=112, seed=13),
+    "feat32_extra": dict(name="feat32", n=4000, width=128, height=96, seed=14),
+    "pose_fanout": dict(name="pose_fanout", n=4000, width=160, height=96, seed=15),
+}
+
+
+def _normalize_vjp(q, g):
+    q = q.astype(np.float64)
+    norm = np.linalg.norm(q, axis=-1, keepdims=True)
+    u = q / norm
+    return (g - u * np.sum(u * g, axis=-1, keepdims=True)) / norm
+
+
+def _run_case(key, entry="rasterize"):
+    cfg = dict(CASES[key])
+    name = cfg.pop("name")
+    background = cfg.pop("background", False)
+    scene = synthetic.make_scene(name, **cfg).to(DEV)
+    views = scene.viewmats.shape[0]
+    print(f"case {key} entry={entry} views={views} n={len(scene.means)}", flush=True)
+    params = dict(means=scene.means, quats=scene.quats, scales=scene.scales, opacities=scene.opacities)
+    leaves = {k: v.clone().requires_grad_(True) for k, v in params.items()}
+    colors = (scene.sh_coeffs if scene.sh_coeffs is not None else scene.features).clone().requires_grad_(True)
+    extra = None if scene.extra_features is None else scene.extra_features[0].clone().requires_grad_(True)
+    viewmats = scene.viewmats.clone().requires_grad_(scene.pose_grad)
+    bg = torch.rand((views, colors.shape[-1]), device=DEV) if background else None
+    sh = scene.sh_coeffs is not None
+    if entry == "rasterize":
+        res = gs3d.rasterize(leaves["means"], leaves["quats"], leaves["scales"], leaves["opacities"], viewmats,
+                             scene.Ks, scene.width, scene.height, features=None if sh else colors,
+                             sh_coeffs=colors if sh else None, sh_degree=scene.sh_degree, backgrounds=bg,
+                             extra_features=extra, absgrad=scene.absgrad)
+        feats, alpha, meta = res.features, res.alpha, res.meta
+        ext = res.extra_features
+    else:
+        feats, alpha, meta = gsplat.rasterization(
+            leaves["means"], leaves["quats"], leaves["scales"], leaves["opacities"], colors, viewmats, scene.Ks,
+            scene.width, scene.height, near_plane=0.2, sh_degree=scene.sh_degree, packed=False, backgrounds=bg,
+            absgrad=scene.absgrad, extra_signals=extra)
+        ext = meta.get("render_extra_signals")
+    W = scene.loss_weights
+    D = feats.shape[-1]
+    loss = (feats * W[..., :D]).sum() + (alpha * W[..., -1:]).sum()
+    if ext is not None:
+        loss = loss + (ext * W[..., D:-1]).sum()
+    meta["means2d"].retain_grad()
+    loss.backward()
+    torch.cuda.synchronize()
+    qn = torch.nn.functional.normalize(scene.quats, dim=-1)
+    ref = oracle_pipeline.run(
+        _np(scene.means), _np(qn), _np(scene.scales), _np(scene.opacities), _np(scene.viewmats), _np(scene.Ks),
+        scene.width, scene.height, features=None if sh else _np(colors), sh=_np(colors) if sh else None,
+        sh_degree=scene.sh_degree, extra=None if extra is None else _np(extra),
+        background=None if bg is None else _np(bg), upstream=_np(W), absgrad=scene.absgrad)
+    # Forward: bit-exact images and metadata.
+    image = torch.cat([feats] + ([ext] if ext is not None else []) + [alpha], -1)
+    np.testing.assert_array_equal(_np(image), ref["image"])
+    proj = ref["proj"]
+    np.testing.assert_array_equal(_np(meta["radii"])[..., 0], proj["radii"])
+    np.testing.assert_array_equal(_np(meta["means2d"]), proj["means2d"])
+    np.testing.assert_array_equal(_np(meta["conics"]), proj["meta_conics"])
+    np.testing.assert_array_equal(_np(meta["opacities"]), proj["meta_opacities"])
+    np.testing.assert_array_equal(_np(meta["tiles_per_gauss"]), proj["tiles"])
+    assert meta["backend"] == "gs3d-hip" and meta["n_cameras"] == views
+    # Backward.
+    pg, rg = ref["proj_grads"], ref["render_grads"]
+    tol = lambda a: dict(rtol=1e-4, atol=1e-5 * max(1.0, float(np.abs(a).max())))
+    compare("means", _np(leaves["means"].grad), pg["means"], **tol(pg["means"]))
+    compare("scales", _np(leaves["scales"].grad), pg["scales"], **tol(pg["scales"]))
+    compare("opacities", _np(leaves["opacities"].grad), pg["opacities"], **tol(pg["opacities"]))
+    gq = _normalize_vjp(_np(scene.quats), pg["quats"])
+    compare("quats", _np(leaves["quats"].grad), gq, **tol(gq))
+    gcol = pg["sh"] if sh else rg["features"]
+    compare("colors", _np(colors.grad), gcol, **tol(gcol))
+    if extra is not None:
+        compare("extra", _np(extra.grad), rg["extra"], **tol(rg["extra"]))
+    compare("means2d", _np(meta["means2d"].grad), rg["centers"], **tol(rg["centers"]))
+    if scene.absgrad:
+        compare("absgrad", _np(meta["means2d"].absgrad), rg["abs"], **tol(rg["abs"]))
+    if scene.pose_grad:
+        compare("viewmats", _np(viewmats.grad), ref["grad_viewmats"], rtol=1e-3,
+                atol=1e-4 * max(1.0, float(np.abs(ref["grad_viewmats"]).max())))
+
+
+@pytest.mark.parametrize("key", list(CASES))
+def test_rasterize_matches_oracle(key):
+    _run_case(key)
+
+
+@pytest.mark.parametrize("key", ["sh3_720p_absgrad", "pose_fanout"])
+def test_gsplat_adapter_matches_oracle(key):
+    _run_case(key, entry="gsplat")
+
+
+def test_gsplat_packed_metadata():
+    scene = synthetic.make_scene("sh3_720p", n=3000, width=128, height=80, seed=21).to(DEV)
+    means = scene.means.clone().requires_grad_(True)
+    colors, alpha, meta = gsplat.rasterization(means, scene.quats, scene.scales, scene.opacities, scene.sh_coeffs,
+                                               scene.viewmats, scene.Ks, scene.width, scene.height, sh_degree=3,
+                                               absgrad=True)
+    dense = gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats, scene.Ks,
+                           scene.width, scene.height, sh_coeffs=scene.sh_coeffs, near_plane=0.01, far_plane=1e10)
+    visible = dense.meta["radii"][0, :, 0] > 0
+    assert meta["packed"] and meta["gaussian_ids"].numel() == int(visible.sum())
+    np.testing.assert_array_equal(_np(meta["gaussian_ids"]), np.nonzero(_np(visible))[0])
+    np.testing.assert_array_equal(_np(meta["means2d"]), _np(dense.meta["means2d"][0][visible]))
+    np.testing.assert_array_equal(_np(colors), _np(dense.features))
+    (colors.sum() + alpha.sum()).backward()
+    assert meta["means2d"].grad.shape == meta["means2d"].shape
+    assert meta["means2d"].absgrad.shape == meta["means2d"].shape
+    assert torch.all(meta["means2d"].absgrad >= meta["means2d"].grad.abs() - 1e-6)
+
+
+def test_ops_staged_api_matches_fused():
+    scene = synthetic.make_scene("small", n=3000, width=96, height=80, seed=31).to(DEV)
+    cam = PinholeCamera(scene.viewmats[0], scene.Ks[0], scene.width, scene.height, near_plane=0.2,
+                        far_plane=float("inf"))
+    means = scene.means.clone().requires_grad_(True)
+    feats = scene.features.clone().requires_grad_(True)
+    geometry = ops.prepare_gaussians(means, scene.quats, scene.scales, scene.opacities, cam)
+    tiles = ops.bin_and_sort(geometry)
+    pix = ops.rasterize_to_pixels(geometry, tiles, feats)
+    fused = gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats, scene.Ks,
+                           scene.width, scene.height, features=scene.features)
+    np.testing.assert_array_equal(_np(pix.features), _np(fused.features[0]))
+    np.testing.assert_array_equal(_np(pix.alpha), _np(fused.alpha[0]))
+    W = scene.loss_weights[0]
+    ((pix.features * W[..., :3]).sum() + (pix.alpha * W[..., 3:]).sum()).backward()
+    m2 = scene.means.clone().requires_grad_(True)
+    f2 = scene.features.clone().requires_grad_(True)
+    r2 = gs3d.rasterize(m2, scene.quats, scene.scales, scene.opacities, scene.viewmats, scene.Ks, scene.width,
+                        scene.height, features=f2)
+    ((r2.features[0] * W[..., :3]).sum() + (r2.alpha[0] * W[..., 3:]).sum()).backward()
+    compare("ops_means", _np(means.grad), _np(m2.grad), rtol=1e-4, atol=1e-5 * float(m2.grad.abs().max()))
+    compare("ops_features", _np(feats.grad), _np(f2.grad), rtol=1e-4, atol=1e-6)
+
+
+def test_empty_and_culled_inputs():
+    scene = synthetic.make_scene("small", n=500, width=64, height=48, seed=41).to(DEV)
+    # Everything behind the camera: no pairs, background only, zero gradients.
+    means = (-scene.means).clone().requires_grad_(True)
+    bg = torch.tensor([[0.2, 0.4, 0.6]], device=DEV)
+    res = gs3d.rasterize(means, scene.quats, scene.scales, scene.opacities, scene.viewmats, scene.Ks, 64, 48,
+                         features=scene.features, backgrounds=bg)
+    assert torch.all(res.meta["radii"] == 0)
+    assert torch.equal(res.features[0], bg[0].expand(48, 64, 3))
+    assert torch.all(res.alpha == 0)
+    res.features.sum().backward()
+    assert torch.all(means.grad == 0)
+    # N = 0.
+    empty = torch.zeros((0, 3), device=DEV)
+    res0 = gs3d.rasterize(empty, torch.zeros((0, 4), device=DEV), empty, torch.zeros((0,), device=DEV),
+                          scene.viewmats, scene.Ks, 64, 48, features=torch.zeros((0, 3), device=DEV))
+    assert res0.features.shape == (1, 48, 64, 3) and torch.all(res0.alpha == 0)
+
+
+def test_camera_errors_raise():
+    scene = synthetic.make_scene("small", n=100, width=32, height=32, seed=51).to(DEV)
+    K = scene.Ks.clone()
+    K[0, 0, 1] = 0.1
+    with pytest.raises(NotImplementedError):
+        gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats, K, 32, 32,
+                       features=scene.features)
+    K = scene.Ks.clone()
+    K[0, 0, 0] = float("nan")
+    with pytest.raises(ValueError):
+        gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats, K, 32, 32,
+                       features=scene.features)
+    V = scene.viewmats.clone()
+    V[0, 2] = V[0, 1]
+    sh = torch.zeros((100, 4, 3), device=DEV)
+    with pytest.raises(torch.linalg.LinAlgError):
+        gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, V, scene.Ks, 32, 32, sh_coeffs=sh)

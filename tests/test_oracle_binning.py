@@ -83,3 +83,17 @@ def test_ranges_ignore_invalid_tile(oracle_lib):
     keys = np.array([(3 << 32), (3 << 32) | 1, (0xFFFFFFFF << 32)], np.uint64)
     r = oracle_lib.tile_ranges(keys, 5)
     assert r[3].tolist() == [0, 2] and r[0].tolist() == [0, 0]
+
+
+def test_parallel_sort_path_matches_stable_order(oracle_lib):
+    rng = np.random.default_rng(11)
+    keys = (rng.integers(0, 1 << 13, 200_000).astype(np.uint64) << np.uint64(32)) | rng.integers(0, 64, 200_000).astype(np.uint64)
+    vals = np.arange(200_000, dtype=np.int32)
+    oracle_lib.set_threads(4)
+    try:
+        sk, sv = oracle_lib.sort_pairs(keys, vals, 45)
+    finally:
+        oracle_lib.set_threads(1)
+    order = np.argsort(keys, kind="stable")
+    np.testing.assert_array_equal(sk, keys[order])
+    np.testing.assert_array_equal(sv, vals[order])
