@@ -99,7 +99,7 @@ def stage_timings(scene, reps):
     sh = scene.sh_coeffs
     deg = scene.sh_degree
     views, n = scene.viewmats.shape[0], len(scene.means)
-    names = ("camera", "project", "scan", "emit", "sort", "ranges", "render_fwd", "render_bwd", "project_bwd")
+    names = ("camera", "project", "order", "emit", "sort", "ranges", "render_fwd", "render_bwd", "project_bwd")
     acc = {k: 0.0 for k in names}
     info = {}
     with torch.no_grad():
@@ -114,19 +114,18 @@ def stage_timings(scene, reps):
                                      sh=sh, sh_degree=deg or 0, camera_centers=centers if deg else None,
                                      metadata=True)
             ev[2].record()
-            offsets, total = tiling.scan_device(st.tile_counts)
+            order, offsets, total = binning.depth_order(st.depths, st.tile_counts)
             ev[3].record()
             count = int(total.item())
             ev[4].record()
-            keys, ids = binning.emit_keys(st.centers, st.radii, st.depths, offsets, count, scene.width, scene.height)
+            tiles_k, ids = binning.emit_ordered(st.centers, st.radii, order, offsets, count, scene.width,
+                                                scene.height)
             ev[5].record()
             tiles = binning.tile_count(scene.width, scene.height, views)
-            end_bit = 32 + int(tiles).bit_length()
-            tiling.sort_pairs(keys, ids, count, end_bit)
+            binning.sort_by_tile(tiles_k, ids, count, tiles)
             ev[6].record()
-            ranges = torch.zeros((tiles, 2), dtype=torch.int32, device=keys.device)
             ev[7].record()
-            tiling.identify_ranges(keys[:count], ranges)
+            ranges = binning.ranges_of(tiles_k, count, tiles)
             ev[8].record()
             feats = st.colors if sh is not None else scene.features
             out = grender.render_views(ranges, ids[:count], st.centers, st.conics, feats, scene.width, scene.height)
@@ -144,26 +143,25 @@ def stage_timings(scene, reps):
             ev[11].record()
             torch.cuda.synchronize()
             if rep == 0:
-                visited = None
-                info = dict(pairs=count, passes=math.ceil(end_bit / 8), end_bit=end_bit, tiles=tiles,
-                            visible=int((st.radii > 0).sum()),
+                info = dict(pairs=count, passes=math.ceil(int(tiles).bit_length() / 8), tiles=tiles,
+                            rows=views * n, visible=int((st.radii > 0).sum()),
                             mean_contributors=float(out.contributors.float().mean()))
                 continue  # warm-up repetition
-            spans = {"camera": (0, 1), "project": (1, 2), "scan": (2, 3), "emit": (4, 5), "sort": (5, 6),
+            spans = {"camera": (0, 1), "project": (1, 2), "order": (2, 3), "emit": (4, 5), "sort": (5, 6),
                      "ranges": (7, 8), "render_fwd": (8, 9), "render_bwd": (9, 10), "project_bwd": (10, 11)}
             for k, (a, b) in spans.items():
                 acc[k] += ev[a].elapsed_time(ev[b]) / reps
     # Algorithmic bytes per launch ("Roofline accounting").
-    M, P, T = info["pairs"], info["passes"], info["tiles"]
+    M, P, T, R = info["pairs"], info["passes"], info["tiles"], info["rows"]
     K = 0 if sh is None else sh.shape[-2]
     sh_bytes = 0 if sh is None else (n if sh.ndim == 3 else views * n) * K * 3 * 4
     by = {
         "project": n * (12 + 16 + 12 + 4) + sh_bytes + views * n * (8 + 16 + 4 + 4 + 4 + 8 + 4 + 12 +
                                                                     (12 if sh is not None else 0)),
-        "scan": views * n * (4 + 4),
-        "emit": views * n * (4 + 8 + 4 + 4) + M * 12,
-        "sort": 24 * P * M,
-        "ranges": 8 * M + 8 * T,
+        "order": R * (8 + 8 + 4 * 16),
+        "emit": R * (4 + 4 + 4 + 8) + M * 8,
+        "sort": 16 * P * M,
+        "ranges": 4 * M + 8 * T,
     }
     return acc, by, info
 
@@ -256,7 +254,7 @@ def main():
     ms = (t1 - t0) * 1000.0 / args.steps
     log(f"[bench] {ms:.3f} ms/iter; stage timings")
     stages, by, info = stage_timings(scene, args.stage_reps)
-    s13 = ("project", "scan", "emit", "sort", "ranges")
+    s13 = ("project", "order", "emit", "sort", "ranges")
     t13 = sum(stages[k] for k in s13)
     b13 = sum(by[k] for k in s13)
     achieved = b13 / (t13 * 1e-3) / 1e9
@@ -292,7 +290,8 @@ def main():
         "bwd_ms": round(bwd_ms / args.steps, 3),
         "roofline": {
             "bound": "hbm",
-            "kernel": "stages 1-3: projection+SH+metadata, scan, key emission, radix sort, tile ranges",
+            "kernel": "stages 1-3: projection+SH+metadata, depth ordering+scan, pair emission, tile radix sort, "
+                      "tile ranges",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

@@ -2,9 +2,11 @@
 
 Same signature, defaults, validation errors, outputs and ``meta`` keys.  Per
 Gaussian batch the host issues: one camera launch, one fused projection
-(+SH +metadata) launch for all cameras, one scan, ONE host synchronisation
-(camera status codes and the pair count together), emission, one radix sort
-over all cameras' pairs, ranges, and one blend launch for all cameras.
+(+SH +metadata) launch for all cameras, the depth ordering of all
+(camera, Gaussian) rows with the scan of their tile counts, ONE host
+synchronisation (camera status codes and the pair count together), pair
+emission in depth order, one stable radix sort of all cameras' pairs on the
+tile id, ranges, and one blend launch for all cameras.
 """
 
 from dataclasses import dataclass, field
@@ -19,8 +21,7 @@ from .autograd import Frame, Rasterize
 from .projection import project_views
 from ..cameras import validate_camera_options
 from ..inputs import batch_item, normalize_inputs
-from ..primitives.tiling import scan_device
-from ..splatting.binning import emit_and_sort, require_radius_mode, validate_tile_mode
+from ..splatting.binning import depth_order, finish_binning, require_radius_mode, validate_tile_mode
 from ..splatting.cameras import launch_prepare, raise_camera_errors
 from ..statistics import StatisticsRequest
 from ..training import prepare_training_metadata
@@ -61,13 +62,13 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
         sh=sh if sh_degree is not None else None, sh_degree=sh_degree or 0,
         camera_centers=centers if with_centers else None, metadata=True,
     )
-    offsets, total = scan_device(state.tile_counts)
+    order, offsets, total = depth_order(state.depths, state.tile_counts)
     host = torch.cat([errors.to(torch.int64), total]).cpu().tolist()
     raise_camera_errors(host[:-1])
     count = int(host[-1]) if len(offsets) else 0
     if count > 2**31 - 1:
         raise OverflowError(f"{count} tile pairs exceed the int32 offsets of the binning stage")
-    bins = emit_and_sort(state.centers, state.radii, state.depths, offsets, count, width, height)
+    bins = finish_binning(state.centers, state.radii, state.depths, order, offsets, count, width, height)
     return Frame(
         width, height, Ks.detach(), full, inverse if with_centers else None, centers if with_centers else None,
         state, bins["ranges"], bins["point_list"], count, sh_degree, background,

@@ -73,12 +73,101 @@ def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tenso
 
 
 @torch.no_grad()
+def depth_order(depths: Tensor, tile_counts: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """Rows (views*N) stably sorted by depth bits; inclusive offsets of their
+    tile counts in that order and the int64 total (all left on the device).
+    Returns (order with 2*rows storage, offsets, total)."""
+    device = depths.device
+    rows = depths.numel()
+    order = torch.empty(2 * rows, dtype=torch.int32, device=device)
+    offsets = torch.empty(rows, dtype=torch.int32, device=device)
+    total = torch.zeros(1, dtype=torch.int64, device=device)
+    if rows:
+        depths, tile_counts = depths.contiguous(), tile_counts.contiguous()
+        scratch = _scratch(native.query("gs3d_depth_order_scratch_bytes", rows), device)
+        native.call("gs3d_depth_order", native.ptr(depths), native.ptr(tile_counts), rows, native.ptr(order),
+                    native.ptr(offsets), native.ptr(total), native.ptr(scratch), scratch.numel(),
+                    native.stream(device))
+    return order, offsets, total
+
+
+@torch.no_grad()
+def emit_ordered(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, count: int, width: int,
+                 height: int) -> tuple[Tensor, Tensor]:
+    """(uint32 global tile ids stored as int32, int32 Gaussian ids), each with
+    2*count storage, of the ordered rows' tile pairs."""
+    device = radii.device
+    views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
+    tiles = torch.empty(2 * count, dtype=torch.int32, device=device)
+    ids = torch.empty(2 * count, dtype=torch.int32, device=device)
+    if count:
+        a = abi.EmitOrderedArgs()
+        a.n, a.views, a.width, a.height = n, views, width, height
+        centers, radii = centers.contiguous(), radii.contiguous()
+        a.centers, a.radii, a.order, a.offsets = (native.ptr(centers), native.ptr(radii), native.ptr(order),
+                                                  native.ptr(offsets))
+        a.tile_keys, a.values = native.ptr(tiles), native.ptr(ids)
+        native.call("gs3d_emit_ordered", ctypes.byref(a), native.stream(device))
+    return tiles, ids
+
+
+@torch.no_grad()
+def sort_by_tile(tiles: Tensor, ids: Tensor, count: int, tile_total: int) -> None:
+    """Stable sort of the (tile, id) pairs on the tile id, in place."""
+    if count > 1:
+        scratch = _scratch(native.query("gs3d_sort_scratch_bytes", count), tiles.device)
+        native.call("gs3d_sort_pairs_u32", native.ptr(tiles), native.ptr(ids), count, int(tile_total).bit_length(),
+                    native.ptr(scratch), scratch.numel(), native.stream(tiles.device))
+
+
+@torch.no_grad()
+def ranges_of(sorted_tiles: Tensor, count: int, tile_total: int) -> Tensor:
+    ranges = torch.zeros((tile_total, 2), dtype=torch.int32, device=sorted_tiles.device)
+    if count:
+        native.call("gs3d_tile_ranges_u32", native.ptr(sorted_tiles), count, native.ptr(ranges), tile_total,
+                    native.stream(sorted_tiles.device))
+    return ranges
+
+
+@torch.no_grad()
+def expand_keys(sorted_tiles: Tensor, ids: Tensor, count: int, depths: Tensor, width: int, height: int) -> Tensor:
+    """The reference's 64-bit keys (tile << 32 | depth bits) of sorted pairs."""
+    n = depths.shape[-1]
+    keys = torch.empty(count, dtype=torch.int64, device=depths.device)
+    if count:
+        native.call("gs3d_expand_keys", native.ptr(sorted_tiles), native.ptr(ids), count,
+                    native.ptr(depths.contiguous()), n, tile_count(width, height), native.ptr(keys),
+                    native.stream(depths.device))
+    return keys
+
+
+@torch.no_grad()
+def finish_binning(centers: Tensor, radii: Tensor, depths: Tensor, order: Tensor, offsets: Tensor, count: int,
+                   width: int, height: int, *, with_keys: bool = False) -> TileBins:
+    """Emission in depth order, stable tile sort and ranges for a known pair
+    count (the host has read the total of ``depth_order``)."""
+    views = 1 if radii.ndim == 1 else radii.shape[0]
+    tile_total = tile_count(width, height, views)
+    tiles, ids = emit_ordered(centers, radii, order, offsets, count, width, height)
+    sort_by_tile(tiles, ids, count, tile_total)
+    bins: TileBins = dict(point_list=ids[:count], ranges=ranges_of(tiles, count, tile_total))
+    if with_keys:
+        bins["point_list_keys"] = expand_keys(tiles, ids, count, depths, width, height)
+    return bins
+
+
+@torch.no_grad()
 def bin_and_sort(centers: Tensor, radii: Tensor, tile_counts: Tensor, depths: Tensor, width: int, height: int,
-                 bindings=None, *, conics: Tensor | None = None, tile_mode="radius") -> TileBins:
-    """Scan, duplicate, sort and range one view's (N,) or several views'
-    (C, N) projected Gaussians."""
+                 bindings=None, *, conics: Tensor | None = None, tile_mode="radius",
+                 with_keys: bool = False) -> TileBins:
+    """Bin one view's (N,) or several views' (C, N) projected Gaussians into
+    depth-sorted per-tile lists (same order and ranges as the reference's
+    scan + duplicate + 64-bit key sort)."""
     if tile_mode != "radius" and conics is None:
         raise ValueError("SnugBox/AccuTile require projected conics")
     require_radius_mode(tile_mode)
-    offsets, count = scan_counts(tile_counts)
-    return emit_and_sort(centers, radii, depths, offsets, count, width, height)
+    order, offsets, total = depth_order(depths, tile_counts)
+    count = int(total.item()) if depths.numel() else 0
+    if count > 2**31 - 1:
+        raise OverflowError("tile pair count exceeds int32 offsets")
+    return finish_binning(centers, radii, depths, order, offsets, count, width, height, with_keys=with_keys)

@@ -214,9 +214,59 @@ int gs3d_sort_pairs_u64(uint64_t* keys, int32_t* values, int64_t count,
 
 /* Per-tile [first, last) ranges of sorted keys: primitives/tiling.py:39-54
  * (identify_ranges, launched at :87-100).  ranges (tile_count,2) must be
- * zero-initialised by the caller; tile id 0xFFFFFFFF is ignored. */
+ * zero-initialised by the caller; tile ids >= tile_count (0xFFFFFFFF
+ * included) are ignored. */
 int gs3d_tile_ranges(const uint64_t* sorted_keys, int64_t count, int32_t* ranges,
                      int64_t tile_count, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Depth-ordered binning: the same (tile, depth, id) order as
+ * gs3d_emit_keys + gs3d_sort_pairs_u64 (splatting/binning.py:71-117 with
+ * primitives/tiling.py:57-100), with the radix sort over 32-bit tile ids
+ * only.  Steps:
+ *   1. gs3d_depth_order: stable sort of the views*N rows by the bits of their
+ *      depth (order has 2*rows int32 storage: the first half receives the
+ *      row permutation), then the inclusive scan of their tile counts taken
+ *      in that order (offsets) and its 64-bit total.
+ *   2. gs3d_emit_ordered: the pairs of the ordered rows, row-major over each
+ *      tile rectangle, as (uint32 global tile id, int32 Gaussian index).
+ *   3. gs3d_sort_pairs_u32 on bits [0, bit_length(views*tiles)): stable, so
+ *      each tile keeps (depth bits, Gaussian index) order.
+ *   4. gs3d_tile_ranges_u32; gs3d_expand_keys rebuilds the 64-bit keys
+ *      (tile << 32 | depth bits) when a caller wants them.
+ * ---------------------------------------------------------------------- */
+size_t gs3d_depth_order_scratch_bytes(int64_t rows);
+int gs3d_depth_order(const float* depths, const int32_t* tiles, int64_t rows,
+                     int32_t* order, int32_t* offsets, int64_t* total,
+                     void* scratch, size_t scratch_bytes, void* stream);
+
+typedef struct gs3d_emit_ordered_args {
+    int32_t n, views, width, height;
+    const float* centers;     /* (views,N,2) */
+    const int32_t* radii;     /* (views,N) */
+    const int32_t* order;     /* (views*N) row permutation */
+    const int32_t* offsets;   /* (views*N) inclusive, in permutation order */
+    uint32_t* tile_keys;      /* (M) global tile id view*tiles + y*gx + x */
+    int32_t* values;          /* (M) Gaussian index within its view */
+} gs3d_emit_ordered_args;
+
+int gs3d_emit_ordered(const gs3d_emit_ordered_args* args, void* stream);
+
+/* Stable LSD radix sort of (uint32 key, int32 value) pairs over key bits
+ * [0, end_bit); 2*count storage as gs3d_sort_pairs_u64.  Scratch size is
+ * gs3d_sort_scratch_bytes(count). */
+int gs3d_sort_pairs_u32(uint32_t* keys, int32_t* values, int64_t count,
+                        int32_t end_bit, void* scratch, size_t scratch_bytes,
+                        void* stream);
+
+int gs3d_tile_ranges_u32(const uint32_t* sorted_tiles, int64_t count, int32_t* ranges,
+                         int64_t tile_count, void* stream);
+
+/* keys[i] = (tiles[i] << 32) | bits(depths[view*n + ids[i]]), view =
+ * tiles[i] / tiles_per_view. */
+int gs3d_expand_keys(const uint32_t* sorted_tiles, const int32_t* ids, int64_t count,
+                     const float* depths, int32_t n, int32_t tiles_per_view,
+                     uint64_t* keys, void* stream);
 
 /* ------------------------------------------------------------------------
  * Forward alpha blending on 16x16 tiles: gs3d/render.py:36-208 (render,

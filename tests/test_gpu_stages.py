@@ -237,3 +237,77 @@ def test_projection_backward_parity(key, degree):
     if degree:
         compare("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], rtol=1e-3,
                 atol=1e-4 * max(1.0, np.abs(ref["camera_centers"]).max()))
+
+
+@pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3), ("sh3_720p", 0)])
+def test_depth_ordered_binning_matches_reference_order(key, degree):
+    # The production binning (depth-ordered rows, 32-bit tile sort) must give
+    # exactly the reference's ids, ranges and 64-bit keys (scan + duplicate
+    # in Gaussian order + stable sort of (tile << 32 | depth bits)).
+    scene = _scene(key)
+    _say(f"depth-ordered binning {key}")
+    quats, full, inverse, centers, errors, st = _project(scene, degree)
+    bins = binning.bin_and_sort(st.centers, st.radii, st.tile_counts, st.depths, scene.width, scene.height,
+                                with_keys=True)
+    ro, rtotal = oracle.scan_i32(_np(st.tile_counts).ravel())
+    keys, vals = oracle.emit_keys(_np(st.centers), _np(st.radii), _np(st.depths), ro, rtotal, scene.width,
+                                  scene.height)
+    views = scene.viewmats.shape[0]
+    T = views * ((scene.width + 15) // 16) * ((scene.height + 15) // 16)
+    sk, sv = oracle.sort_pairs(keys, vals, 32 + int(T).bit_length())
+    assert len(sv) == bins["point_list"].numel() > 0
+    np.testing.assert_array_equal(_np(bins["point_list"]), sv)
+    np.testing.assert_array_equal(_np(bins["point_list_keys"]).view(np.uint64), sk)
+    np.testing.assert_array_equal(_np(bins["ranges"]), oracle.tile_ranges(sk, T))
+
+
+def test_depth_ordered_binning_ties_and_large_rects():
+    # Equal depths everywhere (ties broken by Gaussian index) and rectangles
+    # spanning the whole image (the block-cooperative emission's long rows).
+    g = torch.Generator().manual_seed(3)
+    views, n, W, H = 2, 3000, 200, 120
+    centers = (torch.rand((views, n, 2), generator=g) * torch.tensor([W, H])).to(DEV)
+    radii = torch.randint(1, 40, (views, n), generator=g, dtype=torch.int32)
+    radii[:, ::97] = 500
+    radii[:, 5::13] = 0
+    depths = torch.full((views, n), 2.5)
+    depths[:, ::7] = 1.25
+    depths[radii == 0] = 0.0
+    radii, depths = radii.to(DEV), depths.to(DEV)
+    gx, gy = (W + 15) // 16, (H + 15) // 16
+    c = _np(centers)
+    r = _np(radii)
+    tiles = np.zeros((views, n), np.int32)
+    import torch_ref
+    for v in range(views):
+        for i in range(n):
+            if r[v, i] > 0:
+                x0, y0, x1, y1 = torch_ref.rect_tiles(c[v, i], r[v, i], W, H)
+                tiles[v, i] = (x1 - x0) * (y1 - y0)
+    r[tiles == 0] = 0
+    radii = torch.from_numpy(r).to(DEV)
+    tiles_t = torch.from_numpy(tiles).to(DEV)
+    bins = binning.bin_and_sort(centers, radii, tiles_t, depths, W, H, with_keys=True)
+    ro, rtotal = oracle.scan_i32(tiles.ravel())
+    keys, vals = oracle.emit_keys(c, r, _np(depths), ro, rtotal, W, H)
+    T = views * gx * gy
+    sk, sv = oracle.sort_pairs(keys, vals, 32 + int(T).bit_length())
+    np.testing.assert_array_equal(_np(bins["point_list"]), sv)
+    np.testing.assert_array_equal(_np(bins["point_list_keys"]).view(np.uint64), sk)
+    np.testing.assert_array_equal(_np(bins["ranges"]), oracle.tile_ranges(sk, T))
+
+
+@pytest.mark.parametrize("count,end_bit", [(2, 13), (4097, 15), (1_000_003, 16), (5_000_000, 32)])
+def test_u32_radix_sort_stable(count, end_bit):
+    _say(f"u32 sort count={count} end_bit={end_bit}")
+    rng = np.random.default_rng(count + 1)
+    keys = rng.integers(0, 1 << end_bit, size=count, dtype=np.uint64).astype(np.uint32)
+    vals = np.arange(count, dtype=np.int32)
+    k = torch.empty(2 * count, dtype=torch.int32, device=DEV)
+    v = torch.empty(2 * count, dtype=torch.int32, device=DEV)
+    k[:count] = torch.from_numpy(keys.view(np.int32)).to(DEV)
+    v[:count] = torch.from_numpy(vals).to(DEV)
+    binning.sort_by_tile(k, v, count, 1 << (end_bit - 1) if end_bit > 1 else 1)
+    order = np.argsort(keys, kind="stable")
+    np.testing.assert_array_equal(_np(k[:count]).view(np.uint32), keys[order])
+    np.testing.assert_array_equal(_np(v[:count]), vals[order])
