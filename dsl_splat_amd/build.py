@@ -7,7 +7,7 @@ then linked into dsl_splat_amd/lib/libgs3d_hip.so.  Floating point: no
 contraction (-ffp-contract=off: the kernels spell out their fmaf calls),
 correctly rounded division/sqrt (hipcc's default), hardware float atomics
 (-munsafe-fp-atomics; all accumulation buffers are ordinary device memory)
-and no packed-FP32 instructions.
+without the compiler's atomic optimizer, and no packed-FP32 instructions.
 """
 
 import argparse
@@ -32,6 +32,10 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-ffp-contract=off",
     "-munsafe-fp-atomics",
+    # Kernels reduce across the wavefront themselves before their atomics;
+    # the compiler's atomic optimizer would wrap each single-lane atomic in
+    # another wave scan.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
     f"-I{os.path.join(ROOT, 'include')}",

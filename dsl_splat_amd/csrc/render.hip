@@ -1,29 +1,70 @@
 // Front-to-back alpha blending on 16x16 tiles and its reverse traversal.
 //
-// gs3d/render.py:36-208 (forward) and :211-356 (backward).  One 256-thread
-// workgroup (four wave64 wavefronts, four pixel rows each) per tile; the
-// tile's sorted Gaussians are staged in LDS in batches of 256 (centre, conic
-// + opacity and the full blended channel vector), so the inner loop reads
-// only LDS broadcasts.  A lane leaves the inner loop as soon as its pixel is
-// done, so a wavefront stops when its 64 pixels are; the block stops at the
-// next batch once all 256 are.
+// gs3d/render.py:36-208 (forward) and :211-356 (backward).  One workgroup
+// per tile.  A lane owns PIX pixels of the tile (1: one pixel, 256 threads;
+// 2: a horizontal pair, 128 threads; 4: a 2x2 quad, 64 threads = one
+// wavefront for the whole tile).  The tile's sorted Gaussians are staged in
+// LDS in batches (centre, conic + opacity, exponent cutoff and the full
+// blended channel vector), so the inner loop reads only LDS broadcasts.  A
+// lane leaves the inner loop once its pixels are done, a wavefront once its
+// lanes are, and the workgroup stops at the next batch once all pixels are.
 //
-// Backward: every lane computes its pixel's contribution to the current
-// Gaussian, the wavefront sums the contributions with DPP (lane 63 holds the
-// sums) and lane 63 issues one atomic per gradient entry, instead of one per
-// pixel as in the reference.  Only batches below the largest last
-// contributor of the tile are visited.
+// Exponent cutoff: a Gaussian with opacity o can only reach alpha >= 1/255
+// where power >= -ln(255 o); below that bound minus a 1% margin (far above
+// the few-ulp error of exp, log and the product) the blend rejects the
+// Gaussian without evaluating exp.  Decisions, and therefore every output,
+// are identical to evaluating it.
+//
+// Backward: every lane accumulates its pixels' contributions to the current
+// Gaussian, the wavefront sums them with DPP (lane 63 holds the sums) and
+// lane 63 issues one atomic per gradient entry, instead of one per pixel as
+// in the reference.  Only batches below the largest last contributor of the
+// tile are visited.
 #include "common.hpp"
+
+#ifndef GS3D_FWD_PIX
+#define GS3D_FWD_PIX 2
+#endif
+#ifndef GS3D_BWD_PIX
+#define GS3D_BWD_PIX 2
+#endif
 
 namespace gs3d {
 
 constexpr int kTile = 16;
-constexpr int kRenderThreads = 256;
+constexpr int kTilePixels = kTile * kTile;
+
+// Gaussians staged per batch: 256 while the channel vectors fit the LDS
+// budget, 128 for the widest vectors.
+template <int CH>
+struct Batch {
+    static constexpr int size = CH <= 36 ? 256 : 128;
+};
+
+// Pixels per lane for a channel count (wide vectors keep one pixel per lane
+// to bound register use).
+template <int CH, int P>
+struct PixFor {
+    static constexpr int value = CH <= 8 ? P : 1;
+};
+
+// Tile-local coordinates of pixel k of thread t.
+template <int PIX>
+GS3D_DEV void pixel_of(int t, int k, int& x, int& y) {
+    if (PIX == 1) {
+        x = t & 15;
+        y = t >> 4;
+    } else if (PIX == 2) {
+        x = 2 * (t & 7) + k;
+        y = t >> 3;
+    } else {
+        x = 2 * (t & 7) + (k & 1);
+        y = 2 * (t >> 3) + (k >> 1);
+    }
+}
 
 struct TileInfo {
-    int view, px, py, first, last;
-    bool inside;
-    int64_t pix;
+    int view, x0, y0, first, last;
 };
 
 GS3D_DEV TileInfo tile_info(const gs3d_render_args& a) {
@@ -34,22 +75,29 @@ GS3D_DEV TileInfo tile_info(const gs3d_render_args& a) {
     t.view = tile / per_view;
     const int local = tile - t.view * per_view;
     const int ty = local / gx, tx = local - ty * gx;
-    t.px = tx * kTile + (threadIdx.x & (kTile - 1));
-    t.py = ty * kTile + (threadIdx.x >> 4);
-    t.inside = t.px < a.width && t.py < a.height;
-    t.pix = ((int64_t)t.view * a.height + t.py) * a.width + t.px;
+    t.x0 = tx * kTile;
+    t.y0 = ty * kTile;
     t.first = a.ranges[2 * (int64_t)tile];
     t.last = a.ranges[2 * (int64_t)tile + 1];
     return t;
 }
 
-// Stage one Gaussian's centre, conic and channel vector into LDS slot.
+// Lowest power at which opacity o can still give alpha >= 1/255 (see the
+// file comment); +inf rejects everything (o <= 0), -inf rejects nothing.
+GS3D_DEV float power_cutoff(float o) {
+    if (o > 0.0f) return -__logf(255.0f * o) - 0.01f;
+    return o <= 0.0f ? __builtin_inff() : -__builtin_inff();
+}
+
+// Stage one Gaussian's centre, conic, cutoff and channel vector.
 template <int CH>
 GS3D_DEV void stage_gaussian(const gs3d_render_args& a, int view, int32_t g, int slot, float2* s_xy, float4* s_con,
-                             float* s_feat) {
+                             float* s_cut, float* s_feat) {
     const int64_t row = (int64_t)view * a.n + g;
     s_xy[slot] = reinterpret_cast<const float2*>(a.centers)[row];
-    s_con[slot] = reinterpret_cast<const float4*>(a.conics)[row];
+    const float4 con = reinterpret_cast<const float4*>(a.conics)[row];
+    s_con[slot] = con;
+    s_cut[slot] = power_cutoff(con.w);
     float* dst = s_feat + slot * CH;
     const float* f = a.features + view * a.feat_view_stride + (int64_t)g * a.feat_stride;
     int c = 0;
@@ -61,75 +109,98 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, int view, int32_t g, int
     if (a.one_tail) dst[c++] = 1.0f;
 }
 
-// Gaussians staged per batch: 256 (one per thread) while the channel vectors
-// fit the LDS budget, 128 for the widest vectors.
-template <int CH>
-struct Batch {
-    static constexpr int size = CH <= 36 ? kRenderThreads : kRenderThreads / 2;
-};
-
-template <int CH>
-__global__ __launch_bounds__(kRenderThreads) void render_fwd_kernel(gs3d_render_args a) {
+template <int CH, int PIX>
+__global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_render_args a) {
+    constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
     __shared__ float2 s_xy[B];
     __shared__ float4 s_con[B];
+    __shared__ float s_cut[B];
     __shared__ float s_feat[B * CH];
     const TileInfo t = tile_info(a);
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
-    const float fx = (float)t.px, fy = (float)t.py;
-    float color[CH];
+    float fx[PIX], fy[PIX], T[PIX], color[PIX][CH];
+    int px[PIX], py[PIX], contributor[PIX], last_contributor[PIX];
+    bool done[PIX];
 #pragma unroll
-    for (int c = 0; c < CH; ++c) color[c] = 0.0f;
-    float T = 1.0f;
-    int contributor = 0, last_contributor = 0;
-    bool done = !t.inside;
+    for (int k = 0; k < PIX; ++k) {
+        int lx, ly;
+        pixel_of<PIX>(threadIdx.x, k, lx, ly);
+        px[k] = t.x0 + lx;
+        py[k] = t.y0 + ly;
+        fx[k] = (float)px[k];
+        fy[k] = (float)py[k];
+        done[k] = !(px[k] < a.width && py[k] < a.height);
+        T[k] = 1.0f;
+        contributor[k] = 0;
+        last_contributor[k] = 0;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) color[k][c] = 0.0f;
+    }
     for (int begin = t.first; begin < t.last; begin += B) {
-        if (__syncthreads_count(!done) == 0) break;
-        const int idx = begin + (int)threadIdx.x;
-        if ((int)threadIdx.x < B && idx < t.last)
-            stage_gaussian<CH>(a, t.view, a.ids[idx], threadIdx.x, s_xy, s_con, s_feat);
+        bool active = false;
+#pragma unroll
+        for (int k = 0; k < PIX; ++k) active = active || !done[k];
+        if (__syncthreads_count(active) == 0) break;
+        for (int e = threadIdx.x; e < B; e += NT) {
+            const int idx = begin + e;
+            if (idx < t.last) stage_gaussian<CH>(a, t.view, a.ids[idx], e, s_xy, s_con, s_cut, s_feat);
+        }
         __syncthreads();
         const int cnt = min(B, t.last - begin);
         for (int j = 0; j < cnt; ++j) {
-            if (done) break;
-            ++contributor;
+            bool any = false;
+#pragma unroll
+            for (int k = 0; k < PIX; ++k) any = any || !done[k];
+            if (!any) break;
             const float2 xy = s_xy[j];
             const float4 con = s_con[j];
-            const float dx = xy.x - fx, dy = xy.y - fy;
-            const float power = blend_power(con.x, con.y, con.z, dx, dy);
-            if (!(power <= 0.0f)) continue;
-            const float alpha = sel_min(0.99f, con.w * blend_exp(power));
-            if (!(alpha >= 1.0f / 255.0f)) continue;
-            const float next_t = T * (1.0f - alpha);
-            if (next_t < 0.0001f) {
-                done = true;
-                continue;
-            }
-            const float w = alpha * T;
+            const float cut = s_cut[j];
             const float* f = s_feat + j * CH;
 #pragma unroll
-            for (int c = 0; c < CH; ++c)
-                if (c < D) color[c] = __builtin_fmaf(f[c], w, color[c]);
-            T = next_t;
-            last_contributor = contributor;
+            for (int k = 0; k < PIX; ++k) {
+                if (done[k]) continue;
+                ++contributor[k];
+                const float dx = xy.x - fx[k], dy = xy.y - fy[k];
+                const float power = blend_power(con.x, con.y, con.z, dx, dy);
+                if (!(power <= 0.0f) || !(power >= cut)) continue;
+                const float alpha = sel_min(0.99f, con.w * blend_exp(power));
+                if (!(alpha >= 1.0f / 255.0f)) continue;
+                const float next_t = T[k] * (1.0f - alpha);
+                if (next_t < 0.0001f) {
+                    done[k] = true;
+                    continue;
+                }
+                const float w = alpha * T[k];
+#pragma unroll
+                for (int c = 0; c < CH; ++c)
+                    if (c < D) color[k][c] = __builtin_fmaf(f[c], w, color[k][c]);
+                T[k] = next_t;
+                last_contributor[k] = contributor[k];
+            }
         }
     }
-    if (t.inside) {
-        float* out = a.image + t.pix * D;
-        const float* bg = a.background ? a.background + t.view * a.background_view_stride : nullptr;
+    const float* bg = a.background ? a.background + t.view * a.background_view_stride : nullptr;
+#pragma unroll
+    for (int k = 0; k < PIX; ++k) {
+        if (!(px[k] < a.width && py[k] < a.height)) continue;
+        const int64_t pix = ((int64_t)t.view * a.height + py[k]) * a.width + px[k];
+        float* out = a.image + pix * D;
 #pragma unroll
         for (int c = 0; c < CH; ++c)
-            if (c < D) out[c] = __builtin_fmaf(T, (bg && c < a.feat_channels) ? bg[c] : 0.0f, color[c]);
-        a.final_t[t.pix] = T;
-        a.contributors[t.pix] = last_contributor;
+            if (c < D) out[c] = __builtin_fmaf(T[k], (bg && c < a.feat_channels) ? bg[c] : 0.0f, color[k][c]);
+        a.final_t[pix] = T[k];
+        a.contributors[pix] = last_contributor[k];
     }
 }
 
-template <int CH, bool ABS>
-__global__ __launch_bounds__(kRenderThreads) void render_bwd_kernel(gs3d_render_bwd_args b) {
+template <int CH, bool ABS, int PIX>
+__global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_render_bwd_args b) {
+    constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
     __shared__ float2 s_xy[B];
     __shared__ float4 s_con[B];
+    __shared__ float s_cut[B];
     __shared__ int32_t s_id[B];
     __shared__ float s_feat[B * CH];
     __shared__ int s_max_last;
@@ -137,87 +208,114 @@ __global__ __launch_bounds__(kRenderThreads) void render_bwd_kernel(gs3d_render_
     const TileInfo t = tile_info(a);
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     const int Dg = D - (a.one_tail ? 1 : 0);
-    const float fx = (float)t.px, fy = (float)t.py;
     const int lane = lane_id();
-    float grad[CH], accum[CH], last_color[CH];
-    float T = 0.0f, T_final = 0.0f, bg_grad = 0.0f, last_alpha = 0.0f;
-    int last_contributor = 0;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        grad[c] = 0.0f;
-        accum[c] = 0.0f;
-        last_color[c] = 0.0f;
-    }
+    float fx[PIX], fy[PIX], T[PIX], T_final[PIX], bg_grad[PIX], last_alpha[PIX];
+    float grad[PIX][CH], accum[PIX][CH], last_color[PIX][CH];
+    int last_contributor[PIX];
+    bool inside[PIX];
     if (threadIdx.x == 0) s_max_last = 0;
-    if (t.inside) {
-        T_final = a.final_t[t.pix];
-        T = T_final;
-        last_contributor = a.contributors[t.pix];
-        const float* up = b.upstream + t.pix * D;
-        const float* bg = a.background ? a.background + t.view * a.background_view_stride : nullptr;
+    const float* bg = a.background ? a.background + t.view * a.background_view_stride : nullptr;
+    int my_max = 0;
 #pragma unroll
-        for (int c = 0; c < CH; ++c)
-            if (c < D) {
-                grad[c] = up[c];
-                bg_grad += ((bg && c < a.feat_channels) ? bg[c] : 0.0f) * grad[c];
-            }
+    for (int k = 0; k < PIX; ++k) {
+        int lx, ly;
+        pixel_of<PIX>(threadIdx.x, k, lx, ly);
+        const int x = t.x0 + lx, y = t.y0 + ly;
+        fx[k] = (float)x;
+        fy[k] = (float)y;
+        inside[k] = x < a.width && y < a.height;
+        T[k] = T_final[k] = bg_grad[k] = last_alpha[k] = 0.0f;
+        last_contributor[k] = 0;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            grad[k][c] = 0.0f;
+            accum[k][c] = 0.0f;
+            last_color[k][c] = 0.0f;
+        }
+        if (inside[k]) {
+            const int64_t pix = ((int64_t)t.view * a.height + y) * a.width + x;
+            T_final[k] = a.final_t[pix];
+            T[k] = T_final[k];
+            last_contributor[k] = a.contributors[pix];
+            const float* up = b.upstream + pix * D;
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+                if (c < D) {
+                    grad[k][c] = up[c];
+                    bg_grad[k] += ((bg && c < a.feat_channels) ? bg[c] : 0.0f) * grad[k][c];
+                }
+            my_max = max(my_max, last_contributor[k]);
+        }
     }
     __syncthreads();
-    if (last_contributor > 0) atomicMax(&s_max_last, last_contributor);
+    if (my_max > 0) atomicMax(&s_max_last, my_max);
     __syncthreads();
     const int max_last = min(s_max_last, t.last - t.first);
     for (int top = max_last; top > 0; top -= B) {
         __syncthreads();
-        const int p = top - 1 - (int)threadIdx.x;
-        if ((int)threadIdx.x < B && p >= 0) {
-            const int32_t g = a.ids[t.first + p];
-            s_id[threadIdx.x] = g;
-            stage_gaussian<CH>(a, t.view, g, threadIdx.x, s_xy, s_con, s_feat);
+        for (int e = threadIdx.x; e < B; e += NT) {
+            const int p = top - 1 - e;
+            if (p >= 0) {
+                const int32_t g = a.ids[t.first + p];
+                s_id[e] = g;
+                stage_gaussian<CH>(a, t.view, g, e, s_xy, s_con, s_cut, s_feat);
+            }
         }
         __syncthreads();
         const int cnt = min(B, top);
         for (int j = 0; j < cnt; ++j) {
             const int pos = top - 1 - j;
-            if (__ballot(t.inside && pos < last_contributor) == 0) continue;
+            bool any = false;
+#pragma unroll
+            for (int k = 0; k < PIX; ++k) any = any || (inside[k] && pos < last_contributor[k]);
+            if (__ballot(any) == 0) continue;
             const float2 xy = s_xy[j];
             const float4 con = s_con[j];
-            const float dx = xy.x - fx, dy = xy.y - fy;
-            const float power = blend_power(con.x, con.y, con.z, dx, dy);
-            float G = 0.0f, alpha = 0.0f;
-            bool acc = t.inside && pos < last_contributor && power <= 0.0f;
-            if (acc) {
-                G = blend_exp(power);
-                alpha = sel_min(0.99f, con.w * G);
-                acc = alpha >= 1.0f / 255.0f;
-            }
-            if (__ballot(acc) == 0) continue;
+            const float cut = s_cut[j];
+            const float* f = s_feat + j * CH;
             float gfeat[CH];
-            float dcx = 0.0f, dcy = 0.0f, gk0 = 0.0f, gk1 = 0.0f, gk2 = 0.0f, gk3 = 0.0f;
+            float dcx = 0.0f, dcy = 0.0f, gk0 = 0.0f, gk1 = 0.0f, gk2 = 0.0f, gk3 = 0.0f, ax = 0.0f, ay = 0.0f;
 #pragma unroll
             for (int c = 0; c < CH; ++c) gfeat[c] = 0.0f;
-            if (acc) {
-                T = T / (1.0f - alpha);
-                const float* f = s_feat + j * CH;
+            bool accepted = false;
+#pragma unroll
+            for (int k = 0; k < PIX; ++k) {
+                if (!(inside[k] && pos < last_contributor[k])) continue;
+                const float dx = xy.x - fx[k], dy = xy.y - fy[k];
+                const float power = blend_power(con.x, con.y, con.z, dx, dy);
+                if (!(power <= 0.0f) || !(power >= cut)) continue;
+                const float G = blend_exp(power);
+                const float alpha = sel_min(0.99f, con.w * G);
+                if (!(alpha >= 1.0f / 255.0f)) continue;
+                accepted = true;
+                T[k] = T[k] / (1.0f - alpha);
                 float grad_alpha = 0.0f;
 #pragma unroll
                 for (int c = 0; c < CH; ++c)
                     if (c < D) {
-                        accum[c] = last_alpha * last_color[c] + (1.0f - last_alpha) * accum[c];
-                        last_color[c] = f[c];
-                        grad_alpha += (f[c] - accum[c]) * grad[c];
-                        if (c < Dg) gfeat[c] = alpha * T * grad[c];
+                        accum[k][c] = last_alpha[k] * last_color[k][c] + (1.0f - last_alpha[k]) * accum[k][c];
+                        last_color[k][c] = f[c];
+                        grad_alpha += (f[c] - accum[k][c]) * grad[k][c];
+                        if (c < Dg) gfeat[c] += alpha * T[k] * grad[k][c];
                     }
-                grad_alpha = grad_alpha * T + (-T_final / (1.0f - alpha)) * bg_grad;
-                last_alpha = alpha;
+                grad_alpha = grad_alpha * T[k] + (-T_final[k] / (1.0f - alpha)) * bg_grad[k];
+                last_alpha[k] = alpha;
                 const float gv = con.w * grad_alpha;
                 const float gdx = G * dx, gdy = G * dy;
-                dcx = gv * (-gdx * con.x - gdy * con.y);
-                dcy = gv * (-gdy * con.z - gdx * con.y);
-                gk0 = -0.5f * gdx * dx * gv;
-                gk1 = -gdx * dy * gv;
-                gk2 = -0.5f * gdy * dy * gv;
-                gk3 = G * grad_alpha;
+                const float cx = gv * (-gdx * con.x - gdy * con.y);
+                const float cy = gv * (-gdy * con.z - gdx * con.y);
+                dcx += cx;
+                dcy += cy;
+                if (ABS) {
+                    ax += __builtin_fabsf(cx);
+                    ay += __builtin_fabsf(cy);
+                }
+                gk0 += -0.5f * gdx * dx * gv;
+                gk1 += -gdx * dy * gv;
+                gk2 += -0.5f * gdy * dy * gv;
+                gk3 += G * grad_alpha;
             }
+            if (__ballot(accepted) == 0) continue;
             // Wavefront sums (lane 63) and one atomic per entry.
             const float s_dcx = wave_sum_to_lane63(dcx);
             const float s_dcy = wave_sum_to_lane63(dcy);
@@ -227,8 +325,8 @@ __global__ __launch_bounds__(kRenderThreads) void render_bwd_kernel(gs3d_render_
             const float s_k3 = wave_sum_to_lane63(gk3);
             float s_ax = 0.0f, s_ay = 0.0f;
             if (ABS) {
-                s_ax = wave_sum_to_lane63(__builtin_fabsf(dcx));
-                s_ay = wave_sum_to_lane63(__builtin_fabsf(dcy));
+                s_ax = wave_sum_to_lane63(ax);
+                s_ay = wave_sum_to_lane63(ay);
             }
             float s_f[CH];
 #pragma unroll
@@ -268,16 +366,18 @@ __global__ __launch_bounds__(kRenderThreads) void render_bwd_kernel(gs3d_render_
 
 template <int CH>
 int launch_fwd(const gs3d_render_args& a, unsigned blocks, hipStream_t s) {
-    hipLaunchKernelGGL(render_fwd_kernel<CH>, dim3(blocks), dim3(kRenderThreads), 0, s, a);
+    constexpr int PIX = PixFor<CH, GS3D_FWD_PIX>::value;
+    hipLaunchKernelGGL((render_fwd_kernel<CH, PIX>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a);
     return launch_status("gs3d_render_fwd");
 }
 
 template <int CH>
 int launch_bwd(const gs3d_render_bwd_args& b, unsigned blocks, hipStream_t s) {
+    constexpr int PIX = PixFor<CH, GS3D_BWD_PIX>::value;
     if (b.abs_centers)
-        hipLaunchKernelGGL((render_bwd_kernel<CH, true>), dim3(blocks), dim3(kRenderThreads), 0, s, b);
+        hipLaunchKernelGGL((render_bwd_kernel<CH, true, PIX>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, b);
     else
-        hipLaunchKernelGGL((render_bwd_kernel<CH, false>), dim3(blocks), dim3(kRenderThreads), 0, s, b);
+        hipLaunchKernelGGL((render_bwd_kernel<CH, false, PIX>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, b);
     return launch_status("gs3d_render_bwd");
 }
 
