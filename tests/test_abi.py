@@ -1,0 +1,75 @@
+"""The C-ABI library loads without a GPU, exports every function declared in
+include/gs3d_hip.h, and the ctypes structs match the C layout."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from dsl_splat_amd.runtime import abi, native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gs3d_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gs3d_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = native.load()
+    declared = _declared_functions()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in gs3d_hip.h but not exported"
+        assert name in abi.FUNCTIONS, f"{name} has no ctypes signature"
+    assert lib.gs3d_abi_version() == abi.ABI_VERSION
+    # Size queries need no device.
+    assert native.query("gs3d_sort_scratch_bytes", 1 << 20) > 0
+    assert native.query("gs3d_scan_scratch_bytes", 0) >= 0
+    assert native.query("gs3d_depth_order_scratch_bytes", 1000) > 0
+
+
+def test_argument_errors_are_reported_without_launching():
+    lib = native.load()
+    # Invalid sizes are rejected on the host (no device needed).
+    assert lib.gs3d_camera_prepare(None, None, -1, 10, 10, 0, None, None, None, None, None) == abi.GS3D_ERR_ARGUMENT
+    assert lib.gs3d_sort_pairs_u64(None, None, 10, 70, None, 0, None) == abi.GS3D_ERR_ARGUMENT
+    assert lib.gs3d_sort_pairs_u32(None, None, 10, 33, None, 0, None) == abi.GS3D_ERR_ARGUMENT
+    assert lib.gs3d_scan_i32(None, -5, None, None, None, 0, None) == abi.GS3D_ERR_ARGUMENT
+    args = abi.RenderArgs()
+    args.width, args.height, args.views, args.n = 16, 16, 1, 1
+    args.feat_channels, args.one_tail = 70, 1
+    args.ranges = args.centers = args.conics = args.features = ctypes.c_void_p(256)
+    assert lib.gs3d_render_fwd(ctypes.byref(args), None) == abi.GS3D_ERR_UNSUPPORTED
+    # Zero-size work is a no-op.
+    assert lib.gs3d_tile_ranges_u32(None, 0, None, 0, None) == abi.GS3D_OK
+    with pytest.raises(native.NativeLibraryError, match="invalid argument"):
+        native.call("gs3d_scan_i32", None, -1, None, None, None, 0, None)
+
+
+def test_struct_layout_matches_header(tmp_path):
+    prog = ["#include <stdio.h>", "#include <stddef.h>", '#include "gs3d_hip.h"', "int main(void) {"]
+    for cname, cls in abi.STRUCTS.items():
+        prog.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            prog.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    prog.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(prog))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    c_layout = {}
+    for line in out:
+        if line:
+            struct, field, value = line.split()
+            c_layout[(struct, field)] = int(value)
+    for cname, cls in abi.STRUCTS.items():
+        assert c_layout[(cname, "size")] == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert c_layout[(cname, field)] == getattr(cls, field).offset, (cname, field)

@@ -1,0 +1,94 @@
+"""Host-side contract of the public entry points (no GPU needed): the same
+validation errors and exception types as the reference's gs3d.rasterize
+(gs3d/api.py:86-102), gsplat adapter (gs3d/gsplat.py:15-84), camera options
+(cameras.py:30-41), inputs (inputs.py:164-243) and statistics requests
+(statistics.py:72-128)."""
+
+import math
+
+import pytest
+import torch
+
+from dsl_splat_amd import gs3d
+from dsl_splat_amd.cameras import validate_camera_options
+from dsl_splat_amd.gs3d import gsplat
+from dsl_splat_amd.statistics import MaskedContributionCount, WeightedContributionSum, prepare_statistics
+
+
+def _cpu_scene(n=8):
+    return dict(
+        means=torch.zeros(n, 3), quats=torch.zeros(n, 4), scales=torch.ones(n, 3), opacities=torch.ones(n),
+        viewmats=torch.eye(4)[None], Ks=torch.eye(3)[None],
+    )
+
+
+def test_rasterize_option_errors():
+    s = _cpu_scene()
+    args = (s["means"], s["quats"], s["scales"], s["opacities"], s["viewmats"], s["Ks"], 32, 32)
+    with pytest.raises(ValueError, match="tile_mode"):
+        gs3d.rasterize(*args, features=torch.zeros(8, 3), tile_mode="box")
+    with pytest.raises(ValueError, match="width and height"):
+        gs3d.rasterize(*args[:6], 0, 32, features=torch.zeros(8, 3))
+    with pytest.raises(ValueError, match="near_plane"):
+        gs3d.rasterize(*args, features=torch.zeros(8, 3), near_plane=-1.0)
+    with pytest.raises(ValueError, match="radius_clip"):
+        gs3d.rasterize(*args, features=torch.zeros(8, 3), radius_clip=math.inf)
+    with pytest.raises(ValueError, match="exactly one of features or sh_coeffs"):
+        gs3d.rasterize(*args)
+    with pytest.raises(ValueError, match="exactly one of features or sh_coeffs"):
+        gs3d.rasterize(*args, features=torch.zeros(8, 3), sh_coeffs=torch.zeros(8, 16, 3))
+    with pytest.raises(ValueError, match="sh_degree requires sh_coeffs"):
+        gs3d.rasterize(*args, features=torch.zeros(8, 3), sh_degree=2)
+    with pytest.raises(ValueError, match="sh_degree must be an integer"):
+        gs3d.rasterize(*args, sh_coeffs=torch.zeros(8, 16, 3), sh_degree=4)
+    with pytest.raises(ValueError, match="sh_coeffs must have shape"):
+        gs3d.rasterize(*args, sh_coeffs=torch.zeros(8, 3))
+    # Host tensors are rejected before anything reaches a device.
+    with pytest.raises(ValueError, match="means must be a CUDA float32 tensor"):
+        gs3d.rasterize(*args, features=torch.zeros(8, 3))
+
+
+def test_camera_option_validation():
+    validate_camera_options(10, 10, 0.1, math.inf, 0.0)
+    for bad in ((0, 10, 0.1, 1.0, 0.0), (10, True, 0.1, 1.0, 0.0), (10, 10, 0.0, 1.0, 0.0),
+                (10, 10, 1.0, 1.0, 0.0), (10, 10, 0.1, math.nan, 0.0), (10, 10, 0.1, 1.0, -1.0)):
+        with pytest.raises(ValueError):
+            validate_camera_options(*bad)
+
+
+@pytest.mark.parametrize("kwargs,exc", [
+    (dict(sparse_grad=True), NotImplementedError), (dict(distributed=True), NotImplementedError),
+    (dict(segmented=True), NotImplementedError), (dict(with_ut=True), NotImplementedError),
+    (dict(covars=torch.zeros(1)), NotImplementedError), (dict(radial_coeffs=torch.zeros(1)), NotImplementedError),
+    (dict(extra_signals_sh_degree=1), NotImplementedError), (dict(rolling_shutter="ROLLING"), NotImplementedError),
+    (dict(camera_model="fisheye"), NotImplementedError), (dict(with_eval3d=True), NotImplementedError),
+    (dict(eps2d=0.1), NotImplementedError), (dict(tile_size=8), NotImplementedError),
+    (dict(render_mode="RGB+D"), NotImplementedError), (dict(rasterize_mode="antialiased"), NotImplementedError),
+    (dict(channel_chunk=0), ValueError), (dict(near_plane=0.0), ValueError), (dict(sh_degree=5), ValueError),
+])
+def test_gsplat_adapter_rejects_unsupported_options(kwargs, exc):
+    s = _cpu_scene()
+    with pytest.raises(exc):
+        gsplat.rasterization(s["means"], s["quats"], s["scales"], s["opacities"], torch.zeros(8, 3), s["viewmats"],
+                             s["Ks"], 32, 32, **kwargs)
+
+
+def test_statistics_request_validation():
+    H, W = 4, 5
+    mask = torch.zeros((H, W), dtype=torch.bool)
+    weights = torch.ones((H, W))
+    prepared, outputs = prepare_statistics(
+        [MaskedContributionCount("hits", mask), WeightedContributionSum("score", weights)],
+        batch_dims=(), batch_count=1, cameras=2, n=7, width=W, height=H, device=torch.device("cpu"))
+    assert outputs["hits"].shape == (2, 7) and outputs["hits"].dtype == torch.int32
+    assert outputs["score"].shape == (2, 7) and outputs["score"].dtype == torch.float32
+    assert len(prepared) == 2 and prepared[0].key == (0, 1)
+    with pytest.raises(ValueError, match="unique"):
+        prepare_statistics([MaskedContributionCount("a", mask), MaskedContributionCount("a", mask)], batch_dims=(),
+                           batch_count=1, cameras=1, n=1, width=W, height=H, device=torch.device("cpu"))
+    with pytest.raises(ValueError, match="must use"):
+        prepare_statistics([MaskedContributionCount("a", weights)], batch_dims=(), batch_count=1, cameras=1, n=1,
+                           width=W, height=H, device=torch.device("cpu"))
+    with pytest.raises(TypeError):
+        prepare_statistics(["bogus"], batch_dims=(), batch_count=1, cameras=1, n=1, width=W, height=H,
+                           device=torch.device("cpu"))
