@@ -11,9 +11,10 @@ over all four cameras plus the backward pass of loss = sum(image * W) with W
 the timed region.
 
 Prints one JSON line: the headline ms/iter (lower is better), forward and
-backward ms, the HBM roofline of the projection/scan/emission/sort/range
-stages (algorithmic bytes over their HIP-event time), per-stage timings, and
-a CPU baseline (the C++ oracle on the host cores over a bounded sample).
+backward ms, the HBM roofline of the dominant HBM-bound kernel (algorithmic
+bytes over its HIP-event time on the launch stream), per-stage timings and
+bandwidths, and a CPU baseline (the C++ oracle on the host cores over a
+bounded sample).
 """
 
 import argparse
@@ -24,6 +25,8 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
+KERNELS = {"project": "gs3d::project_fwd_kernel<3, true> (projection + SH3 + metadata, all views)",
+           "project_bwd": "gs3d::project_bwd_kernel<3> (projection + SH3 VJP, all views)"}
 
 
 def parse():
@@ -99,7 +102,7 @@ def stage_timings(scene, reps):
     sh = scene.sh_coeffs
     deg = scene.sh_degree
     views, n = scene.viewmats.shape[0], len(scene.means)
-    names = ("camera", "project", "order", "emit", "sort", "ranges", "render_fwd", "render_bwd", "project_bwd")
+    names = ("camera", "project", "order", "bin", "render_fwd", "render_bwd", "project_bwd")
     acc = {k: 0.0 for k in names}
     info = {}
     with torch.no_grad():
@@ -114,24 +117,19 @@ def stage_timings(scene, reps):
                                      sh=sh, sh_degree=deg or 0, camera_centers=centers if deg else None,
                                      metadata=True)
             ev[2].record()
-            order, offsets, total = binning.depth_order(st.depths, st.tile_counts)
+            order, offsets, totals = binning.order_rows(st.centers, st.radii, st.depths, scene.width,
+                                                        scene.height)
             ev[3].record()
-            count = int(total.item())
+            group_pairs, count = totals.cpu().tolist()
             ev[4].record()
-            tiles_k, ids = binning.emit_ordered(st.centers, st.radii, order, offsets, count, scene.width,
-                                                scene.height)
-            ev[5].record()
-            tiles = binning.tile_count(scene.width, scene.height, views)
-            binning.sort_by_tile(tiles_k, ids, count, tiles)
-            ev[6].record()
-            ev[7].record()
-            ranges = binning.ranges_of(tiles_k, count, tiles)
+            ranges, ids = binning.bin_rows(st.centers, st.radii, order, offsets, group_pairs, count, scene.width,
+                                           scene.height)
             ev[8].record()
             feats = st.colors if sh is not None else scene.features
-            out = grender.render_views(ranges, ids[:count], st.centers, st.conics, feats, scene.width, scene.height)
+            out = grender.render_views(ranges, ids, st.centers, st.conics, feats, scene.width, scene.height)
             ev[9].record()
             up = scene.loss_weights
-            record, gf, _ = grender.backward_views(ranges, ids[:count], st.centers, st.conics, feats,
+            record, gf, _ = grender.backward_views(ranges, ids, st.centers, st.conics, feats,
                                                    out.transmittance, out.contributors, up, scene.width,
                                                    scene.height, absgrad=scene.absgrad)
             ev[10].record()
@@ -143,25 +141,37 @@ def stage_timings(scene, reps):
             ev[11].record()
             torch.cuda.synchronize()
             if rep == 0:
-                info = dict(pairs=count, passes=math.ceil(int(tiles).bit_length() / 8), tiles=tiles,
-                            rows=views * n, visible=int((st.radii > 0).sum()),
+                tiles = binning.tile_count(scene.width, scene.height, views)
+                groups = views * (((scene.width + 15) // 16 + 7) // 8) * (((scene.height + 15) // 16 + 7) // 8)
+                info = dict(pairs=count, group_pairs=group_pairs, groups=groups, tiles=tiles,
+                            group_passes=math.ceil(int(groups - 1).bit_length() / 8), rows=views * n,
+                            visible=int((st.radii > 0).sum()),
                             mean_contributors=float(out.contributors.float().mean()))
                 continue  # warm-up repetition
-            spans = {"camera": (0, 1), "project": (1, 2), "order": (2, 3), "emit": (4, 5), "sort": (5, 6),
-                     "ranges": (7, 8), "render_fwd": (8, 9), "render_bwd": (9, 10), "project_bwd": (10, 11)}
+            spans = {"camera": (0, 1), "project": (1, 2), "order": (2, 3), "bin": (4, 8), "render_fwd": (8, 9),
+                     "render_bwd": (9, 10), "project_bwd": (10, 11)}
             for k, (a, b) in spans.items():
                 acc[k] += ev[a].elapsed_time(ev[b]) / reps
-    # Algorithmic bytes per launch ("Roofline accounting").
-    M, P, T, R = info["pairs"], info["passes"], info["tiles"], info["rows"]
+    # Algorithmic bytes of every stage: what its kernels must read and write
+    # once each.
+    M, S, T, R = info["pairs"], info["group_pairs"], info["tiles"], info["rows"]
     K = 0 if sh is None else sh.shape[-2]
-    sh_bytes = 0 if sh is None else (n if sh.ndim == 3 else views * n) * K * 3 * 4
+    sh_in = 0 if sh is None else (n if sh.ndim == 3 else views * n) * K * 3 * 4
     by = {
-        "project": n * (12 + 16 + 12 + 4) + sh_bytes + views * n * (8 + 16 + 4 + 4 + 4 + 8 + 4 + 12 +
-                                                                    (12 if sh is not None else 0)),
-        "order": R * (8 + 8 + 4 * 16),
-        "emit": R * (4 + 4 + 4 + 8) + M * 8,
-        "sort": 16 * P * M,
-        "ranges": 4 * M + 8 * T,
+        # params 44 B/G (+ SH once for all views) in; per view centers 8, conics+opacity 16, radii 4,
+        # tiles 4, depth 4, means2d 8, meta opacity 4, meta conic 12 (+ colour 12) out
+        "project": n * 44 + sh_in + views * n * (60 + (12 if sh is not None else 0)),
+        # keys and records (depth 4 + centre 8 + radius 4 in, key 4 + record 8 out), 4 radix passes
+        # over (key, record) (24 per pass), group counts (record 8 in, count 4 out), inclusive scan
+        # (4 in, 4 out)
+        "order": R * (28 + 4 * 24 + 12 + 8),
+        # items: records and offsets in (12 B/row), items out (8 B/item); group sort (16 B/item/pass);
+        # group ranges, count and write passes read items (3 x 8 B); ids out (4 B/pair); tile
+        # totals/starts/ranges (16 B/tile)
+        "bin": R * 12 + S * (8 + 16 * info["group_passes"] + 24) + M * 4 + T * 16,
+        # params 44 + SH 4K*3 in, per view radii 4 + centre/conic grads 24 (+ colour grads 12) in;
+        # grads 44 + SH out
+        "project_bwd": n * 88 + 2 * sh_in + views * n * (28 + (12 if sh is not None else 0)),
     }
     return acc, by, info
 
@@ -254,14 +264,17 @@ def main():
     ms = (t1 - t0) * 1000.0 / args.steps
     log(f"[bench] {ms:.3f} ms/iter; stage timings")
     stages, by, info = stage_timings(scene, args.stage_reps)
-    s13 = ("project", "order", "emit", "sort", "ranges")
+    s13 = ("project", "order", "bin")
     t13 = sum(stages[k] for k in s13)
     b13 = sum(by[k] for k in s13)
-    achieved = b13 / (t13 * 1e-3) / 1e9
     per_stage = {k: dict(ms=round(v, 4)) for k, v in stages.items()}
-    for k in s13:
+    for k in by:
         per_stage[k]["gbps"] = round(by[k] / (stages[k] * 1e-3) / 1e9, 1)
+        per_stage[k]["frac"] = round(by[k] / (stages[k] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
         per_stage[k]["bytes"] = by[k]
+    # The dominant HBM-bound kernel: the longer of the two single-kernel stages.
+    dom = max(("project", "project_bwd"), key=lambda k: stages[k])
+    achieved = by[dom] / (stages[dom] * 1e-3) / 1e9
     cpu = None
     if args.cpu_baseline == "on":
         log("[bench] CPU baseline (oracle)")
@@ -284,22 +297,24 @@ def main():
             "workload": f"{args.workload}: N={len(scene.means)}, {views} cameras, {scene.width}x{scene.height}, "
                         f"SH degree {scene.sh_degree}, fwd+bwd of sum(image*W)",
             "gaussians": len(scene.means), "cameras": views, "width": scene.width, "height": scene.height,
-            "sh_degree": scene.sh_degree, "pairs": info["pairs"], "radix_passes": info["passes"],
+            "sh_degree": scene.sh_degree, "pairs": info["pairs"], "group_pairs": info["group_pairs"],
+            "visible_rows": info["visible"],
         },
         "fwd_ms": round(fwd_ms / args.steps, 3),
         "bwd_ms": round(bwd_ms / args.steps, 3),
         "roofline": {
             "bound": "hbm",
-            "kernel": "stages 1-3: projection+SH+metadata, depth ordering+scan, pair emission, tile radix sort, "
-                      "tile ranges",
+            "kernel": KERNELS[dom],
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": None,
-            "ms": round(t13, 4),
-            "bytes": b13,
+            "ms": round(stages[dom], 4),
+            "bytes": by[dom],
         },
+        "stages_1_3": {"ms": round(t13, 4), "bytes": b13, "gbps": round(b13 / (t13 * 1e-3) / 1e9, 1),
+                       "frac": round(b13 / (t13 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
         "stages": per_stage,
         "cpu_baseline": cpu,
     }

@@ -143,9 +143,17 @@ GS3D_DEV uint64_t make_key(uint32_t tile, float depth) {
     return ((uint64_t)tile << 32) | (uint64_t)__float_as_uint(depth);
 }
 
-__global__ void fill_u32_kernel(uint32_t* p, int count, uint32_t value) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < count) p[i] = value;
+__global__ void fill_u32_kernel(uint32_t* p, int64_t count, uint32_t value) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = value;
+}
+
+// Fill kernel launch (no memset nodes, so the sequence stays capturable).
+inline void fill_u32(uint32_t* p, int64_t count, uint32_t value, hipStream_t s) {
+    if (count <= 0) return;
+    const int64_t blocks = (count + 255) / 256;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, p, count,
+                       value);
 }
 
 __global__ __launch_bounds__(kEmitThreads) void emit_small_kernel(gs3d_emit_args a, uint32_t* __restrict__ queue_count,
@@ -250,13 +258,13 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_kernel(const K* _
     }
 }
 
-template <class K>
+template <class K, class V>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
-    const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in, K* __restrict__ keys_out,
-    int32_t* __restrict__ vals_out, int64_t count, int shift, uint32_t mask, int bits,
+    const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
+    V* __restrict__ vals_out, int64_t count, int shift, uint32_t mask, int bits,
     const int32_t* __restrict__ scanned, int64_t tiles) {
     __shared__ K s_keys[kSortTile];
-    __shared__ int32_t s_vals[kSortTile];
+    __shared__ V s_vals[kSortTile];
     __shared__ uint32_t s_wcnt[kSortThreads / 64][kRadix];
     __shared__ int32_t s_gbase[kRadix];
     __shared__ uint32_t s_scan_wave[kSortThreads / 64];
@@ -265,7 +273,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const int64_t tile_base = (int64_t)blockIdx.x * kSortTile;
     const int64_t valid_count = min((int64_t)kSortTile, count - tile_base);
     K key[kSortItems];
-    int32_t val[kSortItems];
+    V val[kSortItems];
     uint32_t rank[kSortItems];
     const int64_t base = tile_base + wave * (kSortTile / 4) + lane;
 #pragma unroll
@@ -273,10 +281,10 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
         const int64_t idx = base + k * 64;
         if (idx < count) {
             key[k] = keys_in[idx];
-            val[k] = vals_in[idx];
+            val[k] = vals_in ? vals_in[idx] : V(0);
         } else {
             key[k] = K(0);
-            val[k] = 0;
+            val[k] = V(0);
         }
     }
     __syncthreads();
@@ -341,7 +349,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
             const K kk = s_keys[p];
             const int64_t dst = (int64_t)s_gbase[digit_of(kk, shift, mask)] + p;
             keys_out[dst] = kk;
-            vals_out[dst] = s_vals[p];
+            if (vals_out) vals_out[dst] = s_vals[p];
         }
     }
 }
@@ -370,16 +378,17 @@ inline size_t sort_scratch_bytes(int64_t count, SortScratch* out, void* base) {
 }
 
 // Sort keys[0:count)/values[0:count) on bits [0, end_bit) using
-// keys[count:2count)/values[count:2count) as the ping-pong buffer.
-template <class K>
-int run_sort(K* keys, int32_t* values, int64_t count, int end_bit, void* scratch, hipStream_t s) {
+// keys[count:2count)/values[count:2count) as the ping-pong buffer; values
+// may be null (keys only).
+template <class K, class V = int32_t>
+int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipStream_t s) {
     SortScratch sc;
     sort_scratch_bytes(count, &sc, scratch);
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
     K* kin = keys;
-    int32_t* vin = values;
+    V* vin = values;
     K* kout = keys + count;
-    int32_t* vout = values + count;
+    V* vout = values ? values + count : nullptr;
     for (int shift = 0; shift < end_bit; shift += 8) {
         const int bits = end_bit - shift < 8 ? end_bit - shift : 8;
         const uint32_t mask = (1u << bits) - 1u;
@@ -387,18 +396,22 @@ int run_sort(K* keys, int32_t* values, int64_t count, int end_bit, void* scratch
                            shift, mask, sc.counts, tiles);
         const int status = run_scan<uint32_t, false>(sc.counts, tiles * kRadix, sc.scanned, nullptr, sc.scan_scratch, s);
         if (status != GS3D_OK) return status;
-        hipLaunchKernelGGL((sort_scatter_kernel<K>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin, vin, kout,
+        hipLaunchKernelGGL((sort_scatter_kernel<K, V>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin, vin, kout,
                            vout, count, shift, mask, bits, sc.scanned, tiles);
         K* tk = kin;
         kin = kout;
         kout = tk;
-        int32_t* tv = vin;
+        V* tv = vin;
         vin = vout;
         vout = tv;
     }
     if (kin != keys) {
-        hipMemcpyAsync(keys, kin, (size_t)count * sizeof(K), hipMemcpyDeviceToDevice, s);
-        hipMemcpyAsync(values, vin, (size_t)count * sizeof(int32_t), hipMemcpyDeviceToDevice, s);
+        if (hipMemcpyAsync(keys, kin, (size_t)count * sizeof(K), hipMemcpyDeviceToDevice, s) != hipSuccess ||
+            (values && hipMemcpyAsync(values, vin, (size_t)count * sizeof(V), hipMemcpyDeviceToDevice, s) != hipSuccess))
+        {
+            set_error("radix sort: copy of the sorted half failed");
+            return GS3D_ERR_LAUNCH;
+        }
     }
     return launch_status("radix sort");
 }
@@ -407,17 +420,17 @@ int run_sort(K* keys, int32_t* values, int64_t count, int end_bit, void* scratch
 // Per-tile ranges (primitives/tiling.py:39-54).  Tile ids at or beyond
 // tile_count (0xFFFFFFFF included) are ignored.
 // ---------------------------------------------------------------------------
-template <class K, int SHIFT>
-__global__ void tile_ranges_kernel(const K* __restrict__ keys, int64_t count, int32_t* __restrict__ ranges,
-                                   int64_t tile_count) {
+template <class K>
+__global__ void tile_ranges_kernel(const K* __restrict__ keys, int64_t count, int shift, uint32_t mask,
+                                   int32_t* __restrict__ ranges, int64_t tile_count) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
-    const int64_t cur = (int64_t)(uint32_t)(keys[i] >> SHIFT);
+    const int64_t cur = (int64_t)((uint32_t)(keys[i] >> shift) & mask);
     const bool cur_ok = cur < tile_count;
     if (i == 0) {
         if (cur_ok) ranges[2 * cur] = 0;
     } else {
-        const int64_t prev = (int64_t)(uint32_t)(keys[i - 1] >> SHIFT);
+        const int64_t prev = (int64_t)((uint32_t)(keys[i - 1] >> shift) & mask);
         if (cur != prev) {
             if (prev < tile_count) ranges[2 * prev + 1] = (int32_t)i;
             if (cur_ok) ranges[2 * cur] = (int32_t)i;
@@ -427,66 +440,208 @@ __global__ void tile_ranges_kernel(const K* __restrict__ keys, int64_t count, in
 }
 
 // ---------------------------------------------------------------------------
-// Depth-ordered binning.  Rows (view, Gaussian) are stably sorted by the
-// bits of their depth; their tile counts are scanned in that order; pairs
-// are emitted in that order with 32-bit tile keys; a stable sort on the tile
-// id then leaves every tile's list in (depth bits, Gaussian id) order --
-// the order of the stable sort of (tile << 32 | depth bits) keys over
-// Gaussian-ordered pairs that the reference performs.
+// Grouped binning.  Every tile's list holds, in (depth bits, Gaussian index)
+// order, the Gaussians whose tile rectangle covers it; lists are laid out in
+// global tile order.  That is the order of a stable sort of the reference's
+// (tile << 32 | depth bits) keys over Gaussian-ordered pairs
+// (splatting/binning.py:16-37, primitives/tiling.py:67-100), produced here
+// without sorting the pairs:
+//   * rows (view, Gaussian) are stably sorted by depth bits;
+//   * each row yields one item per 8x8-tile group its rectangle touches
+//     (group id, the rectangle clipped to the group, the Gaussian index),
+//     emitted in depth order and stably sorted by group (a short radix sort:
+//     groups number in the hundreds);
+//   * a group's item list is cut into 512-item chunks, one per wavefront.
+//     Lane t of the wavefront owns tile t of the group: for every tile that
+//     some item of a 64-item step touches, a ballot gives each item its rank
+//     among the step's items on that tile, and lane t keeps the running
+//     count.  A counting pass stores each chunk's per-tile counts, one
+//     exclusive scan turns them into per-(tile, chunk) offsets and tile
+//     totals, a scan of the totals gives tile starts, and the writing pass
+//     stores every Gaussian index straight to its final position.
 // ---------------------------------------------------------------------------
-__global__ void depth_keys_kernel(const float* __restrict__ depths, int64_t rows, uint32_t* __restrict__ keys,
-                                  int32_t* __restrict__ order) {
+constexpr int kGroupShift = 3;  // groups of 8x8 tiles: one wavefront lane per tile
+constexpr int kGroupBits = 20;  // group id field (low bits) of an item
+constexpr uint32_t kGroupMask = (1u << kGroupBits) - 1u;
+constexpr int kChunkSteps = 8;  // items per lane of a chunk
+constexpr int kChunk = 64 * kChunkSteps;  // items ranked by one wavefront
+constexpr int kBinThreads = 256;
+constexpr int kBinWaves = kBinThreads / 64;
+
+struct GridDims {
+    int gx, gy, tpv;   // tiles per row, per column, per view
+    int sgx, sgy, gpv; // groups per row, per column, per view
+};
+
+inline GridDims grid_dims(int width, int height) {
+    GridDims d;
+    d.gx = (width + 15) / 16;
+    d.gy = (height + 15) / 16;
+    d.tpv = d.gx * d.gy;
+    d.sgx = (d.gx + 7) >> kGroupShift;
+    d.sgy = (d.gy + 7) >> kGroupShift;
+    d.gpv = d.sgx * d.sgy;
+    return d;
+}
+
+GS3D_DEV uint64_t pack_rect(int x0, int y0, int x1, int y1) {
+    return (uint64_t)(uint32_t)x0 | ((uint64_t)(uint32_t)y0 << 16) | ((uint64_t)(uint32_t)x1 << 32) |
+           ((uint64_t)(uint32_t)y1 << 48);
+}
+
+// Bit (ly*8 + lx) set for every tile of the clipped rectangle
+// [lx0, lx1] x [ly0, ly1] (inclusive, 3 bits each, packed lx0 | lx1 << 3 |
+// ly0 << 6 | ly1 << 9).
+GS3D_DEV uint64_t group_tile_mask(uint32_t local) {
+    const int lx0 = local & 7, lx1 = (local >> 3) & 7, ly0 = (local >> 6) & 7, ly1 = (local >> 9) & 7;
+    const uint64_t row = (2ull << lx1) - (1ull << lx0);
+    const uint64_t rows = (~0ull >> (8 * (7 - ly1))) & (~0ull << (8 * ly0));
+    return (row * 0x0101010101010101ull) & rows;
+}
+
+GS3D_DEV uint64_t wave_or64(uint64_t v) {
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        lo |= (uint32_t)__shfl_xor((int)lo, d, 64);
+        hi |= (uint32_t)__shfl_xor((int)hi, d, 64);
+    }
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)hi) << 32) |
+           (uint32_t)__builtin_amdgcn_readfirstlane((int)lo);
+}
+
+// Ordered row records: row index in the low 32 bits; for tile grids of at
+// most 256 x 256 the high 32 bits carry the row's tile rectangle
+// (x0 | y0 << 8 | (x1 - 1) << 16 | (y1 - 1) << 24, kEmptyRect for culled
+// rows) so that nothing downstream gathers per-row data in depth order.
+// Larger grids leave the high half zero and recompute the rectangle from the
+// row's centre and radius.
+constexpr uint32_t kEmptyRect = 0x000000FFu;  // x0 = 255 > x1 - 1 = 0
+
+struct TileRect {
+    int x0, y0, x1, y1;  // exclusive ends; empty when x1 <= x0
+};
+
+GS3D_DEV TileRect row_rect(const float* __restrict__ centers, const int32_t* __restrict__ radii, int64_t row, int gx,
+                           int gy) {
+    TileRect r{0, 0, 0, 0};
+    const int radius = radii[row];
+    if (radius > 0) {
+        const float2 c = reinterpret_cast<const float2*>(centers)[row];
+        const int4 b = tile_rect(c.x, c.y, radius, gx, gy);
+        if (b.z > b.x && b.w > b.y) r = TileRect{b.x, b.y, b.z, b.w};
+    }
+    return r;
+}
+
+template <bool PACKED>
+GS3D_DEV TileRect record_rect(uint64_t record, const float* __restrict__ centers, const int32_t* __restrict__ radii,
+                              int gx, int gy) {
+    if constexpr (PACKED) {
+        const uint32_t p = (uint32_t)(record >> 32);
+        TileRect r{(int)(p & 255u), (int)((p >> 8) & 255u), (int)((p >> 16) & 255u) + 1, (int)(p >> 24) + 1};
+        if (r.x1 <= r.x0) r = TileRect{0, 0, 0, 0};
+        return r;
+    } else {
+        return row_rect(centers, radii, (int64_t)(uint32_t)record, gx, gy);
+    }
+}
+
+GS3D_DEV int groups_of(const TileRect& r) {
+    if (r.x1 <= r.x0) return 0;
+    return (((r.x1 - 1) >> kGroupShift) - (r.x0 >> kGroupShift) + 1) *
+           (((r.y1 - 1) >> kGroupShift) - (r.y0 >> kGroupShift) + 1);
+}
+
+// Row order: depth-bit keys and records (coalesced reads of depth, centre
+// and radius).
+template <bool PACKED>
+__global__ void row_records_kernel(const float* __restrict__ depths, const float* __restrict__ centers,
+                                   const int32_t* __restrict__ radii, int64_t rows, int gx, int gy,
+                                   uint32_t* __restrict__ keys, uint64_t* __restrict__ records) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
     keys[i] = __float_as_uint(depths[i]);
-    order[i] = (int32_t)i;
+    uint64_t rec = (uint64_t)(uint32_t)i;
+    if constexpr (PACKED) {
+        const TileRect r = row_rect(centers, radii, i, gx, gy);
+        const uint32_t p = r.x1 > r.x0 ? (uint32_t)r.x0 | ((uint32_t)r.y0 << 8) | ((uint32_t)(r.x1 - 1) << 16) |
+                                             ((uint32_t)(r.y1 - 1) << 24)
+                                       : kEmptyRect;
+        rec |= (uint64_t)p << 32;
+    }
+    records[i] = rec;
 }
 
-__global__ void gather_counts_kernel(const int32_t* __restrict__ tiles, const int32_t* __restrict__ order,
-                                     int64_t rows, int32_t* __restrict__ out) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < rows) out[i] = tiles[order[i]];
+// Group count of every row in depth order; the block's tile pair count goes
+// to block_pairs[blockIdx.x].
+template <bool PACKED>
+__global__ __launch_bounds__(kBinThreads) void order_counts_kernel(const uint64_t* __restrict__ records, int64_t rows,
+                                                                   const float* __restrict__ centers,
+                                                                   const int32_t* __restrict__ radii, int gx, int gy,
+                                                                   int32_t* __restrict__ group_counts,
+                                                                   int64_t* __restrict__ block_pairs) {
+    __shared__ int64_t s_wave[kBinWaves];
+    const int64_t i = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
+    int64_t area = 0;
+    if (i < rows) {
+        const TileRect r = record_rect<PACKED>(records[i], centers, radii, gx, gy);
+        if (r.x1 > r.x0) area = (int64_t)(r.x1 - r.x0) * (r.y1 - r.y0);
+        group_counts[i] = groups_of(r);
+    }
+    int64_t total;
+    block_exclusive_scan<kBinThreads>(area, s_wave, total);
+    if (threadIdx.x == 0) block_pairs[blockIdx.x] = total;
 }
 
-constexpr int kOrderedThreads = 256;
+// *out = sum of values[0, count) (one block).
+__global__ __launch_bounds__(1024) void sum_i64_kernel(const int64_t* __restrict__ values, int64_t count,
+                                                       int64_t* __restrict__ out) {
+    __shared__ int64_t s_wave[1024 / 64];
+    int64_t v = 0;
+    for (int64_t i = threadIdx.x; i < count; i += 1024) v += values[i];
+    int64_t total;
+    block_exclusive_scan<1024>(v, s_wave, total);
+    if (threadIdx.x == 0) *out = total;
+}
 
-// One block per 256 consecutive ordered rows; the block's pairs form one
-// contiguous output range that its threads fill with stride 256, locating
-// each pair's row by binary search over the rows' inclusive ends in LDS.
-__global__ __launch_bounds__(kOrderedThreads) void emit_ordered_kernel(gs3d_emit_ordered_args a) {
-    __shared__ int32_t s_end[kOrderedThreads];
-    __shared__ int32_t s_x0[kOrderedThreads], s_y0[kOrderedThreads], s_w[kOrderedThreads];
-    __shared__ uint32_t s_tbase[kOrderedThreads];
-    __shared__ int32_t s_id[kOrderedThreads];
-    const int64_t rows = (int64_t)a.n * a.views;
-    const int64_t r0 = (int64_t)blockIdx.x * kOrderedThreads;
-    const int cnt = (int)min((int64_t)kOrderedThreads, rows - r0);
-    const int gx = (a.width + 15) / 16, gy = (a.height + 15) / 16;
+// One block per 256 ordered rows; the block's items form one contiguous
+// output range, filled with stride 256 (coalesced), each item locating its
+// row by binary search over the rows' inclusive ends in LDS.
+// Item = Gaussian index << 32 | clipped rectangle << 20 | group id.
+template <bool PACKED>
+__global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t* __restrict__ records,
+                                                                 const int32_t* __restrict__ offsets, int64_t rows,
+                                                                 const float* __restrict__ centers,
+                                                                 const int32_t* __restrict__ radii, int n, GridDims d,
+                                                                 int64_t limit, uint64_t* __restrict__ items) {
+    __shared__ int32_t s_end[kBinThreads];
+    __shared__ int32_t s_x0[kBinThreads], s_y0[kBinThreads], s_x1[kBinThreads], s_y1[kBinThreads];
+    __shared__ int32_t s_gw[kBinThreads];
+    __shared__ uint32_t s_gbase[kBinThreads];
+    __shared__ uint32_t s_id[kBinThreads];
+    const int64_t r0 = (int64_t)blockIdx.x * kBinThreads;
+    const int cnt = (int)min((int64_t)kBinThreads, rows - r0);
     const int t = threadIdx.x;
     if (t < cnt) {
         const int64_t i = r0 + t;
-        const int64_t row = a.order[i];
-        s_end[t] = a.offsets[i];
-        const int radius = a.radii[row];
-        int x0 = 0, y0 = 0, w = 1;
-        if (radius > 0) {
-            const float2 c = reinterpret_cast<const float2*>(a.centers)[row];
-            const int4 rect = tile_rect(c.x, c.y, radius, gx, gy);
-            x0 = rect.x;
-            y0 = rect.y;
-            w = max(rect.z - rect.x, 1);
-        }
-        const int64_t view = row / a.n;
-        s_x0[t] = x0;
-        s_y0[t] = y0;
-        s_w[t] = w;
-        s_tbase[t] = (uint32_t)(view * gx * gy);
-        s_id[t] = (int32_t)(row - view * a.n);
+        const uint64_t rec = records[i];
+        const int32_t row = (int32_t)(uint32_t)rec;
+        const TileRect r = record_rect<PACKED>(rec, centers, radii, d.gx, d.gy);
+        s_end[t] = offsets[i];
+        s_x0[t] = r.x0;
+        s_y0[t] = r.y0;
+        s_x1[t] = r.x1;
+        s_y1[t] = r.y1;
+        s_gw[t] = r.x1 > r.x0 ? ((r.x1 - 1) >> kGroupShift) - (r.x0 >> kGroupShift) + 1 : 1;
+        const int view = row / n;
+        s_gbase[t] = (uint32_t)(view * d.gpv);
+        s_id[t] = (uint32_t)(row - view * n);
     }
     __syncthreads();
-    const int64_t S = r0 > 0 ? a.offsets[r0 - 1] : 0;
-    const int64_t E = s_end[cnt - 1];
-    for (int64_t p = S + t; p < E; p += kOrderedThreads) {
+    const int64_t S = r0 > 0 ? offsets[r0 - 1] : 0;
+    const int64_t E = min((int64_t)s_end[cnt - 1], limit);
+    for (int64_t p = S + t; p < E; p += kBinThreads) {
         int lo = 0, hi = cnt - 1;  // first j with s_end[j] > p
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
@@ -497,11 +652,175 @@ __global__ __launch_bounds__(kOrderedThreads) void emit_ordered_kernel(gs3d_emit
         }
         const int64_t start = lo > 0 ? s_end[lo - 1] : S;
         const int local = (int)(p - start);
-        const int w = s_w[lo];
-        const int dy = local / w, dx = local - dy * w;
-        a.tile_keys[p] = s_tbase[lo] + (uint32_t)((s_y0[lo] + dy) * gx + s_x0[lo] + dx);
-        a.values[p] = s_id[lo];
+        const int gw = s_gw[lo];
+        const int oy = local / gw, ox = local - oy * gw;
+        const int X = (s_x0[lo] >> kGroupShift) + ox, Y = (s_y0[lo] >> kGroupShift) + oy;
+        const int lx0 = max(s_x0[lo] - (X << kGroupShift), 0), lx1 = min(s_x1[lo] - 1 - (X << kGroupShift), 7);
+        const int ly0 = max(s_y0[lo] - (Y << kGroupShift), 0), ly1 = min(s_y1[lo] - 1 - (Y << kGroupShift), 7);
+        const uint32_t gid = s_gbase[lo] + (uint32_t)(Y * d.sgx + X);
+        const uint32_t clip = (uint32_t)(lx0 | (lx1 << 3) | (ly0 << 6) | (ly1 << 9));
+        items[p] = ((uint64_t)s_id[lo] << 32) | ((uint64_t)clip << kGroupBits) | gid;
     }
+}
+
+// chunk_base[g] = exclusive scan over groups of ceil(len_g / kChunk);
+// chunk_base[groups] = number of chunks.
+__global__ __launch_bounds__(1024) void chunk_base_kernel(const int32_t* __restrict__ granges, int groups,
+                                                          int32_t* __restrict__ chunk_base) {
+    __shared__ int32_t s_wave[1024 / 64];
+    int32_t carry = 0;
+    for (int base = 0; base < groups; base += 1024) {
+        const int g = base + threadIdx.x;
+        const int32_t q = g < groups ? (granges[2 * g + 1] - granges[2 * g] + kChunk - 1) / kChunk : 0;
+        int32_t total;
+        const int32_t ex = block_exclusive_scan<1024>(q, s_wave, total);
+        if (g < groups) chunk_base[g] = carry + ex;
+        carry += total;
+    }
+    if (threadIdx.x == 0) chunk_base[groups] = carry;
+}
+
+// chunk_group[u] = the group g with chunk_base[g] <= u < chunk_base[g + 1].
+__global__ void chunk_group_kernel(const int32_t* __restrict__ chunk_base, int groups, int64_t max_chunks,
+                                   int32_t* __restrict__ chunk_group) {
+    const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= max_chunks || u >= chunk_base[groups]) return;
+    int lo = 0, hi = groups - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (chunk_base[mid] <= u)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    chunk_group[u] = lo;
+}
+
+// Workgroups are dispatched to the 8 XCDs in turn; giving every XCD one
+// contiguous range of logical blocks keeps consecutive chunks of a group --
+// and so the consecutive segments of its tiles' lists -- in one L2.
+GS3D_DEV int64_t xcd_contiguous(int64_t b, int64_t nblocks) {
+    constexpr int64_t kXcds = 8;
+    const int64_t per = nblocks / kXcds, rem = nblocks % kXcds;
+    const int64_t xcd = b % kXcds, k = b / kXcds;
+    return xcd * per + min(xcd, rem) + k;
+}
+
+// One wavefront per chunk of kChunk items (kChunkSteps per lane, masks and
+// ids held in registers).  Counts of group g are laid out [g][tile][chunk]
+// starting at 64*chunk_base[g], so one exclusive scan over the whole array
+// yields every (tile, chunk) offset within the tile's list.  The wavefront
+// walks the tiles its items touch and, per tile, its items in order: one
+// ballot per 64 items ranks them, so a tile's run of the chunk is written by
+// consecutive stores of one wavefront.
+// WRITE = false: counts[(g, t, s)] = items of chunk s touching tile t.
+// WRITE = true: every item's Gaussian index goes to
+//   tile_start[t] + (scanned[(g,t,s)] - scanned[(g,t,0)]) + rank.
+template <bool WRITE>
+__global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
+    const uint64_t* __restrict__ items, const int32_t* __restrict__ granges, const int32_t* __restrict__ chunk_base,
+    const int32_t* __restrict__ chunk_group, int groups, int64_t max_chunks, GridDims d,
+    uint32_t* __restrict__ counts, const int32_t* __restrict__ scanned, const int32_t* __restrict__ tile_start,
+    int32_t* __restrict__ ids, int64_t id_limit) {
+    const int lane = lane_id();
+    const int64_t block = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int64_t u = block * kBinWaves + (threadIdx.x >> 6);
+    if (u >= max_chunks || u >= chunk_base[groups]) return;
+    const int g = chunk_group[u];
+    const int32_t cb = chunk_base[g];
+    const int32_t q = chunk_base[g + 1] - cb;
+    const int32_t s = (int32_t)(u - cb);
+    const int64_t begin = (int64_t)granges[2 * g] + (int64_t)s * kChunk;
+    const int64_t end = min(begin + kChunk, (int64_t)granges[2 * g + 1]);
+    const int64_t slot = (int64_t)cb * 64 + (int64_t)lane * q;  // entry (g, lane, 0)
+    uint64_t mask[kChunkSteps];
+    int32_t id[kChunkSteps];
+    uint64_t any = 0;
+#pragma unroll
+    for (int k = 0; k < kChunkSteps; ++k) {
+        const int64_t i = begin + k * 64 + lane;
+        mask[k] = 0;
+        id[k] = 0;
+        if (i < end) {
+            const uint64_t item = items[i];
+            mask[k] = group_tile_mask((uint32_t)(item >> kGroupBits) & 0xFFFu);
+            id[k] = (int32_t)(item >> 32);
+        }
+        any |= mask[k];
+    }
+    uint32_t init = 0;
+    if constexpr (WRITE) {
+        const int view = g / d.gpv, rem = g - view * d.gpv;
+        const int Y = rem / d.sgx, X = rem - Y * d.sgx;
+        const int ty = (Y << kGroupShift) + (lane >> 3), tx = (X << kGroupShift) + (lane & 7);
+        if (ty < d.gy && tx < d.gx)
+            init = (uint32_t)(tile_start[(int64_t)view * d.tpv + ty * d.gx + tx] + (scanned[slot + s] - scanned[slot]));
+    }
+    uint32_t mine = 0;
+    uint64_t todo = wave_or64(any);
+    while (todo) {
+        const int t = __builtin_ctzll(todo);
+        todo &= todo - 1;
+        uint32_t run = WRITE ? (uint32_t)__builtin_amdgcn_readlane((int)init, t) : 0u;
+#pragma unroll
+        for (int k = 0; k < kChunkSteps; ++k) {
+            const bool has = ((mask[k] >> t) & 1ull) != 0ull;
+            const uint64_t b = __ballot(has);
+            if (b) {
+                if constexpr (WRITE) {
+                    if (has) {
+                        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
+                            (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+                        const int64_t pos = (int64_t)run + rank;
+                        if (pos < id_limit) ids[pos] = id[k];
+                    }
+                }
+                run += (uint32_t)__popcll(b);
+            }
+        }
+        if (lane == t) mine = run;
+    }
+    if constexpr (!WRITE) counts[slot + s] = mine;
+}
+
+// Pairs of every global tile: sum over its group's chunks.
+__global__ void tile_totals_kernel(const int32_t* __restrict__ chunk_base, const uint32_t* __restrict__ counts,
+                                   const int32_t* __restrict__ scanned, GridDims d, int64_t tiles,
+                                   int32_t* __restrict__ totals) {
+    const int64_t tile = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tile >= tiles) return;
+    const int view = (int)(tile / d.tpv);
+    const int r = (int)(tile - (int64_t)view * d.tpv);
+    const int ty = r / d.gx, tx = r - ty * d.gx;
+    const int g = view * d.gpv + (ty >> kGroupShift) * d.sgx + (tx >> kGroupShift);
+    const int t = ((ty & 7) << 3) + (tx & 7);
+    const int32_t cb = chunk_base[g];
+    const int32_t q = chunk_base[g + 1] - cb;
+    int32_t total = 0;
+    if (q > 0) {
+        const int64_t first = (int64_t)cb * 64 + (int64_t)t * q;
+        const int64_t last = first + q - 1;
+        total = scanned[last] + (int32_t)counts[last] - scanned[first];
+    }
+    totals[tile] = total;
+}
+
+__global__ void tile_ranges_from_totals_kernel(const int32_t* __restrict__ totals, const int32_t* __restrict__ starts,
+                                               int64_t tiles, int32_t* __restrict__ ranges) {
+    const int64_t tile = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tile >= tiles) return;
+    const int32_t n = totals[tile];
+    const int32_t a = n > 0 ? starts[tile] : 0;
+    reinterpret_cast<int2*>(ranges)[tile] = make_int2(a, a + n);
+}
+
+// tiles[p] = t for every p in [ranges[t][0], ranges[t][1]); one block per tile.
+__global__ void pair_tiles_kernel(const int32_t* __restrict__ ranges, int64_t tile_count, uint32_t* __restrict__ out,
+                                  int64_t count) {
+    const int64_t tile = blockIdx.x;
+    const int32_t a = ranges[2 * tile], b = ranges[2 * tile + 1];
+    for (int64_t p = (int64_t)a + threadIdx.x; p < b; p += blockDim.x)
+        if (p < count) out[p] = (uint32_t)tile;
 }
 
 // 64-bit reference keys (tile << 32 | depth bits) of sorted (tile, id) pairs.
@@ -515,26 +834,92 @@ __global__ void expand_keys_kernel(const uint32_t* __restrict__ tiles, const int
     keys[i] = ((uint64_t)tile << 32) | (uint64_t)__float_as_uint(depths[view * n + ids[i]]);
 }
 
+// Scratch of gs3d_order_rows.
 struct OrderScratch {
-    uint32_t* keys;   // 2*rows
-    int32_t* counts;  // rows
+    uint32_t* keys;       // 2*rows depth-bit keys
+    int32_t* counts;      // rows group counts
+    int64_t* pairs;       // per-block tile pair counts
     void* sort;
     void* scan;
 };
 
 inline size_t order_scratch_bytes(int64_t rows, OrderScratch* out, void* base) {
+    const int64_t blocks = (rows + kBinThreads - 1) / kBinThreads;
     const size_t a = align256((size_t)rows * 2 * sizeof(uint32_t));
     const size_t b = align256((size_t)rows * sizeof(int32_t));
-    const size_t c = align256(sort_scratch_bytes(rows, nullptr, nullptr));
-    const size_t d = scan_partials_bytes(rows);
+    const size_t c = align256((size_t)blocks * sizeof(int64_t));
+    const size_t e = align256(sort_scratch_bytes(rows, nullptr, nullptr));
+    const size_t f = scan_partials_bytes(rows);
     if (out) {
         char* p = reinterpret_cast<char*>(base);
         out->keys = reinterpret_cast<uint32_t*>(p);
         out->counts = reinterpret_cast<int32_t*>(p + a);
-        out->sort = p + a + b;
-        out->scan = p + a + b + c;
+        out->pairs = reinterpret_cast<int64_t*>(p + a + b);
+        out->sort = p + a + b + c;
+        out->scan = p + a + b + c + e;
     }
-    return a + b + c + d;
+    return a + b + c + e + f;
+}
+
+// Scratch of gs3d_bin_rows.
+struct BinScratch {
+    uint64_t* items;      // 2*group_pairs
+    void* sort;
+    int32_t* granges;     // 2*groups
+    int32_t* chunk_base;  // groups + 1
+    int32_t* chunk_group; // max_chunks
+    uint32_t* counts;     // 64*max_chunks
+    int32_t* scanned;     // 64*max_chunks
+    int32_t* totals;      // tiles
+    int32_t* starts;      // tiles
+    void* scan;
+};
+
+inline int64_t max_chunks_of(int64_t group_pairs, int64_t groups) { return (group_pairs + kChunk - 1) / kChunk + groups; }
+
+inline size_t bin_scratch_bytes(int64_t group_pairs, int64_t groups, int64_t tiles, BinScratch* out, void* base) {
+    const int64_t chunks = max_chunks_of(group_pairs, groups);
+    size_t sizes[10];
+    sizes[0] = align256((size_t)group_pairs * 2 * sizeof(uint64_t));
+    sizes[1] = align256(sort_scratch_bytes(group_pairs, nullptr, nullptr));
+    sizes[2] = align256((size_t)groups * 2 * sizeof(int32_t));
+    sizes[3] = align256((size_t)(groups + 1) * sizeof(int32_t));
+    sizes[4] = align256((size_t)chunks * sizeof(int32_t));
+    sizes[5] = align256((size_t)chunks * 64 * sizeof(uint32_t));
+    sizes[6] = sizes[5];
+    sizes[7] = align256((size_t)tiles * sizeof(int32_t));
+    sizes[8] = sizes[7];
+    const size_t scan_a = scan_partials_bytes(chunks * 64), scan_b = scan_partials_bytes(tiles);
+    sizes[9] = scan_a > scan_b ? scan_a : scan_b;
+    size_t total = 0;
+    char* p = reinterpret_cast<char*>(base);
+    void* parts[10];
+    for (int k = 0; k < 10; ++k) {
+        parts[k] = p ? p + total : nullptr;
+        total += sizes[k];
+    }
+    if (out) {
+        out->items = reinterpret_cast<uint64_t*>(parts[0]);
+        out->sort = parts[1];
+        out->granges = reinterpret_cast<int32_t*>(parts[2]);
+        out->chunk_base = reinterpret_cast<int32_t*>(parts[3]);
+        out->chunk_group = reinterpret_cast<int32_t*>(parts[4]);
+        out->counts = reinterpret_cast<uint32_t*>(parts[5]);
+        out->scanned = reinterpret_cast<int32_t*>(parts[6]);
+        out->totals = reinterpret_cast<int32_t*>(parts[7]);
+        out->starts = reinterpret_cast<int32_t*>(parts[8]);
+        out->scan = parts[9];
+    }
+    return total;
+}
+
+inline int bit_length(int64_t v) {
+    int b = 0;
+    while (v > 0) {
+        ++b;
+        v >>= 1;
+    }
+    return b;
 }
 
 }  // namespace gs3d
@@ -569,7 +954,7 @@ extern "C" int gs3d_emit_keys(const gs3d_emit_args* args, void* scratch, size_t 
     hipStream_t s = gs3d::as_stream(stream);
     uint32_t* queue_count = reinterpret_cast<uint32_t*>(scratch);
     int32_t* queue = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(scratch) + 256);
-    hipLaunchKernelGGL(gs3d::fill_u32_kernel, dim3(1), dim3(64), 0, s, queue_count, 1, 0u);
+    gs3d::fill_u32(queue_count, 1, 0u, s);
     hipLaunchKernelGGL(gs3d::emit_small_kernel, dim3(gs3d::blocks_for(rows, gs3d::kEmitThreads)),
                        dim3(gs3d::kEmitThreads), 0, s, a, queue_count, queue);
     hipLaunchKernelGGL(gs3d::emit_large_kernel, dim3(2048), dim3(gs3d::kEmitThreads), 0, s, a, queue_count, queue);
@@ -606,59 +991,135 @@ extern "C" int gs3d_tile_ranges(const uint64_t* sorted_keys, int64_t count, int3
     if (count < 0 || tile_count < 0) return GS3D_ERR_ARGUMENT;
     if (count == 0) return GS3D_OK;
     if (!sorted_keys || !ranges) return GS3D_ERR_ARGUMENT;
-    hipLaunchKernelGGL((gs3d::tile_ranges_kernel<uint64_t, 32>), dim3(gs3d::blocks_for(count, 256)), dim3(256), 0,
-                       gs3d::as_stream(stream), sorted_keys, count, ranges, tile_count);
+    hipLaunchKernelGGL(gs3d::tile_ranges_kernel<uint64_t>, dim3(gs3d::blocks_for(count, 256)), dim3(256), 0,
+                       gs3d::as_stream(stream), sorted_keys, count, 32, 0xFFFFFFFFu, ranges, tile_count);
     return gs3d::launch_status("gs3d_tile_ranges");
 }
 
-extern "C" int gs3d_tile_ranges_u32(const uint32_t* sorted_tiles, int64_t count, int32_t* ranges,
-                                    int64_t tile_count, void* stream) {
-    if (count < 0 || tile_count < 0) return GS3D_ERR_ARGUMENT;
-    if (count == 0) return GS3D_OK;
-    if (!sorted_tiles || !ranges) return GS3D_ERR_ARGUMENT;
-    hipLaunchKernelGGL((gs3d::tile_ranges_kernel<uint32_t, 0>), dim3(gs3d::blocks_for(count, 256)), dim3(256), 0,
-                       gs3d::as_stream(stream), sorted_tiles, count, ranges, tile_count);
-    return gs3d::launch_status("gs3d_tile_ranges_u32");
-}
-
-extern "C" size_t gs3d_depth_order_scratch_bytes(int64_t rows) {
+extern "C" size_t gs3d_order_rows_scratch_bytes(int64_t rows) {
     return gs3d::order_scratch_bytes(rows < 0 ? 0 : rows, nullptr, nullptr);
 }
 
-extern "C" int gs3d_depth_order(const float* depths, const int32_t* tiles, int64_t rows, int32_t* order,
-                                int32_t* offsets, int64_t* total, void* scratch, size_t scratch_bytes, void* stream) {
-    if (rows < 0) return GS3D_ERR_ARGUMENT;
-    if (rows == 0) return GS3D_OK;
+extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_t scratch_bytes, void* stream) {
+    if (!args) return GS3D_ERR_ARGUMENT;
+    const gs3d_order_args& a = *args;
+    if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0 || !a.totals) return GS3D_ERR_ARGUMENT;
+    const int64_t rows = (int64_t)a.n * a.views;
+    hipStream_t s = gs3d::as_stream(stream);
+    if (rows == 0) {
+        gs3d::fill_u32(reinterpret_cast<uint32_t*>(a.totals), 4, 0u, s);
+        return gs3d::launch_status("gs3d_order_rows");
+    }
     if (rows > INT32_MAX) return GS3D_ERR_OVERFLOW;
-    if (!depths || !tiles || !order || !offsets || !scratch) return GS3D_ERR_ARGUMENT;
-    if (scratch_bytes < gs3d_depth_order_scratch_bytes(rows)) return GS3D_ERR_SCRATCH;
+    const gs3d::GridDims d = gs3d::grid_dims(a.width, a.height);
+    if (d.gx >= 0xFFFF || d.gy >= 0xFFFF) return GS3D_ERR_UNSUPPORTED;
+    if (!a.depths || !a.centers || !a.radii || !a.order || !a.group_offsets || !scratch) return GS3D_ERR_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(a.centers) & 7) || (reinterpret_cast<uintptr_t>(a.order) & 7))
+        return GS3D_ERR_ARGUMENT;
+    if (scratch_bytes < gs3d_order_rows_scratch_bytes(rows)) return GS3D_ERR_SCRATCH;
     gs3d::OrderScratch sc;
     gs3d::order_scratch_bytes(rows, &sc, scratch);
-    hipStream_t s = gs3d::as_stream(stream);
+    const bool packed = d.gx <= 256 && d.gy <= 256;
     const dim3 grid(gs3d::blocks_for(rows, 256)), block(256);
-    hipLaunchKernelGGL(gs3d::depth_keys_kernel, grid, block, 0, s, depths, rows, sc.keys, order);
-    // order holds 2*rows entries: [0, rows) sorted result, [rows, 2rows) ping-pong.
-    int status = gs3d::run_sort<uint32_t>(sc.keys, order, rows, 32, sc.sort, s);
+    if (packed)
+        hipLaunchKernelGGL(gs3d::row_records_kernel<true>, grid, block, 0, s, a.depths, a.centers, a.radii, rows, d.gx,
+                           d.gy, sc.keys, a.order);
+    else
+        hipLaunchKernelGGL(gs3d::row_records_kernel<false>, grid, block, 0, s, a.depths, a.centers, a.radii, rows,
+                           d.gx, d.gy, sc.keys, a.order);
+    // order holds 2*rows records: [0, rows) sorted result, [rows, 2rows) ping-pong.
+    int status = gs3d::run_sort<uint32_t, uint64_t>(sc.keys, a.order, rows, 32, sc.sort, s);
     if (status != GS3D_OK) return status;
-    hipLaunchKernelGGL(gs3d::gather_counts_kernel, grid, block, 0, s, tiles, order, rows, sc.counts);
-    status = gs3d::run_scan<int32_t, true>(sc.counts, rows, offsets, total, sc.scan, s);
+    const dim3 cgrid(gs3d::blocks_for(rows, gs3d::kBinThreads)), cblock(gs3d::kBinThreads);
+    if (packed)
+        hipLaunchKernelGGL(gs3d::order_counts_kernel<true>, cgrid, cblock, 0, s, a.order, rows, a.centers, a.radii,
+                           d.gx, d.gy, sc.counts, sc.pairs);
+    else
+        hipLaunchKernelGGL(gs3d::order_counts_kernel<false>, cgrid, cblock, 0, s, a.order, rows, a.centers, a.radii,
+                           d.gx, d.gy, sc.counts, sc.pairs);
+    hipLaunchKernelGGL(gs3d::sum_i64_kernel, dim3(1), dim3(1024), 0, s, sc.pairs, (int64_t)cgrid.x, a.totals + 1);
+    status = gs3d::run_scan<int32_t, true>(sc.counts, rows, a.group_offsets, a.totals, sc.scan, s);
     if (status != GS3D_OK) return status;
-    return gs3d::launch_status("gs3d_depth_order");
+    return gs3d::launch_status("gs3d_order_rows");
 }
 
-extern "C" int gs3d_emit_ordered(const gs3d_emit_ordered_args* args, void* stream) {
+extern "C" size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t width, int32_t height) {
+    if (group_pairs < 0 || views < 0 || width <= 0 || height <= 0) return 0;
+    const gs3d::GridDims d = gs3d::grid_dims(width, height);
+    return gs3d::bin_scratch_bytes(group_pairs, (int64_t)views * d.gpv, (int64_t)views * d.tpv, nullptr, nullptr);
+}
+
+extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream) {
     if (!args) return GS3D_ERR_ARGUMENT;
-    const gs3d_emit_ordered_args& a = *args;
-    if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0) return GS3D_ERR_ARGUMENT;
+    const gs3d_bin_args& a = *args;
+    if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0 || a.group_pairs < 0 || a.tile_pairs < 0)
+        return GS3D_ERR_ARGUMENT;
+    const gs3d::GridDims d = gs3d::grid_dims(a.width, a.height);
     const int64_t rows = (int64_t)a.n * a.views;
-    if (rows == 0) return GS3D_OK;
-    if (!a.centers || !a.radii || !a.order || !a.offsets || !a.tile_keys || !a.values) return GS3D_ERR_ARGUMENT;
-    if (reinterpret_cast<uintptr_t>(a.centers) & 7) return GS3D_ERR_ARGUMENT;
-    const int64_t tiles_total = (int64_t)((a.width + 15) / 16) * ((a.height + 15) / 16) * a.views;
-    if (tiles_total > 0xFFFFFFFFll) return GS3D_ERR_OVERFLOW;
-    hipLaunchKernelGGL(gs3d::emit_ordered_kernel, dim3(gs3d::blocks_for(rows, gs3d::kOrderedThreads)),
-                       dim3(gs3d::kOrderedThreads), 0, gs3d::as_stream(stream), a);
-    return gs3d::launch_status("gs3d_emit_ordered");
+    const int64_t groups = (int64_t)a.views * d.gpv, tiles = (int64_t)a.views * d.tpv;
+    if (tiles == 0) return GS3D_OK;
+    if (!a.ranges) return GS3D_ERR_ARGUMENT;
+    if (rows > INT32_MAX || a.group_pairs > INT32_MAX || a.tile_pairs > INT32_MAX) return GS3D_ERR_OVERFLOW;
+    if (groups >= (int64_t)1 << gs3d::kGroupBits || d.gx >= 0xFFFF || d.gy >= 0xFFFF) return GS3D_ERR_UNSUPPORTED;
+    hipStream_t s = gs3d::as_stream(stream);
+    if (a.group_pairs == 0 || a.tile_pairs == 0 || rows == 0) {
+        gs3d::fill_u32(reinterpret_cast<uint32_t*>(a.ranges), 2 * tiles, 0u, s);
+        return gs3d::launch_status("gs3d_bin_rows");
+    }
+    if (!a.centers || !a.radii || !a.order || !a.group_offsets || !a.ids || !scratch) return GS3D_ERR_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(a.ranges) & 7) || (reinterpret_cast<uintptr_t>(a.order) & 7) ||
+        (reinterpret_cast<uintptr_t>(a.centers) & 7))
+        return GS3D_ERR_ARGUMENT;
+    if (scratch_bytes < gs3d_bin_rows_scratch_bytes(a.group_pairs, a.views, a.width, a.height))
+        return GS3D_ERR_SCRATCH;
+    gs3d::BinScratch sc;
+    gs3d::bin_scratch_bytes(a.group_pairs, groups, tiles, &sc, scratch);
+    const int64_t S = a.group_pairs;
+    const int64_t chunks = gs3d::max_chunks_of(S, groups);
+    const dim3 egrid(gs3d::blocks_for(rows, gs3d::kBinThreads)), eblock(gs3d::kBinThreads);
+    if (d.gx <= 256 && d.gy <= 256)
+        hipLaunchKernelGGL(gs3d::group_emit_kernel<true>, egrid, eblock, 0, s, a.order, a.group_offsets, rows,
+                           a.centers, a.radii, a.n, d, S, sc.items);
+    else
+        hipLaunchKernelGGL(gs3d::group_emit_kernel<false>, egrid, eblock, 0, s, a.order, a.group_offsets, rows,
+                           a.centers, a.radii, a.n, d, S, sc.items);
+    int status = gs3d::run_sort<uint64_t, int32_t>(sc.items, nullptr, S, gs3d::bit_length(groups - 1 > 0 ? groups - 1 : 1),
+                                          sc.sort, s);
+    if (status != GS3D_OK) return status;
+    gs3d::fill_u32(reinterpret_cast<uint32_t*>(sc.granges), 2 * groups, 0u, s);
+    hipLaunchKernelGGL(gs3d::tile_ranges_kernel<uint64_t>, dim3(gs3d::blocks_for(S, 256)), dim3(256), 0, s, sc.items,
+                       S, 0, gs3d::kGroupMask, sc.granges, groups);
+    hipLaunchKernelGGL(gs3d::chunk_base_kernel, dim3(1), dim3(1024), 0, s, sc.granges, (int)groups, sc.chunk_base);
+    hipLaunchKernelGGL(gs3d::chunk_group_kernel, dim3(gs3d::blocks_for(chunks, 256)), dim3(256), 0, s,
+                       sc.chunk_base, (int)groups, chunks, sc.chunk_group);
+    gs3d::fill_u32(sc.counts, 64 * chunks, 0u, s);
+    const dim3 pass_grid(gs3d::blocks_for(chunks, gs3d::kBinWaves));
+    hipLaunchKernelGGL((gs3d::group_pass_kernel<false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
+                       sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts,
+                       (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0);
+    status = gs3d::run_scan<uint32_t, false>(sc.counts, 64 * chunks, sc.scanned, nullptr, sc.scan, s);
+    if (status != GS3D_OK) return status;
+    hipLaunchKernelGGL(gs3d::tile_totals_kernel, dim3(gs3d::blocks_for(tiles, 256)), dim3(256), 0, s, sc.chunk_base,
+                       sc.counts, sc.scanned, d, tiles, sc.totals);
+    status = gs3d::run_scan<int32_t, false>(sc.totals, tiles, sc.starts, nullptr, sc.scan, s);
+    if (status != GS3D_OK) return status;
+    hipLaunchKernelGGL(gs3d::tile_ranges_from_totals_kernel, dim3(gs3d::blocks_for(tiles, 256)), dim3(256), 0, s,
+                       sc.totals, sc.starts, tiles, a.ranges);
+    hipLaunchKernelGGL((gs3d::group_pass_kernel<true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
+                       sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts, sc.scanned,
+                       sc.starts, a.ids, a.tile_pairs);
+    return gs3d::launch_status("gs3d_bin_rows");
+}
+
+extern "C" int gs3d_pair_tiles(const int32_t* ranges, int64_t tile_count, uint32_t* tiles, int64_t count,
+                               void* stream) {
+    if (tile_count < 0 || count < 0) return GS3D_ERR_ARGUMENT;
+    if (tile_count == 0 || count == 0) return GS3D_OK;
+    if (!ranges || !tiles) return GS3D_ERR_ARGUMENT;
+    if (tile_count > INT32_MAX) return GS3D_ERR_OVERFLOW;
+    hipLaunchKernelGGL(gs3d::pair_tiles_kernel, dim3((unsigned)tile_count), dim3(256), 0, gs3d::as_stream(stream),
+                       ranges, tile_count, tiles, count);
+    return gs3d::launch_status("gs3d_pair_tiles");
 }
 
 extern "C" int gs3d_expand_keys(const uint32_t* sorted_tiles, const int32_t* ids, int64_t count, const float* depths,

@@ -21,7 +21,8 @@ from .autograd import Frame, Rasterize
 from .projection import project_views
 from ..cameras import validate_camera_options
 from ..inputs import batch_item, normalize_inputs
-from ..splatting.binning import depth_order, finish_binning, require_radius_mode, validate_tile_mode
+from ..splatting.binning import (check_pair_counts, finish_binning, order_rows, require_radius_mode,
+                                 validate_tile_mode)
 from ..splatting.cameras import launch_prepare, raise_camera_errors
 from ..statistics import StatisticsRequest
 from ..training import prepare_training_metadata
@@ -54,7 +55,7 @@ class RasterizationResult:
 @torch.no_grad()
 def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height, near, far, radius_clip,
                    sh, sh_degree, background) -> Frame:
-    """Camera rows, fused projection, scan, one synchronisation, binning."""
+    """Camera rows, fused projection, depth order, one synchronisation, binning."""
     with_centers = sh_degree is not None and sh_degree > 0
     full, inverse, centers, errors = launch_prepare(viewmats, Ks, width, height, with_centers)
     state = project_views(
@@ -62,13 +63,13 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
         sh=sh if sh_degree is not None else None, sh_degree=sh_degree or 0,
         camera_centers=centers if with_centers else None, metadata=True,
     )
-    order, offsets, total = depth_order(state.depths, state.tile_counts)
-    host = torch.cat([errors.to(torch.int64), total]).cpu().tolist()
-    raise_camera_errors(host[:-1])
-    count = int(host[-1]) if len(offsets) else 0
-    if count > 2**31 - 1:
-        raise OverflowError(f"{count} tile pairs exceed the int32 offsets of the binning stage")
-    bins = finish_binning(state.centers, state.radii, state.depths, order, offsets, count, width, height)
+    order, offsets, totals = order_rows(state.centers, state.radii, state.depths, width, height)
+    host = torch.cat([errors.to(torch.int64), totals]).cpu().tolist()
+    raise_camera_errors(host[:-2])
+    group_pairs, count = int(host[-2]), int(host[-1])
+    check_pair_counts(group_pairs, count)
+    bins = finish_binning(state.centers, state.radii, order, offsets, group_pairs, count, state.depths, width,
+                          height)
     return Frame(
         width, height, Ks.detach(), full, inverse if with_centers else None, centers if with_centers else None,
         state, bins["ranges"], bins["point_list"], count, sh_degree, background,

@@ -113,7 +113,22 @@ class EmitArgs(ctypes.Structure):
     ]
 
 
-class EmitOrderedArgs(ctypes.Structure):
+class OrderArgs(ctypes.Structure):
+    _fields_ = [
+        ("n", ctypes.c_int32),
+        ("views", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("height", ctypes.c_int32),
+        ("depths", _P),
+        ("centers", _P),
+        ("radii", _P),
+        ("order", _P),
+        ("group_offsets", _P),
+        ("totals", _P),
+    ]
+
+
+class BinArgs(ctypes.Structure):
     _fields_ = [
         ("n", ctypes.c_int32),
         ("views", ctypes.c_int32),
@@ -122,9 +137,11 @@ class EmitOrderedArgs(ctypes.Structure):
         ("centers", _P),
         ("radii", _P),
         ("order", _P),
-        ("offsets", _P),
-        ("tile_keys", _P),
-        ("values", _P),
+        ("group_offsets", _P),
+        ("group_pairs", ctypes.c_int64),
+        ("tile_pairs", ctypes.c_int64),
+        ("ranges", _P),
+        ("ids", _P),
     ]
 
 
@@ -178,7 +195,8 @@ STRUCTS = {
     "gs3d_project_args": ProjectArgs,
     "gs3d_project_bwd_args": ProjectBwdArgs,
     "gs3d_emit_args": EmitArgs,
-    "gs3d_emit_ordered_args": EmitOrderedArgs,
+    "gs3d_order_args": OrderArgs,
+    "gs3d_bin_args": BinArgs,
     "gs3d_render_args": RenderArgs,
     "gs3d_render_bwd_args": RenderBwdArgs,
 }
@@ -215,11 +233,12 @@ FUNCTIONS = {
     "gs3d_sort_scratch_bytes": (_SZ, [_I64]),
     "gs3d_sort_pairs_u64": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),
     "gs3d_tile_ranges": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
-    "gs3d_depth_order_scratch_bytes": (_SZ, [_I64]),
-    "gs3d_depth_order": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _SZ, _P]),
-    "gs3d_emit_ordered": (ctypes.c_int, [ctypes.POINTER(EmitOrderedArgs), _P]),
+    "gs3d_order_rows_scratch_bytes": (_SZ, [_I64]),
+    "gs3d_order_rows": (ctypes.c_int, [ctypes.POINTER(OrderArgs), _P, _SZ, _P]),
+    "gs3d_bin_rows_scratch_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
+    "gs3d_bin_rows": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
+    "gs3d_pair_tiles": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
     "gs3d_sort_pairs_u32": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),
-    "gs3d_tile_ranges_u32": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
     "gs3d_expand_keys": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _I32, _P, _P]),
     "gs3d_render_fwd": (ctypes.c_int, [ctypes.POINTER(RenderArgs), _P]),
     "gs3d_render_bwd": (ctypes.c_int, [ctypes.POINTER(RenderBwdArgs), _P]),

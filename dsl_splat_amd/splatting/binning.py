@@ -1,11 +1,14 @@
-"""Square-tile duplication and sorting (splatting/binning.py:16-117 of the
-reference) for one or several views at once.
+"""Square-tile binning (splatting/binning.py:16-117 of the reference) for one
+or several views at once.
 
-Rows of all views form one flat array (views*N); a pair of view v gets the
-global tile id v*tiles + y*gx + x, so one radix sort over
-32 + bit_length(views*tiles) key bits orders every view and ``ranges`` has
-one row per (view, tile).  With one view this is exactly the reference's
-per-view binning.
+Rows of all views form one flat array (views*N); a tile of view v has the
+global id v*tiles + y*gx + x and ``ranges`` has one row per (view, tile).
+``emit_and_sort`` is the reference's own sequence (inclusive scan, 64-bit
+(tile << 32 | depth bits) keys, stable radix sort, ranges); the rasterizer
+uses ``order_rows`` + ``bin_rows``, which produce the same lists and ranges
+without sorting the pairs (depth-ordered rows, 8x8-tile groups, wavefront
+ballot ranking).  With one view either is exactly the reference's per-view
+binning.
 """
 
 import ctypes
@@ -73,60 +76,63 @@ def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tenso
 
 
 @torch.no_grad()
-def depth_order(depths: Tensor, tile_counts: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    """Rows (views*N) stably sorted by depth bits; inclusive offsets of their
-    tile counts in that order and the int64 total (all left on the device).
-    Returns (order with 2*rows storage, offsets, total)."""
-    device = depths.device
-    rows = depths.numel()
-    order = torch.empty(2 * rows, dtype=torch.int32, device=device)
-    offsets = torch.empty(rows, dtype=torch.int32, device=device)
-    total = torch.zeros(1, dtype=torch.int64, device=device)
-    if rows:
-        depths, tile_counts = depths.contiguous(), tile_counts.contiguous()
-        scratch = _scratch(native.query("gs3d_depth_order_scratch_bytes", rows), device)
-        native.call("gs3d_depth_order", native.ptr(depths), native.ptr(tile_counts), rows, native.ptr(order),
-                    native.ptr(offsets), native.ptr(total), native.ptr(scratch), scratch.numel(),
-                    native.stream(device))
-    return order, offsets, total
+def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int,
+               height: int) -> tuple[Tensor, Tensor, Tensor]:
+    """Depth order of the (views, N) rows.
 
-
-@torch.no_grad()
-def emit_ordered(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, count: int, width: int,
-                 height: int) -> tuple[Tensor, Tensor]:
-    """(uint32 global tile ids stored as int32, int32 Gaussian ids), each with
-    2*count storage, of the ordered rows' tile pairs."""
+    Returns (ordered row records with 2*rows storage, inclusive group
+    offsets, totals = [group pairs, tile pairs]), all left on the device."""
     device = radii.device
     views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
-    tiles = torch.empty(2 * count, dtype=torch.int32, device=device)
-    ids = torch.empty(2 * count, dtype=torch.int32, device=device)
-    if count:
-        a = abi.EmitOrderedArgs()
-        a.n, a.views, a.width, a.height = n, views, width, height
-        centers, radii = centers.contiguous(), radii.contiguous()
-        a.centers, a.radii, a.order, a.offsets = (native.ptr(centers), native.ptr(radii), native.ptr(order),
-                                                  native.ptr(offsets))
-        a.tile_keys, a.values = native.ptr(tiles), native.ptr(ids)
-        native.call("gs3d_emit_ordered", ctypes.byref(a), native.stream(device))
-    return tiles, ids
+    rows = views * n
+    order = torch.empty(2 * rows, dtype=torch.int64, device=device)
+    offsets = torch.empty(rows, dtype=torch.int32, device=device)
+    totals = torch.empty(2, dtype=torch.int64, device=device)
+    a = abi.OrderArgs()
+    a.n, a.views, a.width, a.height = n, views, width, height
+    depths, centers, radii = depths.contiguous(), centers.contiguous(), radii.contiguous()
+    a.depths, a.centers, a.radii = native.ptr(depths), native.ptr(centers), native.ptr(radii)
+    a.order, a.group_offsets, a.totals = native.ptr(order), native.ptr(offsets), native.ptr(totals)
+    scratch = _scratch(native.query("gs3d_order_rows_scratch_bytes", rows), device)
+    native.call("gs3d_order_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
+    return order, offsets, totals
+
+
+def check_pair_counts(group_pairs: int, tile_pairs: int) -> None:
+    if tile_pairs > 2**31 - 1 or group_pairs > 2**31 - 1:
+        raise OverflowError(f"{tile_pairs} tile pairs exceed the int32 offsets of the binning stage")
 
 
 @torch.no_grad()
-def sort_by_tile(tiles: Tensor, ids: Tensor, count: int, tile_total: int) -> None:
-    """Stable sort of the (tile, id) pairs on the tile id, in place."""
-    if count > 1:
-        scratch = _scratch(native.query("gs3d_sort_scratch_bytes", count), tiles.device)
-        native.call("gs3d_sort_pairs_u32", native.ptr(tiles), native.ptr(ids), count, int(tile_total).bit_length(),
-                    native.ptr(scratch), scratch.numel(), native.stream(tiles.device))
+def bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, group_pairs: int, tile_pairs: int,
+             width: int, height: int) -> tuple[Tensor, Tensor]:
+    """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs)
+    of rows ordered by ``order_rows``."""
+    device = order.device
+    views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
+    check_pair_counts(group_pairs, tile_pairs)
+    ranges = torch.empty((tile_count(width, height, views), 2), dtype=torch.int32, device=device)
+    ids = torch.empty(tile_pairs, dtype=torch.int32, device=device)
+    centers, radii = centers.contiguous(), radii.contiguous()
+    a = abi.BinArgs()
+    a.n, a.views, a.width, a.height = n, views, width, height
+    a.centers, a.radii = native.ptr(centers), native.ptr(radii)
+    a.order, a.group_offsets = native.ptr(order), native.ptr(offsets)
+    a.group_pairs, a.tile_pairs = group_pairs, tile_pairs
+    a.ranges, a.ids = native.ptr(ranges), native.ptr(ids)
+    scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, views, width, height), device)
+    native.call("gs3d_bin_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
+    return ranges, ids
 
 
 @torch.no_grad()
-def ranges_of(sorted_tiles: Tensor, count: int, tile_total: int) -> Tensor:
-    ranges = torch.zeros((tile_total, 2), dtype=torch.int32, device=sorted_tiles.device)
+def pair_tiles(ranges: Tensor, count: int) -> Tensor:
+    """Global tile id of every listed pair (uint32 values in int32 storage)."""
+    tiles = torch.empty(count, dtype=torch.int32, device=ranges.device)
     if count:
-        native.call("gs3d_tile_ranges_u32", native.ptr(sorted_tiles), count, native.ptr(ranges), tile_total,
-                    native.stream(sorted_tiles.device))
-    return ranges
+        native.call("gs3d_pair_tiles", native.ptr(ranges), ranges.shape[0], native.ptr(tiles), count,
+                    native.stream(ranges.device))
+    return tiles
 
 
 @torch.no_grad()
@@ -142,17 +148,14 @@ def expand_keys(sorted_tiles: Tensor, ids: Tensor, count: int, depths: Tensor, w
 
 
 @torch.no_grad()
-def finish_binning(centers: Tensor, radii: Tensor, depths: Tensor, order: Tensor, offsets: Tensor, count: int,
-                   width: int, height: int, *, with_keys: bool = False) -> TileBins:
-    """Emission in depth order, stable tile sort and ranges for a known pair
-    count (the host has read the total of ``depth_order``)."""
-    views = 1 if radii.ndim == 1 else radii.shape[0]
-    tile_total = tile_count(width, height, views)
-    tiles, ids = emit_ordered(centers, radii, order, offsets, count, width, height)
-    sort_by_tile(tiles, ids, count, tile_total)
-    bins: TileBins = dict(point_list=ids[:count], ranges=ranges_of(tiles, count, tile_total))
+def finish_binning(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, group_pairs: int,
+                   tile_pairs: int, depths: Tensor, width: int, height: int, *, with_keys: bool = False) -> TileBins:
+    """Tile lists and ranges once the host has read the totals of
+    ``order_rows``."""
+    ranges, ids = bin_rows(centers, radii, order, offsets, group_pairs, tile_pairs, width, height)
+    bins: TileBins = dict(point_list=ids, ranges=ranges)
     if with_keys:
-        bins["point_list_keys"] = expand_keys(tiles, ids, count, depths, width, height)
+        bins["point_list_keys"] = expand_keys(pair_tiles(ranges, tile_pairs), ids, tile_pairs, depths, width, height)
     return bins
 
 
@@ -162,12 +165,12 @@ def bin_and_sort(centers: Tensor, radii: Tensor, tile_counts: Tensor, depths: Te
                  with_keys: bool = False) -> TileBins:
     """Bin one view's (N,) or several views' (C, N) projected Gaussians into
     depth-sorted per-tile lists (same order and ranges as the reference's
-    scan + duplicate + 64-bit key sort)."""
+    scan + duplicate + 64-bit key sort).  ``tile_counts`` is accepted for
+    the reference's signature; the counts follow from centers and radii."""
     if tile_mode != "radius" and conics is None:
         raise ValueError("SnugBox/AccuTile require projected conics")
     require_radius_mode(tile_mode)
-    order, offsets, total = depth_order(depths, tile_counts)
-    count = int(total.item()) if depths.numel() else 0
-    if count > 2**31 - 1:
-        raise OverflowError("tile pair count exceeds int32 offsets")
-    return finish_binning(centers, radii, depths, order, offsets, count, width, height, with_keys=with_keys)
+    order, offsets, totals = order_rows(centers, radii, depths, width, height)
+    group_pairs, tile_pairs = totals.cpu().tolist()
+    return finish_binning(centers, radii, order, offsets, group_pairs, tile_pairs, depths, width, height,
+                          with_keys=with_keys)

@@ -220,37 +220,67 @@ int gs3d_tile_ranges(const uint64_t* sorted_keys, int64_t count, int32_t* ranges
                      int64_t tile_count, void* stream);
 
 /* ------------------------------------------------------------------------
- * Depth-ordered binning: the same (tile, depth, id) order as
- * gs3d_emit_keys + gs3d_sort_pairs_u64 (splatting/binning.py:71-117 with
- * primitives/tiling.py:57-100), with the radix sort over 32-bit tile ids
- * only.  Steps:
- *   1. gs3d_depth_order: stable sort of the views*N rows by the bits of their
- *      depth (order has 2*rows int32 storage: the first half receives the
- *      row permutation), then the inclusive scan of their tile counts taken
- *      in that order (offsets) and its 64-bit total.
- *   2. gs3d_emit_ordered: the pairs of the ordered rows, row-major over each
- *      tile rectangle, as (uint32 global tile id, int32 Gaussian index).
- *   3. gs3d_sort_pairs_u32 on bits [0, bit_length(views*tiles)): stable, so
- *      each tile keeps (depth bits, Gaussian index) order.
- *   4. gs3d_tile_ranges_u32; gs3d_expand_keys rebuilds the 64-bit keys
- *      (tile << 32 | depth bits) when a caller wants them.
+ * Grouped binning: the tile lists that splatting/binning.py:71-117 builds
+ * with scan_counts, duplicate, sort_tile_pairs and identify_ranges
+ * (primitives/tiling.py:39-100) -- each tile's Gaussian indices in
+ * (depth bits, Gaussian index) order, tiles concatenated in global tile order
+ * (view*tiles + y*gx + x), ranges [first, last) with (0, 0) for untouched
+ * tiles -- built without sorting the tile pairs:
+ *   1. gs3d_order_rows: stable sort of the views*N rows by the bits of their
+ *      depth, giving one 64-bit record per row in that order: the row index
+ *      (view*N + Gaussian) in the low 32 bits and, for tile grids of at most
+ *      256 x 256 tiles, the row's tile rectangle in the high 32 bits
+ *      (x0 | y0 << 8 | (x1-1) << 16 | (y1-1) << 24, 0x000000FF when culled;
+ *      larger grids leave them zero); the inclusive scan of the number of
+ *      8x8-tile groups each rectangle touches; two totals: group pairs
+ *      (totals[0]) and tile pairs (totals[1], the reference's offsets[-1]).
+ *   2. The caller reads the totals and allocates ids (tile pairs).
+ *   3. gs3d_bin_rows: one (group, row) item per touched group, emitted in
+ *      depth order and sorted stably by group; every group's list is cut into
+ *      512-item chunks and each wavefront ranks its chunk's tiles with 64-lane
+ *      ballots (one ballot per tile of the group), so every Gaussian index is
+ *      written once, straight to its final position; ranges are written for
+ *      every tile.
+ * Limits: views*groups < 2^20, group and tile pairs < 2^31, tile grid sides
+ * < 2^16.
  * ---------------------------------------------------------------------- */
-size_t gs3d_depth_order_scratch_bytes(int64_t rows);
-int gs3d_depth_order(const float* depths, const int32_t* tiles, int64_t rows,
-                     int32_t* order, int32_t* offsets, int64_t* total,
-                     void* scratch, size_t scratch_bytes, void* stream);
-
-typedef struct gs3d_emit_ordered_args {
+typedef struct gs3d_order_args {
     int32_t n, views, width, height;
+    const float* depths;      /* (views,N) */
     const float* centers;     /* (views,N,2) */
-    const int32_t* radii;     /* (views,N) */
-    const int32_t* order;     /* (views*N) row permutation */
-    const int32_t* offsets;   /* (views*N) inclusive, in permutation order */
-    uint32_t* tile_keys;      /* (M) global tile id view*tiles + y*gx + x */
-    int32_t* values;          /* (M) Gaussian index within its view */
-} gs3d_emit_ordered_args;
+    const int32_t* radii;     /* (views,N); rows with radius <= 0 are culled */
+    uint64_t* order;          /* (2*views*N): first half receives the ordered records */
+    int32_t* group_offsets;   /* (views*N) inclusive scan of group counts, record order */
+    int64_t* totals;          /* (2) group pairs, tile pairs */
+} gs3d_order_args;
 
-int gs3d_emit_ordered(const gs3d_emit_ordered_args* args, void* stream);
+size_t gs3d_order_rows_scratch_bytes(int64_t rows);
+int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_t scratch_bytes, void* stream);
+
+typedef struct gs3d_bin_args {
+    int32_t n, views, width, height;
+    const float* centers;          /* (views,N,2), as given to gs3d_order_rows */
+    const int32_t* radii;          /* (views,N) */
+    const uint64_t* order;         /* outputs of gs3d_order_rows */
+    const int32_t* group_offsets;
+    int64_t group_pairs;           /* totals[0] */
+    int64_t tile_pairs;            /* totals[1] */
+    int32_t* ranges;               /* (views*tiles,2), every entry written */
+    int32_t* ids;                  /* (tile_pairs) Gaussian index within its view */
+} gs3d_bin_args;
+
+size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t width, int32_t height);
+int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream);
+
+/* Global tile id of every listed pair: tiles[p] = t for p in ranges[t]. */
+int gs3d_pair_tiles(const int32_t* ranges, int64_t tile_count, uint32_t* tiles, int64_t count,
+                    void* stream);
+
+/* keys[i] = (tiles[i] << 32) | bits(depths[view*n + ids[i]]), view =
+ * tiles[i] / tiles_per_view: the reference's sorted 64-bit keys. */
+int gs3d_expand_keys(const uint32_t* sorted_tiles, const int32_t* ids, int64_t count,
+                     const float* depths, int32_t n, int32_t tiles_per_view,
+                     uint64_t* keys, void* stream);
 
 /* Stable LSD radix sort of (uint32 key, int32 value) pairs over key bits
  * [0, end_bit); 2*count storage as gs3d_sort_pairs_u64.  Scratch size is
@@ -258,15 +288,6 @@ int gs3d_emit_ordered(const gs3d_emit_ordered_args* args, void* stream);
 int gs3d_sort_pairs_u32(uint32_t* keys, int32_t* values, int64_t count,
                         int32_t end_bit, void* scratch, size_t scratch_bytes,
                         void* stream);
-
-int gs3d_tile_ranges_u32(const uint32_t* sorted_tiles, int64_t count, int32_t* ranges,
-                         int64_t tile_count, void* stream);
-
-/* keys[i] = (tiles[i] << 32) | bits(depths[view*n + ids[i]]), view =
- * tiles[i] / tiles_per_view. */
-int gs3d_expand_keys(const uint32_t* sorted_tiles, const int32_t* ids, int64_t count,
-                     const float* depths, int32_t n, int32_t tiles_per_view,
-                     uint64_t* keys, void* stream);
 
 /* ------------------------------------------------------------------------
  * Forward alpha blending on 16x16 tiles: gs3d/render.py:36-208 (render,

@@ -31,7 +31,8 @@ def test_library_exports_every_declared_symbol():
     # Size queries need no device.
     assert native.query("gs3d_sort_scratch_bytes", 1 << 20) > 0
     assert native.query("gs3d_scan_scratch_bytes", 0) >= 0
-    assert native.query("gs3d_depth_order_scratch_bytes", 1000) > 0
+    assert native.query("gs3d_order_rows_scratch_bytes", 1000) > 0
+    assert native.query("gs3d_bin_rows_scratch_bytes", 10_000, 4, 1920, 1080) > 0
 
 
 def test_argument_errors_are_reported_without_launching():
@@ -47,7 +48,12 @@ def test_argument_errors_are_reported_without_launching():
     args.ranges = args.centers = args.conics = args.features = ctypes.c_void_p(256)
     assert lib.gs3d_render_fwd(ctypes.byref(args), None) == abi.GS3D_ERR_UNSUPPORTED
     # Zero-size work is a no-op.
-    assert lib.gs3d_tile_ranges_u32(None, 0, None, 0, None) == abi.GS3D_OK
+    assert lib.gs3d_pair_tiles(None, 0, None, 0, None) == abi.GS3D_OK
+    args = abi.BinArgs()
+    args.n, args.views, args.width, args.height = 10, 1, 16, 16
+    args.group_pairs, args.tile_pairs = 1 << 31, 5
+    args.ranges = ctypes.c_void_p(256)
+    assert lib.gs3d_bin_rows(ctypes.byref(args), None, 0, None) == abi.GS3D_ERR_OVERFLOW
     with pytest.raises(native.NativeLibraryError, match="invalid argument"):
         native.call("gs3d_scan_i32", None, -1, None, None, None, 0, None)
 

@@ -17,6 +17,7 @@ from dsl_splat_amd import synthetic
 from dsl_splat_amd.gs3d import projection as gproj
 from dsl_splat_amd.gs3d import render as grender
 from dsl_splat_amd.primitives import tiling
+from dsl_splat_amd.runtime import native
 from dsl_splat_amd.splatting import binning, cameras
 
 pytestmark = pytest.mark.gpu
@@ -240,12 +241,13 @@ def test_projection_backward_parity(key, degree):
 
 
 @pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3), ("sh3_720p", 0)])
-def test_depth_ordered_binning_matches_reference_order(key, degree):
-    # The production binning (depth-ordered rows, 32-bit tile sort) must give
-    # exactly the reference's ids, ranges and 64-bit keys (scan + duplicate
-    # in Gaussian order + stable sort of (tile << 32 | depth bits)).
+def test_grouped_binning_matches_reference_order(key, degree):
+    # The production binning (depth-ordered rows, 8x8-tile groups, ballot
+    # ranking) must give exactly the reference's ids, ranges and 64-bit keys
+    # (scan + duplicate in Gaussian order + stable sort of
+    # (tile << 32 | depth bits)).
     scene = _scene(key)
-    _say(f"depth-ordered binning {key}")
+    _say(f"grouped binning {key}")
     quats, full, inverse, centers, errors, st = _project(scene, degree)
     bins = binning.bin_and_sort(st.centers, st.radii, st.tile_counts, st.depths, scene.width, scene.height,
                                 with_keys=True)
@@ -261,12 +263,18 @@ def test_depth_ordered_binning_matches_reference_order(key, degree):
     np.testing.assert_array_equal(_np(bins["ranges"]), oracle.tile_ranges(sk, T))
 
 
-def test_depth_ordered_binning_ties_and_large_rects():
+@pytest.mark.parametrize("views,n,W,H,spread", [
+    (2, 3000, 200, 120, 1.0),      # partial groups at the right/bottom edges, several chunks per group
+    (1, 40000, 128, 128, 0.15),    # crowded corner: long group lists, many 512-item chunks
+    (70, 400, 160, 160, 1.0),      # 280 groups: the group sort takes two radix passes
+    (1, 2000, 4200, 64, 1.0),      # 263 tiles across: rectangles recomputed instead of packed in the records
+])
+def test_grouped_binning_ties_and_large_rects(views, n, W, H, spread):
     # Equal depths everywhere (ties broken by Gaussian index) and rectangles
-    # spanning the whole image (the block-cooperative emission's long rows).
+    # spanning the whole image (rows touching every group).
+    _say(f"grouped binning ties views={views} n={n} {W}x{H}")
     g = torch.Generator().manual_seed(3)
-    views, n, W, H = 2, 3000, 200, 120
-    centers = (torch.rand((views, n, 2), generator=g) * torch.tensor([W, H])).to(DEV)
+    centers = (torch.rand((views, n, 2), generator=g) * spread * torch.tensor([W, H])).to(DEV)
     radii = torch.randint(1, 40, (views, n), generator=g, dtype=torch.int32)
     radii[:, ::97] = 500
     radii[:, 5::13] = 0
@@ -307,7 +315,9 @@ def test_u32_radix_sort_stable(count, end_bit):
     v = torch.empty(2 * count, dtype=torch.int32, device=DEV)
     k[:count] = torch.from_numpy(keys.view(np.int32)).to(DEV)
     v[:count] = torch.from_numpy(vals).to(DEV)
-    binning.sort_by_tile(k, v, count, 1 << (end_bit - 1) if end_bit > 1 else 1)
+    scratch = torch.empty(native.query("gs3d_sort_scratch_bytes", count), dtype=torch.uint8, device=DEV)
+    native.call("gs3d_sort_pairs_u32", native.ptr(k), native.ptr(v), count, end_bit, native.ptr(scratch),
+                scratch.numel(), native.stream(k.device))
     order = np.argsort(keys, kind="stable")
     np.testing.assert_array_equal(_np(k[:count]).view(np.uint32), keys[order])
     np.testing.assert_array_equal(_np(v[:count]), vals[order])
