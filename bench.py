@@ -38,6 +38,9 @@ def parse():
     p.add_argument("--n", type=int, default=None, help="override the Gaussian count")
     p.add_argument("--stage-reps", type=int, default=5)
     p.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
+    p.add_argument("--copy-calibration-mib", type=int, default=0,
+                   help="also run one elementwise device copy (out = in * 1) of this many MiB, the known-size "
+                        "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
     return p.parse_args()
 
 
@@ -262,6 +265,13 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1000.0 / args.steps
+    if args.copy_calibration_mib > 0:
+        src = torch.ones(args.copy_calibration_mib << 18, device=device)
+        dst = torch.empty_like(src)
+        torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: {src.numel() * 4} bytes read and written")
+        del src, dst
     log(f"[bench] {ms:.3f} ms/iter; stage timings")
     stages, by, info = stage_timings(scene, args.stage_reps)
     s13 = ("project", "order", "bin")

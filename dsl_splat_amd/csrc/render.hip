@@ -16,9 +16,10 @@
 // are identical to evaluating it.
 //
 // Backward: every lane accumulates its pixels' contributions to the current
-// Gaussian, the wavefront sums them with DPP (lane 63 holds the sums) and
-// lane 63 issues one atomic per gradient entry, instead of one per pixel as
-// in the reference.  Only batches below the largest last contributor of the
+// Gaussian; the wavefront sums all gradient entries together (permlane swaps
+// pair the entries, a DPP row butterfly finishes them) and one atomic
+// instruction adds them, one entry per lane, instead of one atomic per entry
+// and pixel as in the reference.  Only batches below the largest last contributor of the
 // tile are visited.
 #include "common.hpp"
 
@@ -288,77 +289,86 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
                 const float alpha = sel_min(0.99f, con.w * G);
                 if (!(alpha >= 1.0f / 255.0f)) continue;
                 accepted = true;
-                T[k] = T[k] / (1.0f - alpha);
+                // Gradients only need tolerance-level agreement: one hardware
+                // reciprocal (1 - alpha >= 0.01) and fused multiply-adds.
+                const float inv = __builtin_amdgcn_rcpf(1.0f - alpha);
+                T[k] = T[k] * inv;
+                const float la = last_alpha[k], keep = 1.0f - la, aT = alpha * T[k];
                 float grad_alpha = 0.0f;
 #pragma unroll
                 for (int c = 0; c < CH; ++c)
                     if (c < D) {
-                        accum[k][c] = last_alpha[k] * last_color[k][c] + (1.0f - last_alpha[k]) * accum[k][c];
+                        accum[k][c] = __builtin_fmaf(la, last_color[k][c], keep * accum[k][c]);
                         last_color[k][c] = f[c];
-                        grad_alpha += (f[c] - accum[k][c]) * grad[k][c];
-                        if (c < Dg) gfeat[c] += alpha * T[k] * grad[k][c];
+                        grad_alpha = __builtin_fmaf(f[c] - accum[k][c], grad[k][c], grad_alpha);
+                        if (c < Dg) gfeat[c] = __builtin_fmaf(aT, grad[k][c], gfeat[c]);
                     }
-                grad_alpha = grad_alpha * T[k] + (-T_final[k] / (1.0f - alpha)) * bg_grad[k];
+                grad_alpha = __builtin_fmaf(grad_alpha, T[k], -(T_final[k] * inv) * bg_grad[k]);
                 last_alpha[k] = alpha;
                 const float gv = con.w * grad_alpha;
                 const float gdx = G * dx, gdy = G * dy;
-                const float cx = gv * (-gdx * con.x - gdy * con.y);
-                const float cy = gv * (-gdy * con.z - gdx * con.y);
+                const float cx = -gv * __builtin_fmaf(gdx, con.x, gdy * con.y);
+                const float cy = -gv * __builtin_fmaf(gdy, con.z, gdx * con.y);
                 dcx += cx;
                 dcy += cy;
                 if (ABS) {
                     ax += __builtin_fabsf(cx);
                     ay += __builtin_fabsf(cy);
                 }
-                gk0 += -0.5f * gdx * dx * gv;
-                gk1 += -gdx * dy * gv;
-                gk2 += -0.5f * gdy * dy * gv;
-                gk3 += G * grad_alpha;
+                const float hgv = -0.5f * gv;
+                gk0 = __builtin_fmaf(hgv * gdx, dx, gk0);
+                gk1 = __builtin_fmaf(-gv * gdx, dy, gk1);
+                gk2 = __builtin_fmaf(hgv * gdy, dy, gk2);
+                gk3 = __builtin_fmaf(G, grad_alpha, gk3);
             }
             if (__ballot(accepted) == 0) continue;
-            // Wavefront sums (lane 63) and one atomic per entry.
-            const float s_dcx = wave_sum_to_lane63(dcx);
-            const float s_dcy = wave_sum_to_lane63(dcy);
-            const float s_k0 = wave_sum_to_lane63(gk0);
-            const float s_k1 = wave_sum_to_lane63(gk1);
-            const float s_k2 = wave_sum_to_lane63(gk2);
-            const float s_k3 = wave_sum_to_lane63(gk3);
-            float s_ax = 0.0f, s_ay = 0.0f;
+            // Wavefront sums of all gradient entries at once; one atomic
+            // instruction, each active lane adding one entry.
+            constexpr int FB = ABS ? 8 : 6;  // first feature slot
+            constexpr int NV = FB + CH;
+            constexpr int R = (NV + 3) / 4;
+            float vals[NV];
+            vals[0] = dcx;
+            vals[1] = dcy;
+            vals[2] = gk0;
+            vals[3] = gk1;
+            vals[4] = gk2;
+            vals[5] = gk3;
             if (ABS) {
-                s_ax = wave_sum_to_lane63(ax);
-                s_ay = wave_sum_to_lane63(ay);
+                vals[6] = ax;
+                vals[7] = ay;
             }
-            float s_f[CH];
 #pragma unroll
-            for (int c = 0; c < CH; ++c) s_f[c] = (c < Dg) ? wave_sum_to_lane63(gfeat[c]) : 0.0f;
-            if (lane == 63) {
+            for (int c = 0; c < CH; ++c) vals[FB + c] = gfeat[c];
+            float sums[R];
+            wave_sum_rows<NV>(vals, sums);
+            const int slot = lane & 15;
+            if (slot < R) {
+                float v = sums[0];
+#pragma unroll
+                for (int r = 1; r < R; ++r) v = (slot == r) ? sums[r] : v;
+                const int k = wave_sum_rows_value(lane);
                 const int32_t g = s_id[j];
                 const int64_t row = (int64_t)t.view * a.n + g;
-                float* gc = b.grad_centers + row * b.grad_centers_stride;
-                atomicAdd(gc, s_dcx);
-                atomicAdd(gc + 1, s_dcy);
-                float* gk = b.grad_conics + row * b.grad_conics_stride;
-                atomicAdd(gk, s_k0);
-                atomicAdd(gk + 1, s_k1);
-                atomicAdd(gk + 2, s_k2);
-                atomicAdd(gk + 3, s_k3);
-                if (ABS) {
-                    float* ab = b.abs_centers + row * b.abs_stride;
-                    atomicAdd(ab, s_ax);
-                    atomicAdd(ab + 1, s_ay);
+                float* dst = nullptr;
+                if (k < 2) {
+                    dst = b.grad_centers + row * b.grad_centers_stride + k;
+                } else if (k < 6) {
+                    dst = b.grad_conics + row * b.grad_conics_stride + (k - 2);
+                } else if (ABS && k < 8) {
+                    dst = b.abs_centers + row * b.abs_stride + (k - 6);
+                } else if (k < NV) {
+                    const int c = k - FB;
+                    if (c < a.feat_channels) {
+                        if (b.grad_features)
+                            dst = b.grad_features + t.view * b.grad_feat_view_stride + (int64_t)g * b.grad_feat_stride +
+                                  c;
+                    } else if (c < Dg && b.grad_extra) {
+                        dst = b.grad_extra + t.view * b.grad_extra_view_stride + (int64_t)g * b.grad_extra_stride +
+                              (c - a.feat_channels);
+                    }
                 }
-                if (b.grad_features) {
-                    float* gf = b.grad_features + t.view * b.grad_feat_view_stride + (int64_t)g * b.grad_feat_stride;
-#pragma unroll
-                    for (int c = 0; c < CH; ++c)
-                        if (c < a.feat_channels) atomicAdd(gf + c, s_f[c]);
-                }
-                if (b.grad_extra) {
-                    float* ge = b.grad_extra + t.view * b.grad_extra_view_stride + (int64_t)g * b.grad_extra_stride;
-#pragma unroll
-                    for (int c = 0; c < CH; ++c)
-                        if (c >= a.feat_channels && c < Dg) atomicAdd(ge + (c - a.feat_channels), s_f[c]);
-                }
+                if (dst) atomicAdd(dst, v);
             }
         }
     }
