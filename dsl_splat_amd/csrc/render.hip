@@ -90,15 +90,55 @@ GS3D_DEV float power_cutoff(float o) {
     return o <= 0.0f ? __builtin_inff() : -__builtin_inff();
 }
 
-// Stage one Gaussian's centre, conic, cutoff and channel vector.
-template <int CH>
-GS3D_DEV void stage_gaussian(const gs3d_render_args& a, int view, int32_t g, int slot, float2* s_xy, float4* s_con,
-                             float* s_cut, float* s_feat) {
+// The wavefronts of a tile each own a horizontal strip of its rows.
+template <int PIX>
+struct TileWaves {
+    static constexpr int count = kTilePixels / PIX / 64;
+    static constexpr int rows = kTile / count;
+};
+
+// Bit w is set unless every pixel of wavefront w's strip is certain to reject
+// the Gaussian: the bounding box of the ellipse {power >= cut} (its quadratic
+// form widened by 1% + 0.01, the box by 0.01 px, computed in float64) misses
+// the strip.  The margins exceed the float32 evaluation error of power
+// wherever a*c <= 100*det (correlation below 0.995); more elongated conics,
+// non-positive-definite ones and NaNs are never culled.  Rejected pairs change
+// no output, so culling leaves every result identical.
+template <int PIX>
+GS3D_DEV uint32_t strip_mask(float2 xy, float4 con, float cut, int x0, int y0) {
+    constexpr int NW = TileWaves<PIX>::count, ROWS = TileWaves<PIX>::rows;
+    constexpr uint32_t all = (1u << NW) - 1u;
+    const float q = -2.0f * cut;  // power >= cut  <=>  a dx^2 + 2 b dx dy + c dy^2 <= q
+    if (!(q > 0.0f) && q == q) return 0u;  // nothing passes the cutoff
+    const double a = con.x, b = con.y, c = con.z;
+    const double det = a * c - b * b;
+    if (!(a > 0.0 && c > 0.0 && det > 0.0 && a * c <= 100.0 * det && q < 3.0e38f)) return all;
+    const double qm = (double)q * 1.01 + 0.01;
+    const float hx = (float)__builtin_sqrt(qm * c / det) + 0.01f;
+    const float hy = (float)__builtin_sqrt(qm * a / det) + 0.01f;
+    if (xy.x + hx < (float)x0 || xy.x - hx > (float)(x0 + kTile - 1)) return 0u;
+    uint32_t m = 0u;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const float lo = (float)(y0 + w * ROWS), hi = (float)(y0 + w * ROWS + ROWS - 1);
+        if (!(xy.y + hy < lo || xy.y - hy > hi)) m |= 1u << w;
+    }
+    return m;
+}
+
+// Stage one Gaussian's centre, conic, cutoff, strip mask and channel vector.
+template <int CH, int PIX>
+GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32_t g, int slot, float2* s_xy,
+                             float4* s_con, float* s_cut, uint32_t* s_mask, float* s_feat) {
+    const int view = t.view;
     const int64_t row = (int64_t)view * a.n + g;
-    s_xy[slot] = reinterpret_cast<const float2*>(a.centers)[row];
+    const float2 xy = reinterpret_cast<const float2*>(a.centers)[row];
+    s_xy[slot] = xy;
     const float4 con = reinterpret_cast<const float4*>(a.conics)[row];
     s_con[slot] = con;
-    s_cut[slot] = power_cutoff(con.w);
+    const float cut = power_cutoff(con.w);
+    s_cut[slot] = cut;
+    s_mask[slot] = strip_mask<PIX>(xy, con, cut, t.x0, t.y0);
     float* dst = s_feat + slot * CH;
     const float* f = a.features + view * a.feat_view_stride + (int64_t)g * a.feat_stride;
     int c = 0;
@@ -117,11 +157,13 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
     __shared__ float2 s_xy[B];
     __shared__ float4 s_con[B];
     __shared__ float s_cut[B];
+    __shared__ uint32_t s_mask[B];
     __shared__ float s_feat[B * CH];
     const TileInfo t = tile_info(a);
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
     float fx[PIX], fy[PIX], T[PIX], color[PIX][CH];
-    int px[PIX], py[PIX], contributor[PIX], last_contributor[PIX];
+    int px[PIX], py[PIX], last_contributor[PIX];
     bool done[PIX];
 #pragma unroll
     for (int k = 0; k < PIX; ++k) {
@@ -133,7 +175,6 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
         fy[k] = (float)py[k];
         done[k] = !(px[k] < a.width && py[k] < a.height);
         T[k] = 1.0f;
-        contributor[k] = 0;
         last_contributor[k] = 0;
 #pragma unroll
         for (int c = 0; c < CH; ++c) color[k][c] = 0.0f;
@@ -145,39 +186,49 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
         if (__syncthreads_count(active) == 0) break;
         for (int e = threadIdx.x; e < B; e += NT) {
             const int idx = begin + e;
-            if (idx < t.last) stage_gaussian<CH>(a, t.view, a.ids[idx], e, s_xy, s_con, s_cut, s_feat);
+            if (idx < t.last) stage_gaussian<CH, PIX>(a, t, a.ids[idx], e, s_xy, s_con, s_cut, s_mask, s_feat);
         }
         __syncthreads();
         const int cnt = min(B, t.last - begin);
-        for (int j = 0; j < cnt; ++j) {
-            bool any = false;
+        bool live = true;
+        for (int c0 = 0; c0 < cnt && live; c0 += 64) {
+            // This wavefront's Gaussians of the next 64, in list order.
+            uint64_t todo = __ballot(c0 + lane < cnt && ((s_mask[min(c0 + lane, B - 1)] >> wave) & 1u));
+            while (todo) {
+                bool any = false;
 #pragma unroll
-            for (int k = 0; k < PIX; ++k) any = any || !done[k];
-            if (!any) break;
-            const float2 xy = s_xy[j];
-            const float4 con = s_con[j];
-            const float cut = s_cut[j];
-            const float* f = s_feat + j * CH;
-#pragma unroll
-            for (int k = 0; k < PIX; ++k) {
-                if (done[k]) continue;
-                ++contributor[k];
-                const float dx = xy.x - fx[k], dy = xy.y - fy[k];
-                const float power = blend_power(con.x, con.y, con.z, dx, dy);
-                if (!(power <= 0.0f) || !(power >= cut)) continue;
-                const float alpha = sel_min(0.99f, con.w * blend_exp(power));
-                if (!(alpha >= 1.0f / 255.0f)) continue;
-                const float next_t = T[k] * (1.0f - alpha);
-                if (next_t < 0.0001f) {
-                    done[k] = true;
-                    continue;
+                for (int k = 0; k < PIX; ++k) any = any || !done[k];
+                if (__ballot(any) == 0) {
+                    live = false;
+                    break;
                 }
-                const float w = alpha * T[k];
+                const int j = c0 + __builtin_ctzll(todo);
+                todo &= todo - 1;
+                const int contributor = begin - t.first + j + 1;  // list position, 1-based
+                const float2 xy = s_xy[j];
+                const float4 con = s_con[j];
+                const float cut = s_cut[j];
+                const float* f = s_feat + j * CH;
 #pragma unroll
-                for (int c = 0; c < CH; ++c)
-                    if (c < D) color[k][c] = __builtin_fmaf(f[c], w, color[k][c]);
-                T[k] = next_t;
-                last_contributor[k] = contributor[k];
+                for (int k = 0; k < PIX; ++k) {
+                    if (done[k]) continue;
+                    const float dx = xy.x - fx[k], dy = xy.y - fy[k];
+                    const float power = blend_power(con.x, con.y, con.z, dx, dy);
+                    if (!(power <= 0.0f) || !(power >= cut)) continue;
+                    const float alpha = sel_min(0.99f, con.w * blend_exp(power));
+                    if (!(alpha >= 1.0f / 255.0f)) continue;
+                    const float next_t = T[k] * (1.0f - alpha);
+                    if (next_t < 0.0001f) {
+                        done[k] = true;
+                        continue;
+                    }
+                    const float w = alpha * T[k];
+#pragma unroll
+                    for (int c = 0; c < CH; ++c)
+                        if (c < D) color[k][c] = __builtin_fmaf(f[c], w, color[k][c]);
+                    T[k] = next_t;
+                    last_contributor[k] = contributor;
+                }
             }
         }
     }
@@ -202,6 +253,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
     __shared__ float2 s_xy[B];
     __shared__ float4 s_con[B];
     __shared__ float s_cut[B];
+    __shared__ uint32_t s_mask[B];
     __shared__ int32_t s_id[B];
     __shared__ float s_feat[B * CH];
     __shared__ int s_max_last;
@@ -209,7 +261,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
     const TileInfo t = tile_info(a);
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     const int Dg = D - (a.one_tail ? 1 : 0);
-    const int lane = lane_id();
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
     float fx[PIX], fy[PIX], T[PIX], T_final[PIX], bg_grad[PIX], last_alpha[PIX];
     float grad[PIX][CH], accum[PIX][CH], last_color[PIX][CH];
     int last_contributor[PIX];
@@ -259,12 +311,17 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
             if (p >= 0) {
                 const int32_t g = a.ids[t.first + p];
                 s_id[e] = g;
-                stage_gaussian<CH>(a, t.view, g, e, s_xy, s_con, s_cut, s_feat);
+                stage_gaussian<CH, PIX>(a, t, g, e, s_xy, s_con, s_cut, s_mask, s_feat);
             }
         }
         __syncthreads();
         const int cnt = min(B, top);
-        for (int j = 0; j < cnt; ++j) {
+        for (int c0 = 0; c0 < cnt; c0 += 64) {
+          // This wavefront's Gaussians of the next 64, in traversal order.
+          uint64_t todo = __ballot(c0 + lane < cnt && ((s_mask[min(c0 + lane, B - 1)] >> wave) & 1u));
+          while (todo) {
+            const int j = c0 + __builtin_ctzll(todo);
+            todo &= todo - 1;
             const int pos = top - 1 - j;
             bool any = false;
 #pragma unroll
@@ -370,6 +427,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
                 }
                 if (dst) atomicAdd(dst, v);
             }
+          }
         }
     }
 }

@@ -184,6 +184,44 @@ def test_render_forward_bit_exact(key, degree, extra, bg):
     assert ct.max() > 0
 
 
+def test_render_culling_edge_cases():
+    # Needle-shaped Gaussians at every orientation and opacities straddling
+    # the 1/255 threshold: the per-wavefront strip culling must not change a
+    # single forward bit or the gradients.
+    _say("render culling edge cases")
+    scene = synthetic.make_scene("small", n=3000, width=136, height=100, seed=5)
+    g = torch.Generator().manual_seed(7)
+    n = scene.means.shape[0]
+    long_axis = torch.exp(torch.rand(n, generator=g) * 2.0 - 3.0)
+    thin_axis = torch.exp(torch.rand(n, generator=g) * 3.0 - 7.5)
+    scene.scales = torch.stack([long_axis, thin_axis, thin_axis], dim=1)
+    opac = torch.rand(n, generator=g)
+    opac[::3] = 1.0 / 255.0 + (torch.rand(len(opac[::3]), generator=g) - 0.5) * 2e-4
+    opac[1::7] = 0.999
+    scene.opacities = opac
+    scene = scene.to(DEV)
+    quats, full, inverse, centers, st, bins = _frame(scene, None)
+    feats = scene.features
+    out = grender.render_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats, scene.width,
+                               scene.height)
+    img, ft, ct = oracle.render_fwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]),
+                                    _np(st.centers), _np(st.conics), _np(feats))
+    np.testing.assert_array_equal(_np(out.contributors), ct)
+    np.testing.assert_array_equal(_np(out.transmittance), ft)
+    np.testing.assert_array_equal(_np(out.features), img)
+    up = torch.randn(out.features.shape, device=DEV)
+    record, gf, _ = grender.backward_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats,
+                                           out.transmittance, out.contributors, up, scene.width, scene.height,
+                                           absgrad=True)
+    ref = oracle.render_bwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]), _np(st.centers),
+                            _np(st.conics), _np(feats), _np(out.transmittance), _np(out.contributors), _np(up),
+                            absgrad=True)
+    rec = _np(record)
+    for name, got, want in (("centers", rec[..., 0:2], ref["centers"]), ("conics", rec[..., 2:6], ref["conics"]),
+                            ("abs", rec[..., 6:8], ref["abs"]), ("features", _np(gf), ref["features"])):
+        compare(name, got, want, rtol=1e-4, atol=1e-5 * max(1.0, np.abs(want).max()))
+
+
 @pytest.mark.parametrize("key,degree,absgrad", [("small_rgb", None, True), ("sh3_4view", 3, False)])
 def test_render_backward_parity(key, degree, absgrad):
     scene = _scene(key)
