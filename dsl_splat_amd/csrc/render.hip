@@ -233,14 +233,22 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
         }
     }
     const float* bg = a.background ? a.background + t.view * a.background_view_stride : nullptr;
+    const int F = a.feat_channels, E = a.extra_channels;
 #pragma unroll
     for (int k = 0; k < PIX; ++k) {
         if (!(px[k] < a.width && py[k] < a.height)) continue;
         const int64_t pix = ((int64_t)t.view * a.height + py[k]) * a.width + px[k];
-        float* out = a.image + pix * D;
 #pragma unroll
-        for (int c = 0; c < CH; ++c)
-            if (c < D) out[c] = __builtin_fmaf(T[k], (bg && c < a.feat_channels) ? bg[c] : 0.0f, color[k][c]);
+        for (int c = 0; c < CH; ++c) {
+            if (c >= D) continue;
+            const float v = __builtin_fmaf(T[k], (bg && c < F) ? bg[c] : 0.0f, color[k][c]);
+            if (c < F)
+                a.image[pix * F + c] = v;
+            else if (c < F + E)
+                a.image_extra[pix * E + (c - F)] = v;
+            else
+                a.image_alpha[pix] = v;
+        }
         a.final_t[pix] = T[k];
         a.contributors[pix] = last_contributor[k];
     }
@@ -290,13 +298,21 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
             T_final[k] = a.final_t[pix];
             T[k] = T_final[k];
             last_contributor[k] = a.contributors[pix];
-            const float* up = b.upstream + pix * D;
+            const int F = a.feat_channels, E = a.extra_channels;
 #pragma unroll
-            for (int c = 0; c < CH; ++c)
-                if (c < D) {
-                    grad[k][c] = up[c];
-                    bg_grad[k] += ((bg && c < a.feat_channels) ? bg[c] : 0.0f) * grad[k][c];
+            for (int c = 0; c < CH; ++c) {
+                if (c >= D) continue;
+                float u = 0.0f;
+                if (c < F) {
+                    if (b.upstream) u = b.upstream[pix * b.upstream_stride + c];
+                } else if (c < F + E) {
+                    if (b.upstream_extra) u = b.upstream_extra[pix * b.upstream_extra_stride + (c - F)];
+                } else if (b.upstream_alpha) {
+                    u = b.upstream_alpha[pix * b.upstream_alpha_stride];
                 }
+                grad[k][c] = u;
+                bg_grad[k] += ((bg && c < F) ? bg[c] : 0.0f) * u;
+            }
             my_max = max(my_max, last_contributor[k]);
         }
     }
@@ -476,7 +492,9 @@ extern "C" int gs3d_render_fwd(const gs3d_render_args* args, void* stream) {
     int status = gs3d::check_render_args(a);
     if (status != GS3D_OK) return status;
     if (a.views == 0) return GS3D_OK;
-    if (!a.image || !a.final_t || !a.contributors) return GS3D_ERR_ARGUMENT;
+    if ((a.feat_channels > 0 && !a.image) || (a.extra_channels > 0 && !a.image_extra) ||
+        (a.one_tail && !a.image_alpha) || !a.final_t || !a.contributors)
+        return GS3D_ERR_ARGUMENT;
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     const unsigned blocks = gs3d::render_blocks(a);
     hipStream_t s = gs3d::as_stream(stream);
@@ -494,8 +512,12 @@ extern "C" int gs3d_render_bwd(const gs3d_render_bwd_args* args, void* stream) {
     int status = gs3d::check_render_args(a);
     if (status != GS3D_OK) return status;
     if (a.views == 0) return GS3D_OK;
-    if (!a.final_t || !a.contributors || !b.upstream || !b.grad_centers || !b.grad_conics) return GS3D_ERR_ARGUMENT;
+    if (!a.final_t || !a.contributors || !b.grad_centers || !b.grad_conics) return GS3D_ERR_ARGUMENT;
     if (b.grad_centers_stride < 2 || b.grad_conics_stride < 4 || (b.abs_centers && b.abs_stride < 2))
+        return GS3D_ERR_ARGUMENT;
+    if ((b.upstream && b.upstream_stride < a.feat_channels) ||
+        (b.upstream_extra && b.upstream_extra_stride < a.extra_channels) ||
+        (b.upstream_alpha && b.upstream_alpha_stride < 1))
         return GS3D_ERR_ARGUMENT;
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     const unsigned blocks = gs3d::render_blocks(a);

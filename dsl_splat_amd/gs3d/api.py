@@ -171,20 +171,24 @@ def rasterize(
         screen_gradient_mode="projected_mean",
         tile_mode=tile_mode,
     )
-    images = []
+    planes = []
     grad_enabled = torch.is_grad_enabled()
     for b, frame in enumerate(frames):
         screen = None if training.screen is None else batch_item(training.screen, b)
         targets = training.absolute_targets[b * layout.cameras:(b + 1) * layout.cameras]
         extras = None if layout.extras is None else layout.extras.values[b]
-        image = Rasterize.apply(
+        planes.append(Rasterize.apply(
             layout.means[b], layout.quats[b], layout.scales[b], layout.opacities[b], layout.colors.values[b],
             extras, batch_item(layout.viewmats, b), screen, frame, targets, grad_enabled,
-        )
-        images.append(image)
+        ))
     shape = layout.batch_dims + (layout.cameras, height, width)
-    images = (images[0] if len(images) == 1 else torch.stack(images)).reshape(shape + (images[0].shape[-1],))
-    channels = layout.colors.channels
+
+    def gather(k):
+        items = [p[k] for p in planes]
+        out = items[0] if len(items) == 1 else torch.stack(items)
+        return out.reshape(shape + (items[0].shape[-1],))
+
+    features, alpha = gather(0), gather(2)
     if layout.extras is not None:
-        meta["render_extra_signals"] = images[..., channels:-1]
-    return RasterizationResult(images[..., :channels], images[..., -1:], meta, {})
+        meta["render_extra_signals"] = gather(1)
+    return RasterizationResult(features, alpha, meta, {})

@@ -58,7 +58,9 @@ class Rasterize(torch.autograd.Function):
         frame: Frame,
         absolute: list[AbsGradientTarget | None] | None,
         grad_enabled: bool,
-    ) -> Tensor:
+    ) -> tuple[Tensor, Tensor, Tensor]:
+        """Returns the (C,H,W,D) features, (C,H,W,E) extra (E may be 0) and
+        (C,H,W,1) alpha planes."""
         st = frame.state
         blended = st.colors if frame.sh_degree is not None else colors
         output = render.render_views(
@@ -71,14 +73,21 @@ class Rasterize(torch.autograd.Function):
             ctx.frame = frame
             ctx.absolute = absolute
         ctx.set_materialize_grads(False)
-        return output.features
+        extra = output.extra
+        if extra is None:
+            extra = output.features.new_empty(output.features.shape[:-1] + (0,))
+            ctx.mark_non_differentiable(extra)
+        return output.features, extra, output.alpha
 
     @staticmethod
     @once_differentiable
-    def backward(ctx: Any, gradient: Tensor | None) -> tuple[Tensor | None, ...]:
+    def backward(ctx: Any, grad_features: Tensor | None, grad_extra_image: Tensor | None,
+                 grad_alpha: Tensor | None) -> tuple[Tensor | None, ...]:
         none = (None,) * 11
-        if gradient is None:
+        if grad_features is None and grad_extra_image is None and grad_alpha is None:
             return none
+        if grad_extra_image is not None and grad_extra_image.numel() == 0:
+            grad_extra_image = None
         means, quats, scales, opacities, colors, extra, viewmats, final_t, contributors = ctx.saved_tensors
         frame: Frame = ctx.frame
         st = frame.state
@@ -87,7 +96,8 @@ class Rasterize(torch.autograd.Function):
         blended = st.colors if sh else colors
         absgrad = ctx.absolute is not None and any(t is not None for t in ctx.absolute)
         record, grad_blended, grad_extra = render.backward_views(
-            frame.ranges, frame.ids, st.centers, st.conics, blended, final_t, contributors, gradient,
+            frame.ranges, frame.ids, st.centers, st.conics, blended, final_t, contributors,
+            (grad_features, grad_extra_image, grad_alpha),
             frame.width, frame.height, extra=extra, background=frame.background, one_tail=True,
             absgrad=absgrad, need_features=sh or needs[4], need_extra=needs[5],
         )

@@ -90,16 +90,18 @@ class _Pixels(torch.autograd.Function):
                                   out.contributors)
             ctx.config = config
         ctx.set_materialize_grads(False)
-        return out.features[0]
+        return out.features[0], out.alpha[0]
 
     @staticmethod
     @once_differentiable
-    def backward(ctx: Any, gradient: Tensor | None):
-        if gradient is None:
+    def backward(ctx: Any, grad_features: Tensor | None, grad_alpha: Tensor | None):
+        if grad_features is None and grad_alpha is None:
             return (None,) * 9
         centers, conics, features, ranges, ids, background, final_t, contributors = ctx.saved_tensors
+        upstream = (None if grad_features is None else grad_features[None], None,
+                    None if grad_alpha is None else grad_alpha[None])
         record, gf, _ = render.backward_views(
-            ranges, ids, centers[None], conics[None], features, final_t, contributors, gradient[None],
+            ranges, ids, centers[None], conics[None], features, final_t, contributors, upstream,
             ctx.config.width, ctx.config.height, background=None if background is None else background[None],
             one_tail=True, need_features=ctx.needs_input_grad[2])
         grads = (record[0, :, 0:2], record[0, :, 2:6], gf)
@@ -151,9 +153,10 @@ def rasterize_to_pixels(geometry: GaussianGeometry, tiles: GaussianTiles, featur
             raise NotImplementedError("background gradients are not supported")
     if statistics:
         raise NotImplementedError("contribution statistics are not implemented in the HIP rasterizer yet")
-    image = _Pixels.apply(geometry.centers, geometry.conics, features.contiguous(), geometry.radii, tiles.ranges,
-                          tiles.gaussian_ids, background, geometry._config, torch.is_grad_enabled())
-    return PixelResult(image[..., :channels], image[..., -1:], {})
+    image, alpha = _Pixels.apply(geometry.centers, geometry.conics, features.contiguous(), geometry.radii,
+                                 tiles.ranges, tiles.gaussian_ids, background, geometry._config,
+                                 torch.is_grad_enabled())
+    return PixelResult(image, alpha, {})
 
 
 __all__ = [

@@ -3,8 +3,12 @@ reference) over gs3d_render_fwd / gs3d_render_bwd, for all views at once.
 
 The blended vector of a Gaussian is [features | extra | 1] (the constant
 alpha channel of gs3d/autograd.py:41-46) assembled inside the kernel from
-its sources, so no concatenated copy is made; images come out channel-last
-(C, H, W, D').  Backward gradients of centres/conics/abs-centres share one
+its sources, so no concatenated copy is made.  The image comes out as the
+planes the reference returns after its split (gs3d/api.py:256-265):
+features (C,H,W,D), extra (C,H,W,E) and alpha (C,H,W,1), each contiguous, and
+the backward reads the upstream gradient of each plane where it lies (any
+pixel stride), so autograd never reassembles a full-image gradient.
+Backward gradients of centres/conics/abs-centres share one
 (C, N, 8) record per Gaussian (centre xy, conic a b c, opacity, |centre| xy)
 so a wavefront's atomics for one Gaussian land in one 32-byte row.
 """
@@ -22,9 +26,29 @@ RECORD = 8  # floats per Gaussian in the gradient record
 
 @dataclass(slots=True)
 class RenderedPixels:
-    features: Tensor       # (C, H, W, D') channel-last
+    features: Tensor       # (C, H, W, D) channel-last
+    extra: Tensor | None   # (C, H, W, E) or None
+    alpha: Tensor | None   # (C, H, W, 1) when the constant alpha channel is blended
     transmittance: Tensor  # (C, H, W)
     contributors: Tensor   # (C, H, W) int32
+
+    def stacked(self) -> Tensor:
+        """All blended channels as one (C, H, W, D') tensor, [features | extra | alpha]."""
+        return torch.cat([p for p in (self.features, self.extra, self.alpha) if p is not None], dim=-1)
+
+
+def _plane(grad: Tensor | None, views: int, height: int, width: int, channels: int):
+    """(tensor, pixel stride) of an upstream gradient plane with contiguous
+    channels and a uniform pixel stride (copied only when it has neither)."""
+    if grad is None or channels == 0:
+        return None, 0
+    t = grad.reshape(views, height, width, channels)
+    s = t.stride(2)
+    if (channels > 1 and t.stride(3) != 1) or s < channels or t.stride(1) != width * s or \
+            t.stride(0) != height * width * s:
+        t = t.contiguous()
+        s = channels
+    return t, s
 
 
 def _source(values: Tensor | None, views: int, n: int):
@@ -74,23 +98,29 @@ def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, f
     keep = []
     a, channels = _args(width, height, views, n, ranges, ids, centers, conics, features, extra, background,
                         one_tail, keep)
+    f32 = dict(dtype=torch.float32, device=device)
     out = RenderedPixels(
-        torch.empty((views, height, width, channels), dtype=torch.float32, device=device),
-        torch.empty((views, height, width), dtype=torch.float32, device=device),
+        torch.empty((views, height, width, a.feat_channels), **f32),
+        torch.empty((views, height, width, a.extra_channels), **f32) if a.extra_channels else None,
+        torch.empty((views, height, width, 1), **f32) if one_tail else None,
+        torch.empty((views, height, width), **f32),
         torch.empty((views, height, width), dtype=torch.int32, device=device),
     )
     a.image, a.final_t, a.contributors = (native.ptr(out.features), native.ptr(out.transmittance),
                                           native.ptr(out.contributors))
+    a.image_extra, a.image_alpha = native.ptr(out.extra), native.ptr(out.alpha)
     native.call("gs3d_render_fwd", ctypes.byref(a), native.stream(device))
     return out
 
 
 @torch.no_grad()
 def backward_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, features: Tensor,
-                   final_t: Tensor, contributors: Tensor, upstream: Tensor, width: int, height: int, *,
+                   final_t: Tensor, contributors: Tensor, upstream, width: int, height: int, *,
                    extra: Tensor | None = None, background: Tensor | None = None, one_tail: bool = True,
                    absgrad: bool = False, need_features: bool = True, need_extra: bool = True):
-    """Returns (record (C,N,8), grad_features like features or None,
+    """``upstream`` is either the (grad features, grad extra, grad alpha)
+    planes (each may be None) or one (C,H,W,D') tensor of all channels.
+    Returns (record (C,N,8), grad_features like features or None,
     grad_extra like extra or None)."""
     views, n = centers.shape[0], centers.shape[1]
     device = centers.device
@@ -98,12 +128,20 @@ def backward_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor,
     a, channels = _args(width, height, views, n, ranges, ids, centers, conics, features, extra, background,
                         one_tail, keep)
     final_t, contributors = final_t.contiguous(), contributors.contiguous()
-    upstream = upstream.reshape(views, height, width, channels).contiguous()
-    keep += [final_t, contributors, upstream]
+    fc, ec = a.feat_channels, a.extra_channels
+    if isinstance(upstream, Tensor):
+        full = upstream.reshape(views, height, width, channels)
+        upstream = (full[..., :fc], full[..., fc:fc + ec] if ec else None, full[..., -1:] if one_tail else None)
+    gf_plane, gf_stride = _plane(upstream[0], views, height, width, fc)
+    ge_plane, ge_stride = _plane(upstream[1], views, height, width, ec)
+    ga_plane, ga_stride = _plane(upstream[2] if one_tail else None, views, height, width, 1)
+    keep += [final_t, contributors, gf_plane, ge_plane, ga_plane]
     a.final_t, a.contributors = native.ptr(final_t), native.ptr(contributors)
     b = abi.RenderBwdArgs()
     b.fwd = a
-    b.upstream = native.ptr(upstream)
+    b.upstream, b.upstream_stride = native.ptr(gf_plane), gf_stride
+    b.upstream_extra, b.upstream_extra_stride = native.ptr(ge_plane), ge_stride
+    b.upstream_alpha, b.upstream_alpha_stride = native.ptr(ga_plane), ga_stride
     record = torch.zeros((views, n, RECORD), dtype=torch.float32, device=device)
     b.grad_centers, b.grad_centers_stride = native.ptr(record), RECORD
     b.grad_conics, b.grad_conics_stride = native.ptr(record, 2), RECORD

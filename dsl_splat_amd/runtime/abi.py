@@ -9,7 +9,7 @@ import ctypes
 c_float_p = ctypes.POINTER(ctypes.c_float)
 c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 GS3D_OK = 0
 GS3D_ERR_ARGUMENT = -1
@@ -167,6 +167,8 @@ class RenderArgs(ctypes.Structure):
         ("background", _P),
         ("background_view_stride", ctypes.c_int64),
         ("image", _P),
+        ("image_extra", _P),
+        ("image_alpha", _P),
         ("final_t", _P),
         ("contributors", _P),
     ]
@@ -176,6 +178,11 @@ class RenderBwdArgs(ctypes.Structure):
     _fields_ = [
         ("fwd", RenderArgs),
         ("upstream", _P),
+        ("upstream_stride", ctypes.c_int64),
+        ("upstream_extra", _P),
+        ("upstream_extra_stride", ctypes.c_int64),
+        ("upstream_alpha", _P),
+        ("upstream_alpha_stride", ctypes.c_int64),
         ("grad_centers", _P),
         ("grad_centers_stride", ctypes.c_int64),
         ("grad_conics", _P),

@@ -295,7 +295,10 @@ int gs3d_sort_pairs_u32(uint32_t* keys, int32_t* values, int64_t count,
  * is [features (feat_channels) | extra (extra_channels) | 1.0 if one_tail],
  * D' channels in all; background covers the feature channels only (the rest
  * are zero), as gs3d/autograd.py:41-50 builds it.
- * image is written channel-last (views,H,W,D').
+ * The blended image is written as up to three channel-last planes, the
+ * layout the reference returns after its HWC split (gs3d/api.py:256-265):
+ * image (views,H,W,feat_channels), image_extra (views,H,W,extra_channels)
+ * and, with one_tail, image_alpha (views,H,W).
  * ---------------------------------------------------------------------- */
 typedef struct gs3d_render_args {
     int32_t width, height, views;
@@ -314,7 +317,9 @@ typedef struct gs3d_render_args {
     int32_t one_tail;          /* 1 appends the constant alpha channel */
     const float* background;   /* (views, feat_channels) rows, may be NULL */
     int64_t background_view_stride;
-    float* image;              /* (views,H,W,D') */
+    float* image;              /* (views,H,W,feat_channels) */
+    float* image_extra;        /* (views,H,W,extra_channels); NULL when extra_channels == 0 */
+    float* image_alpha;        /* (views,H,W); NULL unless one_tail */
     float* final_t;            /* (views,H,W) */
     int32_t* contributors;     /* (views,H,W) */
 } gs3d_render_args;
@@ -327,11 +332,19 @@ int gs3d_render_fwd(const gs3d_render_args* args, void* stream);
  * atomics (the caller zeroes them); a wavefront reduces its 64 pixels'
  * contributions to one Gaussian before the atomic.  grad_features and
  * grad_extra honour their view strides (0 = summed over views).  Any
- * gradient pointer may be NULL except grad_centers/grad_conics.
+ * gradient pointer may be NULL except grad_centers/grad_conics.  The
+ * upstream gradient arrives in the planes of the forward output, each with
+ * its own pixel stride (floats between pixels, channels contiguous); a NULL
+ * plane is a zero gradient.
  * ---------------------------------------------------------------------- */
 typedef struct gs3d_render_bwd_args {
-    gs3d_render_args fwd;        /* same inputs; image unused */
-    const float* upstream;       /* (views,H,W,D') channel-last dL/dimage */
+    gs3d_render_args fwd;        /* same inputs; image planes unused */
+    const float* upstream;       /* dL/dimage, feat_channels per pixel */
+    int64_t upstream_stride;
+    const float* upstream_extra; /* dL/dimage_extra, extra_channels per pixel */
+    int64_t upstream_extra_stride;
+    const float* upstream_alpha; /* dL/dimage_alpha, one per pixel */
+    int64_t upstream_alpha_stride;
     float* grad_centers;         /* (views,N,*) rows of grad_centers_stride */
     int64_t grad_centers_stride;
     float* grad_conics;          /* (views,N,*) rows of grad_conics_stride */

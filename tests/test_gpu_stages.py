@@ -180,7 +180,7 @@ def test_render_forward_bit_exact(key, degree, extra, bg):
                                     background=None if background is None else _np(background))
     np.testing.assert_array_equal(_np(out.contributors), ct)
     np.testing.assert_array_equal(_np(out.transmittance), ft)
-    np.testing.assert_array_equal(_np(out.features), img)
+    np.testing.assert_array_equal(_np(out.stacked()), img)
     assert ct.max() > 0
 
 
@@ -208,8 +208,8 @@ def test_render_culling_edge_cases():
                                     _np(st.centers), _np(st.conics), _np(feats))
     np.testing.assert_array_equal(_np(out.contributors), ct)
     np.testing.assert_array_equal(_np(out.transmittance), ft)
-    np.testing.assert_array_equal(_np(out.features), img)
-    up = torch.randn(out.features.shape, device=DEV)
+    np.testing.assert_array_equal(_np(out.stacked()), img)
+    up = torch.randn(out.stacked().shape, device=DEV)
     record, gf, _ = grender.backward_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats,
                                            out.transmittance, out.contributors, up, scene.width, scene.height,
                                            absgrad=True)
@@ -232,7 +232,7 @@ def test_render_backward_parity(key, degree, absgrad):
     background = torch.rand((views, 3), device=DEV)
     out = grender.render_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats, scene.width,
                                scene.height, background=background)
-    up = torch.randn(out.features.shape, device=DEV)
+    up = torch.randn(out.stacked().shape, device=DEV)
     record, gf, _ = grender.backward_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats,
                                            out.transmittance, out.contributors, up, scene.width, scene.height,
                                            background=background, absgrad=absgrad)
