@@ -409,7 +409,9 @@ __global__ __launch_bounds__(kProjBlock) void project_fwd_kernel(gs3d_project_ar
         for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
         opac = a.opacities[i];
     }
-    float coef[L::regs];
+    // Coefficients are read from the LDS staging (odd pitch: conflict-free)
+    // where they are used, which keeps them out of registers.
+    const float* coef = s_sh + threadIdx.x * L::pad;
     const int count = (int)min((int64_t)kProjBlock, (int64_t)n - base);
     for (int v = 0; v < a.views; ++v) {
         if constexpr (DEG >= 0) {
@@ -418,8 +420,6 @@ __global__ __launch_bounds__(kProjBlock) void project_fwd_kernel(gs3d_project_ar
                 const int rf = a.sh_rows * 3;
                 stage_rows_in<kProjBlock>(a.sh + v * a.sh_view_stride + base * rf, count, rf, L::need, s_sh, L::pad);
                 __syncthreads();
-#pragma unroll
-                for (int e = 0; e < L::need; ++e) coef[e] = s_sh[threadIdx.x * L::pad + e];
             }
         }
         if (!valid) continue;
@@ -608,8 +608,9 @@ GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, 
     }
 }
 
-template <int DEG>
-__global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bwd_args a, int want_camera) {
+template <int DEG, bool CAM>
+__global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bwd_args a) {
+    constexpr bool want_camera = CAM;
     using L = ShLayout<DEG>;
     __shared__ float s_sh[L::lds];
     // Wave-private camera accumulators: [wave][view][entry].
@@ -617,7 +618,7 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = a.n;
     const int views = a.views;
-    if (want_camera) {
+    if constexpr (want_camera) {
         for (int e = threadIdx.x; e < (kProjBlock / 64) * kMaxViewsCamLds * kCamEntries; e += kProjBlock)
             (&s_cam[0][0][0])[e] = 0.0f;
     }
@@ -639,7 +640,7 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
             for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
         }
         float gm[3] = {0, 0, 0}, gq[4] = {0, 0, 0, 0}, gs[3] = {0, 0, 0}, go = 0.0f;
-        float coef[L::regs];
+        const float* coef = s_sh + threadIdx.x * L::pad;  // read from the LDS staging where used
         float gco[L::regs];
 #pragma unroll
         for (int e = 0; e < L::regs; ++e) gco[e] = 0.0f;
@@ -650,8 +651,6 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
                     stage_rows_in<kProjBlock>(a.sh + v * a.sh_view_stride + base * rf, count, rf, L::need, s_sh,
                                               L::pad);
                     __syncthreads();
-#pragma unroll
-                    for (int e = 0; e < L::need; ++e) coef[e] = s_sh[threadIdx.x * L::pad + e];
                 }
             }
             const int64_t row = (int64_t)v * n + i;
@@ -745,7 +744,7 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
             }
         }
     }
-    if (want_camera) {
+    if constexpr (want_camera) {
         __syncthreads();
         const int total = views * kCamEntries;
         for (int e = threadIdx.x; e < total; e += kProjBlock) {
@@ -845,7 +844,10 @@ int launch_project_bwd(const gs3d_project_bwd_args& a, int want_camera, hipStrea
     const int64_t needed = blocks_for(a.n, kProjBlock);
     const int64_t persistent = (int64_t)cus * 8;
     const dim3 grid((unsigned)(needed < persistent ? needed : persistent));
-    hipLaunchKernelGGL((project_bwd_kernel<DEG>), grid, dim3(kProjBlock), 0, stream, a, want_camera);
+    if (want_camera)
+        hipLaunchKernelGGL((project_bwd_kernel<DEG, true>), grid, dim3(kProjBlock), 0, stream, a);
+    else
+        hipLaunchKernelGGL((project_bwd_kernel<DEG, false>), grid, dim3(kProjBlock), 0, stream, a);
     return launch_status("gs3d_project_bwd");
 }
 

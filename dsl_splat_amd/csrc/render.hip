@@ -320,6 +320,43 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
     if (my_max > 0) atomicMax(&s_max_last, my_max);
     __syncthreads();
     const int max_last = min(s_max_last, t.last - t.first);
+    // Gradient entry this lane adds after the wavefront sums (see
+    // wave_sum_rows): entry k of Gaussian g lives at dst_base + g * dst_step.
+    constexpr int FB = ABS ? 8 : 6;  // first feature entry
+    constexpr int NV = FB + CH;
+    constexpr int R = (NV + 3) / 4;
+    float* dst_base = nullptr;
+    int64_t dst_step = 0;
+    {
+        const int k = wave_sum_rows_value(lane);
+        const int64_t row0 = (int64_t)t.view * a.n;
+        if ((lane & 15) >= R || k >= NV) {
+        } else if (k < 2) {
+            dst_base = b.grad_centers + row0 * b.grad_centers_stride + k;
+            dst_step = b.grad_centers_stride;
+        } else if (k < 6) {
+            dst_base = b.grad_conics + row0 * b.grad_conics_stride + (k - 2);
+            dst_step = b.grad_conics_stride;
+        } else if (ABS && k < 8) {
+            dst_base = b.abs_centers + row0 * b.abs_stride + (k - 6);
+            dst_step = b.abs_stride;
+        } else {
+            const int c = k - FB;
+            if (c < a.feat_channels) {
+                if (b.grad_features) {
+                    dst_base = b.grad_features + t.view * b.grad_feat_view_stride + c;
+                    dst_step = b.grad_feat_stride;
+                }
+            } else if (c < Dg && b.grad_extra) {
+                dst_base = b.grad_extra + t.view * b.grad_extra_view_stride + (c - a.feat_channels);
+                dst_step = b.grad_extra_stride;
+            }
+        }
+    }
+    // Largest last contributor among this wavefront's pixels (wave-uniform).
+    int wave_last = my_max;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) wave_last = max(wave_last, __shfl_xor(wave_last, d, 64));
     for (int top = max_last; top > 0; top -= B) {
         __syncthreads();
         for (int e = threadIdx.x; e < B; e += NT) {
@@ -333,8 +370,10 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
         __syncthreads();
         const int cnt = min(B, top);
         for (int c0 = 0; c0 < cnt; c0 += 64) {
-          // This wavefront's Gaussians of the next 64, in traversal order.
-          uint64_t todo = __ballot(c0 + lane < cnt && ((s_mask[min(c0 + lane, B - 1)] >> wave) & 1u));
+          // This wavefront's Gaussians of the next 64 that lie before its
+          // pixels' last contributors, in traversal order.
+          const int e = c0 + lane;
+          uint64_t todo = __ballot(e < cnt && top - 1 - e < wave_last && ((s_mask[min(e, B - 1)] >> wave) & 1u));
           while (todo) {
             const int j = c0 + __builtin_ctzll(todo);
             todo &= todo - 1;
@@ -397,9 +436,6 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
             if (__ballot(accepted) == 0) continue;
             // Wavefront sums of all gradient entries at once; one atomic
             // instruction, each active lane adding one entry.
-            constexpr int FB = ABS ? 8 : 6;  // first feature slot
-            constexpr int NV = FB + CH;
-            constexpr int R = (NV + 3) / 4;
             float vals[NV];
             vals[0] = dcx;
             vals[1] = dcy;
@@ -415,33 +451,12 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
             for (int c = 0; c < CH; ++c) vals[FB + c] = gfeat[c];
             float sums[R];
             wave_sum_rows<NV>(vals, sums);
-            const int slot = lane & 15;
-            if (slot < R) {
+            if (dst_base) {
+                const int slot = lane & 15;
                 float v = sums[0];
 #pragma unroll
                 for (int r = 1; r < R; ++r) v = (slot == r) ? sums[r] : v;
-                const int k = wave_sum_rows_value(lane);
-                const int32_t g = s_id[j];
-                const int64_t row = (int64_t)t.view * a.n + g;
-                float* dst = nullptr;
-                if (k < 2) {
-                    dst = b.grad_centers + row * b.grad_centers_stride + k;
-                } else if (k < 6) {
-                    dst = b.grad_conics + row * b.grad_conics_stride + (k - 2);
-                } else if (ABS && k < 8) {
-                    dst = b.abs_centers + row * b.abs_stride + (k - 6);
-                } else if (k < NV) {
-                    const int c = k - FB;
-                    if (c < a.feat_channels) {
-                        if (b.grad_features)
-                            dst = b.grad_features + t.view * b.grad_feat_view_stride + (int64_t)g * b.grad_feat_stride +
-                                  c;
-                    } else if (c < Dg && b.grad_extra) {
-                        dst = b.grad_extra + t.view * b.grad_extra_view_stride + (int64_t)g * b.grad_extra_stride +
-                              (c - a.feat_channels);
-                    }
-                }
-                if (dst) atomicAdd(dst, v);
+                atomicAdd(dst_base + (int64_t)s_id[j] * dst_step, v);
             }
           }
         }
