@@ -87,30 +87,47 @@ __global__ __launch_bounds__(1024) void scan_partials_kernel(int64_t* __restrict
     if (threadIdx.x == 0 && total_out) *total_out = carry;
 }
 
-// Per-tile scan with the tile's prefix; blocked layout per thread (16
-// consecutive elements) so each thread writes a contiguous run.
+// Per-tile scan with the tile's prefix.  Loads and stores are striped
+// across the block (coalesced) and transposed through LDS so that each thread
+// scans 16 consecutive elements; the LDS index e + e/16 keeps both the
+// striped and the per-thread accesses free of bank conflicts.
+GS3D_DEV int scan_lds_index(int e) { return e + (e >> 4); }
+
 template <class In, bool INCLUSIVE>
 __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const In* __restrict__ in, int64_t n,
                                                                  const int64_t* __restrict__ partials,
                                                                  int32_t* __restrict__ out) {
     __shared__ int64_t s_wave[kScanThreads / 64];
-    const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+    __shared__ int32_t s_tile[kScanTile + kScanTile / 16];
+    const int64_t base = (int64_t)blockIdx.x * kScanTile;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        const int e = k * kScanThreads + threadIdx.x;
+        const int64_t idx = base + e;
+        s_tile[scan_lds_index(e)] = idx < n ? (int32_t)in[idx] : 0;
+    }
+    __syncthreads();
     int32_t vals[kScanItems];
     int64_t sum = 0;
 #pragma unroll
     for (int k = 0; k < kScanItems; ++k) {
-        const int64_t idx = base + k;
-        vals[k] = idx < n ? (int32_t)in[idx] : 0;
+        vals[k] = s_tile[scan_lds_index(threadIdx.x * kScanItems + k)];
         sum += vals[k];
     }
     int64_t total;
     int64_t run = block_exclusive_scan<kScanThreads>(sum, s_wave, total) + partials[blockIdx.x];
 #pragma unroll
     for (int k = 0; k < kScanItems; ++k) {
-        const int64_t idx = base + k;
         if (INCLUSIVE) run += vals[k];
-        if (idx < n) out[idx] = (int32_t)run;
+        s_tile[scan_lds_index(threadIdx.x * kScanItems + k)] = (int32_t)run;
         if (!INCLUSIVE) run += vals[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        const int e = k * kScanThreads + threadIdx.x;
+        const int64_t idx = base + e;
+        if (idx < n) out[idx] = s_tile[scan_lds_index(e)];
     }
 }
 
