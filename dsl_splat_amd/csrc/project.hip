@@ -458,13 +458,13 @@ __global__ __launch_bounds__(kProjBlock) void project_fwd_kernel(gs3d_project_ar
 }
 
 // ---------------------------------------------------------------------------
-// Backward.  Persistent grid-stride loop over blocks of Gaussians; camera
-// gradients (view rows 0-2, projection rows 0,1,3 and SH camera centres) are
-// reduced per wavefront with DPP each iteration into wave-private LDS
-// accumulators, and summed over the block once at the end (one atomic per
-// block and entry).
+// Backward: two persistent grid-stride kernels over blocks of Gaussians, the
+// projection VJP and the SH VJP, each with a modest register and LDS
+// footprint.  Camera gradients (view rows 0-2, projection rows 0,1,3, SH
+// camera centres) are reduced per wavefront with DPP each iteration into
+// wave-private LDS accumulators and summed over the block once at the end
+// (one atomic per block and entry).
 // ---------------------------------------------------------------------------
-constexpr int kCamEntries = 12 + 12 + 3;  // view rows 0-2, proj rows 0,1,3, centre
 constexpr int kMaxViewsCamLds = 16;
 
 struct VJP {
@@ -608,25 +608,22 @@ GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, 
     }
 }
 
-template <int DEG, bool CAM>
+// Projection VJP, all views of a Gaussian per thread.
+template <bool CAM>
 __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bwd_args a) {
-    constexpr bool want_camera = CAM;
-    using L = ShLayout<DEG>;
-    __shared__ float s_sh[L::lds];
-    // Wave-private camera accumulators: [wave][view][entry].
-    __shared__ float s_cam[kProjBlock / 64][kMaxViewsCamLds][kCamEntries];
+    // Wave-private camera accumulators: [wave][view][entry] (view and
+    // projection rows; the SH camera centre is handled by sh_views_bwd_kernel).
+    __shared__ float s_cam[CAM ? kProjBlock / 64 : 1][kMaxViewsCamLds][24];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = a.n;
     const int views = a.views;
-    if constexpr (want_camera) {
-        for (int e = threadIdx.x; e < (kProjBlock / 64) * kMaxViewsCamLds * kCamEntries; e += kProjBlock)
+    if constexpr (CAM) {
+        for (int e = threadIdx.x; e < (kProjBlock / 64) * kMaxViewsCamLds * 24; e += kProjBlock)
             (&s_cam[0][0][0])[e] = 0.0f;
     }
-    const int rf = a.sh_rows * 3;
     for (int64_t base = (int64_t)blockIdx.x * kProjBlock; base < n; base += (int64_t)gridDim.x * kProjBlock) {
         const int64_t i = base + threadIdx.x;
         const bool valid = i < n;
-        const int count = (int)min((int64_t)kProjBlock, (int64_t)n - base);
         float mean[3] = {0, 0, 0}, q[4] = {1, 0, 0, 0}, s[3] = {1, 1, 1};
         if (valid) {
 #pragma unroll
@@ -640,25 +637,10 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
             for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
         }
         float gm[3] = {0, 0, 0}, gq[4] = {0, 0, 0, 0}, gs[3] = {0, 0, 0}, go = 0.0f;
-        const float* coef = s_sh + threadIdx.x * L::pad;  // read from the LDS staging where used
-        float gco[L::regs];
-#pragma unroll
-        for (int e = 0; e < L::regs; ++e) gco[e] = 0.0f;
         for (int v = 0; v < views; ++v) {
-            if constexpr (DEG >= 0) {
-                if (v == 0 || a.sh_view_stride != 0) {
-                    __syncthreads();
-                    stage_rows_in<kProjBlock>(a.sh + v * a.sh_view_stride + base * rf, count, rf, L::need, s_sh,
-                                              L::pad);
-                    __syncthreads();
-                }
-            }
             const int64_t row = (int64_t)v * n + i;
             const bool vis = valid && a.radii[row] > 0;
             VJP g;
-            float cam[kCamEntries];
-#pragma unroll
-            for (int e = 0; e < kCamEntries; ++e) cam[e] = 0.0f;
             if (vis) {
                 const float* gcp = a.grad_centers + row * a.grad_centers_stride;
                 const float* gkp = a.grad_conics + row * a.grad_conics_stride;
@@ -673,53 +655,20 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
 #pragma unroll
                 for (int k = 0; k < 3; ++k) gs[k] += g.scale[k];
                 go += g.opacity;
-#pragma unroll
-                for (int r = 0; r < 3; ++r)
-#pragma unroll
-                    for (int cc = 0; cc < 4; ++cc) {
-                        cam[4 * r + cc] = g.view[r][cc];
-                        cam[12 + 4 * r + cc] = g.proj[r][cc];
-                    }
             }
-            if constexpr (DEG >= 0) {
-                if (valid) {
-                    float dir[3] = {0.0f, 0.0f, 0.0f};
-                    if (DEG > 0) {
+            if constexpr (CAM) {
+                if (v < kMaxViewsCamLds) {
 #pragma unroll
-                        for (int k = 0; k < 3; ++k) dir[k] = mean[k] - a.camera_centers[3 * v + k];
-                    }
-                    float color[3], raw[3];
-                    sh_eval<DEG>(coef, dir, vis, color, raw);
-                    const bool act[3] = {vis && raw[0] >= 0.0f, vis && raw[1] >= 0.0f, vis && raw[2] >= 0.0f};
-                    const float* gcol = a.grad_colors + row * a.grad_colors_stride;
-                    const float up[3] = {gcol[0], gcol[1], gcol[2]};
-                    float gd[3];
-                    sh_backward<DEG, true>(coef, dir, vis, act, up, gco, gd);
-                    if (DEG > 0) {
+                    for (int r = 0; r < 3; ++r)
 #pragma unroll
-                        for (int k = 0; k < 3; ++k) {
-                            gm[k] += gd[k];
-                            cam[24 + k] = -gd[k];
+                        for (int cc = 0; cc < 4; ++cc) {
+                            const float sv = wave_sum_to_lane63(vis ? g.view[r][cc] : 0.0f);
+                            const float sp = wave_sum_to_lane63(vis ? g.proj[r][cc] : 0.0f);
+                            if (lane == 63) {
+                                s_cam[wave][v][4 * r + cc] += sv;
+                                s_cam[wave][v][12 + 4 * r + cc] += sp;
+                            }
                         }
-                    }
-                }
-                if (a.sh_view_stride != 0 && a.grad_sh) {
-                    // Per-view coefficients: write this view's gradient block.
-                    __syncthreads();
-#pragma unroll
-                    for (int e = 0; e < L::need; ++e) s_sh[threadIdx.x * L::pad + e] = gco[e];
-                    __syncthreads();
-                    stage_rows_out<kProjBlock>(a.grad_sh + v * a.sh_view_stride + base * rf, count, rf, L::need, s_sh,
-                                               L::pad);
-#pragma unroll
-                    for (int e = 0; e < L::regs; ++e) gco[e] = 0.0f;
-                }
-            }
-            if (want_camera && v < kMaxViewsCamLds) {
-#pragma unroll
-                for (int e = 0; e < kCamEntries; ++e) {
-                    const float sum = wave_sum_to_lane63(cam[e]);
-                    if (lane == 63) s_cam[wave][v][e] += sum;
                 }
             }
         }
@@ -734,40 +683,240 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
                 for (int k = 0; k < 3; ++k) a.grad_scales[3 * i + k] = gs[k];
             if (a.grad_opacities) a.grad_opacities[i] = go;
         }
-        if constexpr (DEG >= 0) {
-            if (a.sh_view_stride == 0 && a.grad_sh) {
-                __syncthreads();
-#pragma unroll
-                for (int e = 0; e < L::need; ++e) s_sh[threadIdx.x * L::pad + e] = gco[e];
-                __syncthreads();
-                stage_rows_out<kProjBlock>(a.grad_sh + base * rf, count, rf, L::need, s_sh, L::pad);
-            }
-        }
     }
-    if constexpr (want_camera) {
+    if constexpr (CAM) {
         __syncthreads();
-        const int total = views * kCamEntries;
+        const int total = views * 24;
         for (int e = threadIdx.x; e < total; e += kProjBlock) {
-            const int v = e / kCamEntries, k = e - v * kCamEntries;
+            const int v = e / 24, k = e - v * 24;
             float sum = 0.0f;
 #pragma unroll
             for (int w = 0; w < kProjBlock / 64; ++w) sum += s_cam[w][v][k];
             if (k < 12) {
                 if (a.grad_view) atomicAdd(a.grad_view + 16 * v + k, sum);
-            } else if (k < 24) {
+            } else {
                 const int r = (k - 12) >> 2, c = (k - 12) & 3;
                 const int prow = r == 2 ? 3 : r;
                 if (a.grad_projection) atomicAdd(a.grad_projection + 16 * v + 4 * prow + c, sum);
-            } else if (a.grad_camera_centers) {
-                atomicAdd(a.grad_camera_centers + 3 * v + (k - 24), sum);
             }
         }
     }
 }
 
-// ---------------------------------------------------------------------------
-// Standalone SH and metadata kernels (used by the staged ops API).
-// ---------------------------------------------------------------------------
+// SH VJP (primitives/sh.py:82-138 with the "means - camera centre" VJP of
+// gs3d/api.py:160-164) over all views, one lane per (Gaussian, colour
+// channel): 21 Gaussians per wavefront, lane 3j + c holds channel c of
+// Gaussian j, its (DEG+1)^2 coefficients and their gradients in registers
+// while the wavefront's contiguous coefficient block (21 rows) moves between
+// HBM and a per-wavefront LDS slice with coalesced float4 accesses.  Each
+// lane evaluates its
+// channel exactly as the forward did (same clamp decisions), accumulates its
+// coefficient gradients (summed over views when the coefficients are shared)
+// and its part of the direction gradient; the three lanes of a Gaussian sum
+// the direction gradient with shuffles, and lane c adds component c to
+// grad_means (after project_bwd_kernel wrote it).  With CAM, the
+// camera-centre gradients are reduced per wavefront into LDS accumulators.
+constexpr int kShBlock = 256;
+constexpr int kShPerWave = 21;
+constexpr int kShStageFloats = kShPerWave * 48;  // per-wavefront LDS slice (rows of up to 48 floats)
+constexpr int kShPrefetch = 4;                    // views whose inputs are loaded up front
+
+// Copy `floats` contiguous floats between global memory and a wavefront's LDS
+// slice (float4 when both ends allow it); the wavefront's own LDS traffic is
+// ordered by the fence that follows.
+template <bool TO_LDS>
+GS3D_DEV void wave_copy(float* lds, float* glob, int floats) {
+    const int lane = lane_id();
+    if (((reinterpret_cast<uintptr_t>(glob) & 15) == 0) && (floats & 3) == 0) {
+        for (int e = lane; e < (floats >> 2); e += 64) {
+            if (TO_LDS)
+                reinterpret_cast<float4*>(lds)[e] = reinterpret_cast<const float4*>(glob)[e];
+            else
+                reinterpret_cast<float4*>(glob)[e] = reinterpret_cast<const float4*>(lds)[e];
+        }
+    } else {
+        for (int e = lane; e < floats; e += 64) {
+            if (TO_LDS)
+                lds[e] = glob[e];
+            else
+                glob[e] = lds[e];
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Coefficient gradients of a wavefront's Gaussians (rows beyond KC zero),
+// through the LDS slice when the rows fit it.
+template <int KC>
+GS3D_DEV void store_sh_grads(const gs3d_project_bwd_args& a, float* stage, bool staged, bool valid, int64_t offset,
+                             int64_t g0, int rows_here, int j, int c, const float* gco) {
+    const int64_t rf = (int64_t)a.sh_rows * 3;
+    if (staged) {
+        if (valid) {
+#pragma unroll
+            for (int k = 0; k < KC; ++k) stage[j * rf + 3 * k + c] = gco[k];
+            for (int k = KC; k < a.sh_rows; ++k) stage[j * rf + 3 * k + c] = 0.0f;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        wave_copy<false>(stage, a.grad_sh + offset + g0 * rf, rows_here * (int)rf);
+    } else if (valid) {
+        float* dst = a.grad_sh + offset + (g0 + j) * rf + c;
+#pragma unroll
+        for (int k = 0; k < KC; ++k) dst[3 * k] = gco[k];
+        for (int k = KC; k < a.sh_rows; ++k) dst[3 * k] = 0.0f;
+    }
+}
+
+template <int DEG, bool CAM, bool STAGED>
+__global__ __launch_bounds__(kShBlock) void sh_views_bwd_kernel(gs3d_project_bwd_args a) {
+    constexpr int KC = (DEG + 1) * (DEG + 1);
+    __shared__ float s_cam[CAM ? kShBlock / 64 : 1][kMaxViewsCamLds][3];
+    __shared__ float s_stage[STAGED ? kShBlock / 64 : 1][STAGED ? kShStageFloats : 1];
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    const int j = lane / 3, c = lane - 3 * j;
+    float* stage = s_stage[wave];
+    constexpr bool staged = STAGED;  // rows of at most 48 floats; else coefficients are read in place
+    const int64_t n = a.n;
+    const int views = a.views;
+    const int64_t rf = (int64_t)a.sh_rows * 3;
+    if constexpr (CAM) {
+        for (int e = threadIdx.x; e < (kShBlock / 64) * kMaxViewsCamLds * 3; e += kShBlock)
+            (&s_cam[0][0][0])[e] = 0.0f;
+        __syncthreads();
+    }
+    const int64_t wave_stride = (int64_t)gridDim.x * (kShBlock / 64) * kShPerWave;
+    for (int64_t g0 = ((int64_t)blockIdx.x * (kShBlock / 64) + wave) * kShPerWave; g0 < n; g0 += wave_stride) {
+        const int64_t i = g0 + j;
+        const bool valid = lane < 3 * kShPerWave && i < n;
+        const int rows_here = (int)min((int64_t)kShPerWave, n - g0);
+        float mean[3] = {0.0f, 0.0f, 0.0f};
+        if (DEG > 0 && valid) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
+        }
+        // Per-view inputs of the first kShPrefetch views and the mean
+        // gradient, loaded together with the coefficients (one latency).
+        int pre_radius[kShPrefetch];
+        float pre_up[kShPrefetch];
+#pragma unroll
+        for (int v = 0; v < kShPrefetch; ++v) {
+            const int64_t row = (int64_t)v * n + i;
+            const bool use = valid && v < views;
+            pre_radius[v] = use ? a.radii[row] : 0;
+            pre_up[v] = use ? a.grad_colors[row * a.grad_colors_stride + c] : 0.0f;
+        }
+        float gm_old = 0.0f;
+        if (DEG > 0 && valid && a.grad_means) gm_old = a.grad_means[3 * i + c];
+        float cf[KC], gco[KC];
+        if constexpr (staged) wave_copy<true>(stage, const_cast<float*>(a.sh) + g0 * rf, rows_here * (int)rf);
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+            cf[k] = valid ? (staged ? stage[j * rf + 3 * k + c] : a.sh[i * rf + 3 * k + c]) : 0.0f;
+            gco[k] = 0.0f;
+        }
+        float gm = 0.0f;
+        for (int v = 0; v < views; ++v) {
+            const int64_t row = (int64_t)v * n + i;
+            if (a.sh_view_stride != 0 && v > 0) {
+                const float* src = a.sh + v * a.sh_view_stride;
+                if constexpr (staged) wave_copy<true>(stage, const_cast<float*>(src) + g0 * rf, rows_here * (int)rf);
+#pragma unroll
+                for (int k = 0; k < KC; ++k)
+                    cf[k] = valid ? (staged ? stage[j * rf + 3 * k + c] : src[i * rf + 3 * k + c]) : 0.0f;
+            }
+            int radius = 0;
+            float up = 0.0f;
+#pragma unroll
+            for (int p = 0; p < kShPrefetch; ++p)
+                if (v == p) {
+                    radius = pre_radius[p];
+                    up = pre_up[p];
+                }
+            if (v >= kShPrefetch && valid) {
+                radius = a.radii[row];
+                up = a.grad_colors[row * a.grad_colors_stride + c];
+            }
+            const bool vis = valid && radius > 0;
+            float unit[3] = {0.0f, 0.0f, 0.0f}, length = 1.0f;
+            if (DEG > 0) {
+                float dir[3];
+#pragma unroll
+                for (int k = 0; k < 3; ++k) dir[k] = mean[k] - a.camera_centers[3 * v + k];
+                length = length3(dir);
+                const float l = sel_max(length, 1.0e-12f);
+#pragma unroll
+                for (int k = 0; k < 3; ++k) unit[k] = dir[k] / l;
+            }
+            // Channel c of the forward colour (sh_eval's order and rounding).
+            float value = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KC; ++k) value = value + sh_basis(unit, k) * cf[k];
+            value = value + 0.5f;
+            const float cg = (vis && value >= 0.0f) ? up : 0.0f;
+            float ugp[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k = 0; k < KC; ++k) {
+                gco[k] += sh_basis(unit, k) * cg;
+                if (DEG > 0) {
+                    float bg[3];
+                    sh_basis_grad(unit, k, bg);
+                    const float d = cf[k] * cg;
+#pragma unroll
+                    for (int q = 0; q < 3; ++q) ugp[q] = ugp[q] + d * bg[q];
+                }
+            }
+            float gd[3] = {0.0f, 0.0f, 0.0f};
+            if (DEG > 0) {
+                float ug[3];
+                const int l0 = 3 * j;
+#pragma unroll
+                for (int q = 0; q < 3; ++q)
+                    ug[q] = __shfl(ugp[q], l0, 64) + __shfl(ugp[q], l0 + 1, 64) + __shfl(ugp[q], l0 + 2, 64);
+                if (vis) {
+                    const float l = sel_max(length, 1.0e-12f);
+#pragma unroll
+                    for (int q = 0; q < 3; ++q) gd[q] = ug[q] / l;
+                    if (length >= 1.0e-12f) {
+                        const float f = (unit[0] * ug[0] + unit[1] * ug[1] + unit[2] * ug[2]) / length;
+#pragma unroll
+                        for (int q = 0; q < 3; ++q) gd[q] = gd[q] - unit[q] * f;
+                    }
+                }
+                gm += (c == 0) ? gd[0] : (c == 1) ? gd[1] : gd[2];
+            }
+            if constexpr (CAM) {
+                if (v < kMaxViewsCamLds) {
+#pragma unroll
+                    for (int q = 0; q < 3; ++q) {
+                        const float sum = wave_sum_to_lane63(c == 0 ? -gd[q] : 0.0f);
+                        if (lane == 63) s_cam[wave][v][q] += sum;
+                    }
+                }
+            }
+            if (a.sh_view_stride != 0 && a.grad_sh) {
+                // Per-view coefficients: write this view's gradient block.
+                store_sh_grads<KC>(a, stage, staged, valid, v * a.sh_view_stride, g0, rows_here, j, c, gco);
+#pragma unroll
+                for (int k = 0; k < KC; ++k) gco[k] = 0.0f;
+            }
+        }
+        if (DEG > 0 && valid && a.grad_means) a.grad_means[3 * i + c] = gm_old + gm;
+        if (a.sh_view_stride == 0 && a.grad_sh) store_sh_grads<KC>(a, stage, staged, valid, 0, g0, rows_here, j, c, gco);
+    }
+    if constexpr (CAM) {
+        __syncthreads();
+        for (int e = threadIdx.x; e < views * 3; e += kShBlock) {
+            const int v = e / 3, k = e - v * 3;
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kShBlock / 64; ++w) sum += s_cam[w][v][k];
+            atomicAdd(a.grad_camera_centers + 3 * v + k, sum);
+        }
+    }
+}
+
 template <int DEG>
 __global__ void sh_fwd_kernel(const float* __restrict__ coefficients, int rows, const float* __restrict__ dirs,
                               const int32_t* __restrict__ radii, int n, float* __restrict__ colors,
@@ -833,21 +982,45 @@ int launch_project_fwd(const gs3d_project_args& a, hipStream_t stream) {
     return launch_status("gs3d_project_fwd");
 }
 
-template <int DEG>
-int launch_project_bwd(const gs3d_project_bwd_args& a, int want_camera, hipStream_t stream) {
+inline dim3 persistent_grid(int64_t n) {
     int device = 0, cus = 256;
     if (hipGetDevice(&device) == hipSuccess) {
         int value = 0;
         if (hipDeviceGetAttribute(&value, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && value > 0)
             cus = value;
     }
-    const int64_t needed = blocks_for(a.n, kProjBlock);
+    const int64_t needed = blocks_for(n, kProjBlock);
     const int64_t persistent = (int64_t)cus * 8;
-    const dim3 grid((unsigned)(needed < persistent ? needed : persistent));
-    if (want_camera)
-        hipLaunchKernelGGL((project_bwd_kernel<DEG, true>), grid, dim3(kProjBlock), 0, stream, a);
+    return dim3((unsigned)(needed < persistent ? needed : persistent));
+}
+
+// Projection VJP first (it writes grad_means), then the SH VJP (it adds the
+// direction gradients to grad_means).
+template <int DEG>
+int launch_project_bwd(const gs3d_project_bwd_args& a, hipStream_t stream) {
+    const dim3 grid = persistent_grid(a.n);
+    if (a.grad_view || a.grad_projection)
+        hipLaunchKernelGGL((project_bwd_kernel<true>), grid, dim3(kProjBlock), 0, stream, a);
     else
-        hipLaunchKernelGGL((project_bwd_kernel<DEG, false>), grid, dim3(kProjBlock), 0, stream, a);
+        hipLaunchKernelGGL((project_bwd_kernel<false>), grid, dim3(kProjBlock), 0, stream, a);
+    if constexpr (DEG >= 0) {
+        const int64_t waves = (a.n + kShPerWave - 1) / kShPerWave;
+        const int64_t needed = (waves + kShBlock / 64 - 1) / (kShBlock / 64);
+        const int64_t cap = (int64_t)grid.x * 2;  // persistent: 16 blocks of 4 wavefronts per CU
+        const dim3 sh_grid((unsigned)(needed < cap ? needed : cap));
+        const bool staged = a.sh_rows * 3 <= 48;
+        if (DEG > 0 && a.grad_camera_centers) {
+            if (staged)
+                hipLaunchKernelGGL((sh_views_bwd_kernel<DEG, true, true>), sh_grid, dim3(kShBlock), 0, stream, a);
+            else
+                hipLaunchKernelGGL((sh_views_bwd_kernel<DEG, true, false>), sh_grid, dim3(kShBlock), 0, stream, a);
+        } else {
+            if (staged)
+                hipLaunchKernelGGL((sh_views_bwd_kernel<DEG, false, true>), sh_grid, dim3(kShBlock), 0, stream, a);
+            else
+                hipLaunchKernelGGL((sh_views_bwd_kernel<DEG, false, false>), sh_grid, dim3(kShBlock), 0, stream, a);
+        }
+    }
     return launch_status("gs3d_project_bwd");
 }
 
@@ -888,18 +1061,18 @@ extern "C" int gs3d_project_bwd(const gs3d_project_bwd_args* args, void* stream)
         return GS3D_ERR_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(a.quats) & 15) || (a.grad_quats && (reinterpret_cast<uintptr_t>(a.grad_quats) & 15)))
         return GS3D_ERR_ARGUMENT;
-    const int want_camera = (a.grad_view || a.grad_projection || (a.sh && a.grad_camera_centers)) ? 1 : 0;
+    const bool want_camera = a.grad_view || a.grad_projection || (a.sh && a.grad_camera_centers);
     if (want_camera && a.views > gs3d::kMaxViewsCamLds) return GS3D_ERR_UNSUPPORTED;
     hipStream_t s = gs3d::as_stream(stream);
-    if (!a.sh) return gs3d::launch_project_bwd<-1>(a, want_camera, s);
+    if (!a.sh) return gs3d::launch_project_bwd<-1>(a, s);
     if (a.sh_degree < 0 || a.sh_degree > 3 || a.sh_rows < (a.sh_degree + 1) * (a.sh_degree + 1) || !a.grad_colors ||
         a.grad_colors_stride < 3 || (a.sh_degree > 0 && !a.camera_centers))
         return GS3D_ERR_ARGUMENT;
     switch (a.sh_degree) {
-    case 0: return gs3d::launch_project_bwd<0>(a, want_camera, s);
-    case 1: return gs3d::launch_project_bwd<1>(a, want_camera, s);
-    case 2: return gs3d::launch_project_bwd<2>(a, want_camera, s);
-    default: return gs3d::launch_project_bwd<3>(a, want_camera, s);
+    case 0: return gs3d::launch_project_bwd<0>(a, s);
+    case 1: return gs3d::launch_project_bwd<1>(a, s);
+    case 2: return gs3d::launch_project_bwd<2>(a, s);
+    default: return gs3d::launch_project_bwd<3>(a, s);
     }
 }
 

@@ -278,6 +278,45 @@ def test_projection_backward_parity(key, degree):
                 atol=1e-4 * max(1.0, np.abs(ref["camera_centers"]).max()))
 
 
+@pytest.mark.parametrize("degree", [2, 3])
+def test_projection_per_view_sh_parity(degree):
+    # Per-view coefficients (C,N,16,3) and, for degree 2, coefficient rows
+    # beyond (degree+1)^2 whose gradients must come back as zeros.
+    scene = _scene("sh3_4view")
+    _say(f"projection per-view SH degree={degree}")
+    views, n = scene.viewmats.shape[0], scene.means.shape[0]
+    g = torch.Generator().manual_seed(11)
+    sh = (scene.sh_coeffs.cpu()[None] + 0.05 * torch.randn((views,) + tuple(scene.sh_coeffs.shape), generator=g))
+    sh = sh.contiguous().to(DEV)
+    quats = torch.nn.functional.normalize(scene.quats, dim=-1)
+    full, inverse, centers, errors = cameras.launch_prepare(scene.viewmats, scene.Ks, scene.width, scene.height, True)
+    st = gproj.project_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks,
+                             scene.width, scene.height, 0.2, float("inf"), 0.0, sh=sh, sh_degree=degree,
+                             camera_centers=centers, metadata=True)
+    ref_f = oracle.project_fwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+                               _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height, sh=_np(sh),
+                               sh_degree=degree, camera_centers=_np(centers), metadata=True)
+    np.testing.assert_array_equal(_np(st.colors), ref_f["colors"])
+    gc = torch.randn((views, n, 2), generator=g).to(DEV)
+    gk = torch.randn((views, n, 4), generator=g).to(DEV) * 0.1
+    gcol = torch.randn((views, n, 3), generator=g).to(DEV)
+    res = gproj.backward_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks,
+                               scene.width, scene.height, st.radii, gc, gk, (True,) * 6, sh=sh, sh_degree=degree,
+                               camera_centers=centers, grad_colors=gcol, need_sh=True, need_centers=True)
+    ref = oracle.project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+                             _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height, _np(st.radii),
+                             _np(gc), _np(gk), sh=_np(sh), sh_degree=degree, camera_centers=_np(centers),
+                             grad_colors=_np(gcol))
+    got_sh = _np(res["sh"])
+    assert got_sh.shape == sh.shape
+    kc = (degree + 1) ** 2
+    assert np.all(got_sh[..., kc:, :] == 0.0)
+    compare("sh", got_sh, ref["sh"], rtol=1e-4, atol=1e-6)
+    compare("means", _np(res["means"]), ref["means"], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(ref["means"]).max()))
+    compare("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], rtol=1e-3,
+            atol=1e-4 * max(1.0, np.abs(ref["camera_centers"]).max()))
+
+
 @pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3), ("sh3_720p", 0)])
 def test_grouped_binning_matches_reference_order(key, degree):
     # The production binning (depth-ordered rows, 8x8-tile groups, ballot
