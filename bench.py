@@ -25,8 +25,22 @@ import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
-KERNELS = {"project": "gs3d::project_fwd_kernel<3, true> (projection + SH3 + metadata, all views)",
-           "project_bwd": "gs3d::project_bwd_kernel<3> (projection + SH3 VJP, all views)"}
+ROOFLINE_KERNEL = "gs3d::project_fwd_kernel<3, true> (projection + SH3 + metadata, all views, one launch)"
+# rocprofv3 FETCH_SIZE / WRITE_SIZE summary of that kernel on the default workload.
+TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "project_fwd_kernel_traffic_3M_1080p_4view_sh3.md")
+
+
+def measured_traffic(workload, n):
+    """HBM bytes per launch of the projection kernel, measured with rocprofv3
+    counters (committed summary; default workload only), or None."""
+    if workload != "sh3_1080p_4view" or n is not None or not os.path.exists(TRAFFIC_SUMMARY):
+        return None
+    with open(TRAFFIC_SUMMARY) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def parse():
@@ -282,8 +296,9 @@ def main():
         per_stage[k]["gbps"] = round(by[k] / (stages[k] * 1e-3) / 1e9, 1)
         per_stage[k]["frac"] = round(by[k] / (stages[k] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
         per_stage[k]["bytes"] = by[k]
-    # The dominant HBM-bound kernel: the longer of the two single-kernel stages.
-    dom = max(("project", "project_bwd"), key=lambda k: stages[k])
+    # The roofline object is the projection forward kernel: HBM-bound, one
+    # launch per step; every other stage's bandwidth is in "stages".
+    dom = "project"
     achieved = by[dom] / (stages[dom] * 1e-3) / 1e9
     cpu = None
     if args.cpu_baseline == "on":
@@ -314,12 +329,12 @@ def main():
         "bwd_ms": round(bwd_ms / args.steps, 3),
         "roofline": {
             "bound": "hbm",
-            "kernel": KERNELS[dom],
+            "kernel": ROOFLINE_KERNEL,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.workload, args.n),
             "ms": round(stages[dom], 4),
             "bytes": by[dom],
         },

@@ -718,28 +718,41 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
 // camera-centre gradients are reduced per wavefront into LDS accumulators.
 constexpr int kShBlock = 256;
 constexpr int kShPerWave = 21;
-constexpr int kShStageFloats = kShPerWave * 48;  // per-wavefront LDS slice (rows of up to 48 floats)
+constexpr int kShStageFloats = kShPerWave * 49;  // per-wavefront LDS slice (rows of up to 48 floats, pitch + 1)
 constexpr int kShPrefetch = 4;                    // views whose inputs are loaded up front
 
-// Copy `floats` contiguous floats between global memory and a wavefront's LDS
-// slice (float4 when both ends allow it); the wavefront's own LDS traffic is
-// ordered by the fence that follows.
-template <bool TO_LDS>
-GS3D_DEV void wave_copy(float* lds, float* glob, int floats) {
+// Copy `rows` rows of RF contiguous floats between global memory and a
+// wavefront's LDS slice, where rows have the odd pitch RF + 1 (per-lane
+// column reads are then free of bank conflicts).  Global accesses are float4
+// when rows and the address allow it; the wavefront's LDS traffic is ordered
+// by the fence that follows.
+template <bool TO_LDS, int RF>
+GS3D_DEV void wave_copy(float* lds, float* glob, int rows) {
+    constexpr int rf = RF;
     const int lane = lane_id();
-    if (((reinterpret_cast<uintptr_t>(glob) & 15) == 0) && (floats & 3) == 0) {
-        for (int e = lane; e < (floats >> 2); e += 64) {
-            if (TO_LDS)
-                reinterpret_cast<float4*>(lds)[e] = reinterpret_cast<const float4*>(glob)[e];
-            else
-                reinterpret_cast<float4*>(glob)[e] = reinterpret_cast<const float4*>(lds)[e];
+    const int floats = rows * rf;
+    if (((reinterpret_cast<uintptr_t>(glob) & 15) == 0) && (rf & 3) == 0) {  // rf: compile-time
+        for (int e4 = lane; e4 < (floats >> 2); e4 += 64) {
+            const int e = e4 << 2;
+            const int row = e / rf;
+            float* l = lds + e + row;
+            if (TO_LDS) {
+                const float4 v = reinterpret_cast<const float4*>(glob)[e4];
+                l[0] = v.x;
+                l[1] = v.y;
+                l[2] = v.z;
+                l[3] = v.w;
+            } else {
+                reinterpret_cast<float4*>(glob)[e4] = make_float4(l[0], l[1], l[2], l[3]);
+            }
         }
     } else {
         for (int e = lane; e < floats; e += 64) {
+            const int row = e / rf;
             if (TO_LDS)
-                lds[e] = glob[e];
+                lds[e + row] = glob[e];
             else
-                glob[e] = lds[e];
+                glob[e] = lds[e + row];
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -755,12 +768,12 @@ GS3D_DEV void store_sh_grads(const gs3d_project_bwd_args& a, float* stage, bool 
     if (staged) {
         if (valid) {
 #pragma unroll
-            for (int k = 0; k < KC; ++k) stage[j * rf + 3 * k + c] = gco[k];
-            for (int k = KC; k < a.sh_rows; ++k) stage[j * rf + 3 * k + c] = 0.0f;
+            for (int k = 0; k < KC; ++k) stage[j * (rf + 1) + 3 * k + c] = gco[k];
+            for (int k = KC; k < a.sh_rows; ++k) stage[j * (rf + 1) + 3 * k + c] = 0.0f;
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         __builtin_amdgcn_wave_barrier();
-        wave_copy<false>(stage, a.grad_sh + offset + g0 * rf, rows_here * (int)rf);
+        wave_copy<false, 3 * KC>(stage, a.grad_sh + offset + g0 * rf, rows_here);
     } else if (valid) {
         float* dst = a.grad_sh + offset + (g0 + j) * rf + c;
 #pragma unroll
@@ -777,7 +790,7 @@ __global__ __launch_bounds__(kShBlock) void sh_views_bwd_kernel(gs3d_project_bwd
     const int lane = lane_id(), wave = threadIdx.x >> 6;
     const int j = lane / 3, c = lane - 3 * j;
     float* stage = s_stage[wave];
-    constexpr bool staged = STAGED;  // rows of at most 48 floats; else coefficients are read in place
+    constexpr bool staged = STAGED;  // a.sh_rows == KC: rows staged; else coefficients are read in place
     const int64_t n = a.n;
     const int views = a.views;
     const int64_t rf = (int64_t)a.sh_rows * 3;
@@ -810,10 +823,10 @@ __global__ __launch_bounds__(kShBlock) void sh_views_bwd_kernel(gs3d_project_bwd
         float gm_old = 0.0f;
         if (DEG > 0 && valid && a.grad_means) gm_old = a.grad_means[3 * i + c];
         float cf[KC], gco[KC];
-        if constexpr (staged) wave_copy<true>(stage, const_cast<float*>(a.sh) + g0 * rf, rows_here * (int)rf);
+        if constexpr (staged) wave_copy<true, 3 * KC>(stage, const_cast<float*>(a.sh) + g0 * rf, rows_here);
 #pragma unroll
         for (int k = 0; k < KC; ++k) {
-            cf[k] = valid ? (staged ? stage[j * rf + 3 * k + c] : a.sh[i * rf + 3 * k + c]) : 0.0f;
+            cf[k] = valid ? (staged ? stage[j * (rf + 1) + 3 * k + c] : a.sh[i * rf + 3 * k + c]) : 0.0f;
             gco[k] = 0.0f;
         }
         float gm = 0.0f;
@@ -821,10 +834,10 @@ __global__ __launch_bounds__(kShBlock) void sh_views_bwd_kernel(gs3d_project_bwd
             const int64_t row = (int64_t)v * n + i;
             if (a.sh_view_stride != 0 && v > 0) {
                 const float* src = a.sh + v * a.sh_view_stride;
-                if constexpr (staged) wave_copy<true>(stage, const_cast<float*>(src) + g0 * rf, rows_here * (int)rf);
+                if constexpr (staged) wave_copy<true, 3 * KC>(stage, const_cast<float*>(src) + g0 * rf, rows_here);
 #pragma unroll
                 for (int k = 0; k < KC; ++k)
-                    cf[k] = valid ? (staged ? stage[j * rf + 3 * k + c] : src[i * rf + 3 * k + c]) : 0.0f;
+                    cf[k] = valid ? (staged ? stage[j * (rf + 1) + 3 * k + c] : src[i * rf + 3 * k + c]) : 0.0f;
             }
             int radius = 0;
             float up = 0.0f;
@@ -1008,7 +1021,7 @@ int launch_project_bwd(const gs3d_project_bwd_args& a, hipStream_t stream) {
         const int64_t needed = (waves + kShBlock / 64 - 1) / (kShBlock / 64);
         const int64_t cap = (int64_t)grid.x * 2;  // persistent: 16 blocks of 4 wavefronts per CU
         const dim3 sh_grid((unsigned)(needed < cap ? needed : cap));
-        const bool staged = a.sh_rows * 3 <= 48;
+        const bool staged = a.sh_rows == (DEG + 1) * (DEG + 1);  // rows of exactly the needed coefficients
         if (DEG > 0 && a.grad_camera_centers) {
             if (staged)
                 hipLaunchKernelGGL((sh_views_bwd_kernel<DEG, true, true>), sh_grid, dim3(kShBlock), 0, stream, a);
