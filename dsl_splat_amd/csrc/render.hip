@@ -68,10 +68,26 @@ struct TileInfo {
     int view, x0, y0, first, last;
 };
 
+// Workgroups go to the 8 XCDs in turn; within every run of 8 * GS3D_TILE_CHUNK
+// workgroups, XCD x takes the x-th chunk of GS3D_TILE_CHUNK consecutive tiles
+// so that neighbouring tiles, which share most of their Gaussians, meet in one
+// L2 (the final partial run keeps the identity order).
+#ifndef GS3D_TILE_CHUNK
+#define GS3D_TILE_CHUNK 8
+#endif
+GS3D_DEV int tile_of_block(int b, int blocks) {
+    constexpr int C = GS3D_TILE_CHUNK, R = 8 * C;
+    if (C <= 1) return b;
+    const int run = b / R;
+    if ((run + 1) * R > blocks) return b;
+    const int w = b - run * R;
+    return run * R + (w & 7) * C + (w >> 3);
+}
+
 GS3D_DEV TileInfo tile_info(const gs3d_render_args& a) {
     const int gx = (a.width + kTile - 1) / kTile, gy = (a.height + kTile - 1) / kTile;
     const int per_view = gx * gy;
-    const int tile = blockIdx.x;
+    const int tile = tile_of_block(blockIdx.x, gridDim.x);
     TileInfo t;
     t.view = tile / per_view;
     const int local = tile - t.view * per_view;
