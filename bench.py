@@ -184,6 +184,26 @@ def stage_timings(scene, reps):
         e1.record()
         torch.cuda.synchronize()
         acc["project_kernel"] = e0.elapsed_time(e1) / launches
+        # Contribution statistics (a masked count and a weighted sum over
+        # per-view pixel maps) observed by the forward blend, against the
+        # plain forward blend, both back-to-back.
+        from dsl_splat_amd.statistics import PreparedStatistics
+        g = torch.Generator().manual_seed(9)
+        hw = scene.width * scene.height
+        pv = torch.stack([(torch.rand((views, hw), generator=g) < 0.5).float(), torch.rand((views, hw), generator=g)],
+                         1).to(quats.device)
+        stats = PreparedStatistics((0, 1), pv, torch.zeros((views, 1, n), dtype=torch.int32, device=quats.device),
+                                   torch.zeros((views, 1, n), device=quats.device))
+        for key, kw in (("render_fwd_kernel", {}), ("render_fwd_stats_kernel", {"statistics": stats})):
+            blend = lambda: grender.render_views(ranges, ids, st.centers, st.conics, feats, scene.width,
+                                                 scene.height, **kw)
+            blend()
+            e0.record()
+            for _ in range(5):
+                blend()
+            e1.record()
+            torch.cuda.synchronize()
+            acc[key] = e0.elapsed_time(e1) / 5
     # Algorithmic bytes of every stage: what its kernels must read and write
     # once each.
     M, S, T, R = info["pairs"], info["group_pairs"], info["tiles"], info["rows"]
@@ -306,7 +326,8 @@ def main():
     s13 = ("project", "order", "bin")
     t13 = sum(stages[k] for k in s13)
     b13 = sum(by[k] for k in s13)
-    per_stage = {k: dict(ms=round(v, 4)) for k, v in stages.items() if k != "project_kernel"}
+    kernels = ("project_kernel", "render_fwd_kernel", "render_fwd_stats_kernel")
+    per_stage = {k: dict(ms=round(v, 4)) for k, v in stages.items() if k not in kernels}
     for k in by:
         per_stage[k]["gbps"] = round(by[k] / (stages[k] * 1e-3) / 1e9, 1)
         per_stage[k]["frac"] = round(by[k] / (stages[k] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
@@ -357,6 +378,9 @@ def main():
         "stages_1_3": {"ms": round(t13, 4), "bytes": b13, "gbps": round(b13 / (t13 * 1e-3) / 1e9, 1),
                        "frac": round(b13 / (t13 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
         "stages": per_stage,
+        "statistics": {"requests": "masked count + weighted sum, per-view maps",
+                       "render_fwd_ms": round(stages["render_fwd_kernel"], 4),
+                       "render_fwd_stats_ms": round(stages["render_fwd_stats_kernel"], 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

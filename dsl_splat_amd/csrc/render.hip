@@ -166,8 +166,49 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32
     if (a.one_tail) dst[c++] = 1.0f;
 }
 
-template <int CH, int PIX>
-__global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_render_args a) {
+// Contribution statistics of one accepted Gaussian (statistics.py:46-70,
+// observed at gs3d/render.py:109-115): for every request r, a masked count
+// adds the number of this wavefront's accepted pixels whose value is nonzero
+// (one ballot per pixel slot), a weighted sum adds value * alpha * T over
+// them (one wavefront reduction).  One lane issues each request's atomic, so
+// a wavefront adds one partial per (Gaussian, request) instead of one per
+// pixel; counts are exact, sums differ from per-pixel atomics only in the
+// order of the float additions (which atomics leave unspecified anyway).
+template <int PIX>
+GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, int view, int n, int32_t g, const bool (&acc)[PIX],
+                                 const float (&w)[PIX], const float (&val)[PIX][GS3D_MAX_STATISTICS], int lane) {
+    int count_row = 0, sum_row = 0;
+#pragma unroll
+    for (int r = 0; r < GS3D_MAX_STATISTICS; ++r) {
+        if (r >= st.requests) break;
+        if ((st.sum_mask >> r) & 1u) {
+            float s = 0.0f;
+            bool any = false;
+#pragma unroll
+            for (int k = 0; k < PIX; ++k) {
+                const bool hit = acc[k] && val[k][r] != 0.0f;
+                any = any || hit;
+                s += hit ? val[k][r] * w[k] : 0.0f;
+            }
+            if (__ballot(any)) {
+                s = wave_sum_to_lane63(s);
+                if (lane == 63)
+                    atomicAdd(st.sums + view * st.sums_view_stride + (int64_t)sum_row * n + g, s);
+            }
+            ++sum_row;
+        } else {
+            int c = 0;
+#pragma unroll
+            for (int k = 0; k < PIX; ++k) c += __popcll(__ballot(acc[k] && val[k][r] != 0.0f));
+            if (c > 0 && lane == 0)
+                atomicAdd(st.counts + view * st.counts_view_stride + (int64_t)count_row * n + g, c);
+            ++count_row;
+        }
+    }
+}
+
+template <int CH, int PIX, bool STATS>
+__global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st) {
     constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
     __shared__ float2 s_xy[B];
@@ -175,12 +216,14 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
     __shared__ float s_cut[B];
     __shared__ uint32_t s_mask[B];
     __shared__ float s_feat[B * CH];
+    __shared__ int32_t s_id[STATS ? B : 1];
     const TileInfo t = tile_info(a);
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     const int lane = lane_id(), wave = threadIdx.x >> 6;
     float fx[PIX], fy[PIX], T[PIX], color[PIX][CH];
     int px[PIX], py[PIX], last_contributor[PIX];
     bool done[PIX];
+    float val[PIX][STATS ? GS3D_MAX_STATISTICS : 1];
 #pragma unroll
     for (int k = 0; k < PIX; ++k) {
         int lx, ly;
@@ -194,6 +237,13 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
         last_contributor[k] = 0;
 #pragma unroll
         for (int c = 0; c < CH; ++c) color[k][c] = 0.0f;
+        if constexpr (STATS) {
+            const float* pv = st.pixel_values + t.view * st.pixel_view_stride + (int64_t)py[k] * a.width + px[k];
+            const int64_t plane = (int64_t)a.width * a.height;
+#pragma unroll
+            for (int r = 0; r < GS3D_MAX_STATISTICS; ++r)
+                val[k][r] = (r < st.requests && !done[k]) ? pv[r * plane] : 0.0f;
+        }
     }
     for (int begin = t.first; begin < t.last; begin += B) {
         bool active = false;
@@ -202,7 +252,11 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
         if (__syncthreads_count(active) == 0) break;
         for (int e = threadIdx.x; e < B; e += NT) {
             const int idx = begin + e;
-            if (idx < t.last) stage_gaussian<CH, PIX>(a, t, a.ids[idx], e, s_xy, s_con, s_cut, s_mask, s_feat);
+            if (idx < t.last) {
+                const int32_t g = a.ids[idx];
+                stage_gaussian<CH, PIX>(a, t, g, e, s_xy, s_con, s_cut, s_mask, s_feat);
+                if constexpr (STATS) s_id[e] = g;
+            }
         }
         __syncthreads();
         const int cnt = min(B, t.last - begin);
@@ -225,8 +279,12 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
                 const float4 con = s_con[j];
                 const float cut = s_cut[j];
                 const float* f = s_feat + j * CH;
+                bool acc[PIX];
+                float wk[PIX];
 #pragma unroll
                 for (int k = 0; k < PIX; ++k) {
+                    acc[k] = false;
+                    wk[k] = 0.0f;
                     if (done[k]) continue;
                     const float dx = xy.x - fx[k], dy = xy.y - fy[k];
                     const float power = blend_power(con.x, con.y, con.z, dx, dy);
@@ -244,6 +302,14 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
                         if (c < D) color[k][c] = __builtin_fmaf(f[c], w, color[k][c]);
                     T[k] = next_t;
                     last_contributor[k] = contributor;
+                    acc[k] = true;
+                    wk[k] = w;
+                }
+                if constexpr (STATS) {
+                    bool hit = false;
+#pragma unroll
+                    for (int k = 0; k < PIX; ++k) hit = hit || acc[k];
+                    if (__ballot(hit)) observe_statistics<PIX>(st, t.view, a.n, s_id[j], acc, wk, val, lane);
                 }
             }
         }
@@ -480,9 +546,14 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
 }
 
 template <int CH>
-int launch_fwd(const gs3d_render_args& a, unsigned blocks, hipStream_t s) {
+int launch_fwd(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned blocks, hipStream_t s) {
     constexpr int PIX = PixFor<CH, GS3D_FWD_PIX>::value;
-    hipLaunchKernelGGL((render_fwd_kernel<CH, PIX>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a);
+    if (st) {
+        hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, true>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a, *st);
+        return launch_status("gs3d_render_fwd_stats");
+    }
+    const gs3d_render_stats_args none = {};
+    hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, false>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a, none);
     return launch_status("gs3d_render_fwd");
 }
 
@@ -517,23 +588,47 @@ inline unsigned render_blocks(const gs3d_render_args& a) {
 
 }  // namespace gs3d
 
-extern "C" int gs3d_render_fwd(const gs3d_render_args* args, void* stream) {
+namespace gs3d {
+
+int render_fwd(const gs3d_render_args* args, const gs3d_render_stats_args* st, void* stream) {
     if (!args) return GS3D_ERR_ARGUMENT;
     const gs3d_render_args& a = *args;
-    int status = gs3d::check_render_args(a);
+    int status = check_render_args(a);
     if (status != GS3D_OK) return status;
     if (a.views == 0) return GS3D_OK;
     if ((a.feat_channels > 0 && !a.image) || (a.extra_channels > 0 && !a.image_extra) ||
         (a.one_tail && !a.image_alpha) || !a.final_t || !a.contributors)
         return GS3D_ERR_ARGUMENT;
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
-    const unsigned blocks = gs3d::render_blocks(a);
-    hipStream_t s = gs3d::as_stream(stream);
-    if (D <= 4) return gs3d::launch_fwd<4>(a, blocks, s);
-    if (D <= 8) return gs3d::launch_fwd<8>(a, blocks, s);
-    if (D <= 16) return gs3d::launch_fwd<16>(a, blocks, s);
-    if (D <= 36) return gs3d::launch_fwd<36>(a, blocks, s);
-    return gs3d::launch_fwd<64>(a, blocks, s);
+    const unsigned blocks = render_blocks(a);
+    hipStream_t s = as_stream(stream);
+    if (D <= 4) return launch_fwd<4>(a, st, blocks, s);
+    if (D <= 8) return launch_fwd<8>(a, st, blocks, s);
+    if (D <= 16) return launch_fwd<16>(a, st, blocks, s);
+    if (D <= 36) return launch_fwd<36>(a, st, blocks, s);
+    return launch_fwd<64>(a, st, blocks, s);
+}
+
+}  // namespace gs3d
+
+extern "C" int gs3d_render_fwd(const gs3d_render_args* args, void* stream) {
+    return gs3d::render_fwd(args, nullptr, stream);
+}
+
+extern "C" int gs3d_render_fwd_stats(const gs3d_render_args* args, const gs3d_render_stats_args* stats,
+                                     void* stream) {
+    if (!args || !stats) return GS3D_ERR_ARGUMENT;
+    const gs3d_render_stats_args& st = *stats;
+    if (st.requests < 1 || st.requests > GS3D_MAX_STATISTICS) return GS3D_ERR_ARGUMENT;
+    const uint32_t used = (1u << st.requests) - 1u;
+    if (st.sum_mask & ~used) return GS3D_ERR_ARGUMENT;
+    const bool any_sum = st.sum_mask != 0, any_count = st.sum_mask != used;
+    if (!st.pixel_values || (any_sum && !st.sums) || (any_count && !st.counts)) return GS3D_ERR_ARGUMENT;
+    if (st.pixel_view_stride < 0 || st.counts_view_stride < 0 || st.sums_view_stride < 0) return GS3D_ERR_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(st.pixel_values) | reinterpret_cast<uintptr_t>(st.counts) |
+         reinterpret_cast<uintptr_t>(st.sums)) & 3)
+        return GS3D_ERR_ARGUMENT;
+    return gs3d::render_fwd(args, stats, stream);
 }
 
 extern "C" int gs3d_render_bwd(const gs3d_render_bwd_args* args, void* stream) {

@@ -24,7 +24,7 @@ from ..inputs import batch_item, normalize_inputs
 from ..splatting.binning import (check_pair_counts, finish_binning, order_rows, require_radius_mode,
                                  validate_tile_mode)
 from ..splatting.cameras import launch_prepare, raise_camera_errors
-from ..statistics import StatisticsRequest
+from ..statistics import StatisticsRequest, prepare_statistics
 from ..training import prepare_training_metadata
 
 BACKEND = "gs3d-hip"
@@ -130,8 +130,6 @@ def rasterize(
         backgrounds, extra_features, None, sh_degree,
     )
     require_radius_mode(tile_mode)
-    if statistics:
-        raise NotImplementedError("contribution statistics are not implemented in the HIP rasterizer yet")
     frames: list[Frame] = []
     dense: dict[str, list[Tensor]] = {n: [] for n in ("radii", "means2d", "opacities", "tiles_per_gauss", "conics")}
     for b in range(layout.batch_count):
@@ -171,6 +169,13 @@ def rasterize(
         screen_gradient_mode="projected_mean",
         tile_mode=tile_mode,
     )
+    prepared_stats, statistics_outputs = (
+        prepare_statistics(
+            statistics, batch_dims=layout.batch_dims, batch_count=layout.batch_count, cameras=layout.cameras,
+            n=layout.n, width=width, height=height, device=layout.device,
+        )
+        if statistics else ([], {})
+    )
     planes = []
     grad_enabled = torch.is_grad_enabled()
     for b, frame in enumerate(frames):
@@ -179,7 +184,8 @@ def rasterize(
         extras = None if layout.extras is None else layout.extras.values[b]
         planes.append(Rasterize.apply(
             layout.means[b], layout.quats[b], layout.scales[b], layout.opacities[b], layout.colors.values[b],
-            extras, batch_item(layout.viewmats, b), screen, frame, targets, grad_enabled,
+            extras, batch_item(layout.viewmats, b), screen, frame, targets,
+            prepared_stats[b] if statistics else None, grad_enabled,
         ))
     shape = layout.batch_dims + (layout.cameras, height, width)
 
@@ -191,4 +197,4 @@ def rasterize(
     features, alpha = gather(0), gather(2)
     if layout.extras is not None:
         meta["render_extra_signals"] = gather(1)
-    return RasterizationResult(features, alpha, meta, {})
+    return RasterizationResult(features, alpha, meta, statistics_outputs)

@@ -23,6 +23,7 @@ from torch.autograd.function import once_differentiable
 from . import projection, render
 from ..runtime.gradients import AbsGradientTarget
 from ..splatting.cameras import camera_backward
+from ..statistics import PreparedStatistics
 
 
 @dataclass(slots=True)
@@ -57,15 +58,17 @@ class Rasterize(torch.autograd.Function):
         screen: Tensor | None,
         frame: Frame,
         absolute: list[AbsGradientTarget | None] | None,
+        statistics: PreparedStatistics | None,
         grad_enabled: bool,
     ) -> tuple[Tensor, Tensor, Tensor]:
         """Returns the (C,H,W,D) features, (C,H,W,E) extra (E may be 0) and
-        (C,H,W,1) alpha planes."""
+        (C,H,W,1) alpha planes; statistics, when given, accumulate in the same
+        blend launch."""
         st = frame.state
         blended = st.colors if frame.sh_degree is not None else colors
         output = render.render_views(
             frame.ranges, frame.ids, st.centers, st.conics, blended, frame.width, frame.height,
-            extra=extra_features, background=frame.background, one_tail=True,
+            extra=extra_features, background=frame.background, one_tail=True, statistics=statistics,
         )
         if grad_enabled and any(ctx.needs_input_grad[:8]):
             ctx.save_for_backward(means, quats, scales, opacities, colors, extra_features, viewmats,
@@ -83,7 +86,7 @@ class Rasterize(torch.autograd.Function):
     @once_differentiable
     def backward(ctx: Any, grad_features: Tensor | None, grad_extra_image: Tensor | None,
                  grad_alpha: Tensor | None) -> tuple[Tensor | None, ...]:
-        none = (None,) * 11
+        none = (None,) * 12
         if grad_features is None and grad_extra_image is None and grad_alpha is None:
             return none
         if grad_extra_image is not None and grad_extra_image.numel() == 0:
@@ -136,6 +139,7 @@ class Rasterize(torch.autograd.Function):
             grad_extra if needs[5] else None,
             grad_view,
             grad_centers if needs[7] else None,
+            None,
             None,
             None,
             None,

@@ -17,7 +17,7 @@ from ..cameras import PinholeCamera
 from ..inputs import check_tensor, spherical_harmonics
 from ..primitives.tiling import TileBins
 from ..splatting.binning import bin_and_sort as _bin_arrays, require_radius_mode, validate_tile_mode
-from ..statistics import StatisticsRequest
+from ..statistics import PreparedStatistics, StatisticsRequest, prepare_statistics
 
 
 @dataclass(slots=True)
@@ -82,9 +82,10 @@ class _Project(torch.autograd.Function):
 class _Pixels(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, centers, conics, features, radii, ranges, ids, background, config: ViewConfig,
-                grad_enabled: bool):
+                statistics: PreparedStatistics | None, grad_enabled: bool):
         out = render.render_views(ranges, ids, centers[None], conics[None], features, config.width, config.height,
-                                  background=None if background is None else background[None], one_tail=True)
+                                  background=None if background is None else background[None], one_tail=True,
+                                  statistics=statistics)
         if grad_enabled and any(ctx.needs_input_grad[:3]):
             ctx.save_for_backward(centers, conics, features, ranges, ids, background, out.transmittance,
                                   out.contributors)
@@ -96,7 +97,7 @@ class _Pixels(torch.autograd.Function):
     @once_differentiable
     def backward(ctx: Any, grad_features: Tensor | None, grad_alpha: Tensor | None):
         if grad_features is None and grad_alpha is None:
-            return (None,) * 9
+            return (None,) * 10
         centers, conics, features, ranges, ids, background, final_t, contributors = ctx.saved_tensors
         upstream = (None if grad_features is None else grad_features[None], None,
                     None if grad_alpha is None else grad_alpha[None])
@@ -106,7 +107,7 @@ class _Pixels(torch.autograd.Function):
             one_tail=True, need_features=ctx.needs_input_grad[2])
         grads = (record[0, :, 0:2], record[0, :, 2:6], gf)
         return (*(g if ctx.needs_input_grad[i] else None for i, g in enumerate(grads)), None, None, None, None, None,
-                None)
+                None, None)
 
 
 def prepare_gaussians(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tensor, camera: PinholeCamera, *,
@@ -151,12 +152,16 @@ def rasterize_to_pixels(geometry: GaussianGeometry, tiles: GaussianTiles, featur
         check_tensor("background", background, device, (channels,))
         if torch.is_grad_enabled() and background.requires_grad:
             raise NotImplementedError("background gradients are not supported")
-    if statistics:
-        raise NotImplementedError("contribution statistics are not implemented in the HIP rasterizer yet")
+    config = geometry._config
+    prepared, outputs = (
+        prepare_statistics(statistics, batch_dims=(), batch_count=1, cameras=1, n=n, width=config.width,
+                           height=config.height, device=device)
+        if statistics else ([], {})
+    )
     image, alpha = _Pixels.apply(geometry.centers, geometry.conics, features.contiguous(), geometry.radii,
-                                 tiles.ranges, tiles.gaussian_ids, background, geometry._config,
-                                 torch.is_grad_enabled())
-    return PixelResult(image, alpha, {})
+                                 tiles.ranges, tiles.gaussian_ids, background, config,
+                                 prepared[0] if statistics else None, torch.is_grad_enabled())
+    return PixelResult(image, alpha, {name: value[0] for name, value in outputs.items()})
 
 
 __all__ = [

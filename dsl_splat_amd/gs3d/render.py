@@ -89,10 +89,34 @@ def _args(width, height, views, n, ranges, ids, centers, conics, features, extra
     return a, fc + ec + int(one_tail)
 
 
+def _stats_args(statistics, views: int, n: int, width: int, height: int, keep: list) -> abi.RenderStatsArgs:
+    """gs3d_render_stats_args over one frame's PreparedStatistics."""
+    key = tuple(statistics.key)
+    pv, counts, sums = statistics.pixel_values, statistics.counts, statistics.sums
+    if pv.shape != (views, len(key), height * width) or counts.shape[::2] != (views, n) or \
+            sums.shape[::2] != (views, n):
+        raise ValueError("prepared statistics do not match the rendered views")
+    for t in (pv, counts, sums):
+        if not t.is_contiguous():
+            raise ValueError("prepared statistics must be contiguous")
+    keep += [pv, counts, sums]
+    st = abi.RenderStatsArgs()
+    st.requests = len(key)
+    st.sum_mask = sum(1 << r for r, kind in enumerate(key) if kind == 1)
+    st.pixel_values, st.pixel_view_stride = native.ptr(pv), pv.stride(0)
+    st.counts = native.ptr(counts) if counts.shape[1] else None
+    st.counts_view_stride = counts.stride(0)
+    st.sums = native.ptr(sums) if sums.shape[1] else None
+    st.sums_view_stride = sums.stride(0)
+    return st
+
+
 @torch.no_grad()
 def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, features: Tensor,
                  width: int, height: int, *, extra: Tensor | None = None, background: Tensor | None = None,
-                 one_tail: bool = True) -> RenderedPixels:
+                 one_tail: bool = True, statistics=None) -> RenderedPixels:
+    """Blend all views; with a PreparedStatistics, its counts and sums
+    accumulate the contribution statistics of the same launch."""
     views, n = centers.shape[0], centers.shape[1]
     device = centers.device
     keep = []
@@ -109,7 +133,11 @@ def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, f
     a.image, a.final_t, a.contributors = (native.ptr(out.features), native.ptr(out.transmittance),
                                           native.ptr(out.contributors))
     a.image_extra, a.image_alpha = native.ptr(out.extra), native.ptr(out.alpha)
-    native.call("gs3d_render_fwd", ctypes.byref(a), native.stream(device))
+    if statistics is not None and len(statistics.key):
+        st = _stats_args(statistics, views, n, width, height, keep)
+        native.call("gs3d_render_fwd_stats", ctypes.byref(a), ctypes.byref(st), native.stream(device))
+    else:
+        native.call("gs3d_render_fwd", ctypes.byref(a), native.stream(device))
     return out
 
 

@@ -174,6 +174,22 @@ class RenderArgs(ctypes.Structure):
     ]
 
 
+MAX_STATISTICS = 8
+
+
+class RenderStatsArgs(ctypes.Structure):
+    _fields_ = [
+        ("requests", ctypes.c_int32),
+        ("sum_mask", ctypes.c_uint32),
+        ("pixel_values", _P),
+        ("pixel_view_stride", ctypes.c_int64),
+        ("counts", _P),
+        ("counts_view_stride", ctypes.c_int64),
+        ("sums", _P),
+        ("sums_view_stride", ctypes.c_int64),
+    ]
+
+
 class RenderBwdArgs(ctypes.Structure):
     _fields_ = [
         ("fwd", RenderArgs),
@@ -205,6 +221,7 @@ STRUCTS = {
     "gs3d_order_args": OrderArgs,
     "gs3d_bin_args": BinArgs,
     "gs3d_render_args": RenderArgs,
+    "gs3d_render_stats_args": RenderStatsArgs,
     "gs3d_render_bwd_args": RenderBwdArgs,
 }
 
@@ -248,5 +265,6 @@ FUNCTIONS = {
     "gs3d_sort_pairs_u32": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),
     "gs3d_expand_keys": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _I32, _P, _P]),
     "gs3d_render_fwd": (ctypes.c_int, [ctypes.POINTER(RenderArgs), _P]),
+    "gs3d_render_fwd_stats": (ctypes.c_int, [ctypes.POINTER(RenderArgs), ctypes.POINTER(RenderStatsArgs), _P]),
     "gs3d_render_bwd": (ctypes.c_int, [ctypes.POINTER(RenderBwdArgs), _P]),
 }

@@ -327,6 +327,31 @@ typedef struct gs3d_render_args {
 int gs3d_render_fwd(const gs3d_render_args* args, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Contribution statistics observed by the forward blend: statistics.py:16-156
+ * (MaskedContributionCount, WeightedContributionSum, make_observer at
+ * :46-70), fed from the accepted-blend branch of gs3d/render.py:109-115 and
+ * bound at :393-397.  For each accepted blend of Gaussian g at pixel p with
+ * weight alpha*T and each request r with value v = pixel_values[r][p] != 0:
+ * a count request adds 1 to counts[row][g], a sum request adds v*alpha*T to
+ * sums[row][g], where row numbers the requests of the same kind in order.
+ * Outputs accumulate (the caller zeroes them).  Same blend outputs as
+ * gs3d_render_fwd.
+ * ---------------------------------------------------------------------- */
+#define GS3D_MAX_STATISTICS 8
+typedef struct gs3d_render_stats_args {
+    int32_t requests;            /* R, 1..GS3D_MAX_STATISTICS */
+    uint32_t sum_mask;           /* bit r set: request r is a weighted sum, else a masked count */
+    const float* pixel_values;   /* (views, R, H*W) */
+    int64_t pixel_view_stride;   /* floats between views (0 = shared) */
+    int32_t* counts;             /* (views, count requests, n); NULL without count requests */
+    int64_t counts_view_stride;
+    float* sums;                 /* (views, sum requests, n); NULL without sum requests */
+    int64_t sums_view_stride;
+} gs3d_render_stats_args;
+
+int gs3d_render_fwd_stats(const gs3d_render_args* args, const gs3d_render_stats_args* stats, void* stream);
+
+/* ------------------------------------------------------------------------
  * Reverse traversal of the blend: gs3d/render.py:211-356 (backward, launched
  * at :409-463) with constant_tail = one_tail.  Gradients are accumulated with
  * atomics (the caller zeroes them); a wavefront reduces its 64 pixels'

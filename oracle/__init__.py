@@ -50,6 +50,7 @@ def lib() -> ctypes.CDLL:
             "oracle_sort_pairs_u64": [P, P, I64, I32],
             "oracle_tile_ranges": [P, I64, P, I64],
             "oracle_render_fwd": [ctypes.POINTER(abi.RenderArgs)],
+            "oracle_render_fwd_stats": [ctypes.POINTER(abi.RenderArgs), ctypes.POINTER(abi.RenderStatsArgs)],
             "oracle_render_bwd": [ctypes.POINTER(abi.RenderBwdArgs)],
             "oracle_projection_loss_f64": [P, P, P, D, P, P, I32, I32, D, D, P, P],
             "oracle_projection_vjp_f64": [P, P, P, D, P, P, I32, I32, D, D, P, P, P],
@@ -331,6 +332,32 @@ def render_fwd(width, height, ranges, ids, centers, conics, features, extra=None
     a.image, a.final_t, a.contributors = _ptr(image), _ptr(final_t), _ptr(contributors)
     lib().oracle_render_fwd(ctypes.byref(a))
     return image, final_t, contributors
+
+
+def render_fwd_stats(width, height, ranges, ids, centers, conics, features, kinds, pixel_values, extra=None,
+                     background=None):
+    """render_fwd plus contribution statistics (statistics.py:46-70): kinds[r]
+    is 0 (masked count) or 1 (weighted sum), pixel_values (views, R, H, W).
+    Returns image, final_t, contributors, counts (views, #counts, N) int32 and
+    sums (views, #sums, N) float32."""
+    keep = []
+    a, c, n, channels = _render_args(width, height, ranges, ids, centers, conics, features, extra, background, keep)
+    image = np.zeros((c, height, width, channels), np.float32)
+    final_t = np.zeros((c, height, width), np.float32)
+    contributors = np.zeros((c, height, width), np.int32)
+    a.image, a.final_t, a.contributors = _ptr(image), _ptr(final_t), _ptr(contributors)
+    kinds = list(kinds)
+    pv = _f32(pixel_values).reshape(c, len(kinds), height * width)
+    counts = np.zeros((c, kinds.count(0), n), np.int32)
+    sums = np.zeros((c, kinds.count(1), n), np.float32)
+    st = abi.RenderStatsArgs()
+    st.requests = len(kinds)
+    st.sum_mask = sum(1 << r for r, k in enumerate(kinds) if k == 1)
+    st.pixel_values, st.pixel_view_stride = _ptr(pv), pv.shape[1] * pv.shape[2]
+    st.counts, st.counts_view_stride = _ptr(counts), counts.shape[1] * n
+    st.sums, st.sums_view_stride = _ptr(sums), sums.shape[1] * n
+    lib().oracle_render_fwd_stats(ctypes.byref(a), ctypes.byref(st))
+    return image, final_t, contributors, counts, sums
 
 
 def render_bwd(width, height, ranges, ids, centers, conics, features, final_t, contributors, upstream,

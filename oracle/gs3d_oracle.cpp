@@ -1002,16 +1002,37 @@ static inline int total_channels(const gs3d_render_args* a) {
     return a->feat_channels + a->extra_channels + (a->one_tail ? 1 : 0);
 }
 
-// gs3d/render.py:36-126 forward, one pixel at a time.
-int oracle_render_fwd(const gs3d_render_args* a) {
+// statistics.py:46-70 (make_observer), called per accepted blend at
+// gs3d/render.py:109-115: request r reads its pixel value; a nonzero value
+// adds 1 to the Gaussian's count row, or value * weight to its sum row.  Rows
+// number the requests of one kind in request order.
+static void observe(const gs3d_render_stats_args* st, int v, int n, int64_t g, int64_t pixel, int64_t plane,
+                    float weight) {
+    int count_row = 0, sum_row = 0;
+    for (int r = 0; r < st->requests; ++r) {
+        const float value = st->pixel_values[v * st->pixel_view_stride + r * plane + pixel];
+        if ((st->sum_mask >> r) & 1u) {
+            if (value != 0.0f) st->sums[v * st->sums_view_stride + (int64_t)sum_row * n + g] += value * weight;
+            ++sum_row;
+        } else {
+            if (value != 0.0f) st->counts[v * st->counts_view_stride + (int64_t)count_row * n + g] += 1;
+            ++count_row;
+        }
+    }
+}
+
+// gs3d/render.py:36-126 forward, one pixel at a time.  With statistics the
+// pixels run in order on one thread (the observer accumulates).
+static int render_fwd(const gs3d_render_args* a, const gs3d_render_stats_args* st) {
     const int W = a->width, H = a->height;
     const int gx = (W + 15) / 16, gy = (H + 15) / 16;
     const int D = total_channels(a);
     std::vector<float> bg(D);
+    const int threads = st ? 1 : g_threads;
     for (int v = 0; v < a->views; ++v) {
         for (int k = 0; k < D; ++k)
             bg[k] = (a->background && k < a->feat_channels) ? a->background[v * a->background_view_stride + k] : 0.0f;
-#pragma omp parallel for schedule(dynamic, 4) num_threads(g_threads)
+#pragma omp parallel for schedule(dynamic, 4) num_threads(threads)
         for (int y = 0; y < H; ++y) {
             std::vector<float> color(D), f(D);
             for (int x = 0; x < W; ++x) {
@@ -1036,6 +1057,7 @@ int oracle_render_fwd(const gs3d_render_args* a) {
                     gather_features(a, v, g, f.data());
                     const float w = alpha * T;
                     for (int k = 0; k < D; ++k) color[k] = fmaf(f[k], w, color[k]);
+                    if (st) observe(st, v, a->n, g, (int64_t)y * W + x, (int64_t)W * H, w);
                     T = next_t;
                     last_contributor = contributor;
                 }
@@ -1048,6 +1070,10 @@ int oracle_render_fwd(const gs3d_render_args* a) {
     }
     return 0;
 }
+
+int oracle_render_fwd(const gs3d_render_args* a) { return render_fwd(a, nullptr); }
+
+int oracle_render_fwd_stats(const gs3d_render_args* a, const gs3d_render_stats_args* st) { return render_fwd(a, st); }
 
 // gs3d/render.py:211-356 backward, sequential accumulation per pixel in
 // tile-then-row-major order (the GPU sums the same terms in another order).

@@ -47,6 +47,17 @@ def test_argument_errors_are_reported_without_launching():
     args.feat_channels, args.one_tail = 70, 1
     args.ranges = args.centers = args.conics = args.features = ctypes.c_void_p(256)
     assert lib.gs3d_render_fwd(ctypes.byref(args), None) == abi.GS3D_ERR_UNSUPPORTED
+    # Statistics: 1..8 requests, kind bits only for existing requests, outputs
+    # present for each kind requested.
+    args.feat_channels = 3
+    st = abi.RenderStatsArgs()
+    st.pixel_values = st.counts = st.sums = ctypes.c_void_p(256)
+    for requests, mask in ((0, 0), (abi.MAX_STATISTICS + 1, 0), (2, 0b100)):
+        st.requests, st.sum_mask = requests, mask
+        assert lib.gs3d_render_fwd_stats(ctypes.byref(args), ctypes.byref(st), None) == abi.GS3D_ERR_ARGUMENT
+    st.requests, st.sum_mask, st.sums = 2, 0b10, None
+    assert lib.gs3d_render_fwd_stats(ctypes.byref(args), ctypes.byref(st), None) == abi.GS3D_ERR_ARGUMENT
+    assert lib.gs3d_render_fwd_stats(ctypes.byref(args), None, None) == abi.GS3D_ERR_ARGUMENT
     # Zero-size work is a no-op.
     assert lib.gs3d_pair_tiles(None, 0, None, 0, None) == abi.GS3D_OK
     args = abi.BinArgs()

@@ -82,7 +82,8 @@ def test_statistics_request_validation():
         batch_dims=(), batch_count=1, cameras=2, n=7, width=W, height=H, device=torch.device("cpu"))
     assert outputs["hits"].shape == (2, 7) and outputs["hits"].dtype == torch.int32
     assert outputs["score"].shape == (2, 7) and outputs["score"].dtype == torch.float32
-    assert len(prepared) == 2 and prepared[0].key == (0, 1)
+    # one entry per batch item, covering all cameras (one blend launch each)
+    assert len(prepared) == 1 and prepared[0].key == (0, 1) and prepared[0].pixel_values.shape == (2, 2, H * W)
     with pytest.raises(ValueError, match="unique"):
         prepare_statistics([MaskedContributionCount("a", mask), MaskedContributionCount("a", mask)], batch_dims=(),
                            batch_count=1, cameras=1, n=1, width=W, height=H, device=torch.device("cpu"))
