@@ -9,6 +9,7 @@
 #include <climits>
 
 #include "common.hpp"
+#include "footprint.hpp"
 
 namespace gs3d {
 
@@ -173,6 +174,17 @@ inline void fill_u32(uint32_t* p, int64_t count, uint32_t value, hipStream_t s) 
                        value);
 }
 
+// Tile rectangle of row r in the rectangle modes (radius square or SnugBox).
+GS3D_DEV int4 emit_rect(const gs3d_emit_args& a, int64_t r, int radius, int gx, int gy) {
+    const float2 c = reinterpret_cast<const float2*>(a.centers)[r];
+    const float4 k = a.tile_mode == GS3D_TILE_RADIUS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                                                     : reinterpret_cast<const float4*>(a.conics)[r];
+    int4 rect = mode_rect(c, k, radius, gx, gy, a.tile_mode);
+    rect.z = max(rect.z, rect.x);
+    rect.w = max(rect.w, rect.y);
+    return rect;
+}
+
 __global__ __launch_bounds__(kEmitThreads) void emit_small_kernel(gs3d_emit_args a, uint32_t* __restrict__ queue_count,
                                                                   int32_t* __restrict__ queue) {
     const int64_t rows = (int64_t)a.n * a.views;
@@ -181,8 +193,7 @@ __global__ __launch_bounds__(kEmitThreads) void emit_small_kernel(gs3d_emit_args
     const int radius = a.radii[r];
     if (radius <= 0) return;
     const int gx = (a.width + 15) / 16, gy = (a.height + 15) / 16;
-    const float2 c = reinterpret_cast<const float2*>(a.centers)[r];
-    const int4 rect = tile_rect(c.x, c.y, radius, gx, gy);
+    const int4 rect = emit_rect(a, r, radius, gx, gy);
     const int w = rect.z - rect.x;
     const int64_t off0 = r > 0 ? a.offsets[r - 1] : 0;
     // The slot reserved by the scan bounds the emission (equal by construction).
@@ -212,8 +223,7 @@ __global__ __launch_bounds__(kEmitThreads) void emit_large_kernel(gs3d_emit_args
     const int gx = (a.width + 15) / 16, gy = (a.height + 15) / 16;
     for (uint32_t q = blockIdx.x; q < total; q += gridDim.x) {
         const int64_t r = queue[q];
-        const float2 c = reinterpret_cast<const float2*>(a.centers)[r];
-        const int4 rect = tile_rect(c.x, c.y, a.radii[r], gx, gy);
+        const int4 rect = emit_rect(a, r, a.radii[r], gx, gy);
         const int w = rect.z - rect.x;
         const int64_t off = r > 0 ? a.offsets[r - 1] : 0;
         const int count = (int)min((int64_t)(w * (rect.w - rect.y)), (int64_t)a.offsets[r] - off);
@@ -228,6 +238,36 @@ __global__ __launch_bounds__(kEmitThreads) void emit_large_kernel(gs3d_emit_args
             a.values[off + k] = id;
         }
     }
+}
+
+// AccuTile emission (splatting/binning.py:40-68 with intersections.py:160-218):
+// one thread per row writes its strips' tiles in traversal order.
+__global__ __launch_bounds__(kEmitThreads) void emit_accutile_kernel(gs3d_emit_args a) {
+    const int64_t rows = (int64_t)a.n * a.views;
+    const int64_t r = (int64_t)blockIdx.x * kEmitThreads + threadIdx.x;
+    if (r >= rows) return;
+    const int radius = a.radii[r];
+    if (radius <= 0) return;
+    const int64_t off = r > 0 ? a.offsets[r - 1] : 0;
+    const int64_t reserved = (int64_t)a.offsets[r] - off;
+    if (reserved <= 0) return;
+    const int gx = (a.width + 15) / 16, gy = (a.height + 15) / 16;
+    const Ellipse e = footprint(reinterpret_cast<const float2*>(a.centers)[r], reinterpret_cast<const float4*>(a.conics)[r],
+                                radius, gx, gy);
+    const int64_t view = r / a.n;
+    const int32_t id = (int32_t)(r - view * a.n);
+    const uint32_t tile0 = (uint32_t)(view * gx * gy);
+    const uint32_t bits = __float_as_uint(a.depths[r]);
+    int64_t k = 0;
+    bool is_y = true;
+    accutile_strips(e, is_y, [&](int row, int lo, int hi) {
+        for (int col = lo; col < hi; ++col, ++k) {
+            if (k >= reserved) continue;
+            const uint32_t tile = tile0 + (uint32_t)(is_y ? row * gx + col : col * gx + row);
+            a.keys[off + k] = ((uint64_t)tile << 32) | (uint64_t)bits;
+            a.values[off + k] = id;
+        }
+    });
 }
 
 // ---------------------------------------------------------------------------
@@ -539,29 +579,63 @@ struct TileRect {
     int x0, y0, x1, y1;  // exclusive ends; empty when x1 <= x0
 };
 
-GS3D_DEV TileRect row_rect(const float* __restrict__ centers, const int32_t* __restrict__ radii, int64_t row, int gx,
-                           int gy) {
+// Per-row inputs of the tile footprint (conics are read only outside the
+// radius mode).
+struct RowGeometry {
+    const float* centers;
+    const float* conics;
+    const int32_t* radii;
+    int mode;
+};
+
+GS3D_DEV TileRect row_rect(const RowGeometry& g, int64_t row, int gx, int gy) {
     TileRect r{0, 0, 0, 0};
-    const int radius = radii[row];
+    const int radius = g.radii[row];
     if (radius > 0) {
-        const float2 c = reinterpret_cast<const float2*>(centers)[row];
-        const int4 b = tile_rect(c.x, c.y, radius, gx, gy);
+        const float2 c = reinterpret_cast<const float2*>(g.centers)[row];
+        const float4 k = g.mode == GS3D_TILE_RADIUS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                                                    : reinterpret_cast<const float4*>(g.conics)[row];
+        const int4 b = mode_rect(c, k, radius, gx, gy, g.mode);
         if (b.z > b.x && b.w > b.y) r = TileRect{b.x, b.y, b.z, b.w};
     }
     return r;
 }
 
 template <bool PACKED>
-GS3D_DEV TileRect record_rect(uint64_t record, const float* __restrict__ centers, const int32_t* __restrict__ radii,
-                              int gx, int gy) {
+GS3D_DEV TileRect record_rect(uint64_t record, const RowGeometry& g, int gx, int gy) {
     if constexpr (PACKED) {
         const uint32_t p = (uint32_t)(record >> 32);
         TileRect r{(int)(p & 255u), (int)((p >> 8) & 255u), (int)((p >> 16) & 255u) + 1, (int)(p >> 24) + 1};
         if (r.x1 <= r.x0) r = TileRect{0, 0, 0, 0};
         return r;
     } else {
-        return row_rect(centers, radii, (int64_t)(uint32_t)record, gx, gy);
+        return row_rect(g, (int64_t)(uint32_t)record, gx, gy);
     }
+}
+
+// AccuTile groups and tiles of one footprint.  Strips of one group row (8
+// strips) touch an interval of group columns: consecutive strips share the
+// crossing points of their common boundary line, so their tile spans
+// overlap and the union over the group row is one interval.  Emission uses
+// the same intervals, so counts and items always agree.
+GS3D_DEV void accutile_groups(const Ellipse& e, int& groups, int& tiles) {
+    bool is_y = true;
+    int cur = -1, gmin = INT_MAX, gmax = -1, total = 0;
+    tiles = accutile_strips(e, is_y, [&](int row, int lo, int hi) {
+        const int G = row >> kGroupShift;
+        if (G != cur) {
+            if (gmax >= gmin) total += gmax - gmin + 1;
+            cur = G;
+            gmin = INT_MAX;
+            gmax = -1;
+        }
+        if (hi > lo) {
+            gmin = min(gmin, lo >> kGroupShift);
+            gmax = max(gmax, (hi - 1) >> kGroupShift);
+        }
+    });
+    if (gmax >= gmin) total += gmax - gmin + 1;
+    groups = total;
 }
 
 GS3D_DEV int groups_of(const TileRect& r) {
@@ -573,15 +647,14 @@ GS3D_DEV int groups_of(const TileRect& r) {
 // Row order: depth-bit keys and records (coalesced reads of depth, centre
 // and radius).
 template <bool PACKED>
-__global__ void row_records_kernel(const float* __restrict__ depths, const float* __restrict__ centers,
-                                   const int32_t* __restrict__ radii, int64_t rows, int gx, int gy,
+__global__ void row_records_kernel(const float* __restrict__ depths, RowGeometry g, int64_t rows, int gx, int gy,
                                    uint32_t* __restrict__ keys, uint64_t* __restrict__ records) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
     keys[i] = __float_as_uint(depths[i]);
     uint64_t rec = (uint64_t)(uint32_t)i;
     if constexpr (PACKED) {
-        const TileRect r = row_rect(centers, radii, i, gx, gy);
+        const TileRect r = row_rect(g, i, gx, gy);
         const uint32_t p = r.x1 > r.x0 ? (uint32_t)r.x0 | ((uint32_t)r.y0 << 8) | ((uint32_t)(r.x1 - 1) << 16) |
                                              ((uint32_t)(r.y1 - 1) << 24)
                                        : kEmptyRect;
@@ -591,20 +664,31 @@ __global__ void row_records_kernel(const float* __restrict__ depths, const float
 }
 
 // Group count of every row in depth order; the block's tile pair count goes
-// to block_pairs[blockIdx.x].
-template <bool PACKED>
+// to block_pairs[blockIdx.x].  ACCU: AccuTile strips of the row's footprint.
+template <bool PACKED, bool ACCU>
 __global__ __launch_bounds__(kBinThreads) void order_counts_kernel(const uint64_t* __restrict__ records, int64_t rows,
-                                                                   const float* __restrict__ centers,
-                                                                   const int32_t* __restrict__ radii, int gx, int gy,
+                                                                   RowGeometry g, int gx, int gy,
                                                                    int32_t* __restrict__ group_counts,
                                                                    int64_t* __restrict__ block_pairs) {
     __shared__ int64_t s_wave[kBinWaves];
     const int64_t i = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
     int64_t area = 0;
     if (i < rows) {
-        const TileRect r = record_rect<PACKED>(records[i], centers, radii, gx, gy);
-        if (r.x1 > r.x0) area = (int64_t)(r.x1 - r.x0) * (r.y1 - r.y0);
-        group_counts[i] = groups_of(r);
+        if constexpr (ACCU) {
+            const int64_t row = (int64_t)(uint32_t)records[i];
+            const int radius = g.radii[row];
+            int groups = 0, tiles = 0;
+            if (radius > 0)
+                accutile_groups(footprint(reinterpret_cast<const float2*>(g.centers)[row],
+                                          reinterpret_cast<const float4*>(g.conics)[row], radius, gx, gy),
+                                groups, tiles);
+            area = tiles;
+            group_counts[i] = groups;
+        } else {
+            const TileRect r = record_rect<PACKED>(records[i], g, gx, gy);
+            if (r.x1 > r.x0) area = (int64_t)(r.x1 - r.x0) * (r.y1 - r.y0);
+            group_counts[i] = groups_of(r);
+        }
     }
     int64_t total;
     block_exclusive_scan<kBinThreads>(area, s_wave, total);
@@ -629,8 +713,7 @@ __global__ __launch_bounds__(1024) void sum_i64_kernel(const int64_t* __restrict
 template <bool PACKED>
 __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t* __restrict__ records,
                                                                  const int32_t* __restrict__ offsets, int64_t rows,
-                                                                 const float* __restrict__ centers,
-                                                                 const int32_t* __restrict__ radii, int n, GridDims d,
+                                                                 RowGeometry geo, int n, GridDims d,
                                                                  int64_t limit, uint64_t* __restrict__ items) {
     __shared__ int32_t s_end[kBinThreads];
     __shared__ int32_t s_x0[kBinThreads], s_y0[kBinThreads], s_x1[kBinThreads], s_y1[kBinThreads];
@@ -644,7 +727,7 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
         const int64_t i = r0 + t;
         const uint64_t rec = records[i];
         const int32_t row = (int32_t)(uint32_t)rec;
-        const TileRect r = record_rect<PACKED>(rec, centers, radii, d.gx, d.gy);
+        const TileRect r = record_rect<PACKED>(rec, geo, d.gx, d.gy);
         s_end[t] = offsets[i];
         s_x0[t] = r.x0;
         s_y0[t] = r.y0;
@@ -678,6 +761,73 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
         const uint32_t clip = (uint32_t)(lx0 | (lx1 << 3) | (ly0 << 6) | (ly1 << 9));
         items[p] = ((uint64_t)s_id[lo] << 32) | ((uint64_t)clip << kGroupBits) | gid;
     }
+}
+
+// AccuTile items: one thread per ordered row writes one item per group of
+// each group row's interval (accutile_groups), with the 64-bit mask of the
+// group's tiles its strips cover (bit ly * 8 + lx), in masks[].  The spans
+// of the current group row's 8 strips wait in per-thread LDS slots.
+__global__ __launch_bounds__(kBinThreads) void accutile_emit_kernel(const uint64_t* __restrict__ records,
+                                                                    const int32_t* __restrict__ offsets, int64_t rows,
+                                                                    RowGeometry geo, int n, GridDims d, int64_t limit,
+                                                                    uint64_t* __restrict__ items,
+                                                                    uint64_t* __restrict__ masks) {
+    __shared__ int2 s_span[1 << kGroupShift][kBinThreads];
+    const int t = threadIdx.x;
+    const int64_t i = (int64_t)blockIdx.x * kBinThreads + t;
+    if (i >= rows) return;
+    const int64_t start = i > 0 ? offsets[i - 1] : 0;
+    const int64_t stop = min((int64_t)offsets[i], limit);
+    if (start >= stop) return;
+    const int64_t row = (int64_t)(uint32_t)records[i];
+    const int radius = geo.radii[row];
+    if (radius <= 0) return;
+    const Ellipse e = footprint(reinterpret_cast<const float2*>(geo.centers)[row],
+                                reinterpret_cast<const float4*>(geo.conics)[row], radius, d.gx, d.gy);
+    const int view = (int)(row / n);
+    const uint64_t id = (uint64_t)(uint32_t)(row - (int64_t)view * n);
+    const uint32_t gbase = (uint32_t)(view * d.gpv);
+    int64_t p = start;
+    bool is_y = true;
+    int cur = -1, gmin = INT_MAX, gmax = -1;
+    auto flush = [&](int G) {
+        for (int gc = gmin; gc <= gmax; ++gc) {
+            const int c0 = gc << kGroupShift;
+            uint64_t m = 0;
+            for (int j = 0; j < (1 << kGroupShift); ++j) {
+                const int2 sp = s_span[j][t];
+                const int lo = max(sp.x, c0), hi = min(sp.y, c0 + 8);
+                if (hi <= lo) continue;
+                if (is_y) {
+                    m |= (((1ull << (hi - lo)) - 1ull) << (lo - c0)) << (8 * j);
+                } else {
+                    for (int k = lo; k < hi; ++k) m |= 1ull << (8 * (k - c0) + j);
+                }
+            }
+            const int GX = is_y ? gc : G, GY = is_y ? G : gc;
+            if (p < stop) {
+                items[p] = (id << 32) | (uint64_t)(gbase + (uint32_t)(GY * d.sgx + GX));
+                masks[p] = m;
+            }
+            ++p;
+        }
+    };
+    accutile_strips(e, is_y, [&](int strip, int lo, int hi) {
+        const int G = strip >> kGroupShift;
+        if (G != cur) {
+            if (cur >= 0) flush(cur);
+            cur = G;
+            gmin = INT_MAX;
+            gmax = -1;
+            for (int j = 0; j < (1 << kGroupShift); ++j) s_span[j][t] = make_int2(0, 0);
+        }
+        s_span[strip & 7][t] = make_int2(lo, hi);
+        if (hi > lo) {
+            gmin = min(gmin, lo >> kGroupShift);
+            gmax = max(gmax, (hi - 1) >> kGroupShift);
+        }
+    });
+    if (cur >= 0) flush(cur);
 }
 
 // chunk_base[g] = exclusive scan over groups of ceil(len_g / kChunk);
@@ -730,12 +880,15 @@ GS3D_DEV int64_t xcd_contiguous(int64_t b, int64_t nblocks) {
 // walks the tiles its items touch and, per tile, its items in order: one
 // ballot per 64 items ranks them, so a tile's run of the chunk is written by
 // consecutive stores of one wavefront.
+// MASKS: each item's tiles come from masks[] (AccuTile), else from the
+// clipped rectangle packed in the item.
 // WRITE = false: counts[(g, t, s)] = items of chunk s touching tile t.
 // WRITE = true: every item's Gaussian index goes to
 //   tile_start[t] + (scanned[(g,t,s)] - scanned[(g,t,0)]) + rank.
-template <bool WRITE>
+template <bool WRITE, bool MASKS>
 __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
-    const uint64_t* __restrict__ items, const int32_t* __restrict__ granges, const int32_t* __restrict__ chunk_base,
+    const uint64_t* __restrict__ items, const uint64_t* __restrict__ masks, const int32_t* __restrict__ granges,
+    const int32_t* __restrict__ chunk_base,
     const int32_t* __restrict__ chunk_group, int groups, int64_t max_chunks, GridDims d,
     uint32_t* __restrict__ counts, const int32_t* __restrict__ scanned, const int32_t* __restrict__ tile_start,
     int32_t* __restrict__ ids, int64_t id_limit) {
@@ -760,7 +913,10 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
         id[k] = 0;
         if (i < end) {
             const uint64_t item = items[i];
-            mask[k] = group_tile_mask((uint32_t)(item >> kGroupBits) & 0xFFFu);
+            if constexpr (MASKS)
+                mask[k] = masks[i];
+            else
+                mask[k] = group_tile_mask((uint32_t)(item >> kGroupBits) & 0xFFFu);
             id[k] = (int32_t)(item >> 32);
         }
         any |= mask[k];
@@ -880,6 +1036,7 @@ inline size_t order_scratch_bytes(int64_t rows, OrderScratch* out, void* base) {
 
 // Scratch of gs3d_bin_rows.
 struct BinScratch {
+    uint64_t* masks;      // 2*group_pairs tile masks (AccuTile only)
     uint64_t* items;      // 2*group_pairs
     void* sort;
     int32_t* granges;     // 2*groups
@@ -894,9 +1051,10 @@ struct BinScratch {
 
 inline int64_t max_chunks_of(int64_t group_pairs, int64_t groups) { return (group_pairs + kChunk - 1) / kChunk + groups; }
 
-inline size_t bin_scratch_bytes(int64_t group_pairs, int64_t groups, int64_t tiles, BinScratch* out, void* base) {
+inline size_t bin_scratch_bytes(int64_t group_pairs, int64_t groups, int64_t tiles, bool masks, BinScratch* out,
+                                void* base) {
     const int64_t chunks = max_chunks_of(group_pairs, groups);
-    size_t sizes[10];
+    size_t sizes[11];
     sizes[0] = align256((size_t)group_pairs * 2 * sizeof(uint64_t));
     sizes[1] = align256(sort_scratch_bytes(group_pairs, nullptr, nullptr));
     sizes[2] = align256((size_t)groups * 2 * sizeof(int32_t));
@@ -908,10 +1066,11 @@ inline size_t bin_scratch_bytes(int64_t group_pairs, int64_t groups, int64_t til
     sizes[8] = sizes[7];
     const size_t scan_a = scan_partials_bytes(chunks * 64), scan_b = scan_partials_bytes(tiles);
     sizes[9] = scan_a > scan_b ? scan_a : scan_b;
+    sizes[10] = masks ? align256((size_t)group_pairs * 2 * sizeof(uint64_t)) : 0;
     size_t total = 0;
     char* p = reinterpret_cast<char*>(base);
-    void* parts[10];
-    for (int k = 0; k < 10; ++k) {
+    void* parts[11];
+    for (int k = 0; k < 11; ++k) {
         parts[k] = p ? p + total : nullptr;
         total += sizes[k];
     }
@@ -926,8 +1085,17 @@ inline size_t bin_scratch_bytes(int64_t group_pairs, int64_t groups, int64_t til
         out->totals = reinterpret_cast<int32_t*>(parts[7]);
         out->starts = reinterpret_cast<int32_t*>(parts[8]);
         out->scan = parts[9];
+        out->masks = masks ? reinterpret_cast<uint64_t*>(parts[10]) : nullptr;
     }
     return total;
+}
+
+// Tile mode and conics of an entry point: conics are required (16-byte
+// aligned) outside the radius mode.
+inline int check_tile_mode(int mode, const float* conics) {
+    if (mode < GS3D_TILE_RADIUS || mode > GS3D_TILE_ACCUTILE) return GS3D_ERR_ARGUMENT;
+    if (mode != GS3D_TILE_RADIUS && (!conics || (reinterpret_cast<uintptr_t>(conics) & 15))) return GS3D_ERR_ARGUMENT;
+    return GS3D_OK;
 }
 
 inline int bit_length(int64_t v) {
@@ -960,6 +1128,8 @@ extern "C" int gs3d_emit_keys(const gs3d_emit_args* args, void* scratch, size_t 
     if (!args) return GS3D_ERR_ARGUMENT;
     const gs3d_emit_args& a = *args;
     if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0) return GS3D_ERR_ARGUMENT;
+    if (gs3d::check_tile_mode(a.tile_mode, a.tile_mode == GS3D_TILE_RADIUS ? nullptr : a.conics) != GS3D_OK)
+        return GS3D_ERR_ARGUMENT;
     const int64_t rows = (int64_t)a.n * a.views;
     if (rows == 0) return GS3D_OK;
     if (!a.centers || !a.radii || !a.depths || !a.offsets || !a.keys || !a.values || !scratch)
@@ -969,6 +1139,11 @@ extern "C" int gs3d_emit_keys(const gs3d_emit_args* args, void* scratch, size_t 
     const int64_t tiles_total = (int64_t)((a.width + 15) / 16) * ((a.height + 15) / 16) * a.views;
     if (tiles_total > 0xFFFFFFFFll) return GS3D_ERR_OVERFLOW;
     hipStream_t s = gs3d::as_stream(stream);
+    if (a.tile_mode == GS3D_TILE_ACCUTILE) {
+        hipLaunchKernelGGL(gs3d::emit_accutile_kernel, dim3(gs3d::blocks_for(rows, gs3d::kEmitThreads)),
+                           dim3(gs3d::kEmitThreads), 0, s, a);
+        return gs3d::launch_status("gs3d_emit_keys");
+    }
     uint32_t* queue_count = reinterpret_cast<uint32_t*>(scratch);
     int32_t* queue = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(scratch) + 256);
     gs3d::fill_u32(queue_count, 1, 0u, s);
@@ -1033,43 +1208,53 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     if (!a.depths || !a.centers || !a.radii || !a.order || !a.group_offsets || !scratch) return GS3D_ERR_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(a.centers) & 7) || (reinterpret_cast<uintptr_t>(a.order) & 7))
         return GS3D_ERR_ARGUMENT;
+    if (gs3d::check_tile_mode(a.tile_mode, a.conics) != GS3D_OK) return GS3D_ERR_ARGUMENT;
     if (scratch_bytes < gs3d_order_rows_scratch_bytes(rows)) return GS3D_ERR_SCRATCH;
     gs3d::OrderScratch sc;
     gs3d::order_scratch_bytes(rows, &sc, scratch);
-    const bool packed = d.gx <= 256 && d.gy <= 256;
+    const gs3d::RowGeometry geo{a.centers, a.conics, a.radii, a.tile_mode};
+    const bool accu = a.tile_mode == GS3D_TILE_ACCUTILE;
+    const bool packed = d.gx <= 256 && d.gy <= 256 && !accu;
     const dim3 grid(gs3d::blocks_for(rows, 256)), block(256);
     if (packed)
-        hipLaunchKernelGGL(gs3d::row_records_kernel<true>, grid, block, 0, s, a.depths, a.centers, a.radii, rows, d.gx,
-                           d.gy, sc.keys, a.order);
+        hipLaunchKernelGGL(gs3d::row_records_kernel<true>, grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy, sc.keys,
+                           a.order);
     else
-        hipLaunchKernelGGL(gs3d::row_records_kernel<false>, grid, block, 0, s, a.depths, a.centers, a.radii, rows,
-                           d.gx, d.gy, sc.keys, a.order);
+        hipLaunchKernelGGL(gs3d::row_records_kernel<false>, grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy,
+                           sc.keys, a.order);
     // order holds 2*rows records: [0, rows) sorted result, [rows, 2rows) ping-pong.
     int status = gs3d::run_sort<uint32_t, uint64_t>(sc.keys, a.order, rows, 32, sc.sort, s);
     if (status != GS3D_OK) return status;
     const dim3 cgrid(gs3d::blocks_for(rows, gs3d::kBinThreads)), cblock(gs3d::kBinThreads);
-    if (packed)
-        hipLaunchKernelGGL(gs3d::order_counts_kernel<true>, cgrid, cblock, 0, s, a.order, rows, a.centers, a.radii,
-                           d.gx, d.gy, sc.counts, sc.pairs);
+    if (accu)
+        hipLaunchKernelGGL((gs3d::order_counts_kernel<false, true>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
+                           d.gy, sc.counts, sc.pairs);
+    else if (packed)
+        hipLaunchKernelGGL((gs3d::order_counts_kernel<true, false>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
+                           d.gy, sc.counts, sc.pairs);
     else
-        hipLaunchKernelGGL(gs3d::order_counts_kernel<false>, cgrid, cblock, 0, s, a.order, rows, a.centers, a.radii,
-                           d.gx, d.gy, sc.counts, sc.pairs);
+        hipLaunchKernelGGL((gs3d::order_counts_kernel<false, false>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
+                           d.gy, sc.counts, sc.pairs);
     hipLaunchKernelGGL(gs3d::sum_i64_kernel, dim3(1), dim3(1024), 0, s, sc.pairs, (int64_t)cgrid.x, a.totals + 1);
     status = gs3d::run_scan<int32_t, true>(sc.counts, rows, a.group_offsets, a.totals, sc.scan, s);
     if (status != GS3D_OK) return status;
     return gs3d::launch_status("gs3d_order_rows");
 }
 
-extern "C" size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t width, int32_t height) {
+extern "C" size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t width, int32_t height,
+                                              int32_t tile_mode) {
     if (group_pairs < 0 || views < 0 || width <= 0 || height <= 0) return 0;
     const gs3d::GridDims d = gs3d::grid_dims(width, height);
-    return gs3d::bin_scratch_bytes(group_pairs, (int64_t)views * d.gpv, (int64_t)views * d.tpv, nullptr, nullptr);
+    return gs3d::bin_scratch_bytes(group_pairs, (int64_t)views * d.gpv, (int64_t)views * d.tpv,
+                                   tile_mode == GS3D_TILE_ACCUTILE, nullptr, nullptr);
 }
 
 extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream) {
     if (!args) return GS3D_ERR_ARGUMENT;
     const gs3d_bin_args& a = *args;
     if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0 || a.group_pairs < 0 || a.tile_pairs < 0)
+        return GS3D_ERR_ARGUMENT;
+    if (gs3d::check_tile_mode(a.tile_mode, a.tile_mode == GS3D_TILE_RADIUS ? nullptr : a.conics) != GS3D_OK)
         return GS3D_ERR_ARGUMENT;
     const gs3d::GridDims d = gs3d::grid_dims(a.width, a.height);
     const int64_t rows = (int64_t)a.n * a.views;
@@ -1087,21 +1272,30 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
     if ((reinterpret_cast<uintptr_t>(a.ranges) & 7) || (reinterpret_cast<uintptr_t>(a.order) & 7) ||
         (reinterpret_cast<uintptr_t>(a.centers) & 7))
         return GS3D_ERR_ARGUMENT;
-    if (scratch_bytes < gs3d_bin_rows_scratch_bytes(a.group_pairs, a.views, a.width, a.height))
+    if (scratch_bytes < gs3d_bin_rows_scratch_bytes(a.group_pairs, a.views, a.width, a.height, a.tile_mode))
         return GS3D_ERR_SCRATCH;
+    const bool accu = a.tile_mode == GS3D_TILE_ACCUTILE;
     gs3d::BinScratch sc;
-    gs3d::bin_scratch_bytes(a.group_pairs, groups, tiles, &sc, scratch);
+    gs3d::bin_scratch_bytes(a.group_pairs, groups, tiles, accu, &sc, scratch);
     const int64_t S = a.group_pairs;
     const int64_t chunks = gs3d::max_chunks_of(S, groups);
+    const gs3d::RowGeometry geo{a.centers, a.conics, a.radii, a.tile_mode};
     const dim3 egrid(gs3d::blocks_for(rows, gs3d::kBinThreads)), eblock(gs3d::kBinThreads);
-    if (d.gx <= 256 && d.gy <= 256)
-        hipLaunchKernelGGL(gs3d::group_emit_kernel<true>, egrid, eblock, 0, s, a.order, a.group_offsets, rows,
-                           a.centers, a.radii, a.n, d, S, sc.items);
-    else
-        hipLaunchKernelGGL(gs3d::group_emit_kernel<false>, egrid, eblock, 0, s, a.order, a.group_offsets, rows,
-                           a.centers, a.radii, a.n, d, S, sc.items);
-    int status = gs3d::run_sort<uint64_t, int32_t>(sc.items, nullptr, S, gs3d::bit_length(groups - 1 > 0 ? groups - 1 : 1),
-                                          sc.sort, s);
+    const int group_bits = gs3d::bit_length(groups - 1 > 0 ? groups - 1 : 1);
+    int status;
+    if (accu) {
+        hipLaunchKernelGGL(gs3d::accutile_emit_kernel, egrid, eblock, 0, s, a.order, a.group_offsets, rows, geo, a.n, d,
+                           S, sc.items, sc.masks);
+        status = gs3d::run_sort<uint64_t, uint64_t>(sc.items, sc.masks, S, group_bits, sc.sort, s);
+    } else {
+        if (d.gx <= 256 && d.gy <= 256)
+            hipLaunchKernelGGL(gs3d::group_emit_kernel<true>, egrid, eblock, 0, s, a.order, a.group_offsets, rows, geo,
+                               a.n, d, S, sc.items);
+        else
+            hipLaunchKernelGGL(gs3d::group_emit_kernel<false>, egrid, eblock, 0, s, a.order, a.group_offsets, rows, geo,
+                               a.n, d, S, sc.items);
+        status = gs3d::run_sort<uint64_t, int32_t>(sc.items, nullptr, S, group_bits, sc.sort, s);
+    }
     if (status != GS3D_OK) return status;
     gs3d::fill_u32(reinterpret_cast<uint32_t*>(sc.granges), 2 * groups, 0u, s);
     hipLaunchKernelGGL(gs3d::tile_ranges_kernel<uint64_t>, dim3(gs3d::blocks_for(S, 256)), dim3(256), 0, s, sc.items,
@@ -1111,9 +1305,14 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
                        sc.chunk_base, (int)groups, chunks, sc.chunk_group);
     gs3d::fill_u32(sc.counts, 64 * chunks, 0u, s);
     const dim3 pass_grid(gs3d::blocks_for(chunks, gs3d::kBinWaves));
-    hipLaunchKernelGGL((gs3d::group_pass_kernel<false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
-                       sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts,
-                       (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0);
+    if (accu)
+        hipLaunchKernelGGL((gs3d::group_pass_kernel<false, true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
+                           sc.masks, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts,
+                           (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0);
+    else
+        hipLaunchKernelGGL((gs3d::group_pass_kernel<false, false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
+                           (const uint64_t*)nullptr, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d,
+                           sc.counts, (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0);
     status = gs3d::run_scan<uint32_t, false>(sc.counts, 64 * chunks, sc.scanned, nullptr, sc.scan, s);
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL(gs3d::tile_totals_kernel, dim3(gs3d::blocks_for(tiles, 256)), dim3(256), 0, s, sc.chunk_base,
@@ -1122,9 +1321,14 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL(gs3d::tile_ranges_from_totals_kernel, dim3(gs3d::blocks_for(tiles, 256)), dim3(256), 0, s,
                        sc.totals, sc.starts, tiles, a.ranges);
-    hipLaunchKernelGGL((gs3d::group_pass_kernel<true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
-                       sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts, sc.scanned,
-                       sc.starts, a.ids, a.tile_pairs);
+    if (accu)
+        hipLaunchKernelGGL((gs3d::group_pass_kernel<true, true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
+                           sc.masks, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts,
+                           sc.scanned, sc.starts, a.ids, a.tile_pairs);
+    else
+        hipLaunchKernelGGL((gs3d::group_pass_kernel<true, false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
+                           (const uint64_t*)nullptr, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d,
+                           sc.counts, sc.scanned, sc.starts, a.ids, a.tile_pairs);
     return gs3d::launch_status("gs3d_bin_rows");
 }
 

@@ -15,6 +15,7 @@
 // global loads and stores are fully coalesced; each thread then reads its
 // row from LDS with an odd row pitch (conflict-free).
 #include "common.hpp"
+#include "footprint.hpp"
 
 namespace gs3d {
 
@@ -1039,10 +1040,42 @@ int launch_project_bwd(const gs3d_project_bwd_args& a, hipStream_t stream) {
 
 }  // namespace gs3d
 
+namespace gs3d {
+
+// Tile counts of the SnugBox/AccuTile modes (gs3d/projection.py:150-161),
+// over the projection's outputs: a separate pass keeps the tile traversal out
+// of the projection kernel's registers.
+__global__ void footprint_tiles_kernel(const float* __restrict__ centers, const float* __restrict__ conics,
+                                       const int32_t* __restrict__ radii, int64_t rows, int gx, int gy, int mode,
+                                       int32_t* __restrict__ tiles) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const int radius = radii[r];
+    if (radius <= 0) return;
+    tiles[r] = footprint_tiles(reinterpret_cast<const float2*>(centers)[r], reinterpret_cast<const float4*>(conics)[r],
+                               radius, gx, gy, mode);
+}
+
+int project_fwd(const gs3d_project_args& a, hipStream_t s) {
+    if (!a.sh) return launch_project_fwd<-1>(a, s);
+    if (a.sh_degree < 0 || a.sh_degree > 3 || a.sh_rows < (a.sh_degree + 1) * (a.sh_degree + 1) || !a.colors ||
+        (a.sh_degree > 0 && !a.camera_centers))
+        return GS3D_ERR_ARGUMENT;
+    switch (a.sh_degree) {
+    case 0: return launch_project_fwd<0>(a, s);
+    case 1: return launch_project_fwd<1>(a, s);
+    case 2: return launch_project_fwd<2>(a, s);
+    default: return launch_project_fwd<3>(a, s);
+    }
+}
+
+}  // namespace gs3d
+
 extern "C" int gs3d_project_fwd(const gs3d_project_args* args, void* stream) {
     if (!args) return GS3D_ERR_ARGUMENT;
     const gs3d_project_args& a = *args;
     if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0) return GS3D_ERR_ARGUMENT;
+    if (a.tile_mode < GS3D_TILE_RADIUS || a.tile_mode > GS3D_TILE_ACCUTILE) return GS3D_ERR_ARGUMENT;
     if (a.n == 0 || a.views == 0) return GS3D_OK;
     if (!a.means || !a.quats || !a.scales || !a.opacities || !a.view || !a.projection || !a.intrinsics ||
         !a.centers || !a.conics || !a.radii || !a.tiles || !a.depths)
@@ -1052,16 +1085,12 @@ extern "C" int gs3d_project_fwd(const gs3d_project_args* args, void* stream) {
         return GS3D_ERR_ARGUMENT;
     if (a.means2d && (!a.meta_opacities || !a.meta_conics)) return GS3D_ERR_ARGUMENT;
     hipStream_t s = gs3d::as_stream(stream);
-    if (!a.sh) return gs3d::launch_project_fwd<-1>(a, s);
-    if (a.sh_degree < 0 || a.sh_degree > 3 || a.sh_rows < (a.sh_degree + 1) * (a.sh_degree + 1) || !a.colors ||
-        (a.sh_degree > 0 && !a.camera_centers))
-        return GS3D_ERR_ARGUMENT;
-    switch (a.sh_degree) {
-    case 0: return gs3d::launch_project_fwd<0>(a, s);
-    case 1: return gs3d::launch_project_fwd<1>(a, s);
-    case 2: return gs3d::launch_project_fwd<2>(a, s);
-    default: return gs3d::launch_project_fwd<3>(a, s);
-    }
+    const int status = gs3d::project_fwd(a, s);
+    if (status != GS3D_OK || a.tile_mode == GS3D_TILE_RADIUS) return status;
+    const int64_t rows = (int64_t)a.n * a.views;
+    hipLaunchKernelGGL(gs3d::footprint_tiles_kernel, dim3(gs3d::blocks_for(rows, 256)), dim3(256), 0, s, a.centers,
+                       a.conics, a.radii, rows, (a.width + 15) / 16, (a.height + 15) / 16, a.tile_mode, a.tiles);
+    return gs3d::launch_status("gs3d_project_fwd");
 }
 
 extern "C" int gs3d_project_bwd(const gs3d_project_bwd_args* args, void* stream) {

@@ -3,10 +3,12 @@
 Same signature, defaults, validation errors, outputs and ``meta`` keys.  Per
 Gaussian batch the host issues: one camera launch, one fused projection
 (+SH +metadata) launch for all cameras, the depth ordering of all
-(camera, Gaussian) rows with the scan of their tile counts, ONE host
-synchronisation (camera status codes and the pair count together), pair
-emission in depth order, one stable radix sort of all cameras' pairs on the
-tile id, ranges, and one blend launch for all cameras.
+(camera, Gaussian) rows with their 8x8-tile group counts, ONE host
+synchronisation (camera status codes and the group/pair totals together),
+the grouped binning that writes every tile's depth-ordered list without
+sorting the pairs, and one blend launch for all cameras.  ``tile_mode``
+selects the reference's radius squares, SnugBox rectangles or AccuTile
+strips (splatting/intersections.py).
 """
 
 from dataclasses import dataclass, field
@@ -21,8 +23,7 @@ from .autograd import Frame, Rasterize
 from .projection import project_views
 from ..cameras import validate_camera_options
 from ..inputs import batch_item, normalize_inputs
-from ..splatting.binning import (check_pair_counts, finish_binning, order_rows, require_radius_mode,
-                                 validate_tile_mode)
+from ..splatting.binning import check_pair_counts, finish_binning, order_rows, validate_tile_mode
 from ..splatting.cameras import launch_prepare, raise_camera_errors
 from ..statistics import StatisticsRequest, prepare_statistics
 from ..training import prepare_training_metadata
@@ -54,22 +55,23 @@ class RasterizationResult:
 
 @torch.no_grad()
 def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height, near, far, radius_clip,
-                   sh, sh_degree, background) -> Frame:
+                   sh, sh_degree, background, tile_mode="radius") -> Frame:
     """Camera rows, fused projection, depth order, one synchronisation, binning."""
     with_centers = sh_degree is not None and sh_degree > 0
     full, inverse, centers, errors = launch_prepare(viewmats, Ks, width, height, with_centers)
     state = project_views(
         means, quats, scales, opacities, viewmats, full, Ks, width, height, near, far, radius_clip,
         sh=sh if sh_degree is not None else None, sh_degree=sh_degree or 0,
-        camera_centers=centers if with_centers else None, metadata=True,
+        camera_centers=centers if with_centers else None, metadata=True, tile_mode=tile_mode,
     )
-    order, offsets, totals = order_rows(state.centers, state.radii, state.depths, width, height)
+    order, offsets, totals = order_rows(state.centers, state.radii, state.depths, width, height,
+                                        conics=state.conics, tile_mode=tile_mode)
     host = torch.cat([errors.to(torch.int64), totals]).cpu().tolist()
     raise_camera_errors(host[:-2])
     group_pairs, count = int(host[-2]), int(host[-1])
     check_pair_counts(group_pairs, count)
     bins = finish_binning(state.centers, state.radii, order, offsets, group_pairs, count, state.depths, width,
-                          height)
+                          height, conics=state.conics, tile_mode=tile_mode)
     return Frame(
         width, height, Ks.detach(), full, inverse if with_centers else None, centers if with_centers else None,
         state, bins["ranges"], bins["point_list"], count, sh_degree, background,
@@ -129,7 +131,6 @@ def rasterize(
         means, quats, scales, opacities, features if sh_coeffs is None else sh_coeffs, viewmats, Ks,
         backgrounds, extra_features, None, sh_degree,
     )
-    require_radius_mode(tile_mode)
     frames: list[Frame] = []
     dense: dict[str, list[Tensor]] = {n: [] for n in ("radii", "means2d", "opacities", "tiles_per_gauss", "conics")}
     for b in range(layout.batch_count):
@@ -138,7 +139,7 @@ def rasterize(
             layout.means[b], layout.quats[b], layout.scales[b], layout.opacities[b],
             batch_item(layout.viewmats, b), batch_item(layout.Ks, b), width, height, near_plane, far_plane,
             radius_clip, colors if sh_degree is not None else None, sh_degree,
-            None if layout.backgrounds is None else batch_item(layout.backgrounds, b),
+            None if layout.backgrounds is None else batch_item(layout.backgrounds, b), tile_mode,
         )
         frames.append(frame)
         st = frame.state

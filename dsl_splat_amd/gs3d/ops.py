@@ -16,7 +16,7 @@ from .cameras import ViewConfig, prepare_camera
 from ..cameras import PinholeCamera
 from ..inputs import check_tensor, spherical_harmonics
 from ..primitives.tiling import TileBins
-from ..splatting.binning import bin_and_sort as _bin_arrays, require_radius_mode, validate_tile_mode
+from ..splatting.binning import bin_and_sort as _bin_arrays, validate_tile_mode
 from ..statistics import PreparedStatistics, StatisticsRequest, prepare_statistics
 
 
@@ -51,7 +51,8 @@ class _Project(torch.autograd.Function):
     def forward(ctx: Any, means, quats, scales, opacities, view, full, intrinsics, config: ViewConfig,
                 grad_enabled: bool):
         state = projection.project_views(means, quats, scales, opacities, view[None], full[None], intrinsics[None],
-                                         config.width, config.height, config.near, config.far, config.radius_clip)
+                                         config.width, config.height, config.near, config.far, config.radius_clip,
+                                         tile_mode=config.tile_mode)
         centers, conics, radii, tiles, depths = (state.centers[0], state.conics[0], state.radii[0],
                                                  state.tile_counts[0], state.depths[0])
         if grad_enabled and any(ctx.needs_input_grad[:6]):
@@ -123,7 +124,6 @@ def prepare_gaussians(means: Tensor, quats: Tensor, scales: Tensor, opacities: T
     if view.device != device:
         raise ValueError("camera and Gaussians must use the same CUDA device")
     config = replace(config, tile_mode=tile_mode)
-    require_radius_mode(tile_mode)
     centers, conics, radii, tiles, depths = _Project.apply(
         means.contiguous(), normalize(quats, dim=-1).contiguous(), scales.contiguous(), opacities.contiguous(), view,
         full, intrinsics, config, torch.is_grad_enabled())

@@ -51,8 +51,10 @@ def _sh_layout(sh: Tensor, views: int) -> tuple[Tensor, int, int]:
 def project_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tensor, view: Tensor,
                   projection: Tensor, intrinsics: Tensor, width: int, height: int, near: float, far: float,
                   radius_clip: float, *, sh: Tensor | None = None, sh_degree: int = 0,
-                  camera_centers: Tensor | None = None, metadata: bool = False) -> ProjectedViews:
-    """Launch the fused projection for every camera in ``view`` (C,4,4)."""
+                  camera_centers: Tensor | None = None, metadata: bool = False,
+                  tile_mode: str = "radius") -> ProjectedViews:
+    """Launch the fused projection for every camera in ``view`` (C,4,4);
+    ``tile_counts`` follow ``tile_mode`` (gs3d/projection.py:150-161)."""
     device = means.device
     n = len(means)
     views = view.reshape(-1, 4, 4).shape[0]
@@ -66,6 +68,7 @@ def project_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tenso
     a = abi.ProjectArgs()
     a.n, a.views, a.width, a.height = n, views, width, height
     a.near_plane, a.far_plane, a.radius_clip = float(near), float(far), float(radius_clip)
+    a.tile_mode = abi.TILE_MODES[tile_mode]
     means, quats, scales, opacities = (t.contiguous() for t in (means, quats, scales, opacities))
     view, projection, intrinsics = (t.reshape(views, *t.shape[-2:]).contiguous() for t in (view, projection, intrinsics))
     keep += [means, quats, scales, opacities, view, projection, intrinsics]

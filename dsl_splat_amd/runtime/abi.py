@@ -9,7 +9,10 @@ import ctypes
 c_float_p = ctypes.POINTER(ctypes.c_float)
 c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
+
+# Tile modes (GS3D_TILE_*), named as the reference's TileMode literals.
+TILE_MODES = {"radius": 0, "snugbox": 1, "accutile": 2}
 
 GS3D_OK = 0
 GS3D_ERR_ARGUMENT = -1
@@ -59,6 +62,7 @@ class ProjectArgs(ctypes.Structure):
         ("means2d", _P),
         ("meta_opacities", _P),
         ("meta_conics", _P),
+        ("tile_mode", ctypes.c_int32),
     ]
 
 
@@ -110,6 +114,8 @@ class EmitArgs(ctypes.Structure):
         ("offsets", _P),
         ("keys", _P),
         ("values", _P),
+        ("conics", _P),
+        ("tile_mode", ctypes.c_int32),
     ]
 
 
@@ -125,6 +131,8 @@ class OrderArgs(ctypes.Structure):
         ("order", _P),
         ("group_offsets", _P),
         ("totals", _P),
+        ("conics", _P),
+        ("tile_mode", ctypes.c_int32),
     ]
 
 
@@ -142,6 +150,8 @@ class BinArgs(ctypes.Structure):
         ("tile_pairs", ctypes.c_int64),
         ("ranges", _P),
         ("ids", _P),
+        ("conics", _P),
+        ("tile_mode", ctypes.c_int32),
     ]
 
 
@@ -259,7 +269,7 @@ FUNCTIONS = {
     "gs3d_tile_ranges": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
     "gs3d_order_rows_scratch_bytes": (_SZ, [_I64]),
     "gs3d_order_rows": (ctypes.c_int, [ctypes.POINTER(OrderArgs), _P, _SZ, _P]),
-    "gs3d_bin_rows_scratch_bytes": (_SZ, [_I64, _I32, _I32, _I32]),
+    "gs3d_bin_rows_scratch_bytes": (_SZ, [_I64, _I32, _I32, _I32, _I32]),
     "gs3d_bin_rows": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
     "gs3d_pair_tiles": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
     "gs3d_sort_pairs_u32": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),

@@ -1,5 +1,7 @@
-"""Square-tile binning (splatting/binning.py:16-117 of the reference) for one
-or several views at once.
+"""Tile binning (splatting/binning.py:16-117 of the reference) for one or
+several views at once, in the three tile modes of
+splatting/intersections.py: "radius" (3-sigma squares), "snugbox"
+(opacity-aware rectangles) and "accutile" (per-strip ellipse spans).
 
 Rows of all views form one flat array (views*N); a tile of view v has the
 global id v*tiles + y*gx + x and ``ranges`` has one row per (view, tile).
@@ -27,13 +29,11 @@ def validate_tile_mode(mode) -> None:
         raise ValueError("tile_mode must be 'radius', 'snugbox' or 'accutile'")
 
 
-def require_radius_mode(mode) -> None:
+def _mode(mode, conics) -> int:
     validate_tile_mode(mode)
-    if mode != "radius":
-        raise NotImplementedError(
-            f"tile_mode={mode!r} (SnugBox/AccuTile intersections) is not implemented in the HIP "
-            "rasterizer yet; use tile_mode='radius'"
-        )
+    if mode != "radius" and conics is None:
+        raise ValueError("SnugBox/AccuTile require projected conics")
+    return abi.TILE_MODES[mode]
 
 
 def tile_count(width: int, height: int, views: int = 1) -> int:
@@ -42,8 +42,9 @@ def tile_count(width: int, height: int, views: int = 1) -> int:
 
 @torch.no_grad()
 def emit_keys(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, count: int, width: int,
-              height: int) -> tuple[Tensor, Tensor]:
+              height: int, *, conics: Tensor | None = None, tile_mode="radius") -> tuple[Tensor, Tensor]:
     """Keys/ids (2*count storage each) of the (views, N) rows' tile pairs."""
+    mode = _mode(tile_mode, conics)
     device = radii.device
     views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
     keys = torch.empty(2 * count, dtype=torch.int64, device=device)
@@ -55,6 +56,10 @@ def emit_keys(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, c
         a.centers, a.radii, a.depths, a.offsets = (
             native.ptr(centers), native.ptr(radii), native.ptr(depths), native.ptr(offsets))
         a.keys, a.values = native.ptr(keys), native.ptr(ids)
+        a.tile_mode = mode
+        if mode:
+            conics = conics.contiguous()
+            a.conics = native.ptr(conics)
         scratch = _scratch(native.query("gs3d_emit_scratch_bytes", views * n), device)
         native.call("gs3d_emit_keys", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
     return keys, ids
@@ -62,12 +67,12 @@ def emit_keys(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, c
 
 @torch.no_grad()
 def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, count: int, width: int,
-                  height: int) -> TileBins:
+                  height: int, *, conics: Tensor | None = None, tile_mode="radius") -> TileBins:
     """Emit keys for (views, N) rows given inclusive offsets and their total,
     then sort them and extract per-(view, tile) ranges."""
     views = 1 if radii.ndim == 1 else radii.shape[0]
     tiles = tile_count(width, height, views)
-    keys, ids = emit_keys(centers, radii, depths, offsets, count, width, height)
+    keys, ids = emit_keys(centers, radii, depths, offsets, count, width, height, conics=conics, tile_mode=tile_mode)
     ranges = torch.zeros((tiles, 2), dtype=torch.int32, device=radii.device)
     if count:
         sort_pairs(keys, ids, count, 32 + int(tiles).bit_length())
@@ -76,12 +81,13 @@ def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tenso
 
 
 @torch.no_grad()
-def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int,
-               height: int) -> tuple[Tensor, Tensor, Tensor]:
+def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, height: int, *,
+               conics: Tensor | None = None, tile_mode="radius") -> tuple[Tensor, Tensor, Tensor]:
     """Depth order of the (views, N) rows.
 
     Returns (ordered row records with 2*rows storage, inclusive group
     offsets, totals = [group pairs, tile pairs]), all left on the device."""
+    mode = _mode(tile_mode, conics)
     device = radii.device
     views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
     rows = views * n
@@ -93,6 +99,10 @@ def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int,
     depths, centers, radii = depths.contiguous(), centers.contiguous(), radii.contiguous()
     a.depths, a.centers, a.radii = native.ptr(depths), native.ptr(centers), native.ptr(radii)
     a.order, a.group_offsets, a.totals = native.ptr(order), native.ptr(offsets), native.ptr(totals)
+    a.tile_mode = mode
+    if mode:
+        conics = conics.contiguous()
+        a.conics = native.ptr(conics)
     scratch = _scratch(native.query("gs3d_order_rows_scratch_bytes", rows), device)
     native.call("gs3d_order_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
     return order, offsets, totals
@@ -105,9 +115,11 @@ def check_pair_counts(group_pairs: int, tile_pairs: int) -> None:
 
 @torch.no_grad()
 def bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, group_pairs: int, tile_pairs: int,
-             width: int, height: int) -> tuple[Tensor, Tensor]:
+             width: int, height: int, *, conics: Tensor | None = None,
+             tile_mode="radius") -> tuple[Tensor, Tensor]:
     """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs)
-    of rows ordered by ``order_rows``."""
+    of rows ordered by ``order_rows`` (same conics and tile mode)."""
+    mode = _mode(tile_mode, conics)
     device = order.device
     views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
     check_pair_counts(group_pairs, tile_pairs)
@@ -120,7 +132,11 @@ def bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, gro
     a.order, a.group_offsets = native.ptr(order), native.ptr(offsets)
     a.group_pairs, a.tile_pairs = group_pairs, tile_pairs
     a.ranges, a.ids = native.ptr(ranges), native.ptr(ids)
-    scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, views, width, height), device)
+    a.tile_mode = mode
+    if mode:
+        conics = conics.contiguous()
+        a.conics = native.ptr(conics)
+    scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, views, width, height, mode), device)
     native.call("gs3d_bin_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
     return ranges, ids
 
@@ -149,10 +165,12 @@ def expand_keys(sorted_tiles: Tensor, ids: Tensor, count: int, depths: Tensor, w
 
 @torch.no_grad()
 def finish_binning(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, group_pairs: int,
-                   tile_pairs: int, depths: Tensor, width: int, height: int, *, with_keys: bool = False) -> TileBins:
+                   tile_pairs: int, depths: Tensor, width: int, height: int, *, with_keys: bool = False,
+                   conics: Tensor | None = None, tile_mode="radius") -> TileBins:
     """Tile lists and ranges once the host has read the totals of
     ``order_rows``."""
-    ranges, ids = bin_rows(centers, radii, order, offsets, group_pairs, tile_pairs, width, height)
+    ranges, ids = bin_rows(centers, radii, order, offsets, group_pairs, tile_pairs, width, height, conics=conics,
+                           tile_mode=tile_mode)
     bins: TileBins = dict(point_list=ids, ranges=ranges)
     if with_keys:
         bins["point_list_keys"] = expand_keys(pair_tiles(ranges, tile_pairs), ids, tile_pairs, depths, width, height)
@@ -166,11 +184,10 @@ def bin_and_sort(centers: Tensor, radii: Tensor, tile_counts: Tensor, depths: Te
     """Bin one view's (N,) or several views' (C, N) projected Gaussians into
     depth-sorted per-tile lists (same order and ranges as the reference's
     scan + duplicate + 64-bit key sort).  ``tile_counts`` is accepted for
-    the reference's signature; the counts follow from centers and radii."""
-    if tile_mode != "radius" and conics is None:
-        raise ValueError("SnugBox/AccuTile require projected conics")
-    require_radius_mode(tile_mode)
-    order, offsets, totals = order_rows(centers, radii, depths, width, height)
+    the reference's signature; the counts follow from centers, radii and,
+    outside the radius mode, conics."""
+    _mode(tile_mode, conics)
+    order, offsets, totals = order_rows(centers, radii, depths, width, height, conics=conics, tile_mode=tile_mode)
     group_pairs, tile_pairs = totals.cpu().tolist()
     return finish_binning(centers, radii, order, offsets, group_pairs, tile_pairs, depths, width, height,
-                          with_keys=with_keys)
+                          with_keys=with_keys, conics=conics, tile_mode=tile_mode)

@@ -74,6 +74,16 @@ int gs3d_camera_backward(const float* Ks, const float* grad_full,
  * means2d != NULL also splatting/metadata.py:12-31 (_prepare, :296-311).
  * Culled rows get radii = tiles = 0 and zeros in centers/conics/depths.
  * ---------------------------------------------------------------------- */
+/* Tile modes (splatting/intersections.py:21-26, gs3d/cameras.py:20-22):
+ * RADIUS lists the square of 3-sigma tiles (the original 3DGS rule); SNUGBOX
+ * the rectangle of the opacity-aware alpha >= 1/255 ellipse inside it
+ * (footprint, intersections.py:46-116); ACCUTILE, per strip of tiles along
+ * the shorter side of that rectangle, only the tiles the ellipse crosses
+ * (visit, :160-218).  Every mode keeps all pixels the blend accepts. */
+#define GS3D_TILE_RADIUS 0
+#define GS3D_TILE_SNUGBOX 1
+#define GS3D_TILE_ACCUTILE 2
+
 typedef struct gs3d_project_args {
     int32_t n;            /* Gaussians */
     int32_t views;        /* cameras handled by this launch */
@@ -102,6 +112,7 @@ typedef struct gs3d_project_args {
     float* means2d;           /* (views,N,2) */
     float* meta_opacities;    /* (views,N) */
     float* meta_conics;       /* (views,N,3) */
+    int32_t tile_mode;        /* GS3D_TILE_*: what tiles (views,N) counts (projection.py:150-161) */
 } gs3d_project_args;
 
 int gs3d_project_fwd(const gs3d_project_args* args, void* stream);
@@ -194,6 +205,8 @@ typedef struct gs3d_emit_args {
     const int32_t* offsets;   /* (views*N) inclusive scan of tiles */
     uint64_t* keys;           /* (M) */
     int32_t* values;          /* (M) */
+    const float* conics;      /* (views,N,4); required unless tile_mode is GS3D_TILE_RADIUS */
+    int32_t tile_mode;        /* GS3D_TILE_* (splatting/binning.py:40-68 duplicate_precise) */
 } gs3d_emit_args;
 
 size_t gs3d_emit_scratch_bytes(int64_t rows);
@@ -252,6 +265,8 @@ typedef struct gs3d_order_args {
     uint64_t* order;          /* (2*views*N): first half receives the ordered records */
     int32_t* group_offsets;   /* (views*N) inclusive scan of group counts, record order */
     int64_t* totals;          /* (2) group pairs, tile pairs */
+    const float* conics;      /* (views,N,4); required unless tile_mode is GS3D_TILE_RADIUS */
+    int32_t tile_mode;        /* GS3D_TILE_* */
 } gs3d_order_args;
 
 size_t gs3d_order_rows_scratch_bytes(int64_t rows);
@@ -267,9 +282,12 @@ typedef struct gs3d_bin_args {
     int64_t tile_pairs;            /* totals[1] */
     int32_t* ranges;               /* (views*tiles,2), every entry written */
     int32_t* ids;                  /* (tile_pairs) Gaussian index within its view */
+    const float* conics;           /* (views,N,4), as given to gs3d_order_rows */
+    int32_t tile_mode;             /* the tile_mode given to gs3d_order_rows */
 } gs3d_bin_args;
 
-size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t width, int32_t height);
+size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t width, int32_t height,
+                                   int32_t tile_mode);
 int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream);
 
 /* Global tile id of every listed pair: tiles[p] = t for p in ranges[t]. */

@@ -50,6 +50,8 @@ def lib() -> ctypes.CDLL:
             "oracle_sort_pairs_u64": [P, P, I64, I32],
             "oracle_tile_ranges": [P, I64, P, I64],
             "oracle_render_fwd": [ctypes.POINTER(abi.RenderArgs)],
+            "oracle_tile_footprint": [I32, P, P, I32, I32, I32, P, P],
+            "oracle_logf": [ctypes.c_float],
             "oracle_render_fwd_stats": [ctypes.POINTER(abi.RenderArgs), ctypes.POINTER(abi.RenderStatsArgs)],
             "oracle_render_bwd": [ctypes.POINTER(abi.RenderBwdArgs)],
             "oracle_projection_loss_f64": [P, P, P, D, P, P, I32, I32, D, D, P, P],
@@ -64,6 +66,7 @@ def lib() -> ctypes.CDLL:
         _lib.oracle_projection_loss_f64.restype = ctypes.c_double
         _lib.oracle_expf.argtypes = [ctypes.c_float]
         _lib.oracle_expf.restype = ctypes.c_float
+        _lib.oracle_logf.restype = ctypes.c_float
         _lib.oracle_sh_basis.argtypes = [P, I32]
         _lib.oracle_sh_basis.restype = ctypes.c_float
         _lib.oracle_set_threads.argtypes = [ctypes.c_int]
@@ -143,7 +146,7 @@ def camera_backward(Ks, grad_full, width, height, inverse, grad_centers):
 
 def project_fwd(means, quats, scales, opacities, view, projection, intrinsics, width, height,
                 near_plane=0.2, far_plane=float("inf"), radius_clip=0.0,
-                sh=None, sh_degree=0, camera_centers=None, metadata=False):
+                sh=None, sh_degree=0, camera_centers=None, metadata=False, tile_mode="radius"):
     """gs3d/projection.py:89-164 for every view; returns a dict of arrays."""
     means, quats, scales, opacities = _f32(means), _f32(quats), _f32(scales), _f32(opacities)
     view, projection, intrinsics = (
@@ -159,6 +162,7 @@ def project_fwd(means, quats, scales, opacities, view, projection, intrinsics, w
     a = abi.ProjectArgs()
     a.n, a.views, a.width, a.height = n, c, width, height
     a.near_plane, a.far_plane, a.radius_clip = near_plane, far_plane, radius_clip
+    a.tile_mode = abi.TILE_MODES[tile_mode]
     for name, arr in (("means", means), ("quats", quats), ("scales", scales), ("opacities", opacities),
                       ("view", view), ("projection", projection), ("intrinsics", intrinsics)):
         setattr(a, name, _ptr(arr))
@@ -262,8 +266,8 @@ def scan_i32(counts):
     return offsets, int(total.value)
 
 
-def emit_keys(centers, radii, depths, offsets, total, width, height):
-    """splatting/binning.py:16-37 over (views, N) rows."""
+def emit_keys(centers, radii, depths, offsets, total, width, height, conics=None, tile_mode="radius"):
+    """splatting/binning.py:16-37 (:40-68 outside the radius mode) over (views, N) rows."""
     centers = _f32(centers)
     c, n = centers.shape[0], centers.shape[1]
     radii, depths, offsets = _i32(radii).reshape(c, n), _f32(depths).reshape(c, n), _i32(offsets).reshape(-1)
@@ -273,8 +277,29 @@ def emit_keys(centers, radii, depths, offsets, total, width, height):
     a.n, a.views, a.width, a.height = n, c, width, height
     a.centers, a.radii, a.depths, a.offsets = _ptr(centers), _ptr(radii), _ptr(depths), _ptr(offsets)
     a.keys, a.values = _ptr(keys), _ptr(values)
+    a.tile_mode = abi.TILE_MODES[tile_mode]
+    if tile_mode != "radius":
+        conics = _f32(conics).reshape(c, n, 4)
+        a.conics = _ptr(conics)
     lib().oracle_emit_keys(ctypes.byref(a))
     return keys, values
+
+
+def tile_footprint(mode, center, conic, radius, gx, gy):
+    """splatting/intersections.py:46-218 for one projected Gaussian: (bounds
+    x0, y0, x1, y1 of the mode's rectangle, listed tile indices in traversal
+    order)."""
+    center, conic = _f32(center).reshape(2), _f32(conic).reshape(4)
+    tiles = np.zeros(max(1, gx * gy), np.int64)
+    bounds = np.zeros(4, np.int32)
+    count = lib().oracle_tile_footprint(abi.TILE_MODES[mode], _ptr(center), _ptr(conic), int(radius), gx, gy,
+                                        _ptr(tiles), _ptr(bounds))
+    return bounds, tiles[:count].copy()
+
+
+def logf(x: float) -> float:
+    """The float32 natural log of the SnugBox/AccuTile alpha level."""
+    return float(lib().oracle_logf(float(x)))
 
 
 def sort_pairs(keys, values, end_bit):

@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <limits>
 #include <cstdint>
 #include <cstring>
 #include <numeric>
@@ -62,6 +63,50 @@ inline float gs_expf(float x) {
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
     return ldexpf(p, (int)k);
+}
+
+// ---------------------------------------------------------------------------
+// Natural log of the alpha level used by the SnugBox/AccuTile footprint
+// (splatting/intersections.py:68 calls wp.log).  Fixed sequence of IEEE
+// double operations, rounded to float once: x = m * 2^e with m in
+// [sqrt(1/2), sqrt(2)), ln m = 2 atanh(s), s = (m - 1)/(m + 1), |s| <= 0.1716,
+// atanh by its Taylor series through s^23 (truncation below 1e-19).
+// ---------------------------------------------------------------------------
+inline float gs_logf(float x) {
+    if (std::isnan(x) || x < 0.0f) return std::numeric_limits<float>::quiet_NaN();
+    if (x == 0.0f) return -std::numeric_limits<float>::infinity();
+    if (std::isinf(x)) return x;
+    int e = 0;
+    if (x < 1.17549435e-38f) {  // subnormal: scale into the normal range
+        x *= 18446744073709551616.0f;  // 2^64
+        e = -64;
+    }
+    uint32_t bits;
+    std::memcpy(&bits, &x, 4);
+    e += (int)(bits >> 23) - 127;
+    bits = (bits & 0x007FFFFFu) | 0x3F800000u;  // mantissa in [1, 2)
+    float mf;
+    std::memcpy(&mf, &bits, 4);
+    double m = (double)mf;
+    if (m > 1.4142135623730951) {
+        m = m * 0.5;
+        e += 1;
+    }
+    const double s = (m - 1.0) / (m + 1.0);
+    const double s2 = s * s;
+    double p = 1.0 / 23.0;
+    p = p * s2 + 1.0 / 21.0;
+    p = p * s2 + 1.0 / 19.0;
+    p = p * s2 + 1.0 / 17.0;
+    p = p * s2 + 1.0 / 15.0;
+    p = p * s2 + 1.0 / 13.0;
+    p = p * s2 + 1.0 / 11.0;
+    p = p * s2 + 1.0 / 9.0;
+    p = p * s2 + 1.0 / 7.0;
+    p = p * s2 + 1.0 / 5.0;
+    p = p * s2 + 1.0 / 3.0;
+    p = p * s2 + 1.0;
+    return (float)(2.0 * s * p + (double)e * 0.6931471805599453);
 }
 
 // ---------------------------------------------------------------------------
@@ -214,6 +259,138 @@ inline void tile_bounds(const float c[2], int radius, int gx, int gy, int b[4]) 
     b[3] = trunc_clamp(((c[1] + r) + 16.0f - 1.0f) / 16.0f, gy);
 }
 
+// ---------------------------------------------------------------------------
+// SnugBox / AccuTile intersections, splatting/intersections.py:46-218,
+// restated step by step (float32 unless the reference converts).
+// ---------------------------------------------------------------------------
+struct Ellipse {
+    float center[2] = {0.0f, 0.0f};
+    float conic[3] = {0.0f, 0.0f, 0.0f};
+    float level = 0.0f, determinant = 0.0f;
+    float extent[2] = {0.0f, 0.0f};
+    int bounds[4] = {0, 0, 0, 0};
+    bool precise = false;
+};
+
+inline float clampf(float x, float lo, float hi) { return std::min(std::max(x, lo), hi); }
+
+// intersections.py:46-116 footprint.
+Ellipse footprint(const float center[2], const float conic[4], int radius, int gx, int gy) {
+    Ellipse r;
+    r.center[0] = center[0];
+    r.center[1] = center[1];
+    r.conic[0] = conic[0];
+    r.conic[1] = conic[1];
+    r.conic[2] = conic[2];
+    tile_bounds(center, radius, gx, gy, r.bounds);
+    const float a = conic[0], b = conic[1], c = conic[2];
+    const float det = (float)((double)a * (double)c - (double)b * (double)b);
+    if (conic[3] < 1.0f / 255.0f) {
+        r.bounds[0] = r.bounds[1] = r.bounds[2] = r.bounds[3] = 0;
+        return r;
+    }
+    if (!(a > 0.0f && c > 0.0f && det > 0.0f)) return r;
+    const float level = 2.0f * gs_logf(conic[3] * 255.0f);
+    const float reach = (float)radius + 32.0f;
+    const float roundoff = 9.5367431640625e-07f * ((a + 2.0f * std::fabs(b) + c) * reach * reach + std::fabs(level) + 1.0f);
+    r.level = std::max(0.0f, level) + roundoff;
+    r.determinant = det;
+    r.extent[0] = sqrtf(r.level * c / det);
+    r.extent[1] = sqrtf(r.level * a / det);
+    if (!(std::isfinite(r.extent[0]) && std::isfinite(r.extent[1]))) return r;
+    const int lo_x = (int)clampf(floorf((center[0] - r.extent[0]) / 16.0f), 0.0f, (float)gx);
+    const int lo_y = (int)clampf(floorf((center[1] - r.extent[1]) / 16.0f), 0.0f, (float)gy);
+    const int hi_x = (int)clampf(floorf((center[0] + r.extent[0]) / 16.0f) + 1.0f, 0.0f, (float)gx);
+    const int hi_y = (int)clampf(floorf((center[1] + r.extent[1]) / 16.0f) + 1.0f, 0.0f, (float)gy);
+    r.bounds[0] = std::max(r.bounds[0], lo_x);
+    r.bounds[1] = std::max(r.bounds[1], lo_y);
+    r.bounds[2] = std::min(r.bounds[2], hi_x);
+    r.bounds[3] = std::min(r.bounds[3], hi_y);
+    r.precise = true;
+    return r;
+}
+
+// intersections.py:119-130: where the line u = 16*line meets the ellipse.
+void line_intersection(const Ellipse& e, int line, bool is_y, float out[2]) {
+    float u = e.center[0], v = e.center[1];
+    const float b = e.conic[1];
+    float c = e.conic[2], extent_u = e.extent[0];
+    if (is_y) {
+        std::swap(u, v);
+        c = e.conic[0];
+        extent_u = e.extent[1];
+    }
+    const float h = clampf((float)(line * 16) - u, -extent_u, extent_u);
+    const float root = sqrtf(std::max(0.0f, e.level * c - e.determinant * h * h));
+    out[0] = v + (-b * h - root) / c;
+    out[1] = v + (-b * h + root) / c;
+}
+
+// intersections.py:133-157: tile span of strip `row`.
+void strip_span(const Ellipse& e, int row, bool is_y, const float low[2], const float high[2], int out[2]) {
+    float u = e.center[0], v = e.center[1];
+    float a = e.conic[0];
+    const float b = e.conic[1];
+    float extent = e.extent[1];
+    int lower = e.bounds[1], upper = e.bounds[3];
+    if (is_y) {
+        std::swap(u, v);
+        a = e.conic[2];
+        extent = e.extent[0];
+        lower = e.bounds[0];
+        upper = e.bounds[2];
+    }
+    float lo = std::min(low[0], high[0]), hi = std::max(low[1], high[1]);
+    const float arg_min = b * extent / a, arg_max = -b * extent / a;
+    const float h0 = (float)(row * 16) - u, h1 = (float)((row + 1) * 16) - u;
+    if (h0 <= arg_min && arg_min <= h1) lo = v - extent;
+    if (h0 <= arg_max && arg_max <= h1) hi = v + extent;
+    out[0] = (int)clampf(floorf(lo / 16.0f), (float)lower, (float)upper);
+    out[1] = (int)clampf(floorf(hi / 16.0f) + 1.0f, (float)lower, (float)upper);
+}
+
+// intersections.py:160-218 visit: the tiles of one projected Gaussian in the
+// reference's traversal order; returns the count and, when `tiles` is
+// non-null, writes the tile indices (row-major within the view).
+int visit_tiles(int mode, const float center[2], const float conic[4], int radius, int gx, int gy,
+                int64_t* tiles) {
+    Ellipse e;
+    tile_bounds(center, radius, gx, gy, e.bounds);
+    if (mode != GS3D_TILE_RADIUS) e = footprint(center, conic, radius, gx, gy);
+    const int* bounds = e.bounds;
+    const int nx = std::max(0, bounds[2] - bounds[0]), ny = std::max(0, bounds[3] - bounds[1]);
+    if (nx == 0 || ny == 0) return 0;
+    bool is_y = true;
+    if (mode == GS3D_TILE_ACCUTILE) is_y = ny < nx;
+    int start = bounds[1], end = bounds[3];
+    if (!is_y) {
+        start = bounds[0];
+        end = bounds[2];
+    }
+    if (mode != GS3D_TILE_ACCUTILE && !tiles) return nx * ny;
+    float low[2] = {0.0f, 0.0f}, high[2];
+    if (mode == GS3D_TILE_ACCUTILE && e.precise) line_intersection(e, start, is_y, low);
+    int count = 0;
+    for (int row = start; row < end; ++row) {
+        int span[2] = {bounds[0], bounds[2]};
+        if (!is_y) {
+            span[0] = bounds[1];
+            span[1] = bounds[3];
+        }
+        if (mode == GS3D_TILE_ACCUTILE && e.precise) {
+            line_intersection(e, row + 1, is_y, high);
+            strip_span(e, row, is_y, low, high, span);
+            low[0] = high[0];
+            low[1] = high[1];
+        }
+        if (tiles)
+            for (int col = span[0]; col < span[1]; ++col)
+                tiles[count + col - span[0]] = is_y ? (int64_t)row * gx + col : (int64_t)col * gx + row;
+        count += std::max(0, span[1] - span[0]);
+    }
+    return count;
+}
+
 // gs3d/projection.py:89-164 project, one Gaussian in one view.
 struct ProjOut {
     float center[2], conic[4];
@@ -223,7 +400,7 @@ struct ProjOut {
 
 bool project_one(const float* mean, const float* quat, const float* scale, float opacity,
                  const float* view, const float* proj, const float* K, int width, int height,
-                 float near_plane, float far_plane, float radius_clip, ProjOut& o) {
+                 float near_plane, float far_plane, float radius_clip, ProjOut& o, int tile_mode = GS3D_TILE_RADIUS) {
     o = ProjOut{};
     const M4<float> V = load44<float>(view);
     float t4[4];
@@ -254,6 +431,8 @@ bool project_one(const float* mean, const float* quat, const float* scale, float
     o.conic[3] = opacity;
     o.radius = radius;
     o.tiles = count;
+    if (tile_mode != GS3D_TILE_RADIUS)  // projection.py:150-161
+        o.tiles = visit_tiles(tile_mode, o.center, o.conic, radius, (width + 15) / 16, (height + 15) / 16, nullptr);
     o.depth = t4[2];
     return true;
 }
@@ -724,7 +903,7 @@ int oracle_project_fwd(const gs3d_project_args* a) {
             ProjOut o;
             const bool vis = project_one(a->means + 3 * i, a->quats + 4 * i, a->scales + 3 * i, a->opacities[i],
                                          a->view + 16 * v, a->projection + 16 * v, a->intrinsics + 9 * v, a->width,
-                                         a->height, a->near_plane, a->far_plane, a->radius_clip, o);
+                                         a->height, a->near_plane, a->far_plane, a->radius_clip, o, a->tile_mode);
             a->centers[2 * row] = o.center[0];
             a->centers[2 * row + 1] = o.center[1];
             for (int k = 0; k < 4; ++k) a->conics[4 * row + k] = o.conic[k];
@@ -890,6 +1069,18 @@ int oracle_projection_vjp_f64(const double* mean, const double* quat, const doub
 // Forward intermediates for the custom-adjoint known-answer tests.
 float oracle_expf(float x) { return gs_expf(x); }
 
+float oracle_logf(float x) { return gs_logf(x); }
+
+int oracle_tile_footprint(int32_t mode, const float* center, const float* conic, int32_t radius, int32_t gx,
+                          int32_t gy, int64_t* tiles, int32_t* bounds) {
+    Ellipse e;
+    tile_bounds(center, radius, gx, gy, e.bounds);
+    if (mode != GS3D_TILE_RADIUS) e = footprint(center, conic, radius, gx, gy);
+    if (bounds)
+        for (int k = 0; k < 4; ++k) bounds[k] = e.bounds[k];
+    return visit_tiles(mode, center, conic, radius, gx, gy, tiles);
+}
+
 int oracle_glm_rotation(const float* q, float* out) {
     M3<float> R = glm_rotation<float>(q);
     for (int i = 0; i < 9; ++i) out[i] = R.m[i / 3][i % 3];
@@ -914,14 +1105,30 @@ int oracle_scan_i32(const int32_t* counts, int64_t n, int32_t* offsets, int64_t*
     return 0;
 }
 
-// splatting/binning.py:16-37 duplicate + primitives/tiling.py:32-36 sort_key.
+// splatting/binning.py:16-37 duplicate (:40-68 duplicate_precise for the
+// SnugBox/AccuTile modes) + primitives/tiling.py:32-36 sort_key.
 int oracle_emit_keys(const gs3d_emit_args* a) {
     const int gx = (a->width + 15) / 16, gy = (a->height + 15) / 16;
     const int64_t tiles_per_view = (int64_t)gx * gy;
     const int64_t rows = (int64_t)a->n * a->views;
+    std::vector<int64_t> tiles;
     for (int64_t r = 0; r < rows; ++r) {
         if (a->radii[r] <= 0) continue;
         const int64_t v = r / a->n;
+        if (a->tile_mode != GS3D_TILE_RADIUS) {
+            tiles.resize((size_t)gx * gy);
+            const int count = visit_tiles(a->tile_mode, a->centers + 2 * r, a->conics + 4 * r, a->radii[r], gx, gy,
+                                          tiles.data());
+            const int64_t off = r > 0 ? a->offsets[r - 1] : 0;
+            uint32_t bits;
+            std::memcpy(&bits, a->depths + r, 4);
+            for (int k = 0; k < count; ++k) {
+                const uint64_t tile = (uint64_t)(uint32_t)(v * tiles_per_view + tiles[k]);
+                a->keys[off + k] = (tile << 32) | (uint64_t)bits;
+                a->values[off + k] = (int32_t)(r % a->n);
+            }
+            continue;
+        }
         int b[4];
         tile_bounds(a->centers + 2 * r, a->radii[r], gx, gy, b);
         int64_t off = r > 0 ? a->offsets[r - 1] : 0;

@@ -32,7 +32,9 @@ def test_library_exports_every_declared_symbol():
     assert native.query("gs3d_sort_scratch_bytes", 1 << 20) > 0
     assert native.query("gs3d_scan_scratch_bytes", 0) >= 0
     assert native.query("gs3d_order_rows_scratch_bytes", 1000) > 0
-    assert native.query("gs3d_bin_rows_scratch_bytes", 10_000, 4, 1920, 1080) > 0
+    assert native.query("gs3d_bin_rows_scratch_bytes", 10_000, 4, 1920, 1080, 0) > 0
+    assert native.query("gs3d_bin_rows_scratch_bytes", 10_000, 4, 1920, 1080, 2) > \
+        native.query("gs3d_bin_rows_scratch_bytes", 10_000, 4, 1920, 1080, 0)
 
 
 def test_argument_errors_are_reported_without_launching():

@@ -8,15 +8,15 @@ import torch_ref
 from dsl_splat_amd import synthetic
 
 
-def _pipeline(oracle_lib, scene, features=None, background=None, extra=None):
+def _pipeline(oracle_lib, scene, features=None, background=None, extra=None, tile_mode="radius"):
     full, inverse, cent, err = oracle_lib.camera_prepare(scene.viewmats.numpy(), scene.Ks.numpy(),
                                                          scene.width, scene.height, False)
     out = oracle_lib.project_fwd(scene.means.numpy(), scene.quats.numpy(), scene.scales.numpy(),
                                  scene.opacities.numpy(), scene.viewmats.numpy(), full, scene.Ks.numpy(),
-                                 scene.width, scene.height)
+                                 scene.width, scene.height, tile_mode=tile_mode)
     offsets, total = oracle_lib.scan_i32(out["tiles"].ravel())
     keys, vals = oracle_lib.emit_keys(out["centers"], out["radii"], out["depths"], offsets, total,
-                                      scene.width, scene.height)
+                                      scene.width, scene.height, conics=out["conics"], tile_mode=tile_mode)
     views = scene.viewmats.shape[0]
     T = views * ((scene.width + 15) // 16) * ((scene.height + 15) // 16)
     sk, sv = oracle_lib.sort_pairs(keys, vals, 32 + int(T).bit_length())
