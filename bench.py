@@ -52,6 +52,10 @@ def parse():
     p.add_argument("--n", type=int, default=None, help="override the Gaussian count")
     p.add_argument("--stage-reps", type=int, default=5)
     p.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
+    p.add_argument("--tile-mode", choices=("radius", "snugbox", "accutile"), default="radius",
+                   help="tile mode of the timed steps (the headline is the reference's default, radius)")
+    p.add_argument("--mode-steps", type=int, default=5,
+                   help="steps timed in each of the other tile modes (0 skips them)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="also run one elementwise device copy (out = in * 1) of this many MiB, the known-size "
                         "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
@@ -81,7 +85,7 @@ def make_inputs(workload, n, device):
     return scene, leaves, colors, extra, viewmats
 
 
-def step_fn(scene, leaves, colors, extra, viewmats):
+def step_fn(scene, leaves, colors, extra, viewmats, tile_mode="radius"):
     from dsl_splat_amd import gs3d
 
     sh = scene.sh_coeffs is not None
@@ -91,7 +95,8 @@ def step_fn(scene, leaves, colors, extra, viewmats):
         res = gs3d.rasterize(leaves["means"], leaves["quats"], leaves["scales"], leaves["opacities"], viewmats,
                              scene.Ks, scene.width, scene.height, features=None if sh else colors,
                              sh_coeffs=colors if sh else None, sh_degree=scene.sh_degree,
-                             extra_features=extra, absgrad=scene.absgrad)
+                             extra_features=extra, absgrad=scene.absgrad, tile_mode=tile_mode)
+        forward.pairs = res.meta["tiles_per_gauss"].sum()
         D = res.features.shape[-1]
         loss = (res.features * W[..., :D]).sum() + (res.alpha * W[..., -1:]).sum()
         if res.extra_features is not None:
@@ -292,7 +297,7 @@ def main():
     torch.cuda.set_device(device)
     log(f"[bench] building inputs: {args.workload}")
     scene, leaves, colors, extra, viewmats = make_inputs(args.workload, args.n, device)
-    forward, backward = step_fn(scene, leaves, colors, extra, viewmats)
+    forward, backward = step_fn(scene, leaves, colors, extra, viewmats, args.tile_mode)
     log(f"[bench] warmup {args.warmup}")
     for _ in range(args.warmup):
         backward(forward())
@@ -314,6 +319,19 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1000.0 / args.steps
+    modes = {args.tile_mode: dict(ms=round(ms, 3), pairs=int(forward.pairs))}
+    for mode in ("radius", "snugbox", "accutile"):
+        if mode == args.tile_mode or args.mode_steps <= 0:
+            continue
+        log(f"[bench] tile_mode={mode}: {args.mode_steps} steps")
+        f_m, b_m = step_fn(scene, leaves, colors, extra, viewmats, mode)
+        b_m(f_m())
+        torch.cuda.synchronize()
+        ta = time.perf_counter()
+        for _ in range(args.mode_steps):
+            b_m(f_m())
+        torch.cuda.synchronize()
+        modes[mode] = dict(ms=round((time.perf_counter() - ta) * 1000.0 / args.mode_steps, 3), pairs=int(f_m.pairs))
     if args.copy_calibration_mib > 0:
         src = torch.ones(args.copy_calibration_mib << 18, device=device)
         dst = torch.empty_like(src)
@@ -359,7 +377,8 @@ def main():
             "workload": f"{args.workload}: N={len(scene.means)}, {views} cameras, {scene.width}x{scene.height}, "
                         f"SH degree {scene.sh_degree}, fwd+bwd of sum(image*W)",
             "gaussians": len(scene.means), "cameras": views, "width": scene.width, "height": scene.height,
-            "sh_degree": scene.sh_degree, "pairs": info["pairs"], "group_pairs": info["group_pairs"],
+            "sh_degree": scene.sh_degree, "tile_mode": args.tile_mode, "pairs": info["pairs"],
+            "group_pairs": info["group_pairs"],
             "visible_rows": info["visible"],
         },
         "fwd_ms": round(fwd_ms / args.steps, 3),
@@ -378,6 +397,7 @@ def main():
         "stages_1_3": {"ms": round(t13, 4), "bytes": b13, "gbps": round(b13 / (t13 * 1e-3) / 1e9, 1),
                        "frac": round(b13 / (t13 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
         "stages": per_stage,
+        "tile_modes": modes,
         "statistics": {"requests": "masked count + weighted sum, per-view maps",
                        "render_fwd_ms": round(stages["render_fwd_kernel"], 4),
                        "render_fwd_stats_ms": round(stages["render_fwd_stats_kernel"], 4)},

@@ -646,19 +646,47 @@ GS3D_DEV int groups_of(const TileRect& r) {
 
 // Row order: depth-bit keys and records (coalesced reads of depth, centre
 // and radius).
-template <bool PACKED>
+//
+// AccuTile (ACCU): the row's footprint and strips are computed here, once, in
+// row order; on grids of at most 256 x 256 tiles the record's high half
+// carries tiles << 12 | groups and footprints[row] the compact footprint, so
+// the depth-ordered passes neither gather nor recompute it.
+// tiles_out (optional) receives every row's tile count in the mode.
+template <bool PACKED, bool ACCU>
 __global__ void row_records_kernel(const float* __restrict__ depths, RowGeometry g, int64_t rows, int gx, int gy,
-                                   uint32_t* __restrict__ keys, uint64_t* __restrict__ records) {
+                                   uint32_t* __restrict__ keys, uint64_t* __restrict__ records,
+                                   int32_t* __restrict__ tiles_out, float4* __restrict__ footprints) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
     keys[i] = __float_as_uint(depths[i]);
     uint64_t rec = (uint64_t)(uint32_t)i;
-    if constexpr (PACKED) {
-        const TileRect r = row_rect(g, i, gx, gy);
-        const uint32_t p = r.x1 > r.x0 ? (uint32_t)r.x0 | ((uint32_t)r.y0 << 8) | ((uint32_t)(r.x1 - 1) << 16) |
-                                             ((uint32_t)(r.y1 - 1) << 24)
-                                       : kEmptyRect;
-        rec |= (uint64_t)p << 32;
+    if constexpr (ACCU) {
+        int groups = 0, tiles = 0;
+        const int radius = g.radii[i];
+        if (radius > 0) {
+            const Ellipse e = footprint(reinterpret_cast<const float2*>(g.centers)[i],
+                                        reinterpret_cast<const float4*>(g.conics)[i], radius, gx, gy);
+            accutile_groups(e, groups, tiles);
+            if constexpr (PACKED) {
+                float4 p0, p1;
+                pack_ellipse(e, p0, p1);
+                footprints[2 * i] = p0;
+                footprints[2 * i + 1] = p1;
+            }
+        }
+        if constexpr (PACKED) rec |= (uint64_t)(((uint32_t)tiles << 12) | (uint32_t)groups) << 32;
+        if (tiles_out) tiles_out[i] = tiles;
+    } else {
+        if (PACKED || tiles_out) {
+            const TileRect r = row_rect(g, i, gx, gy);
+            if constexpr (PACKED) {
+                const uint32_t p = r.x1 > r.x0 ? (uint32_t)r.x0 | ((uint32_t)r.y0 << 8) |
+                                                     ((uint32_t)(r.x1 - 1) << 16) | ((uint32_t)(r.y1 - 1) << 24)
+                                               : kEmptyRect;
+                rec |= (uint64_t)p << 32;
+            }
+            if (tiles_out) tiles_out[i] = r.x1 > r.x0 ? (r.x1 - r.x0) * (r.y1 - r.y0) : 0;
+        }
     }
     records[i] = rec;
 }
@@ -674,7 +702,11 @@ __global__ __launch_bounds__(kBinThreads) void order_counts_kernel(const uint64_
     const int64_t i = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
     int64_t area = 0;
     if (i < rows) {
-        if constexpr (ACCU) {
+        if constexpr (ACCU && PACKED) {
+            const uint32_t hi = (uint32_t)(records[i] >> 32);
+            area = hi >> 12;
+            group_counts[i] = (int32_t)(hi & 4095u);
+        } else if constexpr (ACCU) {
             const int64_t row = (int64_t)(uint32_t)records[i];
             const int radius = g.radii[row];
             int groups = 0, tiles = 0;
@@ -767,9 +799,13 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
 // each group row's interval (accutile_groups), with the 64-bit mask of the
 // group's tiles its strips cover (bit ly * 8 + lx), in masks[].  The spans
 // of the current group row's 8 strips wait in per-thread LDS slots.
+// PACKED: footprints come from the compact per-row copies written by
+// row_records_kernel (one 32-byte gather), else they are recomputed.
+template <bool PACKED>
 __global__ __launch_bounds__(kBinThreads) void accutile_emit_kernel(const uint64_t* __restrict__ records,
                                                                     const int32_t* __restrict__ offsets, int64_t rows,
-                                                                    RowGeometry geo, int n, GridDims d, int64_t limit,
+                                                                    RowGeometry geo, const float4* __restrict__ footprints,
+                                                                    int n, GridDims d, int64_t limit,
                                                                     uint64_t* __restrict__ items,
                                                                     uint64_t* __restrict__ masks) {
     __shared__ int2 s_span[1 << kGroupShift][kBinThreads];
@@ -780,10 +816,15 @@ __global__ __launch_bounds__(kBinThreads) void accutile_emit_kernel(const uint64
     const int64_t stop = min((int64_t)offsets[i], limit);
     if (start >= stop) return;
     const int64_t row = (int64_t)(uint32_t)records[i];
-    const int radius = geo.radii[row];
-    if (radius <= 0) return;
-    const Ellipse e = footprint(reinterpret_cast<const float2*>(geo.centers)[row],
-                                reinterpret_cast<const float4*>(geo.conics)[row], radius, d.gx, d.gy);
+    Ellipse e;
+    if constexpr (PACKED) {
+        e = unpack_ellipse(footprints[2 * row], footprints[2 * row + 1]);
+    } else {
+        const int radius = geo.radii[row];
+        if (radius <= 0) return;
+        e = footprint(reinterpret_cast<const float2*>(geo.centers)[row], reinterpret_cast<const float4*>(geo.conics)[row],
+                      radius, d.gx, d.gy);
+    }
     const int view = (int)(row / n);
     const uint64_t id = (uint64_t)(uint32_t)(row - (int64_t)view * n);
     const uint32_t gbase = (uint32_t)(view * d.gpv);
@@ -1214,19 +1255,30 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     gs3d::order_scratch_bytes(rows, &sc, scratch);
     const gs3d::RowGeometry geo{a.centers, a.conics, a.radii, a.tile_mode};
     const bool accu = a.tile_mode == GS3D_TILE_ACCUTILE;
-    const bool packed = d.gx <= 256 && d.gy <= 256 && !accu;
+    const bool packed = d.gx <= 256 && d.gy <= 256;
+    if (accu && (!a.footprints || (reinterpret_cast<uintptr_t>(a.footprints) & 15))) return GS3D_ERR_ARGUMENT;
+    float4* fp = reinterpret_cast<float4*>(a.footprints);
     const dim3 grid(gs3d::blocks_for(rows, 256)), block(256);
-    if (packed)
-        hipLaunchKernelGGL(gs3d::row_records_kernel<true>, grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy, sc.keys,
-                           a.order);
+    if (accu && packed)
+        hipLaunchKernelGGL((gs3d::row_records_kernel<true, true>), grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy,
+                           sc.keys, a.order, a.tiles_out, fp);
+    else if (accu)
+        hipLaunchKernelGGL((gs3d::row_records_kernel<false, true>), grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy,
+                           sc.keys, a.order, a.tiles_out, fp);
+    else if (packed)
+        hipLaunchKernelGGL((gs3d::row_records_kernel<true, false>), grid, block, 0, s, a.depths, geo, rows, d.gx,
+                           d.gy, sc.keys, a.order, a.tiles_out, fp);
     else
-        hipLaunchKernelGGL(gs3d::row_records_kernel<false>, grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy,
-                           sc.keys, a.order);
+        hipLaunchKernelGGL((gs3d::row_records_kernel<false, false>), grid, block, 0, s, a.depths, geo, rows, d.gx,
+                           d.gy, sc.keys, a.order, a.tiles_out, fp);
     // order holds 2*rows records: [0, rows) sorted result, [rows, 2rows) ping-pong.
     int status = gs3d::run_sort<uint32_t, uint64_t>(sc.keys, a.order, rows, 32, sc.sort, s);
     if (status != GS3D_OK) return status;
     const dim3 cgrid(gs3d::blocks_for(rows, gs3d::kBinThreads)), cblock(gs3d::kBinThreads);
-    if (accu)
+    if (accu && packed)
+        hipLaunchKernelGGL((gs3d::order_counts_kernel<true, true>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
+                           d.gy, sc.counts, sc.pairs);
+    else if (accu)
         hipLaunchKernelGGL((gs3d::order_counts_kernel<false, true>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
                            d.gy, sc.counts, sc.pairs);
     else if (packed)
@@ -1284,8 +1336,14 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
     const int group_bits = gs3d::bit_length(groups - 1 > 0 ? groups - 1 : 1);
     int status;
     if (accu) {
-        hipLaunchKernelGGL(gs3d::accutile_emit_kernel, egrid, eblock, 0, s, a.order, a.group_offsets, rows, geo, a.n, d,
-                           S, sc.items, sc.masks);
+        if (!a.footprints || (reinterpret_cast<uintptr_t>(a.footprints) & 15)) return GS3D_ERR_ARGUMENT;
+        const float4* fp = reinterpret_cast<const float4*>(a.footprints);
+        if (d.gx <= 256 && d.gy <= 256)
+            hipLaunchKernelGGL(gs3d::accutile_emit_kernel<true>, egrid, eblock, 0, s, a.order, a.group_offsets, rows,
+                               geo, fp, a.n, d, S, sc.items, sc.masks);
+        else
+            hipLaunchKernelGGL(gs3d::accutile_emit_kernel<false>, egrid, eblock, 0, s, a.order, a.group_offsets, rows,
+                               geo, fp, a.n, d, S, sc.items, sc.masks);
         status = gs3d::run_sort<uint64_t, uint64_t>(sc.items, sc.masks, S, group_bits, sc.sort, s);
     } else {
         if (d.gx <= 256 && d.gy <= 256)

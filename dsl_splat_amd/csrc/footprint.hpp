@@ -158,6 +158,38 @@ GS3D_DEV int accutile_strips(const Ellipse& e, bool& is_y, F&& f) {
     return count;
 }
 
+// Compact footprint for later passes over grids of at most 256 x 256 tiles
+// (32 bytes): (cx, cy, a, b), (c, level or -1 when not precise, det, bounds
+// x0 | y0 << 8 | (x1 - 1) << 16 | (y1 - 1) << 24).  unpack_ellipse recomputes
+// the extents with the same operations as footprint(), so strips are
+// identical.
+GS3D_DEV void pack_ellipse(const Ellipse& e, float4& p0, float4& p1) {
+    const uint32_t b = (uint32_t)(e.bounds.x & 255) | ((uint32_t)(e.bounds.y & 255) << 8) |
+                       ((uint32_t)((e.bounds.z - 1) & 255) << 16) | ((uint32_t)((e.bounds.w - 1) & 255) << 24);
+    p0 = make_float4(e.cx, e.cy, e.a, e.b);
+    p1 = make_float4(e.c, e.precise ? e.level : -1.0f, e.det, __uint_as_float(b));
+}
+
+GS3D_DEV Ellipse unpack_ellipse(float4 p0, float4 p1) {
+    Ellipse e;
+    e.cx = p0.x;
+    e.cy = p0.y;
+    e.a = p0.z;
+    e.b = p0.w;
+    e.c = p1.x;
+    e.det = p1.z;
+    const uint32_t b = __float_as_uint(p1.w);
+    e.bounds = make_int4((int)(b & 255u), (int)((b >> 8) & 255u), (int)((b >> 16) & 255u) + 1, (int)(b >> 24) + 1);
+    e.precise = p1.y >= 0.0f;
+    e.level = e.precise ? p1.y : 0.0f;
+    e.ex = e.ey = 0.0f;
+    if (e.precise) {
+        e.ex = __builtin_sqrtf(e.level * e.c / e.det);
+        e.ey = __builtin_sqrtf(e.level * e.a / e.det);
+    }
+    return e;
+}
+
 // Tiles listed for one projected Gaussian (the count the projection writes,
 // projection.py:150-161).
 GS3D_DEV int footprint_tiles(float2 center, float4 conic, int radius, int gx, int gy, int mode) {

@@ -62,10 +62,14 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     state = project_views(
         means, quats, scales, opacities, viewmats, full, Ks, width, height, near, far, radius_clip,
         sh=sh if sh_degree is not None else None, sh_degree=sh_degree or 0,
-        camera_centers=centers if with_centers else None, metadata=True, tile_mode=tile_mode,
+        camera_centers=centers if with_centers else None, metadata=True,
     )
+    # The depth ordering computes every row's footprint in the chosen mode
+    # once; it also leaves the mode's tile counts in state.tile_counts (the
+    # projection counted radius squares).
     order, offsets, totals = order_rows(state.centers, state.radii, state.depths, width, height,
-                                        conics=state.conics, tile_mode=tile_mode)
+                                        conics=state.conics, tile_mode=tile_mode,
+                                        tiles_out=None if tile_mode == "radius" else state.tile_counts)
     host = torch.cat([errors.to(torch.int64), totals]).cpu().tolist()
     raise_camera_errors(host[:-2])
     group_pairs, count = int(host[-2]), int(host[-1])

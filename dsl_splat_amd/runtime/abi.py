@@ -133,6 +133,8 @@ class OrderArgs(ctypes.Structure):
         ("totals", _P),
         ("conics", _P),
         ("tile_mode", ctypes.c_int32),
+        ("tiles_out", _P),
+        ("footprints", _P),
     ]
 
 
@@ -152,6 +154,7 @@ class BinArgs(ctypes.Structure):
         ("ids", _P),
         ("conics", _P),
         ("tile_mode", ctypes.c_int32),
+        ("footprints", _P),
     ]
 
 

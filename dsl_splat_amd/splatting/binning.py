@@ -82,16 +82,21 @@ def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tenso
 
 @torch.no_grad()
 def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, height: int, *,
-               conics: Tensor | None = None, tile_mode="radius") -> tuple[Tensor, Tensor, Tensor]:
+               conics: Tensor | None = None, tile_mode="radius",
+               tiles_out: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """Depth order of the (views, N) rows.
 
-    Returns (ordered row records with 2*rows storage, inclusive group
-    offsets, totals = [group pairs, tile pairs]), all left on the device."""
+    Returns (ordered row records with 2*rows storage -- followed, for
+    AccuTile, by the rows' compact footprints, 32 bytes each --, inclusive
+    group offsets, totals = [group pairs, tile pairs]), all left on the
+    device.  ``tiles_out`` (int32, views*N), if given, receives every row's
+    tile count in ``tile_mode``."""
     mode = _mode(tile_mode, conics)
     device = radii.device
     views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
     rows = views * n
-    order = torch.empty(2 * rows, dtype=torch.int64, device=device)
+    accu = mode == abi.TILE_MODES["accutile"]
+    order = torch.empty(2 * rows + (4 * rows if accu else 0), dtype=torch.int64, device=device)
     offsets = torch.empty(rows, dtype=torch.int32, device=device)
     totals = torch.empty(2, dtype=torch.int64, device=device)
     a = abi.OrderArgs()
@@ -103,6 +108,12 @@ def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, heigh
     if mode:
         conics = conics.contiguous()
         a.conics = native.ptr(conics)
+    if accu:
+        a.footprints = native.ptr(order, 2 * rows)
+    if tiles_out is not None:
+        if tiles_out.dtype != torch.int32 or not tiles_out.is_contiguous() or tiles_out.numel() != rows:
+            raise ValueError("tiles_out must be a contiguous int32 tensor with one entry per row")
+        a.tiles_out = native.ptr(tiles_out)
     scratch = _scratch(native.query("gs3d_order_rows_scratch_bytes", rows), device)
     native.call("gs3d_order_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
     return order, offsets, totals
@@ -136,6 +147,10 @@ def bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, gro
     if mode:
         conics = conics.contiguous()
         a.conics = native.ptr(conics)
+    if mode == abi.TILE_MODES["accutile"]:
+        if order.numel() < 6 * views * n:
+            raise ValueError("AccuTile binning needs the order returned by order_rows in the same mode")
+        a.footprints = native.ptr(order, 2 * views * n)
     scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, views, width, height, mode), device)
     native.call("gs3d_bin_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
     return ranges, ids

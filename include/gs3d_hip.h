@@ -267,6 +267,8 @@ typedef struct gs3d_order_args {
     int64_t* totals;          /* (2) group pairs, tile pairs */
     const float* conics;      /* (views,N,4); required unless tile_mode is GS3D_TILE_RADIUS */
     int32_t tile_mode;        /* GS3D_TILE_* */
+    int32_t* tiles_out;       /* optional (views*N): every row's tile count in tile_mode */
+    float* footprints;        /* ACCUTILE: (views*N,8) working footprints, 16-byte aligned, kept for gs3d_bin_rows */
 } gs3d_order_args;
 
 size_t gs3d_order_rows_scratch_bytes(int64_t rows);
@@ -284,6 +286,7 @@ typedef struct gs3d_bin_args {
     int32_t* ids;                  /* (tile_pairs) Gaussian index within its view */
     const float* conics;           /* (views,N,4), as given to gs3d_order_rows */
     int32_t tile_mode;             /* the tile_mode given to gs3d_order_rows */
+    const float* footprints;       /* ACCUTILE: the footprints gs3d_order_rows wrote */
 } gs3d_bin_args;
 
 size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t width, int32_t height,
