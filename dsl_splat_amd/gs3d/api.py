@@ -33,7 +33,9 @@ BACKEND = "gs3d-hip"
 
 @dataclass(slots=True)
 class RasterizationResult:
-    """Channel-last views of frame-owned images and training metadata."""
+    """What ``rasterize`` returns: (..., C, H, W, D) features and (..., C, H, W, 1)
+    alpha (channel-last, owned by the call), the meta dictionary and the
+    requested contribution statistics."""
 
     features: Tensor
     alpha: Tensor
@@ -51,6 +53,25 @@ class RasterizationResult:
     @property
     def extra_features(self) -> Tensor | None:
         return self.meta.get("render_extra_signals")
+
+
+def _sh_degree(features, sh_coeffs, sh_degree) -> int | None:
+    """The SH degree in use (None for plain features); ValueError for
+    contradictory or malformed colour arguments (gs3d/api.py:86-102)."""
+    if (features is None) == (sh_coeffs is None):
+        raise ValueError("provide exactly one of features or sh_coeffs")
+    if sh_coeffs is None:
+        if sh_degree is not None:
+            raise ValueError("sh_degree requires sh_coeffs")
+        return None
+    if not isinstance(sh_coeffs, Tensor) or sh_coeffs.ndim < 3:
+        raise ValueError("sh_coeffs must have shape (...,N,K,3) or (...,C,N,K,3)")
+    if sh_degree is None:
+        rows = sh_coeffs.shape[-2]
+        sh_degree = min(3, math.isqrt(rows) - 1)
+    if isinstance(sh_degree, bool) or not isinstance(sh_degree, Integral) or not 0 <= sh_degree <= 3:
+        raise ValueError("sh_degree must be an integer in [0,3]")
+    return sh_degree
 
 
 @torch.no_grad()
@@ -105,32 +126,23 @@ def rasterize(
     statistics: Sequence[StatisticsRequest] = (),
     tile_mode: str = "radius",
 ) -> RasterizationResult:
-    """Render original 3DGS with centre-Z sorting.
+    """Original 3DGS, forward (and backward through autograd), every camera of
+    every batch item.
 
-    Scales/opacities are activated; wxyz quaternions are normalized. Gaussian
-    batch dimensions and per-view features/SH follow the reference layouts.
-    Pixel centers are (x+0.5, y+0.5) in the supplied K coordinate system;
-    returned means2d uses integer pixel centres (K projection minus 0.5),
-    with culled rows set to zero.  The default centre-depth cutoff z > 0.2
-    matches original CUDA; the 0.3 covariance dilation is fixed.
-    K/background gradients, depth output and higher derivatives are
-    unsupported.
+    Inputs: activated scales and opacities, wxyz quaternions (normalised
+    here), either ``features`` (blended as given) or ``sh_coeffs`` (SH colour,
+    degree defaulting to min(3, isqrt(K) - 1)); features and SH may be shared
+    by the cameras or given per camera.  Pixel (x, y) has its centre at
+    (x + 0.5, y + 0.5) in K's coordinates; meta["means2d"] is the projected
+    centre in integer-pixel coordinates (K projection - 0.5), zero for culled
+    rows.  Gaussians need a centre depth inside (near_plane, far_plane);
+    covariances are dilated by 0.3 px.  Gradients reach means, quats, scales,
+    opacities, features/SH, extra features, viewmats and means2d; K and
+    background gradients are not supported.
     """
     validate_tile_mode(tile_mode)
     validate_camera_options(width, height, near_plane, far_plane, radius_clip)
-    if (features is None) == (sh_coeffs is None):
-        raise ValueError("provide exactly one of features or sh_coeffs")
-    if sh_coeffs is not None:
-        if not isinstance(sh_coeffs, Tensor) or sh_coeffs.ndim < 3:
-            raise ValueError("sh_coeffs must have shape (...,N,K,3) or (...,C,N,K,3)")
-        if sh_degree is None:
-            sh_degree = min(3, math.isqrt(sh_coeffs.shape[-2]) - 1)
-    elif sh_degree is not None:
-        raise ValueError("sh_degree requires sh_coeffs")
-    if sh_degree is not None and (
-        isinstance(sh_degree, bool) or not isinstance(sh_degree, Integral) or sh_degree not in range(4)
-    ):
-        raise ValueError("sh_degree must be an integer in [0,3]")
+    sh_degree = _sh_degree(features, sh_coeffs, sh_degree)
     layout = normalize_inputs(
         means, quats, scales, opacities, features if sh_coeffs is None else sh_coeffs, viewmats, Ks,
         backgrounds, extra_features, None, sh_degree,

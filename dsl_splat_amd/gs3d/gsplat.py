@@ -1,54 +1,66 @@
-"""gsplat-signature adapter for original 3DGS (gs3d/gsplat.py:15-194 of the
-reference): same defaults (near 0.01, far 1e10, packed=True), the same
-rejected options and exception types, colours routed to ``sh_coeffs`` iff
-``sh_degree`` is given."""
+"""gsplat's ``rasterization`` signature over the original-3DGS HIP pipeline
+(the contract of gs3d/gsplat.py:15-194 of the reference).
 
-import math
+Only what original 3DGS defines is accepted -- pinhole cameras, global
+shutter, RGB/feature rendering with the fixed 0.3 dilation on 16-pixel tiles;
+every other option raises NotImplementedError before any work, in the
+reference's order and with its messages, and size, clip and SH options raise
+ValueError.  gsplat's defaults are kept (near 0.01, far 1e10, packed=True);
+``colors`` are SH coefficients exactly when ``sh_degree`` is given.  means2d
+keeps CUDA's integer-centre raster coordinates.
+"""
+
 from numbers import Integral
 from typing import Any, Literal, Sequence
 
 from torch import Tensor
 
 from .api import rasterize
+from ..cameras import validate_camera_options
 from ..inputs import RenderMode
 from ..statistics import StatisticsRequest
 
+# Options original 3DGS does not have: flags that must stay False, inputs that
+# must stay None.
+_FLAGS = ("sparse_grad", "distributed", "segmented", "with_ut")
+_ABSENT = ("covars", "radial_coeffs", "tangential_coeffs", "thin_prism_coeffs", "ftheta_coeffs", "viewmats_rs",
+           "extra_signals_sh_degree")
 
-def _validate_options(width, height, near_plane, far_plane, radius_clip, eps2d, sh_degree, tile_size, render_mode,
-                      rasterize_mode, channel_chunk, camera_model, with_eval3d, rolling_shutter,
-                      unsupported: dict[str, bool], unsupported_values: dict[str, object]) -> None:
-    for name, enabled in unsupported.items():
-        if enabled:
-            raise NotImplementedError(f"3DGS/HIP gsplat adapter does not support {name}=True")
-    for name, value in unsupported_values.items():
-        if value is not None:
+
+def _positive_int(v) -> bool:
+    return isinstance(v, Integral) and not isinstance(v, bool) and v > 0
+
+
+def _reject(options: dict[str, Any]) -> None:
+    for flag in _FLAGS:
+        if options[flag]:
+            raise NotImplementedError(f"3DGS/HIP gsplat adapter does not support {flag}=True")
+    for name in _ABSENT:
+        if options[name] is not None:
             raise NotImplementedError(f"3DGS/HIP gsplat adapter does not support {name}")
-    shutter = getattr(rolling_shutter, "name", rolling_shutter)
-    if shutter not in (None, 0, "GLOBAL", "global"):
-        raise NotImplementedError("only global shutter is supported")
-    if camera_model != "pinhole":
-        raise NotImplementedError("only pinhole cameras are supported")
-    if with_eval3d is True:
-        raise NotImplementedError("original 3DGS uses projected 2D conics; with_eval3d=True is unsupported")
-    if eps2d != 0.3:
-        raise NotImplementedError("original 3DGS currently has fixed eps2d=0.3")
-    if tile_size not in (None, 16):
-        raise NotImplementedError("original 3DGS currently requires tile_size=16")
-    if render_mode != "RGB":
-        raise NotImplementedError(
-            "3DGS/HIP supports render_mode='RGB' for RGB or arbitrary features; depth rendering is not implemented"
-        )
-    if rasterize_mode != "classic":
-        raise NotImplementedError("original 3DGS supports rasterize_mode='classic' only")
-    if any(isinstance(v, bool) or not isinstance(v, Integral) or v <= 0 for v in (width, height, channel_chunk)):
+    shutter = options["rolling_shutter"]
+    shutter = getattr(shutter, "name", shutter)
+    requirements = (
+        (shutter in (None, 0, "GLOBAL", "global"), "only global shutter is supported"),
+        (options["camera_model"] == "pinhole", "only pinhole cameras are supported"),
+        (options["with_eval3d"] is not True,
+         "original 3DGS uses projected 2D conics; with_eval3d=True is unsupported"),
+        (options["eps2d"] == 0.3, "original 3DGS currently has fixed eps2d=0.3"),
+        (options["tile_size"] in (None, 16), "original 3DGS currently requires tile_size=16"),
+        (options["render_mode"] == "RGB",
+         "3DGS/HIP supports render_mode='RGB' for RGB or arbitrary features; depth rendering is not implemented"),
+        (options["rasterize_mode"] == "classic", "original 3DGS supports rasterize_mode='classic' only"),
+    )
+    for satisfied, message in requirements:
+        if not satisfied:
+            raise NotImplementedError(message)
+    if not all(_positive_int(options[k]) for k in ("width", "height", "channel_chunk")):
         raise ValueError("width, height and channel_chunk must be positive integers")
-    if not math.isfinite(near_plane) or near_plane <= 0 or math.isnan(far_plane) or far_plane <= near_plane:
-        raise ValueError("require 0 < near_plane < far_plane")
-    if not math.isfinite(radius_clip) or radius_clip < 0:
-        raise ValueError("radius_clip must be finite and nonnegative")
-    if sh_degree is not None and (
-        isinstance(sh_degree, bool) or not isinstance(sh_degree, Integral) or sh_degree not in range(4)
-    ):
+    validate_camera_options(options["width"], options["height"], options["near_plane"], options["far_plane"],
+                            options["radius_clip"])
+    sh_degree = options["sh_degree"]
+    if sh_degree is not None and (isinstance(sh_degree, bool) or not isinstance(sh_degree, Integral)
+                                  or not 0 <= sh_degree <= 3):
         raise ValueError("sh_degree must be None or an integer in [0,3]")
 
 
@@ -93,28 +105,16 @@ def rasterization(
     statistics: Sequence[StatisticsRequest] = (),
     tile_mode: str = "radius",
 ) -> tuple[Tensor, Tensor, dict[str, Any]]:
-    """Return (features, alpha, metadata) from the original-3DGS HIP pipeline.
-
-    Supports pinhole cameras, arbitrary feature channels, SH0-3, pose
-    gradients and dense/packed training metadata.  means2d keeps CUDA's
-    integer-centre raster coordinates.  Unsupported geometry, output modes and
-    execution options raise explicit errors.
-    """
-    _validate_options(
-        width, height, near_plane, far_plane, radius_clip, eps2d, sh_degree, tile_size, render_mode,
-        rasterize_mode, channel_chunk, camera_model, with_eval3d, rolling_shutter,
-        dict(sparse_grad=sparse_grad, distributed=distributed, segmented=segmented, with_ut=with_ut),
-        dict(covars=covars, radial_coeffs=radial_coeffs, tangential_coeffs=tangential_coeffs,
-             thin_prism_coeffs=thin_prism_coeffs, ftheta_coeffs=ftheta_coeffs, viewmats_rs=viewmats_rs,
-             extra_signals_sh_degree=extra_signals_sh_degree),
-    )
+    """(features, alpha, meta) of gs3d.rasterize under gsplat's names;
+    requested statistics also appear as meta["statistics"]."""
+    _reject(dict(locals()))
     result = rasterize(
         means, quats, scales, opacities, viewmats, Ks, width, height,
-        features=colors if sh_degree is None else None,
+        features=None if sh_degree is not None else colors,
         sh_coeffs=colors if sh_degree is not None else None,
-        sh_degree=sh_degree, backgrounds=backgrounds, extra_features=extra_signals,
-        near_plane=near_plane, far_plane=far_plane, radius_clip=radius_clip, packed=packed, absgrad=absgrad,
-        statistics=statistics, tile_mode=tile_mode,
+        sh_degree=sh_degree, backgrounds=backgrounds, extra_features=extra_signals, near_plane=near_plane,
+        far_plane=far_plane, radius_clip=radius_clip, packed=packed, absgrad=absgrad, statistics=statistics,
+        tile_mode=tile_mode,
     )
     if statistics:
         result.meta["statistics"] = result.statistics

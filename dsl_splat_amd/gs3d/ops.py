@@ -22,7 +22,9 @@ from ..statistics import PreparedStatistics, StatisticsRequest, prepare_statisti
 
 @dataclass(slots=True)
 class GaussianGeometry:
-    """Only rows with radii>0 define centers and conics; bounds are discrete."""
+    """One camera's projected Gaussians: (N,2) centres, (N,4) conic + opacity,
+    (N,) radii, tile counts and depths.  Centres and conics are meaningful only
+    where radii > 0."""
 
     centers: Tensor
     conics: Tensor

@@ -51,36 +51,30 @@ class _SphericalHarmonics(torch.autograd.Function):
         return grad_coefficients, grad_directions, None, None, None
 
 
+def _check(coefficients, directions, radii, degree) -> None:
+    """ValueError for anything the SH kernels cannot take (messages of
+    primitives/spherical_harmonics.py:104-159 of the reference)."""
+    if isinstance(degree, bool) or not isinstance(degree, Integral) or not 0 <= degree <= 3:
+        raise ValueError("SH degree must be an integer in [0,3]")
+    c = coefficients
+    if not (isinstance(c, Tensor) and c.is_cuda and c.dtype == torch.float32 and c.ndim == 3 and c.shape[2] == 3
+            and c.shape[1] >= (degree + 1) ** 2):
+        raise ValueError("SH coefficients must be CUDA float32 (N,K,3) with enough coefficients")
+    d = directions
+    if not (isinstance(d, Tensor) and d.dtype == torch.float32 and d.device == c.device
+            and tuple(d.shape) == (c.shape[0], 3)):
+        raise ValueError("SH directions must be float32 (N,3) on the coefficients' device")
+    if radii is not None and not (radii.dtype == torch.int32 and radii.device == c.device
+                                  and tuple(radii.shape) == (c.shape[0],)):
+        raise ValueError("SH radii must be int32 (N,) on the coefficients' device")
+
+
 def spherical_harmonics(coefficients: Tensor, directions: Tensor, degree: int, *, radii: Tensor | None = None,
                         bindings=None) -> Tensor:
-    """Evaluate SH colour with +0.5/lower clamp; radii<=0 rows return zero.
-
-    Device float32 coefficients (N,K,3) and directions (N,3) are accepted.
-    Gradients include coefficients and directions; padded/culled entries are
-    zero.
-    """
-    if isinstance(degree, bool) or not isinstance(degree, Integral) or degree not in range(4):
-        raise ValueError("SH degree must be an integer in [0,3]")
-    if (
-        not isinstance(coefficients, Tensor)
-        or not coefficients.is_cuda
-        or coefficients.dtype != torch.float32
-        or coefficients.ndim != 3
-        or coefficients.shape[-1] != 3
-        or coefficients.shape[1] < (degree + 1) ** 2
-    ):
-        raise ValueError("SH coefficients must be CUDA float32 (N,K,3) with enough coefficients")
-    if (
-        not isinstance(directions, Tensor)
-        or directions.device != coefficients.device
-        or directions.dtype != torch.float32
-        or directions.shape != (len(coefficients), 3)
-    ):
-        raise ValueError("SH directions must be float32 (N,3) on the coefficients' device")
-    if radii is not None and (
-        radii.device != coefficients.device or radii.dtype != torch.int32 or radii.shape != (len(coefficients),)
-    ):
-        raise ValueError("SH radii must be int32 (N,) on the coefficients' device")
+    """max(sum_k Y_k(unit direction) c_k + 0.5, 0) per Gaussian, zero where
+    radii <= 0; coefficients (N,K,3) and directions (N,3) are device float32.
+    Differentiable in both (degree 0 ignores the directions)."""
+    _check(coefficients, directions, radii, degree)
     if degree == 0:
         directions = directions.detach()
     return _SphericalHarmonics.apply(coefficients, directions, radii, int(degree), torch.is_grad_enabled())
