@@ -120,7 +120,7 @@ def stage_timings(scene, reps):
     from dsl_splat_amd.primitives import tiling
     from dsl_splat_amd.splatting import binning, cameras
 
-    quats = torch.nn.functional.normalize(scene.quats, dim=-1)
+    quats = scene.quats  # raw: the projection kernels normalise them, as rasterize has them do
     sh = scene.sh_coeffs
     deg = scene.sh_degree
     views, n = scene.viewmats.shape[0], len(scene.means)
@@ -137,7 +137,7 @@ def stage_timings(scene, reps):
             st = gproj.project_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full,
                                      scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0,
                                      sh=sh, sh_degree=deg or 0, camera_centers=centers if deg else None,
-                                     metadata=True)
+                                     metadata=True, normalize_quats=True)
             ev[2].record()
             order, offsets, totals = binning.order_rows(st.centers, st.radii, st.depths, scene.width,
                                                         scene.height)
@@ -159,7 +159,7 @@ def stage_timings(scene, reps):
                                  scene.width, scene.height, st.radii, record[..., 0:2], record[..., 2:6],
                                  (True, True, True, True, False, False), sh=sh, sh_degree=deg or 0,
                                  camera_centers=centers if deg else None, grad_colors=gf if sh is not None else None,
-                                 need_sh=sh is not None)
+                                 need_sh=sh is not None, normalize_quats=True)
             ev[11].record()
             torch.cuda.synchronize()
             if rep == 0:
@@ -181,7 +181,7 @@ def stage_timings(scene, reps):
         project = lambda: gproj.project_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full,
                                               scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0, sh=sh,
                                               sh_degree=deg or 0, camera_centers=centers if deg else None,
-                                              metadata=True)
+                                              metadata=True, normalize_quats=True)
         project()
         e0.record()
         for _ in range(launches):

@@ -33,6 +33,30 @@ GS3D_DEV float sel_max(float a, float b) { return (a < b) ? b : a; }
 GS3D_DEV float sel_min(float a, float b) { return (b < a) ? b : a; }
 GS3D_DEV float sel_clamp(float v, float lo, float hi) { return sel_min(sel_max(v, lo), hi); }
 
+// torch.nn.functional.normalize of a quaternion, as the reference applies it
+// before projection (inputs.py:252): q / max(|q|, 1e-12), the squares summed
+// in component order.  Returns |q|.
+GS3D_DEV float normalize_quat(float (&q)[4]) {
+    const float norm = __builtin_sqrtf(((q[0] * q[0] + q[1] * q[1]) + q[2] * q[2]) + q[3] * q[3]);
+    const float d = sel_max(norm, 1e-12f);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q[k] = q[k] / d;
+    return norm;
+}
+
+// Gradient through normalize_quat: g <- (g - u (u.g)) / |q| for the unit
+// quaternion u, or g / 1e-12 where the norm was clamped.
+GS3D_DEV void normalize_quat_vjp(const float (&u)[4], float norm, float (&g)[4]) {
+    if (norm > 1e-12f) {
+        const float dot = ((u[0] * g[0] + u[1] * g[1]) + u[2] * g[2]) + u[3] * g[3];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) g[k] = (g[k] - u[k] * dot) / norm;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) g[k] = g[k] / 1e-12f;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // exp for blending.  x = k ln2 + r, k = rint(x log2 e), two-constant
 // Cody-Waite reduction (the high part of ln2 has 15 significant bits, so

@@ -406,6 +406,7 @@ __global__ __launch_bounds__(kProjBlock) void project_fwd_kernel(gs3d_project_ar
         q[1] = qq.y;
         q[2] = qq.z;
         q[3] = qq.w;
+        if (a.normalize_quats) normalize_quat(q);
 #pragma unroll
         for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
         opac = a.opacities[i];
@@ -625,7 +626,7 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
     for (int64_t base = (int64_t)blockIdx.x * kProjBlock; base < n; base += (int64_t)gridDim.x * kProjBlock) {
         const int64_t i = base + threadIdx.x;
         const bool valid = i < n;
-        float mean[3] = {0, 0, 0}, q[4] = {1, 0, 0, 0}, s[3] = {1, 1, 1};
+        float mean[3] = {0, 0, 0}, q[4] = {1, 0, 0, 0}, s[3] = {1, 1, 1}, qnorm = 1.0f;
         if (valid) {
 #pragma unroll
             for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
@@ -634,6 +635,7 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
             q[1] = qq.y;
             q[2] = qq.z;
             q[3] = qq.w;
+            if (a.normalize_quats) qnorm = normalize_quat(q);
 #pragma unroll
             for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
         }
@@ -677,8 +679,10 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
             if (a.grad_means)
 #pragma unroll
                 for (int k = 0; k < 3; ++k) a.grad_means[3 * i + k] = gm[k];
-            if (a.grad_quats)
+            if (a.grad_quats) {
+                if (a.normalize_quats) normalize_quat_vjp(q, qnorm, gq);
                 reinterpret_cast<float4*>(a.grad_quats)[i] = make_float4(gq[0], gq[1], gq[2], gq[3]);
+            }
             if (a.grad_scales)
 #pragma unroll
                 for (int k = 0; k < 3; ++k) a.grad_scales[3 * i + k] = gs[k];

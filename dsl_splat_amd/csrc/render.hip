@@ -115,10 +115,13 @@ struct TileWaves {
 
 // Bit w is set unless every pixel of wavefront w's strip is certain to reject
 // the Gaussian: the bounding box of the ellipse {power >= cut} (its quadratic
-// form widened by 1% + 0.01, the box by 0.01 px, computed in float64) misses
-// the strip.  The margins exceed the float32 evaluation error of power
-// wherever a*c <= 100*det (correlation below 0.995); more elongated conics,
-// non-positive-definite ones and NaNs are never culled.  Rejected pairs change
+// form widened by 1% + 0.01, the box by 0.01 px) misses the strip.  Culling
+// is attempted only where a*c <= 100*det (correlation below 0.995): there the
+// float32 determinant is within 1.3e-5 relative of the exact one (its
+// cancellation error is at most 2^-24 * 2ac <= 200 * 2^-24 * det), so the box
+// stays wider than the exact ellipse's by far more than the float32 error of
+// the blend's power evaluation.  More elongated conics, non-positive-definite
+// ones, overflowing products and NaNs are never culled.  Rejected pairs change
 // no output, so culling leaves every result identical.
 template <int PIX>
 GS3D_DEV uint32_t strip_mask(float2 xy, float4 con, float cut, int x0, int y0) {
@@ -126,12 +129,13 @@ GS3D_DEV uint32_t strip_mask(float2 xy, float4 con, float cut, int x0, int y0) {
     constexpr uint32_t all = (1u << NW) - 1u;
     const float q = -2.0f * cut;  // power >= cut  <=>  a dx^2 + 2 b dx dy + c dy^2 <= q
     if (!(q > 0.0f) && q == q) return 0u;  // nothing passes the cutoff
-    const double a = con.x, b = con.y, c = con.z;
-    const double det = a * c - b * b;
-    if (!(a > 0.0 && c > 0.0 && det > 0.0 && a * c <= 100.0 * det && q < 3.0e38f)) return all;
-    const double qm = (double)q * 1.01 + 0.01;
-    const float hx = (float)__builtin_sqrt(qm * c / det) + 0.01f;
-    const float hy = (float)__builtin_sqrt(qm * a / det) + 0.01f;
+    const float a = con.x, b = con.y, c = con.z;
+    const float ac = a * c;
+    const float det = ac - b * b;
+    if (!(a > 0.0f && c > 0.0f && det > 0.0f && ac < 1.0e30f && ac <= 100.0f * det && q < 1.0e30f)) return all;
+    const float s = (q * 1.01f + 0.01f) / det;
+    const float hx = __builtin_sqrtf(s * c) + 0.01f;
+    const float hy = __builtin_sqrtf(s * a) + 0.01f;
     if (xy.x + hx < (float)x0 || xy.x - hx > (float)(x0 + kTile - 1)) return 0u;
     uint32_t m = 0u;
 #pragma unroll
@@ -155,15 +159,49 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32
     const float cut = power_cutoff(con.w);
     s_cut[slot] = cut;
     s_mask[slot] = strip_mask<PIX>(xy, con, cut, t.x0, t.y0);
-    float* dst = s_feat + slot * CH;
+    // The channel vector [features | extra | 1]: every load is issued before
+    // the LDS writes (compile-time channel slots, predicated on the counts).
+    const int F = a.feat_channels, E = a.extra_channels;
     const float* f = a.features + view * a.feat_view_stride + (int64_t)g * a.feat_stride;
-    int c = 0;
-    for (int k = 0; k < a.feat_channels; ++k) dst[c++] = f[k];
-    if (a.extra_channels) {
-        const float* e = a.extra + view * a.extra_view_stride + (int64_t)g * a.extra_stride;
-        for (int k = 0; k < a.extra_channels; ++k) dst[c++] = e[k];
+    const float* e = E > 0 ? a.extra + view * a.extra_view_stride + (int64_t)g * a.extra_stride : nullptr;
+    float v[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        float x = 0.0f;
+        if (c < F)
+            x = f[c];
+        else if (c < F + E)
+            x = e[c - F];
+        else if (c == F + E && a.one_tail)
+            x = 1.0f;
+        v[c] = x;
     }
-    if (a.one_tail) dst[c++] = 1.0f;
+    float* dst = s_feat + slot * CH;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) dst[c] = v[c];
+}
+
+// One staged Gaussian as the blend loops read it from LDS.  The loops load
+// the next Gaussian of their wavefront before blending the current one, so
+// the LDS latency overlaps the arithmetic.
+template <int CH>
+struct Staged {
+    float2 xy;
+    float4 con;
+    float cut;
+    float f[CH];
+};
+
+template <int CH>
+GS3D_DEV Staged<CH> load_staged(int j, const float2* s_xy, const float4* s_con, const float* s_cut,
+                                const float* s_feat) {
+    Staged<CH> g;
+    g.xy = s_xy[j];
+    g.con = s_con[j];
+    g.cut = s_cut[j];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) g.f[c] = s_feat[j * CH + c];
+    return g;
 }
 
 // Contribution statistics of one accepted Gaussian (statistics.py:46-70,
@@ -264,7 +302,11 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
         for (int c0 = 0; c0 < cnt && live; c0 += 64) {
             // This wavefront's Gaussians of the next 64, in list order.
             uint64_t todo = __ballot(c0 + lane < cnt && ((s_mask[min(c0 + lane, B - 1)] >> wave) & 1u));
-            while (todo) {
+            if (!todo) continue;
+            int jn = c0 + __builtin_ctzll(todo);
+            todo &= todo - 1;
+            Staged<CH> cur = load_staged<CH>(jn, s_xy, s_con, s_cut, s_feat);
+            while (true) {
                 bool any = false;
 #pragma unroll
                 for (int k = 0; k < PIX; ++k) any = any || !done[k];
@@ -272,13 +314,21 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
                     live = false;
                     break;
                 }
-                const int j = c0 + __builtin_ctzll(todo);
-                todo &= todo - 1;
+                const int j = jn;
+                const bool more = todo != 0;
+                Staged<CH> nxt = cur;
+                if (more) {
+                    jn = c0 + __builtin_ctzll(todo);
+                    todo &= todo - 1;
+                    // The statistics variant loads at use: its extra
+                    // registers would otherwise cost occupancy.
+                    if constexpr (!STATS) nxt = load_staged<CH>(jn, s_xy, s_con, s_cut, s_feat);
+                }
                 const int contributor = begin - t.first + j + 1;  // list position, 1-based
-                const float2 xy = s_xy[j];
-                const float4 con = s_con[j];
-                const float cut = s_cut[j];
-                const float* f = s_feat + j * CH;
+                const float2 xy = cur.xy;
+                const float4 con = cur.con;
+                const float cut = cur.cut;
+                const float* f = cur.f;
                 bool acc[PIX];
                 float wk[PIX];
 #pragma unroll
@@ -311,6 +361,11 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
                     for (int k = 0; k < PIX; ++k) hit = hit || acc[k];
                     if (__ballot(hit)) observe_statistics<PIX>(st, t.view, a.n, s_id[j], acc, wk, val, lane);
                 }
+                if (!more) break;
+                if constexpr (STATS)
+                    cur = load_staged<CH>(jn, s_xy, s_con, s_cut, s_feat);
+                else
+                    cur = nxt;
             }
         }
     }

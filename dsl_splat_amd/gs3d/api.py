@@ -83,7 +83,7 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     state = project_views(
         means, quats, scales, opacities, viewmats, full, Ks, width, height, near, far, radius_clip,
         sh=sh if sh_degree is not None else None, sh_degree=sh_degree or 0,
-        camera_centers=centers if with_centers else None, metadata=True,
+        camera_centers=centers if with_centers else None, metadata=True, normalize_quats=True,
     )
     # The depth ordering computes every row's footprint in the chosen mode
     # once; it also leaves the mode's tile counts in state.tile_counts (the
@@ -143,9 +143,11 @@ def rasterize(
     validate_tile_mode(tile_mode)
     validate_camera_options(width, height, near_plane, far_plane, radius_clip)
     sh_degree = _sh_degree(features, sh_coeffs, sh_degree)
+    # Quaternions stay raw: the projection kernels normalise them (and take
+    # their gradient through the normalisation) as F.normalize does.
     layout = normalize_inputs(
         means, quats, scales, opacities, features if sh_coeffs is None else sh_coeffs, viewmats, Ks,
-        backgrounds, extra_features, None, sh_degree,
+        backgrounds, extra_features, None, sh_degree, normalize_quats=False,
     )
     frames: list[Frame] = []
     dense: dict[str, list[Tensor]] = {n: [] for n in ("radii", "means2d", "opacities", "tiles_per_gauss", "conics")}

@@ -119,7 +119,7 @@ class Rasterize(torch.autograd.Function):
                 means, quats, scales, opacities, viewmats.detach(), frame.full, frame.Ks, frame.width,
                 frame.height, st.radii, grad_centers, grad_conics, proj_needs,
                 sh=colors if sh else None, sh_degree=frame.sh_degree or 0, camera_centers=frame.camera_centers,
-                grad_colors=grad_blended if sh else None, need_sh=sh and needs[4],
+                grad_colors=grad_blended if sh else None, need_sh=sh and needs[4], normalize_quats=True,
                 need_centers=sh and (frame.sh_degree or 0) > 0 and needs[6],
             )
         grad_view = None

@@ -9,7 +9,6 @@ from typing import Any, Sequence
 import torch
 from torch import Tensor
 from torch.autograd.function import once_differentiable
-from torch.nn.functional import normalize
 
 from . import projection, render
 from .cameras import ViewConfig, prepare_camera
@@ -54,7 +53,7 @@ class _Project(torch.autograd.Function):
                 grad_enabled: bool):
         state = projection.project_views(means, quats, scales, opacities, view[None], full[None], intrinsics[None],
                                          config.width, config.height, config.near, config.far, config.radius_clip,
-                                         tile_mode=config.tile_mode)
+                                         tile_mode=config.tile_mode, normalize_quats=True)
         centers, conics, radii, tiles, depths = (state.centers[0], state.conics[0], state.radii[0],
                                                  state.tile_counts[0], state.depths[0])
         if grad_enabled and any(ctx.needs_input_grad[:6]):
@@ -75,7 +74,8 @@ class _Project(torch.autograd.Function):
         gk = torch.zeros((n, 4), dtype=torch.float32, device=means.device) if conics is None else conics.contiguous()
         needs = tuple(ctx.needs_input_grad[:6])
         g = projection.backward_views(means, quats, scales, opacities, view[None], full[None], intrinsics[None],
-                                      ctx.config.width, ctx.config.height, radii[None], gc[None], gk[None], needs)
+                                      ctx.config.width, ctx.config.height, radii[None], gc[None], gk[None], needs,
+                                      normalize_quats=True)
         out = [g["means"], g["quats"], g["scales"], g["opacities"],
                None if g["view"] is None else g["view"][0],
                None if g["projection"] is None else g["projection"][0]]
@@ -127,7 +127,7 @@ def prepare_gaussians(means: Tensor, quats: Tensor, scales: Tensor, opacities: T
         raise ValueError("camera and Gaussians must use the same CUDA device")
     config = replace(config, tile_mode=tile_mode)
     centers, conics, radii, tiles, depths = _Project.apply(
-        means.contiguous(), normalize(quats, dim=-1).contiguous(), scales.contiguous(), opacities.contiguous(), view,
+        means.contiguous(), quats.contiguous(), scales.contiguous(), opacities.contiguous(), view,
         full, intrinsics, config, torch.is_grad_enabled())
     return GaussianGeometry(centers, conics, radii, tiles, depths, config)
 

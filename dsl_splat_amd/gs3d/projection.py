@@ -52,9 +52,11 @@ def project_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tenso
                   projection: Tensor, intrinsics: Tensor, width: int, height: int, near: float, far: float,
                   radius_clip: float, *, sh: Tensor | None = None, sh_degree: int = 0,
                   camera_centers: Tensor | None = None, metadata: bool = False,
-                  tile_mode: str = "radius") -> ProjectedViews:
+                  tile_mode: str = "radius", normalize_quats: bool = False) -> ProjectedViews:
     """Launch the fused projection for every camera in ``view`` (C,4,4);
-    ``tile_counts`` follow ``tile_mode`` (gs3d/projection.py:150-161)."""
+    ``tile_counts`` follow ``tile_mode`` (gs3d/projection.py:150-161).  With
+    ``normalize_quats`` the quaternions are raw and the kernel normalises
+    them as torch.nn.functional.normalize does."""
     device = means.device
     n = len(means)
     views = view.reshape(-1, 4, 4).shape[0]
@@ -69,6 +71,7 @@ def project_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tenso
     a.n, a.views, a.width, a.height = n, views, width, height
     a.near_plane, a.far_plane, a.radius_clip = float(near), float(far), float(radius_clip)
     a.tile_mode = abi.TILE_MODES[tile_mode]
+    a.normalize_quats = int(normalize_quats)
     means, quats, scales, opacities = (t.contiguous() for t in (means, quats, scales, opacities))
     view, projection, intrinsics = (t.reshape(views, *t.shape[-2:]).contiguous() for t in (view, projection, intrinsics))
     keep += [means, quats, scales, opacities, view, projection, intrinsics]
@@ -102,8 +105,10 @@ def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tens
                    projection: Tensor, intrinsics: Tensor, width: int, height: int, radii: Tensor,
                    grad_centers: Tensor, grad_conics: Tensor, needs: tuple[bool, ...], *,
                    sh: Tensor | None = None, sh_degree: int = 0, camera_centers: Tensor | None = None,
-                   grad_colors: Tensor | None = None, need_sh: bool = False, need_centers: bool = False):
-    """Projection (+SH) VJP summed over views.
+                   grad_colors: Tensor | None = None, need_sh: bool = False, need_centers: bool = False,
+                   normalize_quats: bool = False):
+    """Projection (+SH) VJP summed over views; with ``normalize_quats`` the
+    quaternions are raw and their gradient includes the normalisation.
 
     ``needs`` = (means, quats, scales, opacities, view, projection).
     grad_centers / grad_conics may be strided views with unit inner stride.
@@ -139,6 +144,7 @@ def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tens
             raise ValueError("gradient rows must be evenly strided (views, N, k)")
     a = abi.ProjectBwdArgs()
     a.n, a.views, a.width, a.height = n, views, width, height
+    a.normalize_quats = int(normalize_quats)
     for name, t in (("means", means), ("quats", quats), ("scales", scales), ("opacities", opacities),
                     ("view", view), ("projection", projection), ("intrinsics", intrinsics), ("radii", radii)):
         setattr(a, name, native.ptr(t))

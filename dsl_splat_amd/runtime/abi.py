@@ -9,7 +9,7 @@ import ctypes
 c_float_p = ctypes.POINTER(ctypes.c_float)
 c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Tile modes (GS3D_TILE_*), named as the reference's TileMode literals.
 TILE_MODES = {"radius": 0, "snugbox": 1, "accutile": 2}
@@ -63,6 +63,7 @@ class ProjectArgs(ctypes.Structure):
         ("meta_opacities", _P),
         ("meta_conics", _P),
         ("tile_mode", ctypes.c_int32),
+        ("normalize_quats", ctypes.c_int32),
     ]
 
 
@@ -99,6 +100,7 @@ class ProjectBwdArgs(ctypes.Structure):
         ("grad_colors_stride", ctypes.c_int64),
         ("grad_sh", _P),
         ("grad_camera_centers", _P),
+        ("normalize_quats", ctypes.c_int32),
     ]
 
 

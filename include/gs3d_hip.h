@@ -113,6 +113,7 @@ typedef struct gs3d_project_args {
     float* meta_opacities;    /* (views,N) */
     float* meta_conics;       /* (views,N,3) */
     int32_t tile_mode;        /* GS3D_TILE_*: what tiles (views,N) counts (projection.py:150-161) */
+    int32_t normalize_quats;  /* 1: quats are raw and normalised in the kernel as F.normalize does (inputs.py:252) */
 } gs3d_project_args;
 
 int gs3d_project_fwd(const gs3d_project_args* args, void* stream);
@@ -156,6 +157,7 @@ typedef struct gs3d_project_bwd_args {
     int64_t grad_colors_stride;
     float* grad_sh;               /* like sh (dense, rows beyond (deg+1)^2 are zero) */
     float* grad_camera_centers;   /* (views,3) accumulated */
+    int32_t normalize_quats;      /* 1: quats are raw; grad_quats is taken through the normalisation */
 } gs3d_project_bwd_args;
 
 int gs3d_project_bwd(const gs3d_project_bwd_args* args, void* stream);

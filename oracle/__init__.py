@@ -52,6 +52,7 @@ def lib() -> ctypes.CDLL:
             "oracle_render_fwd": [ctypes.POINTER(abi.RenderArgs)],
             "oracle_tile_footprint": [I32, P, P, I32, I32, I32, P, P],
             "oracle_logf": [ctypes.c_float],
+            "oracle_normalize_quats": [P, I64, P, P, P],
             "oracle_render_fwd_stats": [ctypes.POINTER(abi.RenderArgs), ctypes.POINTER(abi.RenderStatsArgs)],
             "oracle_render_bwd": [ctypes.POINTER(abi.RenderBwdArgs)],
             "oracle_projection_loss_f64": [P, P, P, D, P, P, I32, I32, D, D, P, P],
@@ -146,8 +147,11 @@ def camera_backward(Ks, grad_full, width, height, inverse, grad_centers):
 
 def project_fwd(means, quats, scales, opacities, view, projection, intrinsics, width, height,
                 near_plane=0.2, far_plane=float("inf"), radius_clip=0.0,
-                sh=None, sh_degree=0, camera_centers=None, metadata=False, tile_mode="radius"):
-    """gs3d/projection.py:89-164 for every view; returns a dict of arrays."""
+                sh=None, sh_degree=0, camera_centers=None, metadata=False, tile_mode="radius",
+                normalize_quats=False):
+    """gs3d/projection.py:89-164 for every view; returns a dict of arrays.
+    normalize_quats: the quaternions are raw and normalised first, as
+    F.normalize does in the reference (inputs.py:252)."""
     means, quats, scales, opacities = _f32(means), _f32(quats), _f32(scales), _f32(opacities)
     view, projection, intrinsics = (
         _f32(view).reshape(-1, 4, 4), _f32(projection).reshape(-1, 4, 4), _f32(intrinsics).reshape(-1, 3, 3))
@@ -163,6 +167,7 @@ def project_fwd(means, quats, scales, opacities, view, projection, intrinsics, w
     a.n, a.views, a.width, a.height = n, c, width, height
     a.near_plane, a.far_plane, a.radius_clip = near_plane, far_plane, radius_clip
     a.tile_mode = abi.TILE_MODES[tile_mode]
+    a.normalize_quats = int(normalize_quats)
     for name, arr in (("means", means), ("quats", quats), ("scales", scales), ("opacities", opacities),
                       ("view", view), ("projection", projection), ("intrinsics", intrinsics)):
         setattr(a, name, _ptr(arr))
@@ -192,7 +197,8 @@ def project_fwd(means, quats, scales, opacities, view, projection, intrinsics, w
 
 
 def project_bwd(means, quats, scales, opacities, view, projection, intrinsics, width, height, radii,
-                grad_centers, grad_conics, sh=None, sh_degree=0, camera_centers=None, grad_colors=None):
+                grad_centers, grad_conics, sh=None, sh_degree=0, camera_centers=None, grad_colors=None,
+                normalize_quats=False):
     means, quats, scales, opacities = _f32(means), _f32(quats), _f32(scales), _f32(opacities)
     view, projection, intrinsics = (
         _f32(view).reshape(-1, 4, 4), _f32(projection).reshape(-1, 4, 4), _f32(intrinsics).reshape(-1, 3, 3))
@@ -207,6 +213,7 @@ def project_bwd(means, quats, scales, opacities, view, projection, intrinsics, w
     )
     a = abi.ProjectBwdArgs()
     a.n, a.views, a.width, a.height = n, c, width, height
+    a.normalize_quats = int(normalize_quats)
     for name, arr in (("means", means), ("quats", quats), ("scales", scales), ("opacities", opacities),
                       ("view", view), ("projection", projection), ("intrinsics", intrinsics), ("radii", radii)):
         setattr(a, name, _ptr(arr))
@@ -295,6 +302,16 @@ def tile_footprint(mode, center, conic, radius, gx, gy):
     count = lib().oracle_tile_footprint(abi.TILE_MODES[mode], _ptr(center), _ptr(conic), int(radius), gx, gy,
                                         _ptr(tiles), _ptr(bounds))
     return bounds, tiles[:count].copy()
+
+
+def normalize_quats(q, g=None):
+    """(unit quaternions, gradient through the normalisation of g or None)."""
+    q = _f32(q).reshape(-1, 4)
+    u = np.zeros_like(q)
+    grad = None if g is None else np.zeros_like(q)
+    lib().oracle_normalize_quats(_ptr(q), len(q), _ptr(u), None if g is None else _ptr(_f32(g).reshape(-1, 4)),
+                                 _ptr(grad))
+    return u, grad
 
 
 def logf(x: float) -> float:

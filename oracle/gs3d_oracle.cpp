@@ -110,6 +110,27 @@ inline float gs_logf(float x) {
 }
 
 // ---------------------------------------------------------------------------
+// Quaternion normalisation the reference applies before projection
+// (inputs.py:252, torch.nn.functional.normalize): q / max(|q|, 1e-12), and
+// its VJP g -> (g - u (u.g)) / |q| (g / 1e-12 where the norm is clamped).
+// ---------------------------------------------------------------------------
+inline float normalize_quat(const float* q, float* u) {
+    const float norm = sqrtf(((q[0] * q[0] + q[1] * q[1]) + q[2] * q[2]) + q[3] * q[3]);
+    const float d = norm < 1e-12f ? 1e-12f : norm;
+    for (int k = 0; k < 4; ++k) u[k] = q[k] / d;
+    return norm;
+}
+
+inline void normalize_quat_vjp(const float* u, float norm, float* g) {
+    if (norm > 1e-12f) {
+        const float dot = ((u[0] * g[0] + u[1] * g[1]) + u[2] * g[2]) + u[3] * g[3];
+        for (int k = 0; k < 4; ++k) g[k] = (g[k] - u[k] * dot) / norm;
+    } else {
+        for (int k = 0; k < 4; ++k) g[k] = g[k] / 1e-12f;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Small fixed-size math in a scalar template T (float for the oracle,
 // double for finite-difference checks).
 // ---------------------------------------------------------------------------
@@ -901,7 +922,13 @@ int oracle_project_fwd(const gs3d_project_args* a) {
         for (int64_t i = 0; i < n; ++i) {
             const int64_t row = v * n + i;
             ProjOut o;
-            const bool vis = project_one(a->means + 3 * i, a->quats + 4 * i, a->scales + 3 * i, a->opacities[i],
+            float qn[4];
+            const float* q = a->quats + 4 * i;
+            if (a->normalize_quats) {
+                normalize_quat(q, qn);
+                q = qn;
+            }
+            const bool vis = project_one(a->means + 3 * i, q, a->scales + 3 * i, a->opacities[i],
                                          a->view + 16 * v, a->projection + 16 * v, a->intrinsics + 9 * v, a->width,
                                          a->height, a->near_plane, a->far_plane, a->radius_clip, o, a->tile_mode);
             a->centers[2 * row] = o.center[0];
@@ -974,6 +1001,12 @@ int oracle_project_bwd(const gs3d_project_bwd_args* a) {
     for (int64_t i = 0; i < n; ++i) {
         float gco[3 * 64];
         double gm[3] = {0, 0, 0}, gq[4] = {0, 0, 0, 0}, gs[3] = {0, 0, 0}, go = 0;
+        float qn[4], qnorm = 1.0f;
+        const float* quat = a->quats + 4 * i;
+        if (a->normalize_quats) {
+            qnorm = normalize_quat(quat, qn);
+            quat = qn;
+        }
         for (int v = 0; v < a->views; ++v) {
             const int64_t row = v * n + i;
             if (a->radii[row] > 0) {
@@ -984,7 +1017,7 @@ int oracle_project_bwd(const gs3d_project_bwd_args* a) {
                 const float gc[2] = {gcp[0], gcp[1]};
                 const float gk[4] = {gkp[0], gkp[1], gkp[2], gkp[3]};
                 ProjGrad<float> g;
-                projection_vjp<float>(a->means + 3 * i, a->quats + 4 * i, a->scales + 3 * i, a->opacities[i], V, P,
+                projection_vjp<float>(a->means + 3 * i, quat, a->scales + 3 * i, a->opacities[i], V, P,
                                       a->width, a->height, a->intrinsics[9 * v], a->intrinsics[9 * v + 4], gc, gk, g);
                 for (int k = 0; k < 3; ++k) gm[k] += g.mean[k];
                 for (int k = 0; k < 4; ++k) gq[k] += g.quat[k];
@@ -1023,8 +1056,11 @@ int oracle_project_bwd(const gs3d_project_bwd_args* a) {
         }
         if (a->grad_means)
             for (int k = 0; k < 3; ++k) a->grad_means[3 * i + k] = (float)gm[k];
-        if (a->grad_quats)
-            for (int k = 0; k < 4; ++k) a->grad_quats[4 * i + k] = (float)gq[k];
+        if (a->grad_quats) {
+            float g4[4] = {(float)gq[0], (float)gq[1], (float)gq[2], (float)gq[3]};
+            if (a->normalize_quats) normalize_quat_vjp(quat, qnorm, g4);
+            for (int k = 0; k < 4; ++k) a->grad_quats[4 * i + k] = g4[k];
+        }
         if (a->grad_scales)
             for (int k = 0; k < 3; ++k) a->grad_scales[3 * i + k] = (float)gs[k];
         if (a->grad_opacities) a->grad_opacities[i] = (float)go;
@@ -1070,6 +1106,20 @@ int oracle_projection_vjp_f64(const double* mean, const double* quat, const doub
 float oracle_expf(float x) { return gs_expf(x); }
 
 float oracle_logf(float x) { return gs_logf(x); }
+
+// Normalised quaternions u and gradients through the normalisation of count
+// raw quaternions q with upstream gradients g (g and grad may be NULL).
+int oracle_normalize_quats(const float* q, int64_t count, float* u, const float* g, float* grad) {
+    for (int64_t i = 0; i < count; ++i) {
+        const float norm = normalize_quat(q + 4 * i, u + 4 * i);
+        if (g && grad) {
+            float gi[4] = {g[4 * i], g[4 * i + 1], g[4 * i + 2], g[4 * i + 3]};
+            normalize_quat_vjp(u + 4 * i, norm, gi);
+            for (int k = 0; k < 4; ++k) grad[4 * i + k] = gi[k];
+        }
+    }
+    return 0;
+}
 
 int oracle_tile_footprint(int32_t mode, const float* center, const float* conic, int32_t radius, int32_t gx,
                           int32_t gy, int64_t* tiles, int32_t* bounds) {

@@ -4,8 +4,9 @@ Composes the oracle stages in the order the reference composes its kernels
 (gs3d/api.py:116-255 and gs3d/autograd.py:91-171): camera rows, projection
 (+SH), scan, emission, sort, ranges, blending; then the blend VJP, the
 projection (+SH) VJP and the camera VJP.  Inputs are NumPy copies of the
-tensors the GPU path consumed (quaternions already normalised on the device,
-as the parity rule of the survey requires).
+tensors the GPU path consumed; with normalize_quats the quaternions are raw
+and the oracle normalises them (and takes their gradient through the
+normalisation) exactly as the projection kernels do.
 """
 
 import numpy as np
@@ -14,14 +15,16 @@ import oracle
 
 
 def run(means, quats, scales, opacities, viewmats, Ks, width, height, *, features=None, sh=None, sh_degree=None,
-        extra=None, background=None, near=0.2, far=float("inf"), radius_clip=0.0, upstream=None, absgrad=False):
+        extra=None, background=None, near=0.2, far=float("inf"), radius_clip=0.0, upstream=None, absgrad=False,
+        normalize_quats=False):
     views = viewmats.shape[0]
     with_centers = sh is not None and sh_degree > 0
     full, inverse, centers, errors = oracle.camera_prepare(viewmats, Ks, width, height, with_centers)
     assert np.all(errors == 0), errors
     proj = oracle.project_fwd(means, quats, scales, opacities, viewmats, full, Ks, width, height, near, far,
                               radius_clip, sh=sh, sh_degree=sh_degree or 0,
-                              camera_centers=centers if with_centers else None, metadata=True)
+                              camera_centers=centers if with_centers else None, metadata=True,
+                              normalize_quats=normalize_quats)
     offsets, total = oracle.scan_i32(proj["tiles"].ravel())
     keys, vals = oracle.emit_keys(proj["centers"], proj["radii"], proj["depths"], offsets, total, width, height)
     T = views * ((width + 15) // 16) * ((height + 15) // 16)
@@ -41,7 +44,7 @@ def run(means, quats, scales, opacities, viewmats, Ks, width, height, *, feature
     pg = oracle.project_bwd(means, quats, scales, opacities, viewmats, full, Ks, width, height, proj["radii"],
                             g["centers"], g["conics"], sh=sh, sh_degree=sh_degree or 0,
                             camera_centers=centers if with_centers else None,
-                            grad_colors=g["features"] if sh is not None else None)
+                            grad_colors=g["features"] if sh is not None else None, normalize_quats=normalize_quats)
     out["proj_grads"] = pg
     gview = oracle.camera_backward(Ks, pg["projection"], width, height, inverse if with_centers else full,
                                    pg.get("camera_centers") if with_centers else None)

@@ -398,3 +398,41 @@ def test_u32_radix_sort_stable(count, end_bit):
     order = np.argsort(keys, kind="stable")
     np.testing.assert_array_equal(_np(k[:count]).view(np.uint32), keys[order])
     np.testing.assert_array_equal(_np(v[:count]), vals[order])
+
+
+@pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3)])
+def test_projection_normalizes_raw_quaternions(key, degree):
+    # Raw (unnormalised, some tiny or zero) quaternions: the kernels normalise
+    # them as F.normalize does and take the gradient through it; forward
+    # bit-exact and gradients within tolerance of the oracle doing the same.
+    scene = _scene(key)
+    _say(f"projection raw quats {key}")
+    g = torch.Generator().manual_seed(9)
+    n = scene.means.shape[0]
+    raw = scene.quats * (torch.rand((n, 1), generator=g) * 5 + 0.05).to(DEV)
+    raw[::97] = 1e-14
+    raw[5::211] = 0.0
+    with_centers = bool(degree)
+    full, inverse, centers, errors = cameras.launch_prepare(scene.viewmats, scene.Ks, scene.width, scene.height,
+                                                            with_centers)
+    st = gproj.project_views(scene.means, raw, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks,
+                             scene.width, scene.height, 0.2, float("inf"), 0.0,
+                             sh=scene.sh_coeffs if degree is not None else None, sh_degree=degree or 0,
+                             camera_centers=centers if with_centers else None, metadata=True, normalize_quats=True)
+    ref = oracle.project_fwd(_np(scene.means), _np(raw), _np(scene.scales), _np(scene.opacities),
+                             _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height,
+                             sh=_np(scene.sh_coeffs) if degree is not None else None, sh_degree=degree or 0,
+                             camera_centers=_np(centers) if degree else None, metadata=True, normalize_quats=True)
+    for name, got in (("radii", st.radii), ("centers", st.centers), ("conics", st.conics), ("depths", st.depths)):
+        np.testing.assert_array_equal(_np(got), ref[name], err_msg=name)
+    views = st.radii.shape[0]
+    gc = torch.randn((views, n, 2), generator=g).to(DEV)
+    gk = torch.randn((views, n, 4), generator=g).to(DEV) * 0.1
+    res = gproj.backward_views(scene.means, raw, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks,
+                               scene.width, scene.height, st.radii, gc, gk, (True, True, True, True, False, False),
+                               normalize_quats=True)
+    rb = oracle.project_bwd(_np(scene.means), _np(raw), _np(scene.scales), _np(scene.opacities),
+                            _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height, _np(st.radii),
+                            _np(gc), _np(gk), normalize_quats=True)
+    for name in ("means", "quats", "scales", "opacities"):
+        compare(f"raw_{name}", _np(res[name]), rb[name], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(rb[name]).max()))

@@ -211,3 +211,25 @@ def test_float32_vjp_tracks_float64(oracle_lib):
             np.testing.assert_allclose(g32[name][i], v[key], rtol=2e-3, atol=2e-3 * np.abs(v[key]).max() + 1e-6)
     np.testing.assert_allclose(g32["view"][0], view64, rtol=2e-3, atol=1e-3 * np.abs(view64).max())
     np.testing.assert_allclose(g32["projection"][0], proj64, rtol=2e-3, atol=1e-3 * np.abs(proj64).max())
+
+
+def test_quaternion_normalization_matches_torch(oracle_lib):
+    # The projection normalises raw quaternions as torch.nn.functional.normalize
+    # (reference inputs.py:252) and differentiates through it; checked against
+    # torch float64 autograd, with the zero and tiny quaternions clamped at 1e-12.
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn((500, 4), generator=g) * torch.rand((500, 1), generator=g) * 10
+    q[0] = 0.0
+    q[1] = torch.tensor([1.0, 0.0, 0.0, 0.0])
+    q[2] = 3e-13
+    up = torch.randn((500, 4), generator=g)
+    u, grad = oracle_lib.normalize_quats(q.numpy(), up.numpy())
+    q64 = q.double().requires_grad_(True)
+    ref = torch.nn.functional.normalize(q64, dim=-1)
+    ref.backward(up.double())
+    np.testing.assert_allclose(u, ref.detach().numpy(), rtol=2e-7, atol=1e-7)
+    big = np.abs(q.numpy()).max(-1) > 1e-6
+    np.testing.assert_allclose(grad[big], q64.grad.numpy()[big], rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(u[0], np.zeros(4, np.float32))
+    np.testing.assert_array_equal(u[1], [1.0, 0.0, 0.0, 0.0])
+    np.testing.assert_allclose(grad[0], up[0].numpy() / np.float32(1e-12), rtol=1e-6)
