@@ -181,6 +181,14 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32
     for (int c = 0; c < CH; ++c) dst[c] = v[c];
 }
 
+// 0.0f that the compiler cannot see through (a register written by an
+// opaque move), so accumulators initialised from it are updated in place.
+GS3D_DEV float opaque_zero() {
+    float z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
 // One staged Gaussian as the blend loops read it from LDS.  The loops load
 // the next Gaussian of their wavefront before blending the current one, so
 // the LDS latency overlaps the arithmetic.
@@ -348,8 +356,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
                     }
                     const float w = alpha * T[k];
 #pragma unroll
-                    for (int c = 0; c < CH; ++c)
-                        if (c < D) color[k][c] = __builtin_fmaf(f[c], w, color[k][c]);
+                    for (int c = 0; c < CH; ++c) color[k][c] = __builtin_fmaf(f[c], w, color[k][c]);  // zero slots >= D
                     T[k] = next_t;
                     last_contributor[k] = contributor;
                     acc[k] = true;
@@ -523,10 +530,18 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
             const float4 con = s_con[j];
             const float cut = s_cut[j];
             const float* f = s_feat + j * CH;
+            // Accumulators start from an opaque zero: a literal zero would be
+            // folded into each accumulator's first FMA, and every path that
+            // skips a pixel would then re-materialise the zeros.
             float gfeat[CH];
-            float dcx = 0.0f, dcy = 0.0f, gk0 = 0.0f, gk1 = 0.0f, gk2 = 0.0f, gk3 = 0.0f, ax = 0.0f, ay = 0.0f;
+            float dcx = opaque_zero(), dcy = opaque_zero(), gk0 = opaque_zero(), gk1 = opaque_zero();
+            float gk2 = opaque_zero(), gk3 = opaque_zero(), ax = 0.0f, ay = 0.0f;
+            if (ABS) {
+                ax = opaque_zero();
+                ay = opaque_zero();
+            }
 #pragma unroll
-            for (int c = 0; c < CH; ++c) gfeat[c] = 0.0f;
+            for (int c = 0; c < CH; ++c) gfeat[c] = opaque_zero();
             bool accepted = false;
 #pragma unroll
             for (int k = 0; k < PIX; ++k) {
@@ -543,15 +558,18 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
                 const float inv = __builtin_amdgcn_rcpf(1.0f - alpha);
                 T[k] = T[k] * inv;
                 const float la = last_alpha[k], keep = 1.0f - la, aT = alpha * T[k];
+                // Every compiled channel slot is processed: slots at or beyond
+                // D hold zero features and zero upstream gradients (no
+                // contribution), and the constant alpha channel's entry has no
+                // destination, so no per-channel branch is needed.
                 float grad_alpha = 0.0f;
 #pragma unroll
-                for (int c = 0; c < CH; ++c)
-                    if (c < D) {
-                        accum[k][c] = __builtin_fmaf(la, last_color[k][c], keep * accum[k][c]);
-                        last_color[k][c] = f[c];
-                        grad_alpha = __builtin_fmaf(f[c] - accum[k][c], grad[k][c], grad_alpha);
-                        if (c < Dg) gfeat[c] = __builtin_fmaf(aT, grad[k][c], gfeat[c]);
-                    }
+                for (int c = 0; c < CH; ++c) {
+                    accum[k][c] = __builtin_fmaf(la, last_color[k][c], keep * accum[k][c]);
+                    last_color[k][c] = f[c];
+                    grad_alpha = __builtin_fmaf(f[c] - accum[k][c], grad[k][c], grad_alpha);
+                    gfeat[c] = __builtin_fmaf(aT, grad[k][c], gfeat[c]);
+                }
                 grad_alpha = __builtin_fmaf(grad_alpha, T[k], -(T_final[k] * inv) * bg_grad[k]);
                 last_alpha[k] = alpha;
                 const float gv = con.w * grad_alpha;
