@@ -311,32 +311,9 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
             // This wavefront's Gaussians of the next 64, in list order.
             uint64_t todo = __ballot(c0 + lane < cnt && ((s_mask[min(c0 + lane, B - 1)] >> wave) & 1u));
             if (!todo) continue;
-            int jn = c0 + __builtin_ctzll(todo);
-            todo &= todo - 1;
-            Staged<CH> cur = load_staged<CH>(jn, s_xy, s_con, s_cut, s_feat);
-            while (true) {
-                bool any = false;
-#pragma unroll
-                for (int k = 0; k < PIX; ++k) any = any || !done[k];
-                if (__ballot(any) == 0) {
-                    live = false;
-                    break;
-                }
-                const int j = jn;
-                const bool more = todo != 0;
-                Staged<CH> nxt = cur;
-                if (more) {
-                    jn = c0 + __builtin_ctzll(todo);
-                    todo &= todo - 1;
-                    // The statistics variant loads at use: its extra
-                    // registers would otherwise cost occupancy.
-                    if constexpr (!STATS) nxt = load_staged<CH>(jn, s_xy, s_con, s_cut, s_feat);
-                }
+            // Blend one Gaussian (batch slot j) into this lane's pixels.
+            auto blend = [&](const Staged<CH>& g, int j) {
                 const int contributor = begin - t.first + j + 1;  // list position, 1-based
-                const float2 xy = cur.xy;
-                const float4 con = cur.con;
-                const float cut = cur.cut;
-                const float* f = cur.f;
                 bool acc[PIX];
                 float wk[PIX];
 #pragma unroll
@@ -344,10 +321,10 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
                     acc[k] = false;
                     wk[k] = 0.0f;
                     if (done[k]) continue;
-                    const float dx = xy.x - fx[k], dy = xy.y - fy[k];
-                    const float power = blend_power(con.x, con.y, con.z, dx, dy);
-                    if (!(power <= 0.0f) || !(power >= cut)) continue;
-                    const float alpha = sel_min(0.99f, con.w * blend_exp(power));
+                    const float dx = g.xy.x - fx[k], dy = g.xy.y - fy[k];
+                    const float power = blend_power(g.con.x, g.con.y, g.con.z, dx, dy);
+                    if (!(power <= 0.0f) || !(power >= g.cut)) continue;
+                    const float alpha = sel_min(0.99f, g.con.w * blend_exp(power));
                     if (!(alpha >= 1.0f / 255.0f)) continue;
                     const float next_t = T[k] * (1.0f - alpha);
                     if (next_t < 0.0001f) {
@@ -356,7 +333,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
                     }
                     const float w = alpha * T[k];
 #pragma unroll
-                    for (int c = 0; c < CH; ++c) color[k][c] = __builtin_fmaf(f[c], w, color[k][c]);  // zero slots >= D
+                    for (int c = 0; c < CH; ++c) color[k][c] = __builtin_fmaf(g.f[c], w, color[k][c]);  // zero slots >= D
                     T[k] = next_t;
                     last_contributor[k] = contributor;
                     acc[k] = true;
@@ -368,11 +345,58 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
                     for (int k = 0; k < PIX; ++k) hit = hit || acc[k];
                     if (__ballot(hit)) observe_statistics<PIX>(st, t.view, a.n, s_id[j], acc, wk, val, lane);
                 }
-                if (!more) break;
-                if constexpr (STATS)
-                    cur = load_staged<CH>(jn, s_xy, s_con, s_cut, s_feat);
-                else
-                    cur = nxt;
+            };
+            auto alive = [&]() {
+                bool any = false;
+#pragma unroll
+                for (int k = 0; k < PIX; ++k) any = any || !done[k];
+                return __ballot(any) != 0;
+            };
+            auto take = [&]() {
+                const int j = c0 + __builtin_ctzll(todo);
+                todo &= todo - 1;
+                return j;
+            };
+            if constexpr (STATS) {
+                // Loads at use: the pipelined form's extra registers would
+                // cost this variant occupancy.
+                while (todo) {
+                    if (!alive()) {
+                        live = false;
+                        break;
+                    }
+                    const int j = take();
+                    blend(load_staged<CH>(j, s_xy, s_con, s_cut, s_feat), j);
+                }
+            } else {
+                // Unrolled by two: the next Gaussian is loaded into the other
+                // buffer before the current one is blended.
+                int ja = take(), jb = 0;
+                Staged<CH> ga = load_staged<CH>(ja, s_xy, s_con, s_cut, s_feat), gb;
+                while (true) {
+                    if (!alive()) {
+                        live = false;
+                        break;
+                    }
+                    bool more = todo != 0;
+                    if (more) {
+                        jb = take();
+                        gb = load_staged<CH>(jb, s_xy, s_con, s_cut, s_feat);
+                    }
+                    blend(ga, ja);
+                    if (!more) break;
+                    if (!alive()) {
+                        live = false;
+                        break;
+                    }
+                    more = todo != 0;
+                    if (more) {
+                        ja = take();
+                        ga = load_staged<CH>(ja, s_xy, s_con, s_cut, s_feat);
+                    }
+                    blend(gb, jb);
+                    if (!more) break;
+                }
             }
         }
     }
