@@ -279,7 +279,10 @@ __global__ __launch_bounds__(kEmitThreads) void emit_accutile_kernel(gs3d_emit_a
 // by digit in LDS and writes them out in digit runs (coalesced).
 // ---------------------------------------------------------------------------
 constexpr int kSortThreads = 256;
-constexpr int kSortItems = 16;
+#ifndef GS3D_SORT_ITEMS
+#define GS3D_SORT_ITEMS 8
+#endif
+constexpr int kSortItems = GS3D_SORT_ITEMS;  // keys per thread of a sort tile
 constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 keys
 constexpr int kRadix = 256;
 
