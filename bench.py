@@ -96,7 +96,7 @@ def step_fn(scene, leaves, colors, extra, viewmats, tile_mode="radius"):
                              scene.Ks, scene.width, scene.height, features=None if sh else colors,
                              sh_coeffs=colors if sh else None, sh_degree=scene.sh_degree,
                              extra_features=extra, absgrad=scene.absgrad, tile_mode=tile_mode)
-        forward.pairs = res.meta["tiles_per_gauss"].sum()
+        forward.meta = res.meta
         D = res.features.shape[-1]
         loss = (res.features * W[..., :D]).sum() + (res.alpha * W[..., -1:]).sum()
         if res.extra_features is not None:
@@ -319,7 +319,7 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1000.0 / args.steps
-    modes = {args.tile_mode: dict(ms=round(ms, 3), pairs=int(forward.pairs))}
+    modes = {args.tile_mode: dict(ms=round(ms, 3), pairs=int(forward.meta["tiles_per_gauss"].sum()))}
     for mode in ("radius", "snugbox", "accutile"):
         if mode == args.tile_mode or args.mode_steps <= 0:
             continue
@@ -331,7 +331,8 @@ def main():
         for _ in range(args.mode_steps):
             b_m(f_m())
         torch.cuda.synchronize()
-        modes[mode] = dict(ms=round((time.perf_counter() - ta) * 1000.0 / args.mode_steps, 3), pairs=int(f_m.pairs))
+        modes[mode] = dict(ms=round((time.perf_counter() - ta) * 1000.0 / args.mode_steps, 3),
+                           pairs=int(f_m.meta["tiles_per_gauss"].sum()))
     if args.copy_calibration_mib > 0:
         src = torch.ones(args.copy_calibration_mib << 18, device=device)
         dst = torch.empty_like(src)

@@ -644,10 +644,12 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
             const int64_t row = (int64_t)v * n + i;
             const bool vis = valid && a.radii[row] > 0;
             VJP g;
+            float2 screen = make_float2(0.0f, 0.0f);
             if (vis) {
                 const float* gcp = a.grad_centers + row * a.grad_centers_stride;
                 const float* gkp = a.grad_conics + row * a.grad_conics_stride;
                 const float gc[2] = {gcp[0], gcp[1]};
+                screen = make_float2(gc[0], gc[1]);
                 const float gk[4] = {gkp[0], gkp[1], gkp[2], gkp[3]};
                 projection_vjp(mean, q, s, a.view + 16 * v, a.projection + 16 * v, a.width, a.height,
                                a.intrinsics[9 * v], a.intrinsics[9 * v + 4], gc, gk, g);
@@ -659,6 +661,7 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
                 for (int k = 0; k < 3; ++k) gs[k] += g.scale[k];
                 go += g.opacity;
             }
+            if (a.screen_grad && valid) reinterpret_cast<float2*>(a.screen_grad)[row] = screen;
             if constexpr (CAM) {
                 if (v < kMaxViewsCamLds) {
 #pragma unroll

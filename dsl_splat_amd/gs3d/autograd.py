@@ -113,15 +113,18 @@ class Rasterize(torch.autograd.Function):
         proj_needs = (needs[0], needs[1], needs[2], needs[3], needs[6], needs[6])
         want_sh = sh and (needs[4] or (frame.sh_degree > 0 and (needs[0] or needs[6])))
         grads = dict(means=None, quats=None, scales=None, opacities=None, view=None, projection=None, sh=None,
-                     camera_centers=None)
+                     camera_centers=None, screen=None)
         if any(proj_needs) or want_sh:
             grads = projection.backward_views(
                 means, quats, scales, opacities, viewmats.detach(), frame.full, frame.Ks, frame.width,
                 frame.height, st.radii, grad_centers, grad_conics, proj_needs,
                 sh=colors if sh else None, sh_degree=frame.sh_degree or 0, camera_centers=frame.camera_centers,
                 grad_colors=grad_blended if sh else None, need_sh=sh and needs[4], normalize_quats=True,
-                need_centers=sh and (frame.sh_degree or 0) > 0 and needs[6],
+                need_centers=sh and (frame.sh_degree or 0) > 0 and needs[6], need_screen=needs[7],
             )
+        if grads["screen"] is not None:
+            # Contiguous rows: the means2d leaf accumulates them without a strided copy.
+            grad_centers = grads["screen"]
         grad_view = None
         if needs[6]:
             grad_view = camera_backward(frame.Ks, grads["projection"], frame.width, frame.height,

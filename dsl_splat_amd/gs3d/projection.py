@@ -106,12 +106,14 @@ def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tens
                    grad_centers: Tensor, grad_conics: Tensor, needs: tuple[bool, ...], *,
                    sh: Tensor | None = None, sh_degree: int = 0, camera_centers: Tensor | None = None,
                    grad_colors: Tensor | None = None, need_sh: bool = False, need_centers: bool = False,
-                   normalize_quats: bool = False):
+                   normalize_quats: bool = False, need_screen: bool = False):
     """Projection (+SH) VJP summed over views; with ``normalize_quats`` the
     quaternions are raw and their gradient includes the normalisation.
 
     ``needs`` = (means, quats, scales, opacities, view, projection).
-    grad_centers / grad_conics may be strided views with unit inner stride.
+    grad_centers / grad_conics may be strided views with unit inner stride;
+    ``need_screen`` also returns grad_centers as a contiguous (views, N, 2)
+    tensor under "screen" (zero where radii are not positive).
     Returns dict with the requested gradients (None otherwise).
     """
     device = means.device
@@ -119,7 +121,7 @@ def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tens
     views = radii.shape[0]
     f32 = dict(dtype=torch.float32, device=device)
     res = dict(means=None, quats=None, scales=None, opacities=None, view=None, projection=None,
-               sh=None, camera_centers=None)
+               sh=None, camera_centers=None, screen=None)
     if n == 0:
         for key, shape in (("view", (views, 4, 4)), ("projection", (views, 4, 4))):
             res[key] = torch.zeros(shape, **f32)
@@ -136,6 +138,8 @@ def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tens
         res["view"] = torch.zeros((views, 4, 4), **f32)
     if needs[5]:
         res["projection"] = torch.zeros((views, 4, 4), **f32)
+    if need_screen:
+        res["screen"] = torch.empty((views, n, 2), **f32)
     means, quats, scales, opacities = (t.contiguous() for t in (means, quats, scales, opacities))
     view, projection, intrinsics = (t.reshape(views, *t.shape[-2:]).contiguous() for t in (view, projection, intrinsics))
     radii = radii.contiguous()
@@ -156,6 +160,7 @@ def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tens
     a.grad_opacities = native.ptr(res["opacities"])
     a.grad_view = native.ptr(res["view"])
     a.grad_projection = native.ptr(res["projection"])
+    a.screen_grad = native.ptr(res["screen"])
     keep = [means, quats, scales, opacities, view, projection, intrinsics, radii]
     if sh is not None:
         sh, stride, rows = _sh_layout(sh, views)

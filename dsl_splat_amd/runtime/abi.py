@@ -9,7 +9,7 @@ import ctypes
 c_float_p = ctypes.POINTER(ctypes.c_float)
 c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Tile modes (GS3D_TILE_*), named as the reference's TileMode literals.
 TILE_MODES = {"radius": 0, "snugbox": 1, "accutile": 2}
@@ -101,6 +101,7 @@ class ProjectBwdArgs(ctypes.Structure):
         ("grad_sh", _P),
         ("grad_camera_centers", _P),
         ("normalize_quats", ctypes.c_int32),
+        ("screen_grad", ctypes.c_void_p),
     ]
 
 

@@ -158,6 +158,10 @@ typedef struct gs3d_project_bwd_args {
     float* grad_sh;               /* like sh (dense, rows beyond (deg+1)^2 are zero) */
     float* grad_camera_centers;   /* (views,3) accumulated */
     int32_t normalize_quats;      /* 1: quats are raw; grad_quats is taken through the normalisation */
+    /* (views,N,2) contiguous copy of the centre gradients, zero where radii
+     * are not positive: the means2d gradient without a strided copy.  May be
+     * NULL. */
+    float* screen_grad;
 } gs3d_project_bwd_args;
 
 int gs3d_project_bwd(const gs3d_project_bwd_args* args, void* stream);

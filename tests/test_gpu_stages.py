@@ -261,7 +261,10 @@ def test_projection_backward_parity(key, degree):
                                scene.width, scene.height, st.radii, gc, gk, (True,) * 6,
                                sh=scene.sh_coeffs if degree is not None else None, sh_degree=degree or 0,
                                camera_centers=centers if degree else None, grad_colors=gcol,
-                               need_sh=degree is not None, need_centers=bool(degree))
+                               need_sh=degree is not None, need_centers=bool(degree), need_screen=True)
+    # The contiguous screen gradient is grad_centers where radii > 0 and zero elsewhere, bit for bit.
+    visible = (st.radii > 0).unsqueeze(-1)
+    assert torch.equal(res["screen"], torch.where(visible, gc, torch.zeros_like(gc)))
     ref = oracle.project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
                              _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height, _np(st.radii),
                              _np(gc), _np(gk), sh=_np(scene.sh_coeffs) if degree is not None else None,
