@@ -17,6 +17,8 @@
 #include "common.hpp"
 #include "footprint.hpp"
 
+#include <type_traits>
+
 namespace gs3d {
 
 constexpr int kProjBlock = 128;
@@ -197,6 +199,7 @@ GS3D_DEV float sh_basis(const float* u, int k) {
 }
 
 GS3D_DEV void sh_basis_grad(const float* u, int k, float* g) {
+#pragma clang fp contract(fast)  // backward only: compared within a tolerance
     const float x = u[0], y = u[1], z = u[2];
     const float C1 = 0.4886025119029199f, C4 = 1.0925484305920792f, C6 = 0.31539156525252005f,
                 C8 = 0.5462742152960396f, C9 = 0.5900435899266435f, C10 = 2.890611442640554f,
@@ -317,114 +320,27 @@ GS3D_DEV void sh_backward(const float* coef, const float* dir, bool visible, con
 }
 
 // ---------------------------------------------------------------------------
-// LDS staging of SH blocks.  Rows of `row_floats` contiguous floats (only
-// the first `need` are kept) for `count` Gaussians; LDS rows have an odd
-// pitch so the per-thread row reads are bank-conflict free.
+// Forward projection of every view, one thread per Gaussian (the colours are
+// evaluated by sh_rows_fwd_kernel in a second launch).
 // ---------------------------------------------------------------------------
-template <int B>
-GS3D_DEV void stage_rows_in(const float* __restrict__ src, int count, int row_floats, int need, float* lds, int pad) {
-    if ((row_floats & 3) == 0 && ((reinterpret_cast<uintptr_t>(src) & 15) == 0)) {
-        const int rf4 = row_floats >> 2;
-        const int total = count * rf4;
-        const float4* s4 = reinterpret_cast<const float4*>(src);
-        int g = threadIdx.x / rf4, c = threadIdx.x - g * rf4;
-        const int sg = B / rf4, sc = B - sg * rf4;
-        for (int idx = threadIdx.x; idx < total; idx += B) {
-            if (4 * c < need) {
-                const float4 v = s4[idx];
-                float* dst = lds + g * pad + 4 * c;
-                dst[0] = v.x;
-                if (4 * c + 1 < need) dst[1] = v.y;
-                if (4 * c + 2 < need) dst[2] = v.z;
-                if (4 * c + 3 < need) dst[3] = v.w;
-            }
-            g += sg;
-            c += sc;
-            if (c >= rf4) {
-                c -= rf4;
-                g += 1;
-            }
-        }
-        return;
-    }
-    const int total = count * row_floats;
-    int g = threadIdx.x / row_floats, c = threadIdx.x - g * row_floats;
-    const int sg = B / row_floats, sc = B - sg * row_floats;
-    for (int idx = threadIdx.x; idx < total; idx += B) {
-        if (c < need) lds[g * pad + c] = src[idx];
-        g += sg;
-        c += sc;
-        if (c >= row_floats) {
-            c -= row_floats;
-            g += 1;
-        }
-    }
-}
-
-// Inverse of stage_rows_in: write rows to global, zero beyond `need`.
-template <int B>
-GS3D_DEV void stage_rows_out(float* __restrict__ dst, int count, int row_floats, int need, const float* lds, int pad) {
-    const int total = count * row_floats;
-    int g = threadIdx.x / row_floats, c = threadIdx.x - g * row_floats;
-    const int sg = B / row_floats, sc = B - sg * row_floats;
-    for (int idx = threadIdx.x; idx < total; idx += B) {
-        dst[idx] = c < need ? lds[g * pad + c] : 0.0f;
-        g += sg;
-        c += sc;
-        if (c >= row_floats) {
-            c -= row_floats;
-            g += 1;
-        }
-    }
-}
-
-template <int DEG>
-struct ShLayout {
-    static constexpr int need = DEG >= 0 ? 3 * (DEG + 1) * (DEG + 1) : 0;
-    static constexpr int pad = need | 1;
-    static constexpr int lds = DEG >= 0 ? kProjBlock * pad : 1;
-    static constexpr int regs = need > 0 ? need : 1;
-};
-
-// ---------------------------------------------------------------------------
-// Forward.  DEG < 0: no SH evaluation in this launch.
-// ---------------------------------------------------------------------------
-template <int DEG, bool META>
+template <bool META>
 __global__ __launch_bounds__(kProjBlock) void project_fwd_kernel(gs3d_project_args a) {
-    using L = ShLayout<DEG>;
-    __shared__ float s_sh[L::lds];
     const int n = a.n;
-    const int64_t base = (int64_t)blockIdx.x * kProjBlock;
-    const int64_t i = base + threadIdx.x;
-    const bool valid = i < n;
-    float mean[3] = {0, 0, 0}, q[4] = {1, 0, 0, 0}, s[3] = {1, 1, 1}, opac = 0.0f;
-    if (valid) {
+    const int64_t i = (int64_t)blockIdx.x * kProjBlock + threadIdx.x;
+    if (i >= n) return;
+    float mean[3], q[4], s[3];
 #pragma unroll
-        for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
-        const float4 qq = reinterpret_cast<const float4*>(a.quats)[i];
-        q[0] = qq.x;
-        q[1] = qq.y;
-        q[2] = qq.z;
-        q[3] = qq.w;
-        if (a.normalize_quats) normalize_quat(q);
+    for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
+    const float4 qq = reinterpret_cast<const float4*>(a.quats)[i];
+    q[0] = qq.x;
+    q[1] = qq.y;
+    q[2] = qq.z;
+    q[3] = qq.w;
+    if (a.normalize_quats) normalize_quat(q);
 #pragma unroll
-        for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
-        opac = a.opacities[i];
-    }
-    // Coefficients are read from the LDS staging (odd pitch: conflict-free)
-    // where they are used, which keeps them out of registers.
-    const float* coef = s_sh + threadIdx.x * L::pad;
-    const int count = (int)min((int64_t)kProjBlock, (int64_t)n - base);
+    for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
+    const float opac = a.opacities[i];
     for (int v = 0; v < a.views; ++v) {
-        if constexpr (DEG >= 0) {
-            if (v == 0 || a.sh_view_stride != 0) {
-                __syncthreads();
-                const int rf = a.sh_rows * 3;
-                stage_rows_in<kProjBlock>(a.sh + v * a.sh_view_stride + base * rf, count, rf, L::need, s_sh, L::pad);
-                __syncthreads();
-            }
-        }
-        if (!valid) continue;
         const float* V = a.view + 16 * v;
         const float* P = a.projection + 16 * v;
         const float fx = a.intrinsics[9 * v], fy = a.intrinsics[9 * v + 4];
@@ -439,17 +355,6 @@ __global__ __launch_bounds__(kProjBlock) void project_fwd_kernel(gs3d_project_ar
         a.radii[row] = f.radius;
         a.tiles[row] = f.tiles;
         a.depths[row] = f.depth;
-        if constexpr (DEG >= 0) {
-            float dir[3] = {0.0f, 0.0f, 0.0f};
-            if (DEG > 0) {
-#pragma unroll
-                for (int k = 0; k < 3; ++k) dir[k] = mean[k] - a.camera_centers[3 * v + k];
-            }
-            float color[3], raw[3];
-            sh_eval<DEG >= 0 ? DEG : 0>(coef, dir, vis, color, raw);
-#pragma unroll
-            for (int k = 0; k < 3; ++k) a.colors[3 * row + k] = color[k];
-        }
         if constexpr (META) {
             reinterpret_cast<float2*>(a.means2d)[row] = make_float2(f.center[0], f.center[1]);
             a.meta_opacities[row] = vis ? opac : 0.0f;
@@ -477,6 +382,7 @@ struct VJP {
 
 // C = A*B: gA += gC B^T, gB += A^T gC.
 GS3D_DEV void matmul_vjp(const M3& A, const M3& B, const M3& gC, M3& gA, M3& gB) {
+#pragma clang fp contract(fast)
 #pragma unroll
     for (int i = 0; i < 3; ++i)
 #pragma unroll
@@ -503,6 +409,10 @@ GS3D_DEV M3 zero3() {
 
 GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, const float* V, const float* P,
                              int width, int height, float fx, float fy, const float* gc, const float* gk, VJP& g) {
+    // Gradients are compared within a tolerance: products and sums here may
+    // fuse (the recomputed forward quantities come from the shared helpers,
+    // which keep the forward's rounding).
+#pragma clang fp contract(fast)
     float pos[3];
 #pragma unroll
     for (int r = 0; r < 3; ++r) pos[r] = point_row(V, r, mean);
@@ -614,7 +524,7 @@ GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, 
 template <bool CAM>
 __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bwd_args a) {
     // Wave-private camera accumulators: [wave][view][entry] (view and
-    // projection rows; the SH camera centre is handled by sh_views_bwd_kernel).
+    // projection rows; the SH camera centre is handled by sh_rows_bwd_kernel).
     __shared__ float s_cam[CAM ? kProjBlock / 64 : 1][kMaxViewsCamLds][24];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = a.n;
@@ -711,228 +621,363 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
     }
 }
 
-// SH VJP (primitives/sh.py:82-138 with the "means - camera centre" VJP of
-// gs3d/api.py:160-164) over all views, one lane per (Gaussian, colour
-// channel): 21 Gaussians per wavefront, lane 3j + c holds channel c of
-// Gaussian j, its (DEG+1)^2 coefficients and their gradients in registers
-// while the wavefront's contiguous coefficient block (21 rows) moves between
-// HBM and a per-wavefront LDS slice with coalesced float4 accesses.  Each
-// lane evaluates its
-// channel exactly as the forward did (same clamp decisions), accumulates its
-// coefficient gradients (summed over views when the coefficients are shared)
-// and its part of the direction gradient; the three lanes of a Gaussian sum
-// the direction gradient with shuffles, and lane c adds component c to
-// grad_means (after project_bwd_kernel wrote it).  With CAM, the
-// camera-centre gradients are reduced per wavefront into LDS accumulators.
-constexpr int kShBlock = 256;
-constexpr int kShPerWave = 21;
-constexpr int kShStageFloats = kShPerWave * 49;  // per-wavefront LDS slice (rows of up to 48 floats, pitch + 1)
-constexpr int kShPrefetch = 4;                    // views whose inputs are loaded up front
+constexpr int kShPrefetch = 4;  // views whose per-view inputs are loaded up front
 
-// Copy `rows` rows of RF contiguous floats between global memory and a
-// wavefront's LDS slice, where rows have the odd pitch RF + 1 (per-lane
-// column reads are then free of bank conflicts).  Global accesses are float4
-// when rows and the address allow it; the wavefront's LDS traffic is ordered
-// by the fence that follows.
-template <bool TO_LDS, int RF>
-GS3D_DEV void wave_copy(float* lds, float* glob, int rows) {
-    constexpr int rf = RF;
+constexpr int kShRowBlock = 256;
+// A wavefront's 64 rows of RF contiguous floats (16-byte aligned, RF a
+// multiple of 4) between global memory and its LDS slice, where rows have the
+// odd pitch RF + 1 (per-lane row reads are then free of bank conflicts).
+// Every lane issues all of its float4 accesses before the first LDS write
+// (one memory latency per copy); rows beyond `rows` are not touched.
+template <int RF>
+GS3D_DEV void rows_to_lds(float* lds, const float* glob, int rows) {
+    static_assert(RF % 4 == 0, "float4 rows");
+    constexpr int IT = RF / 4;  // float4s per lane for 64 rows
     const int lane = lane_id();
-    const int floats = rows * rf;
-    if (((reinterpret_cast<uintptr_t>(glob) & 15) == 0) && (rf & 3) == 0) {  // rf: compile-time
-        for (int e4 = lane; e4 < (floats >> 2); e4 += 64) {
-            const int e = e4 << 2;
-            const int row = e / rf;
-            float* l = lds + e + row;
-            if (TO_LDS) {
-                const float4 v = reinterpret_cast<const float4*>(glob)[e4];
-                l[0] = v.x;
-                l[1] = v.y;
-                l[2] = v.z;
-                l[3] = v.w;
-            } else {
-                reinterpret_cast<float4*>(glob)[e4] = make_float4(l[0], l[1], l[2], l[3]);
-            }
-        }
-    } else {
-        for (int e = lane; e < floats; e += 64) {
-            const int row = e / rf;
-            if (TO_LDS)
-                lds[e + row] = glob[e];
-            else
-                glob[e] = lds[e + row];
+    const int limit = rows * (RF / 4);
+    float4 v[IT];
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int e4 = it * 64 + lane;
+        if (e4 < limit) v[it] = reinterpret_cast<const float4*>(glob)[e4];
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int e4 = it * 64 + lane;
+        if (e4 < limit) {
+            const int e = 4 * e4;
+            float* l = lds + e + e / RF;
+            l[0] = v[it].x;
+            l[1] = v[it].y;
+            l[2] = v[it].z;
+            l[3] = v[it].w;
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
 }
 
-// Coefficient gradients of a wavefront's Gaussians (rows beyond KC zero),
-// through the LDS slice when the rows fit it.
-template <int KC>
-GS3D_DEV void store_sh_grads(const gs3d_project_bwd_args& a, float* stage, bool staged, bool valid, int64_t offset,
-                             int64_t g0, int rows_here, int j, int c, const float* gco) {
+template <int RF>
+GS3D_DEV void lds_to_rows(const float* lds, float* glob, int rows) {
+    static_assert(RF % 4 == 0, "float4 rows");
+    constexpr int IT = RF / 4;
+    const int lane = lane_id();
+    const int limit = rows * (RF / 4);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int e4 = it * 64 + lane;
+        if (e4 < limit) {
+            const int e = 4 * e4;
+            const float* l = lds + e + e / RF;
+            reinterpret_cast<float4*>(glob)[e4] = make_float4(l[0], l[1], l[2], l[3]);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Row access modes of the SH kernels: per-lane scalar or float4 accesses,
+// or rows staged through a wavefront's LDS slice (pitch E + 1).
+enum ShRows : int { kRowsScalar = 0, kRowsFloat4 = 1, kRowsStaged = 2 };
+
+// Colours of every view (primitives/sh.py:58-77 per row, sh_eval's order and
+// rounding), one thread per Gaussian with its 3 * (DEG + 1)^2 coefficients in
+// registers, loaded as float4 when VEC (rows 16-byte aligned, E a multiple
+// of 4).  Runs after
+// the projection kernel, whose radii mark the visible rows.
+template <int DEG, bool VEC>
+__global__ __launch_bounds__(kShRowBlock) void sh_rows_fwd_kernel(gs3d_project_args a) {
+    constexpr int KC = (DEG + 1) * (DEG + 1);
+    const int64_t n = a.n;
+    const int64_t i = (int64_t)blockIdx.x * kShRowBlock + threadIdx.x;
+    const bool valid = i < n;
+    const int views = a.views;
     const int64_t rf = (int64_t)a.sh_rows * 3;
-    if (staged) {
+    float mean[3] = {0.0f, 0.0f, 0.0f};
+    if (DEG > 0 && valid) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
+    }
+    int pre_radius[kShPrefetch];
+#pragma unroll
+    for (int p = 0; p < kShPrefetch; ++p) pre_radius[p] = (valid && p < views) ? a.radii[(int64_t)p * n + i] : 0;
+    float cf[3 * KC];
+    for (int v = 0; v < views; ++v) {
+        if (v == 0 || a.sh_view_stride != 0) {
+            const float* src = a.sh + v * a.sh_view_stride + i * rf;
+            if (!valid) {
+#pragma unroll
+                for (int e = 0; e < 3 * KC; ++e) cf[e] = 0.0f;
+            } else if constexpr (VEC && (3 * KC) % 4 == 0) {
+#pragma unroll
+                for (int e = 0; e < 3 * KC; e += 4) {
+                    const float4 q = reinterpret_cast<const float4*>(src)[e >> 2];
+                    cf[e] = q.x;
+                    cf[e + 1] = q.y;
+                    cf[e + 2] = q.z;
+                    cf[e + 3] = q.w;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 3 * KC; ++e) cf[e] = src[e];
+            }
+        }
+        const int64_t row = (int64_t)v * n + i;
+        int radius = 0;
+#pragma unroll
+        for (int p = 0; p < kShPrefetch; ++p)
+            if (v == p) radius = pre_radius[p];
+        if (v >= kShPrefetch && valid) radius = a.radii[row];
+        float dir[3] = {0.0f, 0.0f, 0.0f};
+        if (DEG > 0) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) dir[k] = mean[k] - a.camera_centers[3 * v + k];
+        }
+        float color[3], raw[3];
+        sh_eval<DEG>(cf, dir, radius > 0, color, raw);
         if (valid) {
 #pragma unroll
-            for (int k = 0; k < KC; ++k) stage[j * (rf + 1) + 3 * k + c] = gco[k];
-            for (int k = KC; k < a.sh_rows; ++k) stage[j * (rf + 1) + 3 * k + c] = 0.0f;
+            for (int c = 0; c < 3; ++c) a.colors[3 * row + c] = color[c];
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        wave_copy<false, 3 * KC>(stage, a.grad_sh + offset + g0 * rf, rows_here);
-    } else if (valid) {
-        float* dst = a.grad_sh + offset + (g0 + j) * rf + c;
-#pragma unroll
-        for (int k = 0; k < KC; ++k) dst[3 * k] = gco[k];
-        for (int k = KC; k < a.sh_rows; ++k) dst[3 * k] = 0.0f;
     }
 }
 
-template <int DEG, bool CAM, bool STAGED>
-__global__ __launch_bounds__(kShBlock) void sh_views_bwd_kernel(gs3d_project_bwd_args a) {
+// f(std::integral_constant<int, K>) for K = 0 .. N-1, unrolled at compile time.
+template <int N, int K = 0, class F>
+GS3D_DEV void static_for(F&& f) {
+    if constexpr (K < N) {
+        f(std::integral_constant<int, K>{});
+        static_for<N, K + 1>(f);
+    }
+}
+
+// Hides a value from the optimiser, so that expressions of it are evaluated
+// again rather than kept live from an earlier use.
+GS3D_DEV float opaque(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+// Adds (or, when !ACC, writes) COUNT gradient values at dst + BASE; float4
+// accesses when VEC and the group is a whole 16-byte-aligned run of 12.
+template <bool VEC, int BASE, int COUNT>
+GS3D_DEV void put_sh_grads(float* dst, bool acc, const float* g) {
+    if constexpr (VEC && COUNT == 12 && BASE % 4 == 0) {
+        float4* d4 = reinterpret_cast<float4*>(dst + BASE);
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+            float4 v = make_float4(g[4 * q], g[4 * q + 1], g[4 * q + 2], g[4 * q + 3]);
+            if (acc) {
+                const float4 o = d4[q];
+                v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+            }
+            d4[q] = v;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < COUNT; ++e) dst[BASE + e] = acc ? dst[BASE + e] + g[e] : g[e];
+    }
+}
+
+// SH VJP of every view (primitives/sh.py:100-136 per row), one thread per
+// Gaussian with its E = 3 * (DEG + 1)^2 coefficients in registers, its rows
+// read and written as MODE says (staged: coalesced copies through the
+// wavefront's LDS slice, which also holds the gradient rows until they are
+// stored).  Views are taken kShPrefetch at a time (one at a
+// time for per-view coefficients): the clamp masks and directions of the
+// group first, then one pass over the coefficient index that forms each
+// coefficient's gradient over the group's views and stores it at once, so
+// no accumulator per coefficient stays live; groups after the first add to
+// the stored rows.  The direction gradients are added to grad_means (after
+// project_bwd_kernel wrote it); with CAM the camera-centre gradients are
+// reduced per wavefront into LDS accumulators.
+template <int DEG, bool CAM, int MODE>
+__global__ __launch_bounds__(kShRowBlock) void sh_rows_bwd_kernel(gs3d_project_bwd_args a) {
     constexpr int KC = (DEG + 1) * (DEG + 1);
-    __shared__ float s_cam[CAM ? kShBlock / 64 : 1][kMaxViewsCamLds][3];
-    __shared__ float s_stage[STAGED ? kShBlock / 64 : 1][STAGED ? kShStageFloats : 1];
+    constexpr int E = 3 * KC;
+    constexpr int U = kShPrefetch;
+    constexpr bool vec = MODE == kRowsFloat4 && E % 4 == 0;
+    constexpr bool staged = MODE == kRowsStaged && E % 4 == 0;
+    constexpr int PITCH = E + 1;  // odd: per-lane row accesses are free of bank conflicts
+    __shared__ float s_cam[CAM ? kShRowBlock / 64 : 1][kMaxViewsCamLds][3];
+    __shared__ float s_stage[staged ? kShRowBlock / 64 : 1][staged ? 64 * PITCH : 1];
     const int lane = lane_id(), wave = threadIdx.x >> 6;
-    const int j = lane / 3, c = lane - 3 * j;
-    float* stage = s_stage[wave];
-    constexpr bool staged = STAGED;  // a.sh_rows == KC: rows staged; else coefficients are read in place
-    const int64_t n = a.n;
-    const int views = a.views;
-    const int64_t rf = (int64_t)a.sh_rows * 3;
     if constexpr (CAM) {
-        for (int e = threadIdx.x; e < (kShBlock / 64) * kMaxViewsCamLds * 3; e += kShBlock)
+        for (int e = threadIdx.x; e < (kShRowBlock / 64) * kMaxViewsCamLds * 3; e += kShRowBlock)
             (&s_cam[0][0][0])[e] = 0.0f;
         __syncthreads();
     }
-    const int64_t wave_stride = (int64_t)gridDim.x * (kShBlock / 64) * kShPerWave;
-    for (int64_t g0 = ((int64_t)blockIdx.x * (kShBlock / 64) + wave) * kShPerWave; g0 < n; g0 += wave_stride) {
-        const int64_t i = g0 + j;
-        const bool valid = lane < 3 * kShPerWave && i < n;
-        const int rows_here = (int)min((int64_t)kShPerWave, n - g0);
-        float mean[3] = {0.0f, 0.0f, 0.0f};
-        if (DEG > 0 && valid) {
+    const int64_t n = a.n;
+    const int views = a.views;
+    const bool per_view = a.sh_view_stride != 0;
+    const int step = per_view ? 1 : U;
+    const int64_t rf = (int64_t)a.sh_rows * 3;
+    const int64_t g0 = (int64_t)blockIdx.x * kShRowBlock + (threadIdx.x & ~63);  // the wavefront's first row
+    const int64_t i = g0 + lane;
+    const bool valid = i < n;
+    const int rows_here = (int)max((int64_t)0, min((int64_t)64, n - g0));
+    float* stage = s_stage[staged ? wave : 0];
+    float* const row_lds = stage + lane * PITCH;
+    float mean[3] = {0.0f, 0.0f, 0.0f}, gm_old[3] = {0.0f, 0.0f, 0.0f}, gm[3] = {0.0f, 0.0f, 0.0f};
+    if (DEG > 0 && valid) {
 #pragma unroll
-            for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
+        for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
+        if (a.grad_means) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) gm_old[k] = a.grad_means[3 * i + k];
         }
-        // Per-view inputs of the first kShPrefetch views and the mean
-        // gradient, loaded together with the coefficients (one latency).
-        int pre_radius[kShPrefetch];
-        float pre_up[kShPrefetch];
+    }
+    float cf[E];
+    for (int v0 = 0; v0 < views; v0 += step) {
+        const int nv = min(step, views - v0);
+        if (v0 == 0 || per_view) {
+            const float* src = a.sh + v0 * a.sh_view_stride + i * rf;
+            if constexpr (staged) {
+                rows_to_lds<E>(stage, a.sh + v0 * a.sh_view_stride + g0 * rf, rows_here);
 #pragma unroll
-        for (int v = 0; v < kShPrefetch; ++v) {
-            const int64_t row = (int64_t)v * n + i;
-            const bool use = valid && v < views;
-            pre_radius[v] = use ? a.radii[row] : 0;
-            pre_up[v] = use ? a.grad_colors[row * a.grad_colors_stride + c] : 0.0f;
-        }
-        float gm_old = 0.0f;
-        if (DEG > 0 && valid && a.grad_means) gm_old = a.grad_means[3 * i + c];
-        float cf[KC], gco[KC];
-        if constexpr (staged) wave_copy<true, 3 * KC>(stage, const_cast<float*>(a.sh) + g0 * rf, rows_here);
+                for (int e = 0; e < E; ++e) cf[e] = valid ? row_lds[e] : 0.0f;
+            } else if (!valid) {
 #pragma unroll
-        for (int k = 0; k < KC; ++k) {
-            cf[k] = valid ? (staged ? stage[j * (rf + 1) + 3 * k + c] : a.sh[i * rf + 3 * k + c]) : 0.0f;
-            gco[k] = 0.0f;
-        }
-        float gm = 0.0f;
-        for (int v = 0; v < views; ++v) {
-            const int64_t row = (int64_t)v * n + i;
-            if (a.sh_view_stride != 0 && v > 0) {
-                const float* src = a.sh + v * a.sh_view_stride;
-                if constexpr (staged) wave_copy<true, 3 * KC>(stage, const_cast<float*>(src) + g0 * rf, rows_here);
+                for (int e = 0; e < E; ++e) cf[e] = 0.0f;
+            } else if constexpr (vec) {
 #pragma unroll
-                for (int k = 0; k < KC; ++k)
-                    cf[k] = valid ? (staged ? stage[j * (rf + 1) + 3 * k + c] : src[i * rf + 3 * k + c]) : 0.0f;
-            }
-            int radius = 0;
-            float up = 0.0f;
-#pragma unroll
-            for (int p = 0; p < kShPrefetch; ++p)
-                if (v == p) {
-                    radius = pre_radius[p];
-                    up = pre_up[p];
+                for (int e = 0; e < E; e += 4) {
+                    const float4 q = reinterpret_cast<const float4*>(src)[e >> 2];
+                    cf[e] = q.x;
+                    cf[e + 1] = q.y;
+                    cf[e + 2] = q.z;
+                    cf[e + 3] = q.w;
                 }
-            if (v >= kShPrefetch && valid) {
-                radius = a.radii[row];
-                up = a.grad_colors[row * a.grad_colors_stride + c];
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) cf[e] = src[e];
             }
-            const bool vis = valid && radius > 0;
-            float unit[3] = {0.0f, 0.0f, 0.0f}, length = 1.0f;
-            if (DEG > 0) {
+        }
+        // The group's directions and clamp-masked colour gradients.
+        float unit[U][3], length[U], cg[U][3];
+        bool vis[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int v = v0 + u;
+            const bool use = valid && u < nv;
+            const int64_t row = (int64_t)v * n + i;
+            const int radius = use ? a.radii[row] : 0;
+            float up[3];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) up[c] = use ? a.grad_colors[row * a.grad_colors_stride + c] : 0.0f;
+            vis[u] = radius > 0;
+            length[u] = 1.0f;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) unit[u][k] = 0.0f;
+            if (DEG > 0 && use) {
                 float dir[3];
 #pragma unroll
                 for (int k = 0; k < 3; ++k) dir[k] = mean[k] - a.camera_centers[3 * v + k];
-                length = length3(dir);
-                const float l = sel_max(length, 1.0e-12f);
+                length[u] = length3(dir);
+                const float l = sel_max(length[u], 1.0e-12f);
 #pragma unroll
-                for (int k = 0; k < 3; ++k) unit[k] = dir[k] / l;
+                for (int k = 0; k < 3; ++k) unit[u][k] = dir[k] / l;
             }
-            // Channel c of the forward colour (sh_eval's order and rounding).
-            float value = 0.0f;
-#pragma unroll
-            for (int k = 0; k < KC; ++k) value = value + sh_basis(unit, k) * cf[k];
-            value = value + 0.5f;
-            const float cg = (vis && value >= 0.0f) ? up : 0.0f;
-            float ugp[3] = {0.0f, 0.0f, 0.0f};
+            // The forward colour before the clamp (sh_eval's order and rounding).
+            float value[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int k = 0; k < KC; ++k) {
-                gco[k] += sh_basis(unit, k) * cg;
+                const float b = sh_basis(unit[u], k);
+#pragma unroll
+                for (int c = 0; c < 3; ++c) value[c] = value[c] + b * cf[3 * k + c];
+            }
+#pragma unroll
+            for (int c = 0; c < 3; ++c) cg[u][c] = (vis[u] && value[c] + 0.5f >= 0.0f) ? up[c] : 0.0f;
+        }
+        // Basis values are evaluated again below, not kept from the loop above.
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int k = 0; k < 3; ++k) unit[u][k] = opaque(unit[u][k]);
+        float ug[U][3];
+#pragma unroll
+        for (int u = 0; u < U; ++u) ug[u][0] = ug[u][1] = ug[u][2] = 0.0f;
+        float* dst = a.grad_sh ? a.grad_sh + (per_view ? v0 * a.sh_view_stride : 0) + i * rf : nullptr;
+        const bool acc = !per_view && v0 > 0;
+        float group[12];
+        static_for<KC>([&](auto kk) {
+#pragma clang fp contract(fast)
+            constexpr int k = decltype(kk)::value;
+            float g[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float b = sh_basis(unit[u], k);
+#pragma unroll
+                for (int c = 0; c < 3; ++c) g[c] += b * cg[u][c];
                 if (DEG > 0) {
                     float bg[3];
-                    sh_basis_grad(unit, k, bg);
-                    const float d = cf[k] * cg;
+                    sh_basis_grad(unit[u], k, bg);
+                    const float d = cf[3 * k] * cg[u][0] + cf[3 * k + 1] * cg[u][1] + cf[3 * k + 2] * cg[u][2];
 #pragma unroll
-                    for (int q = 0; q < 3; ++q) ugp[q] = ugp[q] + d * bg[q];
+                    for (int q = 0; q < 3; ++q) ug[u][q] = ug[u][q] + d * bg[q];
                 }
             }
-            float gd[3] = {0.0f, 0.0f, 0.0f};
-            if (DEG > 0) {
-                float ug[3];
-                const int l0 = 3 * j;
+            if constexpr (staged) {
+                // The stage holds the wavefront's gradient rows until they are stored.
 #pragma unroll
-                for (int q = 0; q < 3; ++q)
-                    ug[q] = __shfl(ugp[q], l0, 64) + __shfl(ugp[q], l0 + 1, 64) + __shfl(ugp[q], l0 + 2, 64);
-                if (vis) {
-                    const float l = sel_max(length, 1.0e-12f);
+                for (int c = 0; c < 3; ++c) row_lds[3 * k + c] = acc ? row_lds[3 * k + c] + g[c] : g[c];
+            } else {
+                constexpr int slot = 3 * (k % 4);
 #pragma unroll
-                    for (int q = 0; q < 3; ++q) gd[q] = ug[q] / l;
-                    if (length >= 1.0e-12f) {
-                        const float f = (unit[0] * ug[0] + unit[1] * ug[1] + unit[2] * ug[2]) / length;
-#pragma unroll
-                        for (int q = 0; q < 3; ++q) gd[q] = gd[q] - unit[q] * f;
-                    }
+                for (int c = 0; c < 3; ++c) group[slot + c] = g[c];
+                if constexpr (k % 4 == 3 || k == KC - 1) {
+                    if (dst && valid) put_sh_grads<vec, 3 * (k - k % 4), slot + 3>(dst, acc, group);
                 }
-                gm += (c == 0) ? gd[0] : (c == 1) ? gd[1] : gd[2];
+            }
+        });
+        if constexpr (staged) {
+            if (a.grad_sh && (per_view || v0 + step >= views))
+                lds_to_rows<E>(stage, a.grad_sh + (per_view ? v0 * a.sh_view_stride : 0) + g0 * rf, rows_here);
+        } else if (dst && valid && !acc) {
+            for (int64_t e = E; e < rf; ++e) dst[e] = 0.0f;
+        }
+        // Direction gradients of the group's views.
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float gd[3] = {0.0f, 0.0f, 0.0f};
+            if (DEG > 0 && vis[u]) {
+#pragma clang fp contract(fast)
+                const float il = 1.0f / sel_max(length[u], 1.0e-12f);
+#pragma unroll
+                for (int q = 0; q < 3; ++q) gd[q] = ug[u][q] * il;
+                if (length[u] >= 1.0e-12f) {
+                    const float f = (unit[u][0] * ug[u][0] + unit[u][1] * ug[u][1] + unit[u][2] * ug[u][2]) / length[u];
+#pragma unroll
+                    for (int q = 0; q < 3; ++q) gd[q] = gd[q] - unit[u][q] * f;
+                }
+#pragma unroll
+                for (int q = 0; q < 3; ++q) gm[q] += gd[q];
             }
             if constexpr (CAM) {
-                if (v < kMaxViewsCamLds) {
+                const int v = v0 + u;
+                if (u < nv && v < kMaxViewsCamLds) {
 #pragma unroll
                     for (int q = 0; q < 3; ++q) {
-                        const float sum = wave_sum_to_lane63(c == 0 ? -gd[q] : 0.0f);
+                        const float sum = wave_sum_to_lane63(-gd[q]);
                         if (lane == 63) s_cam[wave][v][q] += sum;
                     }
                 }
             }
-            if (a.sh_view_stride != 0 && a.grad_sh) {
-                // Per-view coefficients: write this view's gradient block.
-                store_sh_grads<KC>(a, stage, staged, valid, v * a.sh_view_stride, g0, rows_here, j, c, gco);
-#pragma unroll
-                for (int k = 0; k < KC; ++k) gco[k] = 0.0f;
-            }
         }
-        if (DEG > 0 && valid && a.grad_means) a.grad_means[3 * i + c] = gm_old + gm;
-        if (a.sh_view_stride == 0 && a.grad_sh) store_sh_grads<KC>(a, stage, staged, valid, 0, g0, rows_here, j, c, gco);
+    }
+    if (DEG > 0 && valid && a.grad_means) {
+#pragma unroll
+        for (int q = 0; q < 3; ++q) a.grad_means[3 * i + q] = gm_old[q] + gm[q];
     }
     if constexpr (CAM) {
         __syncthreads();
-        for (int e = threadIdx.x; e < views * 3; e += kShBlock) {
+        for (int e = threadIdx.x; e < views * 3; e += kShRowBlock) {
             const int v = e / 3, k = e - v * 3;
             float sum = 0.0f;
 #pragma unroll
-            for (int w = 0; w < kShBlock / 64; ++w) sum += s_cam[w][v][k];
+            for (int w = 0; w < kShRowBlock / 64; ++w) sum += s_cam[w][v][k];
             atomicAdd(a.grad_camera_centers + 3 * v + k, sum);
         }
     }
@@ -993,13 +1038,36 @@ __global__ void metadata_kernel(const int32_t* __restrict__ radii, const float* 
     meta_conics[3 * i + 2] = k.z;
 }
 
+// Row access of the SH kernels: float4 when rows start 16-byte aligned and
+// the needed coefficients are whole float4s, scalar otherwise; with
+// `allow_staged`, rows of exactly the needed coefficients are staged through
+// LDS (coalesced copies).
+inline int sh_row_mode(int deg, int sh_rows, const float* sh, int64_t view_stride, const float* grad_sh,
+                       bool allow_staged) {
+    const int e = 3 * (deg + 1) * (deg + 1);
+    const bool aligned = (reinterpret_cast<uintptr_t>(sh) & 15) == 0 && (reinterpret_cast<uintptr_t>(grad_sh) & 15) == 0 &&
+                         (view_stride & 3) == 0 && (sh_rows * 3) % 4 == 0 && e % 4 == 0;
+    if (!aligned) return kRowsScalar;
+    return allow_staged && sh_rows * 3 == e ? kRowsStaged : kRowsFloat4;
+}
+
+// Projection of every view, then (DEG >= 0) the colours in a second launch
+// with one thread per Gaussian: the projection kernel then keeps its
+// occupancy, and the SH basis is evaluated once per (Gaussian, view).
 template <int DEG>
 int launch_project_fwd(const gs3d_project_args& a, hipStream_t stream) {
     const dim3 grid(blocks_for(a.n, kProjBlock));
     if (a.means2d)
-        hipLaunchKernelGGL((project_fwd_kernel<DEG, true>), grid, dim3(kProjBlock), 0, stream, a);
+        hipLaunchKernelGGL((project_fwd_kernel<true>), grid, dim3(kProjBlock), 0, stream, a);
     else
-        hipLaunchKernelGGL((project_fwd_kernel<DEG, false>), grid, dim3(kProjBlock), 0, stream, a);
+        hipLaunchKernelGGL((project_fwd_kernel<false>), grid, dim3(kProjBlock), 0, stream, a);
+    if constexpr (DEG >= 0) {
+        const dim3 rgrid(blocks_for(a.n, kShRowBlock));
+        if (sh_row_mode(DEG, a.sh_rows, a.sh, a.sh_view_stride, nullptr, false) == kRowsFloat4)
+            hipLaunchKernelGGL((sh_rows_fwd_kernel<DEG, true>), rgrid, dim3(kShRowBlock), 0, stream, a);
+        else
+            hipLaunchKernelGGL((sh_rows_fwd_kernel<DEG, false>), rgrid, dim3(kShRowBlock), 0, stream, a);
+    }
     return launch_status("gs3d_project_fwd");
 }
 
@@ -1025,22 +1093,23 @@ int launch_project_bwd(const gs3d_project_bwd_args& a, hipStream_t stream) {
     else
         hipLaunchKernelGGL((project_bwd_kernel<false>), grid, dim3(kProjBlock), 0, stream, a);
     if constexpr (DEG >= 0) {
-        const int64_t waves = (a.n + kShPerWave - 1) / kShPerWave;
-        const int64_t needed = (waves + kShBlock / 64 - 1) / (kShBlock / 64);
-        const int64_t cap = (int64_t)grid.x * 2;  // persistent: 16 blocks of 4 wavefronts per CU
-        const dim3 sh_grid((unsigned)(needed < cap ? needed : cap));
-        const bool staged = a.sh_rows == (DEG + 1) * (DEG + 1);  // rows of exactly the needed coefficients
-        if (DEG > 0 && a.grad_camera_centers) {
-            if (staged)
-                hipLaunchKernelGGL((sh_views_bwd_kernel<DEG, true, true>), sh_grid, dim3(kShBlock), 0, stream, a);
-            else
-                hipLaunchKernelGGL((sh_views_bwd_kernel<DEG, true, false>), sh_grid, dim3(kShBlock), 0, stream, a);
-        } else {
-            if (staged)
-                hipLaunchKernelGGL((sh_views_bwd_kernel<DEG, false, true>), sh_grid, dim3(kShBlock), 0, stream, a);
-            else
-                hipLaunchKernelGGL((sh_views_bwd_kernel<DEG, false, false>), sh_grid, dim3(kShBlock), 0, stream, a);
-        }
+        const int mode = sh_row_mode(DEG, a.sh_rows, a.sh, a.sh_view_stride, a.grad_sh, true);
+        const dim3 rgrid(blocks_for(a.n, kShRowBlock));
+        const bool cam = DEG > 0 && a.grad_camera_centers;
+#define GS3D_SH_BWD_LAUNCH(M)                                                                              \
+    do {                                                                                                   \
+        if (cam)                                                                                           \
+            hipLaunchKernelGGL((sh_rows_bwd_kernel<DEG, true, M>), rgrid, dim3(kShRowBlock), 0, stream, a);  \
+        else                                                                                               \
+            hipLaunchKernelGGL((sh_rows_bwd_kernel<DEG, false, M>), rgrid, dim3(kShRowBlock), 0, stream, a); \
+    } while (0)
+        if (mode == kRowsStaged)
+            GS3D_SH_BWD_LAUNCH(kRowsStaged);
+        else if (mode == kRowsFloat4)
+            GS3D_SH_BWD_LAUNCH(kRowsFloat4);
+        else
+            GS3D_SH_BWD_LAUNCH(kRowsScalar);
+#undef GS3D_SH_BWD_LAUNCH
     }
     return launch_status("gs3d_project_bwd");
 }

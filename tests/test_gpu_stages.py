@@ -281,6 +281,49 @@ def test_projection_backward_parity(key, degree):
                 atol=1e-4 * max(1.0, np.abs(ref["camera_centers"]).max()))
 
 
+@pytest.mark.parametrize("degree", [1, 3])
+def test_projection_sh_shared_many_views(degree):
+    # Shared coefficients seen by 7 cameras: more views than the SH kernels
+    # take in one group, so the colour pass loads later radii in the loop
+    # and the coefficient gradients of later groups are added to the stored
+    # rows; camera-centre gradients on.
+    scene = _scene("sh3_4view")
+    _say(f"projection shared SH, 7 views, degree={degree}")
+    order = [0, 1, 2, 3, 1, 3, 0]
+    viewmats = scene.viewmats[order].contiguous()
+    viewmats[4:, :3, 3] += torch.tensor([0.3, -0.2, 0.1], device=DEV)
+    Ks = scene.Ks[order].contiguous()
+    views, n = viewmats.shape[0], scene.means.shape[0]
+    quats = torch.nn.functional.normalize(scene.quats, dim=-1)
+    full, inverse, centers, errors = cameras.launch_prepare(viewmats, Ks, scene.width, scene.height, True)
+    st = gproj.project_views(scene.means, quats, scene.scales, scene.opacities, viewmats, full, Ks,
+                             scene.width, scene.height, 0.2, float("inf"), 0.0, sh=scene.sh_coeffs,
+                             sh_degree=degree, camera_centers=centers, metadata=True)
+    ref_f = oracle.project_fwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+                               _np(viewmats), _np(full), _np(Ks), scene.width, scene.height,
+                               sh=_np(scene.sh_coeffs), sh_degree=degree, camera_centers=_np(centers), metadata=True)
+    assert (st.radii > 0).sum() > 0
+    np.testing.assert_array_equal(_np(st.colors), ref_f["colors"])
+    g = torch.Generator().manual_seed(13)
+    gc = torch.randn((views, n, 2), generator=g).to(DEV)
+    gk = torch.randn((views, n, 4), generator=g).to(DEV) * 0.1
+    gcol = torch.randn((views, n, 3), generator=g).to(DEV)
+    res = gproj.backward_views(scene.means, quats, scene.scales, scene.opacities, viewmats, full, Ks,
+                               scene.width, scene.height, st.radii, gc, gk, (True,) * 6, sh=scene.sh_coeffs,
+                               sh_degree=degree, camera_centers=centers, grad_colors=gcol, need_sh=True,
+                               need_centers=True)
+    ref = oracle.project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+                             _np(viewmats), _np(full), _np(Ks), scene.width, scene.height, _np(st.radii),
+                             _np(gc), _np(gk), sh=_np(scene.sh_coeffs), sh_degree=degree,
+                             camera_centers=_np(centers), grad_colors=_np(gcol))
+    got_sh = _np(res["sh"])
+    assert np.all(got_sh[..., (degree + 1) ** 2:, :] == 0.0)
+    compare("sh", got_sh, ref["sh"], rtol=1e-4, atol=1e-6)
+    compare("means", _np(res["means"]), ref["means"], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(ref["means"]).max()))
+    compare("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], rtol=1e-3,
+            atol=1e-4 * max(1.0, np.abs(ref["camera_centers"]).max()))
+
+
 @pytest.mark.parametrize("degree", [2, 3])
 def test_projection_per_view_sh_parity(degree):
     # Per-view coefficients (C,N,16,3) and, for degree 2, coefficient rows
