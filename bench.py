@@ -181,21 +181,29 @@ def stage_timings(scene, reps):
                      "render_bwd": (9, 10), "project_bwd": (10, 11)}
             for k, (a, b) in spans.items():
                 acc[k] += ev[a].elapsed_time(ev[b]) / reps
-        # The roofline kernel alone: back-to-back launches keep the queue
-        # full, so the HIP-event time per launch is the kernel's duration.
+        # The roofline kernel alone, one launch at a time with HIP events
+        # around it, after a 512 MiB read that evicts the L2 and the Infinity
+        # Cache with clean lines: its inputs then come from HBM, as they do
+        # inside a step (back-to-back launches would find the 132 MB of
+        # parameters cached; a fill would leave 512 MiB of dirty lines for the
+        # kernel to write back).
         launches = 10
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        flush = torch.ones(128 << 20, dtype=torch.float32, device=quats.device)
         # (without coefficients: the projection kernel only, no colour launch)
         project = lambda: gproj.project_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full,
                                               scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0,
                                               metadata=True, normalize_quats=True)
         project()
-        e0.record()
+        acc["project_kernel"] = 0.0
         for _ in range(launches):
+            flush.amax()
+            e0.record()
             project()
-        e1.record()
-        torch.cuda.synchronize()
-        acc["project_kernel"] = e0.elapsed_time(e1) / launches
+            e1.record()
+            torch.cuda.synchronize()
+            acc["project_kernel"] += e0.elapsed_time(e1) / launches
+        del flush
         # Contribution statistics (a masked count and a weighted sum over
         # per-view pixel maps) observed by the forward blend, against the
         # plain forward blend, both back-to-back.

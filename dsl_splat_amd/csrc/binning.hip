@@ -408,7 +408,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
         if (p < valid_count) {
             const K kk = s_keys[p];
             const int64_t dst = (int64_t)s_gbase[digit_of(kk, shift, mask)] + p;
-            keys_out[dst] = kk;
+            keys_out[dst] = kk;  // plain stores: digit runs start mid-line and the L2 merges them
             if (vals_out) vals_out[dst] = s_vals[p];
         }
     }
@@ -794,7 +794,7 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
         const int ly0 = max(s_y0[lo] - (Y << kGroupShift), 0), ly1 = min(s_y1[lo] - 1 - (Y << kGroupShift), 7);
         const uint32_t gid = s_gbase[lo] + (uint32_t)(Y * d.sgx + X);
         const uint32_t clip = (uint32_t)(lx0 | (lx1 << 3) | (ly0 << 6) | (ly1 << 9));
-        items[p] = ((uint64_t)s_id[lo] << 32) | ((uint64_t)clip << kGroupBits) | gid;
+        st_stream(items + p, ((uint64_t)s_id[lo] << 32) | ((uint64_t)clip << kGroupBits) | gid);
     }
 }
 
@@ -850,8 +850,8 @@ __global__ __launch_bounds__(kBinThreads) void accutile_emit_kernel(const uint64
             }
             const int GX = is_y ? gc : G, GY = is_y ? G : gc;
             if (p < stop) {
-                items[p] = (id << 32) | (uint64_t)(gbase + (uint32_t)(GY * d.sgx + GX));
-                masks[p] = m;
+                st_stream(items + p, (id << 32) | (uint64_t)(gbase + (uint32_t)(GY * d.sgx + GX)));
+                st_stream(masks + p, m);
             }
             ++p;
         }
@@ -989,7 +989,7 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
                         const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
                             (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
                         const int64_t pos = (int64_t)run + rank;
-                        if (pos < id_limit) ids[pos] = id[k];
+                        if (pos < id_limit) ids[pos] = id[k];  // plain: short runs per tile, merged in L2
                     }
                 }
                 run += (uint32_t)__popcll(b);

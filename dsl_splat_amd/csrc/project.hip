@@ -323,8 +323,10 @@ GS3D_DEV void sh_backward(const float* coef, const float* dir, bool visible, con
 // Forward projection of every view, one thread per Gaussian (the colours are
 // evaluated by sh_rows_fwd_kernel in a second launch).
 // ---------------------------------------------------------------------------
+// At most 64 VGPRs (8 wavefronts per SIMD): this kernel is bound by its
+// output stream, and more wavefronts in flight keep more stores queued.
 template <bool META>
-__global__ __launch_bounds__(kProjBlock) void project_fwd_kernel(gs3d_project_args a) {
+__global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(8))) void project_fwd_kernel(gs3d_project_args a) {
     const int n = a.n;
     const int64_t i = (int64_t)blockIdx.x * kProjBlock + threadIdx.x;
     if (i >= n) return;
@@ -349,17 +351,17 @@ __global__ __launch_bounds__(kProjBlock) void project_fwd_kernel(gs3d_project_ar
                                      a.radius_clip, f);
         const int64_t row = (int64_t)v * n + i;
         if (!vis) f = Footprint{{0.0f, 0.0f}, {0.0f, 0.0f, 0.0f}, 0, 0, 0.0f};
-        reinterpret_cast<float2*>(a.centers)[row] = make_float2(f.center[0], f.center[1]);
-        reinterpret_cast<float4*>(a.conics)[row] =
-            make_float4(f.conic[0], f.conic[1], f.conic[2], vis ? opac : 0.0f);
-        a.radii[row] = f.radius;
-        a.tiles[row] = f.tiles;
-        a.depths[row] = f.depth;
+        st_stream(reinterpret_cast<float2*>(a.centers) + row, make_float2(f.center[0], f.center[1]));
+        st_stream(reinterpret_cast<float4*>(a.conics) + row,
+                make_float4(f.conic[0], f.conic[1], f.conic[2], vis ? opac : 0.0f));
+        st_stream(a.radii + row, f.radius);
+        st_stream(a.tiles + row, f.tiles);
+        st_stream(a.depths + row, f.depth);
         if constexpr (META) {
-            reinterpret_cast<float2*>(a.means2d)[row] = make_float2(f.center[0], f.center[1]);
-            a.meta_opacities[row] = vis ? opac : 0.0f;
+            st_stream(reinterpret_cast<float2*>(a.means2d) + row, make_float2(f.center[0], f.center[1]));
+            st_stream(a.meta_opacities + row, vis ? opac : 0.0f);
 #pragma unroll
-            for (int k = 0; k < 3; ++k) a.meta_conics[3 * row + k] = f.conic[k];
+            for (int k = 0; k < 3; ++k) st_stream(a.meta_conics + 3 * row + k, f.conic[k]);
         }
     }
 }
@@ -571,7 +573,7 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
                 for (int k = 0; k < 3; ++k) gs[k] += g.scale[k];
                 go += g.opacity;
             }
-            if (a.screen_grad && valid) reinterpret_cast<float2*>(a.screen_grad)[row] = screen;
+            if (a.screen_grad && valid) st_stream(reinterpret_cast<float2*>(a.screen_grad) + row, screen);
             if constexpr (CAM) {
                 if (v < kMaxViewsCamLds) {
 #pragma unroll
@@ -591,15 +593,15 @@ __global__ __launch_bounds__(kProjBlock) void project_bwd_kernel(gs3d_project_bw
         if (valid) {
             if (a.grad_means)
 #pragma unroll
-                for (int k = 0; k < 3; ++k) a.grad_means[3 * i + k] = gm[k];
+                for (int k = 0; k < 3; ++k) a.grad_means[3 * i + k] = gm[k];  // read again by the SH VJP
             if (a.grad_quats) {
                 if (a.normalize_quats) normalize_quat_vjp(q, qnorm, gq);
-                reinterpret_cast<float4*>(a.grad_quats)[i] = make_float4(gq[0], gq[1], gq[2], gq[3]);
+                st_stream(reinterpret_cast<float4*>(a.grad_quats) + i, make_float4(gq[0], gq[1], gq[2], gq[3]));
             }
             if (a.grad_scales)
 #pragma unroll
-                for (int k = 0; k < 3; ++k) a.grad_scales[3 * i + k] = gs[k];
-            if (a.grad_opacities) a.grad_opacities[i] = go;
+                for (int k = 0; k < 3; ++k) st_stream(a.grad_scales + 3 * i + k, gs[k]);
+            if (a.grad_opacities) st_stream(a.grad_opacities + i, go);
         }
     }
     if constexpr (CAM) {
@@ -671,7 +673,7 @@ GS3D_DEV void lds_to_rows(const float* lds, float* glob, int rows) {
         if (e4 < limit) {
             const int e = 4 * e4;
             const float* l = lds + e + e / RF;
-            reinterpret_cast<float4*>(glob)[e4] = make_float4(l[0], l[1], l[2], l[3]);
+            st_stream(reinterpret_cast<float4*>(glob) + e4, make_float4(l[0], l[1], l[2], l[3]));
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -739,7 +741,7 @@ __global__ __launch_bounds__(kShRowBlock) void sh_rows_fwd_kernel(gs3d_project_a
         sh_eval<DEG>(cf, dir, radius > 0, color, raw);
         if (valid) {
 #pragma unroll
-            for (int c = 0; c < 3; ++c) a.colors[3 * row + c] = color[c];
+            for (int c = 0; c < 3; ++c) st_stream(a.colors + 3 * row + c, color[c]);
         }
     }
 }
