@@ -182,14 +182,15 @@ def stage_timings(scene, reps):
             for k, (a, b) in spans.items():
                 acc[k] += ev[a].elapsed_time(ev[b]) / reps
         # The roofline kernel alone, one launch at a time with HIP events
-        # around it, after a 512 MiB read that evicts the L2 and the Infinity
+        # around it, after a 2 GiB read that evicts the L2 and the Infinity
         # Cache with clean lines: its inputs then come from HBM, as they do
         # inside a step (back-to-back launches would find the 132 MB of
-        # parameters cached; a fill would leave 512 MiB of dirty lines for the
-        # kernel to write back).
+        # parameters cached; a fill would leave dirty lines for the kernel to
+        # write back).  The read (~0.3 ms) outlasts the host's enqueueing of
+        # the launch, so no idle time falls between the events.
         launches = 10
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        flush = torch.ones(128 << 20, dtype=torch.float32, device=quats.device)
+        flush = torch.ones(512 << 20, dtype=torch.float32, device=quats.device)
         # (without coefficients: the projection kernel only, no colour launch)
         project = lambda: gproj.project_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full,
                                               scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0,
@@ -317,23 +318,25 @@ def main():
     for _ in range(args.warmup):
         backward(forward())
     torch.cuda.synchronize()
-    fwd_ms = bwd_ms = 0.0
     log(f"[bench] timing {args.steps} steps")
+    # Steps follow each other as in a training loop: no synchronisation
+    # between them (each forward synchronises once, on its pair totals), so
+    # the host prepares step i+1 while step i's backward runs.  Per-step
+    # forward/backward spans come from events read after the final sync.
+    events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    for e0, e1, e2 in events:
         e0.record()
         loss = forward()
         e1.record()
         backward(loss)
         e2.record()
-        e2.synchronize()
-        fwd_ms += e0.elapsed_time(e1)
-        bwd_ms += e1.elapsed_time(e2)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1000.0 / args.steps
+    fwd_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in events)
+    bwd_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in events)
     modes = {args.tile_mode: dict(ms=round(ms, 3), pairs=int(forward.meta["tiles_per_gauss"].sum()))}
     for mode in ("radius", "snugbox", "accutile"):
         if mode == args.tile_mode or args.mode_steps <= 0:

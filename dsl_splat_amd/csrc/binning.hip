@@ -8,6 +8,7 @@
 // matrix cores.
 #include <climits>
 
+#include <type_traits>
 #include "common.hpp"
 #include "footprint.hpp"
 
@@ -523,7 +524,7 @@ __global__ void tile_ranges_kernel(const K* __restrict__ keys, int64_t count, in
 constexpr int kGroupShift = 3;  // groups of 8x8 tiles: one wavefront lane per tile
 constexpr int kGroupBits = 20;  // group id field (low bits) of an item
 constexpr uint32_t kGroupMask = (1u << kGroupBits) - 1u;
-constexpr int kChunkSteps = 8;  // items per lane of a chunk
+constexpr int kChunkSteps = 8;  // items per lane of a chunk (4 and 16 measured slower)
 constexpr int kChunk = 64 * kChunkSteps;  // items ranked by one wavefront
 constexpr int kBinThreads = 256;
 constexpr int kBinWaves = kBinThreads / 64;
@@ -929,17 +930,26 @@ GS3D_DEV int64_t xcd_contiguous(int64_t b, int64_t nblocks) {
 // WRITE = false: counts[(g, t, s)] = items of chunk s touching tile t.
 // WRITE = true: every item's Gaussian index goes to
 //   tile_start[t] + (scanned[(g,t,s)] - scanned[(g,t,0)]) + rank.
-template <bool WRITE, bool MASKS>
+// BUF (WRITE, id lists under 4 GiB): a tile's run of the chunk is gathered
+// in the wavefront's LDS slice (one ballot-ranked write per 64 items) and
+// then stored with consecutive lanes (about one full-width store per tile
+// instead of one partial store per 64 items); buffer stores take the run's
+// start as the scalar offset, and the buffer's range check stands in for the
+// id_limit test.  Tiles are walked in two halves so that each membership
+// test reads one 32-bit word of the item's mask.
+template <bool WRITE, bool MASKS, bool BUF = false>
 __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     const uint64_t* __restrict__ items, const uint64_t* __restrict__ masks, const int32_t* __restrict__ granges,
     const int32_t* __restrict__ chunk_base,
     const int32_t* __restrict__ chunk_group, int groups, int64_t max_chunks, GridDims d,
     uint32_t* __restrict__ counts, const int32_t* __restrict__ scanned, const int32_t* __restrict__ tile_start,
     int32_t* __restrict__ ids, int64_t id_limit) {
+    __shared__ int32_t s_run[WRITE && BUF ? kBinWaves : 1][WRITE && BUF ? kChunk : 1];
     const int lane = lane_id();
     const int64_t block = xcd_contiguous(blockIdx.x, gridDim.x);
     const int64_t u = block * kBinWaves + (threadIdx.x >> 6);
     if (u >= max_chunks || u >= chunk_base[groups]) return;
+    int32_t* const run_lds = s_run[WRITE && BUF ? threadIdx.x >> 6 : 0];
     const int g = chunk_group[u];
     const int32_t cb = chunk_base[g];
     const int32_t q = chunk_base[g + 1] - cb;
@@ -974,29 +984,55 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
             init = (uint32_t)(tile_start[(int64_t)view * d.tpv + ty * d.gx + tx] + (scanned[slot + s] - scanned[slot]));
     }
     uint32_t mine = 0;
-    uint64_t todo = wave_or64(any);
-    while (todo) {
-        const int t = __builtin_ctzll(todo);
-        todo &= todo - 1;
-        uint32_t run = WRITE ? (uint32_t)__builtin_amdgcn_readlane((int)init, t) : 0u;
+    const uint64_t todo_all = wave_or64(any);
+    // (unused unless WRITE && BUF)
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(ids, (short)0, (int)(uint32_t)(BUF ? id_limit * 4 : 0), 0x00020000);
+    auto walk = [&](auto half) {
+        constexpr int H = decltype(half)::value;
+        uint32_t todo = (uint32_t)(todo_all >> (32 * H));
+        while (todo) {
+            const int tb = __builtin_ctz(todo);
+            todo &= todo - 1;
+            const int t = 32 * H + tb;
+            const uint32_t bit = 1u << tb;
+            const uint32_t start = WRITE ? (uint32_t)__builtin_amdgcn_readlane((int)init, t) : 0u;
+            uint32_t run = WRITE && BUF ? 0u : start;
 #pragma unroll
-        for (int k = 0; k < kChunkSteps; ++k) {
-            const bool has = ((mask[k] >> t) & 1ull) != 0ull;
-            const uint64_t b = __ballot(has);
-            if (b) {
-                if constexpr (WRITE) {
-                    if (has) {
-                        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
-                            (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-                        const int64_t pos = (int64_t)run + rank;
-                        if (pos < id_limit) ids[pos] = id[k];  // plain: short runs per tile, merged in L2
+            for (int k = 0; k < kChunkSteps; ++k) {
+                const uint32_t word = H ? (uint32_t)(mask[k] >> 32) : (uint32_t)mask[k];
+                const bool has = (word & bit) != 0u;
+                const uint64_t b = __ballot(has);
+                if (b) {
+                    if constexpr (WRITE) {
+                        if (has) {
+                            const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
+                                (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+                            if constexpr (BUF) {
+                                run_lds[run + rank] = id[k];
+                            } else {
+                                const int64_t pos = (int64_t)run + rank;
+                                if (pos < id_limit) ids[pos] = id[k];  // plain: short runs per tile, merged in L2
+                            }
+                        }
                     }
+                    run += (uint32_t)__popcll(b);
                 }
-                run += (uint32_t)__popcll(b);
             }
+            if constexpr (WRITE && BUF) {
+                // The run is complete in LDS: store it with consecutive lanes.
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                for (uint32_t e = (uint32_t)lane; e < run; e += 64)
+                    __builtin_amdgcn_raw_buffer_store_b32(run_lds[e], rsrc, (int)(e * 4u), (int)(start * 4u), 0);
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+            }
+            if (lane == t) mine = run;
         }
-        if (lane == t) mine = run;
-    }
+    };
+    walk(std::integral_constant<int, 0>{});
+    walk(std::integral_constant<int, 1>{});
     if constexpr (!WRITE) counts[slot + s] = mine;
 }
 
@@ -1382,14 +1418,24 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL(gs3d::tile_ranges_from_totals_kernel, dim3(gs3d::blocks_for(tiles, 256)), dim3(256), 0, s,
                        sc.totals, sc.starts, tiles, a.ranges);
-    if (accu)
-        hipLaunchKernelGGL((gs3d::group_pass_kernel<true, true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
-                           sc.masks, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts,
-                           sc.scanned, sc.starts, a.ids, a.tile_pairs);
-    else
-        hipLaunchKernelGGL((gs3d::group_pass_kernel<true, false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
-                           (const uint64_t*)nullptr, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d,
-                           sc.counts, sc.scanned, sc.starts, a.ids, a.tile_pairs);
+    // Buffer stores address the id list with 32-bit byte offsets.
+    const bool buf = a.tile_pairs <= (int64_t)(0xFFFFFFFFu / 4);
+#define GS3D_WRITE_PASS(M, B)                                                                                      \
+    hipLaunchKernelGGL((gs3d::group_pass_kernel<true, M, B>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items, \
+                       M ? (const uint64_t*)sc.masks : nullptr, sc.granges, sc.chunk_base, sc.chunk_group,        \
+                       (int)groups, chunks, d, sc.counts, sc.scanned, sc.starts, a.ids, a.tile_pairs)
+    if (accu) {
+        if (buf)
+            GS3D_WRITE_PASS(true, true);
+        else
+            GS3D_WRITE_PASS(true, false);
+    } else {
+        if (buf)
+            GS3D_WRITE_PASS(false, true);
+        else
+            GS3D_WRITE_PASS(false, false);
+    }
+#undef GS3D_WRITE_PASS
     return gs3d::launch_status("gs3d_bin_rows");
 }
 
