@@ -113,9 +113,24 @@ struct TileWaves {
     static constexpr int rows = kTile / count;
 };
 
+// Minimum over dx in [lo, hi] of Q = a dx^2 + 2 b dx dy + c dy^2 at a fixed
+// dy (a > 0): Q at the clamped stationary point -b dy / a.  The reciprocal
+// is approximate; moving the point by a relative 1e-7 changes Q by a second
+// order amount, far inside the culling margin.
+GS3D_DEV float edge_min(float a, float inv_a, float b, float c, float dy, float lo, float hi) {
+    const float d = sel_clamp(-b * dy * inv_a, lo, hi);
+    return (a * d + 2.0f * b * dy) * d + c * dy * dy;
+}
+
 // Bit w is set unless every pixel of wavefront w's strip is certain to reject
-// the Gaussian: the bounding box of the ellipse {power >= cut} (its quadratic
-// form widened by 1% + 0.01, the box by 0.01 px) misses the strip.  Culling
+// the Gaussian: the ellipse {power >= cut}, its quadratic form Q widened by
+// 1% + 0.01, misses the strip's rectangle of pixel centres -- first by its
+// bounding box (widened by 0.01 px), then exactly: the strip is kept when
+// the centre lies inside the rectangle or Q's minimum over one of the
+// rectangle's four edges is within the widened bound.  Float32 evaluation of
+// Q is off by at most about 8 * 2^-24 * (a + c) |d|^2, below 2e-4 Q for the
+// conics culled here, and the blend's power evaluation by as little, both far
+// inside the 1% margin.  Culling
 // is attempted only where a*c <= 100*det (correlation below 0.995): there the
 // float32 determinant is within 1.3e-5 relative of the exact one (its
 // cancellation error is at most 2^-24 * 2ac <= 200 * 2^-24 * det), so the box
@@ -137,11 +152,25 @@ GS3D_DEV uint32_t strip_mask(float2 xy, float4 con, float cut, int x0, int y0) {
     const float hx = __builtin_sqrtf(s * c) + 0.01f;
     const float hy = __builtin_sqrtf(s * a) + 0.01f;
     if (xy.x + hx < (float)x0 || xy.x - hx > (float)(x0 + kTile - 1)) return 0u;
+    const float bound = q * 1.01f + 0.01f;
+    const float inv_a = __builtin_amdgcn_rcpf(a), inv_c = __builtin_amdgcn_rcpf(c);
+    // Centre minus pixel over the tile's columns.
+    const float dx_lo = xy.x - (float)(x0 + kTile - 1), dx_hi = xy.x - (float)x0;
     uint32_t m = 0u;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
         const float lo = (float)(y0 + w * ROWS), hi = (float)(y0 + w * ROWS + ROWS - 1);
-        if (!(xy.y + hy < lo || xy.y - hy > hi)) m |= 1u << w;
+        if (xy.y + hy < lo || xy.y - hy > hi) continue;
+        const float dy_lo = xy.y - hi, dy_hi = xy.y - lo;
+        bool keep = dx_lo <= 0.0f && dx_hi >= 0.0f && dy_lo <= 0.0f && dy_hi >= 0.0f;  // centre inside
+        if (!keep) {
+            const float e0 = edge_min(a, inv_a, b, c, dy_lo, dx_lo, dx_hi);
+            const float e1 = edge_min(a, inv_a, b, c, dy_hi, dx_lo, dx_hi);
+            const float e2 = edge_min(c, inv_c, b, a, dx_lo, dy_lo, dy_hi);
+            const float e3 = edge_min(c, inv_c, b, a, dx_hi, dy_lo, dy_hi);
+            keep = !(sel_min(sel_min(e0, e1), sel_min(e2, e3)) > bound);
+        }
+        if (keep) m |= 1u << w;
     }
     return m;
 }
