@@ -9,8 +9,9 @@ features (C,H,W,D), extra (C,H,W,E) and alpha (C,H,W,1), each contiguous, and
 the backward reads the upstream gradient of each plane where it lies (any
 pixel stride), so autograd never reassembles a full-image gradient.
 Backward gradients of centres/conics/abs-centres share one
-(C, N, 8) record per Gaussian (centre xy, conic a b c, opacity, |centre| xy)
-so a wavefront's atomics for one Gaussian land in one 32-byte row.
+(C, N, 6) record per Gaussian (centre xy, conic a b c, opacity; |centre| xy
+in two more columns with absgrad), so a wavefront's atomics for one Gaussian
+land in one 24-byte (32-byte) row.
 """
 
 from dataclasses import dataclass
@@ -21,7 +22,10 @@ from torch import Tensor
 
 from ..runtime import abi, native
 
-RECORD = 8  # floats per Gaussian in the gradient record
+# Floats per Gaussian in the gradient record: [dcx, dcy, da, db, dc, dopacity]
+# and, with absgrad, [|dcx|, |dcy|].
+RECORD = 6
+RECORD_ABS = 8
 
 
 @dataclass(slots=True)
@@ -148,8 +152,8 @@ def backward_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor,
                    absgrad: bool = False, need_features: bool = True, need_extra: bool = True):
     """``upstream`` is either the (grad features, grad extra, grad alpha)
     planes (each may be None) or one (C,H,W,D') tensor of all channels.
-    Returns (record (C,N,8), grad_features like features or None,
-    grad_extra like extra or None)."""
+    Returns (record (C,N,6), or (C,N,8) with absgrad, grad_features like
+    features or None, grad_extra like extra or None)."""
     views, n = centers.shape[0], centers.shape[1]
     device = centers.device
     keep = []
@@ -170,11 +174,12 @@ def backward_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor,
     b.upstream, b.upstream_stride = native.ptr(gf_plane), gf_stride
     b.upstream_extra, b.upstream_extra_stride = native.ptr(ge_plane), ge_stride
     b.upstream_alpha, b.upstream_alpha_stride = native.ptr(ga_plane), ga_stride
-    record = torch.zeros((views, n, RECORD), dtype=torch.float32, device=device)
-    b.grad_centers, b.grad_centers_stride = native.ptr(record), RECORD
-    b.grad_conics, b.grad_conics_stride = native.ptr(record, 2), RECORD
+    width = RECORD_ABS if absgrad else RECORD
+    record = torch.zeros((views, n, width), dtype=torch.float32, device=device)
+    b.grad_centers, b.grad_centers_stride = native.ptr(record), width
+    b.grad_conics, b.grad_conics_stride = native.ptr(record, 2), width
     if absgrad:
-        b.abs_centers, b.abs_stride = native.ptr(record, 6), RECORD
+        b.abs_centers, b.abs_stride = native.ptr(record, 6), width
     grad_features = grad_extra = None
     if need_features and features is not None:
         grad_features = torch.zeros(features.shape, dtype=torch.float32, device=device)
