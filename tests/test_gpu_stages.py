@@ -390,6 +390,7 @@ def test_grouped_binning_matches_reference_order(key, degree):
     (2, 3000, 200, 120, 1.0),      # partial groups at the right/bottom edges, several chunks per group
     (1, 40000, 128, 128, 0.15),    # crowded corner: long group lists, many 512-item chunks
     (70, 400, 160, 160, 1.0),      # 280 groups: the group sort takes two radix passes
+    (130, 250, 400, 400, 1.0),     # 2080 groups: 12-bit group keys
     (1, 2000, 4200, 64, 1.0),      # 263 tiles across: rectangles recomputed instead of packed in the records
 ])
 def test_grouped_binning_ties_and_large_rects(views, n, W, H, spread):
@@ -428,7 +429,8 @@ def test_grouped_binning_ties_and_large_rects(views, n, W, H, spread):
     np.testing.assert_array_equal(_np(bins["ranges"]), oracle.tile_ranges(sk, T))
 
 
-@pytest.mark.parametrize("count,end_bit", [(2, 13), (4097, 15), (1_000_003, 16), (5_000_000, 32)])
+@pytest.mark.parametrize("count,end_bit", [(2, 13), (4097, 15), (1_000_003, 16), (5_000_000, 32), (3, 11),
+                                           (4097, 9), (1_000_003, 10), (70_001, 11), (2048, 11)])
 def test_u32_radix_sort_stable(count, end_bit):
     _say(f"u32 sort count={count} end_bit={end_bit}")
     rng = np.random.default_rng(count + 1)
