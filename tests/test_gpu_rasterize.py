@@ -194,3 +194,68 @@ def test_camera_errors_raise():
     sh = torch.zeros((100, 4, 3), device=DEV)
     with pytest.raises(torch.linalg.LinAlgError):
         gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, V, scene.Ks, 32, 32, sh_coeffs=sh)
+
+
+def _leaf(t):
+    return t.detach().clone().requires_grad_(True)
+
+
+def test_batched_inputs_match_per_item_calls():
+    # Leading batch dimensions (B=2, 4 cameras each): every batch item renders
+    # exactly as a separate call on that item, gradients included.
+    a = synthetic.make_scene("sh3_1080p_4view", n=3000, width=128, height=80, seed=61).to(DEV)
+    b = synthetic.make_scene("sh3_1080p_4view", n=3000, width=128, height=80, seed=62).to(DEV)
+    print("batched inputs B=2 C=4", flush=True)
+    stack = lambda name: torch.stack([getattr(a, name), getattr(b, name)])
+    params = {k: _leaf(stack(k)) for k in ("means", "quats", "scales", "opacities", "sh_coeffs")}
+    viewmats, Ks = stack("viewmats"), stack("Ks")
+    W = torch.stack([a.loss_weights, b.loss_weights])
+    res = gs3d.rasterize(params["means"], params["quats"], params["scales"], params["opacities"], viewmats, Ks,
+                         a.width, a.height, sh_coeffs=params["sh_coeffs"], sh_degree=3)
+    assert res.features.shape == (2, 4, a.height, a.width, 3) and res.alpha.shape == (2, 4, a.height, a.width, 1)
+    ((res.features * W[..., :3]).sum() + (res.alpha * W[..., 3:]).sum()).backward()
+    for i in range(2):
+        item = {k: _leaf(v[i]) for k, v in params.items()}
+        one = gs3d.rasterize(item["means"], item["quats"], item["scales"], item["opacities"], viewmats[i], Ks[i],
+                             a.width, a.height, sh_coeffs=item["sh_coeffs"], sh_degree=3)
+        np.testing.assert_array_equal(_np(res.features[i]), _np(one.features))
+        np.testing.assert_array_equal(_np(res.alpha[i]), _np(one.alpha))
+        np.testing.assert_array_equal(_np(res.meta["radii"][i]), _np(one.meta["radii"]))
+        np.testing.assert_array_equal(_np(res.meta["means2d"][i]), _np(one.meta["means2d"]))
+        ((one.features * W[i, ..., :3]).sum() + (one.alpha * W[i, ..., 3:]).sum()).backward()
+        for k in item:
+            g = _np(item[k].grad)
+            compare(f"batch{i}_{k}", _np(params[k].grad[i]), g, rtol=1e-4, atol=1e-5 * max(1.0, float(np.abs(g).max())))
+
+
+def test_packed_metadata_several_cameras_and_batches():
+    # Packed metadata over (batch, camera, Gaussian): the triples with both
+    # radii positive in row-major order, their values and index vectors, and
+    # means2d.grad / absgrad equal to the dense gradients at those entries.
+    a = synthetic.make_scene("sh3_1080p_4view", n=2500, width=128, height=80, seed=71).to(DEV)
+    b = synthetic.make_scene("sh3_1080p_4view", n=2500, width=128, height=80, seed=72).to(DEV)
+    print("packed metadata B=2 C=4", flush=True)
+    stack = lambda name: torch.stack([getattr(a, name), getattr(b, name)])
+    args = [stack(k) for k in ("means", "quats", "scales", "opacities")]
+    viewmats, Ks, sh = stack("viewmats"), stack("Ks"), stack("sh_coeffs")
+    W = torch.stack([a.loss_weights, b.loss_weights])
+    out = {}
+    for packed in (False, True):
+        res = gs3d.rasterize(*[_leaf(t) for t in args], viewmats, Ks, a.width, a.height, sh_coeffs=sh, sh_degree=3,
+                             packed=packed, absgrad=True)
+        ((res.features * W[..., :3]).sum() + (res.alpha * W[..., 3:]).sum()).backward()
+        out[packed] = res
+    dense, packed = out[False].meta, out[True].meta
+    visible = (dense["radii"] > 0).all(-1)  # (B, C, N)
+    bi, ci, gi = (_np(t) for t in visible.nonzero(as_tuple=True))
+    assert packed["packed"] and not dense["packed"]
+    np.testing.assert_array_equal(_np(packed["batch_ids"]), bi)
+    np.testing.assert_array_equal(_np(packed["camera_ids"]), ci)
+    np.testing.assert_array_equal(_np(packed["gaussian_ids"]), gi)
+    for name in ("radii", "means2d", "opacities", "conics", "tiles_per_gauss"):
+        np.testing.assert_array_equal(_np(packed[name]), _np(dense[name])[bi, ci, gi])
+    np.testing.assert_array_equal(_np(out[True].features), _np(out[False].features))
+    for attr in ("grad", "absgrad"):
+        want = _np(getattr(dense["means2d"], attr))[bi, ci, gi]
+        compare(f"packed_means2d_{attr}", _np(getattr(packed["means2d"], attr)), want, rtol=1e-4,
+                atol=1e-5 * max(1.0, float(np.abs(want).max())))
