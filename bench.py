@@ -155,12 +155,14 @@ def stage_timings(scene, reps):
                                            scene.height)
             ev[8].record()
             feats = st.colors if sh is not None else scene.features
-            out = grender.render_views(ranges, ids, st.centers, st.conics, feats, scene.width, scene.height)
+            extra = scene.extra_features  # blended after the features, before alpha
+            out = grender.render_views(ranges, ids, st.centers, st.conics, feats, scene.width, scene.height,
+                                       extra=extra)
             ev[9].record()
             up = scene.loss_weights
             record, gf, _ = grender.backward_views(ranges, ids, st.centers, st.conics, feats,
                                                    out.transmittance, out.contributors, up, scene.width,
-                                                   scene.height, absgrad=scene.absgrad)
+                                                   scene.height, extra=extra, absgrad=scene.absgrad)
             ev[10].record()
             gproj.backward_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks,
                                  scene.width, scene.height, st.radii, record[..., 0:2], record[..., 2:6],

@@ -805,6 +805,36 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
 // of the current group row's 8 strips wait in per-thread LDS slots.
 // PACKED: footprints come from the compact per-row copies written by
 // row_records_kernel (one 32-byte gather), else they are recomputed.
+// Rows whose footprint spans more strips than this are emitted by their
+// whole wavefront (one group-row of 8 strips per lane), the others by one
+// thread each.
+constexpr int kCoopStrips = 16;
+
+// The 64-bit tile mask of group column gc of a group-row, from its 8 strip
+// spans (tile intervals along the strips' long direction).
+GS3D_DEV uint64_t group_mask(const int2 (&span)[1 << kGroupShift], int gc, bool is_y) {
+    const int c0 = gc << kGroupShift;
+    uint64_t m = 0;
+#pragma unroll
+    for (int j = 0; j < (1 << kGroupShift); ++j) {
+        const int lo = max(span[j].x, c0), hi = min(span[j].y, c0 + 8);
+        if (hi <= lo) continue;
+        if (is_y) {
+            m |= (((1ull << (hi - lo)) - 1ull) << (lo - c0)) << (8 * j);
+        } else {
+            // column strip j: bit 8 * (k - c0) + j for k in [lo, hi)
+            const uint64_t bytes = (hi - c0 == 8 ? ~0ull : (1ull << (8 * (hi - c0))) - 1ull) & ~((1ull << (8 * (lo - c0))) - 1ull);
+            m |= (0x0101010101010101ull & bytes) << j;
+        }
+    }
+    return m;
+}
+
+// Items of one row in group-row order, then group-column order, at
+// [start, stop): rows spanning few strips by their own thread, the others by
+// their whole wavefront (lanes take group-rows; a wave prefix sum of the
+// lanes' item counts gives each group-row's place, so the items land exactly
+// where the one-thread walk puts them).
 template <bool PACKED>
 __global__ __launch_bounds__(kBinThreads) void accutile_emit_kernel(const uint64_t* __restrict__ records,
                                                                     const int32_t* __restrict__ offsets, int64_t rows,
@@ -814,65 +844,146 @@ __global__ __launch_bounds__(kBinThreads) void accutile_emit_kernel(const uint64
                                                                     uint64_t* __restrict__ masks) {
     __shared__ int2 s_span[1 << kGroupShift][kBinThreads];
     const int t = threadIdx.x;
+    const int lane = lane_id();
     const int64_t i = (int64_t)blockIdx.x * kBinThreads + t;
-    if (i >= rows) return;
-    const int64_t start = i > 0 ? offsets[i - 1] : 0;
-    const int64_t stop = min((int64_t)offsets[i], limit);
-    if (start >= stop) return;
-    const int64_t row = (int64_t)(uint32_t)records[i];
-    Ellipse e;
-    if constexpr (PACKED) {
-        e = unpack_ellipse(footprints[2 * row], footprints[2 * row + 1]);
-    } else {
-        const int radius = geo.radii[row];
-        if (radius <= 0) return;
-        e = footprint(reinterpret_cast<const float2*>(geo.centers)[row], reinterpret_cast<const float4*>(geo.conics)[row],
-                      radius, d.gx, d.gy);
-    }
-    const int view = (int)(row / n);
-    const uint64_t id = (uint64_t)(uint32_t)(row - (int64_t)view * n);
-    const uint32_t gbase = (uint32_t)(view * d.gpv);
-    int64_t p = start;
-    bool is_y = true;
-    int cur = -1, gmin = INT_MAX, gmax = -1;
-    auto flush = [&](int G) {
-        for (int gc = gmin; gc <= gmax; ++gc) {
-            const int c0 = gc << kGroupShift;
-            uint64_t m = 0;
-            for (int j = 0; j < (1 << kGroupShift); ++j) {
-                const int2 sp = s_span[j][t];
-                const int lo = max(sp.x, c0), hi = min(sp.y, c0 + 8);
-                if (hi <= lo) continue;
-                if (is_y) {
-                    m |= (((1ull << (hi - lo)) - 1ull) << (lo - c0)) << (8 * j);
-                } else {
-                    for (int k = lo; k < hi; ++k) m |= 1ull << (8 * (k - c0) + j);
+    int64_t start = 0, stop = 0, row = 0;
+    float4 p0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), p1 = p0, conic = p0;
+    float2 center = make_float2(0.0f, 0.0f);
+    int radius = 0;
+    bool live = false;
+    if (i < rows) {
+        start = i > 0 ? offsets[i - 1] : 0;
+        stop = min((int64_t)offsets[i], limit);
+        if (start < stop) {
+            row = (int64_t)(uint32_t)records[i];
+            if constexpr (PACKED) {
+                p0 = footprints[2 * row];
+                p1 = footprints[2 * row + 1];
+                live = true;
+            } else {
+                radius = geo.radii[row];
+                if (radius > 0) {
+                    center = reinterpret_cast<const float2*>(geo.centers)[row];
+                    conic = reinterpret_cast<const float4*>(geo.conics)[row];
+                    live = true;
                 }
             }
-            const int GX = is_y ? gc : G, GY = is_y ? G : gc;
-            if (p < stop) {
-                st_stream(items + p, (id << 32) | (uint64_t)(gbase + (uint32_t)(GY * d.sgx + GX)));
-                st_stream(masks + p, m);
-            }
-            ++p;
         }
+    }
+    auto ellipse_of = [&](float4 q0, float4 q1, float2 ctr, float4 con, int rad) {
+        if constexpr (PACKED)
+            return unpack_ellipse(q0, q1);
+        else
+            return footprint(ctr, con, rad, d.gx, d.gy);
     };
-    accutile_strips(e, is_y, [&](int strip, int lo, int hi) {
-        const int G = strip >> kGroupShift;
-        if (G != cur) {
-            if (cur >= 0) flush(cur);
-            cur = G;
-            gmin = INT_MAX;
-            gmax = -1;
-            for (int j = 0; j < (1 << kGroupShift); ++j) s_span[j][t] = make_int2(0, 0);
+    int strips = 0;
+    Ellipse e{};
+    if (live) {
+        e = ellipse_of(p0, p1, center, conic, radius);
+        const int nx = max(0, e.bounds.z - e.bounds.x), ny = max(0, e.bounds.w - e.bounds.y);
+        strips = (nx == 0 || ny == 0) ? 0 : min(nx, ny);
+    }
+    const bool coop = strips > kCoopStrips;
+    if (live && !coop) {
+        const int view = (int)(row / n);
+        const uint64_t id = (uint64_t)(uint32_t)(row - (int64_t)view * n);
+        const uint32_t gbase = (uint32_t)(view * d.gpv);
+        int64_t p = start;
+        bool is_y = true;
+        int cur = -1, gmin = INT_MAX, gmax = -1;
+        auto flush = [&](int G) {
+            int2 span[1 << kGroupShift];
+#pragma unroll
+            for (int j = 0; j < (1 << kGroupShift); ++j) span[j] = s_span[j][t];
+            for (int gc = gmin; gc <= gmax; ++gc) {
+                const uint64_t m = group_mask(span, gc, is_y);
+                const int GX = is_y ? gc : G, GY = is_y ? G : gc;
+                if (p < stop) {
+                    st_stream(items + p, (id << 32) | (uint64_t)(gbase + (uint32_t)(GY * d.sgx + GX)));
+                    st_stream(masks + p, m);
+                }
+                ++p;
+            }
+        };
+        accutile_strips(e, is_y, [&](int strip, int lo, int hi) {
+            const int G = strip >> kGroupShift;
+            if (G != cur) {
+                if (cur >= 0) flush(cur);
+                cur = G;
+                gmin = INT_MAX;
+                gmax = -1;
+                for (int j = 0; j < (1 << kGroupShift); ++j) s_span[j][t] = make_int2(0, 0);
+            }
+            s_span[strip & 7][t] = make_int2(lo, hi);
+            if (hi > lo) {
+                gmin = min(gmin, lo >> kGroupShift);
+                gmax = max(gmax, (hi - 1) >> kGroupShift);
+            }
+        });
+        if (cur >= 0) flush(cur);
+    }
+    // Wide rows: the wavefront takes them one at a time.
+    uint64_t todo = __ballot(coop);
+    while (todo) {
+        const int src = __builtin_ctzll(todo);
+        todo &= todo - 1;
+        auto bcast_f = [&](float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src)); };
+        auto bcast_i64 = [&](int64_t v) {
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), src);
+            return (int64_t)(((uint64_t)hi << 32) | lo);
+        };
+        const int64_t w_start = bcast_i64(start), w_stop = bcast_i64(stop), w_row = bcast_i64(row);
+        const float4 q0 = make_float4(bcast_f(p0.x), bcast_f(p0.y), bcast_f(p0.z), bcast_f(p0.w));
+        const float4 q1 = make_float4(bcast_f(p1.x), bcast_f(p1.y), bcast_f(p1.z), bcast_f(p1.w));
+        const float4 con = make_float4(bcast_f(conic.x), bcast_f(conic.y), bcast_f(conic.z), bcast_f(conic.w));
+        const float2 ctr = make_float2(bcast_f(center.x), bcast_f(center.y));
+        const int rad = __builtin_amdgcn_readlane(radius, src);
+        const Ellipse we = ellipse_of(q0, q1, ctr, con, rad);
+        const int4 bb = we.bounds;
+        const bool is_y = (bb.w - bb.y) < (bb.z - bb.x);
+        const int s0 = is_y ? bb.y : bb.x, s1 = is_y ? bb.w : bb.z;
+        const int full0 = is_y ? bb.x : bb.y, full1 = is_y ? bb.z : bb.w;
+        const int view = (int)(w_row / n);
+        const uint64_t id = (uint64_t)(uint32_t)(w_row - (int64_t)view * n);
+        const uint32_t gbase = (uint32_t)(view * d.gpv);
+        const int G0 = s0 >> kGroupShift, G1 = (s1 - 1) >> kGroupShift;
+        int64_t base = w_start;
+        for (int Gb = G0; Gb <= G1; Gb += 64) {
+            const int G = Gb + lane;
+            int2 span[1 << kGroupShift];
+            int gmin = INT_MAX, gmax = -1;
+#pragma unroll
+            for (int j = 0; j < (1 << kGroupShift); ++j) {
+                span[j] = make_int2(0, 0);
+                const int strip = (G << kGroupShift) + j;
+                if (G <= G1 && strip >= s0 && strip < s1) {
+                    int2 sp = make_int2(full0, full1);
+                    if (we.precise)
+                        sp = strip_span(we, strip, is_y, line_intersection(we, strip, is_y),
+                                        line_intersection(we, strip + 1, is_y));
+                    span[j] = sp;
+                    if (sp.y > sp.x) {
+                        gmin = min(gmin, sp.x >> kGroupShift);
+                        gmax = max(gmax, (sp.y - 1) >> kGroupShift);
+                    }
+                }
+            }
+            const int cnt = gmax >= gmin ? gmax - gmin + 1 : 0;
+            const int incl = wave_inclusive_scan(cnt);
+            int64_t p = base + (incl - cnt);
+            for (int gc = gmin; gc <= gmax; ++gc) {
+                const uint64_t m = group_mask(span, gc, is_y);
+                const int GX = is_y ? gc : G, GY = is_y ? G : gc;
+                if (p < w_stop) {
+                    st_stream(items + p, (id << 32) | (uint64_t)(gbase + (uint32_t)(GY * d.sgx + GX)));
+                    st_stream(masks + p, m);
+                }
+                ++p;
+            }
+            base += __builtin_amdgcn_readlane(incl, 63);
         }
-        s_span[strip & 7][t] = make_int2(lo, hi);
-        if (hi > lo) {
-            gmin = min(gmin, lo >> kGroupShift);
-            gmax = max(gmax, (hi - 1) >> kGroupShift);
-        }
-    });
-    if (cur >= 0) flush(cur);
+    }
 }
 
 // chunk_base[g] = exclusive scan over groups of ceil(len_g / kChunk);

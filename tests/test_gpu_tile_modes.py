@@ -82,20 +82,21 @@ def test_tile_mode_counts_and_lists_bit_exact(mode, key, degree):
 
 
 @pytest.mark.parametrize("mode", MODES)
-@pytest.mark.parametrize("views,n,W,H,spread", [
-    (2, 3000, 200, 120, 1.0),      # partial groups at the edges
-    (1, 20000, 128, 128, 0.15),    # crowded corner: many chunks per group
-    (70, 400, 160, 160, 1.0),      # 280 groups: two group-sort passes
-    (1, 2000, 4200, 64, 1.0),      # 263 tiles across: rectangles not packed in the records
+@pytest.mark.parametrize("views,n,W,H,spread,smax", [
+    (2, 3000, 200, 120, 1.0, 60.0),      # partial groups at the edges
+    (1, 20000, 128, 128, 0.15, 60.0),    # crowded corner: many chunks per group
+    (70, 400, 160, 160, 1.0, 60.0),      # 280 groups: two group-sort passes
+    (1, 2000, 4200, 64, 1.0, 60.0),      # 263 tiles across: rectangles not packed in the records
+    (2, 1500, 640, 480, 1.0, 160.0),     # footprints over 16 tiles both ways: emitted by whole wavefronts
 ])
-def test_tile_mode_grouped_binning_edge_cases(mode, views, n, W, H, spread):
+def test_tile_mode_grouped_binning_edge_cases(mode, views, n, W, H, spread, smax):
     # Equal depths (ties broken by index), wide and thin rotated ellipses,
     # opacities below the 1/255 threshold, non-positive-definite conics.
     _say(f"tile mode binning {mode} views={views} n={n} {W}x{H}")
     rng = np.random.default_rng(11)
     gx, gy = (W + 15) // 16, (H + 15) // 16
     centers = (rng.random((views, n, 2)) * spread * np.array([W, H])).astype(np.float32)
-    s1 = np.exp(rng.uniform(0.0, np.log(60.0), (views, n)))
+    s1 = np.exp(rng.uniform(0.0, np.log(smax), (views, n)))
     s2 = s1 * np.exp(rng.uniform(np.log(0.05), 0.0, (views, n)))
     th = rng.uniform(0, np.pi, (views, n))
     ct, sn = np.cos(th), np.sin(th)
@@ -116,6 +117,15 @@ def test_tile_mode_grouped_binning_edge_cases(mode, views, n, W, H, spread):
         for i in range(n):
             if radii[v, i] > 0:
                 tiles[v, i] = len(oracle.tile_footprint(mode, centers[v, i], conics[v, i], radii[v, i], gx, gy)[1])
+    if smax > 100.0 and mode == "accutile":
+        # some footprints must span more than 16 tiles in both directions
+        wide = 0
+        for v in range(views):
+            for i in range(0, n, 7):
+                if radii[v, i] > 0:
+                    rect = oracle.tile_footprint("snugbox", centers[v, i], conics[v, i], radii[v, i], gx, gy)[0]
+                    wide += min(rect[2] - rect[0], rect[3] - rect[1]) > 16
+        assert wide > 0
     sk, sv, rr = _oracle_lists(centers, conics, radii, depths, tiles, W, H, views, mode)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
     bins = binning.bin_and_sort(t(centers), t(radii), t(tiles), t(depths), W, H, conics=t(conics), tile_mode=mode,
