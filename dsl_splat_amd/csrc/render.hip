@@ -467,8 +467,14 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     const int Dg = D - (a.one_tail ? 1 : 0);
     const int lane = lane_id(), wave = threadIdx.x >> 6;
-    float fx[PIX], fy[PIX], T[PIX], T_final[PIX], bg_grad[PIX], last_alpha[PIX];
-    float grad[PIX][CH], accum[PIX][CH], last_color[PIX][CH];
+    // Per pixel: S = sum_c accum_c * grad_c, the colour accumulated behind
+    // the current Gaussian dotted with the upstream gradient, and last_dot =
+    // sum_c f_c * grad_c of the last accepted Gaussian.  With them the alpha
+    // gradient sum_c (f_c - accum_c) grad_c (gs3d/render.py:300-312) is
+    // dot - S, and accum_c = la last_c + (1 - la) accum_c becomes
+    // S = la last_dot + (1 - la) S: no per-channel state besides grad.
+    float fx[PIX], fy[PIX], T[PIX], T_final[PIX], bg_grad[PIX], last_alpha[PIX], S[PIX], last_dot[PIX];
+    float grad[PIX][CH];
     int last_contributor[PIX];
     bool inside[PIX];
     if (threadIdx.x == 0) s_max_last = 0;
@@ -482,14 +488,10 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
         fx[k] = (float)x;
         fy[k] = (float)y;
         inside[k] = x < a.width && y < a.height;
-        T[k] = T_final[k] = bg_grad[k] = last_alpha[k] = 0.0f;
+        T[k] = T_final[k] = bg_grad[k] = last_alpha[k] = S[k] = last_dot[k] = 0.0f;
         last_contributor[k] = 0;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            grad[k][c] = 0.0f;
-            accum[k][c] = 0.0f;
-            last_color[k][c] = 0.0f;
-        }
+        for (int c = 0; c < CH; ++c) grad[k][c] = 0.0f;
         if (inside[k]) {
             const int64_t pix = ((int64_t)t.view * a.height + y) * a.width + x;
             T_final[k] = a.final_t[pix];
@@ -610,20 +612,20 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
                 // reciprocal (1 - alpha >= 0.01) and fused multiply-adds.
                 const float inv = __builtin_amdgcn_rcpf(1.0f - alpha);
                 T[k] = T[k] * inv;
-                const float la = last_alpha[k], keep = 1.0f - la, aT = alpha * T[k];
+                const float la = last_alpha[k], aT = alpha * T[k];
                 // Every compiled channel slot is processed: slots at or beyond
                 // D hold zero features and zero upstream gradients (no
                 // contribution), and the constant alpha channel's entry has no
                 // destination, so no per-channel branch is needed.
-                float grad_alpha = 0.0f;
+                float dot = 0.0f;
 #pragma unroll
                 for (int c = 0; c < CH; ++c) {
-                    accum[k][c] = __builtin_fmaf(la, last_color[k][c], keep * accum[k][c]);
-                    last_color[k][c] = f[c];
-                    grad_alpha = __builtin_fmaf(f[c] - accum[k][c], grad[k][c], grad_alpha);
+                    dot = __builtin_fmaf(f[c], grad[k][c], dot);
                     gfeat[c] = __builtin_fmaf(aT, grad[k][c], gfeat[c]);
                 }
-                grad_alpha = __builtin_fmaf(grad_alpha, T[k], -(T_final[k] * inv) * bg_grad[k]);
+                S[k] = __builtin_fmaf(la, last_dot[k], (1.0f - la) * S[k]);
+                last_dot[k] = dot;
+                const float grad_alpha = __builtin_fmaf(dot - S[k], T[k], -(T_final[k] * inv) * bg_grad[k]);
                 last_alpha[k] = alpha;
                 const float gv = con.w * grad_alpha;
                 const float gdx = G * dx, gdy = G * dy;
