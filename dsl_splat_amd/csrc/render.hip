@@ -345,29 +345,37 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_rend
                 const int contributor = begin - t.first + j + 1;  // list position, 1-based
                 bool acc[PIX];
                 float wk[PIX];
+                // Branch-free per pixel except for the exponential: a
+                // divergent branch per test costs more in exec-mask work than
+                // the selects it replaces (the wavefront issues the tail
+                // whenever any lane needs it).  Updates are selected, not
+                // multiplied by zero, so non-finite features of a rejected
+                // Gaussian cannot reach the pixel.
 #pragma unroll
                 for (int k = 0; k < PIX; ++k) {
-                    acc[k] = false;
-                    wk[k] = 0.0f;
-                    if (done[k]) continue;
                     const float dx = g.xy.x - fx[k], dy = g.xy.y - fy[k];
                     const float power = blend_power(g.con.x, g.con.y, g.con.z, dx, dy);
-                    if (!(power <= 0.0f) || !(power >= g.cut)) continue;
-                    const float alpha = sel_min(0.99f, g.con.w * blend_exp(power));
-                    if (!(alpha >= 1.0f / 255.0f)) continue;
+                    const bool in = !done[k] && power <= 0.0f && power >= g.cut;
+                    float e = 0.0f;
+                    if (in) e = blend_exp(power);
+                    const float alpha = in ? sel_min(0.99f, g.con.w * e) : 0.0f;
+                    const bool take = alpha >= 1.0f / 255.0f;
                     const float next_t = T[k] * (1.0f - alpha);
-                    if (next_t < 0.0001f) {
-                        done[k] = true;
-                        continue;
-                    }
+                    const bool term = take && next_t < 0.0001f;
+                    const bool upd = take && !term;
+                    done[k] = done[k] || term;
                     const float w = alpha * T[k];
 #pragma unroll
-                    for (int c = 0; c < CH; ++c) color[k][c] = __builtin_fmaf(g.f[c], w, color[k][c]);  // zero slots >= D
-                    T[k] = next_t;
-                    last_contributor[k] = contributor;
-                    acc[k] = true;
-                    wk[k] = w;
+                    for (int c = 0; c < CH; ++c) {
+                        const float nc = __builtin_fmaf(g.f[c], w, color[k][c]);
+                        color[k][c] = upd ? nc : color[k][c];
+                    }
+                    T[k] = upd ? next_t : T[k];
+                    last_contributor[k] = upd ? contributor : last_contributor[k];
+                    acc[k] = upd;
+                    wk[k] = upd ? w : 0.0f;
                 }
+
                 if constexpr (STATS) {
                     bool hit = false;
 #pragma unroll
