@@ -282,8 +282,11 @@ GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, int view, int
     }
 }
 
+// Up to 8 channels the kernel is held to 80 VGPRs (6 wavefronts per SIMD
+// instead of 5: 1.180 -> 1.130 ms on RGB); wider channel vectors keep the
+// registers they need.
 template <int CH, int PIX, bool STATS>
-__global__ __launch_bounds__(kTilePixels / PIX) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st) {
+__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 8 ? 6 : 1))) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st) {
     constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
     __shared__ float2 s_xy[B];
