@@ -319,13 +319,15 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_kernel(const K* _
     }
 }
 
-template <class K, class V>
+// VALS = false sorts keys alone: no value loads, stores or LDS staging, which
+// leaves room for one more block per CU.
+template <class K, class V, bool VALS>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
     V* __restrict__ vals_out, int64_t count, int shift, uint32_t mask, int bits,
     const int32_t* __restrict__ scanned, int64_t tiles) {
     __shared__ K s_keys[kSortTile];
-    __shared__ V s_vals[kSortTile];
+    __shared__ V s_vals[VALS ? kSortTile : 1];
     __shared__ uint32_t s_wcnt[kSortThreads / 64][kRadix];
     __shared__ int32_t s_gbase[kRadix];
     __shared__ uint32_t s_scan_wave[kSortThreads / 64];
@@ -342,7 +344,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
         const int64_t idx = base + k * 64;
         if (idx < count) {
             key[k] = keys_in[idx];
-            val[k] = vals_in ? vals_in[idx] : V(0);
+            val[k] = VALS ? vals_in[idx] : V(0);
         } else {
             key[k] = K(0);
             val[k] = V(0);
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
             const uint32_t d = digit_of(key[k], shift, mask);
             const uint32_t pos = s_wcnt[wave][d] + rank[k];
             s_keys[pos] = key[k];
-            s_vals[pos] = val[k];
+            if (VALS) s_vals[pos] = val[k];
         }
     }
     __syncthreads();
@@ -410,7 +412,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
             const K kk = s_keys[p];
             const int64_t dst = (int64_t)s_gbase[digit_of(kk, shift, mask)] + p;
             keys_out[dst] = kk;  // plain stores: digit runs start mid-line and the L2 merges them
-            if (vals_out) vals_out[dst] = s_vals[p];
+            if (VALS) vals_out[dst] = s_vals[p];
         }
     }
 }
@@ -457,8 +459,12 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
                            shift, mask, sc.counts, tiles);
         const int status = run_scan<uint32_t, false>(sc.counts, tiles * kRadix, sc.scanned, nullptr, sc.scan_scratch, s);
         if (status != GS3D_OK) return status;
-        hipLaunchKernelGGL((sort_scatter_kernel<K, V>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin, vin, kout,
-                           vout, count, shift, mask, bits, sc.scanned, tiles);
+        if (values)
+            hipLaunchKernelGGL((sort_scatter_kernel<K, V, true>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin,
+                               vin, kout, vout, count, shift, mask, bits, sc.scanned, tiles);
+        else
+            hipLaunchKernelGGL((sort_scatter_kernel<K, V, false>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin,
+                               vin, kout, vout, count, shift, mask, bits, sc.scanned, tiles);
         K* tk = kin;
         kin = kout;
         kout = tk;

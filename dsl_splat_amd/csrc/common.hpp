@@ -161,7 +161,8 @@ GS3D_DEV float wave_sum(float v) {
 // levels pair the values so that each add serves two of them (32-lane
 // halves, then 16-lane rows), then a row butterfly finishes every row.  On
 // return out[r] holds, in every lane of row q (lanes 16q..16q+15), the total
-// of value 4r + {0, 2, 1, 3}[q].  All 64 lanes must be active.
+// of value 4r + {0, 2, 1, 3}[q]; rows whose index is V or more hold
+// unspecified values.  All 64 lanes must be active.
 template <int V>
 GS3D_DEV void wave_sum_rows(const float (&v)[V], float (&out)[(V + 3) / 4]) {
     constexpr int W = (V + 1) / 2;
@@ -170,7 +171,7 @@ GS3D_DEV void wave_sum_rows(const float (&v)[V], float (&out)[(V + 3) / 4]) {
 #pragma unroll
     for (int i = 0; i < W; ++i) {
         const float a = v[2 * i];
-        const float b = (2 * i + 1 < V) ? v[2 * i + 1] : 0.0f;
+        const float b = (2 * i + 1 < V) ? v[2 * i + 1] : a;  // an unpaired value pairs with itself
         // first = [a lanes 0-31 | b lanes 0-31], second = [a lanes 32-63 | b lanes 32-63]
         const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
         w[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
@@ -178,7 +179,7 @@ GS3D_DEV void wave_sum_rows(const float (&v)[V], float (&out)[(V + 3) / 4]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const float a = w[2 * r];
-        const float b = (2 * r + 1 < W) ? w[2 * r + 1] : 0.0f;
+        const float b = (2 * r + 1 < W) ? w[2 * r + 1] : a;
         // first = rows [a0 b0 a2 b2], second = rows [a1 b1 a3 b3]
         const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
         out[r] = row_sum16(__uint_as_float(p[0]) + __uint_as_float(p[1]));

@@ -694,8 +694,9 @@ enum ShRows : int { kRowsScalar = 0, kRowsFloat4 = 1, kRowsStaged = 2 };
 // registers, loaded as float4 when VEC (rows 16-byte aligned, E a multiple
 // of 4).  Runs after
 // the projection kernel, whose radii mark the visible rows.
+// Capped at 80 VGPRs (six wavefronts per SIMD; degree 3 needs 83 uncapped).
 template <int DEG, bool VEC>
-__global__ __launch_bounds__(kShRowBlock) void sh_rows_fwd_kernel(gs3d_project_args a) {
+__global__ __launch_bounds__(kShRowBlock) __attribute__((amdgpu_waves_per_eu(6))) void sh_rows_fwd_kernel(gs3d_project_args a) {
     constexpr int KC = (DEG + 1) * (DEG + 1);
     const int64_t n = a.n;
     const int64_t i = (int64_t)blockIdx.x * kShRowBlock + threadIdx.x;

@@ -218,6 +218,14 @@ GS3D_DEV float opaque_zero() {
     return z;
 }
 
+// Two opaque zeros from one 64-bit move.
+GS3D_DEV void opaque_zero2(float& a, float& b) {
+    uint64_t z;
+    asm volatile("v_mov_b64 %0, 0" : "=v"(z));
+    a = __uint_as_float((uint32_t)z);
+    b = __uint_as_float((uint32_t)(z >> 32));
+}
+
 // One staged Gaussian as the blend loops read it from LDS.  The loops load
 // the next Gaussian of their wavefront before blending the current one, so
 // the LDS latency overlaps the arithmetic.
@@ -462,8 +470,10 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     }
 }
 
+// Four channels without absolute gradients fit 80 VGPRs, six wavefronts per
+// SIMD (the LDS limit of a 13 KiB block); the uncapped allocation is 84.
 template <int CH, bool ABS, int PIX>
-__global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_render_bwd_args b) {
+__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 4 && !ABS ? 6 : 1))) void render_bwd_kernel(gs3d_render_bwd_args b) {
     constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
     __shared__ float2 s_xy[B];
@@ -537,8 +547,11 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
     constexpr int R = (NV + 3) / 4;
     float* dst_base = nullptr;
     int64_t dst_step = 0;
+    float dst_scale = 1.0f;
     {
         const int k = wave_sum_rows_value(lane);
+        if (k < 2 || k == 3) dst_scale = -1.0f;
+        if (k == 2 || k == 4) dst_scale = -0.5f;
         const int64_t row0 = (int64_t)t.view * a.n;
         if ((lane & 15) >= R || k >= NV) {
         } else if (k < 2) {
@@ -564,6 +577,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
         }
     }
     // Largest last contributor among this wavefront's pixels (wave-uniform).
+    const int lane_last = my_max;
     int wave_last = my_max;
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) wave_last = max(wave_last, __shfl_xor(wave_last, d, 64));
@@ -588,35 +602,34 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
             const int j = c0 + __builtin_ctzll(todo);
             todo &= todo - 1;
             const int pos = top - 1 - j;
-            bool any = false;
-#pragma unroll
-            for (int k = 0; k < PIX; ++k) any = any || (inside[k] && pos < last_contributor[k]);
-            if (__ballot(any) == 0) continue;
+            // Pixels outside the image have last contributor 0.
+            if (__ballot(pos < lane_last) == 0) continue;
             const float2 xy = s_xy[j];
             const float4 con = s_con[j];
             const float cut = s_cut[j];
             const float* f = s_feat + j * CH;
             // Accumulators start from an opaque zero: a literal zero would be
             // folded into each accumulator's first FMA, and every path that
-            // skips a pixel would then re-materialise the zeros.
-            float gfeat[CH];
-            float dcx = opaque_zero(), dcy = opaque_zero(), gk0 = opaque_zero(), gk1 = opaque_zero();
-            float gk2 = opaque_zero(), gk3 = opaque_zero(), ax = 0.0f, ay = 0.0f;
-            if (ABS) {
-                ax = opaque_zero();
-                ay = opaque_zero();
-            }
+            // skips a pixel would then re-materialise the zeros.  vals holds,
+            // in gradient-entry order, sum w (a dx + b dy), sum w (c dy + b dx),
+            // sum w dx dx, sum w dx dy, sum w dy dy with w = o G dL/dalpha,
+            // then sum G dL/dalpha, the absolute centre terms and the feature
+            // terms; the constant factors (-1, -1/2) are applied per lane
+            // after the wavefront sum.
+            float vals[NV];
 #pragma unroll
-            for (int c = 0; c < CH; ++c) gfeat[c] = opaque_zero();
+            for (int i = 0; i + 1 < NV; i += 2) opaque_zero2(vals[i], vals[i + 1]);
+            if constexpr (NV % 2) vals[NV - 1] = opaque_zero();
             bool accepted = false;
 #pragma unroll
             for (int k = 0; k < PIX; ++k) {
-                if (!(inside[k] && pos < last_contributor[k])) continue;
+                if (!(pos < last_contributor[k])) continue;
                 const float dx = xy.x - fx[k], dy = xy.y - fy[k];
                 const float power = blend_power(con.x, con.y, con.z, dx, dy);
                 if (!(power <= 0.0f) || !(power >= cut)) continue;
                 const float G = blend_exp(power);
-                const float alpha = sel_min(0.99f, con.w * G);
+                const float og = con.w * G;
+                const float alpha = sel_min(0.99f, og);
                 if (!(alpha >= 1.0f / 255.0f)) continue;
                 accepted = true;
                 // Gradients only need tolerance-level agreement: one hardware
@@ -632,52 +645,49 @@ __global__ __launch_bounds__(kTilePixels / PIX) void render_bwd_kernel(gs3d_rend
 #pragma unroll
                 for (int c = 0; c < CH; ++c) {
                     dot = __builtin_fmaf(f[c], grad[k][c], dot);
-                    gfeat[c] = __builtin_fmaf(aT, grad[k][c], gfeat[c]);
+                    vals[FB + c] = __builtin_fmaf(aT, grad[k][c], vals[FB + c]);
                 }
                 S[k] = __builtin_fmaf(la, last_dot[k], (1.0f - la) * S[k]);
                 last_dot[k] = dot;
                 const float grad_alpha = __builtin_fmaf(dot - S[k], T[k], -(T_final[k] * inv) * bg_grad[k]);
                 last_alpha[k] = alpha;
-                const float gv = con.w * grad_alpha;
-                const float gdx = G * dx, gdy = G * dy;
-                const float cx = -gv * __builtin_fmaf(gdx, con.x, gdy * con.y);
-                const float cy = -gv * __builtin_fmaf(gdy, con.z, gdx * con.y);
-                dcx += cx;
-                dcy += cy;
+                // dL/dG = o dL/dalpha; the centre gradient is
+                // -w (a dx + b dy, c dy + b dx) and the conic gradient
+                // -w (dx dx / 2, dx dy, dy dy / 2).
+                const float w = og * grad_alpha;
+                const float ux = __builtin_fmaf(con.x, dx, con.y * dy);
+                const float uy = __builtin_fmaf(con.z, dy, con.y * dx);
                 if (ABS) {
-                    ax += __builtin_fabsf(cx);
-                    ay += __builtin_fabsf(cy);
+                    const float cx = w * ux, cy = w * uy;
+                    vals[0] += cx;
+                    vals[1] += cy;
+                    vals[6] += __builtin_fabsf(cx);
+                    vals[7] += __builtin_fabsf(cy);
+                } else {
+                    vals[0] = __builtin_fmaf(w, ux, vals[0]);
+                    vals[1] = __builtin_fmaf(w, uy, vals[1]);
                 }
-                const float hgv = -0.5f * gv;
-                gk0 = __builtin_fmaf(hgv * gdx, dx, gk0);
-                gk1 = __builtin_fmaf(-gv * gdx, dy, gk1);
-                gk2 = __builtin_fmaf(hgv * gdy, dy, gk2);
-                gk3 = __builtin_fmaf(G, grad_alpha, gk3);
+                const float wx = w * dx, wy = w * dy;
+                vals[2] = __builtin_fmaf(wx, dx, vals[2]);
+                vals[3] = __builtin_fmaf(wx, dy, vals[3]);
+                vals[4] = __builtin_fmaf(wy, dy, vals[4]);
+                vals[5] = __builtin_fmaf(G, grad_alpha, vals[5]);
             }
             if (__ballot(accepted) == 0) continue;
             // Wavefront sums of all gradient entries at once; one atomic
             // instruction, each active lane adding one entry.
-            float vals[NV];
-            vals[0] = dcx;
-            vals[1] = dcy;
-            vals[2] = gk0;
-            vals[3] = gk1;
-            vals[4] = gk2;
-            vals[5] = gk3;
-            if (ABS) {
-                vals[6] = ax;
-                vals[7] = ay;
-            }
-#pragma unroll
-            for (int c = 0; c < CH; ++c) vals[FB + c] = gfeat[c];
             float sums[R];
             wave_sum_rows<NV>(vals, sums);
+            // Finish the sums on every lane, ahead of the branch: the last
+            // row step then stays one DPP add.
+#pragma unroll
+            for (int r = 0; r < R; ++r) asm volatile("" : "+v"(sums[r]));
             if (dst_base) {
                 const int slot = lane & 15;
                 float v = sums[0];
 #pragma unroll
                 for (int r = 1; r < R; ++r) v = (slot == r) ? sums[r] : v;
-                atomicAdd(dst_base + (int64_t)s_id[j] * dst_step, v);
+                atomicAdd(dst_base + (int64_t)s_id[j] * dst_step, v * dst_scale);
             }
           }
         }
