@@ -470,10 +470,10 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     }
 }
 
-// Four channels without absolute gradients fit 80 VGPRs, six wavefronts per
-// SIMD (the LDS limit of a 13 KiB block); the uncapped allocation is 84.
+// Four channels fit 80 VGPRs, six wavefronts per SIMD (the LDS limit of a
+// 13 KiB block); with absolute gradients the uncapped allocation is 83.
 template <int CH, bool ABS, int PIX>
-__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 4 && !ABS ? 6 : 1))) void render_bwd_kernel(gs3d_render_bwd_args b) {
+__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 4 ? 6 : 1))) void render_bwd_kernel(gs3d_render_bwd_args b) {
     constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
     __shared__ float2 s_xy[B];
@@ -489,12 +489,14 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     const int Dg = D - (a.one_tail ? 1 : 0);
     const int lane = lane_id(), wave = threadIdx.x >> 6;
     // Per pixel: S = sum_c accum_c * grad_c, the colour accumulated behind
-    // the current Gaussian dotted with the upstream gradient, and last_dot =
-    // sum_c f_c * grad_c of the last accepted Gaussian.  With them the alpha
-    // gradient sum_c (f_c - accum_c) grad_c (gs3d/render.py:300-312) is
-    // dot - S, and accum_c = la last_c + (1 - la) accum_c becomes
-    // S = la last_dot + (1 - la) S: no per-channel state besides grad.
-    float fx[PIX], fy[PIX], T[PIX], T_final[PIX], bg_grad[PIX], last_alpha[PIX], S[PIX], last_dot[PIX];
+    // the current Gaussian dotted with the upstream gradient.  With
+    // dot = sum_c f_c * grad_c the alpha gradient sum_c (f_c - accum_c) grad_c
+    // (gs3d/render.py:300-312) is E = dot - S, and
+    // accum_c = la last_c + (1 - la) accum_c becomes S = S + la E_last with
+    // la and E_last those of the last accepted Gaussian: no per-channel state
+    // besides grad.  bg_t = -T_final * sum_c bg_c grad_c is the background
+    // term, divided by the transmittance factors as they are undone.
+    float fx[PIX], fy[PIX], T[PIX], bg_t[PIX], last_alpha[PIX], S[PIX], last_e[PIX];
     float grad[PIX][CH];
     int last_contributor[PIX];
     bool inside[PIX];
@@ -509,14 +511,14 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
         fx[k] = (float)x;
         fy[k] = (float)y;
         inside[k] = x < a.width && y < a.height;
-        T[k] = T_final[k] = bg_grad[k] = last_alpha[k] = S[k] = last_dot[k] = 0.0f;
+        T[k] = bg_t[k] = last_alpha[k] = S[k] = last_e[k] = 0.0f;
         last_contributor[k] = 0;
 #pragma unroll
         for (int c = 0; c < CH; ++c) grad[k][c] = 0.0f;
         if (inside[k]) {
             const int64_t pix = ((int64_t)t.view * a.height + y) * a.width + x;
-            T_final[k] = a.final_t[pix];
-            T[k] = T_final[k];
+            T[k] = a.final_t[pix];
+            float bg_grad = 0.0f;
             last_contributor[k] = a.contributors[pix];
             const int F = a.feat_channels, E = a.extra_channels;
 #pragma unroll
@@ -531,8 +533,9 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                     u = b.upstream_alpha[pix * b.upstream_alpha_stride];
                 }
                 grad[k][c] = u;
-                bg_grad[k] += ((bg && c < F) ? bg[c] : 0.0f) * u;
+                bg_grad += ((bg && c < F) ? bg[c] : 0.0f) * u;
             }
+            bg_t[k] = -T[k] * bg_grad;
             my_max = max(my_max, last_contributor[k]);
         }
     }
@@ -647,9 +650,9 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                     dot = __builtin_fmaf(f[c], grad[k][c], dot);
                     vals[FB + c] = __builtin_fmaf(aT, grad[k][c], vals[FB + c]);
                 }
-                S[k] = __builtin_fmaf(la, last_dot[k], (1.0f - la) * S[k]);
-                last_dot[k] = dot;
-                const float grad_alpha = __builtin_fmaf(dot - S[k], T[k], -(T_final[k] * inv) * bg_grad[k]);
+                S[k] = __builtin_fmaf(la, last_e[k], S[k]);
+                last_e[k] = dot - S[k];
+                const float grad_alpha = __builtin_fmaf(last_e[k], T[k], bg_t[k] * inv);
                 last_alpha[k] = alpha;
                 // dL/dG = o dL/dalpha; the centre gradient is
                 // -w (a dx + b dy, c dy + b dx) and the conic gradient
