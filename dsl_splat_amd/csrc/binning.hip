@@ -737,12 +737,23 @@ __global__ __launch_bounds__(kBinThreads) void order_counts_kernel(const uint64_
     if (threadIdx.x == 0) block_pairs[blockIdx.x] = total;
 }
 
-// *out = sum of values[0, count) (one block).
+// *out = sum of values[0, count) (one block).  Eight loads per thread are in
+// flight at a time: the kernel is latency-bound (tens of thousands of values).
 __global__ __launch_bounds__(1024) void sum_i64_kernel(const int64_t* __restrict__ values, int64_t count,
                                                        int64_t* __restrict__ out) {
     __shared__ int64_t s_wave[1024 / 64];
+    constexpr int U = 8;
     int64_t v = 0;
-    for (int64_t i = threadIdx.x; i < count; i += 1024) v += values[i];
+    for (int64_t i0 = threadIdx.x; i0 < count; i0 += 1024 * U) {
+        int64_t x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + (int64_t)u * 1024;
+            x[u] = i < count ? values[i] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) v += x[u];
+    }
     int64_t total;
     block_exclusive_scan<1024>(v, s_wave, total);
     if (threadIdx.x == 0) *out = total;

@@ -23,7 +23,7 @@ from .autograd import Frame, Rasterize
 from .projection import project_views
 from ..cameras import validate_camera_options
 from ..inputs import batch_item, normalize_inputs
-from ..splatting.binning import check_pair_counts, finish_binning, order_rows, validate_tile_mode
+from ..splatting.binning import launch_bin_rows, order_rows, prepare_bin_rows, validate_tile_mode
 from ..splatting.cameras import launch_prepare, raise_camera_errors
 from ..statistics import StatisticsRequest, prepare_statistics
 from ..training import prepare_training_metadata
@@ -79,7 +79,12 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
                    sh, sh_degree, background, tile_mode="radius") -> Frame:
     """Camera rows, fused projection, depth order, one synchronisation, binning."""
     with_centers = sh_degree is not None and sh_degree > 0
-    full, inverse, centers, errors = launch_prepare(viewmats, Ks, width, height, with_centers)
+    # One int64 status buffer read back once: [group pairs, tile pairs] and
+    # then the cameras' int32 status codes.
+    cameras = viewmats.numel() // 16
+    status = torch.empty(2 + (cameras + 1) // 2, dtype=torch.int64, device=viewmats.device)
+    camera_status = status[2:].view(torch.int32)[:cameras]
+    full, inverse, centers, _ = launch_prepare(viewmats, Ks, width, height, with_centers, errors=camera_status)
     state = project_views(
         means, quats, scales, opacities, viewmats, full, Ks, width, height, near, far, radius_clip,
         sh=sh if sh_degree is not None else None, sh_degree=sh_degree or 0,
@@ -88,18 +93,21 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     # The depth ordering computes every row's footprint in the chosen mode
     # once; it also leaves the mode's tile counts in state.tile_counts (the
     # projection counted radius squares).
-    order, offsets, totals = order_rows(state.centers, state.radii, state.depths, width, height,
-                                        conics=state.conics, tile_mode=tile_mode,
-                                        tiles_out=None if tile_mode == "radius" else state.tile_counts)
-    host = torch.cat([errors.to(torch.int64), totals]).cpu().tolist()
-    raise_camera_errors(host[:-2])
-    group_pairs, count = int(host[-2]), int(host[-1])
-    check_pair_counts(group_pairs, count)
-    bins = finish_binning(state.centers, state.radii, order, offsets, group_pairs, count, state.depths, width,
-                          height, conics=state.conics, tile_mode=tile_mode)
+    order, offsets, _ = order_rows(state.centers, state.radii, state.depths, width, height,
+                                   conics=state.conics, tile_mode=tile_mode,
+                                   tiles_out=None if tile_mode == "radius" else state.tile_counts,
+                                   totals=status[:2])
+    # Everything the binning launch needs besides the totals is prepared
+    # while the device works on the depth order.
+    launch = prepare_bin_rows(state.centers, state.radii, order, offsets, width, height, conics=state.conics,
+                              tile_mode=tile_mode)
+    host = status.cpu()
+    raise_camera_errors(host[2:].view(torch.int32)[:cameras].tolist())
+    group_pairs, count = host[:2].tolist()
+    ranges, ids = launch_bin_rows(launch, group_pairs, count)
     return Frame(
         width, height, Ks.detach(), full, inverse if with_centers else None, centers if with_centers else None,
-        state, bins["ranges"], bins["point_list"], count, sh_degree, background,
+        state, ranges, ids, count, sh_degree, background,
     )
 
 

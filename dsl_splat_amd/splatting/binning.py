@@ -14,6 +14,7 @@ binning.
 """
 
 import ctypes
+from dataclasses import dataclass
 
 import torch
 from torch import Tensor
@@ -83,14 +84,15 @@ def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tenso
 @torch.no_grad()
 def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, height: int, *,
                conics: Tensor | None = None, tile_mode="radius",
-               tiles_out: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+               tiles_out: Tensor | None = None, totals: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """Depth order of the (views, N) rows.
 
     Returns (ordered row records with 2*rows storage -- followed, for
     AccuTile, by the rows' compact footprints, 32 bytes each --, inclusive
     group offsets, totals = [group pairs, tile pairs]), all left on the
     device.  ``tiles_out`` (int32, views*N), if given, receives every row's
-    tile count in ``tile_mode``."""
+    tile count in ``tile_mode``; ``totals`` (contiguous int64, 2), if given,
+    receives the totals."""
     mode = _mode(tile_mode, conics)
     device = radii.device
     views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
@@ -98,7 +100,10 @@ def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, heigh
     accu = mode == abi.TILE_MODES["accutile"]
     order = torch.empty(2 * rows + (4 * rows if accu else 0), dtype=torch.int64, device=device)
     offsets = torch.empty(rows, dtype=torch.int32, device=device)
-    totals = torch.empty(2, dtype=torch.int64, device=device)
+    if totals is None:
+        totals = torch.empty(2, dtype=torch.int64, device=device)
+    elif totals.dtype != torch.int64 or not totals.is_contiguous() or totals.numel() != 2:
+        raise ValueError("totals must be a contiguous int64 tensor of two entries")
     a = abi.OrderArgs()
     a.n, a.views, a.width, a.height = n, views, width, height
     depths, centers, radii = depths.contiguous(), centers.contiguous(), radii.contiguous()
@@ -124,25 +129,29 @@ def check_pair_counts(group_pairs: int, tile_pairs: int) -> None:
         raise OverflowError(f"{tile_pairs} tile pairs exceed the int32 offsets of the binning stage")
 
 
+@dataclass(slots=True)
+class BinLaunch:
+    """Arguments of gs3d_bin_rows that do not depend on the totals, built
+    while the device still works on the depth order; ``inputs`` keeps the
+    tensors behind the pointers alive."""
+    args: abi.BinArgs
+    ranges: Tensor
+    inputs: tuple
+
+
 @torch.no_grad()
-def bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, group_pairs: int, tile_pairs: int,
-             width: int, height: int, *, conics: Tensor | None = None,
-             tile_mode="radius") -> tuple[Tensor, Tensor]:
-    """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs)
-    of rows ordered by ``order_rows`` (same conics and tile mode)."""
+def prepare_bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, width: int, height: int, *,
+                     conics: Tensor | None = None, tile_mode="radius") -> BinLaunch:
     mode = _mode(tile_mode, conics)
     device = order.device
     views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
-    check_pair_counts(group_pairs, tile_pairs)
     ranges = torch.empty((tile_count(width, height, views), 2), dtype=torch.int32, device=device)
-    ids = torch.empty(tile_pairs, dtype=torch.int32, device=device)
     centers, radii = centers.contiguous(), radii.contiguous()
     a = abi.BinArgs()
     a.n, a.views, a.width, a.height = n, views, width, height
     a.centers, a.radii = native.ptr(centers), native.ptr(radii)
     a.order, a.group_offsets = native.ptr(order), native.ptr(offsets)
-    a.group_pairs, a.tile_pairs = group_pairs, tile_pairs
-    a.ranges, a.ids = native.ptr(ranges), native.ptr(ids)
+    a.ranges = native.ptr(ranges)
     a.tile_mode = mode
     if mode:
         conics = conics.contiguous()
@@ -151,9 +160,31 @@ def bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, gro
         if order.numel() < 6 * views * n:
             raise ValueError("AccuTile binning needs the order returned by order_rows in the same mode")
         a.footprints = native.ptr(order, 2 * views * n)
-    scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, views, width, height, mode), device)
+    return BinLaunch(a, ranges, (centers, radii, order, offsets, conics))
+
+
+@torch.no_grad()
+def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int) -> tuple[Tensor, Tensor]:
+    """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs)."""
+    check_pair_counts(group_pairs, tile_pairs)
+    a, device = launch.args, launch.ranges.device
+    ids = torch.empty(tile_pairs, dtype=torch.int32, device=device)
+    a.group_pairs, a.tile_pairs = group_pairs, tile_pairs
+    a.ids = native.ptr(ids)
+    scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, a.views, a.width, a.height,
+                                    a.tile_mode), device)
     native.call("gs3d_bin_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
-    return ranges, ids
+    return launch.ranges, ids
+
+
+def bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, group_pairs: int, tile_pairs: int,
+             width: int, height: int, *, conics: Tensor | None = None,
+             tile_mode="radius") -> tuple[Tensor, Tensor]:
+    """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs)
+    of rows ordered by ``order_rows`` (same conics and tile mode)."""
+    check_pair_counts(group_pairs, tile_pairs)
+    launch = prepare_bin_rows(centers, radii, order, offsets, width, height, conics=conics, tile_mode=tile_mode)
+    return launch_bin_rows(launch, group_pairs, tile_pairs)
 
 
 @torch.no_grad()
