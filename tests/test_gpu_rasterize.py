@@ -177,23 +177,32 @@ def test_empty_and_culled_inputs():
     assert res0.features.shape == (1, 48, 64, 3) and torch.all(res0.alpha == 0)
 
 
-def test_camera_errors_raise():
+@pytest.mark.parametrize("cameras,bad", [(1, 0), (3, 2), (4, 1)])
+def test_camera_errors_raise(cameras, bad):
+    # The status codes of every camera travel with the pair totals in one
+    # read-back; an error on any camera (odd and even counts) must surface.
     scene = synthetic.make_scene("small", n=100, width=32, height=32, seed=51).to(DEV)
-    K = scene.Ks.clone()
-    K[0, 0, 1] = 0.1
+    rows = torch.arange(cameras, device=DEV) % scene.viewmats.shape[0]
+    viewmats, Ks = scene.viewmats[rows].contiguous(), scene.Ks[rows].contiguous()
+    K = Ks.clone()
+    K[bad, 0, 1] = 0.1
     with pytest.raises(NotImplementedError):
-        gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats, K, 32, 32,
+        gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, viewmats, K, 32, 32,
                        features=scene.features)
-    K = scene.Ks.clone()
-    K[0, 0, 0] = float("nan")
+    K = Ks.clone()
+    K[bad, 0, 0] = float("nan")
     with pytest.raises(ValueError):
-        gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats, K, 32, 32,
+        gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, viewmats, K, 32, 32,
                        features=scene.features)
-    V = scene.viewmats.clone()
-    V[0, 2] = V[0, 1]
+    # Valid cameras still render after the failures.
+    res = gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, viewmats, Ks, 32, 32,
+                         features=scene.features)
+    assert res.features.shape[0] == cameras and torch.isfinite(res.features).all()
+    V = viewmats.clone()
+    V[bad, 2] = V[bad, 1]
     sh = torch.zeros((100, 4, 3), device=DEV)
     with pytest.raises(torch.linalg.LinAlgError):
-        gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, V, scene.Ks, 32, 32, sh_coeffs=sh)
+        gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, V, Ks, 32, 32, sh_coeffs=sh)
 
 
 def _leaf(t):
