@@ -290,13 +290,16 @@ constexpr int kRadix = 256;
 template <class K>
 GS3D_DEV uint32_t digit_of(K key, int shift, uint32_t mask) { return (uint32_t)(key >> shift) & mask; }
 
-template <class K>
+// RB: digit width in bits (8 for multi-pass sorts; 10 for a one-pass sort of
+// keys of at most 10 bits).
+template <class K, int RB = 8>
 __global__ __launch_bounds__(kSortThreads) void sort_histogram_kernel(const K* __restrict__ keys, int64_t count,
                                                                       int shift, uint32_t mask,
                                                                       uint32_t* __restrict__ counts, int64_t tiles) {
-    __shared__ uint32_t s_hist[kSortThreads / 64][kRadix];
+    constexpr int R = 1 << RB;
+    __shared__ uint32_t s_hist[kSortThreads / 64][R];
     const int wave = threadIdx.x >> 6;
-    for (int e = threadIdx.x; e < (kSortThreads / 64) * kRadix; e += kSortThreads) (&s_hist[0][0])[e] = 0;
+    for (int e = threadIdx.x; e < (kSortThreads / 64) * R; e += kSortThreads) (&s_hist[0][0])[e] = 0;
     const int64_t base = (int64_t)blockIdx.x * kSortTile + wave * (kSortTile / 4) + lane_id();
     K key[kSortItems];
 #pragma unroll
@@ -311,7 +314,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_kernel(const K* _
         if (idx < count) atomicAdd(&s_hist[wave][digit_of(key[k], shift, mask)], 1u);
     }
     __syncthreads();
-    for (int d = threadIdx.x; d < kRadix; d += kSortThreads) {
+    for (int d = threadIdx.x; d < R; d += kSortThreads) {
         uint32_t sum = 0;
 #pragma unroll
         for (int w = 0; w < kSortThreads / 64; ++w) sum += s_hist[w][d];
@@ -321,18 +324,20 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_kernel(const K* _
 
 // VALS = false sorts keys alone: no value loads, stores or LDS staging, which
 // leaves room for one more block per CU.
-template <class K, class V, bool VALS>
+template <class K, class V, bool VALS, int RB = 8>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
     V* __restrict__ vals_out, int64_t count, int shift, uint32_t mask, int bits,
     const int32_t* __restrict__ scanned, int64_t tiles) {
+    constexpr int R = 1 << RB;
+    static_assert(R % kSortThreads == 0, "whole digits per thread");
     __shared__ K s_keys[kSortTile];
     __shared__ V s_vals[VALS ? kSortTile : 1];
-    __shared__ uint32_t s_wcnt[kSortThreads / 64][kRadix];
-    __shared__ int32_t s_gbase[kRadix];
+    __shared__ uint32_t s_wcnt[kSortThreads / 64][R];
+    __shared__ int32_t s_gbase[R];
     __shared__ uint32_t s_scan_wave[kSortThreads / 64];
     const int wave = threadIdx.x >> 6, lane = lane_id();
-    for (int e = threadIdx.x; e < (kSortThreads / 64) * kRadix; e += kSortThreads) (&s_wcnt[0][0])[e] = 0;
+    for (int e = threadIdx.x; e < (kSortThreads / 64) * R; e += kSortThreads) (&s_wcnt[0][0])[e] = 0;
     const int64_t tile_base = (int64_t)blockIdx.x * kSortTile;
     const int64_t valid_count = min((int64_t)kSortTile, count - tile_base);
     K key[kSortItems];
@@ -374,24 +379,31 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     __syncthreads();
     {
         // Start of digit d in this tile's digit-sorted order, then each
-        // wavefront's offset within the digit (kSortThreads == kRadix).
-        const int d = threadIdx.x;
-        uint32_t c[kSortThreads / 64];
+        // wavefront's offset within the digit; thread t owns the M
+        // consecutive digits from M t.
+        constexpr int M = R / kSortThreads;
+        uint32_t c[M][kSortThreads / 64];
         uint32_t tot = 0;
 #pragma unroll
-        for (int w = 0; w < kSortThreads / 64; ++w) {
-            c[w] = s_wcnt[w][d];
-            tot += c[w];
+        for (int i = 0; i < M; ++i) {
+#pragma unroll
+            for (int w = 0; w < kSortThreads / 64; ++w) {
+                c[i][w] = s_wcnt[w][threadIdx.x * M + i];
+                tot += c[i][w];
+            }
         }
         uint32_t block_total;
-        const uint32_t start = block_exclusive_scan<kSortThreads>(tot, s_scan_wave, block_total);
-        uint32_t run = start;
+        uint32_t run = block_exclusive_scan<kSortThreads>(tot, s_scan_wave, block_total);
 #pragma unroll
-        for (int w = 0; w < kSortThreads / 64; ++w) {
-            s_wcnt[w][d] = run;
-            run += c[w];
+        for (int i = 0; i < M; ++i) {
+            const int d = threadIdx.x * M + i;
+            s_gbase[d] = scanned[(int64_t)d * tiles + blockIdx.x] - (int32_t)run;
+#pragma unroll
+            for (int w = 0; w < kSortThreads / 64; ++w) {
+                s_wcnt[w][d] = run;
+                run += c[i][w];
+            }
         }
-        s_gbase[d] = scanned[(int64_t)d * tiles + blockIdx.x] - (int32_t)start;
     }
     __syncthreads();
 #pragma unroll
@@ -425,9 +437,9 @@ struct SortScratch {
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-inline size_t sort_scratch_bytes(int64_t count, SortScratch* out, void* base) {
+inline size_t sort_scratch_bytes(int64_t count, SortScratch* out, void* base, int radix_bits = 8) {
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
-    const int64_t entries = tiles * kRadix;
+    const int64_t entries = tiles << radix_bits;
     const size_t a = align256((size_t)entries * 4);
     const size_t b = align256((size_t)entries * 4);
     const size_t c = scan_partials_bytes(entries);
@@ -481,6 +493,84 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
         }
     }
     return launch_status("radix sort");
+}
+
+// Histogram of TPB consecutive sort tiles per block, for wide digits: each
+// digit's TPB counts are consecutive in the [digit][tile] layout, so a block
+// writes runs of TPB words instead of one scattered word per digit.  One
+// LDS histogram per tile (pitch R + 1: the transposed read is conflict-free).
+template <class K, int RB, int TPB>
+__global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(const K* __restrict__ keys, int64_t count,
+                                                                            int shift, uint32_t mask,
+                                                                            uint32_t* __restrict__ counts,
+                                                                            int64_t tiles) {
+    constexpr int R = 1 << RB, P = R + 1;
+    __shared__ uint32_t s_hist[TPB * P];
+    for (int e = threadIdx.x; e < TPB * P; e += kSortThreads) s_hist[e] = 0;
+    __syncthreads();
+    const int64_t t0 = (int64_t)blockIdx.x * TPB;
+    for (int tt = 0; tt < TPB; ++tt) {
+        const int64_t base = (t0 + tt) * kSortTile;
+        if (base >= count) break;
+        K key[kSortItems];
+#pragma unroll
+        for (int k = 0; k < kSortItems; ++k) {
+            const int64_t idx = base + k * kSortThreads + threadIdx.x;
+            key[k] = idx < count ? keys[idx] : K(0);
+        }
+#pragma unroll
+        for (int k = 0; k < kSortItems; ++k) {
+            const int64_t idx = base + k * kSortThreads + threadIdx.x;
+            if (idx < count) atomicAdd(&s_hist[tt * P + digit_of(key[k], shift, mask)], 1u);
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < TPB * R; e += kSortThreads) {
+        const int d = e / TPB, tt = e - d * TPB;
+        const int64_t t = t0 + tt;
+        if (t < tiles) counts[(int64_t)d * tiles + t] = s_hist[tt * P + d];
+    }
+}
+
+// Start and end of every digit's run in the output of a one-pass sort: the
+// exclusive scan of the [digit][tile] counts holds each digit's start at
+// tile 0.
+__global__ void digit_ranges_kernel(const int32_t* __restrict__ scanned, int64_t tiles, int64_t count, int digits,
+                                    int ranges_count, int32_t* __restrict__ ranges) {
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= ranges_count) return;
+    const int32_t start = scanned[(int64_t)d * tiles];
+    const int32_t end = d + 1 < digits ? scanned[(int64_t)(d + 1) * tiles] : (int32_t)count;
+    ranges[2 * d] = start;
+    ranges[2 * d + 1] = end;
+}
+
+// Stable keys-only sort of keys[0:count) on bits [0, end_bit), end_bit <=
+// kOnePassBits, in one 10-bit pass: the result is written to
+// keys[count:2count) and ranges[2d], ranges[2d + 1] (d < ranges_count)
+// receive the run of key value d.  Scratch as sort_scratch_bytes(count, ...,
+// kOnePassBits).
+constexpr int kOnePassBits = 10;
+
+template <class K>
+int run_sort_once(K* keys, int64_t count, int end_bit, void* scratch, int ranges_count, int32_t* ranges,
+                  hipStream_t s) {
+    constexpr int RB = kOnePassBits;
+    SortScratch sc;
+    sort_scratch_bytes(count, &sc, scratch, RB);
+    const int64_t tiles = (count + kSortTile - 1) / kSortTile;
+    const uint32_t mask = (1u << end_bit) - 1u;
+    constexpr int TPB = 8;
+    hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
+                       dim3(kSortThreads), 0, s, keys, count, 0, mask, sc.counts, tiles);
+    const int status = run_scan<uint32_t, false>(sc.counts, tiles << RB, sc.scanned, nullptr, sc.scan_scratch, s);
+    if (status != GS3D_OK) return status;
+    hipLaunchKernelGGL((sort_scatter_kernel<K, int32_t, false, RB>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
+                       keys, (const int32_t*)nullptr, keys + count, (int32_t*)nullptr, count, 0, mask, end_bit,
+                       sc.scanned, tiles);
+    hipLaunchKernelGGL(digit_ranges_kernel, dim3((unsigned)((ranges_count + 255) / 256)), dim3(256), 0, s,
+                       sc.scanned, tiles, count, 1 << RB, ranges_count, ranges);
+    return launch_status("one-pass radix sort");
 }
 
 // ---------------------------------------------------------------------------
@@ -1264,7 +1354,8 @@ inline size_t bin_scratch_bytes(int64_t group_pairs, int64_t groups, int64_t til
     const int64_t chunks = max_chunks_of(group_pairs, groups);
     size_t sizes[11];
     sizes[0] = align256((size_t)group_pairs * 2 * sizeof(uint64_t));
-    sizes[1] = align256(sort_scratch_bytes(group_pairs, nullptr, nullptr));
+    sizes[1] = align256(sort_scratch_bytes(group_pairs, nullptr, nullptr,
+                                           groups <= (int64_t)1 << kOnePassBits ? kOnePassBits : 8));
     sizes[2] = align256((size_t)groups * 2 * sizeof(int32_t));
     sizes[3] = align256((size_t)(groups + 1) * sizeof(int32_t));
     sizes[4] = align256((size_t)chunks * sizeof(int32_t));
@@ -1501,6 +1592,7 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
     const gs3d::RowGeometry geo{a.centers, a.conics, a.radii, a.tile_mode};
     const dim3 egrid(gs3d::blocks_for(rows, gs3d::kBinThreads)), eblock(gs3d::kBinThreads);
     const int group_bits = gs3d::bit_length(groups - 1 > 0 ? groups - 1 : 1);
+    const uint64_t* items = sc.items;  // the sorted group items
     int status;
     if (accu) {
         if (!a.footprints || (reinterpret_cast<uintptr_t>(a.footprints) & 15)) return GS3D_ERR_ARGUMENT;
@@ -1519,23 +1611,31 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
         else
             hipLaunchKernelGGL(gs3d::group_emit_kernel<false>, egrid, eblock, 0, s, a.order, a.group_offsets, rows, geo,
                                a.n, d, S, sc.items);
-        status = gs3d::run_sort<uint64_t, int32_t>(sc.items, nullptr, S, group_bits, sc.sort, s);
+        if (group_bits <= gs3d::kOnePassBits) {
+            // One 10-bit pass; its digit scan gives the group ranges.
+            status = gs3d::run_sort_once<uint64_t>(sc.items, S, group_bits, sc.sort, (int)groups, sc.granges, s);
+            items = sc.items + S;
+        } else {
+            status = gs3d::run_sort<uint64_t, int32_t>(sc.items, nullptr, S, group_bits, sc.sort, s);
+        }
     }
     if (status != GS3D_OK) return status;
-    gs3d::fill_u32(reinterpret_cast<uint32_t*>(sc.granges), 2 * groups, 0u, s);
-    hipLaunchKernelGGL(gs3d::tile_ranges_kernel<uint64_t>, dim3(gs3d::blocks_for(S, 256)), dim3(256), 0, s, sc.items,
-                       S, 0, gs3d::kGroupMask, sc.granges, groups);
+    if (items == sc.items) {
+        gs3d::fill_u32(reinterpret_cast<uint32_t*>(sc.granges), 2 * groups, 0u, s);
+        hipLaunchKernelGGL(gs3d::tile_ranges_kernel<uint64_t>, dim3(gs3d::blocks_for(S, 256)), dim3(256), 0, s, items,
+                           S, 0, gs3d::kGroupMask, sc.granges, groups);
+    }
     hipLaunchKernelGGL(gs3d::chunk_base_kernel, dim3(1), dim3(1024), 0, s, sc.granges, (int)groups, sc.chunk_base);
     hipLaunchKernelGGL(gs3d::chunk_group_kernel, dim3(gs3d::blocks_for(chunks, 256)), dim3(256), 0, s,
                        sc.chunk_base, (int)groups, chunks, sc.chunk_group);
     gs3d::fill_u32(sc.counts, 64 * chunks, 0u, s);
     const dim3 pass_grid(gs3d::blocks_for(chunks, gs3d::kBinWaves));
     if (accu)
-        hipLaunchKernelGGL((gs3d::group_pass_kernel<false, true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
+        hipLaunchKernelGGL((gs3d::group_pass_kernel<false, true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,
                            sc.masks, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts,
                            (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0);
     else
-        hipLaunchKernelGGL((gs3d::group_pass_kernel<false, false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items,
+        hipLaunchKernelGGL((gs3d::group_pass_kernel<false, false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,
                            (const uint64_t*)nullptr, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d,
                            sc.counts, (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0);
     status = gs3d::run_scan<uint32_t, false>(sc.counts, 64 * chunks, sc.scanned, nullptr, sc.scan, s);
@@ -1549,7 +1649,7 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
     // Buffer stores address the id list with 32-bit byte offsets.
     const bool buf = a.tile_pairs <= (int64_t)(0xFFFFFFFFu / 4);
 #define GS3D_WRITE_PASS(M, B)                                                                                      \
-    hipLaunchKernelGGL((gs3d::group_pass_kernel<true, M, B>), pass_grid, dim3(gs3d::kBinThreads), 0, s, sc.items, \
+    hipLaunchKernelGGL((gs3d::group_pass_kernel<true, M, B>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,     \
                        M ? (const uint64_t*)sc.masks : nullptr, sc.granges, sc.chunk_base, sc.chunk_group,        \
                        (int)groups, chunks, d, sc.counts, sc.scanned, sc.starts, a.ids, a.tile_pairs)
     if (accu) {
