@@ -175,7 +175,8 @@ def stage_timings(scene, reps):
                 tiles = binning.tile_count(scene.width, scene.height, views)
                 groups = views * (((scene.width + 15) // 16 + 7) // 8) * (((scene.height + 15) // 16 + 7) // 8)
                 info = dict(pairs=count, group_pairs=group_pairs, groups=groups, tiles=tiles,
-                            group_passes=math.ceil(int(groups - 1).bit_length() / 8), rows=views * n,
+                            group_passes=1 if groups <= 1024 else math.ceil(int(groups - 1).bit_length() / 8),
+                            rows=views * n,
                             visible=int((st.radii > 0).sum()),
                             mean_contributors=float(out.contributors.float().mean()))
                 continue  # warm-up repetition
@@ -240,10 +241,12 @@ def stage_timings(scene, reps):
         # over (key, record) (24 per pass), group counts (record 8 in, count 4 out), inclusive scan
         # (4 in, 4 out)
         "order": R * (28 + 4 * 24 + 12 + 8),
-        # items: records and offsets in (12 B/row), items out (8 B/item); group sort (16 B/item/pass);
-        # group ranges, count and write passes read items (3 x 8 B); ids out (4 B/pair); tile
-        # totals/starts/ranges (16 B/tile)
-        "bin": R * 12 + S * (8 + 16 * info["group_passes"] + 24) + M * 4 + T * 16,
+        # items: records and offsets in (12 B/row), items out (8 B/item); group sort (16 B/item/pass,
+        # one 10-bit pass up to 1024 groups, whose digit scan gives the group ranges, else 8-bit
+        # passes and a range search over the items, 8 B/item); count and write passes read items
+        # (2 x 8 B); ids out (4 B/pair); tile totals/starts/ranges (16 B/tile)
+        "bin": R * 12 + S * (8 + 16 * info["group_passes"] + (16 if info["group_passes"] == 1 else 24))
+               + M * 4 + T * 16,
         # params 44 + SH 4K*3 in, per view radii 4 + centre/conic grads 24 (+ colour grads 12) in;
         # grads 44 + SH out
         "project_bwd": n * 88 + 2 * sh_in + views * n * (28 + (12 if sh is not None else 0)),
