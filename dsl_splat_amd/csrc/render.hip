@@ -21,6 +21,18 @@
 // instruction adds them, one entry per lane, instead of one atomic per entry
 // and pixel as in the reference.  Only batches below the largest last contributor of the
 // tile are visited.
+//
+// Channel windows: the reference specialises its kernels on any channel count
+// D' (gs3d/render.py:36-38, :211-213).  A launch here blends a window of at
+// most 64 channels [c0, c0 + CH) of the D'-channel vector; wider vectors run
+// one launch per window.  Forward windows are independent (the blend weights
+// do not depend on the channels); window 0 writes the transmittance and last
+// contributors.  Backward: the geometry launch (window 0) owns the centre,
+// conic and opacity gradients, which need the dot product of the Gaussian's
+// full channel vector with the pixel's upstream gradient; its window holds at
+// most 64 - 8 channels, so its gradient entries fit the 64 lanes of one
+// wavefront sum, and channels beyond it enter the dot product from global
+// memory.  Further windows add only their channels' feature gradients.
 #include "common.hpp"
 
 #ifndef GS3D_FWD_PIX
@@ -41,6 +53,12 @@ template <int CH>
 struct Batch {
     static constexpr int size = CH <= 36 ? 256 : 128;
 };
+
+// Channels of the geometry launch's window: with the 8 geometric entries
+// (absolute gradients included) they fill one 64-entry wavefront sum.
+constexpr int kGeomWindow = 56;
+// Channels of a forward window and of a further backward window.
+constexpr int kWindow = 64;
 
 // Pixels per lane for a channel count (wide vectors keep one pixel per lane
 // to bound register use).
@@ -175,10 +193,11 @@ GS3D_DEV uint32_t strip_mask(float2 xy, float4 con, float cut, int x0, int y0) {
     return m;
 }
 
-// Stage one Gaussian's centre, conic, cutoff, strip mask and channel vector.
+// Stage one Gaussian's centre, conic, cutoff, strip mask and the channels
+// [c0, c0 + CH) of its channel vector (zero beyond D').
 template <int CH, int PIX>
-GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32_t g, int slot, float2* s_xy,
-                             float4* s_con, float* s_cut, uint32_t* s_mask, float* s_feat) {
+GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32_t g, int slot, int c0,
+                             float2* s_xy, float4* s_con, float* s_cut, uint32_t* s_mask, float* s_feat) {
     const int view = t.view;
     const int64_t row = (int64_t)view * a.n + g;
     const float2 xy = reinterpret_cast<const float2*>(a.centers)[row];
@@ -196,12 +215,13 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32
     float v[CH];
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
+        const int gc = c0 + c;
         float x = 0.0f;
-        if (c < F)
-            x = f[c];
-        else if (c < F + E)
-            x = e[c - F];
-        else if (c == F + E && a.one_tail)
+        if (gc < F)
+            x = f[gc];
+        else if (gc < F + E)
+            x = e[gc - F];
+        else if (gc == F + E && a.one_tail)
             x = 1.0f;
         v[c] = x;
     }
@@ -294,7 +314,7 @@ GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, int view, int
 // instead of 5: 1.180 -> 1.130 ms on RGB); wider channel vectors keep the
 // registers they need.
 template <int CH, int PIX, bool STATS>
-__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 8 ? 6 : 1))) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st) {
+__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 8 ? 6 : 1))) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st, int c0) {
     constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
     __shared__ float2 s_xy[B];
@@ -340,7 +360,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
             const int idx = begin + e;
             if (idx < t.last) {
                 const int32_t g = a.ids[idx];
-                stage_gaussian<CH, PIX>(a, t, g, e, s_xy, s_con, s_cut, s_mask, s_feat);
+                stage_gaussian<CH, PIX>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
                 if constexpr (STATS) s_id[e] = g;
             }
         }
@@ -456,26 +476,64 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
         const int64_t pix = ((int64_t)t.view * a.height + py[k]) * a.width + px[k];
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            if (c >= D) continue;
-            const float v = __builtin_fmaf(T[k], (bg && c < F) ? bg[c] : 0.0f, color[k][c]);
-            if (c < F)
-                a.image[pix * F + c] = v;
-            else if (c < F + E)
-                a.image_extra[pix * E + (c - F)] = v;
+            const int gc = c0 + c;
+            if (gc >= D) continue;
+            const float v = __builtin_fmaf(T[k], (bg && gc < F) ? bg[gc] : 0.0f, color[k][c]);
+            if (gc < F)
+                a.image[pix * F + gc] = v;
+            else if (gc < F + E)
+                a.image_extra[pix * E + (gc - F)] = v;
             else
                 a.image_alpha[pix] = v;
         }
-        a.final_t[pix] = T[k];
-        a.contributors[pix] = last_contributor[k];
+        if (c0 == 0) {
+            a.final_t[pix] = T[k];
+            a.contributors[pix] = last_contributor[k];
+        }
     }
+}
+
+// Channels [c_begin, D) of Gaussian g's vector dotted with the upstream
+// gradient of pixel (px, py) (geometry launch of a vector wider than its
+// window: the channels beyond the window come from global memory).
+GS3D_DEV float rest_dot(const gs3d_render_bwd_args& b, int view, int64_t g, float px, float py, int c_begin) {
+    const gs3d_render_args& a = b.fwd;
+    const int64_t pix = ((int64_t)view * a.height + (int)py) * a.width + (int)px;
+    const int F = a.feat_channels, E = a.extra_channels;
+    float dot = 0.0f;
+    int c = c_begin;
+    if (c < F) {
+        const float* f = a.features + view * a.feat_view_stride + g * a.feat_stride;
+        const float* u = b.upstream ? b.upstream + pix * b.upstream_stride : nullptr;
+        for (; c < F; ++c) dot = __builtin_fmaf(f[c], u ? u[c] : 0.0f, dot);
+    }
+    if (c < F + E) {
+        const float* f = a.extra + view * a.extra_view_stride + g * a.extra_stride;
+        const float* u = b.upstream_extra ? b.upstream_extra + pix * b.upstream_extra_stride : nullptr;
+        for (; c < F + E; ++c) dot = __builtin_fmaf(f[c - F], u ? u[c - F] : 0.0f, dot);
+    }
+    if (c == F + E && a.one_tail && b.upstream_alpha) dot += b.upstream_alpha[pix * b.upstream_alpha_stride];
+    return dot;
 }
 
 // Four channels fit 80 VGPRs, six wavefronts per SIMD (the LDS limit of a
 // 13 KiB block); with absolute gradients the uncapped allocation is 83.
-template <int CH, bool ABS, int PIX>
-__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 4 ? 6 : 1))) void render_bwd_kernel(gs3d_render_bwd_args b) {
+//
+// GEOM: the geometry launch (window 0, c0 = 0): centre, conic and opacity
+// gradients (+ absolute centre gradients with ABS) and the window's feature
+// gradients; channels from CH on, if any, enter the alpha gradient through
+// rest_dot.  !GEOM: a further window [c0, c0 + CH), feature gradients only.
+template <int CH, bool ABS, int PIX, bool GEOM>
+__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 4 ? 6 : 1))) void render_bwd_kernel(gs3d_render_bwd_args b, int c0) {
     constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
+    // Gradient entries per Gaussian: [centre xy, conic abc, opacity, |centre| xy]
+    // for the geometry launch, then the window's channels; one wavefront sum
+    // covers at most 64.
+    constexpr int FB = GEOM ? (ABS ? 8 : 6) : 0;
+    constexpr int NV = FB + CH;
+    static_assert(NV <= 64, "one wavefront sum holds at most 64 gradient entries");
+    constexpr int R = (NV + 3) / 4;
     __shared__ float2 s_xy[B];
     __shared__ float4 s_con[B];
     __shared__ float s_cut[B];
@@ -487,6 +545,8 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     const TileInfo t = tile_info(a);
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     const int Dg = D - (a.one_tail ? 1 : 0);
+    // Only the widest geometry window can be followed by further channels.
+    const bool rest = GEOM && CH == kGeomWindow && D > CH;  // wave-uniform
     const int lane = lane_id(), wave = threadIdx.x >> 6;
     // Per pixel: S = sum_c accum_c * grad_c, the colour accumulated behind
     // the current Gaussian dotted with the upstream gradient.  With
@@ -523,19 +583,25 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
             const int F = a.feat_channels, E = a.extra_channels;
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
-                if (c >= D) continue;
+                const int gc = c0 + c;
+                if (gc >= D) continue;
                 float u = 0.0f;
-                if (c < F) {
-                    if (b.upstream) u = b.upstream[pix * b.upstream_stride + c];
-                } else if (c < F + E) {
-                    if (b.upstream_extra) u = b.upstream_extra[pix * b.upstream_extra_stride + (c - F)];
+                if (gc < F) {
+                    if (b.upstream) u = b.upstream[pix * b.upstream_stride + gc];
+                } else if (gc < F + E) {
+                    if (b.upstream_extra) u = b.upstream_extra[pix * b.upstream_extra_stride + (gc - F)];
                 } else if (b.upstream_alpha) {
                     u = b.upstream_alpha[pix * b.upstream_alpha_stride];
                 }
                 grad[k][c] = u;
-                bg_grad += ((bg && c < F) ? bg[c] : 0.0f) * u;
+                bg_grad += ((bg && gc < F) ? bg[gc] : 0.0f) * u;
             }
-            bg_t[k] = -T[k] * bg_grad;
+            if (GEOM) {
+                // Background channels beyond the window (geometry launch only).
+                if (bg && b.upstream)
+                    for (int gc = CH; gc < F; ++gc) bg_grad += bg[gc] * b.upstream[pix * b.upstream_stride + gc];
+                bg_t[k] = -T[k] * bg_grad;
+            }
             my_max = max(my_max, last_contributor[k]);
         }
     }
@@ -545,29 +611,28 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     const int max_last = min(s_max_last, t.last - t.first);
     // Gradient entry this lane adds after the wavefront sums (see
     // wave_sum_rows): entry k of Gaussian g lives at dst_base + g * dst_step.
-    constexpr int FB = ABS ? 8 : 6;  // first feature entry
-    constexpr int NV = FB + CH;
-    constexpr int R = (NV + 3) / 4;
     float* dst_base = nullptr;
     int64_t dst_step = 0;
     float dst_scale = 1.0f;
     {
         const int k = wave_sum_rows_value(lane);
-        if (k < 2 || k == 3) dst_scale = -1.0f;
-        if (k == 2 || k == 4) dst_scale = -0.5f;
+        if (GEOM) {
+            if (k < 2 || k == 3) dst_scale = -1.0f;
+            if (k == 2 || k == 4) dst_scale = -0.5f;
+        }
         const int64_t row0 = (int64_t)t.view * a.n;
         if ((lane & 15) >= R || k >= NV) {
-        } else if (k < 2) {
+        } else if (GEOM && k < 2) {
             dst_base = b.grad_centers + row0 * b.grad_centers_stride + k;
             dst_step = b.grad_centers_stride;
-        } else if (k < 6) {
+        } else if (GEOM && k < 6) {
             dst_base = b.grad_conics + row0 * b.grad_conics_stride + (k - 2);
             dst_step = b.grad_conics_stride;
-        } else if (ABS && k < 8) {
+        } else if (GEOM && ABS && k < 8) {
             dst_base = b.abs_centers + row0 * b.abs_stride + (k - 6);
             dst_step = b.abs_stride;
         } else {
-            const int c = k - FB;
+            const int c = c0 + k - FB;
             if (c < a.feat_channels) {
                 if (b.grad_features) {
                     dst_base = b.grad_features + t.view * b.grad_feat_view_stride + c;
@@ -591,18 +656,18 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
             if (p >= 0) {
                 const int32_t g = a.ids[t.first + p];
                 s_id[e] = g;
-                stage_gaussian<CH, PIX>(a, t, g, e, s_xy, s_con, s_cut, s_mask, s_feat);
+                stage_gaussian<CH, PIX>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
             }
         }
         __syncthreads();
         const int cnt = min(B, top);
-        for (int c0 = 0; c0 < cnt; c0 += 64) {
+        for (int c0b = 0; c0b < cnt; c0b += 64) {
           // This wavefront's Gaussians of the next 64 that lie before its
           // pixels' last contributors, in traversal order.
-          const int e = c0 + lane;
+          const int e = c0b + lane;
           uint64_t todo = __ballot(e < cnt && top - 1 - e < wave_last && ((s_mask[min(e, B - 1)] >> wave) & 1u));
           while (todo) {
-            const int j = c0 + __builtin_ctzll(todo);
+            const int j = c0b + __builtin_ctzll(todo);
             todo &= todo - 1;
             const int pos = top - 1 - j;
             // Pixels outside the image have last contributor 0.
@@ -639,42 +704,45 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 // reciprocal (1 - alpha >= 0.01) and fused multiply-adds.
                 const float inv = __builtin_amdgcn_rcpf(1.0f - alpha);
                 T[k] = T[k] * inv;
-                const float la = last_alpha[k], aT = alpha * T[k];
+                const float aT = alpha * T[k];
                 // Every compiled channel slot is processed: slots at or beyond
                 // D hold zero features and zero upstream gradients (no
                 // contribution), and the constant alpha channel's entry has no
                 // destination, so no per-channel branch is needed.
-                float dot = 0.0f;
 #pragma unroll
-                for (int c = 0; c < CH; ++c) {
-                    dot = __builtin_fmaf(f[c], grad[k][c], dot);
-                    vals[FB + c] = __builtin_fmaf(aT, grad[k][c], vals[FB + c]);
+                for (int c = 0; c < CH; ++c) vals[FB + c] = __builtin_fmaf(aT, grad[k][c], vals[FB + c]);
+                if constexpr (GEOM) {
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < CH; ++c) dot = __builtin_fmaf(f[c], grad[k][c], dot);
+                    if (rest) dot += rest_dot(b, t.view, s_id[j], fx[k], fy[k], CH);
+                    const float la = last_alpha[k];
+                    S[k] = __builtin_fmaf(la, last_e[k], S[k]);
+                    last_e[k] = dot - S[k];
+                    const float grad_alpha = __builtin_fmaf(last_e[k], T[k], bg_t[k] * inv);
+                    last_alpha[k] = alpha;
+                    // dL/dG = o dL/dalpha; the centre gradient is
+                    // -w (a dx + b dy, c dy + b dx) and the conic gradient
+                    // -w (dx dx / 2, dx dy, dy dy / 2).
+                    const float w = og * grad_alpha;
+                    const float ux = __builtin_fmaf(con.x, dx, con.y * dy);
+                    const float uy = __builtin_fmaf(con.z, dy, con.y * dx);
+                    if (ABS) {
+                        const float cx = w * ux, cy = w * uy;
+                        vals[0] += cx;
+                        vals[1] += cy;
+                        vals[6] += __builtin_fabsf(cx);
+                        vals[7] += __builtin_fabsf(cy);
+                    } else {
+                        vals[0] = __builtin_fmaf(w, ux, vals[0]);
+                        vals[1] = __builtin_fmaf(w, uy, vals[1]);
+                    }
+                    const float wx = w * dx, wy = w * dy;
+                    vals[2] = __builtin_fmaf(wx, dx, vals[2]);
+                    vals[3] = __builtin_fmaf(wx, dy, vals[3]);
+                    vals[4] = __builtin_fmaf(wy, dy, vals[4]);
+                    vals[5] = __builtin_fmaf(G, grad_alpha, vals[5]);
                 }
-                S[k] = __builtin_fmaf(la, last_e[k], S[k]);
-                last_e[k] = dot - S[k];
-                const float grad_alpha = __builtin_fmaf(last_e[k], T[k], bg_t[k] * inv);
-                last_alpha[k] = alpha;
-                // dL/dG = o dL/dalpha; the centre gradient is
-                // -w (a dx + b dy, c dy + b dx) and the conic gradient
-                // -w (dx dx / 2, dx dy, dy dy / 2).
-                const float w = og * grad_alpha;
-                const float ux = __builtin_fmaf(con.x, dx, con.y * dy);
-                const float uy = __builtin_fmaf(con.z, dy, con.y * dx);
-                if (ABS) {
-                    const float cx = w * ux, cy = w * uy;
-                    vals[0] += cx;
-                    vals[1] += cy;
-                    vals[6] += __builtin_fabsf(cx);
-                    vals[7] += __builtin_fabsf(cy);
-                } else {
-                    vals[0] = __builtin_fmaf(w, ux, vals[0]);
-                    vals[1] = __builtin_fmaf(w, uy, vals[1]);
-                }
-                const float wx = w * dx, wy = w * dy;
-                vals[2] = __builtin_fmaf(wx, dx, vals[2]);
-                vals[3] = __builtin_fmaf(wx, dy, vals[3]);
-                vals[4] = __builtin_fmaf(wy, dy, vals[4]);
-                vals[5] = __builtin_fmaf(G, grad_alpha, vals[5]);
             }
             if (__ballot(accepted) == 0) continue;
             // Wavefront sums of all gradient entries at once; one atomic
@@ -698,24 +766,37 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
 }
 
 template <int CH>
-int launch_fwd(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned blocks, hipStream_t s) {
+int launch_fwd(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned blocks, int c0, hipStream_t s) {
     constexpr int PIX = PixFor<CH, GS3D_FWD_PIX>::value;
     if (st) {
-        hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, true>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a, *st);
+        hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, true>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a, *st, c0);
         return launch_status("gs3d_render_fwd_stats");
     }
     const gs3d_render_stats_args none = {};
-    hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, false>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a, none);
+    hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, false>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a, none, c0);
     return launch_status("gs3d_render_fwd");
 }
 
-template <int CH>
-int launch_bwd(const gs3d_render_bwd_args& b, unsigned blocks, hipStream_t s) {
+// One forward window of `width` channels starting at c0.
+inline int launch_fwd_window(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned blocks, int c0,
+                             int width, hipStream_t s) {
+    if (width <= 4) return launch_fwd<4>(a, st, blocks, c0, s);
+    if (width <= 8) return launch_fwd<8>(a, st, blocks, c0, s);
+    if (width <= 16) return launch_fwd<16>(a, st, blocks, c0, s);
+    if (width <= 36) return launch_fwd<36>(a, st, blocks, c0, s);
+    return launch_fwd<kWindow>(a, st, blocks, c0, s);
+}
+
+template <int CH, bool GEOM>
+int launch_bwd(const gs3d_render_bwd_args& b, unsigned blocks, int c0, hipStream_t s) {
     constexpr int PIX = PixFor<CH, GS3D_BWD_PIX>::value;
-    if (b.abs_centers)
-        hipLaunchKernelGGL((render_bwd_kernel<CH, true, PIX>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, b);
-    else
-        hipLaunchKernelGGL((render_bwd_kernel<CH, false, PIX>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, b);
+    if constexpr (GEOM) {
+        if (b.abs_centers) {
+            hipLaunchKernelGGL((render_bwd_kernel<CH, true, PIX, true>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, b, c0);
+            return launch_status("gs3d_render_bwd");
+        }
+    }
+    hipLaunchKernelGGL((render_bwd_kernel<CH, false, PIX, GEOM>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, b, c0);
     return launch_status("gs3d_render_bwd");
 }
 
@@ -729,7 +810,6 @@ inline int check_render_args(const gs3d_render_args& a) {
         return GS3D_ERR_ARGUMENT;
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     if (D <= 0) return GS3D_ERR_ARGUMENT;
-    if (D > 64) return GS3D_ERR_UNSUPPORTED;  // widest compiled channel vector
     return GS3D_OK;
 }
 
@@ -754,11 +834,12 @@ int render_fwd(const gs3d_render_args* args, const gs3d_render_stats_args* st, v
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     const unsigned blocks = render_blocks(a);
     hipStream_t s = as_stream(stream);
-    if (D <= 4) return launch_fwd<4>(a, st, blocks, s);
-    if (D <= 8) return launch_fwd<8>(a, st, blocks, s);
-    if (D <= 16) return launch_fwd<16>(a, st, blocks, s);
-    if (D <= 36) return launch_fwd<36>(a, st, blocks, s);
-    return launch_fwd<64>(a, st, blocks, s);
+    // Windows of up to 64 channels; the statistics ride on window 0.
+    for (int c0 = 0; c0 < D; c0 += kWindow) {
+        status = launch_fwd_window(a, c0 == 0 ? st : nullptr, blocks, c0, min(kWindow, D - c0), s);
+        if (status != GS3D_OK) return status;
+    }
+    return GS3D_OK;
 }
 
 }  // namespace gs3d
@@ -797,12 +878,28 @@ extern "C" int gs3d_render_bwd(const gs3d_render_bwd_args* args, void* stream) {
         (b.upstream_extra && b.upstream_extra_stride < a.extra_channels) ||
         (b.upstream_alpha && b.upstream_alpha_stride < 1))
         return GS3D_ERR_ARGUMENT;
+    using namespace gs3d;
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
-    const unsigned blocks = gs3d::render_blocks(a);
-    hipStream_t s = gs3d::as_stream(stream);
-    if (D <= 4) return gs3d::launch_bwd<4>(b, blocks, s);
-    if (D <= 8) return gs3d::launch_bwd<8>(b, blocks, s);
-    if (D <= 16) return gs3d::launch_bwd<16>(b, blocks, s);
-    if (D <= 36) return gs3d::launch_bwd<36>(b, blocks, s);
-    return gs3d::launch_bwd<64>(b, blocks, s);
+    const int Dg = D - (a.one_tail ? 1 : 0);
+    const unsigned blocks = render_blocks(a);
+    hipStream_t s = as_stream(stream);
+    // Geometry launch over the first window (channels beyond it enter its
+    // alpha gradient from global memory), then the feature gradients of the
+    // further windows that hold channels with a destination.
+    if (D <= 4) status = launch_bwd<4, true>(b, blocks, 0, s);
+    else if (D <= 8) status = launch_bwd<8, true>(b, blocks, 0, s);
+    else if (D <= 16) status = launch_bwd<16, true>(b, blocks, 0, s);
+    else if (D <= 36) status = launch_bwd<36, true>(b, blocks, 0, s);
+    else status = launch_bwd<kGeomWindow, true>(b, blocks, 0, s);
+    if (status != GS3D_OK || (!b.grad_features && !b.grad_extra)) return status;
+    for (int c0 = kGeomWindow; c0 < Dg; c0 += kWindow) {
+        const int width = min(kWindow, D - c0);
+        if (width <= 4) status = launch_bwd<4, false>(b, blocks, c0, s);
+        else if (width <= 8) status = launch_bwd<8, false>(b, blocks, c0, s);
+        else if (width <= 16) status = launch_bwd<16, false>(b, blocks, c0, s);
+        else if (width <= 36) status = launch_bwd<36, false>(b, blocks, c0, s);
+        else status = launch_bwd<kWindow, false>(b, blocks, c0, s);
+        if (status != GS3D_OK) return status;
+    }
+    return GS3D_OK;
 }

@@ -19,10 +19,11 @@ from typing import Any, Sequence
 import torch
 from torch import Tensor
 
-from .autograd import Frame, Rasterize
+from .autograd import Frame, Rasterize, ViewBins
 from .projection import project_views
 from ..cameras import validate_camera_options
 from ..inputs import batch_item, normalize_inputs
+from ..splatting import binning
 from ..splatting.binning import launch_bin_rows, order_rows, prepare_bin_rows, validate_tile_mode
 from ..splatting.cameras import launch_prepare, raise_camera_errors
 from ..statistics import StatisticsRequest, prepare_statistics
@@ -104,11 +105,33 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     host = status.cpu()
     raise_camera_errors(host[2:].view(torch.int32)[:cameras].tolist())
     group_pairs, count = host[:2].tolist()
-    ranges, ids = launch_bin_rows(launch, group_pairs, count)
+    if count <= binning.PAIR_LIMIT and group_pairs <= binning.PAIR_LIMIT:
+        ranges, ids = launch_bin_rows(launch, group_pairs, count)
+        bins = [ViewBins(0, cameras, ranges, ids)]
+    else:
+        bins = _bin_view_groups(state, width, height, tile_mode)
     return Frame(
         width, height, Ks.detach(), full, inverse if with_centers else None, centers if with_centers else None,
-        state, ranges, ids, count, sh_degree, background,
+        state, bins, count, sh_degree, background,
     )
+
+
+def _bin_view_groups(state, width: int, height: int, tile_mode: str) -> list[ViewBins]:
+    """Binning per group of cameras when all cameras together exceed the
+    int32 pair offsets of one binning launch (the reference bins each view
+    alone, so its limit is per view)."""
+    per_view = state.tile_counts.sum(dim=1, dtype=torch.int64).tolist()
+    bins = []
+    for v0, v1 in binning.view_groups(per_view):
+        sl = slice(v0, v1)
+        order, offsets, totals = order_rows(state.centers[sl], state.radii[sl], state.depths[sl], width, height,
+                                            conics=state.conics[sl], tile_mode=tile_mode)
+        launch = prepare_bin_rows(state.centers[sl], state.radii[sl], order, offsets, width, height,
+                                  conics=state.conics[sl], tile_mode=tile_mode)
+        group_pairs, count = totals.cpu().tolist()
+        ranges, ids = launch_bin_rows(launch, group_pairs, count)
+        bins.append(ViewBins(v0, v1, ranges, ids))
+    return bins
 
 
 def rasterize(

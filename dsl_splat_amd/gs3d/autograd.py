@@ -27,8 +27,21 @@ from ..statistics import PreparedStatistics
 
 
 @dataclass(slots=True)
+class ViewBins:
+    """Tile lists of cameras [v0, v1): ranges ((v1-v0)*T, 2) into ids."""
+
+    v0: int
+    v1: int
+    ranges: Tensor
+    ids: Tensor
+
+
+@dataclass(slots=True)
 class Frame:
-    """Forward state of one Gaussian batch (all C cameras)."""
+    """Forward state of one Gaussian batch (all C cameras).  ``bins`` is one
+    entry for all cameras unless their pairs together exceed the int32
+    offsets of one binning launch; then each group of cameras has its own
+    lists and is blended by its own launch."""
 
     width: int
     height: int
@@ -37,11 +50,25 @@ class Frame:
     inverse: Tensor | None     # (C,4,4) view inverse (SH only)
     camera_centers: Tensor | None
     state: projection.ProjectedViews
-    ranges: Tensor             # (C*T, 2)
-    ids: Tensor                # (M,)
+    bins: list[ViewBins]
     pair_count: int
     sh_degree: int | None
     background: Tensor | None  # (C, D) or None
+
+
+def _views(t, v0: int, v1: int, views: int, per_view_ndim: int):
+    """Cameras [v0, v1) of a per-camera tensor (leading camera axis at
+    ``per_view_ndim`` dimensions); shared tensors pass through."""
+    if t is None or t.ndim < per_view_ndim or t.shape[0] != views:
+        return t
+    return t[v0:v1]
+
+
+def _statistics_views(statistics, v0: int, v1: int):
+    if statistics is None:
+        return None
+    return PreparedStatistics(statistics.key, statistics.pixel_values[v0:v1], statistics.counts[v0:v1],
+                              statistics.sums[v0:v1])
 
 
 class Rasterize(torch.autograd.Function):
@@ -66,10 +93,26 @@ class Rasterize(torch.autograd.Function):
         blend launch."""
         st = frame.state
         blended = st.colors if frame.sh_degree is not None else colors
-        output = render.render_views(
-            frame.ranges, frame.ids, st.centers, st.conics, blended, frame.width, frame.height,
-            extra=extra_features, background=frame.background, one_tail=True, statistics=statistics,
-        )
+        if len(frame.bins) == 1:
+            bins = frame.bins[0]
+            output = render.render_views(
+                bins.ranges, bins.ids, st.centers, st.conics, blended, frame.width, frame.height,
+                extra=extra_features, background=frame.background, one_tail=True, statistics=statistics,
+            )
+        else:
+            views = st.centers.shape[0]
+            parts = []
+            for bins in frame.bins:
+                v0, v1 = bins.v0, bins.v1
+                parts.append(render.render_views(
+                    bins.ranges, bins.ids, st.centers[v0:v1], st.conics[v0:v1], _views(blended, v0, v1, views, 3),
+                    frame.width, frame.height, extra=_views(extra_features, v0, v1, views, 3),
+                    background=_views(frame.background, v0, v1, views, 2), one_tail=True,
+                    statistics=_statistics_views(statistics, v0, v1),
+                ))
+            output = render.RenderedPixels(*(
+                None if getattr(parts[0], f) is None else torch.cat([getattr(p, f) for p in parts])
+                for f in ("features", "extra", "alpha", "transmittance", "contributors")))
         if grad_enabled and any(ctx.needs_input_grad[:8]):
             ctx.save_for_backward(means, quats, scales, opacities, colors, extra_features, viewmats,
                                   output.transmittance, output.contributors)
@@ -98,12 +141,34 @@ class Rasterize(torch.autograd.Function):
         sh = frame.sh_degree is not None
         blended = st.colors if sh else colors
         absgrad = ctx.absolute is not None and any(t is not None for t in ctx.absolute)
-        record, grad_blended, grad_extra = render.backward_views(
-            frame.ranges, frame.ids, st.centers, st.conics, blended, final_t, contributors,
-            (grad_features, grad_extra_image, grad_alpha),
-            frame.width, frame.height, extra=extra, background=frame.background, one_tail=True,
-            absgrad=absgrad, need_features=sh or needs[4], need_extra=needs[5],
-        )
+        upstream = (grad_features, grad_extra_image, grad_alpha)
+        blend_args = dict(one_tail=True, absgrad=absgrad, need_features=sh or needs[4], need_extra=needs[5])
+        if len(frame.bins) == 1:
+            bins = frame.bins[0]
+            record, grad_blended, grad_extra = render.backward_views(
+                bins.ranges, bins.ids, st.centers, st.conics, blended, final_t, contributors, upstream,
+                frame.width, frame.height, extra=extra, background=frame.background, **blend_args,
+            )
+        else:
+            views = st.centers.shape[0]
+            parts = []
+            for bins in frame.bins:
+                v0, v1 = bins.v0, bins.v1
+                parts.append(render.backward_views(
+                    bins.ranges, bins.ids, st.centers[v0:v1], st.conics[v0:v1], _views(blended, v0, v1, views, 3),
+                    final_t[v0:v1], contributors[v0:v1], tuple(_views(u, v0, v1, views, 1) for u in upstream),
+                    frame.width, frame.height, extra=_views(extra, v0, v1, views, 3),
+                    background=_views(frame.background, v0, v1, views, 2), **blend_args,
+                ))
+
+            def join(k, source):
+                items = [p[k] for p in parts]
+                if items[0] is None:
+                    return None
+                # Per-camera sources get per-camera gradients; shared ones sum.
+                return torch.cat(items) if source is None or source.ndim == 3 else torch.stack(items).sum(0)
+
+            record, grad_blended, grad_extra = join(0, None), join(1, blended), join(2, extra)
         if absgrad:
             for c, target in enumerate(ctx.absolute):
                 if target is not None:

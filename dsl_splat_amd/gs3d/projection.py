@@ -100,6 +100,11 @@ def project_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tenso
     return out
 
 
+# Cameras whose camera gradients one gs3d_project_bwd launch accumulates
+# (per-wavefront LDS accumulators); more cameras run in groups of this size.
+CAMERA_GRADIENT_GROUP = 16
+
+
 @torch.no_grad()
 def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tensor, view: Tensor,
                    projection: Tensor, intrinsics: Tensor, width: int, height: int, radii: Tensor,
@@ -115,6 +120,11 @@ def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tens
     ``need_screen`` also returns grad_centers as a contiguous (views, N, 2)
     tensor under "screen" (zero where radii are not positive).
     Returns dict with the requested gradients (None otherwise).
+
+    Any number of cameras: when camera gradients are requested for more than
+    CAMERA_GRADIENT_GROUP cameras, the launch runs per group of cameras and
+    the per-Gaussian gradients of the groups are summed (the reference
+    launches its projection VJP once per view, gs3d/api.py:132-189).
     """
     device = means.device
     n = len(means)
@@ -146,39 +156,57 @@ def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tens
     for t in (grad_centers, grad_conics):
         if t.stride(-1) != 1 or t.stride(0) != t.stride(1) * n:
             raise ValueError("gradient rows must be evenly strided (views, N, k)")
-    a = abi.ProjectBwdArgs()
-    a.n, a.views, a.width, a.height = n, views, width, height
-    a.normalize_quats = int(normalize_quats)
-    for name, t in (("means", means), ("quats", quats), ("scales", scales), ("opacities", opacities),
-                    ("view", view), ("projection", projection), ("intrinsics", intrinsics), ("radii", radii)):
-        setattr(a, name, native.ptr(t))
-    a.grad_centers, a.grad_centers_stride = native.ptr(grad_centers), grad_centers.stride(1)
-    a.grad_conics, a.grad_conics_stride = native.ptr(grad_conics), grad_conics.stride(1)
-    a.grad_means = native.ptr(res["means"])
-    a.grad_quats = native.ptr(res["quats"])
-    a.grad_scales = native.ptr(res["scales"])
-    a.grad_opacities = native.ptr(res["opacities"])
-    a.grad_view = native.ptr(res["view"])
-    a.grad_projection = native.ptr(res["projection"])
-    a.screen_grad = native.ptr(res["screen"])
-    keep = [means, quats, scales, opacities, view, projection, intrinsics, radii]
+    cc = None
     if sh is not None:
         sh, stride, rows = _sh_layout(sh, views)
-        keep.append(sh)
-        a.sh, a.sh_view_stride, a.sh_rows, a.sh_degree = native.ptr(sh), stride, rows, int(sh_degree)
         if sh_degree > 0:
             cc = camera_centers.reshape(views, 3).contiguous()
-            keep.append(cc)
-            a.camera_centers = native.ptr(cc)
             if need_centers:
                 res["camera_centers"] = torch.zeros((views, 3), **f32)
-                a.grad_camera_centers = native.ptr(res["camera_centers"])
         if grad_colors.stride(-1) != 1:
             grad_colors = grad_colors.contiguous()
-        keep.append(grad_colors)
-        a.grad_colors, a.grad_colors_stride = native.ptr(grad_colors), grad_colors.stride(1)
         if need_sh:
             res["sh"] = torch.empty(sh.shape, **f32)
-            a.grad_sh = native.ptr(res["sh"])
-    native.call("gs3d_project_bwd", ctypes.byref(a), native.stream(device))
+    camera_grads = needs[4] or needs[5] or res["camera_centers"] is not None
+    group = CAMERA_GRADIENT_GROUP if camera_grads else views
+    per_gaussian = ("means", "quats", "scales", "opacities") + (("sh",) if sh is not None and stride == 0 else ())
+    for v0 in range(0, views, group):
+        v1 = min(views, v0 + group)
+        out = dict(res)
+        if v0 > 0:
+            # Later groups write per-Gaussian sums into fresh buffers, added below.
+            for key in per_gaussian:
+                if res[key] is not None:
+                    out[key] = torch.empty_like(res[key])
+        a = abi.ProjectBwdArgs()
+        a.n, a.views, a.width, a.height = n, v1 - v0, width, height
+        a.normalize_quats = int(normalize_quats)
+        for name, t in (("means", means), ("quats", quats), ("scales", scales), ("opacities", opacities),
+                        ("view", view[v0:v1]), ("projection", projection[v0:v1]),
+                        ("intrinsics", intrinsics[v0:v1]), ("radii", radii[v0:v1])):
+            setattr(a, name, native.ptr(t))
+        a.grad_centers, a.grad_centers_stride = native.ptr(grad_centers[v0:v1]), grad_centers.stride(1)
+        a.grad_conics, a.grad_conics_stride = native.ptr(grad_conics[v0:v1]), grad_conics.stride(1)
+        a.grad_means = native.ptr(out["means"])
+        a.grad_quats = native.ptr(out["quats"])
+        a.grad_scales = native.ptr(out["scales"])
+        a.grad_opacities = native.ptr(out["opacities"])
+        a.grad_view = native.ptr(None if out["view"] is None else out["view"][v0:v1])
+        a.grad_projection = native.ptr(None if out["projection"] is None else out["projection"][v0:v1])
+        a.screen_grad = native.ptr(None if out["screen"] is None else out["screen"][v0:v1])
+        if sh is not None:
+            a.sh = native.ptr(sh if stride == 0 else sh[v0:v1])
+            a.sh_view_stride, a.sh_rows, a.sh_degree = stride, rows, int(sh_degree)
+            if cc is not None:
+                a.camera_centers = native.ptr(cc[v0:v1])
+                if out["camera_centers"] is not None:
+                    a.grad_camera_centers = native.ptr(out["camera_centers"][v0:v1])
+            a.grad_colors, a.grad_colors_stride = native.ptr(grad_colors[v0:v1]), grad_colors.stride(1)
+            if out["sh"] is not None:
+                a.grad_sh = native.ptr(out["sh"] if stride == 0 else out["sh"][v0:v1])
+        native.call("gs3d_project_bwd", ctypes.byref(a), native.stream(device))
+        if v0 > 0:
+            for key in per_gaussian:
+                if res[key] is not None:
+                    res[key] += out[key]
     return res

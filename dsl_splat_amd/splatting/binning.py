@@ -124,9 +124,31 @@ def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, heigh
     return order, offsets, totals
 
 
+# Largest pair count one binning launch addresses: tile lists, ranges and
+# offsets are int32, as the reference's (primitives/tiling.py:57-64,
+# splatting/binning.py:88-89), whose limit applies per view.
+PAIR_LIMIT = 2**31 - 1
+
+
 def check_pair_counts(group_pairs: int, tile_pairs: int) -> None:
-    if tile_pairs > 2**31 - 1 or group_pairs > 2**31 - 1:
+    if tile_pairs > PAIR_LIMIT or group_pairs > PAIR_LIMIT:
         raise OverflowError(f"{tile_pairs} tile pairs exceed the int32 offsets of the binning stage")
+
+
+def view_groups(pairs_per_view: list[int]) -> list[tuple[int, int]]:
+    """Consecutive view ranges [v0, v1) whose tile-pair totals each fit one
+    binning launch (group pairs never exceed tile pairs); OverflowError when
+    a single view does not fit, as in the reference."""
+    groups, v0, total = [], 0, 0
+    for v, pairs in enumerate(pairs_per_view):
+        if pairs > PAIR_LIMIT:
+            raise OverflowError(f"view {v} has {pairs} tile pairs, more than the int32 offsets of the binning stage")
+        if total + pairs > PAIR_LIMIT:
+            groups.append((v0, v))
+            v0, total = v, 0
+        total += pairs
+    groups.append((v0, len(pairs_per_view)))
+    return groups
 
 
 @dataclass(slots=True)

@@ -55,6 +55,10 @@ def lib() -> ctypes.CDLL:
             "oracle_normalize_quats": [P, I64, P, P, P],
             "oracle_render_fwd_stats": [ctypes.POINTER(abi.RenderArgs), ctypes.POINTER(abi.RenderStatsArgs)],
             "oracle_render_bwd": [ctypes.POINTER(abi.RenderBwdArgs)],
+            "oracle_render_bwd_bound": [ctypes.POINTER(abi.RenderBwdArgs), P, P, P, P, P],
+            "oracle_render_bwd_f64": [ctypes.POINTER(abi.RenderBwdArgs), P, P, P, P, P],
+            "oracle_project_bwd_bound": [ctypes.POINTER(abi.ProjectBwdArgs), P, P, P, P, P, P, P, P, P, P, P],
+            "oracle_camera_backward_bound": [P, P, P, I32, I32, P, P, P, I32, P],
             "oracle_projection_loss_f64": [P, P, P, D, P, P, I32, I32, D, D, P, P],
             "oracle_projection_vjp_f64": [P, P, P, D, P, P, I32, I32, D, D, P, P, P],
             "oracle_glm_rotation": [P, P],
@@ -452,3 +456,131 @@ def projection_vjp_f64(mean, quat, scale, opacity, view, proj, width, height, fx
         width, height, float(fx), float(fy), _ptr(gc), _ptr(gk), _ptr(out))
     return dict(mean=out[0:3], quat=out[3:7], scale=out[7:10], opacity=out[10],
                 view=out[11:27].reshape(4, 4), proj=out[27:43].reshape(4, 4))
+
+
+# ---------------------------------------------------------------------------
+# Float32 error bounds of the gradient path (running error analysis in the
+# C restatement, see Err in gs3d_oracle.cpp).  A gradient entry computed in
+# float32 by two implementations that sum the same terms in different orders
+# and with different fused operations may differ by at most
+#     B = P + 2 R + LAMBDA * sqrt(n) * u * A
+# where, over the entry's n terms t, A = sum |t|, P = sum of the bounds the
+# terms inherit from their inputs' differences, R = sum of the first-order
+# rounding-error bounds of each term's own evaluation (counted once for each
+# implementation), and LAMBDA sqrt(n) u A bounds the difference between two
+# summation orders (the probabilistic rounding-error bound of Higham and
+# Mary, SIAM J. Sci. Comput. 41(5), 2019: it holds with probability at least
+# 1 - 2 exp(-LAMBDA^2 / 2) for independent rounding errors; LAMBDA = 6 gives
+# 3e-8).  u = 2^-24.
+# ---------------------------------------------------------------------------
+UNIT_ROUNDOFF = 2.0 ** -24
+REORDER_LAMBDA = 6.0
+
+
+def sum_bound(stats):
+    """B of entries given their [sum |t|, sum p, sum r, count] statistics."""
+    stats = np.asarray(stats, np.float64)
+    A, P, R, n = stats[..., 0], stats[..., 1], stats[..., 2], stats[..., 3]
+    return P + 2.0 * R + REORDER_LAMBDA * np.sqrt(n) * UNIT_ROUNDOFF * A
+
+
+def pair_bound(pr):
+    """B of entries computed once per implementation from [p, r] pairs."""
+    pr = np.asarray(pr, np.float64)
+    return pr[..., 0] + 2.0 * pr[..., 1]
+
+
+def render_bwd_bound(width, height, ranges, ids, centers, conics, features, final_t, contributors, upstream,
+                     extra=None, background=None, float64=False):
+    """Per-entry bounds B of render_bwd's gradients (same keys); with
+    float64, instead the gradients evaluated in double arithmetic."""
+    keep = []
+    a, c, n, channels = _render_args(width, height, ranges, ids, centers, conics, features, extra, background, keep)
+    final_t, contributors = _f32(final_t), _i32(contributors)
+    upstream = _f32(upstream).reshape(c, height, width, channels)
+    a.final_t, a.contributors = _ptr(final_t), _ptr(contributors)
+    b = abi.RenderBwdArgs()
+    b.fwd = a
+    b.upstream = _ptr(upstream)
+    features = _f32(features)
+    b.grad_feat_stride, b.grad_feat_view_stride = features.shape[-1], a.feat_view_stride
+    stats = dict(centers=np.zeros((c, n, 2, 4)), conics=np.zeros((c, n, 4, 4)), abs=np.zeros((c, n, 2, 4)),
+                 features=np.zeros(features.shape + (4,)))
+    if extra is not None:
+        extra = _f32(extra)
+        b.grad_extra_stride, b.grad_extra_view_stride = extra.shape[-1], a.extra_view_stride
+        stats["extra"] = np.zeros(extra.shape + (4,))
+    if float64:
+        vals = {k: np.zeros(v.shape[:-1]) for k, v in stats.items()}
+        lib().oracle_render_bwd_f64(ctypes.byref(b), _ptr(vals["centers"]), _ptr(vals["conics"]),
+                                    _ptr(vals["abs"]), _ptr(vals["features"]), _ptr(vals.get("extra")))
+        vals.setdefault("extra", None)
+        return vals
+    lib().oracle_render_bwd_bound(ctypes.byref(b), _ptr(stats["centers"]), _ptr(stats["conics"]),
+                                  _ptr(stats["abs"]), _ptr(stats["features"]), _ptr(stats.get("extra")))
+    out = {k: sum_bound(v) for k, v in stats.items()}
+    out.setdefault("extra", None)
+    return out
+
+
+def project_bwd_bound(means, quats, scales, opacities, view, projection, intrinsics, width, height, radii,
+                      grad_centers, grad_conics, e_centers, e_conics, sh=None, sh_degree=0, camera_centers=None,
+                      grad_colors=None, e_colors=None, normalize_quats=False):
+    """Per-entry bounds B of project_bwd's outputs given bounds e_* of the
+    upstream gradients (same keys as project_bwd)."""
+    means, quats, scales, opacities = _f32(means), _f32(quats), _f32(scales), _f32(opacities)
+    view, projection, intrinsics = (
+        _f32(view).reshape(-1, 4, 4), _f32(projection).reshape(-1, 4, 4), _f32(intrinsics).reshape(-1, 3, 3))
+    n, c = len(means), len(view)
+    radii = _i32(radii).reshape(c, n)
+    gc = _f32(grad_centers).reshape(c, n, 2)
+    gk = _f32(grad_conics).reshape(c, n, 4)
+    ec = np.ascontiguousarray(e_centers, np.float64).reshape(c, n, 2)
+    ek = np.ascontiguousarray(e_conics, np.float64).reshape(c, n, 4)
+    a = abi.ProjectBwdArgs()
+    a.n, a.views, a.width, a.height = n, c, width, height
+    a.normalize_quats = int(normalize_quats)
+    for name, arr in (("means", means), ("quats", quats), ("scales", scales), ("opacities", opacities),
+                      ("view", view), ("projection", projection), ("intrinsics", intrinsics), ("radii", radii)):
+        setattr(a, name, _ptr(arr))
+    a.grad_centers, a.grad_centers_stride = _ptr(gc), 2
+    a.grad_conics, a.grad_conics_stride = _ptr(gk), 4
+    pr = dict(means=np.zeros((n, 3, 2)), quats=np.zeros((n, 4, 2)), scales=np.zeros((n, 3, 2)),
+              opacities=np.zeros((n, 2)))
+    st = dict(view=np.zeros((c, 4, 4, 4)), projection=np.zeros((c, 4, 4, 4)))
+    keep, ecol = [], None
+    if sh is not None:
+        sh = _f32(sh)
+        a.sh = _ptr(sh)
+        a.sh_rows = sh.shape[-2]
+        a.sh_view_stride = sh.shape[-3] * sh.shape[-2] * 3 if sh.ndim == 4 else 0
+        a.sh_degree = sh_degree
+        cc = _f32(np.zeros((c, 3)) if camera_centers is None else camera_centers).reshape(c, 3)
+        gcol = _f32(grad_colors).reshape(c, n, 3)
+        ecol = np.ascontiguousarray(e_colors, np.float64).reshape(c, n, 3)
+        keep += [sh, cc, gcol]
+        a.camera_centers = _ptr(cc)
+        a.grad_colors, a.grad_colors_stride = _ptr(gcol), 3
+        pr["sh"] = np.zeros(sh.shape + (2,))
+        st["camera_centers"] = np.zeros((c, 3, 4))
+    lib().oracle_project_bwd_bound(ctypes.byref(a), _ptr(ec), _ptr(ek), _ptr(ecol), _ptr(pr["means"]),
+                                   _ptr(pr["quats"]), _ptr(pr["scales"]), _ptr(pr["opacities"]), _ptr(pr.get("sh")),
+                                   _ptr(st["view"]), _ptr(st["projection"]), _ptr(st.get("camera_centers")))
+    out = {k: pair_bound(v) for k, v in pr.items()}
+    out.update({k: sum_bound(v) for k, v in st.items()})
+    return out
+
+
+def camera_backward_bound(Ks, grad_full, e_full, width, height, inverse, grad_centers, e_centers):
+    """Per-entry bound B of camera_backward's (C,4,4) result."""
+    Ks = _f32(Ks).reshape(-1, 3, 3)
+    c = len(Ks)
+    gf = None if grad_full is None else _f32(grad_full).reshape(c, 4, 4)
+    ef = None if e_full is None else np.ascontiguousarray(e_full, np.float64).reshape(c, 4, 4)
+    gc = None if grad_centers is None else _f32(grad_centers).reshape(c, 3)
+    ec = None if e_centers is None else np.ascontiguousarray(e_centers, np.float64).reshape(c, 3)
+    inv = _f32(inverse).reshape(c, 4, 4)
+    out = np.zeros((c, 4, 4, 2))
+    lib().oracle_camera_backward_bound(_ptr(Ks), _ptr(gf), _ptr(ef), width, height, _ptr(inv), _ptr(gc), _ptr(ec), c,
+                                       _ptr(out))
+    return pair_bound(out)

@@ -121,12 +121,12 @@ inline float normalize_quat(const float* q, float* u) {
     return norm;
 }
 
-inline void normalize_quat_vjp(const float* u, float norm, float* g) {
+template <class T> inline void normalize_quat_vjp(const float* u, float norm, T* g) {
     if (norm > 1e-12f) {
-        const float dot = ((u[0] * g[0] + u[1] * g[1]) + u[2] * g[2]) + u[3] * g[3];
-        for (int k = 0; k < 4; ++k) g[k] = (g[k] - u[k] * dot) / norm;
+        const T dot = ((T(u[0]) * g[0] + T(u[1]) * g[1]) + T(u[2]) * g[2]) + T(u[3]) * g[3];
+        for (int k = 0; k < 4; ++k) g[k] = (g[k] - T(u[k]) * dot) / T(norm);
     } else {
-        for (int k = 0; k < 4; ++k) g[k] = g[k] / 1e-12f;
+        for (int k = 0; k < 4; ++k) g[k] = g[k] / T(1e-12f);
     }
 }
 
@@ -136,6 +136,65 @@ inline void normalize_quat_vjp(const float* u, float norm, float* g) {
 // ---------------------------------------------------------------------------
 template <class T> inline T fma_(T a, T b, T c) { return std::fma(a, b, c); }
 template <> inline float fma_<float>(float a, float b, float c) { return fmaf(a, b, c); }
+
+// ---------------------------------------------------------------------------
+// Running error analysis (Wilkinson) of the gradient path, used to state how
+// far two float32 evaluations of the same gradient in different operation
+// orders may lie apart.  Err carries the value v exactly as the float32
+// oracle computes it (every branch, clamp and threshold therefore decides
+// identically) and two first-order bounds in double on |v - exact|:
+//   p -- the part inherited from errors in the inputs (e.g. the upstream
+//        gradients of a VJP, which arrive with their own bound),
+//   r -- the part caused by this computation's own roundings.
+// Each operation propagates both (|y| e_x + |x| e_y for a product,
+// (e_x + |q| e_y) / |y| for a quotient, sums for sums and differences) and
+// adds u |result| to r for its own rounding, u = 2^-24.
+// ---------------------------------------------------------------------------
+constexpr double kUnitRoundoff = 1.0 / 16777216.0;
+
+struct Err {
+    float v;
+    double p, r;
+    Err() = default;
+    Err(float x) : v(x), p(0.0), r(0.0) {}
+    Err(double x) : v((float)x), p(0.0), r(0.0) {}
+    Err(int x) : v((float)x), p(0.0), r(0.0) {}
+    Err(float x, double prop, double round) : v(x), p(prop), r(round) {}
+};
+inline double ad(float x) { return std::fabs((double)x); }
+inline Err operator+(Err a, Err b) {
+    const float v = a.v + b.v;
+    return Err(v, a.p + b.p, a.r + b.r + kUnitRoundoff * ad(v));
+}
+inline Err operator-(Err a, Err b) {
+    const float v = a.v - b.v;
+    return Err(v, a.p + b.p, a.r + b.r + kUnitRoundoff * ad(v));
+}
+inline Err operator-(Err a) { return Err(-a.v, a.p, a.r); }
+inline Err operator*(Err a, Err b) {
+    const float v = a.v * b.v;
+    return Err(v, ad(b.v) * a.p + ad(a.v) * b.p, ad(b.v) * a.r + ad(a.v) * b.r + kUnitRoundoff * ad(v));
+}
+inline Err operator/(Err a, Err b) {
+    const float v = a.v / b.v;
+    const double d = ad(b.v);
+    return Err(v, (a.p + ad(v) * b.p) / d, (a.r + ad(v) * b.r) / d + kUnitRoundoff * ad(v));
+}
+inline Err& operator+=(Err& a, Err b) { return a = a + b; }
+inline Err& operator-=(Err& a, Err b) { return a = a - b; }
+inline Err& operator*=(Err& a, Err b) { return a = a * b; }
+inline bool operator<(Err a, Err b) { return a.v < b.v; }
+inline bool operator>(Err a, Err b) { return a.v > b.v; }
+inline bool operator<=(Err a, Err b) { return a.v <= b.v; }
+inline bool operator>=(Err a, Err b) { return a.v >= b.v; }
+inline bool operator==(Err a, Err b) { return a.v == b.v; }
+inline bool operator!=(Err a, Err b) { return a.v != b.v; }
+template <> inline Err fma_<Err>(Err a, Err b, Err c) {
+    const float v = fmaf(a.v, b.v, c.v);
+    return Err(v, ad(b.v) * a.p + ad(a.v) * b.p + c.p, ad(b.v) * a.r + ad(a.v) * b.r + c.r + kUnitRoundoff * ad(v));
+}
+inline float val(float x) { return x; }
+inline float val(Err x) { return x.v; }
 
 template <class T> struct M3 { T m[3][3]; };
 template <class T> struct M4 { T m[4][4]; };
@@ -562,39 +621,42 @@ inline void sh_eval(const float* coef, const float dir[3], int degree, bool visi
 }
 
 // primitives/sh.py:100-136 for one row.  active[ch] is the saved clamp mask.
+// T is float (the oracle) or Err (its running error analysis); the
+// direction, basis values and basis gradients are forward quantities.
+template <class T>
 inline void sh_backward_row(const float* coef, const float dir[3], int degree, bool visible,
-                            const bool active[3], const float upstream[3], float* grad_coef,
-                            int rows, float grad_dir[3]) {
-    grad_dir[0] = grad_dir[1] = grad_dir[2] = 0.0f;
+                            const bool active[3], const T upstream[3], T* grad_coef,
+                            int rows, T grad_dir[3]) {
+    grad_dir[0] = grad_dir[1] = grad_dir[2] = T(0.0f);
     if (grad_coef)
-        for (int i = 0; i < rows * 3; ++i) grad_coef[i] = 0.0f;
+        for (int i = 0; i < rows * 3; ++i) grad_coef[i] = T(0.0f);
     if (!visible) return;
-    float cg[3];
-    for (int ch = 0; ch < 3; ++ch) cg[ch] = active[ch] ? upstream[ch] : 0.0f;
+    T cg[3];
+    for (int ch = 0; ch < 3; ++ch) cg[ch] = active[ch] ? upstream[ch] : T(0.0f);
     float unit[3] = {0.0f, 0.0f, 0.0f}, length = 1.0f;
     if (degree > 0) {
         length = length3(dir);
         const float l = std::max(length, 1.0e-12f);
         for (int i = 0; i < 3; ++i) unit[i] = dir[i] / l;
     }
-    float ug[3] = {0.0f, 0.0f, 0.0f};
+    T ug[3] = {T(0.0f), T(0.0f), T(0.0f)};
     const int count = (degree + 1) * (degree + 1);
     for (int k = 0; k < count; ++k) {
         const float b = sh_basis(unit, k);
         if (grad_coef)
-            for (int ch = 0; ch < 3; ++ch) grad_coef[3 * k + ch] = b * cg[ch];
+            for (int ch = 0; ch < 3; ++ch) grad_coef[3 * k + ch] = T(b) * cg[ch];
         float bg[3];
         sh_basis_grad(unit, k, bg);
-        const float d = coef[3 * k] * cg[0] + coef[3 * k + 1] * cg[1] + coef[3 * k + 2] * cg[2];
-        for (int i = 0; i < 3; ++i) ug[i] = ug[i] + d * bg[i];
+        const T d = T(coef[3 * k]) * cg[0] + T(coef[3 * k + 1]) * cg[1] + T(coef[3 * k + 2]) * cg[2];
+        for (int i = 0; i < 3; ++i) ug[i] = ug[i] + d * T(bg[i]);
     }
     if (degree > 0) {
         const float l = std::max(length, 1.0e-12f);
-        for (int i = 0; i < 3; ++i) grad_dir[i] = ug[i] / l;
+        for (int i = 0; i < 3; ++i) grad_dir[i] = ug[i] / T(l);
         if (length >= 1.0e-12f) {
-            const float dot = unit[0] * ug[0] + unit[1] * ug[1] + unit[2] * ug[2];
-            const float f = dot / length;
-            for (int i = 0; i < 3; ++i) grad_dir[i] = grad_dir[i] - unit[i] * f;
+            const T dot = T(unit[0]) * ug[0] + T(unit[1]) * ug[1] + T(unit[2]) * ug[2];
+            const T f = dot / T(length);
+            for (int i = 0; i < 3; ++i) grad_dir[i] = grad_dir[i] - T(unit[i]) * f;
         }
     }
 }
@@ -997,6 +1059,14 @@ int oracle_project_bwd(const gs3d_project_bwd_args* a) {
         const int64_t per = a->sh_view_stride ? a->sh_view_stride * a->views : (int64_t)3 * K * n;
         std::fill(a->grad_sh, a->grad_sh + per, 0.0f);
     }
+    // Camera gradients sum one term per visible Gaussian; the sums are
+    // carried in double and rounded once (see RenderGradSink).
+    std::vector<double> sum_view(a->grad_view ? 16 * a->views : 0), sum_proj(a->grad_projection ? 16 * a->views : 0);
+    std::vector<double> sum_cc(a->grad_camera_centers ? 3 * a->views : 0);
+    auto dacc = [](double* p, double v) {
+#pragma omp atomic
+        *p += v;
+    };
 #pragma omp parallel for schedule(static) num_threads(g_threads)
     for (int64_t i = 0; i < n; ++i) {
         float gco[3 * 64];
@@ -1025,10 +1095,10 @@ int oracle_project_bwd(const gs3d_project_bwd_args* a) {
                 go += g.opacity;
                 if (a->grad_view)
                     for (int r = 0; r < 4; ++r)
-                        for (int c = 0; c < 4; ++c) acc(&a->grad_view[16 * v + 4 * r + c], g.view[r][c]);
+                        for (int c = 0; c < 4; ++c) dacc(&sum_view[16 * v + 4 * r + c], g.view[r][c]);
                 if (a->grad_projection)
                     for (int r = 0; r < 4; ++r)
-                        for (int c = 0; c < 4; ++c) acc(&a->grad_projection[16 * v + 4 * r + c], g.proj[r][c]);
+                        for (int c = 0; c < 4; ++c) dacc(&sum_proj[16 * v + 4 * r + c], g.proj[r][c]);
             }
             if (a->sh) {
                 const float* coef = a->sh + v * a->sh_view_stride + (int64_t)3 * K * i;
@@ -1050,7 +1120,7 @@ int oracle_project_bwd(const gs3d_project_bwd_args* a) {
                 if (a->sh_degree > 0) {
                     for (int k = 0; k < 3; ++k) gm[k] += gd[k];
                     if (a->grad_camera_centers)
-                        for (int k = 0; k < 3; ++k) acc(&a->grad_camera_centers[3 * v + k], -gd[k]);
+                        for (int k = 0; k < 3; ++k) dacc(&sum_cc[3 * v + k], -gd[k]);
                 }
             }
         }
@@ -1064,6 +1134,163 @@ int oracle_project_bwd(const gs3d_project_bwd_args* a) {
         if (a->grad_scales)
             for (int k = 0; k < 3; ++k) a->grad_scales[3 * i + k] = (float)gs[k];
         if (a->grad_opacities) a->grad_opacities[i] = (float)go;
+    }
+    for (size_t k = 0; k < sum_view.size(); ++k) a->grad_view[k] += (float)sum_view[k];
+    for (size_t k = 0; k < sum_proj.size(); ++k) a->grad_projection[k] += (float)sum_proj[k];
+    for (size_t k = 0; k < sum_cc.size(); ++k) a->grad_camera_centers[k] += (float)sum_cc[k];
+    return 0;
+}
+
+// Running error analysis of oracle_project_bwd (see Err).  Inputs: the
+// forward data of `a` (exact) and the upstream gradients' values in `a`
+// with error bounds e_centers (views,N,2), e_conics (views,N,4) and, with
+// SH, e_colors (views,N,3) (bounds on their difference between two
+// evaluations; NULL = exact).  Outputs (any may be NULL): per-Gaussian
+// [p, r] pairs for means (N,3), quats (N,4), scales (N,3), opacities (N)
+// and SH coefficients (grad_sh layout); for the camera sums over Gaussians
+// [sum |t|, sum p, sum r, count] per entry of grad_view (views,16),
+// grad_projection (views,16) and grad_camera_centers (views,3).
+int oracle_project_bwd_bound(const gs3d_project_bwd_args* a, const double* e_centers, const double* e_conics,
+                             const double* e_colors, double* b_means, double* b_quats, double* b_scales,
+                             double* b_opacities, double* b_sh, double* s_view, double* s_proj, double* s_cc) {
+    const int64_t n = a->n;
+    const int K = a->sh_rows;
+    auto put2 = [](double* dst, const Err& t) {
+        dst[0] = t.p;
+        dst[1] = t.r;
+    };
+    auto sum4 = [](double* dst, const Err& t) {
+#pragma omp atomic
+        dst[0] += ad(t.v);
+#pragma omp atomic
+        dst[1] += t.p;
+#pragma omp atomic
+        dst[2] += t.r;
+#pragma omp atomic
+        dst[3] += 1.0;
+    };
+    if (b_sh) {
+        const int64_t per = a->sh_view_stride ? a->sh_view_stride * a->views : (int64_t)3 * K * n;
+        std::fill(b_sh, b_sh + 2 * per, 0.0);
+    }
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int64_t i = 0; i < n; ++i) {
+        std::vector<Err> gco(3 * K), shsum(a->sh && a->sh_view_stride == 0 ? 3 * K : 0, Err(0.0f));
+        Err gm[3] = {Err(0.0f), Err(0.0f), Err(0.0f)}, gq[4] = {Err(0.0f), Err(0.0f), Err(0.0f), Err(0.0f)};
+        Err gs[3] = {Err(0.0f), Err(0.0f), Err(0.0f)}, go = Err(0.0f);
+        float qn[4], qnorm = 1.0f;
+        const float* quat = a->quats + 4 * i;
+        if (a->normalize_quats) {
+            qnorm = normalize_quat(quat, qn);
+            quat = qn;
+        }
+        Err mean[3], q[4], sc[3];
+        for (int k = 0; k < 3; ++k) mean[k] = Err(a->means[3 * i + k]);
+        for (int k = 0; k < 4; ++k) q[k] = Err(quat[k]);
+        for (int k = 0; k < 3; ++k) sc[k] = Err(a->scales[3 * i + k]);
+        for (int v = 0; v < a->views; ++v) {
+            const int64_t row = v * n + i;
+            if (a->radii[row] > 0) {
+                const M4<Err> V = load44<Err>(a->view + 16 * v);
+                const M4<Err> P = load44<Err>(a->projection + 16 * v);
+                const float* gcp = a->grad_centers + row * a->grad_centers_stride;
+                const float* gkp = a->grad_conics + row * a->grad_conics_stride;
+                Err gc[2], gk[4];
+                for (int k = 0; k < 2; ++k) gc[k] = Err(gcp[k], e_centers ? e_centers[2 * row + k] : 0.0, 0.0);
+                for (int k = 0; k < 4; ++k) gk[k] = Err(gkp[k], e_conics ? e_conics[4 * row + k] : 0.0, 0.0);
+                ProjGrad<Err> g;
+                projection_vjp<Err>(mean, q, sc, Err(a->opacities[i]), V, P, a->width, a->height,
+                                    Err(a->intrinsics[9 * v]), Err(a->intrinsics[9 * v + 4]), gc, gk, g);
+                for (int k = 0; k < 3; ++k) gm[k] += g.mean[k];
+                for (int k = 0; k < 4; ++k) gq[k] += g.quat[k];
+                for (int k = 0; k < 3; ++k) gs[k] += g.scale[k];
+                go += g.opacity;
+                for (int r = 0; r < 4; ++r)
+                    for (int c = 0; c < 4; ++c) {
+                        if (s_view) sum4(s_view + 4 * (16 * v + 4 * r + c), g.view[r][c]);
+                        if (s_proj) sum4(s_proj + 4 * (16 * v + 4 * r + c), g.proj[r][c]);
+                    }
+            }
+            if (a->sh) {
+                const float* coef = a->sh + v * a->sh_view_stride + (int64_t)3 * K * i;
+                const bool vis = a->radii[row] > 0;
+                float dir[3] = {0.0f, 0.0f, 0.0f};
+                if (a->sh_degree > 0)
+                    for (int k = 0; k < 3; ++k) dir[k] = a->means[3 * i + k] - a->camera_centers[3 * v + k];
+                float color[3], raw[3];
+                sh_eval(coef, dir, a->sh_degree, vis, color, raw);
+                const bool act[3] = {vis && raw[0] >= 0.0f, vis && raw[1] >= 0.0f, vis && raw[2] >= 0.0f};
+                const float* gcol = a->grad_colors + row * a->grad_colors_stride;
+                Err up[3];
+                for (int k = 0; k < 3; ++k) up[k] = Err(gcol[k], e_colors ? e_colors[3 * row + k] : 0.0, 0.0);
+                Err gd[3];
+                sh_backward_row(coef, dir, a->sh_degree, vis, act, up, gco.data(), K, gd);
+                if (b_sh) {
+                    if (a->sh_view_stride == 0) {
+                        for (int e = 0; e < 3 * K; ++e) shsum[e] += gco[e];
+                    } else {
+                        double* dst = b_sh + 2 * (v * a->sh_view_stride + (int64_t)3 * K * i);
+                        for (int e = 0; e < 3 * K; ++e) put2(dst + 2 * e, gco[e]);
+                    }
+                }
+                if (a->sh_degree > 0) {
+                    for (int k = 0; k < 3; ++k) gm[k] += gd[k];
+                    if (s_cc)
+                        for (int k = 0; k < 3; ++k) sum4(s_cc + 4 * (3 * v + k), -gd[k]);
+                }
+            }
+        }
+        if (b_sh && a->sh_view_stride == 0)
+            for (int e = 0; e < 3 * K; ++e) put2(b_sh + 2 * ((int64_t)3 * K * i + e), shsum[e]);
+        if (b_means)
+            for (int k = 0; k < 3; ++k) put2(b_means + 2 * (3 * i + k), gm[k]);
+        if (b_quats) {
+            if (a->normalize_quats) normalize_quat_vjp(quat, qnorm, gq);
+            for (int k = 0; k < 4; ++k) put2(b_quats + 2 * (4 * i + k), gq[k]);
+        }
+        if (b_scales)
+            for (int k = 0; k < 3; ++k) put2(b_scales + 2 * (3 * i + k), gs[k]);
+        if (b_opacities) put2(b_opacities + 2 * i, go);
+    }
+    return 0;
+}
+
+// Running error analysis of oracle_camera_backward: grad_full and
+// grad_centers with error bounds e_full (count,16) and e_centers (count,3)
+// (NULL = exact); writes [p, r] per entry of the (count,4,4) result.
+int oracle_camera_backward_bound(const float* Ks, const float* grad_full, const double* e_full, int32_t width,
+                                 int32_t height, const float* inverse, const float* grad_centers,
+                                 const double* e_centers, int32_t count, double* out) {
+    for (int i = 0; i < count; ++i) {
+        const float* K = Ks + 9 * i;
+        const Err px = Err(2.0f * K[0] / (float)width), py = Err(2.0f * K[4] / (float)height);
+        const Err cx = Err(2.0f * K[2] / (float)width - 1.0f), cy = Err(2.0f * K[5] / (float)height - 1.0f);
+        Err G[16], gcen[3];
+        for (int k = 0; k < 16; ++k)
+            G[k] = grad_full ? Err(grad_full[16 * i + k], e_full ? e_full[16 * i + k] : 0.0, 0.0) : Err(0.0f);
+        for (int k = 0; k < 3; ++k)
+            gcen[k] = grad_centers ? Err(grad_centers[3 * i + k], e_centers ? e_centers[3 * i + k] : 0.0, 0.0)
+                                   : Err(0.0f);
+        for (int row = 0; row < 4; ++row)
+            for (int col = 0; col < 4; ++col) {
+                Err value = Err(0.0f);
+                if (grad_full) {
+                    if (row == 0)
+                        value = px * G[col];
+                    else if (row == 1)
+                        value = py * G[4 + col];
+                    else if (row == 2)
+                        value = (cx * G[col] + cy * G[4 + col]) + G[8 + col] + G[12 + col];
+                }
+                if (grad_centers) {
+                    const float* inv = inverse + 16 * i;
+                    Err vjp = Err(0.0f);
+                    for (int k = 0; k < 3; ++k) vjp += Err(inv[4 * k + row]) * gcen[k];
+                    value -= vjp * Err(inv[4 * col + 3]);
+                }
+                out[2 * (16 * i + 4 * row + col)] = value.p;
+                out[2 * (16 * i + 4 * row + col) + 1] = value.r;
+            }
     }
     return 0;
 }
@@ -1332,9 +1559,18 @@ int oracle_render_fwd(const gs3d_render_args* a) { return render_fwd(a, nullptr)
 
 int oracle_render_fwd_stats(const gs3d_render_args* a, const gs3d_render_stats_args* st) { return render_fwd(a, st); }
 
+}  // extern "C"
+
 // gs3d/render.py:211-356 backward, sequential accumulation per pixel in
 // tile-then-row-major order (the GPU sums the same terms in another order).
-int oracle_render_bwd(const gs3d_render_bwd_args* b) {
+// T is float (the oracle) or Err (the same arithmetic with its running error
+// bound); every term goes to sink.add(kind, index, value) with kind 0
+// centres (views,N,2), 1 conics (views,N,4), 2 absolute centres (views,N,2),
+// 3 features and 4 extra channels (indices in the gradient arrays' layout).
+enum { kSinkCenters, kSinkConics, kSinkAbs, kSinkFeatures, kSinkExtra };
+
+template <class T, class Sink>
+static void render_bwd_core(const gs3d_render_bwd_args* b, Sink& sink) {
     const gs3d_render_args* a = &b->fwd;
     const int W = a->width, H = a->height;
     const int gx = (W + 15) / 16, gy = (H + 15) / 16;
@@ -1346,22 +1582,23 @@ int oracle_render_bwd(const gs3d_render_bwd_args* b) {
             bg[k] = (a->background && k < a->feat_channels) ? a->background[v * a->background_view_stride + k] : 0.0f;
 #pragma omp parallel for schedule(dynamic, 4) num_threads(g_threads)
         for (int y = 0; y < H; ++y) {
-            std::vector<float> grad(D), accum(D), last_color(D), f(D);
+            std::vector<T> grad(D), accum(D), last_color(D);
+            std::vector<float> f(D);
             for (int x = 0; x < W; ++x) {
                 const int64_t tile = (int64_t)v * gx * gy + (y / 16) * gx + (x / 16);
                 const int first = a->ranges[2 * tile], last = a->ranges[2 * tile + 1];
                 const int64_t pix = ((int64_t)v * H + y) * W + x;
                 const float final_T = a->final_t[pix];
-                float T = final_T;
+                T Tr = T(final_T);
                 const int last_contributor = a->contributors[pix];
-                float bg_grad = 0.0f;
+                T bg_grad = T(0.0f);
                 for (int k = 0; k < D; ++k) {
-                    grad[k] = b->upstream[pix * D + k];
-                    bg_grad += bg[k] * grad[k];
-                    accum[k] = 0.0f;
-                    last_color[k] = 0.0f;
+                    grad[k] = T(b->upstream[pix * D + k]);
+                    bg_grad += T(bg[k]) * grad[k];
+                    accum[k] = T(0.0f);
+                    last_color[k] = T(0.0f);
                 }
-                float last_alpha = 0.0f;
+                T last_alpha = T(0.0f);
                 int contributor = last - first;
                 for (int idx = last - 1; idx >= first; --idx) {
                     contributor -= 1;
@@ -1376,50 +1613,147 @@ int oracle_render_bwd(const gs3d_render_bwd_args* b) {
                     const float G = gs_expf(power);
                     const float alpha = std::min(0.99f, conic[3] * G);
                     if (!(alpha >= 1.0f / 255.0f)) continue;
-                    T = T / (1.0f - alpha);
+                    Tr = Tr / T(1.0f - alpha);
                     gather_features(a, v, g, f.data());
-                    float grad_alpha = 0.0f;
+                    T grad_alpha = T(0.0f);
                     for (int k = 0; k < D; ++k) {
-                        accum[k] = last_alpha * last_color[k] + (1.0f - last_alpha) * accum[k];
-                        last_color[k] = f[k];
-                        grad_alpha += (f[k] - accum[k]) * grad[k];
+                        accum[k] = last_alpha * last_color[k] + (T(1.0f) - last_alpha) * accum[k];
+                        last_color[k] = T(f[k]);
+                        grad_alpha += (T(f[k]) - accum[k]) * grad[k];
                         if (k < Dg) {
-                            const float gv = alpha * T * grad[k];
-                            if (k < a->feat_channels) {
-                                if (b->grad_features)
-                                    acc(&b->grad_features[v * b->grad_feat_view_stride + g * b->grad_feat_stride + k],
-                                        gv);
-                            } else if (b->grad_extra) {
-                                acc(&b->grad_extra[v * b->grad_extra_view_stride + g * b->grad_extra_stride +
-                                                   (k - a->feat_channels)],
-                                    gv);
-                            }
+                            const T gv = T(alpha) * Tr * grad[k];
+                            if (k < a->feat_channels)
+                                sink.add(kSinkFeatures, v * b->grad_feat_view_stride + g * b->grad_feat_stride + k, gv);
+                            else
+                                sink.add(kSinkExtra,
+                                         v * b->grad_extra_view_stride + g * b->grad_extra_stride + (k - a->feat_channels),
+                                         gv);
                         }
                     }
-                    grad_alpha = grad_alpha * T + (-final_T / (1.0f - alpha)) * bg_grad;
-                    last_alpha = alpha;
-                    const float gvv = conic[3] * grad_alpha;
+                    grad_alpha = grad_alpha * Tr + T(-final_T / (1.0f - alpha)) * bg_grad;
+                    last_alpha = T(alpha);
+                    const T gvv = T(conic[3]) * grad_alpha;
                     const float gdx = G * dx, gdy = G * dy;
-                    const float dcx = gvv * (-gdx * conic[0] - gdy * conic[1]);
-                    const float dcy = gvv * (-gdy * conic[2] - gdx * conic[1]);
-                    float* gc = b->grad_centers + row * b->grad_centers_stride;
-                    acc(&gc[0], dcx);
-                    acc(&gc[1], dcy);
-                    if (b->abs_centers) {
-                        float* ab = b->abs_centers + row * b->abs_stride;
-                        acc(&ab[0], std::fabs(dcx));
-                        acc(&ab[1], std::fabs(dcy));
-                    }
-                    float* gk = b->grad_conics + row * b->grad_conics_stride;
-                    acc(&gk[0], -0.5f * gdx * dx * gvv);
-                    acc(&gk[1], -gdx * dy * gvv);
-                    acc(&gk[2], -0.5f * gdy * dy * gvv);
-                    acc(&gk[3], G * grad_alpha);
+                    const T dcx = gvv * T(-gdx * conic[0] - gdy * conic[1]);
+                    const T dcy = gvv * T(-gdy * conic[2] - gdx * conic[1]);
+                    sink.add(kSinkCenters, 2 * row, dcx);
+                    sink.add(kSinkCenters, 2 * row + 1, dcy);
+                    sink.add(kSinkAbs, 2 * row, dcx);
+                    sink.add(kSinkAbs, 2 * row + 1, dcy);
+                    sink.add(kSinkConics, 4 * row, T(-0.5f * gdx * dx) * gvv);
+                    sink.add(kSinkConics, 4 * row + 1, T(-gdx * dy) * gvv);
+                    sink.add(kSinkConics, 4 * row + 2, T(-0.5f * gdy * dy) * gvv);
+                    sink.add(kSinkConics, 4 * row + 3, T(G) * grad_alpha);
                 }
             }
         }
     }
+}
+
+// Sink of the oracle: the reference's atomic adds of the float32 terms into
+// the gradient arrays (gs3d/render.py:306-354).  The sums are carried in
+// double and rounded once at the end: the reference's atomics add in an
+// unspecified order, and one sequential float32 sum of the ~10^6 terms of a
+// large Gaussian loses up to 5e-3 of its value (increments below half an ulp
+// of the running sum vanish), far more than any order a GPU adds them in.
+struct RenderGradSink {
+    const gs3d_render_bwd_args* b;
+    std::vector<double> sum[5];
+    explicit RenderGradSink(const gs3d_render_bwd_args* args) : b(args) {
+        const gs3d_render_args& a = b->fwd;
+        const int64_t rows = (int64_t)a.views * a.n;
+        sum[kSinkCenters].assign(2 * rows, 0.0);
+        sum[kSinkConics].assign(4 * rows, 0.0);
+        if (b->abs_centers) sum[kSinkAbs].assign(2 * rows, 0.0);
+        if (b->grad_features)
+            sum[kSinkFeatures].assign(b->grad_feat_view_stride ? a.views * b->grad_feat_view_stride
+                                                               : a.n * b->grad_feat_stride, 0.0);
+        if (b->grad_extra)
+            sum[kSinkExtra].assign(b->grad_extra_view_stride ? a.views * b->grad_extra_view_stride
+                                                             : a.n * b->grad_extra_stride, 0.0);
+    }
+    void add(int kind, int64_t i, float t) {
+        if (sum[kind].empty()) return;
+        double* d = &sum[kind][i];
+        const double v = kind == kSinkAbs ? std::fabs((double)t) : (double)t;
+#pragma omp atomic
+        *d += v;
+    }
+    // Adds the rounded sums to the gradient arrays.
+    void finish() const {
+        for (size_t i = 0; i < sum[kSinkCenters].size(); ++i)
+            b->grad_centers[(i / 2) * b->grad_centers_stride + (i % 2)] += (float)sum[kSinkCenters][i];
+        for (size_t i = 0; i < sum[kSinkConics].size(); ++i)
+            b->grad_conics[(i / 4) * b->grad_conics_stride + (i % 4)] += (float)sum[kSinkConics][i];
+        for (size_t i = 0; i < sum[kSinkAbs].size(); ++i)
+            b->abs_centers[(i / 2) * b->abs_stride + (i % 2)] += (float)sum[kSinkAbs][i];
+        for (size_t i = 0; i < sum[kSinkFeatures].size(); ++i) b->grad_features[i] += (float)sum[kSinkFeatures][i];
+        for (size_t i = 0; i < sum[kSinkExtra].size(); ++i) b->grad_extra[i] += (float)sum[kSinkExtra][i];
+    }
+};
+
+// Sink of the error analysis: per gradient entry, 4 doubles
+// [sum |term|, sum p, sum r, number of terms] in dense per-kind arrays
+// (centres/abs (views*N*2), conics (views*N*4), features and extra in the
+// layout of their gradient arrays).
+struct RenderBoundSink {
+    double* out[5];
+    static void add4(double* q, const Err& t) {
+        double* d = q;
+#pragma omp atomic
+        d[0] += ad(t.v);
+#pragma omp atomic
+        d[1] += t.p;
+#pragma omp atomic
+        d[2] += t.r;
+#pragma omp atomic
+        d[3] += 1.0;
+    }
+    void add(int kind, int64_t i, const Err& t) const {
+        if (out[kind]) add4(out[kind] + 4 * i, kind == kSinkAbs ? Err(std::fabs(t.v), t.p, t.r) : t);
+    }
+};
+
+// Sink of the float64 evaluation (the same template in double arithmetic,
+// the forward decisions still in float32): near-exact gradients against
+// which the error bound is checked.
+struct RenderF64Sink {
+    double* out[5];
+    void add(int kind, int64_t i, double t) const {
+        if (!out[kind]) return;
+        double* d = out[kind] + i;
+#pragma omp atomic
+        *d += kind == kSinkAbs ? std::fabs(t) : t;
+    }
+};
+
+extern "C" {
+
+int oracle_render_bwd(const gs3d_render_bwd_args* b) {
+    RenderGradSink sink(b);
+    render_bwd_core<float>(b, sink);
+    sink.finish();
     return 0;
 }
+
+// Running error analysis of oracle_render_bwd: for every gradient entry the
+// terms' [sum |t|, sum p, sum r, count] (see RenderBoundSink); any of the
+// five outputs may be NULL.
+int oracle_render_bwd_bound(const gs3d_render_bwd_args* b, double* centers, double* conics, double* abs_centers,
+                            double* features, double* extra) {
+    RenderBoundSink sink{{centers, conics, abs_centers, features, extra}};
+    render_bwd_core<Err>(b, sink);
+    return 0;
+}
+
+// oracle_render_bwd evaluated in double (dense outputs in the layouts of
+// the bound's arrays, one double per entry).
+int oracle_render_bwd_f64(const gs3d_render_bwd_args* b, double* centers, double* conics, double* abs_centers,
+                          double* features, double* extra) {
+    RenderF64Sink sink{{centers, conics, abs_centers, features, extra}};
+    render_bwd_core<double>(b, sink);
+    return 0;
+}
+
 
 }  // extern "C"

@@ -46,9 +46,12 @@ def test_argument_errors_are_reported_without_launching():
     assert lib.gs3d_scan_i32(None, -5, None, None, None, 0, None) == abi.GS3D_ERR_ARGUMENT
     args = abi.RenderArgs()
     args.width, args.height, args.views, args.n = 16, 16, 1, 1
-    args.feat_channels, args.one_tail = 70, 1
+    # Any channel count is blended (in windows of up to 64 channels), but an
+    # empty channel vector is an argument error.
+    args.feat_channels, args.one_tail = 0, 0
     args.ranges = args.centers = args.conics = args.features = ctypes.c_void_p(256)
-    assert lib.gs3d_render_fwd(ctypes.byref(args), None) == abi.GS3D_ERR_UNSUPPORTED
+    assert lib.gs3d_render_fwd(ctypes.byref(args), None) == abi.GS3D_ERR_ARGUMENT
+    args.one_tail = 1
     # Statistics: 1..8 requests, kind bits only for existing requests, outputs
     # present for each kind requested.
     args.feat_channels = 3

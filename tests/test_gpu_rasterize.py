@@ -3,17 +3,19 @@
 gs3d.rasterize / gs3d.gsplat.rasterization / gs3d.ops run forward and
 backward on the GPU for a loss sum(image * W) over every blended channel
 (features, extra channels, alpha); the oracle composes the same stages on
-the GPU-normalised quaternions.  Forward images and metadata are bit-exact;
-gradients are within rtol 1e-4 / atol 1e-5 of the gradient scale (atomic
-accumulation order differs).
+the caller's quaternions.  Forward images and metadata are bit-exact; every
+gradient entry is within rtol 1e-4 / atol 1e-5 of the oracle's, or, where
+float32 summation order alone can move it further, within the entry's
+stated float32 error bound (oracle_pipeline.check_gradient).
 """
 
 import numpy as np
 import pytest
 import torch
 
+import oracle
 import oracle_pipeline
-from oracle_pipeline import compare
+from oracle_pipeline import check_gradient, compare
 from dsl_splat_amd import gs3d, synthetic
 from dsl_splat_amd.cameras import PinholeCamera
 from dsl_splat_amd.gs3d import gsplat, ops
@@ -40,8 +42,15 @@ def _run_case(key, entry="rasterize"):
     name = cfg.pop("name")
     background = cfg.pop("background", False)
     scene = synthetic.make_scene(name, **cfg).to(DEV)
+    print(f"case {key} entry={entry} views={scene.viewmats.shape[0]} n={len(scene.means)}", flush=True)
+    return run_scene(scene, entry, background)
+
+
+def run_scene(scene, entry="rasterize", background=False, oracle_threads=None):
+    """Forward + backward of ``scene`` through a public entry point, compared
+    with the oracle pipeline (bit-exact forward, gradient criterion); returns
+    the forward outputs."""
     views = scene.viewmats.shape[0]
-    print(f"case {key} entry={entry} views={views} n={len(scene.means)}", flush=True)
     params = dict(means=scene.means, quats=scene.quats, scales=scene.scales, opacities=scene.opacities)
     leaves = {k: v.clone().requires_grad_(True) for k, v in params.items()}
     colors = (scene.sh_coeffs if scene.sh_coeffs is not None else scene.features).clone().requires_grad_(True)
@@ -70,12 +79,15 @@ def _run_case(key, entry="rasterize"):
     meta["means2d"].retain_grad()
     loss.backward()
     torch.cuda.synchronize()
+    if oracle_threads:
+        oracle.set_threads(oracle_threads)
     ref = oracle_pipeline.run(
         _np(scene.means), _np(scene.quats), _np(scene.scales), _np(scene.opacities), _np(scene.viewmats),
         _np(scene.Ks),
         scene.width, scene.height, features=None if sh else _np(colors), sh=_np(colors) if sh else None,
         sh_degree=scene.sh_degree, extra=None if extra is None else _np(extra),
-        background=None if bg is None else _np(bg), upstream=_np(W), absgrad=scene.absgrad, normalize_quats=True)
+        background=None if bg is None else _np(bg), upstream=_np(W), absgrad=scene.absgrad, normalize_quats=True,
+        bounds=True)
     # Forward: bit-exact images and metadata.
     image = torch.cat([feats] + ([ext] if ext is not None else []) + [alpha], -1)
     np.testing.assert_array_equal(_np(image), ref["image"])
@@ -86,23 +98,26 @@ def _run_case(key, entry="rasterize"):
     np.testing.assert_array_equal(_np(meta["opacities"]), proj["meta_opacities"])
     np.testing.assert_array_equal(_np(meta["tiles_per_gauss"]), proj["tiles"])
     assert meta["backend"] == "gs3d-hip" and meta["n_cameras"] == views
-    # Backward.
-    pg, rg = ref["proj_grads"], ref["render_grads"]
-    tol = lambda a: dict(rtol=1e-4, atol=1e-5 * max(1.0, float(np.abs(a).max())))
-    compare("means", _np(leaves["means"].grad), pg["means"], **tol(pg["means"]))
-    compare("scales", _np(leaves["scales"].grad), pg["scales"], **tol(pg["scales"]))
-    compare("opacities", _np(leaves["opacities"].grad), pg["opacities"], **tol(pg["opacities"]))
-    compare("quats", _np(leaves["quats"].grad), pg["quats"], **tol(pg["quats"]))
-    gcol = pg["sh"] if sh else rg["features"]
-    compare("colors", _np(colors.grad), gcol, **tol(gcol))
+    # Backward: every entry within rtol 1e-4 / atol 1e-5 or its float32 bound.
+    check_gradients(ref, leaves, colors, extra, meta, viewmats, scene, sh)
+    return image, meta, ref
+
+
+def check_gradients(ref, leaves, colors, extra, meta, viewmats, scene, sh):
+    pg, rg, bd = ref["proj_grads"], ref["render_grads"], ref["bounds"]
+    for name in ("means", "scales", "opacities", "quats"):
+        check_gradient(name, _np(leaves[name].grad), pg[name], bd["proj"][name])
+    if sh:
+        check_gradient("sh_coeffs", _np(colors.grad), pg["sh"], bd["proj"]["sh"])
+    else:
+        check_gradient("features", _np(colors.grad), rg["features"], bd["render"]["features"])
     if extra is not None:
-        compare("extra", _np(extra.grad), rg["extra"], **tol(rg["extra"]))
-    compare("means2d", _np(meta["means2d"].grad), rg["centers"], **tol(rg["centers"]))
+        check_gradient("extra", _np(extra.grad), rg["extra"], bd["render"]["extra"])
+    check_gradient("means2d", _np(meta["means2d"].grad), rg["centers"], bd["render"]["centers"])
     if scene.absgrad:
-        compare("absgrad", _np(meta["means2d"].absgrad), rg["abs"], **tol(rg["abs"]))
+        check_gradient("absgrad", _np(meta["means2d"].absgrad), rg["abs"], bd["render"]["abs"])
     if scene.pose_grad:
-        compare("viewmats", _np(viewmats.grad), ref["grad_viewmats"], rtol=1e-3,
-                atol=1e-4 * max(1.0, float(np.abs(ref["grad_viewmats"]).max())))
+        check_gradient("viewmats", _np(viewmats.grad), ref["grad_viewmats"], bd["viewmats"])
 
 
 @pytest.mark.parametrize("key", list(CASES))

@@ -3,8 +3,9 @@
 Integer stages (radii, tile counts, offsets, sorted keys/values, ranges,
 contributors) are compared bit-exactly; the forward float stages follow the
 same operation sequence as the oracle and are compared bit-exactly too;
-gradients (atomically accumulated in another order) within
-rtol 1e-4 / atol 1e-5 relative to the gradient scale.
+every gradient entry (atomically accumulated in another order) is within
+rtol 1e-4 / atol 1e-5 of the oracle's or within its stated float32 error
+bound (oracle_pipeline.check_gradient).
 """
 
 import numpy as np
@@ -12,7 +13,7 @@ import pytest
 import torch
 
 import oracle
-from oracle_pipeline import compare
+from oracle_pipeline import check_gradient, compare
 from dsl_splat_amd import synthetic
 from dsl_splat_amd.gs3d import projection as gproj
 from dsl_splat_amd.gs3d import render as grender
@@ -56,6 +57,25 @@ def _project(scene, sh_degree=None):
         scene.height, 0.2, float("inf"), 0.0, sh=scene.sh_coeffs if sh_degree is not None else None,
         sh_degree=sh_degree or 0, camera_centers=centers if with_centers else None, metadata=True)
     return quats, full, inverse, centers, errors, state
+
+
+def _oracle_project_bwd(*args, **kw):
+    """oracle.project_bwd and the per-entry float32 bounds of its outputs
+    (upstream gradients exact: both sides read the same tensors)."""
+    ref = oracle.project_bwd(*args, **kw)
+    views, n = np.asarray(args[9]).shape
+    zeros = dict(e_centers=np.zeros((views, n, 2)), e_conics=np.zeros((views, n, 4)))
+    if kw.get("sh") is not None:
+        zeros["e_colors"] = np.zeros((views, n, 3))
+    bound = oracle.project_bwd_bound(*args, **zeros, **kw)
+    return ref, bound
+
+
+def _oracle_render_bwd(width, height, ranges, ids, centers, conics, feats, final_t, contributors, up, **kw):
+    """oracle.render_bwd and the per-entry float32 bounds of its outputs."""
+    absgrad = kw.pop("absgrad", False)
+    args = (width, height, ranges, ids, centers, conics, feats, final_t, contributors, up)
+    return oracle.render_bwd(*args, absgrad=absgrad, **kw), oracle.render_bwd_bound(*args, **kw)
 
 
 def test_camera_prepare_bit_exact():
@@ -213,13 +233,13 @@ def test_render_culling_edge_cases():
     record, gf, _ = grender.backward_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats,
                                            out.transmittance, out.contributors, up, scene.width, scene.height,
                                            absgrad=True)
-    ref = oracle.render_bwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]), _np(st.centers),
-                            _np(st.conics), _np(feats), _np(out.transmittance), _np(out.contributors), _np(up),
-                            absgrad=True)
+    ref, bound = _oracle_render_bwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]),
+                                    _np(st.centers), _np(st.conics), _np(feats), _np(out.transmittance),
+                                    _np(out.contributors), _np(up), absgrad=True)
     rec = _np(record)
-    for name, got, want in (("centers", rec[..., 0:2], ref["centers"]), ("conics", rec[..., 2:6], ref["conics"]),
-                            ("abs", rec[..., 6:8], ref["abs"]), ("features", _np(gf), ref["features"])):
-        compare(name, got, want, rtol=1e-4, atol=1e-5 * max(1.0, np.abs(want).max()))
+    for name, got in (("centers", rec[..., 0:2]), ("conics", rec[..., 2:6]), ("abs", rec[..., 6:8]),
+                      ("features", _np(gf))):
+        check_gradient(name, got, ref[name], bound[name])
 
 
 @pytest.mark.parametrize("key,degree,absgrad", [("small_rgb", None, True), ("sh3_4view", 3, False)])
@@ -236,15 +256,60 @@ def test_render_backward_parity(key, degree, absgrad):
     record, gf, _ = grender.backward_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats,
                                            out.transmittance, out.contributors, up, scene.width, scene.height,
                                            background=background, absgrad=absgrad)
-    ref = oracle.render_bwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]), _np(st.centers),
-                            _np(st.conics), _np(feats), _np(out.transmittance), _np(out.contributors), _np(up),
-                            background=_np(background), absgrad=absgrad)
+    ref, bound = _oracle_render_bwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]),
+                                    _np(st.centers), _np(st.conics), _np(feats), _np(out.transmittance),
+                                    _np(out.contributors), _np(up), background=_np(background), absgrad=absgrad)
     rec = _np(record)
-    for name, got, want in (("centers", rec[..., 0:2], ref["centers"]), ("conics", rec[..., 2:6], ref["conics"]),
-                            ("features", _np(gf), ref["features"])):
-        compare(name, got, want, rtol=1e-4, atol=1e-5 * max(1.0, np.abs(want).max()))
+    for name, got in (("centers", rec[..., 0:2]), ("conics", rec[..., 2:6]), ("features", _np(gf))):
+        check_gradient(name, got, ref[name], bound[name])
     if absgrad:
-        compare("abs", rec[..., 6:8], ref["abs"], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(ref["abs"]).max()))
+        check_gradient("abs", rec[..., 6:8], ref["abs"], bound["abs"])
+
+
+# Blended-channel widths D' = features + extra + 1 covering every compiled
+# channel window: one window (D' <= 56: kernels of 4, 8, 16, 36 and 56
+# channels), the geometry window of 56 followed by feature windows (57-64,
+# where all gradient entries no longer fit one 64-lane sum), and forward
+# windows of 64 (D' > 64).
+@pytest.mark.parametrize("feat,extra,absgrad", [(11, 0, True), (15, 0, False), (37, 2, True), (55, 0, True),
+                                                (57, 0, False), (56, 3, True), (60, 3, True), (70, 1, True),
+                                                (128, 2, False)])
+def test_render_channel_windows(feat, extra, absgrad):
+    scene = synthetic.make_scene("small", n=1500, width=72, height=56, seed=feat + extra).to(DEV)
+    D = feat + extra + 1
+    _say(f"render channel windows D'={D} absgrad={absgrad}")
+    quats, full, inverse, centers, st, bins = _frame(scene, None)
+    g = torch.Generator().manual_seed(D)
+    feats = torch.randn((scene.means.shape[0], feat), generator=g).to(DEV)
+    ex = torch.randn((scene.means.shape[0], extra), generator=g).to(DEV) if extra else None
+    background = torch.rand((1, feat), generator=g).to(DEV)
+    out = grender.render_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats, scene.width,
+                               scene.height, extra=ex, background=background)
+    img, ft, ct = oracle.render_fwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]),
+                                    _np(st.centers), _np(st.conics), _np(feats), extra=None if ex is None else _np(ex),
+                                    background=_np(background))
+    np.testing.assert_array_equal(_np(out.contributors), ct)
+    np.testing.assert_array_equal(_np(out.transmittance), ft)
+    np.testing.assert_array_equal(_np(out.stacked()), img)
+    up = torch.randn(out.stacked().shape, generator=g).to(DEV)
+    record, gf, ge = grender.backward_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats,
+                                            out.transmittance, out.contributors, up, scene.width, scene.height,
+                                            extra=ex, background=background, absgrad=absgrad)
+    ref, bound = _oracle_render_bwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]),
+                                    _np(st.centers), _np(st.conics), _np(feats), _np(out.transmittance),
+                                    _np(out.contributors), _np(up), extra=None if ex is None else _np(ex),
+                                    background=_np(background), absgrad=absgrad)
+    rec = _np(record)
+    checks = [("centers", rec[..., 0:2]), ("conics", rec[..., 2:6]), ("features", _np(gf))]
+    if absgrad:
+        checks.append(("abs", rec[..., 6:8]))
+    if extra:
+        checks.append(("extra", _np(ge)))
+    for name, got in checks:
+        check_gradient(name, got, ref[name], bound[name])
+    # Every feature channel received gradient (a window that lost its entries
+    # would leave zeros).
+    assert np.all(np.abs(_np(gf)).max(axis=0) > 0)
 
 
 @pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3), ("sh3_720p", 1)])
@@ -265,20 +330,19 @@ def test_projection_backward_parity(key, degree):
     # The contiguous screen gradient is grad_centers where radii > 0 and zero elsewhere, bit for bit.
     visible = (st.radii > 0).unsqueeze(-1)
     assert torch.equal(res["screen"], torch.where(visible, gc, torch.zeros_like(gc)))
-    ref = oracle.project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+    ref, bound = _oracle_project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
                              _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height, _np(st.radii),
                              _np(gc), _np(gk), sh=_np(scene.sh_coeffs) if degree is not None else None,
                              sh_degree=degree or 0, camera_centers=_np(centers) if degree else None,
                              grad_colors=None if gcol is None else _np(gcol))
     for name in ("means", "quats", "scales", "opacities"):
-        compare(name, _np(res[name]), ref[name], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(ref[name]).max()))
+        check_gradient(name, _np(res[name]), ref[name], bound[name])
     for name in ("view", "projection"):
-        compare(name, _np(res[name]), ref[name], rtol=1e-3, atol=1e-4 * max(1.0, np.abs(ref[name]).max()))
+        check_gradient(name, _np(res[name]), ref[name], bound[name])
     if degree is not None:
-        compare("sh", _np(res["sh"]), ref["sh"], rtol=1e-4, atol=1e-6)
+        check_gradient("sh", _np(res["sh"]), ref["sh"], bound["sh"])
     if degree:
-        compare("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], rtol=1e-3,
-                atol=1e-4 * max(1.0, np.abs(ref["camera_centers"]).max()))
+        check_gradient("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], bound["camera_centers"])
 
 
 @pytest.mark.parametrize("degree", [1, 3])
@@ -312,16 +376,15 @@ def test_projection_sh_shared_many_views(degree):
                                scene.width, scene.height, st.radii, gc, gk, (True,) * 6, sh=scene.sh_coeffs,
                                sh_degree=degree, camera_centers=centers, grad_colors=gcol, need_sh=True,
                                need_centers=True)
-    ref = oracle.project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+    ref, bound = _oracle_project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
                              _np(viewmats), _np(full), _np(Ks), scene.width, scene.height, _np(st.radii),
                              _np(gc), _np(gk), sh=_np(scene.sh_coeffs), sh_degree=degree,
                              camera_centers=_np(centers), grad_colors=_np(gcol))
     got_sh = _np(res["sh"])
     assert np.all(got_sh[..., (degree + 1) ** 2:, :] == 0.0)
-    compare("sh", got_sh, ref["sh"], rtol=1e-4, atol=1e-6)
-    compare("means", _np(res["means"]), ref["means"], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(ref["means"]).max()))
-    compare("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], rtol=1e-3,
-            atol=1e-4 * max(1.0, np.abs(ref["camera_centers"]).max()))
+    check_gradient("sh", got_sh, ref["sh"], bound["sh"])
+    check_gradient("means", _np(res["means"]), ref["means"], bound["means"])
+    check_gradient("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], bound["camera_centers"])
 
 
 @pytest.mark.parametrize("degree", [2, 3])
@@ -349,7 +412,7 @@ def test_projection_per_view_sh_parity(degree):
     res = gproj.backward_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks,
                                scene.width, scene.height, st.radii, gc, gk, (True,) * 6, sh=sh, sh_degree=degree,
                                camera_centers=centers, grad_colors=gcol, need_sh=True, need_centers=True)
-    ref = oracle.project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
+    ref, bound = _oracle_project_bwd(_np(scene.means), _np(quats), _np(scene.scales), _np(scene.opacities),
                              _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height, _np(st.radii),
                              _np(gc), _np(gk), sh=_np(sh), sh_degree=degree, camera_centers=_np(centers),
                              grad_colors=_np(gcol))
@@ -357,10 +420,9 @@ def test_projection_per_view_sh_parity(degree):
     assert got_sh.shape == sh.shape
     kc = (degree + 1) ** 2
     assert np.all(got_sh[..., kc:, :] == 0.0)
-    compare("sh", got_sh, ref["sh"], rtol=1e-4, atol=1e-6)
-    compare("means", _np(res["means"]), ref["means"], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(ref["means"]).max()))
-    compare("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], rtol=1e-3,
-            atol=1e-4 * max(1.0, np.abs(ref["camera_centers"]).max()))
+    check_gradient("sh", got_sh, ref["sh"], bound["sh"])
+    check_gradient("means", _np(res["means"]), ref["means"], bound["means"])
+    check_gradient("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], bound["camera_centers"])
 
 
 @pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3), ("sh3_720p", 0)])
@@ -481,8 +543,8 @@ def test_projection_normalizes_raw_quaternions(key, degree):
     res = gproj.backward_views(scene.means, raw, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks,
                                scene.width, scene.height, st.radii, gc, gk, (True, True, True, True, False, False),
                                normalize_quats=True)
-    rb = oracle.project_bwd(_np(scene.means), _np(raw), _np(scene.scales), _np(scene.opacities),
-                            _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height, _np(st.radii),
-                            _np(gc), _np(gk), normalize_quats=True)
+    rb, bound = _oracle_project_bwd(_np(scene.means), _np(raw), _np(scene.scales), _np(scene.opacities),
+                                    _np(scene.viewmats), _np(full), _np(scene.Ks), scene.width, scene.height,
+                                    _np(st.radii), _np(gc), _np(gk), normalize_quats=True)
     for name in ("means", "quats", "scales", "opacities"):
-        compare(f"raw_{name}", _np(res[name]), rb[name], rtol=1e-4, atol=1e-5 * max(1.0, np.abs(rb[name]).max()))
+        check_gradient(f"raw_{name}", _np(res[name]), rb[name], bound[name])
