@@ -9,6 +9,8 @@
 #include <climits>
 
 #include <type_traits>
+#include <mutex>
+
 #include "common.hpp"
 #include "footprint.hpp"
 
@@ -1475,6 +1477,73 @@ extern "C" int gs3d_sort_pairs_u64(uint64_t* keys, int32_t* values, int64_t coun
 extern "C" int gs3d_sort_pairs_u32(uint32_t* keys, int32_t* values, int64_t count, int32_t end_bit, void* scratch,
                                    size_t scratch_bytes, void* stream) {
     return sort_entry<uint32_t>(keys, values, count, end_bit, scratch, scratch_bytes, stream, 32);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free pair sort (gs3d_sort_pairs_u64_static): the scratch of the
+// radix sort lives in this file-scope device array, one copy per GPU, held
+// until the process ends.  Host code never passes the array's name to a
+// kernel (on the host it is only a stand-in for the symbol): the first call
+// on each device, with that device current, resolves the array's device
+// address with hipGetSymbolAddress and keeps it per device; every launch
+// takes that address.  The sort writes every histogram and scan entry it
+// reads, so nothing has to start at zero.  Calls that overlap on one GPU
+// (other streams or threads) share the array and race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char static_scratch[GS3D_STATIC_SCRATCH_BYTES];
+
+namespace gs3d {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_static_scratch_mutex;
+void* g_static_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// Device address of static_scratch on the device of `stream` (which must be
+// the current device).
+static int static_scratch_address(hipStream_t stream, void** out) {
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+        set_error("gs3d_sort_pairs_u64_static: no usable current device");
+        return GS3D_ERR_LAUNCH;
+    }
+    if (stream) {
+        hipDevice_t stream_device = -1;
+        if (hipStreamGetDevice(stream, &stream_device) != hipSuccess || stream_device != device) {
+            set_error("gs3d_sort_pairs_u64_static: the stream must belong to the current device");
+            return GS3D_ERR_ARGUMENT;
+        }
+    }
+    std::lock_guard<std::mutex> lock(g_static_scratch_mutex);
+    if (!g_static_scratch_ptr[device]) {
+        void* address = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(static_scratch));
+        if (err != hipSuccess || !address) {
+            set_error("gs3d_sort_pairs_u64_static: hipGetSymbolAddress of the static scratch failed");
+            return GS3D_ERR_LAUNCH;
+        }
+        g_static_scratch_ptr[device] = address;
+    }
+    *out = g_static_scratch_ptr[device];
+    return GS3D_OK;
+}
+}  // namespace gs3d
+
+extern "C" int gs3d_sort_pairs_u64_static(uint64_t* keys, int32_t* values, int64_t count, int32_t end_bit,
+                                          void* stream) {
+    if (count < 0 || end_bit < 0 || end_bit > 64) return GS3D_ERR_ARGUMENT;
+    if (count <= 1 || end_bit == 0) return GS3D_OK;
+    if (count > INT32_MAX) return GS3D_ERR_OVERFLOW;
+    if (!keys || !values) return GS3D_ERR_ARGUMENT;
+    if (gs3d_sort_scratch_bytes(count) > (size_t)GS3D_STATIC_SCRATCH_BYTES) {
+        gs3d::set_error("gs3d_sort_pairs_u64_static: count needs more scratch than GS3D_STATIC_SCRATCH_BYTES");
+        return GS3D_ERR_SCRATCH;
+    }
+    void* scratch = nullptr;
+    hipStream_t s = gs3d::as_stream(stream);
+    const int status = gs3d::static_scratch_address(s, &scratch);
+    if (status != GS3D_OK) return status;
+    return gs3d::run_sort<uint64_t>(keys, values, count, end_bit, scratch, s);
 }
 
 extern "C" int gs3d_tile_ranges(const uint64_t* sorted_keys, int64_t count, int32_t* ranges, int64_t tile_count,

@@ -20,6 +20,8 @@ GS3D_ERR_LAUNCH = -2
 GS3D_ERR_UNSUPPORTED = -3
 GS3D_ERR_SCRATCH = -4
 GS3D_ERR_OVERFLOW = -5
+# Static scratch of gs3d_sort_pairs_u64_static (GS3D_STATIC_SCRATCH_BYTES).
+STATIC_SCRATCH_BYTES = 128 << 20
 
 STATUS_NAMES = {
     GS3D_ERR_ARGUMENT: "invalid argument",
@@ -272,6 +274,7 @@ FUNCTIONS = {
     "gs3d_emit_keys": (ctypes.c_int, [ctypes.POINTER(EmitArgs), _P, _SZ, _P]),
     "gs3d_sort_scratch_bytes": (_SZ, [_I64]),
     "gs3d_sort_pairs_u64": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),
+    "gs3d_sort_pairs_u64_static": (ctypes.c_int, [_P, _P, _I64, _I32, _P]),
     "gs3d_tile_ranges": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
     "gs3d_order_rows_scratch_bytes": (_SZ, [_I64]),
     "gs3d_order_rows": (ctypes.c_int, [ctypes.POINTER(OrderArgs), _P, _SZ, _P]),

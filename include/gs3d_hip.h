@@ -231,6 +231,21 @@ int gs3d_sort_pairs_u64(uint64_t* keys, int32_t* values, int64_t count,
                         int32_t end_bit, void* scratch, size_t scratch_bytes,
                         void* stream);
 
+/* Allocation-free variant of gs3d_sort_pairs_u64.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ * Same arguments and result as gs3d_sort_pairs_u64 without the scratch
+ * buffer: the scratch is a static device array of GS3D_STATIC_SCRATCH_BYTES
+ * per GPU (128 MiB, held until the process ends), so count is limited to
+ * gs3d_sort_scratch_bytes(count) <= GS3D_STATIC_SCRATCH_BYTES (about 268M
+ * pairs); larger counts return GS3D_ERR_SCRATCH.  The stream must belong to
+ * the current device.  The call allocates nothing, but every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams or
+ * host threads) race and must be serialised by the caller. */
+#define GS3D_STATIC_SCRATCH_BYTES (128u << 20)
+int gs3d_sort_pairs_u64_static(uint64_t* keys, int32_t* values, int64_t count,
+                               int32_t end_bit, void* stream);
+
 /* Per-tile [first, last) ranges of sorted keys: primitives/tiling.py:39-54
  * (identify_ranges, launched at :87-100).  ranges (tile_count,2) must be
  * zero-initialised by the caller; tile ids >= tile_count (0xFFFFFFFF

@@ -72,6 +72,15 @@ def test_argument_errors_are_reported_without_launching():
     assert lib.gs3d_bin_rows(ctypes.byref(args), None, 0, None) == abi.GS3D_ERR_OVERFLOW
     with pytest.raises(native.NativeLibraryError, match="invalid argument"):
         native.call("gs3d_scan_i32", None, -1, None, None, None, 0, None)
+    # The allocation-free sort rejects counts beyond its static scratch before
+    # touching a device (the pointers are never dereferenced).
+    big = 300_000_000
+    assert native.query("gs3d_sort_scratch_bytes", big) > abi.STATIC_SCRATCH_BYTES
+    assert lib.gs3d_sort_pairs_u64_static(ctypes.c_void_p(256), ctypes.c_void_p(256), big, 45,
+                                          None) == abi.GS3D_ERR_SCRATCH
+    assert b"GS3D_STATIC_SCRATCH_BYTES" in lib.gs3d_last_error()
+    assert lib.gs3d_sort_pairs_u64_static(None, None, 1000, 45, None) == abi.GS3D_ERR_ARGUMENT
+    assert lib.gs3d_sort_pairs_u64_static(None, None, 1, 45, None) == abi.GS3D_OK
 
 
 def test_struct_layout_matches_header(tmp_path):
