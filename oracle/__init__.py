@@ -45,6 +45,7 @@ def lib() -> ctypes.CDLL:
             "oracle_project_bwd": [ctypes.POINTER(abi.ProjectBwdArgs)],
             "oracle_sh_fwd": [P, I32, P, P, I32, I32, P, P],
             "oracle_sh_bwd": [P, I32, P, P, P, P, I32, I32, P, P],
+            "oracle_sh_bwd_bound": [P, I32, P, P, P, P, I32, I32, P, P],
             "oracle_scan_i32": [P, I64, P, P],
             "oracle_emit_keys": [ctypes.POINTER(abi.EmitArgs)],
             "oracle_sort_pairs_u64": [P, P, I64, I32],
@@ -267,6 +268,19 @@ def sh_bwd(coefficients, directions, degree, active, upstream, radii=None):
     lib().oracle_sh_bwd(_ptr(coefficients), rows, _ptr(directions), _ptr(radii), _ptr(active), _ptr(upstream),
                         n, degree, _ptr(gco), _ptr(gdir))
     return gco, gdir
+
+
+def sh_bwd_bound(coefficients, directions, degree, active, upstream, radii=None):
+    """Per-entry bounds B of sh_bwd's (coefficient, direction) gradients."""
+    coefficients, directions, upstream = _f32(coefficients), _f32(directions), _f32(upstream)
+    active = np.ascontiguousarray(active, dtype=np.uint8)
+    n, rows = coefficients.shape[0], coefficients.shape[1]
+    radii = None if radii is None else _i32(radii)
+    bco = np.zeros(coefficients.shape + (2,))
+    bdir = np.zeros((n, 3, 2))
+    lib().oracle_sh_bwd_bound(_ptr(coefficients), rows, _ptr(directions), _ptr(radii), _ptr(active), _ptr(upstream),
+                              n, degree, _ptr(bco), _ptr(bdir))
+    return pair_bound(bco), pair_bound(bdir)
 
 
 def scan_i32(counts):

@@ -1050,6 +1050,32 @@ int oracle_sh_bwd(const float* coefficients, int32_t rows, const float* directio
     return 0;
 }
 
+// Running error analysis of oracle_sh_bwd (exact upstream gradients):
+// [p, r] per entry of the (N,rows,3) coefficient and (N,3) direction
+// gradients.
+int oracle_sh_bwd_bound(const float* coefficients, int32_t rows, const float* directions, const int32_t* radii,
+                        const uint8_t* active, const float* upstream, int32_t n, int32_t degree, double* b_coefficients,
+                        double* b_directions) {
+    std::vector<Err> gco(3 * rows);
+    for (int64_t i = 0; i < n; ++i) {
+        const bool vis = radii ? radii[i] > 0 : true;
+        const bool act[3] = {active[3 * i] != 0, active[3 * i + 1] != 0, active[3 * i + 2] != 0};
+        const Err up[3] = {Err(upstream[3 * i]), Err(upstream[3 * i + 1]), Err(upstream[3 * i + 2])};
+        Err gd[3];
+        sh_backward_row(coefficients + (int64_t)3 * rows * i, directions + 3 * i, degree, vis, act, up, gco.data(),
+                        rows, gd);
+        for (int e = 0; b_coefficients && e < 3 * rows; ++e) {
+            b_coefficients[2 * ((int64_t)3 * rows * i + e)] = gco[e].p;
+            b_coefficients[2 * ((int64_t)3 * rows * i + e) + 1] = gco[e].r;
+        }
+        for (int k = 0; b_directions && k < 3; ++k) {
+            b_directions[2 * (3 * i + k)] = gd[k].p;
+            b_directions[2 * (3 * i + k) + 1] = gd[k].r;
+        }
+    }
+    return 0;
+}
+
 // gs3d/projection.py:213-285 (+ primitives/sh.py:82-138 and the
 // means - centre VJP of gs3d/api.py:160-164).  Sequential accumulation.
 int oracle_project_bwd(const gs3d_project_bwd_args* a) {

@@ -216,3 +216,20 @@ def test_camera_backward_matches_autograd(oracle_lib):
     loss = (P * torch.tensor(g_full, dtype=torch.float64)).sum() + (cen * torch.tensor(g_cent, dtype=torch.float64)).sum()
     (gv,) = torch.autograd.grad(loss, V)
     np.testing.assert_allclose(ours, gv.numpy(), rtol=1e-4, atol=1e-4)
+
+
+def test_logf_is_the_rounded_float64_log(oracle_lib):
+    # The footprint's natural log (splatting/intersections.py:68, wp.log):
+    # a double computation rounded once, so it is the float32 rounding of
+    # the exact log except where that rounding is a near tie; always within
+    # one float32 ulp.  Covers the alpha levels 255*o for o in (1/255, 1]
+    # densely and the rest of the positive float range sparsely.
+    rng = np.random.default_rng(5)
+    levels = np.concatenate([np.linspace(1.0, 255.0, 20001), rng.uniform(1.0, 255.0, 20000),
+                             10.0 ** rng.uniform(-30, 30, 20000)]).astype(np.float32)
+    got = np.array([oracle_lib.logf(float(x)) for x in levels], np.float32)
+    exact = np.log(levels.astype(np.float64))
+    ulp = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got.astype(np.float64) - exact) <= ulp)
+    assert np.mean(got == exact.astype(np.float32)) > 0.9999
+    assert oracle_lib.logf(1.0) == 0.0
