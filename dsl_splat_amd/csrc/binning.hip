@@ -288,41 +288,25 @@ constexpr int kSortThreads = 256;
 constexpr int kSortItems = GS3D_SORT_ITEMS;  // keys per thread of a sort tile
 constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 keys
 constexpr int kRadix = 256;
+#ifndef GS3D_SORT_XCD
+#define GS3D_SORT_XCD 1
+#endif
+#ifndef GS3D_HIST_TILES8
+#define GS3D_HIST_TILES8 4
+#endif
+
+// Workgroups are dispatched to the 8 XCDs in turn; giving every XCD one
+// contiguous range of logical blocks keeps consecutive chunks of a group --
+// and so the consecutive segments of its tiles' lists -- in one L2.
+GS3D_DEV int64_t xcd_contiguous(int64_t b, int64_t nblocks) {
+    constexpr int64_t kXcds = 8;
+    const int64_t per = nblocks / kXcds, rem = nblocks % kXcds;
+    const int64_t xcd = b % kXcds, k = b / kXcds;
+    return xcd * per + min(xcd, rem) + k;
+}
 
 template <class K>
 GS3D_DEV uint32_t digit_of(K key, int shift, uint32_t mask) { return (uint32_t)(key >> shift) & mask; }
-
-// RB: digit width in bits (8 for multi-pass sorts; 10 for a one-pass sort of
-// keys of at most 10 bits).
-template <class K, int RB = 8>
-__global__ __launch_bounds__(kSortThreads) void sort_histogram_kernel(const K* __restrict__ keys, int64_t count,
-                                                                      int shift, uint32_t mask,
-                                                                      uint32_t* __restrict__ counts, int64_t tiles) {
-    constexpr int R = 1 << RB;
-    __shared__ uint32_t s_hist[kSortThreads / 64][R];
-    const int wave = threadIdx.x >> 6;
-    for (int e = threadIdx.x; e < (kSortThreads / 64) * R; e += kSortThreads) (&s_hist[0][0])[e] = 0;
-    const int64_t base = (int64_t)blockIdx.x * kSortTile + wave * (kSortTile / 4) + lane_id();
-    K key[kSortItems];
-#pragma unroll
-    for (int k = 0; k < kSortItems; ++k) {
-        const int64_t idx = base + k * 64;
-        key[k] = idx < count ? keys[idx] : K(0);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kSortItems; ++k) {
-        const int64_t idx = base + k * 64;
-        if (idx < count) atomicAdd(&s_hist[wave][digit_of(key[k], shift, mask)], 1u);
-    }
-    __syncthreads();
-    for (int d = threadIdx.x; d < R; d += kSortThreads) {
-        uint32_t sum = 0;
-#pragma unroll
-        for (int w = 0; w < kSortThreads / 64; ++w) sum += s_hist[w][d];
-        counts[(int64_t)d * tiles + blockIdx.x] = sum;
-    }
-}
 
 // VALS = false sorts keys alone: no value loads, stores or LDS staging, which
 // leaves room for one more block per CU.
@@ -330,7 +314,7 @@ template <class K, class V, bool VALS, int RB = 8>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
     V* __restrict__ vals_out, int64_t count, int shift, uint32_t mask, int bits,
-    const int32_t* __restrict__ scanned, int64_t tiles) {
+    const int32_t* __restrict__ offsets, int64_t tiles) {
     constexpr int R = 1 << RB;
     static_assert(R % kSortThreads == 0, "whole digits per thread");
     __shared__ K s_keys[kSortTile];
@@ -340,7 +324,10 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     __shared__ uint32_t s_scan_wave[kSortThreads / 64];
     const int wave = threadIdx.x >> 6, lane = lane_id();
     for (int e = threadIdx.x; e < (kSortThreads / 64) * R; e += kSortThreads) (&s_wcnt[0][0])[e] = 0;
-    const int64_t tile_base = (int64_t)blockIdx.x * kSortTile;
+    // Consecutive tiles on one XCD: their runs of the same digit are adjacent
+    // in the output, and partial lines merge in that XCD's L2.
+    const int64_t tile = GS3D_SORT_XCD ? xcd_contiguous(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
+    const int64_t tile_base = tile * kSortTile;
     const int64_t valid_count = min((int64_t)kSortTile, count - tile_base);
     K key[kSortItems];
     V val[kSortItems];
@@ -399,7 +386,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
 #pragma unroll
         for (int i = 0; i < M; ++i) {
             const int d = threadIdx.x * M + i;
-            s_gbase[d] = scanned[(int64_t)d * tiles + blockIdx.x] - (int32_t)run;
+            s_gbase[d] = offsets[tile * R + d] - (int32_t)run;
 #pragma unroll
             for (int w = 0; w < kSortThreads / 64; ++w) {
                 s_wcnt[w][d] = run;
@@ -431,10 +418,17 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     }
 }
 
+// Digit counts of the radix sort: a [digit][tile] table (the order in which a
+// stable LSD pass places the keys, so its flat exclusive scan gives every
+// tile's offset for every digit), written by histogram blocks of several
+// consecutive tiles (runs of words instead of one scattered word per digit).
+// The scanned table is transposed to [tile][digit] so that each scatter
+// block reads its offsets as one contiguous row.
 struct SortScratch {
-    uint32_t* counts;     // [256][tiles]
-    int32_t* scanned;     // [256][tiles]
-    void* scan_scratch;   // scan partials for 256*tiles entries
+    uint32_t* counts;     // [R][tiles]
+    int32_t* scanned;     // [R][tiles]
+    int32_t* offsets;     // [tiles][R], the transpose of scanned
+    void* scan_scratch;   // scan partials for R*tiles entries
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -443,20 +437,39 @@ inline size_t sort_scratch_bytes(int64_t count, SortScratch* out, void* base, in
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
     const int64_t entries = tiles << radix_bits;
     const size_t a = align256((size_t)entries * 4);
-    const size_t b = align256((size_t)entries * 4);
     const size_t c = scan_partials_bytes(entries);
     if (out) {
         char* p = reinterpret_cast<char*>(base);
         out->counts = reinterpret_cast<uint32_t*>(p);
         out->scanned = reinterpret_cast<int32_t*>(p + a);
-        out->scan_scratch = p + a + b;
+        out->offsets = reinterpret_cast<int32_t*>(p + 2 * a);
+        out->scan_scratch = p + 3 * a;
     }
-    return a + b + c;
+    return 3 * a + c;
 }
 
-// Sort keys[0:count)/values[0:count) on bits [0, end_bit) using
-// keys[count:2count)/values[count:2count) as the ping-pong buffer; values
-// may be null (keys only).
+// offsets[t][d] = scanned[d][t] through 32x32 LDS tiles (coalesced both ways).
+__global__ __launch_bounds__(256) void transpose_offsets_kernel(const int32_t* __restrict__ scanned, int64_t tiles,
+                                                                int digits, int32_t* __restrict__ offsets) {
+    __shared__ int32_t s[32][33];
+    const int64_t t0 = (int64_t)blockIdx.x * 32;
+    const int d0 = blockIdx.y * 32;
+    const int x = threadIdx.x & 31, y = threadIdx.x >> 5;
+    for (int r = y; r < 32; r += 8) {
+        const int64_t t = t0 + x;
+        if (t < tiles) s[r][x] = scanned[(int64_t)(d0 + r) * tiles + t];
+    }
+    __syncthreads();
+    for (int r = y; r < 32; r += 8) {
+        const int64_t t = t0 + r;
+        if (t < tiles) offsets[t * digits + d0 + x] = s[x][r];
+    }
+}
+
+// Histogram and scan of one sort pass (digits of `bits` bits at `shift`).
+template <class K, int RB>
+int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, const SortScratch& sc, hipStream_t s);
+
 template <class K, class V = int32_t>
 int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipStream_t s) {
     SortScratch sc;
@@ -469,16 +482,14 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
     for (int shift = 0; shift < end_bit; shift += 8) {
         const int bits = end_bit - shift < 8 ? end_bit - shift : 8;
         const uint32_t mask = (1u << bits) - 1u;
-        hipLaunchKernelGGL((sort_histogram_kernel<K>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin, count,
-                           shift, mask, sc.counts, tiles);
-        const int status = run_scan<uint32_t, false>(sc.counts, tiles * kRadix, sc.scanned, nullptr, sc.scan_scratch, s);
+        const int status = sort_counts<K, 8>(kin, count, shift, mask, sc, s);
         if (status != GS3D_OK) return status;
         if (values)
             hipLaunchKernelGGL((sort_scatter_kernel<K, V, true>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin,
-                               vin, kout, vout, count, shift, mask, bits, sc.scanned, tiles);
+                               vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles);
         else
             hipLaunchKernelGGL((sort_scatter_kernel<K, V, false>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin,
-                               vin, kout, vout, count, shift, mask, bits, sc.scanned, tiles);
+                               vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles);
         K* tk = kin;
         kin = kout;
         kout = tk;
@@ -497,10 +508,10 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
     return launch_status("radix sort");
 }
 
-// Histogram of TPB consecutive sort tiles per block, for wide digits: each
-// digit's TPB counts are consecutive in the [digit][tile] layout, so a block
-// writes runs of TPB words instead of one scattered word per digit.  One
-// LDS histogram per tile (pitch R + 1: the transposed read is conflict-free).
+// Histogram of TPB consecutive sort tiles per block: each digit's TPB counts
+// are consecutive in the [digit][tile] layout, so a block writes runs of TPB
+// words instead of one scattered word per digit.  One LDS histogram per tile
+// (pitch R + 1: the transposed read is conflict-free).
 template <class K, int RB, int TPB>
 __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(const K* __restrict__ keys, int64_t count,
                                                                             int shift, uint32_t mask,
@@ -523,26 +534,52 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
 #pragma unroll
         for (int k = 0; k < kSortItems; ++k) {
             const int64_t idx = base + k * kSortThreads + threadIdx.x;
-            if (idx < count) atomicAdd(&s_hist[tt * P + digit_of(key[k], shift, mask)], 1u);
+            const bool valid = idx < count;
+            const uint32_t d = digit_of(key[k], shift, mask);
+            // A wavefront whose valid keys share one digit (high key bits:
+            // exponents, view ids) adds them with one atomic instead of 64
+            // serialised ones on the same LDS word.
+            const uint64_t live = __ballot(valid);
+            const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)d);
+            if (__ballot(valid && d != d0) == 0) {
+                if (live && lane_id() == (int)__builtin_ctzll(live)) atomicAdd(&s_hist[tt * P + d0], (uint32_t)__popcll(live));
+            } else if (valid) {
+                atomicAdd(&s_hist[tt * P + d], 1u);
+            }
         }
     }
     __syncthreads();
     for (int e = threadIdx.x; e < TPB * R; e += kSortThreads) {
         const int d = e / TPB, tt = e - d * TPB;
         const int64_t t = t0 + tt;
-        if (t < tiles) counts[(int64_t)d * tiles + t] = s_hist[tt * P + d];
+        if (t < tiles) counts[(int64_t)d * tiles + t] = s_hist[tt * P + d];  // runs of TPB words
     }
 }
 
-// Start and end of every digit's run in the output of a one-pass sort: the
-// exclusive scan of the [digit][tile] counts holds each digit's start at
-// tile 0.
-__global__ void digit_ranges_kernel(const int32_t* __restrict__ scanned, int64_t tiles, int64_t count, int digits,
+template <class K, int RB>
+int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, const SortScratch& sc, hipStream_t s) {
+    constexpr int R = 1 << RB;
+    // Tiles per histogram block: runs of 16 words (whole 64-byte sectors) for
+    // 8-bit digits; 8 for 10-bit digits, whose LDS histograms are 4x larger.
+    constexpr int TPB = RB > 8 ? 8 : GS3D_HIST_TILES8;
+    const int64_t tiles = (count + kSortTile - 1) / kSortTile;
+    hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
+                       dim3(kSortThreads), 0, s, keys, count, shift, mask, sc.counts, tiles);
+    const int status = run_scan<uint32_t, false>(sc.counts, tiles * R, sc.scanned, nullptr, sc.scan_scratch, s);
+    if (status != GS3D_OK) return status;
+    hipLaunchKernelGGL(transpose_offsets_kernel, dim3((unsigned)((tiles + 31) / 32), R / 32), dim3(256), 0, s,
+                       sc.scanned, tiles, R, sc.offsets);
+    return launch_status("radix sort counts");
+}
+
+// Start and end of every digit's run in the output of a one-pass sort: row
+// 0 of the transposed offsets holds each digit's start.
+__global__ void digit_ranges_kernel(const int32_t* __restrict__ offsets, int64_t count, int digits,
                                     int ranges_count, int32_t* __restrict__ ranges) {
     const int d = blockIdx.x * blockDim.x + threadIdx.x;
     if (d >= ranges_count) return;
-    const int32_t start = scanned[(int64_t)d * tiles];
-    const int32_t end = d + 1 < digits ? scanned[(int64_t)(d + 1) * tiles] : (int32_t)count;
+    const int32_t start = offsets[d];
+    const int32_t end = d + 1 < digits ? offsets[d + 1] : (int32_t)count;
     ranges[2 * d] = start;
     ranges[2 * d + 1] = end;
 }
@@ -562,16 +599,13 @@ int run_sort_once(K* keys, int64_t count, int end_bit, void* scratch, int ranges
     sort_scratch_bytes(count, &sc, scratch, RB);
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
     const uint32_t mask = (1u << end_bit) - 1u;
-    constexpr int TPB = 8;
-    hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
-                       dim3(kSortThreads), 0, s, keys, count, 0, mask, sc.counts, tiles);
-    const int status = run_scan<uint32_t, false>(sc.counts, tiles << RB, sc.scanned, nullptr, sc.scan_scratch, s);
+    const int status = sort_counts<K, RB>(keys, count, 0, mask, sc, s);
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL((sort_scatter_kernel<K, int32_t, false, RB>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
                        keys, (const int32_t*)nullptr, keys + count, (int32_t*)nullptr, count, 0, mask, end_bit,
-                       sc.scanned, tiles);
+                       sc.offsets, tiles);
     hipLaunchKernelGGL(digit_ranges_kernel, dim3((unsigned)((ranges_count + 255) / 256)), dim3(256), 0, s,
-                       sc.scanned, tiles, count, 1 << RB, ranges_count, ranges);
+                       sc.offsets, count, 1 << RB, ranges_count, ranges);
     return launch_status("one-pass radix sort");
 }
 
@@ -1128,15 +1162,6 @@ __global__ void chunk_group_kernel(const int32_t* __restrict__ chunk_base, int g
     chunk_group[u] = lo;
 }
 
-// Workgroups are dispatched to the 8 XCDs in turn; giving every XCD one
-// contiguous range of logical blocks keeps consecutive chunks of a group --
-// and so the consecutive segments of its tiles' lists -- in one L2.
-GS3D_DEV int64_t xcd_contiguous(int64_t b, int64_t nblocks) {
-    constexpr int64_t kXcds = 8;
-    const int64_t per = nblocks / kXcds, rem = nblocks % kXcds;
-    const int64_t xcd = b % kXcds, k = b / kXcds;
-    return xcd * per + min(xcd, rem) + k;
-}
 
 // One wavefront per chunk of kChunk items (kChunkSteps per lane, masks and
 // ids held in registers).  Counts of group g are laid out [g][tile][chunk]

@@ -41,6 +41,13 @@
 #ifndef GS3D_BWD_PIX
 #define GS3D_BWD_PIX 2
 #endif
+// Pixels per lane for 9-36 channels.
+#ifndef GS3D_WIDE_FWD_PIX
+#define GS3D_WIDE_FWD_PIX 1
+#endif
+#ifndef GS3D_WIDE_BWD_PIX
+#define GS3D_WIDE_BWD_PIX 1
+#endif
 
 namespace gs3d {
 
@@ -60,11 +67,13 @@ constexpr int kGeomWindow = 56;
 // Channels of a forward window and of a further backward window.
 constexpr int kWindow = 64;
 
-// Pixels per lane for a channel count (wide vectors keep one pixel per lane
-// to bound register use).
-template <int CH, int P>
+// Pixels per lane for a channel count (the widest vectors keep one pixel per
+// lane to bound register use).
+template <int CH, bool BWD>
 struct PixFor {
-    static constexpr int value = CH <= 8 ? P : 1;
+    static constexpr int value = CH <= 8    ? (BWD ? GS3D_BWD_PIX : GS3D_FWD_PIX)
+                                 : CH <= 36 ? (BWD ? GS3D_WIDE_BWD_PIX : GS3D_WIDE_FWD_PIX)
+                                            : 1;
 };
 
 // Tile-local coordinates of pixel k of thread t.
@@ -767,7 +776,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
 
 template <int CH>
 int launch_fwd(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned blocks, int c0, hipStream_t s) {
-    constexpr int PIX = PixFor<CH, GS3D_FWD_PIX>::value;
+    constexpr int PIX = PixFor<CH, false>::value;
     if (st) {
         hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, true>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a, *st, c0);
         return launch_status("gs3d_render_fwd_stats");
@@ -789,7 +798,7 @@ inline int launch_fwd_window(const gs3d_render_args& a, const gs3d_render_stats_
 
 template <int CH, bool GEOM>
 int launch_bwd(const gs3d_render_bwd_args& b, unsigned blocks, int c0, hipStream_t s) {
-    constexpr int PIX = PixFor<CH, GS3D_BWD_PIX>::value;
+    constexpr int PIX = PixFor<CH, true>::value;
     if constexpr (GEOM) {
         if (b.abs_centers) {
             hipLaunchKernelGGL((render_bwd_kernel<CH, true, PIX, true>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, b, c0);
