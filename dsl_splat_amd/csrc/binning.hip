@@ -1190,10 +1190,51 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     uint32_t* __restrict__ counts, const int32_t* __restrict__ scanned, const int32_t* __restrict__ tile_start,
     int32_t* __restrict__ ids, int64_t id_limit) {
     __shared__ int32_t s_run[WRITE && BUF ? kBinWaves : 1][WRITE && BUF ? kChunk : 1];
+    // Counting rectangles: a 9x9 difference grid per wavefront.
+    constexpr bool RECT_COUNT = !WRITE && !MASKS;
+    __shared__ int32_t s_diff[RECT_COUNT ? kBinWaves : 1][RECT_COUNT ? 96 : 1];
     const int lane = lane_id();
     const int64_t block = xcd_contiguous(blockIdx.x, gridDim.x);
     const int64_t u = block * kBinWaves + (threadIdx.x >> 6);
     if (u >= max_chunks || u >= chunk_base[groups]) return;
+    if constexpr (RECT_COUNT) {
+        // Counts of a chunk of rectangle items: each item adds its
+        // rectangle's four corners to a difference grid; the 2D prefix sum of
+        // the grid at tile t is the number of items covering t.
+        int32_t* diff = s_diff[threadIdx.x >> 6];
+        const int g = chunk_group[u];
+        const int32_t cb = chunk_base[g];
+        const int32_t q = chunk_base[g + 1] - cb;
+        const int32_t s = (int32_t)(u - cb);
+        const int64_t begin = (int64_t)granges[2 * g] + (int64_t)s * kChunk;
+        const int64_t end = min(begin + kChunk, (int64_t)granges[2 * g + 1]);
+        for (int e = lane; e < 96; e += 64) diff[e] = 0;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int k = 0; k < kChunkSteps; ++k) {
+            const int64_t i = begin + k * 64 + lane;
+            if (i < end) {
+                const uint32_t local = (uint32_t)(items[i] >> kGroupBits) & 0xFFFu;
+                const int lx0 = local & 7, lx1 = ((local >> 3) & 7) + 1, ly0 = (local >> 6) & 7,
+                          ly1 = ((local >> 9) & 7) + 1;
+                atomicAdd(&diff[ly0 * 9 + lx0], 1);
+                atomicAdd(&diff[ly0 * 9 + lx1], -1);
+                atomicAdd(&diff[ly1 * 9 + lx0], -1);
+                atomicAdd(&diff[ly1 * 9 + lx1], 1);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int tx = lane & 7, ty = lane >> 3;
+        int32_t c = 0;
+        for (int y = 0; y <= ty; ++y)
+            for (int x = 0; x <= tx; ++x) c += diff[y * 9 + x];
+        counts[(int64_t)cb * 64 + (int64_t)lane * q + s] = (uint32_t)c;
+        return;
+    }
     int32_t* const run_lds = s_run[WRITE && BUF ? threadIdx.x >> 6 : 0];
     const int g = chunk_group[u];
     const int32_t cb = chunk_base[g];
