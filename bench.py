@@ -1,40 +1,50 @@
 #!/usr/bin/env python3
 """Forward+backward benchmark of the MI355X gs3d rasterizer.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads all|headline]
 
-Default workload: 3,000,000 Gaussians, SH degree 3, four 1920x1080 cameras on
-a radius-5 ring around 64 Gaussian clusters (synthetic data drawn from a
+Headline workload: 3,000,000 Gaussians, SH degree 3, four 1920x1080 cameras
+on a radius-5 ring around 64 Gaussian clusters (synthetic data drawn from a
 fixed seed; see dsl_splat_amd.synthetic).  A step is one gs3d.rasterize call
 over all four cameras plus the backward pass of loss = sum(image * W) with W
-~ N(0,1) over the RGB and alpha channels; inputs are resident in HBM before
-the timed region.
+~ N(0,1) over every rendered channel; inputs are resident in HBM before the
+timed region.
+
+The other benchmark workloads (10k Gaussians at 256x256 RGB; 500k at 720p
+SH3 with absgrad; 1M at 1600x1200 with 32 feature channels and a camera-z
+channel; 2M at 1080p SH3 with 5% large Gaussians, pose gradients and
+absgrad) are timed the same way and reported under "workloads".
 
 Prints one JSON line: the headline ms/iter (lower is better), forward and
-backward ms, the HBM roofline of the dominant HBM-bound kernel (algorithmic
-bytes over its HIP-event time on the launch stream), per-stage timings and
-bandwidths, and a CPU baseline (the C++ oracle on the host cores over a
-bounded sample).
+backward ms, stage spans measured with HIP events inside the timed steps,
+their algorithmic bytes and fraction of HBM peak, the (pixel, Gaussian) pair
+counts of the blend stages, the HBM roofline of the projection kernel, and a
+CPU baseline (the C++ oracle on the host cores over a bounded sample).
 """
 
 import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
 ROOFLINE_KERNEL = "gs3d::project_fwd_kernel<true> (EWA projection + metadata of every view, one launch)"
-# rocprofv3 FETCH_SIZE / WRITE_SIZE summary of that kernel on the default workload.
+# rocprofv3 FETCH_SIZE / WRITE_SIZE summary of that kernel on the headline workload.
 TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "project_fwd_kernel_traffic_3M_1080p_4view.md")
+HEADLINE = "sh3_1080p_4view"
+# Benchmark workloads in order (synthetic.make_scene names).
+WORKLOADS = ("small", "sh3_720p", "sh3_1080p_4view", "feat32", "pose_fanout")
+HBM_STAGES = ("project", "order", "bin", "project_bwd")
 
 
 def measured_traffic(workload, n):
     """HBM bytes per launch of the projection kernel, measured with rocprofv3
-    counters (committed summary; default workload only), or None."""
-    if workload != "sh3_1080p_4view" or n is not None or not os.path.exists(TRAFFIC_SUMMARY):
+    counters (committed summary; headline workload only), or None."""
+    if workload != HEADLINE or n is not None or not os.path.exists(TRAFFIC_SUMMARY):
         return None
     with open(TRAFFIC_SUMMARY) as f:
         for line in f:
@@ -48,17 +58,18 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="sh3_1080p_4view")
-    p.add_argument("--n", type=int, default=None, help="override the Gaussian count")
-    p.add_argument("--stage-reps", type=int, default=5)
+    p.add_argument("--workload", default=HEADLINE, help="headline workload")
+    p.add_argument("--workloads", choices=("all", "headline"), default="all",
+                   help="also time the other benchmark workloads")
+    p.add_argument("--workload-steps", type=int, default=5, help="timed steps of each other workload")
+    p.add_argument("--n", type=int, default=None, help="override the headline Gaussian count")
     p.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
     p.add_argument("--tile-mode", choices=("radius", "snugbox", "accutile"), default="radius",
-                   help="tile mode of the timed steps (the headline is the reference's default, radius)")
+                   help="tile_mode of the headline steps (the other modes are timed for comparison)")
     p.add_argument("--mode-steps", type=int, default=5,
-                   help="steps timed in each of the other tile modes (0 skips them)")
+                   help="timed steps per other tile mode on the headline workload (0 skips them)")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
-                   help="also run one elementwise device copy (out = in * 1) of this many MiB, the known-size "
-                        "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
+                   help="also run a device copy of this many MiB (counter calibration under rocprofv3)")
     return p.parse_args()
 
 
@@ -119,146 +130,180 @@ def step_fn(scene, leaves, colors, extra, viewmats, tile_mode="radius"):
     return forward, backward
 
 
-def stage_timings(scene, reps):
-    """HIP-event times (ms) and algorithmic bytes of every stage, measured on
-    the launch stream with the same calls the rasterizer makes."""
+def time_steps(forward, backward, steps, warmup, stage_events=False):
+    """ms per step between two synchronisations, forward and backward HIP
+    event spans, and with stage_events the median span of every stage
+    recorded inside the steps.  Steps follow each other as in a training
+    loop, without a synchronisation between them (each forward synchronises
+    once, on its pair totals), so the host prepares step i+1 while step i's
+    backward runs."""
+    import torch
+    from dsl_splat_amd import profiling
+
+    for _ in range(warmup):
+        backward(forward())
+    torch.cuda.synchronize()
+    events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
+    recorder = profiling.StageEvents() if stage_events else None
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    if recorder is not None:
+        recorder.__enter__()
+    for e0, e1, e2 in events:
+        e0.record()
+        loss = forward()
+        e1.record()
+        backward(loss)
+        e2.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    if recorder is not None:
+        recorder.__exit__(None, None, None)
+    out = dict(ms=(t1 - t0) * 1000.0 / steps,
+               fwd_ms=sum(a.elapsed_time(b) for a, b, _ in events) / steps,
+               bwd_ms=sum(b.elapsed_time(c) for _, b, c in events) / steps)
+    if recorder is not None:
+        out["stages"] = {k: statistics.median(v) for k, v in recorder.spans().items() if v}
+    return out
+
+
+def frame_info(scene):
+    """Projection and binning of the workload's frame (the calls the
+    rasterizer makes) for the byte accounting, and the blend's pair counts
+    from the counting forward pass (outside any timed region)."""
     import torch
     from dsl_splat_amd.gs3d import projection as gproj, render as grender
-    from dsl_splat_amd.primitives import tiling
     from dsl_splat_amd.splatting import binning, cameras
 
-    quats = scene.quats  # raw: the projection kernels normalise them, as rasterize has them do
-    sh = scene.sh_coeffs
-    deg = scene.sh_degree
+    deg, sh = scene.sh_degree, scene.sh_coeffs
     views, n = scene.viewmats.shape[0], len(scene.means)
-    names = ("camera", "project", "order", "bin", "render_fwd", "render_bwd", "project_bwd")
-    acc = {k: 0.0 for k in names}
-    info = {}
     with torch.no_grad():
-        for rep in range(reps + 1):
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(20)]
-            ev[0].record()
-            full, inverse, centers, errors = cameras.launch_prepare(scene.viewmats, scene.Ks, scene.width,
-                                                                    scene.height, deg is not None and deg > 0)
-            ev[1].record()
-            st = gproj.project_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full,
-                                     scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0,
-                                     sh=sh, sh_degree=deg or 0, camera_centers=centers if deg else None,
-                                     metadata=True, normalize_quats=True)
-            ev[2].record()
-            order, offsets, totals = binning.order_rows(st.centers, st.radii, st.depths, scene.width,
-                                                        scene.height)
-            ev[3].record()
-            group_pairs, count = totals.cpu().tolist()
-            ev[4].record()
-            ranges, ids = binning.bin_rows(st.centers, st.radii, order, offsets, group_pairs, count, scene.width,
-                                           scene.height)
-            ev[8].record()
-            feats = st.colors if sh is not None else scene.features
-            extra = scene.extra_features  # blended after the features, before alpha
-            out = grender.render_views(ranges, ids, st.centers, st.conics, feats, scene.width, scene.height,
-                                       extra=extra)
-            ev[9].record()
-            up = scene.loss_weights
-            record, gf, _ = grender.backward_views(ranges, ids, st.centers, st.conics, feats,
-                                                   out.transmittance, out.contributors, up, scene.width,
-                                                   scene.height, extra=extra, absgrad=scene.absgrad)
-            ev[10].record()
-            gproj.backward_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full, scene.Ks,
-                                 scene.width, scene.height, st.radii, record[..., 0:2], record[..., 2:6],
-                                 (True, True, True, True, False, False), sh=sh, sh_degree=deg or 0,
-                                 camera_centers=centers if deg else None, grad_colors=gf if sh is not None else None,
-                                 need_sh=sh is not None, normalize_quats=True)
-            ev[11].record()
-            torch.cuda.synchronize()
-            if rep == 0:
-                tiles = binning.tile_count(scene.width, scene.height, views)
-                groups = views * (((scene.width + 15) // 16 + 7) // 8) * (((scene.height + 15) // 16 + 7) // 8)
-                info = dict(pairs=count, group_pairs=group_pairs, groups=groups, tiles=tiles,
-                            group_passes=1 if groups <= 1024 else math.ceil(int(groups - 1).bit_length() / 8),
-                            rows=views * n,
-                            visible=int((st.radii > 0).sum()),
-                            mean_contributors=float(out.contributors.float().mean()))
-                continue  # warm-up repetition
-            spans = {"camera": (0, 1), "project": (1, 2), "order": (2, 3), "bin": (4, 8), "render_fwd": (8, 9),
-                     "render_bwd": (9, 10), "project_bwd": (10, 11)}
-            for k, (a, b) in spans.items():
-                acc[k] += ev[a].elapsed_time(ev[b]) / reps
-        # The roofline kernel alone, one launch at a time with HIP events
-        # around it, after a 2 GiB read that evicts the L2 and the Infinity
-        # Cache with clean lines: its inputs then come from HBM, as they do
-        # inside a step (back-to-back launches would find the 132 MB of
-        # parameters cached; a fill would leave dirty lines for the kernel to
-        # write back).  The read (~0.3 ms) outlasts the host's enqueueing of
-        # the launch, so no idle time falls between the events.
+        full, inverse, centers, errors = cameras.launch_prepare(scene.viewmats, scene.Ks, scene.width, scene.height,
+                                                                deg is not None and deg > 0)
+        st = gproj.project_views(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats, full,
+                                 scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0, sh=sh, sh_degree=deg or 0,
+                                 camera_centers=centers if deg else None, metadata=True, normalize_quats=True)
+        order, offsets, totals = binning.order_rows(st.centers, st.radii, st.depths, scene.width, scene.height)
+        group_pairs, count = totals.cpu().tolist()
+        ranges, ids = binning.bin_rows(st.centers, st.radii, order, offsets, group_pairs, count, scene.width,
+                                       scene.height)
+        feats = st.colors if sh is not None else scene.features
+        pairs = grender.pair_counts(ranges, ids, st.centers, st.conics, feats, scene.width, scene.height,
+                                    extra=scene.extra_features)
+        torch.cuda.synchronize()
+    tiles = binning.tile_count(scene.width, scene.height, views)
+    groups = views * (((scene.width + 15) // 16 + 7) // 8) * (((scene.height + 15) // 16 + 7) // 8)
+    info = dict(pairs=count, group_pairs=group_pairs, groups=groups, tiles=tiles,
+                group_passes=1 if groups <= 1024 else math.ceil(int(groups - 1).bit_length() / 8),
+                rows=views * n, visible=int((st.radii > 0).sum()), blend_pairs=pairs)
+    return info, dict(full=full, st=st, ranges=ranges, ids=ids, feats=feats)
+
+
+def stage_bytes(scene, info):
+    """Algorithmic bytes of every HBM-bound stage: what its kernels must read
+    and write once each."""
+    M, S, T, R = info["pairs"], info["group_pairs"], info["tiles"], info["rows"]
+    sh = scene.sh_coeffs
+    views, n = scene.viewmats.shape[0], len(scene.means)
+    K = 0 if sh is None else sh.shape[-2]
+    sh_in = 0 if sh is None else (n if sh.ndim == 3 else views * n) * K * 3 * 4
+    return {
+        # params 44 B/G (+ SH once for all views) in; per view centers 8, conics+opacity 16, radii 4,
+        # tiles 4, depth 4, means2d 8, meta opacity 4, meta conic 12 (+ colour 12) out
+        "project": n * 44 + sh_in + views * n * (60 + (12 if sh is not None else 0)),
+        # keys and records (depth 4 + centre 8 + radius 4 in, key 4 + record 8 out); 4 radix passes,
+        # each reading the keys for its histogram (4) and reading + writing (key, record) (24); group
+        # counts (record 8 in, count 4 out); inclusive scan (4 in, 4 out)
+        "order": R * (28 + 4 * (4 + 24) + 12 + 8),
+        # items: records and offsets in (12 B/row), items out (8 B/item); group sort (keys read for the
+        # histogram 8 + read and written 16 per pass; one 10-bit pass up to 1024 groups, whose digit
+        # scan gives the group ranges, else 8-bit passes and a range search, 8 B/item); count and
+        # write passes read items (2 x 8 B); ids out (4 B/pair); tile totals/starts/ranges (16 B/tile)
+        "bin": R * 12 + S * (8 + 24 * info["group_passes"] + (16 if info["group_passes"] == 1 else 24))
+               + M * 4 + T * 16,
+        # params 44 + SH 4K*3 in, per view radii 4 + centre/conic grads 24 (+ colour grads 12) in;
+        # grads 44 + SH out
+        "project_bwd": n * 88 + 2 * sh_in + views * n * (28 + (12 if sh is not None else 0)),
+    }
+
+
+def stage_report(stages, by, info):
+    out = {}
+    for k, ms in stages.items():
+        entry = dict(ms=round(ms, 4))
+        if k in by:
+            gbps = by[k] / (ms * 1e-3) / 1e9
+            entry.update(bytes=by[k], gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4))
+        if k in ("render_fwd", "render_bwd"):
+            p = info["blend_pairs"]
+            entry.update(visited_pairs_per_us=round(p["visited"] / (ms * 1e3), 1),
+                         accepted_pairs_per_us=round(p["accepted"] / (ms * 1e3), 1))
+        out[k] = entry
+    return out
+
+
+def kernel_timings(scene, frame):
+    """The roofline kernel alone, and the forward blend with and without
+    contribution statistics, with HIP events on the launch stream."""
+    import torch
+    from dsl_splat_amd.gs3d import projection as gproj, render as grender
+    from dsl_splat_amd.statistics import PreparedStatistics
+
+    views, n = scene.viewmats.shape[0], len(scene.means)
+    full, st, ranges, ids, feats = (frame[k] for k in ("full", "st", "ranges", "ids", "feats"))
+    out = {}
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.no_grad():
+        # One launch at a time after a 2 GiB read that evicts the L2 and the
+        # Infinity Cache with clean lines: the kernel's inputs then come from
+        # HBM, as inside a step (back-to-back launches would find the 132 MB
+        # of parameters cached; a fill would leave dirty lines for the kernel
+        # to write back).  The read (~0.3 ms) outlasts the host's enqueueing
+        # of the launch, so no idle time falls between the events.  Without
+        # coefficients the call launches the projection kernel only.
         launches = 10
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        flush = torch.ones(512 << 20, dtype=torch.float32, device=quats.device)
-        # (without coefficients: the projection kernel only, no colour launch)
-        project = lambda: gproj.project_views(scene.means, quats, scene.scales, scene.opacities, scene.viewmats, full,
-                                              scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0,
+        flush = torch.ones(512 << 20, dtype=torch.float32, device=scene.means.device)
+        project = lambda: gproj.project_views(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats,
+                                              full, scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0,
                                               metadata=True, normalize_quats=True)
         project()
-        acc["project_kernel"] = 0.0
+        out["project_kernel"] = 0.0
         for _ in range(launches):
             flush.amax()
             e0.record()
             project()
             e1.record()
             torch.cuda.synchronize()
-            acc["project_kernel"] += e0.elapsed_time(e1) / launches
+            out["project_kernel"] += e0.elapsed_time(e1) / launches
         del flush
         # Contribution statistics (a masked count and a weighted sum over
         # per-view pixel maps) observed by the forward blend, against the
         # plain forward blend, both back-to-back.
-        from dsl_splat_amd.statistics import PreparedStatistics
         g = torch.Generator().manual_seed(9)
         hw = scene.width * scene.height
         pv = torch.stack([(torch.rand((views, hw), generator=g) < 0.5).float(), torch.rand((views, hw), generator=g)],
-                         1).to(quats.device)
-        stats = PreparedStatistics((0, 1), pv, torch.zeros((views, 1, n), dtype=torch.int32, device=quats.device),
-                                   torch.zeros((views, 1, n), device=quats.device))
+                         1).to(scene.means.device)
+        stats = PreparedStatistics((0, 1), pv, torch.zeros((views, 1, n), dtype=torch.int32, device=pv.device),
+                                   torch.zeros((views, 1, n), device=pv.device))
         for key, kw in (("render_fwd_kernel", {}), ("render_fwd_stats_kernel", {"statistics": stats})):
             blend = lambda: grender.render_views(ranges, ids, st.centers, st.conics, feats, scene.width,
-                                                 scene.height, **kw)
+                                                 scene.height, extra=scene.extra_features, **kw)
             blend()
             e0.record()
             for _ in range(5):
                 blend()
             e1.record()
             torch.cuda.synchronize()
-            acc[key] = e0.elapsed_time(e1) / 5
-    # Algorithmic bytes of every stage: what its kernels must read and write
-    # once each.
-    M, S, T, R = info["pairs"], info["group_pairs"], info["tiles"], info["rows"]
-    K = 0 if sh is None else sh.shape[-2]
-    sh_in = 0 if sh is None else (n if sh.ndim == 3 else views * n) * K * 3 * 4
-    by = {
-        # params 44 B/G (+ SH once for all views) in; per view centers 8, conics+opacity 16, radii 4,
-        # tiles 4, depth 4, means2d 8, meta opacity 4, meta conic 12 (+ colour 12) out
-        "project": n * 44 + sh_in + views * n * (60 + (12 if sh is not None else 0)),
-        # keys and records (depth 4 + centre 8 + radius 4 in, key 4 + record 8 out), 4 radix passes
-        # over (key, record) (24 per pass), group counts (record 8 in, count 4 out), inclusive scan
-        # (4 in, 4 out)
-        "order": R * (28 + 4 * 24 + 12 + 8),
-        # items: records and offsets in (12 B/row), items out (8 B/item); group sort (16 B/item/pass,
-        # one 10-bit pass up to 1024 groups, whose digit scan gives the group ranges, else 8-bit
-        # passes and a range search over the items, 8 B/item); count and write passes read items
-        # (2 x 8 B); ids out (4 B/pair); tile totals/starts/ranges (16 B/tile)
-        "bin": R * 12 + S * (8 + 16 * info["group_passes"] + (16 if info["group_passes"] == 1 else 24))
-               + M * 4 + T * 16,
-        # params 44 + SH 4K*3 in, per view radii 4 + centre/conic grads 24 (+ colour grads 12) in;
-        # grads 44 + SH out
-        "project_bwd": n * 88 + 2 * sh_in + views * n * (28 + (12 if sh is not None else 0)),
-    }
-    return acc, by, info
+            out[key] = e0.elapsed_time(e1) / 5
+    return out
 
 
-def cpu_baseline(scene):
-    """The C++ oracle (fwd+bwd, OpenMP on the host cores) on one of the
-    workload's cameras at full N and resolution; the per-iteration figure is
-    scaled by the camera count (cameras are independent in the algorithm)."""
-    import numpy as np
+def cpu_baseline(scene, workload):
+    """The C++ oracle (fwd+bwd, OpenMP on the host cores): the workload's
+    first camera at full N and resolution, scaled by the camera count for
+    several cameras (they are independent in the algorithm); for the two
+    small workloads one warm-up and the median of 3 iterations."""
+    import numpy as np  # noqa: F401
     import torch
 
     import oracle
@@ -267,39 +312,101 @@ def cpu_baseline(scene):
     cores = len(os.sched_getaffinity(0))
     oracle.set_threads(cores)
     npy = lambda t: t.detach().cpu().numpy()
-    qn = npy(torch.nn.functional.normalize(scene.quats, dim=-1))
     V, K = npy(scene.viewmats[:1]), npy(scene.Ks[:1])
     W, H = scene.width, scene.height
-    sh = scene.sh_coeffs
-    deg = scene.sh_degree
-    means, scales, opac = npy(scene.means), npy(scene.scales), npy(scene.opacities)
+    sh, deg = scene.sh_coeffs, scene.sh_degree
+    means, quats, scales, opac = npy(scene.means), npy(scene.quats), npy(scene.scales), npy(scene.opacities)
     shn = None if sh is None else npy(sh)
     feats = None if scene.features is None else npy(scene.features)
+    extra = None if scene.extra_features is None else npy(scene.extra_features[0])
     up = npy(scene.loss_weights[:1])
-    t0 = time.perf_counter()
-    full, inverse, centers, err = oracle.camera_prepare(V, K, W, H, bool(deg))
-    proj = oracle.project_fwd(means, qn, scales, opac, V, full, K, W, H, sh=shn, sh_degree=deg or 0,
-                              camera_centers=centers if deg else None, metadata=True)
-    offsets, total = oracle.scan_i32(proj["tiles"].ravel())
-    keys, vals = oracle.emit_keys(proj["centers"], proj["radii"], proj["depths"], offsets, total, W, H)
-    T = ((W + 15) // 16) * ((H + 15) // 16)
-    sk, sv = oracle.sort_pairs(keys, vals, 32 + int(T).bit_length())
-    ranges = oracle.tile_ranges(sk, T)
-    blended = proj["colors"] if shn is not None else feats
-    image, final_t, contrib = oracle.render_fwd(W, H, ranges, sv, proj["centers"], proj["conics"], blended)
-    t1 = time.perf_counter()
-    g = oracle.render_bwd(W, H, ranges, sv, proj["centers"], proj["conics"], blended, final_t, contrib, up,
-                          absgrad=scene.absgrad)
-    oracle.project_bwd(means, qn, scales, opac, V, full, K, W, H, proj["radii"], g["centers"], g["conics"],
-                       sh=shn, sh_degree=deg or 0, camera_centers=centers if deg else None,
-                       grad_colors=g["features"] if shn is not None else None)
-    t2 = time.perf_counter()
+
+    def once():
+        t0 = time.perf_counter()
+        full, inverse, centers, err = oracle.camera_prepare(V, K, W, H, bool(deg))
+        proj = oracle.project_fwd(means, quats, scales, opac, V, full, K, W, H, sh=shn, sh_degree=deg or 0,
+                                  camera_centers=centers if deg else None, metadata=True, normalize_quats=True)
+        offsets, total = oracle.scan_i32(proj["tiles"].ravel())
+        keys, vals = oracle.emit_keys(proj["centers"], proj["radii"], proj["depths"], offsets, total, W, H)
+        T = ((W + 15) // 16) * ((H + 15) // 16)
+        sk, sv = oracle.sort_pairs(keys, vals, 32 + int(T).bit_length())
+        del keys, vals
+        ranges = oracle.tile_ranges(sk, T)
+        del sk
+        blended = proj["colors"] if shn is not None else feats
+        image, final_t, contrib = oracle.render_fwd(W, H, ranges, sv, proj["centers"], proj["conics"], blended,
+                                                    extra=extra)
+        t1 = time.perf_counter()
+        g = oracle.render_bwd(W, H, ranges, sv, proj["centers"], proj["conics"], blended, final_t, contrib, up,
+                              extra=extra, absgrad=scene.absgrad)
+        oracle.project_bwd(means, quats, scales, opac, V, full, K, W, H, proj["radii"], g["centers"], g["conics"],
+                           sh=shn, sh_degree=deg or 0, camera_centers=centers if deg else None,
+                           grad_colors=g["features"] if shn is not None else None, normalize_quats=True)
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+
+    small = workload in ("small", "sh3_720p")
+    if small:
+        once()
+        runs = sorted((once() for _ in range(3)), key=lambda r: r[0] + r[1])
+        fwd, bwd = runs[1]
+        how = "median of 3 iterations after one warm-up"
+    else:
+        fwd, bwd = once()
+        how = "one iteration"
     views = scene.viewmats.shape[0]
-    return dict(value=round((t2 - t0) * 1000.0 * views, 1), unit="ms", cores=cores, kind="port",
-                sample=f"C++ oracle fwd+bwd on camera 1 of {views} (full N, {W}x{H}), "
-                       f"{(t2 - t0):.1f} s measured, scaled x{views} to one iteration; "
-                       f"fwd {(t1 - t0) * 1000 * views:.0f} ms + bwd {(t2 - t1) * 1000 * views:.0f} ms",
-                fwd_ms=round((t1 - t0) * 1000.0 * views, 1), bwd_ms=round((t2 - t1) * 1000.0 * views, 1))
+    scope = f"camera 1 of {views} (full N, {W}x{H}), scaled x{views}" if views > 1 else f"full frame {W}x{H}"
+    return dict(value=round((fwd + bwd) * 1000.0 * views, 1), unit="ms", cores=cores, kind="port",
+                sample=f"C++ oracle fwd+bwd, {scope}; {how}; {(fwd + bwd):.2f} s measured",
+                fwd_ms=round(fwd * 1000.0 * views, 1), bwd_ms=round(bwd * 1000.0 * views, 1))
+
+
+def describe(scene, workload):
+    views = scene.viewmats.shape[0]
+    colour = f"SH degree {scene.sh_degree}" if scene.sh_coeffs is not None else \
+        f"{scene.features.shape[-1]} feature channels" + (" + camera-z channel" if scene.extra_features is not None
+                                                         else "")
+    extras = [s for s, on in (("absgrad", scene.absgrad), ("pose gradients", scene.pose_grad)) if on]
+    return (f"{workload}: N={len(scene.means)}, {views} camera{'s' if views > 1 else ''}, "
+            f"{scene.width}x{scene.height}, {colour}" + (", " + ", ".join(extras) if extras else "") +
+            ", fwd+bwd of sum(image*W)")
+
+
+def run_workload(workload, n, device, steps, warmup, cpu, tile_mode="radius"):
+    """Timed steps (clean, then with stage events) and the workload's
+    accounting; returns (entry, scene, frame, inputs)."""
+    import torch
+
+    log(f"[bench] {workload}: building inputs")
+    inputs = make_inputs(workload, n, device)
+    scene = inputs[0]
+    forward, backward = step_fn(*inputs, tile_mode)
+    log(f"[bench] {workload}: {warmup} warm-up + {steps} timed steps")
+    clean = time_steps(forward, backward, steps, warmup)
+    staged = time_steps(forward, backward, steps, 1, stage_events=True)
+    info, frame = frame_info(scene)
+    by = stage_bytes(scene, info)
+    stages = stage_report(staged["stages"], by, info)
+    hbm = [k for k in ("project", "order", "bin") if k in stages]
+    t13 = sum(stages[k]["ms"] for k in hbm)
+    b13 = sum(by[k] for k in hbm)
+    entry = dict(
+        config=describe(scene, workload),
+        ms=round(clean["ms"], 3), fwd_ms=round(clean["fwd_ms"], 3), bwd_ms=round(clean["bwd_ms"], 3),
+        staged_ms=round(staged["ms"], 3),
+        stages=stages,
+        stages_1_3={"ms": round(t13, 4), "bytes": b13, "gbps": round(b13 / (t13 * 1e-3) / 1e9, 1),
+                    "frac": round(b13 / (t13 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                    "note": "project + order + bin spans inside the steps (the host's read of the pair totals "
+                            "between order and bin is the separate totals_read span)"},
+        pairs=dict(tile_pairs=info["pairs"], group_items=info["group_pairs"], visible_rows=info["visible"],
+                   rows=info["rows"], **info["blend_pairs"]),
+    )
+    torch.cuda.synchronize()
+    if cpu:
+        log(f"[bench] {workload}: CPU baseline (oracle)")
+        entry["cpu_baseline"] = cpu_baseline(scene, workload)
+    return entry, scene, frame, inputs, forward
 
 
 def main():
@@ -316,46 +423,19 @@ def main():
         sys.exit(1)
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
-    log(f"[bench] building inputs: {args.workload}")
-    scene, leaves, colors, extra, viewmats = make_inputs(args.workload, args.n, device)
-    forward, backward = step_fn(scene, leaves, colors, extra, viewmats, args.tile_mode)
-    log(f"[bench] warmup {args.warmup}")
-    for _ in range(args.warmup):
-        backward(forward())
-    torch.cuda.synchronize()
-    log(f"[bench] timing {args.steps} steps")
-    # Steps follow each other as in a training loop: no synchronisation
-    # between them (each forward synchronises once, on its pair totals), so
-    # the host prepares step i+1 while step i's backward runs.  Per-step
-    # forward/backward spans come from events read after the final sync.
-    events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for e0, e1, e2 in events:
-        e0.record()
-        loss = forward()
-        e1.record()
-        backward(loss)
-        e2.record()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms = (t1 - t0) * 1000.0 / args.steps
-    fwd_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in events)
-    bwd_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in events)
-    modes = {args.tile_mode: dict(ms=round(ms, 3), pairs=int(forward.meta["tiles_per_gauss"].sum()))}
+    cpu = args.cpu_baseline == "on"
+    head, scene, frame, inputs, forward = run_workload(args.workload, args.n, device, args.steps, args.warmup, cpu,
+                                                       args.tile_mode)
+    modes = {args.tile_mode: dict(ms=head["ms"], pairs=int(forward.meta["tiles_per_gauss"].sum()))}
     for mode in ("radius", "snugbox", "accutile"):
         if mode == args.tile_mode or args.mode_steps <= 0:
             continue
         log(f"[bench] tile_mode={mode}: {args.mode_steps} steps")
-        f_m, b_m = step_fn(scene, leaves, colors, extra, viewmats, mode)
-        b_m(f_m())
-        torch.cuda.synchronize()
-        ta = time.perf_counter()
-        for _ in range(args.mode_steps):
-            b_m(f_m())
-        torch.cuda.synchronize()
-        modes[mode] = dict(ms=round((time.perf_counter() - ta) * 1000.0 / args.mode_steps, 3),
-                           pairs=int(f_m.meta["tiles_per_gauss"].sum()))
+        f_m, b_m = step_fn(*inputs, mode)
+        t = time_steps(f_m, b_m, args.mode_steps, 1)
+        modes[mode] = dict(ms=round(t["ms"], 3), pairs=int(f_m.meta["tiles_per_gauss"].sum()))
+    log("[bench] kernel timings")
+    kt = kernel_timings(scene, frame)
     if args.copy_calibration_mib > 0:
         src = torch.ones(args.copy_calibration_mib << 18, device=device)
         dst = torch.empty_like(src)
@@ -363,53 +443,44 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] copy calibration: {src.numel() * 4} bytes read and written")
         del src, dst
-    log(f"[bench] {ms:.3f} ms/iter; stage timings")
-    stages, by, info = stage_timings(scene, args.stage_reps)
-    s13 = ("project", "order", "bin")
-    t13 = sum(stages[k] for k in s13)
-    b13 = sum(by[k] for k in s13)
-    kernels = ("project_kernel", "render_fwd_kernel", "render_fwd_stats_kernel")
-    per_stage = {k: dict(ms=round(v, 4)) for k, v in stages.items() if k not in kernels}
-    for k in by:
-        per_stage[k]["gbps"] = round(by[k] / (stages[k] * 1e-3) / 1e9, 1)
-        per_stage[k]["frac"] = round(by[k] / (stages[k] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
-        per_stage[k]["bytes"] = by[k]
+    del frame, inputs
+    torch.cuda.empty_cache()
+    others = {}
+    if args.workloads == "all":
+        for wl in WORKLOADS:
+            if wl == args.workload:
+                continue
+            entry, *_ = run_workload(wl, None, device, args.workload_steps, 2, cpu)
+            others[wl] = entry
+            torch.cuda.empty_cache()
     # The roofline object is the projection forward kernel: HBM-bound, one
     # launch per step, params 44 B/G in and 60 B per view out (the colour
     # kernel's bytes are in the "project" stage); every other stage's
     # bandwidth is in "stages".
     n_g, n_v = len(scene.means), scene.viewmats.shape[0]
     kernel_bytes = n_g * 44 + n_v * n_g * 60
-    kernel_ms = stages["project_kernel"]
+    kernel_ms = kt["project_kernel"]
     achieved = kernel_bytes / (kernel_ms * 1e-3) / 1e9
-    cpu = None
-    if args.cpu_baseline == "on":
-        log("[bench] CPU baseline (oracle)")
-        cpu = cpu_baseline(scene)
-    views = scene.viewmats.shape[0]
     result = {
         "metric": "3DGS fwd+bwd ms/iter @3M Gaussians 1080p SH3; sort/proj HBM GB/s",
-        "value": round(ms, 3),
+        "value": head["ms"],
         "unit": "ms",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 3),
+        "ms_per_step": head["ms"],
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded)",
         "config": {
-            "workload": f"{args.workload}: N={len(scene.means)}, {views} cameras, {scene.width}x{scene.height}, "
-                        f"SH degree {scene.sh_degree}, fwd+bwd of sum(image*W)",
-            "gaussians": len(scene.means), "cameras": views, "width": scene.width, "height": scene.height,
-            "sh_degree": scene.sh_degree, "tile_mode": args.tile_mode, "pairs": info["pairs"],
-            "group_pairs": info["group_pairs"],
-            "visible_rows": info["visible"],
+            "workload": head["config"],
+            "gaussians": n_g, "cameras": n_v, "width": scene.width, "height": scene.height,
+            "sh_degree": scene.sh_degree, "tile_mode": args.tile_mode,
         },
-        "fwd_ms": round(fwd_ms / args.steps, 3),
-        "bwd_ms": round(bwd_ms / args.steps, 3),
+        "fwd_ms": head["fwd_ms"],
+        "bwd_ms": head["bwd_ms"],
         "roofline": {
             "bound": "hbm",
             "kernel": ROOFLINE_KERNEL,
@@ -420,15 +491,19 @@ def main():
             "traffic": measured_traffic(args.workload, args.n),
             "ms": round(kernel_ms, 4),
             "bytes": kernel_bytes,
+            "note": "parameters read once for all views (44 B/G) and 60 B per (view, Gaussian) written; the "
+                    "colour kernel's bytes are in stages.project",
         },
-        "stages_1_3": {"ms": round(t13, 4), "bytes": b13, "gbps": round(b13 / (t13 * 1e-3) / 1e9, 1),
-                       "frac": round(b13 / (t13 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
-        "stages": per_stage,
+        "stages": head["stages"],
+        "stages_1_3": head["stages_1_3"],
+        "staged_ms": head["staged_ms"],
+        "pairs": head["pairs"],
         "tile_modes": modes,
         "statistics": {"requests": "masked count + weighted sum, per-view maps",
-                       "render_fwd_ms": round(stages["render_fwd_kernel"], 4),
-                       "render_fwd_stats_ms": round(stages["render_fwd_stats_kernel"], 4)},
-        "cpu_baseline": cpu,
+                       "render_fwd_ms": round(kt["render_fwd_kernel"], 4),
+                       "render_fwd_stats_ms": round(kt["render_fwd_stats_kernel"], 4)},
+        "cpu_baseline": head.get("cpu_baseline"),
+        "workloads": others,
     }
     print(json.dumps(result), flush=True)
 

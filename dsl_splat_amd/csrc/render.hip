@@ -322,8 +322,15 @@ GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, int view, int
 // Up to 8 channels the kernel is held to 80 VGPRs (6 wavefronts per SIMD
 // instead of 5: 1.180 -> 1.130 ms on RGB); wider channel vectors keep the
 // registers they need.
-template <int CH, int PIX, bool STATS>
-__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 8 ? 6 : 1))) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st, int c0) {
+//
+// MODE: 0 plain; 1 with contribution statistics; 2 also counting (pixel,
+// Gaussian) pairs into counts[0..2]: visited as the reference's loop visits
+// them (list entries up to and including the one that terminates the pixel,
+// the whole list otherwise), evaluated by this kernel (after strip culling,
+// while the pixel is live) and accepted (blended).
+template <int CH, int PIX, int MODE>
+__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 8 ? 6 : 1))) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st, int c0, unsigned long long* counts) {
+    constexpr bool STATS = MODE == 1, COUNTS = MODE == 2;
     constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
     __shared__ float2 s_xy[B];
@@ -339,6 +346,8 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     int px[PIX], py[PIX], last_contributor[PIX];
     bool done[PIX];
     float val[PIX][STATS ? GS3D_MAX_STATISTICS : 1];
+    int visited[PIX];
+    uint32_t evaluated = 0, accepted = 0;
 #pragma unroll
     for (int k = 0; k < PIX; ++k) {
         int lx, ly;
@@ -348,6 +357,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
         fx[k] = (float)px[k];
         fy[k] = (float)py[k];
         done[k] = !(px[k] < a.width && py[k] < a.height);
+        visited[k] = done[k] ? 0 : t.last - t.first;  // the whole list unless the pixel terminates
         T[k] = 1.0f;
         last_contributor[k] = 0;
 #pragma unroll
@@ -395,6 +405,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 for (int k = 0; k < PIX; ++k) {
                     const float dx = g.xy.x - fx[k], dy = g.xy.y - fy[k];
                     const float power = blend_power(g.con.x, g.con.y, g.con.z, dx, dy);
+                    if constexpr (COUNTS) evaluated += done[k] ? 0u : 1u;
                     const bool in = !done[k] && power <= 0.0f && power >= g.cut;
                     float e = 0.0f;
                     if (in) e = blend_exp(power);
@@ -403,6 +414,10 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                     const float next_t = T[k] * (1.0f - alpha);
                     const bool term = take && next_t < 0.0001f;
                     const bool upd = take && !term;
+                    if constexpr (COUNTS) {
+                        visited[k] = term ? contributor : visited[k];
+                        accepted += upd ? 1u : 0u;
+                    }
                     done[k] = done[k] || term;
                     const float w = alpha * T[k];
 #pragma unroll
@@ -498,6 +513,23 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
         if (c0 == 0) {
             a.final_t[pix] = T[k];
             a.contributors[pix] = last_contributor[k];
+        }
+    }
+    if constexpr (COUNTS) {
+        uint64_t v = 0;
+#pragma unroll
+        for (int k = 0; k < PIX; ++k) v += (uint64_t)visited[k];
+        uint64_t e = evaluated, c = accepted;
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) {
+            v += (uint64_t)__shfl_xor((long long)v, d, 64);
+            e += (uint64_t)__shfl_xor((long long)e, d, 64);
+            c += (uint64_t)__shfl_xor((long long)c, d, 64);
+        }
+        if (lane == 0) {
+            atomicAdd(counts, (unsigned long long)v);
+            atomicAdd(counts + 1, (unsigned long long)e);
+            atomicAdd(counts + 2, (unsigned long long)c);
         }
     }
 }
@@ -775,25 +807,31 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
 }
 
 template <int CH>
-int launch_fwd(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned blocks, int c0, hipStream_t s) {
+int launch_fwd(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned long long* counts,
+               unsigned blocks, int c0, hipStream_t s) {
     constexpr int PIX = PixFor<CH, false>::value;
+    const dim3 grid(blocks), block(kTilePixels / PIX);
     if (st) {
-        hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, true>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a, *st, c0);
+        hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1>), grid, block, 0, s, a, *st, c0, nullptr);
         return launch_status("gs3d_render_fwd_stats");
     }
     const gs3d_render_stats_args none = {};
-    hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, false>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, a, none, c0);
+    if (counts) {
+        hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 2>), grid, block, 0, s, a, none, c0, counts);
+        return launch_status("gs3d_render_pair_counts");
+    }
+    hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 0>), grid, block, 0, s, a, none, c0, nullptr);
     return launch_status("gs3d_render_fwd");
 }
 
 // One forward window of `width` channels starting at c0.
-inline int launch_fwd_window(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned blocks, int c0,
-                             int width, hipStream_t s) {
-    if (width <= 4) return launch_fwd<4>(a, st, blocks, c0, s);
-    if (width <= 8) return launch_fwd<8>(a, st, blocks, c0, s);
-    if (width <= 16) return launch_fwd<16>(a, st, blocks, c0, s);
-    if (width <= 36) return launch_fwd<36>(a, st, blocks, c0, s);
-    return launch_fwd<kWindow>(a, st, blocks, c0, s);
+inline int launch_fwd_window(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned long long* counts,
+                             unsigned blocks, int c0, int width, hipStream_t s) {
+    if (width <= 4) return launch_fwd<4>(a, st, counts, blocks, c0, s);
+    if (width <= 8) return launch_fwd<8>(a, st, counts, blocks, c0, s);
+    if (width <= 16) return launch_fwd<16>(a, st, counts, blocks, c0, s);
+    if (width <= 36) return launch_fwd<36>(a, st, counts, blocks, c0, s);
+    return launch_fwd<kWindow>(a, st, counts, blocks, c0, s);
 }
 
 template <int CH, bool GEOM>
@@ -831,7 +869,8 @@ inline unsigned render_blocks(const gs3d_render_args& a) {
 
 namespace gs3d {
 
-int render_fwd(const gs3d_render_args* args, const gs3d_render_stats_args* st, void* stream) {
+int render_fwd(const gs3d_render_args* args, const gs3d_render_stats_args* st, unsigned long long* counts,
+               void* stream) {
     if (!args) return GS3D_ERR_ARGUMENT;
     const gs3d_render_args& a = *args;
     int status = check_render_args(a);
@@ -845,7 +884,8 @@ int render_fwd(const gs3d_render_args* args, const gs3d_render_stats_args* st, v
     hipStream_t s = as_stream(stream);
     // Windows of up to 64 channels; the statistics ride on window 0.
     for (int c0 = 0; c0 < D; c0 += kWindow) {
-        status = launch_fwd_window(a, c0 == 0 ? st : nullptr, blocks, c0, min(kWindow, D - c0), s);
+        status = launch_fwd_window(a, c0 == 0 ? st : nullptr, c0 == 0 ? counts : nullptr, blocks, c0,
+                                   min(kWindow, D - c0), s);
         if (status != GS3D_OK) return status;
     }
     return GS3D_OK;
@@ -854,7 +894,12 @@ int render_fwd(const gs3d_render_args* args, const gs3d_render_stats_args* st, v
 }  // namespace gs3d
 
 extern "C" int gs3d_render_fwd(const gs3d_render_args* args, void* stream) {
-    return gs3d::render_fwd(args, nullptr, stream);
+    return gs3d::render_fwd(args, nullptr, nullptr, stream);
+}
+
+extern "C" int gs3d_render_pair_counts(const gs3d_render_args* args, uint64_t* counts, void* stream) {
+    if (!counts || (reinterpret_cast<uintptr_t>(counts) & 7)) return GS3D_ERR_ARGUMENT;
+    return gs3d::render_fwd(args, nullptr, reinterpret_cast<unsigned long long*>(counts), stream);
 }
 
 extern "C" int gs3d_render_fwd_stats(const gs3d_render_args* args, const gs3d_render_stats_args* stats,
@@ -870,7 +915,7 @@ extern "C" int gs3d_render_fwd_stats(const gs3d_render_args* args, const gs3d_re
     if ((reinterpret_cast<uintptr_t>(st.pixel_values) | reinterpret_cast<uintptr_t>(st.counts) |
          reinterpret_cast<uintptr_t>(st.sums)) & 3)
         return GS3D_ERR_ARGUMENT;
-    return gs3d::render_fwd(args, stats, stream);
+    return gs3d::render_fwd(args, stats, nullptr, stream);
 }
 
 extern "C" int gs3d_render_bwd(const gs3d_render_bwd_args* args, void* stream) {

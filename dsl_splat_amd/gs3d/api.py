@@ -20,6 +20,7 @@ import torch
 from torch import Tensor
 
 from .autograd import Frame, Rasterize, ViewBins
+from .. import profiling
 from .projection import project_views
 from ..cameras import validate_camera_options
 from ..inputs import batch_item, normalize_inputs
@@ -79,6 +80,7 @@ def _sh_degree(features, sh_coeffs, sh_degree) -> int | None:
 def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height, near, far, radius_clip,
                    sh, sh_degree, background, tile_mode="radius") -> Frame:
     """Camera rows, fused projection, depth order, one synchronisation, binning."""
+    profiling.mark("start")
     with_centers = sh_degree is not None and sh_degree > 0
     # One int64 status buffer read back once: [group pairs, tile pairs] and
     # then the cameras' int32 status codes.
@@ -91,6 +93,7 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
         sh=sh if sh_degree is not None else None, sh_degree=sh_degree or 0,
         camera_centers=centers if with_centers else None, metadata=True, normalize_quats=True,
     )
+    profiling.mark("projected")
     # The depth ordering computes every row's footprint in the chosen mode
     # once; it also leaves the mode's tile counts in state.tile_counts (the
     # projection counted radius squares).
@@ -102,7 +105,9 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     # while the device works on the depth order.
     launch = prepare_bin_rows(state.centers, state.radii, order, offsets, width, height, conics=state.conics,
                               tile_mode=tile_mode)
+    profiling.mark("ordered")
     host = status.cpu()
+    profiling.mark("totals_read")
     raise_camera_errors(host[2:].view(torch.int32)[:cameras].tolist())
     group_pairs, count = host[:2].tolist()
     if count <= binning.PAIR_LIMIT and group_pairs <= binning.PAIR_LIMIT:
@@ -110,6 +115,7 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
         bins = [ViewBins(0, cameras, ranges, ids)]
     else:
         bins = _bin_view_groups(state, width, height, tile_mode)
+    profiling.mark("binned")
     return Frame(
         width, height, Ks.detach(), full, inverse if with_centers else None, centers if with_centers else None,
         state, bins, count, sh_degree, background,

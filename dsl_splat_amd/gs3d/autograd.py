@@ -21,6 +21,7 @@ from torch import Tensor
 from torch.autograd.function import once_differentiable
 
 from . import projection, render
+from .. import profiling
 from ..runtime.gradients import AbsGradientTarget
 from ..splatting.cameras import camera_backward
 from ..statistics import PreparedStatistics
@@ -113,6 +114,7 @@ class Rasterize(torch.autograd.Function):
             output = render.RenderedPixels(*(
                 None if getattr(parts[0], f) is None else torch.cat([getattr(p, f) for p in parts])
                 for f in ("features", "extra", "alpha", "transmittance", "contributors")))
+        profiling.mark("blended")
         if grad_enabled and any(ctx.needs_input_grad[:8]):
             ctx.save_for_backward(means, quats, scales, opacities, colors, extra_features, viewmats,
                                   output.transmittance, output.contributors)
@@ -141,6 +143,7 @@ class Rasterize(torch.autograd.Function):
         sh = frame.sh_degree is not None
         blended = st.colors if sh else colors
         absgrad = ctx.absolute is not None and any(t is not None for t in ctx.absolute)
+        profiling.mark("backward")
         upstream = (grad_features, grad_extra_image, grad_alpha)
         blend_args = dict(one_tail=True, absgrad=absgrad, need_features=sh or needs[4], need_extra=needs[5])
         if len(frame.bins) == 1:
@@ -173,6 +176,7 @@ class Rasterize(torch.autograd.Function):
             for c, target in enumerate(ctx.absolute):
                 if target is not None:
                     target.write(record[c, :, 6:8])
+        profiling.mark("blend_vjp")
         grad_centers = record[..., 0:2]
         grad_conics = record[..., 2:6]
         proj_needs = (needs[0], needs[1], needs[2], needs[3], needs[6], needs[6])
@@ -187,6 +191,7 @@ class Rasterize(torch.autograd.Function):
                 grad_colors=grad_blended if sh else None, need_sh=sh and needs[4], normalize_quats=True,
                 need_centers=sh and (frame.sh_degree or 0) > 0 and needs[6], need_screen=needs[7],
             )
+        profiling.mark("projection_vjp")
         if grads["screen"] is not None:
             # Contiguous rows: the means2d leaf accumulates them without a strided copy.
             grad_centers = grads["screen"]
@@ -198,6 +203,7 @@ class Rasterize(torch.autograd.Function):
             if grads["view"] is not None:
                 grad_view = grad_view + grads["view"]
             grad_view = grad_view.reshape(viewmats.shape)
+        profiling.mark("camera_vjp")
         return (
             grads["means"] if needs[0] else None,
             grads["quats"] if needs[1] else None,

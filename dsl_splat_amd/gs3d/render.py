@@ -193,3 +193,29 @@ def backward_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor,
         b.grad_extra_view_stride = n * extra.shape[-1] if extra.ndim == 3 else 0
     native.call("gs3d_render_bwd", ctypes.byref(b), native.stream(device))
     return record, grad_features, grad_extra
+
+
+@torch.no_grad()
+def pair_counts(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, features: Tensor, width: int,
+                height: int, *, extra: Tensor | None = None, background: Tensor | None = None,
+                one_tail: bool = True) -> dict[str, int]:
+    """(pixel, Gaussian) pairs of one blend of all views: visited as the
+    reference's loop visits them, evaluated by the forward kernel after its
+    strip culling, and accepted (blended).  A measurement aid: runs the
+    forward blend once more (its image is discarded)."""
+    views, n = centers.shape[0], centers.shape[1]
+    keep = []
+    a, _ = _args(width, height, views, n, ranges, ids, centers, conics, features, extra, background, one_tail, keep)
+    f32 = dict(dtype=torch.float32, device=centers.device)
+    planes = [torch.empty((views, height, width, a.feat_channels), **f32),
+              torch.empty((views, height, width, max(a.extra_channels, 1)), **f32),
+              torch.empty((views, height, width), **f32), torch.empty((views, height, width), **f32),
+              torch.empty((views, height, width), dtype=torch.int32, device=centers.device)]
+    a.image = native.ptr(planes[0])
+    a.image_extra = native.ptr(planes[1]) if a.extra_channels else None
+    a.image_alpha = native.ptr(planes[2]) if one_tail else None
+    a.final_t, a.contributors = native.ptr(planes[3]), native.ptr(planes[4])
+    counts = torch.zeros(3, dtype=torch.int64, device=centers.device)
+    native.call("gs3d_render_pair_counts", ctypes.byref(a), native.ptr(counts), native.stream(centers.device))
+    visited, evaluated, accepted = counts.tolist()
+    return dict(visited=visited, evaluated=evaluated, accepted=accepted)

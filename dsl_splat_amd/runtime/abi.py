@@ -284,6 +284,7 @@ FUNCTIONS = {
     "gs3d_sort_pairs_u32": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),
     "gs3d_expand_keys": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _I32, _P, _P]),
     "gs3d_render_fwd": (ctypes.c_int, [ctypes.POINTER(RenderArgs), _P]),
+    "gs3d_render_pair_counts": (ctypes.c_int, [ctypes.POINTER(RenderArgs), _P, _P]),
     "gs3d_render_fwd_stats": (ctypes.c_int, [ctypes.POINTER(RenderArgs), ctypes.POINTER(RenderStatsArgs), _P]),
     "gs3d_render_bwd": (ctypes.c_int, [ctypes.POINTER(RenderBwdArgs), _P]),
 }

@@ -368,6 +368,16 @@ typedef struct gs3d_render_args {
 
 int gs3d_render_fwd(const gs3d_render_args* args, void* stream);
 
+/* Measurement aid, no counterpart in the reference: gs3d_render_fwd (same
+ * outputs) that also adds to counts[0..2] (device uint64, accumulated: the
+ * caller zeroes them) the (pixel, Gaussian) pairs of the frame that the
+ * reference's blend loop (gs3d/render.py:82-117) visits (list entries up to
+ * and including the one that terminates the pixel, the whole list
+ * otherwise), those this kernel evaluates (after strip culling, while the
+ * pixel is live) and those it accepts (blends).  Used to normalise the
+ * blend kernels' instruction counts. */
+int gs3d_render_pair_counts(const gs3d_render_args* args, uint64_t* counts, void* stream);
+
 /* ------------------------------------------------------------------------
  * Contribution statistics observed by the forward blend: statistics.py:16-156
  * (MaskedContributionCount, WeightedContributionSum, make_observer at

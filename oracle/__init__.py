@@ -51,6 +51,7 @@ def lib() -> ctypes.CDLL:
             "oracle_sort_pairs_u64": [P, P, I64, I32],
             "oracle_tile_ranges": [P, I64, P, I64],
             "oracle_render_fwd": [ctypes.POINTER(abi.RenderArgs)],
+            "oracle_render_pair_counts": [ctypes.POINTER(abi.RenderArgs), P],
             "oracle_tile_footprint": [I32, P, P, I32, I32, I32, P, P],
             "oracle_logf": [ctypes.c_float],
             "oracle_normalize_quats": [P, I64, P, P, P],
@@ -392,6 +393,21 @@ def render_fwd(width, height, ranges, ids, centers, conics, features, extra=None
     a.image, a.final_t, a.contributors = _ptr(image), _ptr(final_t), _ptr(contributors)
     lib().oracle_render_fwd(ctypes.byref(a))
     return image, final_t, contributors
+
+
+def render_pair_counts(width, height, ranges, ids, centers, conics, features, extra=None, background=None):
+    """(visited, accepted) (pixel, Gaussian) pairs of the blend loop
+    (gs3d/render.py:82-117): entries visited up to and including the one
+    that terminates a pixel, and blends."""
+    keep = []
+    a, c, n, channels = _render_args(width, height, ranges, ids, centers, conics, features, extra, background, keep)
+    image = np.zeros((c, height, width, channels), np.float32)
+    final_t = np.zeros((c, height, width), np.float32)
+    contributors = np.zeros((c, height, width), np.int32)
+    a.image, a.final_t, a.contributors = _ptr(image), _ptr(final_t), _ptr(contributors)
+    counts = np.zeros(2, np.int64)
+    lib().oracle_render_pair_counts(ctypes.byref(a), _ptr(counts))
+    return int(counts[0]), int(counts[1])
 
 
 def render_fwd_stats(width, height, ranges, ids, centers, conics, features, kinds, pixel_values, extra=None,

@@ -1533,16 +1533,17 @@ static void observe(const gs3d_render_stats_args* st, int v, int n, int64_t g, i
 
 // gs3d/render.py:36-126 forward, one pixel at a time.  With statistics the
 // pixels run in order on one thread (the observer accumulates).
-static int render_fwd(const gs3d_render_args* a, const gs3d_render_stats_args* st) {
+static int render_fwd(const gs3d_render_args* a, const gs3d_render_stats_args* st, int64_t* pair_counts = nullptr) {
     const int W = a->width, H = a->height;
     const int gx = (W + 15) / 16, gy = (H + 15) / 16;
     const int D = total_channels(a);
     std::vector<float> bg(D);
     const int threads = st ? 1 : g_threads;
+    int64_t visited_all = 0, accepted_all = 0;
     for (int v = 0; v < a->views; ++v) {
         for (int k = 0; k < D; ++k)
             bg[k] = (a->background && k < a->feat_channels) ? a->background[v * a->background_view_stride + k] : 0.0f;
-#pragma omp parallel for schedule(dynamic, 4) num_threads(threads)
+#pragma omp parallel for schedule(dynamic, 4) num_threads(threads) reduction(+ : visited_all, accepted_all)
         for (int y = 0; y < H; ++y) {
             std::vector<float> color(D), f(D);
             for (int x = 0; x < W; ++x) {
@@ -1570,7 +1571,9 @@ static int render_fwd(const gs3d_render_args* a, const gs3d_render_stats_args* s
                     if (st) observe(st, v, a->n, g, (int64_t)y * W + x, (int64_t)W * H, w);
                     T = next_t;
                     last_contributor = contributor;
+                    accepted_all += 1;
                 }
+                visited_all += contributor;  // entries the loop visited, the terminating one included
                 const int64_t pix = ((int64_t)v * H + y) * W + x;
                 for (int k = 0; k < D; ++k) a->image[pix * D + k] = fmaf(T, bg[k], color[k]);
                 a->final_t[pix] = T;
@@ -1578,10 +1581,18 @@ static int render_fwd(const gs3d_render_args* a, const gs3d_render_stats_args* s
             }
         }
     }
+    if (pair_counts) {
+        pair_counts[0] = visited_all;
+        pair_counts[1] = accepted_all;
+    }
     return 0;
 }
 
 int oracle_render_fwd(const gs3d_render_args* a) { return render_fwd(a, nullptr); }
+
+// render_fwd and the (pixel, Gaussian) pairs its loop visits and accepts
+// (counts[0], counts[1]).
+int oracle_render_pair_counts(const gs3d_render_args* a, int64_t* counts) { return render_fwd(a, nullptr, counts); }
 
 int oracle_render_fwd_stats(const gs3d_render_args* a, const gs3d_render_stats_args* st) { return render_fwd(a, st); }
 

@@ -548,3 +548,22 @@ def test_projection_normalizes_raw_quaternions(key, degree):
                                     _np(st.radii), _np(gc), _np(gk), normalize_quats=True)
     for name in ("means", "quats", "scales", "opacities"):
         check_gradient(f"raw_{name}", _np(res[name]), rb[name], bound[name])
+
+
+@pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3)])
+def test_blend_pair_counts_match_the_reference_loop(key, degree):
+    # gs3d_render_pair_counts: visited pairs (list entries up to and
+    # including the terminating one, gs3d/render.py:82-117) and accepted
+    # blends are exact counts of the reference loop; the kernel's evaluated
+    # pairs (after strip culling) lie between them.
+    scene = _scene(key)
+    _say(f"blend pair counts {key}")
+    quats, full, inverse, centers, st, bins = _frame(scene, degree)
+    feats = st.colors if degree is not None else scene.features
+    got = grender.pair_counts(bins["ranges"], bins["point_list"], st.centers, st.conics, feats, scene.width,
+                              scene.height)
+    visited, accepted = oracle.render_pair_counts(scene.width, scene.height, _np(bins["ranges"]),
+                                                  _np(bins["point_list"]), _np(st.centers), _np(st.conics),
+                                                  _np(feats))
+    assert (got["visited"], got["accepted"]) == (visited, accepted)
+    assert accepted <= got["evaluated"] <= visited and accepted > 0
