@@ -314,7 +314,7 @@ template <class K, class V, bool VALS, int RB = 8>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
     V* __restrict__ vals_out, int64_t count, int shift, uint32_t mask, int bits,
-    const int32_t* __restrict__ offsets, int64_t tiles) {
+    const int32_t* __restrict__ offsets, int64_t tiles, int digits) {
     constexpr int R = 1 << RB;
     static_assert(R % kSortThreads == 0, "whole digits per thread");
     __shared__ K s_keys[kSortTile];
@@ -386,7 +386,8 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
 #pragma unroll
         for (int i = 0; i < M; ++i) {
             const int d = threadIdx.x * M + i;
-            s_gbase[d] = offsets[tile * R + d] - (int32_t)run;
+            // Digits at or beyond `digits` (the offsets' row length) hold no key.
+            s_gbase[d] = d < digits ? offsets[tile * digits + d] - (int32_t)run : 0;
 #pragma unroll
             for (int w = 0; w < kSortThreads / 64; ++w) {
                 s_wcnt[w][d] = run;
@@ -466,9 +467,11 @@ __global__ __launch_bounds__(256) void transpose_offsets_kernel(const int32_t* _
     }
 }
 
-// Histogram and scan of one sort pass (digits of `bits` bits at `shift`).
+// Histogram and scan of one sort pass (digits of `bits` bits at `shift`;
+// every key's digit below `digits`, a multiple of 32 up to 1 << RB).
 template <class K, int RB>
-int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, const SortScratch& sc, hipStream_t s);
+int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
+                hipStream_t s);
 
 template <class K, class V = int32_t>
 int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipStream_t s) {
@@ -482,14 +485,14 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
     for (int shift = 0; shift < end_bit; shift += 8) {
         const int bits = end_bit - shift < 8 ? end_bit - shift : 8;
         const uint32_t mask = (1u << bits) - 1u;
-        const int status = sort_counts<K, 8>(kin, count, shift, mask, sc, s);
+        const int status = sort_counts<K, 8>(kin, count, shift, mask, 256, sc, s);
         if (status != GS3D_OK) return status;
         if (values)
             hipLaunchKernelGGL((sort_scatter_kernel<K, V, true>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin,
-                               vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles);
+                               vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256);
         else
             hipLaunchKernelGGL((sort_scatter_kernel<K, V, false>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin,
-                               vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles);
+                               vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256);
         K* tk = kin;
         kin = kout;
         kout = tk;
@@ -516,7 +519,7 @@ template <class K, int RB, int TPB>
 __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(const K* __restrict__ keys, int64_t count,
                                                                             int shift, uint32_t mask,
                                                                             uint32_t* __restrict__ counts,
-                                                                            int64_t tiles) {
+                                                                            int64_t tiles, int digits) {
     constexpr int R = 1 << RB, P = R + 1;
     __shared__ uint32_t s_hist[TPB * P];
     for (int e = threadIdx.x; e < TPB * P; e += kSortThreads) s_hist[e] = 0;
@@ -549,7 +552,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
         }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < TPB * R; e += kSortThreads) {
+    for (int e = threadIdx.x; e < TPB * digits; e += kSortThreads) {
         const int d = e / TPB, tt = e - d * TPB;
         const int64_t t = t0 + tt;
         if (t < tiles) counts[(int64_t)d * tiles + t] = s_hist[tt * P + d];  // runs of TPB words
@@ -557,18 +560,18 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
 }
 
 template <class K, int RB>
-int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, const SortScratch& sc, hipStream_t s) {
-    constexpr int R = 1 << RB;
+int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
+                hipStream_t s) {
     // Tiles per histogram block: runs of 16 words (whole 64-byte sectors) for
     // 8-bit digits; 8 for 10-bit digits, whose LDS histograms are 4x larger.
     constexpr int TPB = RB > 8 ? 8 : GS3D_HIST_TILES8;
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
     hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
-                       dim3(kSortThreads), 0, s, keys, count, shift, mask, sc.counts, tiles);
-    const int status = run_scan<uint32_t, false>(sc.counts, tiles * R, sc.scanned, nullptr, sc.scan_scratch, s);
+                       dim3(kSortThreads), 0, s, keys, count, shift, mask, sc.counts, tiles, digits);
+    const int status = run_scan<uint32_t, false>(sc.counts, tiles * digits, sc.scanned, nullptr, sc.scan_scratch, s);
     if (status != GS3D_OK) return status;
-    hipLaunchKernelGGL(transpose_offsets_kernel, dim3((unsigned)((tiles + 31) / 32), R / 32), dim3(256), 0, s,
-                       sc.scanned, tiles, R, sc.offsets);
+    hipLaunchKernelGGL(transpose_offsets_kernel, dim3((unsigned)((tiles + 31) / 32), digits / 32), dim3(256), 0, s,
+                       sc.scanned, tiles, digits, sc.offsets);
     return launch_status("radix sort counts");
 }
 
@@ -599,13 +602,16 @@ int run_sort_once(K* keys, int64_t count, int end_bit, void* scratch, int ranges
     sort_scratch_bytes(count, &sc, scratch, RB);
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
     const uint32_t mask = (1u << end_bit) - 1u;
-    const int status = sort_counts<K, RB>(keys, count, 0, mask, sc, s);
+    // Only the digits of the key range are counted, scanned and transposed
+    // (the keys are below ranges_count).
+    const int digits = min(1 << RB, (ranges_count + 31) & ~31);
+    const int status = sort_counts<K, RB>(keys, count, 0, mask, digits, sc, s);
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL((sort_scatter_kernel<K, int32_t, false, RB>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
                        keys, (const int32_t*)nullptr, keys + count, (int32_t*)nullptr, count, 0, mask, end_bit,
-                       sc.offsets, tiles);
+                       sc.offsets, tiles, digits);
     hipLaunchKernelGGL(digit_ranges_kernel, dim3((unsigned)((ranges_count + 255) / 256)), dim3(256), 0, s,
-                       sc.offsets, count, 1 << RB, ranges_count, ranges);
+                       sc.offsets, count, digits, ranges_count, ranges);
     return launch_status("one-pass radix sort");
 }
 
@@ -1189,7 +1195,9 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     const int32_t* __restrict__ chunk_group, int groups, int64_t max_chunks, GridDims d,
     uint32_t* __restrict__ counts, const int32_t* __restrict__ scanned, const int32_t* __restrict__ tile_start,
     int32_t* __restrict__ ids, int64_t id_limit) {
-    __shared__ int32_t s_run[WRITE && BUF ? kBinWaves : 1][WRITE && BUF ? kChunk : 1];
+    // A chunk's run for one tile, then one slot per lane that rejected items
+    // are written to (so the writes need neither a branch nor an exec mask).
+    __shared__ int32_t s_run[WRITE && BUF ? kBinWaves : 1][WRITE && BUF ? kChunk + 64 : 1];
     // Counting rectangles: a 9x9 difference grid per wavefront.
     constexpr bool RECT_COUNT = !WRITE && !MASKS;
     __shared__ int32_t s_diff[RECT_COUNT ? kBinWaves : 1][RECT_COUNT ? 96 : 1];
@@ -1289,17 +1297,18 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
                 const uint32_t word = H ? (uint32_t)(mask[k] >> 32) : (uint32_t)mask[k];
                 const bool has = (word & bit) != 0u;
                 const uint64_t b = __ballot(has);
-                if (b) {
+                if constexpr (WRITE && BUF) {
+                    const uint32_t rank =
+                        __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+                    run_lds[has ? run + rank : (uint32_t)(kChunk + lane)] = id[k];
+                    run += (uint32_t)__popcll(b);
+                } else if (b) {
                     if constexpr (WRITE) {
                         if (has) {
                             const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
                                 (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-                            if constexpr (BUF) {
-                                run_lds[run + rank] = id[k];
-                            } else {
-                                const int64_t pos = (int64_t)run + rank;
-                                if (pos < id_limit) ids[pos] = id[k];  // plain: short runs per tile, merged in L2
-                            }
+                            const int64_t pos = (int64_t)run + rank;
+                            if (pos < id_limit) ids[pos] = id[k];  // plain: short runs per tile, merged in L2
                         }
                     }
                     run += (uint32_t)__popcll(b);

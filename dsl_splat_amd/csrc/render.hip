@@ -54,11 +54,16 @@ namespace gs3d {
 constexpr int kTile = 16;
 constexpr int kTilePixels = kTile * kTile;
 
-// Gaussians staged per batch: 256 while the channel vectors fit the LDS
-// budget, 128 for the widest vectors.
+// Gaussians staged per batch.  Up to 8 channels a workgroup holds 2
+// wavefronts and LDS bounds the resident workgroups: batches of 128 leave
+// room for more of them (3M Gaussians, 4 x 1080p: backward 1.93 -> 1.86 ms,
+// forward 1.11 -> 1.09 ms against 256; 64 and 96 were slower).  Wider
+// vectors run 4 wavefronts per workgroup at one pixel per lane, where
+// smaller batches only add staging rounds (32 channels: 128 was 3% slower
+// than 256); the widest vectors take 128 to fit the LDS budget.
 template <int CH>
 struct Batch {
-    static constexpr int size = CH <= 36 ? 256 : 128;
+    static constexpr int size = CH <= 8 ? 128 : CH <= 36 ? 256 : 128;
 };
 
 // Channels of the geometry launch's window: with the 8 geometric entries
