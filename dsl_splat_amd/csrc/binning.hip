@@ -1703,9 +1703,29 @@ extern "C" size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views
                                    tile_mode == GS3D_TILE_ACCUTILE, nullptr, nullptr);
 }
 
-extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream) {
+namespace gs3d {
+
+// Group items of depth-ordered rectangle rows (radius and SnugBox modes):
+// at most S of them, written to the start of the binning scratch, where the
+// group sort reads them.
+inline void emit_group_items(const gs3d_bin_args& a, const GridDims& d, int64_t S, uint64_t* items, hipStream_t s) {
+    const int64_t rows = (int64_t)a.n * a.views;
+    const RowGeometry geo{a.centers, a.conics, a.radii, a.tile_mode};
+    const dim3 egrid(blocks_for(rows, kBinThreads)), eblock(kBinThreads);
+    if (d.gx <= 256 && d.gy <= 256)
+        hipLaunchKernelGGL(group_emit_kernel<true>, egrid, eblock, 0, s, a.order, a.group_offsets, rows, geo, a.n, d, S,
+                           items);
+    else
+        hipLaunchKernelGGL(group_emit_kernel<false>, egrid, eblock, 0, s, a.order, a.group_offsets, rows, geo, a.n, d,
+                           S, items);
+}
+
+// gs3d_bin_rows; with `emitted` the group items are already in the scratch
+// (gs3d_emit_group_items with a capacity of at least group_pairs).
+int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream, bool emitted) {
     if (!args) return GS3D_ERR_ARGUMENT;
     const gs3d_bin_args& a = *args;
+    if (emitted && a.tile_mode == GS3D_TILE_ACCUTILE) return GS3D_ERR_ARGUMENT;
     if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0 || a.group_pairs < 0 || a.tile_pairs < 0)
         return GS3D_ERR_ARGUMENT;
     if (gs3d::check_tile_mode(a.tile_mode, a.tile_mode == GS3D_TILE_RADIUS ? nullptr : a.conics) != GS3D_OK)
@@ -1749,12 +1769,7 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
                                geo, fp, a.n, d, S, sc.items, sc.masks);
         status = gs3d::run_sort<uint64_t, uint64_t>(sc.items, sc.masks, S, group_bits, sc.sort, s);
     } else {
-        if (d.gx <= 256 && d.gy <= 256)
-            hipLaunchKernelGGL(gs3d::group_emit_kernel<true>, egrid, eblock, 0, s, a.order, a.group_offsets, rows, geo,
-                               a.n, d, S, sc.items);
-        else
-            hipLaunchKernelGGL(gs3d::group_emit_kernel<false>, egrid, eblock, 0, s, a.order, a.group_offsets, rows, geo,
-                               a.n, d, S, sc.items);
+        if (!emitted) gs3d::emit_group_items(a, d, S, sc.items, s);
         if (group_bits <= gs3d::kOnePassBits) {
             // One 10-bit pass; its digit scan gives the group ranges.
             status = gs3d::run_sort_once<uint64_t>(sc.items, S, group_bits, sc.sort, (int)groups, sc.granges, s);
@@ -1809,6 +1824,38 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
     }
 #undef GS3D_WRITE_PASS
     return gs3d::launch_status("gs3d_bin_rows");
+}
+
+}  // namespace gs3d
+
+extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream) {
+    return gs3d::bin_rows(args, scratch, scratch_bytes, stream, false);
+}
+
+extern "C" int gs3d_emit_group_items(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream) {
+    if (!args) return GS3D_ERR_ARGUMENT;
+    const gs3d_bin_args& a = *args;
+    if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0 || a.group_pairs < 0) return GS3D_ERR_ARGUMENT;
+    if (a.tile_mode == GS3D_TILE_ACCUTILE) return GS3D_ERR_UNSUPPORTED;
+    if (gs3d::check_tile_mode(a.tile_mode, a.tile_mode == GS3D_TILE_RADIUS ? nullptr : a.conics) != GS3D_OK)
+        return GS3D_ERR_ARGUMENT;
+    const gs3d::GridDims d = gs3d::grid_dims(a.width, a.height);
+    const int64_t rows = (int64_t)a.n * a.views;
+    const int64_t groups = (int64_t)a.views * d.gpv;
+    if (rows > INT32_MAX || a.group_pairs > INT32_MAX) return GS3D_ERR_OVERFLOW;
+    if (groups >= (int64_t)1 << gs3d::kGroupBits || d.gx >= 0xFFFF || d.gy >= 0xFFFF) return GS3D_ERR_UNSUPPORTED;
+    if (a.group_pairs == 0 || rows == 0 || groups == 0) return GS3D_OK;
+    if (!a.centers || !a.radii || !a.order || !a.group_offsets || !scratch) return GS3D_ERR_ARGUMENT;
+    if ((reinterpret_cast<uintptr_t>(a.order) & 7) || (reinterpret_cast<uintptr_t>(a.centers) & 7))
+        return GS3D_ERR_ARGUMENT;
+    if (scratch_bytes < gs3d_bin_rows_scratch_bytes(a.group_pairs, a.views, a.width, a.height, a.tile_mode))
+        return GS3D_ERR_SCRATCH;
+    gs3d::emit_group_items(a, d, a.group_pairs, reinterpret_cast<uint64_t*>(scratch), gs3d::as_stream(stream));
+    return gs3d::launch_status("gs3d_emit_group_items");
+}
+
+extern "C" int gs3d_bin_emitted_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream) {
+    return gs3d::bin_rows(args, scratch, scratch_bytes, stream, true);
 }
 
 extern "C" int gs3d_pair_tiles(const int32_t* ranges, int64_t tile_count, uint32_t* tiles, int64_t count,

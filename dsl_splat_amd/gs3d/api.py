@@ -6,7 +6,9 @@ Gaussian batch the host issues: one camera launch, one fused projection
 (camera, Gaussian) rows with their 8x8-tile group counts, ONE host
 synchronisation (camera status codes and the group/pair totals together),
 the grouped binning that writes every tile's depth-ordered list without
-sorting the pairs, and one blend launch for all cameras.  ``tile_mode``
+sorting the pairs (its first kernel enqueued before the synchronisation
+once an earlier frame of the same shape has given the item capacity), and
+one blend launch for all cameras.  ``tile_mode``
 selects the reference's radius squares, SnugBox rectangles or AccuTile
 strips (splatting/intersections.py).
 """
@@ -105,13 +107,21 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     # while the device works on the depth order.
     launch = prepare_bin_rows(state.centers, state.radii, order, offsets, width, height, conics=state.conics,
                               tile_mode=tile_mode)
+    # The totals are copied to pinned host memory right after the depth
+    # order; with a group-item capacity from an earlier frame of this shape,
+    # the device then emits the group items while the host waits for them.
+    host = torch.empty(status.shape, dtype=status.dtype, pin_memory=True)
+    host.copy_(status, non_blocking=True)
+    copied = torch.cuda.Event()
+    copied.record(torch.cuda.current_stream(status.device))
+    early = binning.emit_early(launch)
     profiling.mark("ordered")
-    host = status.cpu()
+    copied.synchronize()
     profiling.mark("totals_read")
     raise_camera_errors(host[2:].view(torch.int32)[:cameras].tolist())
     group_pairs, count = host[:2].tolist()
     if count <= binning.PAIR_LIMIT and group_pairs <= binning.PAIR_LIMIT:
-        ranges, ids = launch_bin_rows(launch, group_pairs, count)
+        ranges, ids = launch_bin_rows(launch, group_pairs, count, early)
         bins = [ViewBins(0, cameras, ranges, ids)]
     else:
         bins = _bin_view_groups(state, width, height, tile_mode)

@@ -65,6 +65,44 @@ def _views(t, v0: int, v1: int, views: int, per_view_ndim: int):
     return t[v0:v1]
 
 
+# One side stream per device clears the backward's accumulation buffers
+# (blend gradient record, colour and extra-channel gradients) while the
+# forward blend, which is bound by arithmetic, runs on the caller's stream.
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+@dataclass(slots=True)
+class ClearedBuffers:
+    """Zeroed accumulation targets of the blend VJP, ready once ``done``."""
+
+    record: Tensor
+    features: Tensor | None
+    extra: Tensor | None
+    done: torch.cuda.Event
+
+
+def _clear_for_backward(device: torch.device, record_shape, feature_shape, extra_shape) -> ClearedBuffers:
+    main = torch.cuda.current_stream(device)
+    side = _SIDE_STREAMS.get(device.index)
+    if side is None:
+        side = _SIDE_STREAMS[device.index] = torch.cuda.Stream(device=device)
+    f32 = dict(dtype=torch.float32, device=device)
+    bufs = [None if shape is None else torch.empty(shape, **f32) for shape in (record_shape, feature_shape, extra_shape)]
+    # The side stream starts after everything enqueued so far (the memory may
+    # have served earlier work on the caller's stream), not after the blend.
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        for b in bufs:
+            if b is not None:
+                b.zero_()
+    for b in bufs:
+        if b is not None:
+            b.record_stream(side)
+    done = torch.cuda.Event()
+    done.record(side)
+    return ClearedBuffers(*bufs, done)
+
+
 def _statistics_views(statistics, v0: int, v1: int):
     if statistics is None:
         return None
@@ -94,6 +132,17 @@ class Rasterize(torch.autograd.Function):
         blend launch."""
         st = frame.state
         blended = st.colors if frame.sh_degree is not None else colors
+        train = grad_enabled and any(ctx.needs_input_grad[:8])
+        ctx.cleared = None
+        if train and len(frame.bins) == 1:
+            needs = ctx.needs_input_grad
+            absgrad = absolute is not None and any(t is not None for t in absolute)
+            views, n = st.centers.shape[0], st.centers.shape[1]
+            need_features = frame.sh_degree is not None or needs[4]
+            ctx.cleared = _clear_for_backward(
+                st.centers.device, (views, n, render.RECORD_ABS if absgrad else render.RECORD),
+                blended.shape if need_features and blended is not None else None,
+                extra_features.shape if needs[5] and extra_features is not None else None)
         if len(frame.bins) == 1:
             bins = frame.bins[0]
             output = render.render_views(
@@ -115,7 +164,7 @@ class Rasterize(torch.autograd.Function):
                 None if getattr(parts[0], f) is None else torch.cat([getattr(p, f) for p in parts])
                 for f in ("features", "extra", "alpha", "transmittance", "contributors")))
         profiling.mark("blended")
-        if grad_enabled and any(ctx.needs_input_grad[:8]):
+        if train:
             ctx.save_for_backward(means, quats, scales, opacities, colors, extra_features, viewmats,
                                   output.transmittance, output.contributors)
             ctx.frame = frame
@@ -148,9 +197,13 @@ class Rasterize(torch.autograd.Function):
         blend_args = dict(one_tail=True, absgrad=absgrad, need_features=sh or needs[4], need_extra=needs[5])
         if len(frame.bins) == 1:
             bins = frame.bins[0]
+            cleared = ctx.cleared
+            if cleared is not None:
+                torch.cuda.current_stream(st.centers.device).wait_event(cleared.done)
+                ctx.cleared = None
             record, grad_blended, grad_extra = render.backward_views(
                 bins.ranges, bins.ids, st.centers, st.conics, blended, final_t, contributors, upstream,
-                frame.width, frame.height, extra=extra, background=frame.background, **blend_args,
+                frame.width, frame.height, extra=extra, background=frame.background, cleared=cleared, **blend_args,
             )
         else:
             views = st.centers.shape[0]

@@ -149,11 +149,13 @@ def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, f
 def backward_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, features: Tensor,
                    final_t: Tensor, contributors: Tensor, upstream, width: int, height: int, *,
                    extra: Tensor | None = None, background: Tensor | None = None, one_tail: bool = True,
-                   absgrad: bool = False, need_features: bool = True, need_extra: bool = True):
+                   absgrad: bool = False, need_features: bool = True, need_extra: bool = True, cleared=None):
     """``upstream`` is either the (grad features, grad extra, grad alpha)
     planes (each may be None) or one (C,H,W,D') tensor of all channels.
     Returns (record (C,N,6), or (C,N,8) with absgrad, grad_features like
-    features or None, grad_extra like extra or None)."""
+    features or None, grad_extra like extra or None).  ``cleared``, if
+    given, holds zeroed buffers of those shapes (record, features, extra)
+    that the launch accumulates into instead of fresh ones."""
     views, n = centers.shape[0], centers.shape[1]
     device = centers.device
     keep = []
@@ -175,19 +177,27 @@ def backward_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor,
     b.upstream_extra, b.upstream_extra_stride = native.ptr(ge_plane), ge_stride
     b.upstream_alpha, b.upstream_alpha_stride = native.ptr(ga_plane), ga_stride
     width = RECORD_ABS if absgrad else RECORD
-    record = torch.zeros((views, n, width), dtype=torch.float32, device=device)
+
+    def zeros(shape, given):
+        if given is not None:
+            if tuple(given.shape) != tuple(shape) or given.dtype != torch.float32 or not given.is_contiguous():
+                raise ValueError(f"cleared buffer of shape {tuple(given.shape)} does not match {tuple(shape)}")
+            return given
+        return torch.zeros(shape, dtype=torch.float32, device=device)
+
+    record = zeros((views, n, width), cleared and cleared.record)
     b.grad_centers, b.grad_centers_stride = native.ptr(record), width
     b.grad_conics, b.grad_conics_stride = native.ptr(record, 2), width
     if absgrad:
         b.abs_centers, b.abs_stride = native.ptr(record, 6), width
     grad_features = grad_extra = None
     if need_features and features is not None:
-        grad_features = torch.zeros(features.shape, dtype=torch.float32, device=device)
+        grad_features = zeros(features.shape, cleared and cleared.features)
         b.grad_features = native.ptr(grad_features)
         b.grad_feat_stride = features.shape[-1]
         b.grad_feat_view_stride = n * features.shape[-1] if features.ndim == 3 else 0
     if need_extra and extra is not None:
-        grad_extra = torch.zeros(extra.shape, dtype=torch.float32, device=device)
+        grad_extra = zeros(extra.shape, cleared and cleared.extra)
         b.grad_extra = native.ptr(grad_extra)
         b.grad_extra_stride = extra.shape[-1]
         b.grad_extra_view_stride = n * extra.shape[-1] if extra.ndim == 3 else 0

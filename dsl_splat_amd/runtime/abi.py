@@ -9,7 +9,7 @@ import ctypes
 c_float_p = ctypes.POINTER(ctypes.c_float)
 c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Tile modes (GS3D_TILE_*), named as the reference's TileMode literals.
 TILE_MODES = {"radius": 0, "snugbox": 1, "accutile": 2}
@@ -280,6 +280,8 @@ FUNCTIONS = {
     "gs3d_order_rows": (ctypes.c_int, [ctypes.POINTER(OrderArgs), _P, _SZ, _P]),
     "gs3d_bin_rows_scratch_bytes": (_SZ, [_I64, _I32, _I32, _I32, _I32]),
     "gs3d_bin_rows": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
+    "gs3d_emit_group_items": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
+    "gs3d_bin_emitted_rows": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
     "gs3d_pair_tiles": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
     "gs3d_sort_pairs_u32": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),
     "gs3d_expand_keys": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _I32, _P, _P]),

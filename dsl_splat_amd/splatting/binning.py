@@ -185,17 +185,73 @@ def prepare_bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Ten
     return BinLaunch(a, ranges, (centers, radii, order, offsets, conics))
 
 
+# Group-item capacities of earlier frames, per binning shape.  With a known
+# capacity the group items are emitted before the host reads the totals, so
+# the device emits while the host synchronises (radius and SnugBox modes).
+_CAPACITY: dict[tuple, int] = {}
+_CAPACITY_SHAPES = 64
+CAPACITY_HEADROOM = 1.125
+
+
+@dataclass(slots=True)
+class EarlyItems:
+    """Binning scratch holding the group items emitted with ``capacity``."""
+    scratch: Tensor
+    capacity: int
+
+
+def _shape_key(launch: BinLaunch) -> tuple:
+    a = launch.args
+    return (launch.ranges.device.index, a.n, a.views, a.width, a.height, a.tile_mode)
+
+
 @torch.no_grad()
-def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int) -> tuple[Tensor, Tensor]:
-    """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs)."""
+def emit_early(launch: BinLaunch) -> EarlyItems | None:
+    """Enqueue the emission of group items before the totals are known, when
+    an earlier frame of the same shape gave a capacity; None otherwise."""
+    a = launch.args
+    capacity = _CAPACITY.get(_shape_key(launch))
+    if not capacity or a.tile_mode == abi.TILE_MODES["accutile"]:
+        return None
+    device = launch.ranges.device
+    scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", capacity, a.views, a.width, a.height,
+                                    a.tile_mode), device)
+    a.group_pairs, a.tile_pairs = capacity, 0
+    native.call("gs3d_emit_group_items", ctypes.byref(a), native.ptr(scratch), scratch.numel(),
+                native.stream(device))
+    return EarlyItems(scratch, capacity)
+
+
+def _remember_capacity(launch: BinLaunch, group_pairs: int) -> None:
+    if launch.args.tile_mode == abi.TILE_MODES["accutile"] or group_pairs <= 0:
+        return
+    key = _shape_key(launch)
+    want = min(PAIR_LIMIT, int(group_pairs * CAPACITY_HEADROOM) + 1)
+    if _CAPACITY.get(key, 0) >= want:
+        return
+    if key not in _CAPACITY and len(_CAPACITY) >= _CAPACITY_SHAPES:
+        del _CAPACITY[next(iter(_CAPACITY))]
+    _CAPACITY[key] = want
+
+
+@torch.no_grad()
+def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int,
+                    early: EarlyItems | None = None) -> tuple[Tensor, Tensor]:
+    """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs);
+    ``early`` (from emit_early) is used when its capacity holds every item."""
     check_pair_counts(group_pairs, tile_pairs)
     a, device = launch.args, launch.ranges.device
     ids = torch.empty(tile_pairs, dtype=torch.int32, device=device)
     a.group_pairs, a.tile_pairs = group_pairs, tile_pairs
     a.ids = native.ptr(ids)
-    scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, a.views, a.width, a.height,
-                                    a.tile_mode), device)
-    native.call("gs3d_bin_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
+    if early is not None and group_pairs <= early.capacity:
+        native.call("gs3d_bin_emitted_rows", ctypes.byref(a), native.ptr(early.scratch), early.scratch.numel(),
+                    native.stream(device))
+    else:
+        scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, a.views, a.width, a.height,
+                                        a.tile_mode), device)
+        native.call("gs3d_bin_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
+    _remember_capacity(launch, group_pairs)
     return launch.ranges, ids
 
 

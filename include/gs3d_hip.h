@@ -314,6 +314,21 @@ size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t w
                                    int32_t tile_mode);
 int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream);
 
+/* gs3d_bin_rows in two calls (radius and SnugBox modes), so that step 3's
+ * first kernel can be enqueued before the caller has read the totals:
+ *   gs3d_emit_group_items with args->group_pairs = a capacity C (an upper
+ *   bound the caller expects, e.g. from an earlier frame) and a scratch of
+ *   gs3d_bin_rows_scratch_bytes(C, ...) bytes writes the first min(totals[0], C)
+ *   group items to the start of that scratch (nothing beyond C);
+ *   then, once totals[0] <= C is known, gs3d_bin_emitted_rows with the true
+ *   totals and the same scratch finishes the binning exactly as gs3d_bin_rows
+ *   does (same ranges and ids).  When totals[0] > C the caller discards the
+ *   scratch and calls gs3d_bin_rows.  ACCUTILE: GS3D_ERR_UNSUPPORTED /
+ *   GS3D_ERR_ARGUMENT (its items carry tile masks; use gs3d_bin_rows).
+ * Same reference counterpart as gs3d_bin_rows (splatting/binning.py:16-117). */
+int gs3d_emit_group_items(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream);
+int gs3d_bin_emitted_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream);
+
 /* Global tile id of every listed pair: tiles[p] = t for p in ranges[t]. */
 int gs3d_pair_tiles(const int32_t* ranges, int64_t tile_count, uint32_t* tiles, int64_t count,
                     void* stream);

@@ -37,6 +37,27 @@ def test_library_exports_every_declared_symbol():
         native.query("gs3d_bin_rows_scratch_bytes", 10_000, 4, 1920, 1080, 0)
 
 
+def test_early_group_item_entry_points_check_their_arguments():
+    lib = native.load()
+    a = abi.BinArgs()
+    a.n, a.views, a.width, a.height = 10, 1, 64, 64
+    a.group_pairs = 100
+    # AccuTile items carry tile masks: not emitted early.
+    a.tile_mode = abi.TILE_MODES["accutile"]
+    assert lib.gs3d_emit_group_items(ctypes.byref(a), None, 0, None) == abi.GS3D_ERR_UNSUPPORTED
+    assert lib.gs3d_bin_emitted_rows(ctypes.byref(a), None, 0, None) == abi.GS3D_ERR_ARGUMENT
+    a.tile_mode = abi.TILE_MODES["radius"]
+    # Missing inputs, then a scratch smaller than the capacity needs.
+    assert lib.gs3d_emit_group_items(ctypes.byref(a), None, 0, None) == abi.GS3D_ERR_ARGUMENT
+    a.centers = a.radii = a.order = a.group_offsets = ctypes.c_void_p(256)
+    need = native.query("gs3d_bin_rows_scratch_bytes", 100, 1, 64, 64, 0)
+    assert lib.gs3d_emit_group_items(ctypes.byref(a), ctypes.c_void_p(256), need - 1, None) == abi.GS3D_ERR_SCRATCH
+    a.group_pairs = 1 << 31
+    assert lib.gs3d_emit_group_items(ctypes.byref(a), ctypes.c_void_p(256), need, None) == abi.GS3D_ERR_OVERFLOW
+    a.group_pairs = -1
+    assert lib.gs3d_emit_group_items(ctypes.byref(a), ctypes.c_void_p(256), need, None) == abi.GS3D_ERR_ARGUMENT
+
+
 def test_argument_errors_are_reported_without_launching():
     lib = native.load()
     # Invalid sizes are rejected on the host (no device needed).

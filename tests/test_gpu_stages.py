@@ -14,7 +14,7 @@ import torch
 
 import oracle
 from oracle_pipeline import check_gradient, compare
-from dsl_splat_amd import synthetic
+from dsl_splat_amd import gs3d, synthetic
 from dsl_splat_amd.gs3d import projection as gproj
 from dsl_splat_amd.gs3d import render as grender
 from dsl_splat_amd.primitives import tiling
@@ -491,6 +491,58 @@ def test_grouped_binning_ties_and_large_rects(views, n, W, H, spread):
     np.testing.assert_array_equal(_np(bins["point_list"]), sv)
     np.testing.assert_array_equal(_np(bins["point_list_keys"]).view(np.uint64), sk)
     np.testing.assert_array_equal(_np(bins["ranges"]), oracle.tile_ranges(sk, T))
+
+
+@pytest.mark.parametrize("key,degree,mode", [("small_rgb", None, "radius"), ("sh3_4view", 3, "radius"),
+                                             ("sh3_720p", 0, "snugbox")])
+def test_group_items_emitted_before_the_totals(key, degree, mode, monkeypatch):
+    # The emission enqueued before the host reads the totals (capacity from an
+    # earlier frame) must give exactly gs3d_bin_rows' ids and ranges when the
+    # capacity holds every item, and fall back to gs3d_bin_rows when not.
+    scene = _scene(key)
+    _say(f"early group items {key} {mode}")
+    quats, full, inverse, centers, errors, st = _project(scene, degree)
+    W, H = scene.width, scene.height
+    order, offsets, totals = binning.order_rows(st.centers, st.radii, st.depths, W, H, conics=st.conics,
+                                                tile_mode=mode)
+    S, M = totals.cpu().tolist()
+    assert S > 1
+    ref_ranges, ref_ids = binning.bin_rows(st.centers, st.radii, order, offsets, S, M, W, H, conics=st.conics,
+                                           tile_mode=mode)
+    calls = []
+    real_call = binning.native.call
+    monkeypatch.setattr(binning.native, "call", lambda name, *a: (calls.append(name), real_call(name, *a))[1])
+    for capacity in (S, S + 4097, S - 1, S // 2):
+        launch = binning.prepare_bin_rows(st.centers, st.radii, order, offsets, W, H, conics=st.conics,
+                                          tile_mode=mode)
+        key_ = binning._shape_key(launch)
+        binning._CAPACITY[key_] = capacity
+        calls.clear()
+        try:
+            early = binning.emit_early(launch)
+            assert early is not None and early.capacity == capacity
+            ranges, ids = binning.launch_bin_rows(launch, S, M, early)
+        finally:
+            binning._CAPACITY.pop(key_, None)
+        expect = "gs3d_bin_emitted_rows" if capacity >= S else "gs3d_bin_rows"
+        assert calls == ["gs3d_emit_group_items", expect], calls
+        np.testing.assert_array_equal(_np(ids), _np(ref_ids))
+        np.testing.assert_array_equal(_np(ranges), _np(ref_ranges))
+
+
+def test_rasterize_reuses_the_group_item_capacity():
+    # A second frame of the same shape takes the early emission; its outputs
+    # equal the first frame's bit for bit.
+    scene = _scene("sh3_4view")
+    _say("rasterize twice, early group items")
+    binning._CAPACITY.clear()
+    args = (scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats, scene.Ks, scene.width,
+            scene.height)
+    first = gs3d.rasterize(*args, sh_coeffs=scene.sh_coeffs, sh_degree=3)
+    assert len(binning._CAPACITY) == 1
+    second = gs3d.rasterize(*args, sh_coeffs=scene.sh_coeffs, sh_degree=3)
+    for a, b in ((first.features, second.features), (first.alpha, second.alpha)):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("count,end_bit", [(2, 13), (4097, 15), (1_000_003, 16), (5_000_000, 32), (3, 11),
