@@ -397,8 +397,9 @@ def run_workload(workload, n, device, steps, warmup, cpu, tile_mode="radius"):
         stages=stages,
         stages_1_3={"ms": round(t13, 4), "bytes": b13, "gbps": round(b13 / (t13 * 1e-3) / 1e9, 1),
                     "frac": round(b13 / (t13 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                    "note": "project + order + bin spans inside the steps (the host's read of the pair totals "
-                            "between order and bin is the separate totals_read span)"},
+                    "note": "project + order + bin spans inside the steps (bin starts at the end of the depth "
+                            "order and includes the host's read of the pair totals, reported alone as "
+                            "totals_read)"},
         pairs=dict(tile_pairs=info["pairs"], group_items=info["group_pairs"], visible_rows=info["visible"],
                    rows=info["rows"], **info["blend_pairs"]),
     )

@@ -1,0 +1,23 @@
+"""The reference package's import path for the 3DGS rasterizer.
+
+With this directory (``dsl_splat_amd/compat``) ahead of the reference on
+``sys.path``, code written against ``dsl_splat.gs3d`` (``rasterize``,
+``RasterizationResult``, ``ops``, ``gsplat.rasterization``), ``dsl_splat.cameras``,
+``dsl_splat.statistics``, ``dsl_splat.training``, ``dsl_splat.inputs`` and
+``dsl_splat.primitives.tiling`` / ``.spherical_harmonics`` runs unchanged on
+the HIP build: every module here is the ``dsl_splat_amd`` module of the same
+name (one object, not a copy).  The reference's other methods (its root
+exports, aaa, geer, pgsr, rade, strategy) are not part of this build.
+"""
+
+import importlib
+
+from dsl_splat_amd.cameras import PinholeCamera
+
+__all__ = ["PinholeCamera", "gs3d"]
+
+
+def __getattr__(name):
+    if name == "gs3d":
+        return importlib.import_module(f"{__name__}.gs3d")
+    raise AttributeError(name)

@@ -278,7 +278,7 @@ __global__ __launch_bounds__(kEmitThreads) void emit_accutile_kernel(gs3d_emit_a
 // 64-bit keys.  Per pass: per-tile digit histograms (digit-major
 // [256][tiles]), one exclusive scan over them (the scatter base of every
 // (digit, tile)), then a stable rank-and-scatter: each wavefront ranks its
-// 1024 keys with ballot-based digit matching, the block orders its 4096 keys
+// 512 keys with ballot-based digit matching, the block orders its 2048 keys
 // by digit in LDS and writes them out in digit runs (coalesced).
 // ---------------------------------------------------------------------------
 constexpr int kSortThreads = 256;
@@ -286,7 +286,7 @@ constexpr int kSortThreads = 256;
 #define GS3D_SORT_ITEMS 8
 #endif
 constexpr int kSortItems = GS3D_SORT_ITEMS;  // keys per thread of a sort tile
-constexpr int kSortTile = kSortThreads * kSortItems;  // 4096 keys
+constexpr int kSortTile = kSortThreads * kSortItems;  // 2048 keys
 constexpr int kRadix = 256;
 #ifndef GS3D_SORT_XCD
 #define GS3D_SORT_XCD 1

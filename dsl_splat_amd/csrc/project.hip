@@ -323,12 +323,29 @@ GS3D_DEV void sh_backward(const float* coef, const float* dir, bool visible, con
 // Forward projection of every view, one thread per Gaussian (the colours are
 // evaluated by sh_rows_fwd_kernel in a second launch).
 // ---------------------------------------------------------------------------
+// Cameras whose rows (view 16, projection 16, fx, fy) a block stages in LDS:
+// the per-view loop then reads them with LDS broadcasts instead of vector
+// loads through the L1 (0.174 -> 0.168 ms at 4 views).  More cameras read
+// them from global memory.
+constexpr int kCamLds = 16;
+
 // At most 64 VGPRs (8 wavefronts per SIMD): this kernel is bound by its
 // output stream, and more wavefronts in flight keep more stores queued.
 template <bool META>
 __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(8))) void project_fwd_kernel(gs3d_project_args a) {
     const int n = a.n;
     const int64_t i = (int64_t)blockIdx.x * kProjBlock + threadIdx.x;
+    __shared__ float s_cam[kCamLds][34];
+    const bool staged = a.views <= kCamLds;
+    if (staged) {
+        for (int e = threadIdx.x; e < a.views * 34; e += kProjBlock) {
+            const int v = e / 34, k = e - v * 34;
+            s_cam[v][k] = k < 16   ? a.view[16 * v + k]
+                          : k < 32 ? a.projection[16 * v + k - 16]
+                                   : a.intrinsics[9 * v + (k == 32 ? 0 : 4)];
+        }
+        __syncthreads();
+    }
     if (i >= n) return;
     float mean[3], q[4], s[3];
 #pragma unroll
@@ -342,10 +359,7 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(8)))
 #pragma unroll
     for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
     const float opac = a.opacities[i];
-    for (int v = 0; v < a.views; ++v) {
-        const float* V = a.view + 16 * v;
-        const float* P = a.projection + 16 * v;
-        const float fx = a.intrinsics[9 * v], fy = a.intrinsics[9 * v + 4];
+    auto one = [&](int v, const float* V, const float* P, float fx, float fy) {
         Footprint f;
         const bool vis = project_one(mean, q, s, V, P, fx, fy, a.width, a.height, a.near_plane, a.far_plane,
                                      a.radius_clip, f);
@@ -363,6 +377,12 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(8)))
 #pragma unroll
             for (int k = 0; k < 3; ++k) st_stream(a.meta_conics + 3 * row + k, f.conic[k]);
         }
+    };
+    if (staged) {
+        for (int v = 0; v < a.views; ++v) one(v, &s_cam[v][0], &s_cam[v][16], s_cam[v][32], s_cam[v][33]);
+    } else {
+        for (int v = 0; v < a.views; ++v)
+            one(v, a.view + 16 * v, a.projection + 16 * v, a.intrinsics[9 * v], a.intrinsics[9 * v + 4]);
     }
 }
 

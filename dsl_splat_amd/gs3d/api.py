@@ -114,8 +114,8 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     host.copy_(status, non_blocking=True)
     copied = torch.cuda.Event()
     copied.record(torch.cuda.current_stream(status.device))
-    early = binning.emit_early(launch)
     profiling.mark("ordered")
+    early = binning.emit_early(launch)
     copied.synchronize()
     profiling.mark("totals_read")
     raise_camera_errors(host[2:].view(torch.int32)[:cameras].tolist())

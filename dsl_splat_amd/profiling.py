@@ -4,11 +4,13 @@ While a ``StageEvents`` recorder is active, gs3d.rasterize records a HIP
 event on the current stream (the stream every gs3d_* launch uses) at each
 stage boundary of its forward and backward passes, so stage spans can be
 taken inside real training steps: camera + projection + SH ("project"),
-depth ordering ("order"), the host's read of the pair totals (the GPU idles
-from the end of the ordering until the binning is launched: "totals_read"),
-grouped binning ("bin"), forward blend ("render_fwd"), blend VJP ("render_bwd"),
-projection + SH VJP ("project_bwd") and camera VJP ("camera_bwd").  With no
-recorder active a boundary costs one global lookup.
+depth ordering ("order"), grouped binning from the end of the ordering
+("bin", which includes any time the device waits for the host to read the
+pair totals), forward blend ("render_fwd"), blend VJP ("render_bwd"),
+projection + SH VJP ("project_bwd") and camera VJP ("camera_bwd").
+"totals_read" is the part of "bin" until the host has the totals (on the
+device: the early emission of group items, or idle time without it).  With
+no recorder active a boundary costs one global lookup.
 """
 
 import torch
@@ -20,7 +22,7 @@ SPANS = (
     ("project", "start", "projected"),
     ("order", "projected", "ordered"),
     ("totals_read", "ordered", "totals_read"),
-    ("bin", "totals_read", "binned"),
+    ("bin", "ordered", "binned"),
     ("render_fwd", "binned", "blended"),
     ("render_bwd", "backward", "blend_vjp"),
     ("project_bwd", "blend_vjp", "projection_vjp"),

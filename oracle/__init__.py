@@ -18,7 +18,9 @@ import numpy as np
 from dsl_splat_amd.runtime import abi
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle_gs3d.so")
+# ORACLE_LIBRARY selects another build of the same source (the sanitized
+# build of the Makefile's "sanitized" target).
+_LIB_PATH = os.environ.get("ORACLE_LIBRARY") or os.path.join(_HERE, "liboracle_gs3d.so")
 _lib = None
 
 

@@ -1,0 +1,42 @@
+"""The reference's import path (dsl_splat.gs3d ...) resolves to this build's
+modules when dsl_splat_amd/compat is on sys.path (checked in a fresh
+interpreter, so nothing here is imported from the test process)."""
+
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+SCRIPT = r"""
+import sys
+import dsl_splat
+from dsl_splat import gs3d
+from dsl_splat.gs3d import RasterizationResult, ops, rasterize
+from dsl_splat.gs3d.gsplat import rasterization
+from dsl_splat.gs3d.ops import bin_and_sort, prepare_gaussians, rasterize_to_pixels, spherical_harmonics
+from dsl_splat.cameras import PinholeCamera
+from dsl_splat.statistics import MaskedContributionCount, WeightedContributionSum
+from dsl_splat.primitives.tiling import sort_tile_pairs
+import dsl_splat.training, dsl_splat.inputs, dsl_splat.primitives.spherical_harmonics
+import dsl_splat_amd.gs3d, dsl_splat_amd.gs3d.gsplat, dsl_splat_amd.cameras, dsl_splat_amd.statistics
+import dsl_splat_amd.primitives.tiling
+assert rasterize is dsl_splat_amd.gs3d.rasterize
+assert RasterizationResult is dsl_splat_amd.gs3d.RasterizationResult
+assert ops is dsl_splat_amd.gs3d.ops and gs3d.ops is ops and dsl_splat.gs3d.ops is ops
+assert rasterization is dsl_splat_amd.gs3d.gsplat.rasterization
+assert PinholeCamera is dsl_splat_amd.cameras.PinholeCamera is dsl_splat.PinholeCamera
+assert MaskedContributionCount is dsl_splat_amd.statistics.MaskedContributionCount
+assert sort_tile_pairs is dsl_splat_amd.primitives.tiling.sort_tile_pairs
+for name in ("gs3d.gsplat", "gs3d.ops", "cameras", "statistics", "training", "inputs", "primitives.tiling",
+             "primitives.spherical_harmonics"):
+    assert sys.modules["dsl_splat." + name] is sys.modules["dsl_splat_amd." + name], name
+print("ok")
+"""
+
+
+def test_reference_import_path_resolves_to_this_build():
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "dsl_splat_amd", "compat"), ROOT]))
+    run = subprocess.run([sys.executable, "-c", SCRIPT], cwd="/", env=env, capture_output=True, text=True)
+    assert run.returncode == 0, run.stderr[-3000:]
+    assert run.stdout.strip() == "ok"
