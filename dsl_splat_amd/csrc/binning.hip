@@ -927,18 +927,26 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
     const int64_t S = r0 > 0 ? offsets[r0 - 1] : 0;
     const int64_t E = min((int64_t)s_end[cnt - 1], limit);
     for (int64_t p = S + t; p < E; p += kBinThreads) {
-        int lo = 0, hi = cnt - 1;  // first j with s_end[j] > p
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (s_end[mid] > p)
-                hi = mid;
-            else
-                lo = mid + 1;
-        }
+        // First j with s_end[j] > p (p < s_end[cnt - 1], offsets are int32):
+        // a fixed 8-step search, every entry below lo ends at or before p.
+        const int32_t p32 = (int32_t)p;
+        int lo = 0;
+#pragma unroll
+        for (int step = kBinThreads / 2; step > 0; step >>= 1)
+            if (lo + step <= cnt && s_end[lo + step - 1] <= p32) lo += step;
         const int64_t start = lo > 0 ? s_end[lo - 1] : S;
         const int local = (int)(p - start);
         const int gw = s_gw[lo];
-        const int oy = local / gw, ox = local - oy * gw;
+        int oy;
+        if constexpr (PACKED) {
+            // local < gw * gh <= 32 * 32: (local + 0.5) / gw is at least
+            // 0.5 / gw >= 1/64 away from an integer, far beyond the
+            // reciprocal's error, so truncation gives the exact quotient.
+            oy = (int)(((float)local + 0.5f) * __builtin_amdgcn_rcpf((float)gw));
+        } else {
+            oy = local / gw;
+        }
+        const int ox = local - oy * gw;
         const int X = (s_x0[lo] >> kGroupShift) + ox, Y = (s_y0[lo] >> kGroupShift) + oy;
         const int lx0 = max(s_x0[lo] - (X << kGroupShift), 0), lx1 = min(s_x1[lo] - 1 - (X << kGroupShift), 7);
         const int ly0 = max(s_y0[lo] - (Y << kGroupShift), 0), ly1 = min(s_y1[lo] - 1 - (Y << kGroupShift), 7);
@@ -1204,7 +1212,13 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     const int lane = lane_id();
     const int64_t block = xcd_contiguous(blockIdx.x, gridDim.x);
     const int64_t u = block * kBinWaves + (threadIdx.x >> 6);
-    if (u >= max_chunks || u >= chunk_base[groups]) return;
+    if (u >= max_chunks) return;
+    if (u >= chunk_base[groups]) {
+        // Chunks beyond the last group's: their counts (the tail of the
+        // scanned table) are zero.
+        if constexpr (!WRITE) counts[u * 64 + lane] = 0u;
+        return;
+    }
     if constexpr (RECT_COUNT) {
         // Counts of a chunk of rectangle items: each item adds its
         // rectangle's four corners to a difference grid; the 2D prefix sum of
@@ -1236,10 +1250,20 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int tx = lane & 7, ty = lane >> 3;
-        int32_t c = 0;
-        for (int y = 0; y <= ty; ++y)
-            for (int x = 0; x <= tx; ++x) c += diff[y * 9 + x];
+        // Inclusive 2D prefix sum of the grid's 8x8 corner: along each row of
+        // 8 lanes, then down the columns (lanes 8 apart).
+        const int tx = lane & 7;
+        int32_t c = diff[(lane >> 3) * 9 + tx];
+#pragma unroll
+        for (int d = 1; d < 8; d <<= 1) {
+            const int32_t u = __shfl_up(c, d, 8);
+            if (tx >= d) c += u;
+        }
+#pragma unroll
+        for (int d = 8; d < 64; d <<= 1) {
+            const int32_t u = __shfl_up(c, d, 64);
+            if (lane >= d) c += u;
+        }
         counts[(int64_t)cb * 64 + (int64_t)lane * q + s] = (uint32_t)c;
         return;
     }
@@ -1787,7 +1811,8 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
     hipLaunchKernelGGL(gs3d::chunk_base_kernel, dim3(1), dim3(1024), 0, s, sc.granges, (int)groups, sc.chunk_base);
     hipLaunchKernelGGL(gs3d::chunk_group_kernel, dim3(gs3d::blocks_for(chunks, 256)), dim3(256), 0, s,
                        sc.chunk_base, (int)groups, chunks, sc.chunk_group);
-    gs3d::fill_u32(sc.counts, 64 * chunks, 0u, s);
+    // The count pass writes every entry of the 64 * chunks table (zeros for
+    // chunks beyond the groups' own).
     const dim3 pass_grid(gs3d::blocks_for(chunks, gs3d::kBinWaves));
     if (accu)
         hipLaunchKernelGGL((gs3d::group_pass_kernel<false, true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,
