@@ -74,36 +74,27 @@ __global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const In* __r
     if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
 
-// Exclusive scan of the tile partials in place (single block); writes the
-// grand total.
-__global__ __launch_bounds__(1024) void scan_partials_kernel(int64_t* __restrict__ partials, int64_t count,
-                                                             int64_t* __restrict__ total_out) {
-    __shared__ int64_t s_wave[1024 / 64];
-    int64_t carry = 0;
-    for (int64_t base = 0; base < count; base += 1024) {
-        const int64_t idx = base + threadIdx.x;
-        const int64_t v = idx < count ? partials[idx] : 0;
-        int64_t total;
-        const int64_t ex = block_exclusive_scan<1024>(v, s_wave, total);
-        if (idx < count) partials[idx] = carry + ex;
-        carry += total;
-    }
-    if (threadIdx.x == 0 && total_out) *total_out = carry;
-}
-
 // Per-tile scan with the tile's prefix.  Loads and stores are striped
 // across the block (coalesced) and transposed through LDS so that each thread
 // scans 16 consecutive elements; the LDS index e + e/16 keeps both the
 // striped and the per-thread accesses free of bank conflicts.
 GS3D_DEV int scan_lds_index(int e) { return e + (e >> 4); }
 
+// The tile's prefix is the sum of the earlier tiles' totals, which every
+// block adds up itself (a few thousand L2-resident values at most), so no
+// separate launch scans the totals.  The last block writes the grand total.
 template <class In, bool INCLUSIVE>
 __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const In* __restrict__ in, int64_t n,
                                                                  const int64_t* __restrict__ partials,
-                                                                 int32_t* __restrict__ out) {
+                                                                 int32_t* __restrict__ out,
+                                                                 int64_t* __restrict__ total_out) {
     __shared__ int64_t s_wave[kScanThreads / 64];
     __shared__ int32_t s_tile[kScanTile + kScanTile / 16];
     const int64_t base = (int64_t)blockIdx.x * kScanTile;
+    int64_t before = 0;
+    for (int64_t j = threadIdx.x; j < (int64_t)blockIdx.x; j += kScanThreads) before += partials[j];
+    int64_t prefix;
+    block_exclusive_scan<kScanThreads>(before, s_wave, prefix);
 #pragma unroll
     for (int k = 0; k < kScanItems; ++k) {
         const int e = k * kScanThreads + threadIdx.x;
@@ -119,7 +110,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const In* __res
         sum += vals[k];
     }
     int64_t total;
-    int64_t run = block_exclusive_scan<kScanThreads>(sum, s_wave, total) + partials[blockIdx.x];
+    int64_t run = block_exclusive_scan<kScanThreads>(sum, s_wave, total) + prefix;
+    if (total_out && blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *total_out = prefix + total;
 #pragma unroll
     for (int k = 0; k < kScanItems; ++k) {
         if (INCLUSIVE) run += vals[k];
@@ -140,15 +132,15 @@ inline size_t scan_partials_bytes(int64_t n) {
     return (size_t)((tiles + 1) * sizeof(int64_t) + 255) & ~(size_t)255;
 }
 
-// Scratch layout: [partials (tiles int64)] [total int64 when total == NULL].
+// Scratch layout: [tile totals (tiles int64)].
 template <class In, bool INCLUSIVE>
 int run_scan(const In* in, int64_t n, int32_t* out, int64_t* total, void* scratch, hipStream_t stream) {
     const int64_t tiles = (n + kScanTile - 1) / kScanTile;
+    if (tiles == 0) return GS3D_OK;  // callers handle empty inputs (total untouched)
     int64_t* partials = reinterpret_cast<int64_t*>(scratch);
     hipLaunchKernelGGL((scan_reduce_kernel<In>), dim3((unsigned)tiles), dim3(kScanThreads), 0, stream, in, n, partials);
-    hipLaunchKernelGGL(scan_partials_kernel, dim3(1), dim3(1024), 0, stream, partials, tiles, total);
     hipLaunchKernelGGL((scan_down_kernel<In, INCLUSIVE>), dim3((unsigned)tiles), dim3(kScanThreads), 0, stream, in, n,
-                       partials, out);
+                       partials, out, total);
     return launch_status("scan");
 }
 
