@@ -300,13 +300,25 @@ GS3D_DEV int64_t xcd_contiguous(int64_t b, int64_t nblocks) {
 template <class K>
 GS3D_DEV uint32_t digit_of(K key, int shift, uint32_t mask) { return (uint32_t)(key >> shift) & mask; }
 
+// Outputs of the depth order's last pass (TAIL != 0): the group count of
+// every record at its sorted position and each block's tile-pair sum, taken
+// from the packed record (TAIL 1: tile rectangle, TAIL 2: AccuTile
+// tiles << 12 | groups).
+struct OrderTail {
+    int32_t* group_counts;
+    int64_t* block_pairs;
+};
+template <int TAIL>
+GS3D_DEV void record_extent(uint64_t record, int32_t& groups, int64_t& area);
+
 // VALS = false sorts keys alone: no value loads, stores or LDS staging, which
 // leaves room for one more block per CU.
-template <class K, class V, bool VALS, int RB = 8>
+template <class K, class V, bool VALS, int RB = 8, int TAIL = 0>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
     V* __restrict__ vals_out, int64_t count, int shift, uint32_t mask, int bits,
-    const int32_t* __restrict__ offsets, int64_t tiles, int digits) {
+    const int32_t* __restrict__ offsets, int64_t tiles, int digits, OrderTail tail) {
+    static_assert(TAIL == 0 || (VALS && sizeof(V) == 8), "the order tail reads 64-bit records");
     constexpr int R = 1 << RB;
     static_assert(R % kSortThreads == 0, "whole digits per thread");
     __shared__ K s_keys[kSortTile];
@@ -399,6 +411,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
         }
     }
     __syncthreads();
+    int64_t area_sum = 0;
 #pragma unroll
     for (int j = 0; j < kSortItems; ++j) {
         const int p = j * kSortThreads + threadIdx.x;
@@ -407,7 +420,20 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
             const int64_t dst = (int64_t)s_gbase[digit_of(kk, shift, mask)] + p;
             keys_out[dst] = kk;  // plain stores: digit runs start mid-line and the L2 merges them
             if (VALS) vals_out[dst] = s_vals[p];
+            if constexpr (TAIL != 0) {
+                int32_t groups;
+                int64_t area;
+                record_extent<TAIL>((uint64_t)s_vals[p], groups, area);
+                tail.group_counts[dst] = groups;
+                area_sum += area;
+            }
         }
+    }
+    if constexpr (TAIL != 0) {
+        __shared__ int64_t s_area[kSortThreads / 64];
+        int64_t total;
+        block_exclusive_scan<kSortThreads>(area_sum, s_area, total);
+        if (threadIdx.x == 0) tail.block_pairs[blockIdx.x] = total;
     }
 }
 
@@ -465,8 +491,11 @@ template <class K, int RB>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
                 hipStream_t s);
 
+// tail_kind (1 or 2, 64-bit values only): the last pass also writes the
+// order tail (record_extent<tail_kind>).
 template <class K, class V = int32_t>
-int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipStream_t s) {
+int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipStream_t s, int tail_kind = 0,
+             OrderTail tail = OrderTail{}) {
     SortScratch sc;
     sort_scratch_bytes(count, &sc, scratch);
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
@@ -479,12 +508,23 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
         const uint32_t mask = (1u << bits) - 1u;
         const int status = sort_counts<K, 8>(kin, count, shift, mask, 256, sc, s);
         if (status != GS3D_OK) return status;
-        if (values)
-            hipLaunchKernelGGL((sort_scatter_kernel<K, V, true>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin,
-                               vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256);
-        else
-            hipLaunchKernelGGL((sort_scatter_kernel<K, V, false>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s, kin,
-                               vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256);
+        const int tail_here = values && shift + 8 >= end_bit ? tail_kind : 0;
+        if constexpr (sizeof(V) == 8) {
+            if (tail_here == 1)
+                hipLaunchKernelGGL((sort_scatter_kernel<K, V, true, 8, 1>), dim3((unsigned)tiles), dim3(kSortThreads),
+                                   0, s, kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, tail);
+            else if (tail_here == 2)
+                hipLaunchKernelGGL((sort_scatter_kernel<K, V, true, 8, 2>), dim3((unsigned)tiles), dim3(kSortThreads),
+                                   0, s, kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, tail);
+        }
+        if (tail_here == 0 || sizeof(V) != 8) {
+            if (values)
+                hipLaunchKernelGGL((sort_scatter_kernel<K, V, true>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
+                                   kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, OrderTail{});
+            else
+                hipLaunchKernelGGL((sort_scatter_kernel<K, V, false>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
+                                   kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, OrderTail{});
+        }
         K* tk = kin;
         kin = kout;
         kout = tk;
@@ -601,7 +641,7 @@ int run_sort_once(K* keys, int64_t count, int end_bit, void* scratch, int ranges
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL((sort_scatter_kernel<K, int32_t, false, RB>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
                        keys, (const int32_t*)nullptr, keys + count, (int32_t*)nullptr, count, 0, mask, end_bit,
-                       sc.offsets, tiles, digits);
+                       sc.offsets, tiles, digits, OrderTail{});
     hipLaunchKernelGGL(digit_ranges_kernel, dim3((unsigned)((ranges_count + 255) / 256)), dim3(256), 0, s,
                        sc.offsets, count, digits, ranges_count, ranges);
     return launch_status("one-pass radix sort");
@@ -776,6 +816,21 @@ GS3D_DEV int groups_of(const TileRect& r) {
     if (r.x1 <= r.x0) return 0;
     return (((r.x1 - 1) >> kGroupShift) - (r.x0 >> kGroupShift) + 1) *
            (((r.y1 - 1) >> kGroupShift) - (r.y0 >> kGroupShift) + 1);
+}
+
+// Group count and tile pairs of a packed record (the order tail; the same
+// values order_counts_kernel computes for PACKED records).
+template <int TAIL>
+GS3D_DEV void record_extent(uint64_t record, int32_t& groups, int64_t& area) {
+    if constexpr (TAIL == 1) {
+        const TileRect r = record_rect<true>(record, RowGeometry{nullptr, nullptr, nullptr, 0}, 0, 0);
+        groups = groups_of(r);
+        area = r.x1 > r.x0 ? (int64_t)(r.x1 - r.x0) * (r.y1 - r.y0) : 0;
+    } else {
+        const uint32_t hi = (uint32_t)(record >> 32);
+        groups = (int32_t)(hi & 4095u);
+        area = hi >> 12;
+    }
 }
 
 // Row order: depth-bit keys and records (coalesced reads of depth, centre
@@ -1689,23 +1744,25 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     else
         hipLaunchKernelGGL((gs3d::row_records_kernel<false, false>), grid, block, 0, s, a.depths, geo, rows, d.gx,
                            d.gy, sc.keys, a.order, a.tiles_out, fp);
-    // order holds 2*rows records: [0, rows) sorted result, [rows, 2rows) ping-pong.
-    int status = gs3d::run_sort<uint32_t, uint64_t>(sc.keys, a.order, rows, 32, sc.sort, s);
+    // order holds 2*rows records: [0, rows) sorted result, [rows, 2rows) ping-pong.  With packed
+    // records the last pass also writes each row's group count at its sorted position and the
+    // blocks' tile-pair sums; otherwise order_counts_kernel computes them from the geometry.
+    const int tail_kind = packed ? (accu ? 2 : 1) : 0;
+    int status = gs3d::run_sort<uint32_t, uint64_t>(sc.keys, a.order, rows, 32, sc.sort, s, tail_kind,
+                                                    gs3d::OrderTail{sc.counts, sc.pairs});
     if (status != GS3D_OK) return status;
-    const dim3 cgrid(gs3d::blocks_for(rows, gs3d::kBinThreads)), cblock(gs3d::kBinThreads);
-    if (accu && packed)
-        hipLaunchKernelGGL((gs3d::order_counts_kernel<true, true>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
-                           d.gy, sc.counts, sc.pairs);
-    else if (accu)
-        hipLaunchKernelGGL((gs3d::order_counts_kernel<false, true>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
-                           d.gy, sc.counts, sc.pairs);
-    else if (packed)
-        hipLaunchKernelGGL((gs3d::order_counts_kernel<true, false>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
-                           d.gy, sc.counts, sc.pairs);
-    else
-        hipLaunchKernelGGL((gs3d::order_counts_kernel<false, false>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
-                           d.gy, sc.counts, sc.pairs);
-    hipLaunchKernelGGL(gs3d::sum_i64_kernel, dim3(1), dim3(1024), 0, s, sc.pairs, (int64_t)cgrid.x, a.totals + 1);
+    int64_t pair_blocks = (rows + gs3d::kSortTile - 1) / gs3d::kSortTile;
+    if (!packed) {
+        const dim3 cgrid(gs3d::blocks_for(rows, gs3d::kBinThreads)), cblock(gs3d::kBinThreads);
+        if (accu)
+            hipLaunchKernelGGL((gs3d::order_counts_kernel<false, true>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
+                               d.gy, sc.counts, sc.pairs);
+        else
+            hipLaunchKernelGGL((gs3d::order_counts_kernel<false, false>), cgrid, cblock, 0, s, a.order, rows, geo,
+                               d.gx, d.gy, sc.counts, sc.pairs);
+        pair_blocks = cgrid.x;
+    }
+    hipLaunchKernelGGL(gs3d::sum_i64_kernel, dim3(1), dim3(1024), 0, s, sc.pairs, pair_blocks, a.totals + 1);
     status = gs3d::run_scan<int32_t, true>(sc.counts, rows, a.group_offsets, a.totals, sc.scan, s);
     if (status != GS3D_OK) return status;
     return gs3d::launch_status("gs3d_order_rows");
