@@ -213,8 +213,9 @@ def stage_bytes(scene, info):
         "project": n * 44 + sh_in + views * n * (60 + (12 if sh is not None else 0)),
         # keys and records (depth 4 + centre 8 + radius 4 in, key 4 + record 8 out); 4 radix passes,
         # each reading the keys for its histogram (4) and reading + writing (key, record) (24); group
-        # counts (record 8 in, count 4 out); inclusive scan (4 in, 4 out)
-        "order": R * (28 + 4 * (4 + 24) + 12 + 8),
+        # counts written by the last pass (4; tile grids of at most 256 x 256, whose records carry
+        # the rectangle); inclusive scan (4 in, 4 out)
+        "order": R * (28 + 4 * (4 + 24) + 4 + 8),
         # items: records and offsets in (12 B/row), items out (8 B/item); group sort (keys read for the
         # histogram 8 + read and written 16 per pass; one 10-bit pass up to 1024 groups, whose digit
         # scan gives the group ranges, else 8-bit passes and a range search, 8 B/item); count and
