@@ -283,3 +283,54 @@ def test_packed_metadata_several_cameras_and_batches():
         want = _np(getattr(dense["means2d"], attr))[bi, ci, gi]
         compare(f"packed_means2d_{attr}", _np(getattr(packed["means2d"], attr)), want, rtol=1e-4,
                 atol=1e-5 * max(1.0, float(np.abs(want).max())))
+
+
+def test_repeated_backward_and_interleaved_frames():
+    # The blend VJP accumulates into buffers cleared on a second stream
+    # during the forward blend: a second backward of the same graph
+    # (retain_graph) must use fresh buffers (gradients add up to twice one
+    # backward), and two frames whose forwards run before either backward
+    # must keep their own buffers.
+    scene = synthetic.make_scene("sh3_720p", n=4000, width=128, height=96, seed=17).to(DEV)
+    print("repeated backward, interleaved frames", flush=True)
+    W = scene.loss_weights
+
+    def frame(leaves, sh, absgrad):
+        res = gs3d.rasterize(leaves["means"], leaves["quats"], leaves["scales"], leaves["opacities"],
+                             scene.viewmats, scene.Ks, scene.width, scene.height, sh_coeffs=sh, sh_degree=3,
+                             absgrad=absgrad)
+        return (res.features * W[..., :3]).sum() + (res.alpha * W[..., 3:]).sum()
+
+    def close(got, want):
+        # Run-to-run differences come only from the order of float atomics.
+        torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-6 * float(want.abs().max().clamp(min=1.0)))
+
+    def fresh():
+        leaves = {k: getattr(scene, k).clone().requires_grad_(True) for k in ("means", "quats", "scales", "opacities")}
+        return leaves, scene.sh_coeffs.clone().requires_grad_(True)
+
+    for absgrad in (False, True):
+        leaves, sh = fresh()
+        frame(leaves, sh, absgrad).backward()
+        once = {k: v.grad.clone() for k, v in leaves.items()} | {"sh": sh.grad.clone()}
+        leaves, sh = fresh()
+        loss = frame(leaves, sh, absgrad)
+        loss.backward(retain_graph=True)
+        loss.backward()
+        for k, v in list(leaves.items()) + [("sh", sh)]:
+            close(v.grad, 2 * once[k])
+        # Two forwards, then both backwards in reverse order.
+        la, sa = fresh()
+        lb, sb = fresh()
+        loss_a = frame(la, sa, absgrad)
+        loss_b = frame(lb, sb, absgrad)
+        loss_b.backward()
+        loss_a.backward()
+        for k in leaves:
+            close(la[k].grad, once[k])
+            close(lb[k].grad, once[k])
+        close(sa.grad, once["sh"])
+    # A forward that needs gradients but is never differentiated.
+    leaves, sh = fresh()
+    frame(leaves, sh, False)
+    torch.cuda.synchronize()
