@@ -1397,8 +1397,77 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
             if (lane == t) mine = run;
         }
     };
-    walk(std::integral_constant<int, 0>{});
-    walk(std::integral_constant<int, 1>{});
+    // Buffered write: the tiles of each half are visited from the highest bit
+    // down and every step's mask word is shifted left as the walk proceeds, so
+    // one add of the word to itself both advances it and yields the tile's
+    // membership bit as its carry (the carry mask is the ballot).  Each step
+    // then costs the carry add, the two-part lane count, one address and one
+    // select; non-members write to their own slot beyond the run.
+    auto walk_buf = [&](auto half) {
+        constexpr int H = decltype(half)::value;
+        static_assert(kChunk % 128 == 0, "store loop reads two 64-word rows below kChunk");
+        uint32_t todo = (uint32_t)(todo_all >> (32 * H));
+        uint32_t w[kChunkSteps];
+#pragma unroll
+        for (int k = 0; k < kChunkSteps; ++k) w[k] = (uint32_t)(mask[k] >> (32 * H));
+        using lds_i32 = __attribute__((address_space(3))) int32_t;
+        // LDS byte addresses: the slice's first word (wave-uniform) and this
+        // lane's spare slot.
+        const uint32_t slice_word =
+            (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(uintptr_t)(lds_i32*)run_lds >> 2));
+        const uint32_t spare = (slice_word + (uint32_t)(kChunk + lane)) << 2;
+        int top = 31;  // bit of the original word now at bit 31 of w[]
+        while (todo) {
+            const int tb = 31 - __builtin_clz(todo);
+            todo ^= 1u << tb;
+            const int sh = top - tb;
+            if (sh != 0) {
+#pragma unroll
+                for (int k = 0; k < kChunkSteps; ++k) w[k] <<= sh;
+            }
+            top = tb - 1;
+            const int t = 32 * H + tb;
+            const uint32_t start = (uint32_t)__builtin_amdgcn_readlane((int)init, t);
+            uint32_t end_word = slice_word;  // LDS word after the run so far
+#pragma unroll
+            for (int k = 0; k < kChunkSteps; ++k) {
+                // b = carry mask of w + w: lanes whose item covers tile t.
+                uint32_t next;
+                uint64_t b;
+                asm volatile("v_add_co_u32_e64 %0, %1, %2, %2" : "=v"(next), "=s"(b) : "v"(w[k]));
+                w[k] = next;
+                const uint32_t rank =
+                    __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+                const uint32_t member = (rank + end_word) << 2;
+                uint32_t at;
+                asm volatile("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(at) : "v"(spare), "v"(member), "s"(b));
+                *(lds_i32*)(uintptr_t)at = id[k];
+                end_word += (uint32_t)__popcll(b);
+            }
+            const uint32_t run = end_word - slice_word;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            // Two LDS reads in flight per lane before the stores: a run holds
+            // at most kChunk ids, so e0 <= kChunk - 128 and both reads stay in
+            // the slice (words past the run are read but not stored).
+            for (uint32_t e0 = 0; e0 < run; e0 += 128) {
+                const uint32_t e1 = e0 + (uint32_t)lane, e2 = e1 + 64u;
+                int32_t v1 = run_lds[e1], v2 = run_lds[e2];
+                asm volatile("" : "+v"(v1), "+v"(v2));  // both reads issued before either store
+                if (e1 < run) __builtin_amdgcn_raw_buffer_store_b32(v1, rsrc, (int)(e1 * 4u), (int)(start * 4u), 0);
+                if (e2 < run) __builtin_amdgcn_raw_buffer_store_b32(v2, rsrc, (int)(e2 * 4u), (int)(start * 4u), 0);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+    };
+    if constexpr (WRITE && BUF) {
+        walk_buf(std::integral_constant<int, 0>{});
+        walk_buf(std::integral_constant<int, 1>{});
+    } else {
+        walk(std::integral_constant<int, 0>{});
+        walk(std::integral_constant<int, 1>{});
+    }
     if constexpr (!WRITE) counts[slot + s] = mine;
 }
 
