@@ -93,3 +93,19 @@ def test_statistics_request_validation():
     with pytest.raises(TypeError):
         prepare_statistics(["bogus"], batch_dims=(), batch_count=1, cameras=1, n=1, width=W, height=H,
                            device=torch.device("cpu"))
+
+
+def test_pair_count_checks():
+    # Totals beyond the int32 offsets are an overflow; view groups split at
+    # the int32 limit, as the reference's per-view limit allows.
+    from dsl_splat_amd.splatting import binning
+
+    binning.check_pair_counts(0, 0)
+    binning.check_pair_counts(binning.PAIR_LIMIT, binning.PAIR_LIMIT)
+    with pytest.raises(OverflowError):
+        binning.check_pair_counts(1, binning.PAIR_LIMIT + 1)
+    limit = binning.PAIR_LIMIT
+    assert binning.view_groups([limit // 2, limit // 2, 3]) == [(0, 2), (2, 3)]
+    assert binning.view_groups([1, 2, 3]) == [(0, 3)]
+    with pytest.raises(OverflowError):
+        binning.view_groups([1, limit + 1])
