@@ -811,10 +811,18 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     }
 }
 
-template <int CH>
-int launch_fwd(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned long long* counts,
-               unsigned blocks, int c0, hipStream_t s) {
-    constexpr int PIX = PixFor<CH, false>::value;
+// Grids of fewer tiles than this (all views) run the narrow-channel blends
+// at one pixel per lane: four wavefronts per tile instead of two, so that a
+// small frame still spreads over the SIMDs (each tile's list is walked
+// serially, and a frame of a few hundred tiles is bound by that latency).
+#ifndef GS3D_SMALL_GRID
+#define GS3D_SMALL_GRID 1024
+#endif
+constexpr unsigned kSmallGrid = GS3D_SMALL_GRID;
+
+template <int CH, int PIX>
+int launch_fwd_pix(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned long long* counts,
+                   unsigned blocks, int c0, hipStream_t s) {
     const dim3 grid(blocks), block(kTilePixels / PIX);
     if (st) {
         hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1>), grid, block, 0, s, a, *st, c0, nullptr);
@@ -829,6 +837,16 @@ int launch_fwd(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsi
     return launch_status("gs3d_render_fwd");
 }
 
+template <int CH>
+int launch_fwd(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned long long* counts,
+               unsigned blocks, int c0, hipStream_t s) {
+    constexpr int PIX = PixFor<CH, false>::value;
+    if constexpr (PIX > 1) {
+        if (blocks < kSmallGrid) return launch_fwd_pix<CH, 1>(a, st, counts, blocks, c0, s);
+    }
+    return launch_fwd_pix<CH, PIX>(a, st, counts, blocks, c0, s);
+}
+
 // One forward window of `width` channels starting at c0.
 inline int launch_fwd_window(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned long long* counts,
                              unsigned blocks, int c0, int width, hipStream_t s) {
@@ -839,9 +857,8 @@ inline int launch_fwd_window(const gs3d_render_args& a, const gs3d_render_stats_
     return launch_fwd<kWindow>(a, st, counts, blocks, c0, s);
 }
 
-template <int CH, bool GEOM>
-int launch_bwd(const gs3d_render_bwd_args& b, unsigned blocks, int c0, hipStream_t s) {
-    constexpr int PIX = PixFor<CH, true>::value;
+template <int CH, bool GEOM, int PIX>
+int launch_bwd_pix(const gs3d_render_bwd_args& b, unsigned blocks, int c0, hipStream_t s) {
     if constexpr (GEOM) {
         if (b.abs_centers) {
             hipLaunchKernelGGL((render_bwd_kernel<CH, true, PIX, true>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, b, c0);
@@ -850,6 +867,15 @@ int launch_bwd(const gs3d_render_bwd_args& b, unsigned blocks, int c0, hipStream
     }
     hipLaunchKernelGGL((render_bwd_kernel<CH, false, PIX, GEOM>), dim3(blocks), dim3(kTilePixels / PIX), 0, s, b, c0);
     return launch_status("gs3d_render_bwd");
+}
+
+template <int CH, bool GEOM>
+int launch_bwd(const gs3d_render_bwd_args& b, unsigned blocks, int c0, hipStream_t s) {
+    constexpr int PIX = PixFor<CH, true>::value;
+    if constexpr (PIX > 1) {
+        if (blocks < kSmallGrid) return launch_bwd_pix<CH, GEOM, 1>(b, blocks, c0, s);
+    }
+    return launch_bwd_pix<CH, GEOM, PIX>(b, blocks, c0, s);
 }
 
 inline int check_render_args(const gs3d_render_args& a) {

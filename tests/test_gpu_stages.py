@@ -34,10 +34,14 @@ def _say(*args):
     print(*args, flush=True)
 
 
+# Frames of fewer than 1024 tiles (all views) blend at one pixel per lane,
+# larger ones at two: the "wide" scenes cover the two-pixel kernels.
 SCENES = {
     "small_rgb": dict(name="small", n=4000, width=128, height=96, seed=1),
     "sh3_4view": dict(name="sh3_1080p_4view", n=6000, width=160, height=96, seed=2),
     "sh3_720p": dict(name="sh3_720p", n=5000, width=200, height=120, seed=3),
+    "wide_rgb": dict(name="small", n=16000, width=576, height=480, seed=11),
+    "wide_sh3_4view": dict(name="sh3_1080p_4view", n=12000, width=288, height=240, seed=12),
 }
 
 
@@ -184,7 +188,8 @@ def _frame(scene, degree):
 
 
 @pytest.mark.parametrize("key,degree,extra,bg", [("small_rgb", None, False, True), ("sh3_4view", 3, False, False),
-                                                 ("small_rgb", None, True, True)])
+                                                 ("small_rgb", None, True, True), ("wide_rgb", None, True, True),
+                                                 ("wide_sh3_4view", 3, False, False)])
 def test_render_forward_bit_exact(key, degree, extra, bg):
     scene = _scene(key)
     _say(f"render fwd {key} extra={extra} bg={bg}")
@@ -204,12 +209,13 @@ def test_render_forward_bit_exact(key, degree, extra, bg):
     assert ct.max() > 0
 
 
-def test_render_culling_edge_cases():
+@pytest.mark.parametrize("n,width,height", [(3000, 136, 100), (12000, 576, 480)])
+def test_render_culling_edge_cases(n, width, height):
     # Needle-shaped Gaussians at every orientation and opacities straddling
     # the 1/255 threshold: the per-wavefront strip culling must not change a
-    # single forward bit or the gradients.
-    _say("render culling edge cases")
-    scene = synthetic.make_scene("small", n=3000, width=136, height=100, seed=5)
+    # single forward bit or the gradients (one and two pixels per lane).
+    _say(f"render culling edge cases {width}x{height}")
+    scene = synthetic.make_scene("small", n=n, width=width, height=height, seed=5)
     g = torch.Generator().manual_seed(7)
     n = scene.means.shape[0]
     long_axis = torch.exp(torch.rand(n, generator=g) * 2.0 - 3.0)
@@ -242,7 +248,8 @@ def test_render_culling_edge_cases():
         check_gradient(name, got, ref[name], bound[name])
 
 
-@pytest.mark.parametrize("key,degree,absgrad", [("small_rgb", None, True), ("sh3_4view", 3, False)])
+@pytest.mark.parametrize("key,degree,absgrad", [("small_rgb", None, True), ("sh3_4view", 3, False),
+                                                ("wide_rgb", None, True), ("wide_sh3_4view", 3, False)])
 def test_render_backward_parity(key, degree, absgrad):
     scene = _scene(key)
     _say(f"render bwd {key}")
