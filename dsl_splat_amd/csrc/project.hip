@@ -78,13 +78,26 @@ struct CovParts {
     M3 R, M, Sigma, J, W, Tm, X;
 };
 
-// gs3d/projection.py:37-86.
+// a / b, correctly rounded; with APPROX a times the hardware reciprocal of b
+// (about one ulp), for quantities that only enter gradients.
+template <bool APPROX>
+GS3D_DEV float quotient(float a, float b) {
+    if constexpr (APPROX)
+        return a * __builtin_amdgcn_rcpf(b);
+    else
+        return a / b;
+}
+
+// gs3d/projection.py:37-86.  APPROX (the VJP's recomputation): the divisions
+// of t, J and nothing else are approximate -- the clamp limits stay exact,
+// and the VJP takes its clamp decisions from exact quotients of its own.
+template <bool APPROX = false>
 GS3D_DEV void screen_covariance(const float* pos, const float* q, const float* s, const float* V, int width,
                                 int height, float fx, float fy, CovParts& st, float* cov) {
     st.limx = 1.3f * (float)width / (2.0f * fx);
     st.limy = 1.3f * (float)height / (2.0f * fy);
-    st.t[0] = sel_clamp(pos[0] / pos[2], -st.limx, st.limx) * pos[2];
-    st.t[1] = sel_clamp(pos[1] / pos[2], -st.limy, st.limy) * pos[2];
+    st.t[0] = sel_clamp(quotient<APPROX>(pos[0], pos[2]), -st.limx, st.limx) * pos[2];
+    st.t[1] = sel_clamp(quotient<APPROX>(pos[1], pos[2]), -st.limy, st.limy) * pos[2];
     st.t[2] = pos[2];
     st.R = glm_rotation(q);
     M3 S;
@@ -98,14 +111,14 @@ GS3D_DEV void screen_covariance(const float* pos, const float* q, const float* s
     st.M = ref_matmul(S, st.R);
     st.Sigma = ref_matmul(transpose3(st.M), st.M);
     const float* t = st.t;
-    st.J.m[0][0] = fx / t[2];
+    st.J.m[0][0] = quotient<APPROX>(fx, t[2]);
     st.J.m[0][1] = 0.0f;
     st.J.m[0][2] = 0.0f;
     st.J.m[1][0] = 0.0f;
-    st.J.m[1][1] = fy / t[2];
+    st.J.m[1][1] = quotient<APPROX>(fy, t[2]);
     st.J.m[1][2] = 0.0f;
-    st.J.m[2][0] = -(fx * t[0]) / (t[2] * t[2]);
-    st.J.m[2][1] = -(fy * t[1]) / (t[2] * t[2]);
+    st.J.m[2][0] = quotient<APPROX>(-(fx * t[0]), t[2] * t[2]);
+    st.J.m[2][1] = quotient<APPROX>(-(fy * t[1]), t[2] * t[2]);
     st.J.m[2][2] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 3; ++i)
@@ -396,8 +409,12 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(8)))
 // ---------------------------------------------------------------------------
 constexpr int kMaxViewsCamLds = 16;
 
+// One view's projection VJP.  The covariance part stops at the gradient of
+// the 3D covariance Sigma: it is linear in that gradient, so the views' sum
+// goes through covariance_vjp once per Gaussian.
 struct VJP {
-    float mean[3], quat[4], scale[3], opacity;
+    float mean[3], opacity;
+    M3 sigma;           // d loss / d Sigma
     float view[3][4];   // rows 0..2
     float proj[3][4];   // rows 0, 1, 3
 };
@@ -438,14 +455,16 @@ GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, 
     float pos[3];
 #pragma unroll
     for (int r = 0; r < 3; ++r) pos[r] = point_row(V, r, mean);
+    // Divisions that only scale gradients use the hardware reciprocal; the
+    // clamp decisions below keep exact quotients, as in the forward.
     CovParts st;
     float cov[3];
-    screen_covariance(pos, q, s, V, width, height, fx, fy, st, cov);
+    screen_covariance<true>(pos, q, s, V, width, height, fx, fy, st, cov);
     g.opacity = gk[3];
     // splatting/geometry.py:61-71.
     const float a = cov[0], b = cov[1], c = cov[2];
     const float det = a * c - b * b;
-    const float factor = 1.0f / (det * det + 0.0000001f);
+    const float factor = __builtin_amdgcn_rcpf(det * det + 0.0000001f);
     const float x = gk[0], y = gk[1], z = gk[2];
     M3 gcov2 = zero3();
     gcov2.m[0][0] = factor * (-c * c * x + b * c * y + (det - a * c) * z);
@@ -459,37 +478,9 @@ GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, 
     for (int i = 0; i < 3; ++i)
 #pragma unroll
         for (int j = 0; j < 3; ++j) gTm.m[i][j] += gTmT.m[j][i];
-    const M3 gSigma = transpose3(gSigmaT);
+    g.sigma = transpose3(gSigmaT);
     M3 gW = zero3(), gJ = zero3();
     matmul_vjp(st.W, st.J, gTm, gW, gJ);
-    M3 gMT = zero3(), gM = zero3();
-    matmul_vjp(transpose3(st.M), st.M, gSigma, gMT, gM);
-#pragma unroll
-    for (int i = 0; i < 3; ++i)
-#pragma unroll
-        for (int j = 0; j < 3; ++j) gM.m[i][j] += gMT.m[j][i];
-    M3 gR;
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            acc += gM.m[i][j] * st.R.m[i][j];
-            gR.m[i][j] = s[i] * gM.m[i][j];
-        }
-        g.scale[i] = acc;
-    }
-    {   // splatting/math.py:13-28.
-        const float r = q[0], qx = q[1], qy = q[2], qz = q[3];
-        const auto& G = gR.m;
-        g.quat[0] = 2.0f * (qz * (G[0][1] - G[1][0]) + qy * (G[2][0] - G[0][2]) + qx * (G[1][2] - G[2][1]));
-        g.quat[1] = 2.0f * (qy * (G[0][1] + G[1][0]) + qz * (G[0][2] + G[2][0]) + r * (G[1][2] - G[2][1])) -
-                    4.0f * qx * (G[1][1] + G[2][2]);
-        g.quat[2] = 2.0f * (qx * (G[0][1] + G[1][0]) + r * (G[2][0] - G[0][2]) + qz * (G[1][2] + G[2][1])) -
-                    4.0f * qy * (G[0][0] + G[2][2]);
-        g.quat[3] = 2.0f * (r * (G[0][1] - G[1][0]) + qx * (G[0][2] + G[2][0]) + qy * (G[1][2] + G[2][1])) -
-                    4.0f * qz * (G[0][0] + G[1][1]);
-    }
 #pragma unroll
     for (int r = 0; r < 3; ++r)
 #pragma unroll
@@ -500,11 +491,12 @@ GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, 
         for (int j = 0; j < 3; ++j) g.view[j][i] += gW.m[i][j];
     const float* t = st.t;
     const float tz2 = t[2] * t[2];
+    const float rz2 = __builtin_amdgcn_rcpf(tz2), rz3 = __builtin_amdgcn_rcpf(tz2 * t[2]);
     float gt[3];
-    gt[0] = gJ.m[2][0] * (-fx / tz2);
-    gt[1] = gJ.m[2][1] * (-fy / tz2);
-    gt[2] = gJ.m[0][0] * (-fx / tz2) + gJ.m[1][1] * (-fy / tz2) + gJ.m[2][0] * (2.0f * fx * t[0] / (tz2 * t[2])) +
-            gJ.m[2][1] * (2.0f * fy * t[1] / (tz2 * t[2]));
+    gt[0] = gJ.m[2][0] * (-fx * rz2);
+    gt[1] = gJ.m[2][1] * (-fy * rz2);
+    gt[2] = gJ.m[0][0] * (-fx * rz2) + gJ.m[1][1] * (-fy * rz2) + gJ.m[2][0] * (2.0f * fx * t[0] * rz3) +
+            gJ.m[2][1] * (2.0f * fy * t[1] * rz3);
     // splatting/geometry.py:42-51: saturated x/y are constants.
     const float xr = pos[0] / pos[2], yr = pos[1] / pos[2];
     float gpos[3];
@@ -526,7 +518,7 @@ GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, 
     float clip[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) clip[r] = point_row(P, r, mean);
-    const float inv_w = 1.0f / (clip[3] + 0.0000001f);
+    const float inv_w = __builtin_amdgcn_rcpf(clip[3] + 0.0000001f);
     const float gnx = gc[0] * (0.5f * (float)width);
     const float gny = gc[1] * (0.5f * (float)height);
     const float gclip[3] = {gnx * inv_w, gny * inv_w, -(gnx * clip[0] + gny * clip[1]) * inv_w * inv_w};
@@ -540,6 +532,44 @@ GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, 
         }
         g.proj[r][3] = gclip[r];
     }
+}
+
+// Sigma = M^T M with M = S R(q): quaternion and scale gradients of a summed
+// d loss / d Sigma (splatting/math.py:13-28 for the rotation).
+GS3D_DEV void covariance_vjp(const float* q, const float* s, const M3& gSigma, float* gq, float* gs) {
+#pragma clang fp contract(fast)
+    const M3 R = glm_rotation(q);
+    M3 M;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) M.m[i][j] = s[i] * R.m[i][j];
+    M3 gMT = zero3(), gM = zero3();
+    matmul_vjp(transpose3(M), M, gSigma, gMT, gM);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) gM.m[i][j] += gMT.m[j][i];
+    M3 gR;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            acc += gM.m[i][j] * R.m[i][j];
+            gR.m[i][j] = s[i] * gM.m[i][j];
+        }
+        gs[i] = acc;
+    }
+    const float r = q[0], qx = q[1], qy = q[2], qz = q[3];
+    const auto& G = gR.m;
+    gq[0] = 2.0f * (qz * (G[0][1] - G[1][0]) + qy * (G[2][0] - G[0][2]) + qx * (G[1][2] - G[2][1]));
+    gq[1] = 2.0f * (qy * (G[0][1] + G[1][0]) + qz * (G[0][2] + G[2][0]) + r * (G[1][2] - G[2][1])) -
+            4.0f * qx * (G[1][1] + G[2][2]);
+    gq[2] = 2.0f * (qx * (G[0][1] + G[1][0]) + r * (G[2][0] - G[0][2]) + qz * (G[1][2] + G[2][1])) -
+            4.0f * qy * (G[0][0] + G[2][2]);
+    gq[3] = 2.0f * (r * (G[0][1] - G[1][0]) + qx * (G[0][2] + G[2][0]) + qy * (G[1][2] + G[2][1])) -
+            4.0f * qz * (G[0][0] + G[1][1]);
 }
 
 // Projection VJP, all views of a Gaussian per thread.  Held to 128 VGPRs
@@ -574,6 +604,7 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(4)))
             for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
         }
         float gm[3] = {0, 0, 0}, gq[4] = {0, 0, 0, 0}, gs[3] = {0, 0, 0}, go = 0.0f;
+        M3 gsigma = zero3();
         for (int v = 0; v < views; ++v) {
             const int64_t row = (int64_t)v * n + i;
             const bool vis = valid && a.radii[row] > 0;
@@ -590,9 +621,9 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
                 for (int k = 0; k < 3; ++k) gm[k] += g.mean[k];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) gq[k] += g.quat[k];
+                for (int r = 0; r < 3; ++r)
 #pragma unroll
-                for (int k = 0; k < 3; ++k) gs[k] += g.scale[k];
+                    for (int c = 0; c < 3; ++c) gsigma.m[r][c] += g.sigma.m[r][c];
                 go += g.opacity;
             }
             if (a.screen_grad && valid) st_stream(reinterpret_cast<float2*>(a.screen_grad) + row, screen);
@@ -613,6 +644,7 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(4)))
             }
         }
         if (valid) {
+            covariance_vjp(q, s, gsigma, gq, gs);
             if (a.grad_means)
 #pragma unroll
                 for (int k = 0; k < 3; ++k) a.grad_means[3 * i + k] = gm[k];  // read again by the SH VJP
