@@ -1004,11 +1004,12 @@ __global__ __launch_bounds__(kShRowBlock) void sh_rows_bwd_kernel(gs3d_project_b
             float gd[3] = {0.0f, 0.0f, 0.0f};
             if (DEG > 0 && vis[u]) {
 #pragma clang fp contract(fast)
-                const float il = 1.0f / sel_max(length[u], 1.0e-12f);
+                const float il = __builtin_amdgcn_rcpf(sel_max(length[u], 1.0e-12f));  // gradient only
 #pragma unroll
                 for (int q = 0; q < 3; ++q) gd[q] = ug[u][q] * il;
                 if (length[u] >= 1.0e-12f) {
-                    const float f = (unit[u][0] * ug[u][0] + unit[u][1] * ug[u][1] + unit[u][2] * ug[u][2]) / length[u];
+                    const float f = (unit[u][0] * ug[u][0] + unit[u][1] * ug[u][1] + unit[u][2] * ug[u][2]) *
+                                    __builtin_amdgcn_rcpf(length[u]);
 #pragma unroll
                     for (int q = 0; q < 3; ++q) gd[q] = gd[q] - unit[u][q] * f;
                 }
