@@ -276,7 +276,17 @@ def kernel_timings(scene, frame):
             e1.record()
             torch.cuda.synchronize()
             out["project_kernel"] += e0.elapsed_time(e1) / launches
-        del flush
+        # A plain 2 GiB device copy on the same GPU: the bandwidth a
+        # streaming kernel reaches here, beside the 8 TB/s peak.
+        dst = torch.empty_like(flush)
+        dst.copy_(flush)
+        e0.record()
+        for _ in range(launches):
+            dst.copy_(flush)
+        e1.record()
+        torch.cuda.synchronize()
+        out["copy_gbps"] = 2 * flush.numel() * 4 / (e0.elapsed_time(e1) / launches * 1e-3) / 1e9
+        del flush, dst
         # Contribution statistics (a masked count and a weighted sum over
         # per-view pixel maps) observed by the forward blend, against the
         # plain forward blend, both back-to-back.
@@ -495,6 +505,8 @@ def main():
             "bytes": kernel_bytes,
             "note": "parameters read once for all views (44 B/G) and 60 B per (view, Gaussian) written; the "
                     "colour kernel's bytes are in stages.project",
+            "copy_gbps": round(kt["copy_gbps"], 1),
+            "copy_note": "a 2 GiB device-to-device copy (read + write) timed on the same GPU, for context",
         },
         "stages": head["stages"],
         "stages_1_3": head["stages_1_3"],
