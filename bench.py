@@ -202,7 +202,7 @@ def frame_info(scene):
 def stage_bytes(scene, info):
     """Algorithmic bytes of every HBM-bound stage: what its kernels must read
     and write once each."""
-    M, S, T, R = info["pairs"], info["group_pairs"], info["tiles"], info["rows"]
+    M, S, T, R, V = info["pairs"], info["group_pairs"], info["tiles"], info["rows"], info["visible"]
     sh = scene.sh_coeffs
     views, n = scene.viewmats.shape[0], len(scene.means)
     K = 0 if sh is None else sh.shape[-2]
@@ -211,11 +211,12 @@ def stage_bytes(scene, info):
         # params 44 B/G (+ SH once for all views) in; per view centers 8, conics+opacity 16, radii 4,
         # tiles 4, depth 4, means2d 8, meta opacity 4, meta conic 12 (+ colour 12) out
         "project": n * 44 + sh_in + views * n * (60 + (12 if sh is not None else 0)),
-        # keys and records (depth 4 + centre 8 + radius 4 in, key 4 + record 8 out); 4 radix passes,
-        # each reading the keys for its histogram (4) and reading + writing (key, record) (24); group
-        # counts written by the last pass (4; tile grids of at most 256 x 256, whose records carry
-        # the rectangle); inclusive scan (4 in, 4 out)
-        "order": R * (28 + 4 * (4 + 24) + 4 + 8),
+        # keys and records (depth 4 + centre 8 + radius 4 in, key 4 + record 8 out); the first radix
+        # pass reads every row's key for its histogram (4) and (key, record) (12) and writes the V
+        # rows that touch a tile (12); three more passes over those V rows (key 4 for the histogram,
+        # (key, record) 12 in and 12 out); group counts at the sorted positions (4) and filler
+        # records + zero counts after them ((R - V) x 12); inclusive scan of the counts (4 in, 4 out)
+        "order": R * (28 + 4 + 12 + 8) + V * (12 + 3 * 28 + 4) + (R - V) * 12,
         # items: records and offsets in (12 B/row), items out (8 B/item); group sort (keys read for the
         # histogram 8 + read and written 16 per pass; one 10-bit pass up to 1024 groups, whose digit
         # scan gives the group ranges, else 8-bit passes and a range search, 8 B/item); count and

@@ -9,6 +9,7 @@
 #include <climits>
 
 #include <type_traits>
+#include <utility>
 #include <mutex>
 
 #include "common.hpp"
@@ -311,13 +312,26 @@ struct OrderTail {
 template <int TAIL>
 GS3D_DEV void record_extent(uint64_t record, int32_t& groups, int64_t& area);
 
+// Rows that the depth order leaves out: they touch no tile group, and
+// row_records_kernel gives them the key kDroppedKey (a NaN pattern, never the
+// depth bits of a projected row).  The first pass (DROP) neither counts nor
+// places such keys; `live` (device memory, from that pass's digit scan) is
+// then the number of keys the later passes sort, and the last pass (`fill`)
+// writes `filler` into every position of [live, count).
+constexpr uint32_t kDroppedKey = 0xFFFFFFFFu;
+struct Culled {
+    const int64_t* live;  // null: every key of [0, count) is sorted
+    bool fill;
+    uint64_t filler;
+};
+
 // VALS = false sorts keys alone: no value loads, stores or LDS staging, which
 // leaves room for one more block per CU.
-template <class K, class V, bool VALS, int RB = 8, int TAIL = 0>
+template <class K, class V, bool VALS, int RB = 8, int TAIL = 0, bool DROP = false>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
     V* __restrict__ vals_out, int64_t count, int shift, uint32_t mask, int bits,
-    const int32_t* __restrict__ offsets, int64_t tiles, int digits, OrderTail tail) {
+    const int32_t* __restrict__ offsets, int64_t tiles, int digits, OrderTail tail, Culled cull) {
     static_assert(TAIL == 0 || (VALS && sizeof(V) == 8), "the order tail reads 64-bit records");
     constexpr int R = 1 << RB;
     static_assert(R % kSortThreads == 0, "whole digits per thread");
@@ -332,29 +346,30 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     // in the output, and partial lines merge in that XCD's L2.
     const int64_t tile = GS3D_SORT_XCD ? xcd_contiguous(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
     const int64_t tile_base = tile * kSortTile;
-    const int64_t valid_count = min((int64_t)kSortTile, count - tile_base);
+    const int64_t live = cull.live ? min(count, *cull.live) : count;
     K key[kSortItems];
     V val[kSortItems];
     uint32_t rank[kSortItems];
+    bool in[kSortItems];  // the key takes part in this pass
     const int64_t base = tile_base + wave * (kSortTile / 4) + lane;
 #pragma unroll
     for (int k = 0; k < kSortItems; ++k) {
         const int64_t idx = base + k * 64;
-        if (idx < count) {
+        if (idx < live) {
             key[k] = keys_in[idx];
             val[k] = VALS ? vals_in[idx] : V(0);
         } else {
             key[k] = K(0);
             val[k] = V(0);
         }
+        in[k] = idx < live && !(DROP && key[k] == (K)kDroppedKey);
     }
     __syncthreads();
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 #pragma unroll
     for (int k = 0; k < kSortItems; ++k) {
-        const int64_t idx = base + k * 64;
         rank[k] = 0;
-        if (idx < count) {
+        if (in[k]) {
             const uint32_t d = digit_of(key[k], shift, mask);
             uint64_t peers = __ballot(1);
             for (int b = 0; b < bits; ++b) {
@@ -370,6 +385,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
         }
     }
     __syncthreads();
+    uint32_t block_total;  // keys of this tile taking part in the pass
     {
         // Start of digit d in this tile's digit-sorted order, then each
         // wavefront's offset within the digit; thread t owns the M
@@ -385,7 +401,6 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
                 tot += c[i][w];
             }
         }
-        uint32_t block_total;
         uint32_t run = block_exclusive_scan<kSortThreads>(tot, s_scan_wave, block_total);
 #pragma unroll
         for (int i = 0; i < M; ++i) {
@@ -402,8 +417,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kSortItems; ++k) {
-        const int64_t idx = base + k * 64;
-        if (idx < count) {
+        if (in[k]) {
             const uint32_t d = digit_of(key[k], shift, mask);
             const uint32_t pos = s_wcnt[wave][d] + rank[k];
             s_keys[pos] = key[k];
@@ -415,7 +429,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
 #pragma unroll
     for (int j = 0; j < kSortItems; ++j) {
         const int p = j * kSortThreads + threadIdx.x;
-        if (p < valid_count) {
+        if (p < (int)block_total) {
             const K kk = s_keys[p];
             const int64_t dst = (int64_t)s_gbase[digit_of(kk, shift, mask)] + p;
             keys_out[dst] = kk;  // plain stores: digit runs start mid-line and the L2 merges them
@@ -426,6 +440,19 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
                 record_extent<TAIL>((uint64_t)s_vals[p], groups, area);
                 tail.group_counts[dst] = groups;
                 area_sum += area;
+            }
+        }
+    }
+    if constexpr (VALS) {
+        if (cull.fill && cull.live) {
+            // This tile's share of the positions after the sorted keys.
+#pragma unroll
+            for (int j = 0; j < kSortItems; ++j) {
+                const int64_t q = tile_base + j * kSortThreads + threadIdx.x;
+                if (q >= live && q < count) {
+                    vals_out[q] = (V)cull.filler;
+                    if constexpr (TAIL != 0) tail.group_counts[q] = 0;
+                }
             }
         }
     }
@@ -487,9 +514,9 @@ __global__ __launch_bounds__(256) void transpose_offsets_kernel(const int32_t* _
 
 // Histogram and scan of one sort pass (digits of `bits` bits at `shift`;
 // every key's digit below `digits`, a multiple of 32 up to 1 << RB).
-template <class K, int RB>
+template <class K, int RB, bool DROP = false>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
-                hipStream_t s);
+                hipStream_t s, const int64_t* live = nullptr, int64_t* total = nullptr);
 
 // tail_kind (1 or 2, 64-bit values only): the last pass also writes the
 // order tail (record_extent<tail_kind>).
@@ -512,18 +539,22 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
         if constexpr (sizeof(V) == 8) {
             if (tail_here == 1)
                 hipLaunchKernelGGL((sort_scatter_kernel<K, V, true, 8, 1>), dim3((unsigned)tiles), dim3(kSortThreads),
-                                   0, s, kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, tail);
+                                   0, s, kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, tail,
+                                   Culled{});
             else if (tail_here == 2)
                 hipLaunchKernelGGL((sort_scatter_kernel<K, V, true, 8, 2>), dim3((unsigned)tiles), dim3(kSortThreads),
-                                   0, s, kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, tail);
+                                   0, s, kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, tail,
+                                   Culled{});
         }
         if (tail_here == 0 || sizeof(V) != 8) {
             if (values)
                 hipLaunchKernelGGL((sort_scatter_kernel<K, V, true>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
-                                   kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, OrderTail{});
+                                   kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, OrderTail{},
+                                   Culled{});
             else
                 hipLaunchKernelGGL((sort_scatter_kernel<K, V, false>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
-                                   kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, OrderTail{});
+                                   kin, vin, kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, OrderTail{},
+                                   Culled{});
         }
         K* tk = kin;
         kin = kout;
@@ -543,33 +574,80 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
     return launch_status("radix sort");
 }
 
+// The depth order of the rows that touch a tile group: 32-bit keys with
+// kDroppedKey for the others, 64-bit records, four 8-bit passes.  The first
+// pass leaves the dropped rows out and its digit scan counts the rest into
+// *live; the later passes sort [0, *live), and the last one writes `filler`
+// records (and, with a tail, zero group counts) to [*live, count).  The
+// result is in the first halves, as with run_sort.
+inline int run_order_sort(uint32_t* keys, uint64_t* values, int64_t count, void* scratch, int64_t* live,
+                          uint64_t filler, hipStream_t s, int tail_kind, OrderTail tail) {
+    SortScratch sc;
+    sort_scratch_bytes(count, &sc, scratch);
+    const int64_t tiles = (count + kSortTile - 1) / kSortTile;
+    uint32_t* kin = keys;
+    uint64_t* vin = values;
+    uint32_t* kout = keys + count;
+    uint64_t* vout = values + count;
+    const dim3 grid((unsigned)tiles), block(kSortThreads);
+    for (int shift = 0; shift < 32; shift += 8) {
+        const bool first = shift == 0, last = shift == 24;
+        const int status = first ? sort_counts<uint32_t, 8, true>(kin, count, shift, 255u, 256, sc, s, nullptr, live)
+                                 : sort_counts<uint32_t, 8, false>(kin, count, shift, 255u, 256, sc, s, live, nullptr);
+        if (status != GS3D_OK) return status;
+        if (first) {
+            hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 8, 0, true>), grid, block, 0, s, kin, vin,
+                               kout, vout, count, shift, 255u, 8, sc.offsets, tiles, 256, OrderTail{},
+                               Culled{nullptr, false, 0});
+        } else {
+            const Culled cull{live, last, filler};
+            if (last && tail_kind == 1)
+                hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 8, 1>), grid, block, 0, s, kin, vin,
+                                   kout, vout, count, shift, 255u, 8, sc.offsets, tiles, 256, tail, cull);
+            else if (last && tail_kind == 2)
+                hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 8, 2>), grid, block, 0, s, kin, vin,
+                                   kout, vout, count, shift, 255u, 8, sc.offsets, tiles, 256, tail, cull);
+            else
+                hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 8, 0>), grid, block, 0, s, kin, vin,
+                                   kout, vout, count, shift, 255u, 8, sc.offsets, tiles, 256, OrderTail{}, cull);
+        }
+        std::swap(kin, kout);
+        std::swap(vin, vout);
+    }
+    return launch_status("depth order");
+}
+
 // Histogram of TPB consecutive sort tiles per block: each digit's TPB counts
 // are consecutive in the [digit][tile] layout, so a block writes runs of TPB
 // words instead of one scattered word per digit.  One LDS histogram per tile
 // (pitch R + 1: the transposed read is conflict-free).
-template <class K, int RB, int TPB>
+// DROP and live as in sort_scatter_kernel (tiles at or beyond live count
+// nothing, and their columns are written as zeros).
+template <class K, int RB, int TPB, bool DROP = false>
 __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(const K* __restrict__ keys, int64_t count,
                                                                             int shift, uint32_t mask,
                                                                             uint32_t* __restrict__ counts,
-                                                                            int64_t tiles, int digits) {
+                                                                            int64_t tiles, int digits,
+                                                                            const int64_t* __restrict__ live_count) {
     constexpr int R = 1 << RB, P = R + 1;
     __shared__ uint32_t s_hist[TPB * P];
     for (int e = threadIdx.x; e < TPB * P; e += kSortThreads) s_hist[e] = 0;
     __syncthreads();
+    const int64_t live = live_count ? min(count, *live_count) : count;
     const int64_t t0 = (int64_t)blockIdx.x * TPB;
     for (int tt = 0; tt < TPB; ++tt) {
         const int64_t base = (t0 + tt) * kSortTile;
-        if (base >= count) break;
+        if (base >= live) break;
         K key[kSortItems];
 #pragma unroll
         for (int k = 0; k < kSortItems; ++k) {
             const int64_t idx = base + k * kSortThreads + threadIdx.x;
-            key[k] = idx < count ? keys[idx] : K(0);
+            key[k] = idx < live ? keys[idx] : K(0);
         }
 #pragma unroll
         for (int k = 0; k < kSortItems; ++k) {
             const int64_t idx = base + k * kSortThreads + threadIdx.x;
-            const bool valid = idx < count;
+            const bool valid = idx < live && !(DROP && key[k] == (K)kDroppedKey);
             const uint32_t d = digit_of(key[k], shift, mask);
             // A wavefront whose valid keys share one digit (high key bits:
             // exponents, view ids) adds them with one atomic instead of 64
@@ -591,16 +669,17 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
     }
 }
 
-template <class K, int RB>
+// total (optional) receives the number of keys counted.
+template <class K, int RB, bool DROP>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
-                hipStream_t s) {
+                hipStream_t s, const int64_t* live, int64_t* total) {
     // Tiles per histogram block: runs of 16 words (whole 64-byte sectors) for
     // 8-bit digits; 8 for 10-bit digits, whose LDS histograms are 4x larger.
     constexpr int TPB = RB > 8 ? 8 : GS3D_HIST_TILES8;
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
-    hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
-                       dim3(kSortThreads), 0, s, keys, count, shift, mask, sc.counts, tiles, digits);
-    const int status = run_scan<uint32_t, false>(sc.counts, tiles * digits, sc.scanned, nullptr, sc.scan_scratch, s);
+    hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB, DROP>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
+                       dim3(kSortThreads), 0, s, keys, count, shift, mask, sc.counts, tiles, digits, live);
+    const int status = run_scan<uint32_t, false>(sc.counts, tiles * digits, sc.scanned, total, sc.scan_scratch, s);
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL(transpose_offsets_kernel, dim3((unsigned)((tiles + 31) / 32), digits / 32), dim3(256), 0, s,
                        sc.scanned, tiles, digits, sc.offsets);
@@ -641,7 +720,7 @@ int run_sort_once(K* keys, int64_t count, int end_bit, void* scratch, int ranges
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL((sort_scatter_kernel<K, int32_t, false, RB>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
                        keys, (const int32_t*)nullptr, keys + count, (int32_t*)nullptr, count, 0, mask, end_bit,
-                       sc.offsets, tiles, digits, OrderTail{});
+                       sc.offsets, tiles, digits, OrderTail{}, Culled{});
     hipLaunchKernelGGL(digit_ranges_kernel, dim3((unsigned)((ranges_count + 255) / 256)), dim3(256), 0, s,
                        sc.offsets, count, digits, ranges_count, ranges);
     return launch_status("one-pass radix sort");
@@ -834,7 +913,8 @@ GS3D_DEV void record_extent(uint64_t record, int32_t& groups, int64_t& area) {
 }
 
 // Row order: depth-bit keys and records (coalesced reads of depth, centre
-// and radius).
+// and radius).  Outside AccuTile, rows whose footprint touches no tile get
+// kDroppedKey instead of their depth bits: the depth order leaves them out.
 //
 // AccuTile (ACCU): the row's footprint and strips are computed here, once, in
 // row order; on grids of at most 256 x 256 tiles the record's high half
@@ -847,7 +927,7 @@ __global__ void row_records_kernel(const float* __restrict__ depths, RowGeometry
                                    int32_t* __restrict__ tiles_out, float4* __restrict__ footprints) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
-    keys[i] = __float_as_uint(depths[i]);
+    uint32_t key = __float_as_uint(depths[i]);
     uint64_t rec = (uint64_t)(uint32_t)i;
     if constexpr (ACCU) {
         int groups = 0, tiles = 0;
@@ -866,31 +946,35 @@ __global__ void row_records_kernel(const float* __restrict__ depths, RowGeometry
         if constexpr (PACKED) rec |= (uint64_t)(((uint32_t)tiles << 12) | (uint32_t)groups) << 32;
         if (tiles_out) tiles_out[i] = tiles;
     } else {
-        if (PACKED || tiles_out) {
-            const TileRect r = row_rect(g, i, gx, gy);
-            if constexpr (PACKED) {
-                const uint32_t p = r.x1 > r.x0 ? (uint32_t)r.x0 | ((uint32_t)r.y0 << 8) |
-                                                     ((uint32_t)(r.x1 - 1) << 16) | ((uint32_t)(r.y1 - 1) << 24)
-                                               : kEmptyRect;
-                rec |= (uint64_t)p << 32;
-            }
-            if (tiles_out) tiles_out[i] = r.x1 > r.x0 ? (r.x1 - r.x0) * (r.y1 - r.y0) : 0;
+        const TileRect r = row_rect(g, i, gx, gy);
+        if constexpr (PACKED) {
+            const uint32_t p = r.x1 > r.x0 ? (uint32_t)r.x0 | ((uint32_t)r.y0 << 8) |
+                                                 ((uint32_t)(r.x1 - 1) << 16) | ((uint32_t)(r.y1 - 1) << 24)
+                                           : kEmptyRect;
+            rec |= (uint64_t)p << 32;
         }
+        if (tiles_out) tiles_out[i] = r.x1 > r.x0 ? (r.x1 - r.x0) * (r.y1 - r.y0) : 0;
+        if (!(r.x1 > r.x0)) key = kDroppedKey;
     }
+    keys[i] = key;
     records[i] = rec;
 }
 
 // Group count of every row in depth order; the block's tile pair count goes
 // to block_pairs[blockIdx.x].  ACCU: AccuTile strips of the row's footprint.
+// live (optional): ordered rows at or beyond *live are fillers with no groups.
 template <bool PACKED, bool ACCU>
 __global__ __launch_bounds__(kBinThreads) void order_counts_kernel(const uint64_t* __restrict__ records, int64_t rows,
                                                                    RowGeometry g, int gx, int gy,
                                                                    int32_t* __restrict__ group_counts,
-                                                                   int64_t* __restrict__ block_pairs) {
+                                                                   int64_t* __restrict__ block_pairs,
+                                                                   const int64_t* __restrict__ live) {
     __shared__ int64_t s_wave[kBinWaves];
     const int64_t i = (int64_t)blockIdx.x * kBinThreads + threadIdx.x;
     int64_t area = 0;
-    if (i < rows) {
+    if (live && i >= *live && i < rows) {
+        group_counts[i] = 0;
+    } else if (i < rows) {
         if constexpr (ACCU && PACKED) {
             const uint32_t hi = (uint32_t)(records[i] >> 32);
             area = hi >> 12;
@@ -1527,6 +1611,7 @@ struct OrderScratch {
     uint32_t* keys;       // 2*rows depth-bit keys
     int32_t* counts;      // rows group counts
     int64_t* pairs;       // per-block tile pair counts
+    int64_t* live;        // rows that the depth order keeps (outside AccuTile)
     void* sort;
     void* scan;
 };
@@ -1536,6 +1621,7 @@ inline size_t order_scratch_bytes(int64_t rows, OrderScratch* out, void* base) {
     const size_t a = align256((size_t)rows * 2 * sizeof(uint32_t));
     const size_t b = align256((size_t)rows * sizeof(int32_t));
     const size_t c = align256((size_t)blocks * sizeof(int64_t));
+    const size_t l = align256(sizeof(int64_t));
     const size_t e = align256(sort_scratch_bytes(rows, nullptr, nullptr));
     const size_t f = scan_partials_bytes(rows);
     if (out) {
@@ -1543,10 +1629,11 @@ inline size_t order_scratch_bytes(int64_t rows, OrderScratch* out, void* base) {
         out->keys = reinterpret_cast<uint32_t*>(p);
         out->counts = reinterpret_cast<int32_t*>(p + a);
         out->pairs = reinterpret_cast<int64_t*>(p + a + b);
-        out->sort = p + a + b + c;
-        out->scan = p + a + b + c + e;
+        out->live = reinterpret_cast<int64_t*>(p + a + b + c);
+        out->sort = p + a + b + c + l;
+        out->scan = p + a + b + c + l + e;
     }
-    return a + b + c + e + f;
+    return a + b + c + l + e + f;
 }
 
 // Scratch of gs3d_bin_rows.
@@ -1816,19 +1903,27 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     // order holds 2*rows records: [0, rows) sorted result, [rows, 2rows) ping-pong.  With packed
     // records the last pass also writes each row's group count at its sorted position and the
     // blocks' tile-pair sums; otherwise order_counts_kernel computes them from the geometry.
+    // Outside AccuTile the rows that touch no tile are left out of the sort; their places at
+    // the end hold filler records (row 0, no rectangle) with no groups.
     const int tail_kind = packed ? (accu ? 2 : 1) : 0;
-    int status = gs3d::run_sort<uint32_t, uint64_t>(sc.keys, a.order, rows, 32, sc.sort, s, tail_kind,
+    int status;
+    if (accu)
+        status = gs3d::run_sort<uint32_t, uint64_t>(sc.keys, a.order, rows, 32, sc.sort, s, tail_kind,
                                                     gs3d::OrderTail{sc.counts, sc.pairs});
+    else
+        status = gs3d::run_order_sort(sc.keys, a.order, rows, sc.sort, sc.live,
+                                      packed ? (uint64_t)gs3d::kEmptyRect << 32 : 0u, s, tail_kind,
+                                      gs3d::OrderTail{sc.counts, sc.pairs});
     if (status != GS3D_OK) return status;
     int64_t pair_blocks = (rows + gs3d::kSortTile - 1) / gs3d::kSortTile;
     if (!packed) {
         const dim3 cgrid(gs3d::blocks_for(rows, gs3d::kBinThreads)), cblock(gs3d::kBinThreads);
         if (accu)
             hipLaunchKernelGGL((gs3d::order_counts_kernel<false, true>), cgrid, cblock, 0, s, a.order, rows, geo, d.gx,
-                               d.gy, sc.counts, sc.pairs);
+                               d.gy, sc.counts, sc.pairs, (const int64_t*)nullptr);
         else
             hipLaunchKernelGGL((gs3d::order_counts_kernel<false, false>), cgrid, cblock, 0, s, a.order, rows, geo,
-                               d.gx, d.gy, sc.counts, sc.pairs);
+                               d.gx, d.gy, sc.counts, sc.pairs, (const int64_t*)sc.live);
         pair_blocks = cgrid.x;
     }
     hipLaunchKernelGGL(gs3d::sum_i64_kernel, dim3(1), dim3(1024), 0, s, sc.pairs, pair_blocks, a.totals + 1);

@@ -265,9 +265,12 @@ int gs3d_tile_ranges(const uint64_t* sorted_keys, int64_t count, int32_t* ranges
  *      (view*N + Gaussian) in the low 32 bits and, for tile grids of at most
  *      256 x 256 tiles, the row's tile rectangle in the high 32 bits
  *      (x0 | y0 << 8 | (x1-1) << 16 | (y1-1) << 24, 0x000000FF when culled;
- *      larger grids leave them zero); the inclusive scan of the number of
- *      8x8-tile groups each rectangle touches; two totals: group pairs
- *      (totals[0]) and tile pairs (totals[1], the reference's offsets[-1]).
+ *      larger grids leave them zero).  Outside GS3D_TILE_ACCUTILE the rows
+ *      that touch no tile are left out of the sort and the records end with
+ *      as many fillers (row 0, rectangle 0x000000FF), which touch no group;
+ *      then the inclusive scan of the number of 8x8-tile groups each record
+ *      touches; two totals: group pairs (totals[0]) and tile pairs
+ *      (totals[1], the reference's offsets[-1]).
  *   2. The caller reads the totals and allocates ids (tile pairs).
  *   3. gs3d_bin_rows: one (group, row) item per touched group, emitted in
  *      depth order and sorted stably by group; every group's list is cut into
