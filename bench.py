@@ -384,15 +384,21 @@ def describe(scene, workload):
             ", fwd+bwd of sum(image*W)")
 
 
-def run_workload(workload, n, device, steps, warmup, cpu, tile_mode="radius"):
+def run_workload(workload, n, device, steps, warmup, cpu, tile_mode="radius", min_timed_ms=0.0):
     """Timed steps (clean, then with stage events) and the workload's
-    accounting; returns (entry, scene, frame, inputs)."""
+    accounting; returns (entry, scene, frame, inputs).  With min_timed_ms
+    the step count grows (to at most 100) until the timed steps take about
+    that long: short steps are otherwise dominated by host jitter."""
     import torch
 
     log(f"[bench] {workload}: building inputs")
     inputs = make_inputs(workload, n, device)
     scene = inputs[0]
     forward, backward = step_fn(*inputs, tile_mode)
+    if min_timed_ms > 0:
+        probe = time_steps(forward, backward, 2, warmup)
+        steps = max(steps, min(100, math.ceil(min_timed_ms / max(probe["ms"], 1e-3))))
+        warmup = 1
     log(f"[bench] {workload}: {warmup} warm-up + {steps} timed steps")
     clean = time_steps(forward, backward, steps, warmup)
     staged = time_steps(forward, backward, steps, 1, stage_events=True)
@@ -404,6 +410,7 @@ def run_workload(workload, n, device, steps, warmup, cpu, tile_mode="radius"):
     b13 = sum(by[k] for k in hbm)
     entry = dict(
         config=describe(scene, workload),
+        steps=steps,
         ms=round(clean["ms"], 3), fwd_ms=round(clean["fwd_ms"], 3), bwd_ms=round(clean["bwd_ms"], 3),
         staged_ms=round(staged["ms"], 3),
         stages=stages,
@@ -463,7 +470,7 @@ def main():
         for wl in WORKLOADS:
             if wl == args.workload:
                 continue
-            entry, *_ = run_workload(wl, None, device, args.workload_steps, 2, cpu)
+            entry, *_ = run_workload(wl, None, device, args.workload_steps, 2, cpu, min_timed_ms=50.0)
             others[wl] = entry
             torch.cuda.empty_cache()
     # The roofline object is the projection forward kernel: HBM-bound, one
