@@ -456,9 +456,12 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 todo &= todo - 1;
                 return j;
             };
-            if constexpr (STATS) {
+            if constexpr (STATS || (CH > 16 && CH <= 36)) {
                 // Loads at use: the pipelined form's extra registers would
-                // cost this variant occupancy.
+                // cost occupancy -- the statistics variant's, and for 36
+                // channels a third wavefront per SIMD (148 VGPRs against 190
+                // with the next Gaussian's vector prefetched: 0.83 -> 0.72
+                // ms on the 32-feature workload).
                 while (todo) {
                     if (!alive()) {
                         live = false;
