@@ -59,20 +59,35 @@ GS3D_DEV T block_exclusive_scan(T v, T* s_wave, T& total) {
 // ---------------------------------------------------------------------------
 // Scan (reduce-then-scan over 4096-element tiles).
 // ---------------------------------------------------------------------------
+// One wavefront per 4096-element tile: all 64 loads of a lane in flight at
+// once, then a butterfly sum (no LDS, no block barrier).
+constexpr int kReduceWaves = 4;
 template <class In>
-__global__ __launch_bounds__(kScanThreads) void scan_reduce_kernel(const In* __restrict__ in, int64_t n,
-                                                                   int64_t* __restrict__ partials) {
-    __shared__ int64_t s_wave[kScanThreads / 64];
-    const int64_t base = (int64_t)blockIdx.x * kScanTile;
+__global__ __launch_bounds__(64 * kReduceWaves) void scan_reduce_kernel(const In* __restrict__ in, int64_t n,
+                                                                        int64_t tiles,
+                                                                        int64_t* __restrict__ partials) {
+    const int lane = lane_id();
+    const int64_t tile = (int64_t)blockIdx.x * kReduceWaves + (threadIdx.x >> 6);
+    if (tile >= tiles) return;
+    const int64_t base = tile * kScanTile;
+    constexpr int kPerLane = kScanTile / 64;
+    // Clamped addresses and a select keep every load unconditional (a
+    // guarded load is a branch that waits for its data).
+    In v[kPerLane];
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k) {
+        const int64_t idx = base + k * 64 + lane;
+        v[k] = in[min(idx, n - 1)];
+    }
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k)
+        if (base + k * 64 + lane >= n) v[k] = In(0);
     int64_t sum = 0;
 #pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
-        const int64_t idx = base + k * kScanThreads + threadIdx.x;
-        if (idx < n) sum += (int64_t)in[idx];
-    }
-    int64_t total;
-    block_exclusive_scan<kScanThreads>(sum, s_wave, total);
-    if (threadIdx.x == 0) partials[blockIdx.x] = total;
+    for (int k = 0; k < kPerLane; ++k) sum += (int64_t)v[k];
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) sum += __shfl_xor(sum, d, 64);
+    if (lane == 0) partials[tile] = sum;
 }
 
 // Per-tile scan with the tile's prefix.  Loads and stores are striped
@@ -92,16 +107,27 @@ __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const In* __res
     __shared__ int64_t s_wave[kScanThreads / 64];
     __shared__ int32_t s_tile[kScanTile + kScanTile / 16];
     const int64_t base = (int64_t)blockIdx.x * kScanTile;
+    // The tile's loads are issued first: they overlap the prefix's.
+    int32_t raw[kScanItems];
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) raw[k] = (int32_t)in[min(base + k * kScanThreads + threadIdx.x, n - 1)];
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k)
+        if (base + k * kScanThreads + threadIdx.x >= n) raw[k] = 0;
     int64_t before = 0;
-    for (int64_t j = threadIdx.x; j < (int64_t)blockIdx.x; j += kScanThreads) before += partials[j];
+    for (int64_t j0 = threadIdx.x; j0 < (int64_t)blockIdx.x; j0 += 4 * kScanThreads) {
+        int64_t p[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) p[u] = partials[min(j0 + u * kScanThreads, (int64_t)blockIdx.x - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (j0 + u * kScanThreads >= (int64_t)blockIdx.x) p[u] = 0;
+        before += (p[0] + p[1]) + (p[2] + p[3]);
+    }
     int64_t prefix;
     block_exclusive_scan<kScanThreads>(before, s_wave, prefix);
 #pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
-        const int e = k * kScanThreads + threadIdx.x;
-        const int64_t idx = base + e;
-        s_tile[scan_lds_index(e)] = idx < n ? (int32_t)in[idx] : 0;
-    }
+    for (int k = 0; k < kScanItems; ++k) s_tile[scan_lds_index(k * kScanThreads + threadIdx.x)] = raw[k];
     __syncthreads();
     int32_t vals[kScanItems];
     int64_t sum = 0;
@@ -139,7 +165,8 @@ int run_scan(const In* in, int64_t n, int32_t* out, int64_t* total, void* scratc
     const int64_t tiles = (n + kScanTile - 1) / kScanTile;
     if (tiles == 0) return GS3D_OK;  // callers handle empty inputs (total untouched)
     int64_t* partials = reinterpret_cast<int64_t*>(scratch);
-    hipLaunchKernelGGL((scan_reduce_kernel<In>), dim3((unsigned)tiles), dim3(kScanThreads), 0, stream, in, n, partials);
+    hipLaunchKernelGGL((scan_reduce_kernel<In>), dim3((unsigned)((tiles + kReduceWaves - 1) / kReduceWaves)),
+                       dim3(64 * kReduceWaves), 0, stream, in, n, tiles, partials);
     hipLaunchKernelGGL((scan_down_kernel<In, INCLUSIVE>), dim3((unsigned)tiles), dim3(kScanThreads), 0, stream, in, n,
                        partials, out, total);
     return launch_status("scan");
@@ -1365,11 +1392,16 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // All loads first, from clamped addresses (begin < end): a guarded
+        // load would be a branch that waits for its data.
+        uint64_t got[kChunkSteps];
+#pragma unroll
+        for (int k = 0; k < kChunkSteps; ++k) got[k] = items[min(begin + k * 64 + lane, end - 1)];
 #pragma unroll
         for (int k = 0; k < kChunkSteps; ++k) {
             const int64_t i = begin + k * 64 + lane;
             if (i < end) {
-                const uint32_t local = (uint32_t)(items[i] >> kGroupBits) & 0xFFFu;
+                const uint32_t local = (uint32_t)(got[k] >> kGroupBits) & 0xFFFu;
                 const int lx0 = local & 7, lx1 = ((local >> 3) & 7) + 1, ly0 = (local >> 6) & 7,
                           ly1 = ((local >> 9) & 7) + 1;
                 atomicAdd(&diff[ly0 * 9 + lx0], 1);
@@ -1409,19 +1441,21 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     uint64_t mask[kChunkSteps];
     int32_t id[kChunkSteps];
     uint64_t any = 0;
+    // All loads first, from clamped addresses (begin < end), then the lanes
+    // beyond the chunk's end are cleared.
+    uint64_t got[kChunkSteps];
 #pragma unroll
     for (int k = 0; k < kChunkSteps; ++k) {
-        const int64_t i = begin + k * 64 + lane;
-        mask[k] = 0;
-        id[k] = 0;
-        if (i < end) {
-            const uint64_t item = items[i];
-            if constexpr (MASKS)
-                mask[k] = masks[i];
-            else
-                mask[k] = group_tile_mask((uint32_t)(item >> kGroupBits) & 0xFFFu);
-            id[k] = (int32_t)(item >> 32);
-        }
+        const int64_t i = min(begin + k * 64 + lane, end - 1);
+        got[k] = items[i];
+        if constexpr (MASKS) mask[k] = masks[i];
+    }
+#pragma unroll
+    for (int k = 0; k < kChunkSteps; ++k) {
+        const bool in = begin + k * 64 + lane < end;
+        if constexpr (!MASKS) mask[k] = group_tile_mask((uint32_t)(got[k] >> kGroupBits) & 0xFFFu);
+        if (!in) mask[k] = 0;
+        id[k] = in ? (int32_t)(got[k] >> 32) : 0;
         any |= mask[k];
     }
     uint32_t init = 0;

@@ -880,13 +880,17 @@ __global__ __launch_bounds__(kShRowBlock) void sh_rows_bwd_kernel(gs3d_project_b
     const int rows_here = (int)max((int64_t)0, min((int64_t)64, n - g0));
     float* stage = s_stage[staged ? wave : 0];
     float* const row_lds = stage + lane * PITCH;
+    // Loads use clamped indices (row n - 1, the group's last view) and their
+    // values are selected afterwards: a guarded load is a branch that waits
+    // for its data, so every load of a step is in flight at once.
+    const int64_t ic = valid ? i : n - 1;
     float mean[3] = {0.0f, 0.0f, 0.0f}, gm_old[3] = {0.0f, 0.0f, 0.0f}, gm[3] = {0.0f, 0.0f, 0.0f};
-    if (DEG > 0 && valid) {
+    if (DEG > 0) {
 #pragma unroll
-        for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
+        for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * ic + k];
         if (a.grad_means) {
 #pragma unroll
-            for (int k = 0; k < 3; ++k) gm_old[k] = a.grad_means[3 * i + k];
+            for (int k = 0; k < 3; ++k) gm_old[k] = a.grad_means[3 * ic + k];
         }
     }
     float cf[E];
@@ -918,15 +922,27 @@ __global__ __launch_bounds__(kShRowBlock) void sh_rows_bwd_kernel(gs3d_project_b
         // The group's directions and clamp-masked colour gradients.
         float unit[U][3], length[U], cg[U][3];
         bool vis[U];
+        int radius_in[U];
+        float up_in[U][3], centre_in[U][3];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int v = v0 + u;
+            const int vc = min(v0 + u, views - 1);
+            const int64_t row = (int64_t)vc * n + ic;
+            radius_in[u] = a.radii[row];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) up_in[u][c] = a.grad_colors[row * a.grad_colors_stride + c];
+            if (DEG > 0) {
+#pragma unroll
+                for (int k = 0; k < 3; ++k) centre_in[u][k] = a.camera_centers[3 * vc + k];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
             const bool use = valid && u < nv;
-            const int64_t row = (int64_t)v * n + i;
-            const int radius = use ? a.radii[row] : 0;
+            const int radius = use ? radius_in[u] : 0;
             float up[3];
 #pragma unroll
-            for (int c = 0; c < 3; ++c) up[c] = use ? a.grad_colors[row * a.grad_colors_stride + c] : 0.0f;
+            for (int c = 0; c < 3; ++c) up[c] = use ? up_in[u][c] : 0.0f;
             vis[u] = radius > 0;
             length[u] = 1.0f;
 #pragma unroll
@@ -934,7 +950,7 @@ __global__ __launch_bounds__(kShRowBlock) void sh_rows_bwd_kernel(gs3d_project_b
             if (DEG > 0 && use) {
                 float dir[3];
 #pragma unroll
-                for (int k = 0; k < 3; ++k) dir[k] = mean[k] - a.camera_centers[3 * v + k];
+                for (int k = 0; k < 3; ++k) dir[k] = mean[k] - centre_in[u][k];
                 length[u] = length3(dir);
                 const float l = sel_max(length[u], 1.0e-12f);
 #pragma unroll

@@ -217,14 +217,10 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32
     const int view = t.view;
     const int64_t row = (int64_t)view * a.n + g;
     const float2 xy = reinterpret_cast<const float2*>(a.centers)[row];
-    s_xy[slot] = xy;
     const float4 con = reinterpret_cast<const float4*>(a.conics)[row];
-    s_con[slot] = con;
-    const float cut = power_cutoff(con.w);
-    s_cut[slot] = cut;
-    s_mask[slot] = strip_mask<PIX>(xy, con, cut, t.x0, t.y0);
-    // The channel vector [features | extra | 1]: every load is issued before
-    // the LDS writes (compile-time channel slots, predicated on the counts).
+    // The channel vector [features | extra | 1]: its loads are issued with
+    // the centre's and conic's, before the cutoff and strip mask wait for
+    // those (compile-time channel slots, predicated on the counts).
     const int F = a.feat_channels, E = a.extra_channels;
     const float* f = a.features + view * a.feat_view_stride + (int64_t)g * a.feat_stride;
     const float* e = E > 0 ? a.extra + view * a.extra_view_stride + (int64_t)g * a.extra_stride : nullptr;
@@ -241,6 +237,11 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32
             x = 1.0f;
         v[c] = x;
     }
+    s_xy[slot] = xy;
+    s_con[slot] = con;
+    const float cut = power_cutoff(con.w);
+    s_cut[slot] = cut;
+    s_mask[slot] = strip_mask<PIX>(xy, con, cut, t.x0, t.y0);
     float* dst = s_feat + slot * CH;
 #pragma unroll
     for (int c = 0; c < CH; ++c) dst[c] = v[c];
@@ -614,6 +615,12 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     if (threadIdx.x == 0) s_max_last = 0;
     const float* bg = a.background ? a.background + t.view * a.background_view_stride : nullptr;
     int my_max = 0;
+    // Per-pixel inputs: every load first, from the pixel clamped into the
+    // image (the branches below depend only on the channel, so all lanes
+    // load together), then the pixels outside the image are cleared.  A load
+    // under a per-lane condition would be a branch that waits for its data.
+    const int F = a.feat_channels, E = a.extra_channels;
+    int64_t pix[PIX];
 #pragma unroll
     for (int k = 0; k < PIX; ++k) {
         int lx, ly;
@@ -622,39 +629,48 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
         fx[k] = (float)x;
         fy[k] = (float)y;
         inside[k] = x < a.width && y < a.height;
-        T[k] = bg_t[k] = last_alpha[k] = S[k] = last_e[k] = 0.0f;
-        last_contributor[k] = 0;
+        pix[k] = ((int64_t)t.view * a.height + min(y, a.height - 1)) * a.width + min(x, a.width - 1);
+        T[k] = a.final_t[pix[k]];
+        last_contributor[k] = a.contributors[pix[k]];
 #pragma unroll
-        for (int c = 0; c < CH; ++c) grad[k][c] = 0.0f;
-        if (inside[k]) {
-            const int64_t pix = ((int64_t)t.view * a.height + y) * a.width + x;
-            T[k] = a.final_t[pix];
-            float bg_grad = 0.0f;
-            last_contributor[k] = a.contributors[pix];
-            const int F = a.feat_channels, E = a.extra_channels;
-#pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const int gc = c0 + c;
-                if (gc >= D) continue;
-                float u = 0.0f;
-                if (gc < F) {
-                    if (b.upstream) u = b.upstream[pix * b.upstream_stride + gc];
-                } else if (gc < F + E) {
-                    if (b.upstream_extra) u = b.upstream_extra[pix * b.upstream_extra_stride + (gc - F)];
-                } else if (b.upstream_alpha) {
-                    u = b.upstream_alpha[pix * b.upstream_alpha_stride];
-                }
-                grad[k][c] = u;
-                bg_grad += ((bg && gc < F) ? bg[gc] : 0.0f) * u;
-            }
-            if (GEOM) {
-                // Background channels beyond the window (geometry launch only).
-                if (bg && b.upstream)
-                    for (int gc = CH; gc < F; ++gc) bg_grad += bg[gc] * b.upstream[pix * b.upstream_stride + gc];
-                bg_t[k] = -T[k] * bg_grad;
-            }
-            my_max = max(my_max, last_contributor[k]);
+        for (int c = 0; c < CH; ++c) {
+            // The channel's source (wave-uniform selects, no branch); channels
+            // without one read final_t and take 0.
+            const int gc = c0 + c;
+            const float* src = gc < F ? b.upstream : gc < F + E ? b.upstream_extra : b.upstream_alpha;
+            const int64_t stride = gc < F ? b.upstream_stride
+                                          : gc < F + E ? b.upstream_extra_stride : b.upstream_alpha_stride;
+            const int off = gc < F ? gc : gc < F + E ? gc - F : 0;
+            const bool has = gc < D && src != nullptr;
+            const float u = has ? src[pix[k] * stride + off] : a.final_t[pix[k]];
+            grad[k][c] = has ? u : 0.0f;
         }
+    }
+#pragma unroll
+    for (int k = 0; k < PIX; ++k) {
+        bg_t[k] = last_alpha[k] = S[k] = last_e[k] = 0.0f;
+        if (!inside[k]) {
+            T[k] = 0.0f;
+            last_contributor[k] = 0;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) grad[k][c] = 0.0f;
+            continue;
+        }
+        if (GEOM) {
+            float bg_grad = 0.0f;
+            if (bg) {
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    const int gc = c0 + c;
+                    bg_grad += (gc < D && gc < F ? bg[gc] : 0.0f) * grad[k][c];
+                }
+                // Background channels beyond the window.
+                if (b.upstream)
+                    for (int gc = CH; gc < F; ++gc) bg_grad += bg[gc] * b.upstream[pix[k] * b.upstream_stride + gc];
+            }
+            bg_t[k] = -T[k] * bg_grad;
+        }
+        my_max = max(my_max, last_contributor[k]);
     }
     __syncthreads();
     if (my_max > 0) atomicMax(&s_max_last, my_max);
