@@ -590,32 +590,38 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(4)))
     for (int64_t base = (int64_t)blockIdx.x * kProjBlock; base < n; base += (int64_t)gridDim.x * kProjBlock) {
         const int64_t i = base + threadIdx.x;
         const bool valid = i < n;
-        float mean[3] = {0, 0, 0}, q[4] = {1, 0, 0, 0}, s[3] = {1, 1, 1}, qnorm = 1.0f;
-        if (valid) {
+        // Lanes past the last Gaussian read row n - 1 and write nothing: no
+        // load waits behind a per-lane branch (each view's radius and
+        // gradients are loaded together).
+        const int64_t ic = valid ? i : (int64_t)n - 1;
+        float mean[3], q[4], s[3], qnorm = 1.0f;
 #pragma unroll
-            for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
-            const float4 qq = reinterpret_cast<const float4*>(a.quats)[i];
-            q[0] = qq.x;
-            q[1] = qq.y;
-            q[2] = qq.z;
-            q[3] = qq.w;
-            if (a.normalize_quats) qnorm = normalize_quat(q);
+        for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * ic + k];
+        const float4 qq = reinterpret_cast<const float4*>(a.quats)[ic];
+        q[0] = qq.x;
+        q[1] = qq.y;
+        q[2] = qq.z;
+        q[3] = qq.w;
+        if (a.normalize_quats) qnorm = normalize_quat(q);
 #pragma unroll
-            for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
-        }
+        for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * ic + k];
         float gm[3] = {0, 0, 0}, gq[4] = {0, 0, 0, 0}, gs[3] = {0, 0, 0}, go = 0.0f;
         M3 gsigma = zero3();
         for (int v = 0; v < views; ++v) {
-            const int64_t row = (int64_t)v * n + i;
-            const bool vis = valid && a.radii[row] > 0;
+            const int64_t row = (int64_t)v * n + ic;
+            const float* gcp = a.grad_centers + row * a.grad_centers_stride;
+            const float* gkp = a.grad_conics + row * a.grad_conics_stride;
+            const int radius = a.radii[row];
+            const float gc[2] = {gcp[0], gcp[1]};
+            const float gk[4] = {gkp[0], gkp[1], gkp[2], gkp[3]};
+            // Keeps the gradient loads beside the radius's instead of inside
+            // the branch below.
+            asm volatile("" ::"v"(gc[0]), "v"(gc[1]), "v"(gk[0]), "v"(gk[1]), "v"(gk[2]), "v"(gk[3]));
+            const bool vis = valid && radius > 0;
             VJP g;
             float2 screen = make_float2(0.0f, 0.0f);
             if (vis) {
-                const float* gcp = a.grad_centers + row * a.grad_centers_stride;
-                const float* gkp = a.grad_conics + row * a.grad_conics_stride;
-                const float gc[2] = {gcp[0], gcp[1]};
                 screen = make_float2(gc[0], gc[1]);
-                const float gk[4] = {gkp[0], gkp[1], gkp[2], gkp[3]};
                 projection_vjp(mean, q, s, a.view + 16 * v, a.projection + 16 * v, a.width, a.height,
                                a.intrinsics[9 * v], a.intrinsics[9 * v + 4], gc, gk, g);
 #pragma unroll
@@ -755,22 +761,23 @@ __global__ __launch_bounds__(kShRowBlock) __attribute__((amdgpu_waves_per_eu(6))
     const bool valid = i < n;
     const int views = a.views;
     const int64_t rf = (int64_t)a.sh_rows * 3;
+    // Lanes past the last Gaussian load row n - 1 and store nothing: no load
+    // sits behind a per-lane branch, so each step's loads are in flight
+    // together.
+    const int64_t ic = valid ? i : n - 1;
     float mean[3] = {0.0f, 0.0f, 0.0f};
-    if (DEG > 0 && valid) {
+    if (DEG > 0) {
 #pragma unroll
-        for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * i + k];
+        for (int k = 0; k < 3; ++k) mean[k] = a.means[3 * ic + k];
     }
     int pre_radius[kShPrefetch];
 #pragma unroll
-    for (int p = 0; p < kShPrefetch; ++p) pre_radius[p] = (valid && p < views) ? a.radii[(int64_t)p * n + i] : 0;
+    for (int p = 0; p < kShPrefetch; ++p) pre_radius[p] = p < views ? a.radii[(int64_t)p * n + ic] : 0;
     float cf[3 * KC];
     for (int v = 0; v < views; ++v) {
         if (v == 0 || a.sh_view_stride != 0) {
-            const float* src = a.sh + v * a.sh_view_stride + i * rf;
-            if (!valid) {
-#pragma unroll
-                for (int e = 0; e < 3 * KC; ++e) cf[e] = 0.0f;
-            } else if constexpr (VEC && (3 * KC) % 4 == 0) {
+            const float* src = a.sh + v * a.sh_view_stride + ic * rf;
+            if constexpr (VEC && (3 * KC) % 4 == 0) {
 #pragma unroll
                 for (int e = 0; e < 3 * KC; e += 4) {
                     const float4 q = reinterpret_cast<const float4*>(src)[e >> 2];
@@ -789,7 +796,7 @@ __global__ __launch_bounds__(kShRowBlock) __attribute__((amdgpu_waves_per_eu(6))
 #pragma unroll
         for (int p = 0; p < kShPrefetch; ++p)
             if (v == p) radius = pre_radius[p];
-        if (v >= kShPrefetch && valid) radius = a.radii[row];
+        if (v >= kShPrefetch) radius = a.radii[(int64_t)v * n + ic];
         float dir[3] = {0.0f, 0.0f, 0.0f};
         if (DEG > 0) {
 #pragma unroll
