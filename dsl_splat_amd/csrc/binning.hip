@@ -378,6 +378,15 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     V val[kSortItems];
     uint32_t rank[kSortItems];
     bool in[kSortItems];  // the key takes part in this pass
+    // This tile's global digit offsets (thread t owns the M consecutive
+    // digits from M t), loaded now so that they arrive during the ranking.
+    constexpr int M = R / kSortThreads;
+    int32_t digit_offset[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const int d = threadIdx.x * M + i;
+        digit_offset[i] = offsets[tile * digits + min(d, digits - 1)];
+    }
     const int64_t base = tile_base + wave * (kSortTile / 4) + lane;
 #pragma unroll
     for (int k = 0; k < kSortItems; ++k) {
@@ -415,9 +424,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     uint32_t block_total;  // keys of this tile taking part in the pass
     {
         // Start of digit d in this tile's digit-sorted order, then each
-        // wavefront's offset within the digit; thread t owns the M
-        // consecutive digits from M t.
-        constexpr int M = R / kSortThreads;
+        // wavefront's offset within the digit.
         uint32_t c[M][kSortThreads / 64];
         uint32_t tot = 0;
 #pragma unroll
@@ -433,7 +440,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
         for (int i = 0; i < M; ++i) {
             const int d = threadIdx.x * M + i;
             // Digits at or beyond `digits` (the offsets' row length) hold no key.
-            s_gbase[d] = d < digits ? offsets[tile * digits + d] - (int32_t)run : 0;
+            s_gbase[d] = d < digits ? digit_offset[i] - (int32_t)run : 0;
 #pragma unroll
             for (int w = 0; w < kSortThreads / 64; ++w) {
                 s_wcnt[w][d] = run;
