@@ -877,11 +877,13 @@ struct RowGeometry {
 
 GS3D_DEV TileRect row_rect(const RowGeometry& g, int64_t row, int gx, int gy) {
     TileRect r{0, 0, 0, 0};
+    // Centre and conic are loaded with the radius, not after it.
     const int radius = g.radii[row];
+    const float2 c = reinterpret_cast<const float2*>(g.centers)[row];
+    const float4 k = g.mode == GS3D_TILE_RADIUS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                                                : reinterpret_cast<const float4*>(g.conics)[row];
+    asm volatile("" ::"v"(c.x), "v"(c.y), "v"(k.x), "v"(k.y), "v"(k.z), "v"(k.w));
     if (radius > 0) {
-        const float2 c = reinterpret_cast<const float2*>(g.centers)[row];
-        const float4 k = g.mode == GS3D_TILE_RADIUS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                                                    : reinterpret_cast<const float4*>(g.conics)[row];
         const int4 b = mode_rect(c, k, radius, gx, gy, g.mode);
         if (b.z > b.x && b.w > b.y) r = TileRect{b.x, b.y, b.z, b.w};
     }
@@ -1073,12 +1075,15 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
     const int64_t r0 = (int64_t)blockIdx.x * kBinThreads;
     const int cnt = (int)min((int64_t)kBinThreads, rows - r0);
     const int t = threadIdx.x;
+    const int64_t S = r0 > 0 ? offsets[r0 - 1] : 0;  // issued with the rows' loads
     if (t < cnt) {
         const int64_t i = r0 + t;
         const uint64_t rec = records[i];
+        const int32_t end = offsets[i];
+        asm volatile("" ::"v"(end));  // loaded beside the record, not after its decoding
         const int32_t row = (int32_t)(uint32_t)rec;
         const TileRect r = record_rect<PACKED>(rec, geo, d.gx, d.gy);
-        s_end[t] = offsets[i];
+        s_end[t] = end;
         s_x0[t] = r.x0;
         s_y0[t] = r.y0;
         s_x1[t] = r.x1;
@@ -1089,7 +1094,6 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
         s_id[t] = (uint32_t)(row - view * n);
     }
     __syncthreads();
-    const int64_t S = r0 > 0 ? offsets[r0 - 1] : 0;
     const int64_t E = min((int64_t)s_end[cnt - 1], limit);
     for (int64_t p = S + t; p < E; p += kBinThreads) {
         // First j with s_end[j] > p (p < s_end[cnt - 1], offsets are int32):
