@@ -669,15 +669,21 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
     __syncthreads();
     const int64_t live = live_count ? min(count, *live_count) : count;
     const int64_t t0 = (int64_t)blockIdx.x * TPB;
+    // The next tile's keys are loaded while this tile's are counted
+    // (clamped addresses: no load waits behind a per-lane branch).
+    auto load_tile = [&](int64_t base, K (&key)[kSortItems]) {
+#pragma unroll
+        for (int k = 0; k < kSortItems; ++k) key[k] = keys[min(base + k * kSortThreads + threadIdx.x, live - 1)];
+    };
+    K next[kSortItems];
+    if (t0 * kSortTile < live) load_tile(t0 * kSortTile, next);
     for (int tt = 0; tt < TPB; ++tt) {
         const int64_t base = (t0 + tt) * kSortTile;
         if (base >= live) break;
         K key[kSortItems];
 #pragma unroll
-        for (int k = 0; k < kSortItems; ++k) {
-            const int64_t idx = base + k * kSortThreads + threadIdx.x;
-            key[k] = idx < live ? keys[idx] : K(0);
-        }
+        for (int k = 0; k < kSortItems; ++k) key[k] = next[k];
+        if (tt + 1 < TPB && base + kSortTile < live) load_tile(base + kSortTile, next);
 #pragma unroll
         for (int k = 0; k < kSortItems; ++k) {
             const int64_t idx = base + k * kSortThreads + threadIdx.x;
