@@ -378,18 +378,24 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 val[k][r] = (r < st.requests && !done[k]) ? pv[r * plane] : 0.0f;
         }
     }
+    // Each thread stages at most one Gaussian per batch (B <= NT); its index
+    // for the next batch is loaded while the current batch blends (clamped
+    // into the list, so the load is unconditional).
+    static_assert(B <= NT, "one staged Gaussian per thread and batch");
+    int32_t next_id = t.last > t.first ? a.ids[min(t.first + (int)threadIdx.x, t.last - 1)] : 0;
     for (int begin = t.first; begin < t.last; begin += B) {
         bool active = false;
 #pragma unroll
         for (int k = 0; k < PIX; ++k) active = active || !done[k];
         if (__syncthreads_count(active) == 0) break;
-        for (int e = threadIdx.x; e < B; e += NT) {
-            const int idx = begin + e;
-            if (idx < t.last) {
-                const int32_t g = a.ids[idx];
+        if (threadIdx.x < B) {
+            const int e = threadIdx.x;
+            const int32_t g = next_id;
+            if (begin + e < t.last) {
                 stage_gaussian<CH, PIX>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
                 if constexpr (STATS) s_id[e] = g;
             }
+            if (begin + B < t.last) next_id = a.ids[min(begin + B + e, t.last - 1)];
         }
         __syncthreads();
         const int cnt = min(B, t.last - begin);
@@ -716,15 +722,21 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     int wave_last = my_max;
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) wave_last = max(wave_last, __shfl_xor(wave_last, d, 64));
+    // As in the forward: one staged Gaussian per thread and batch, its index
+    // for the next batch loaded while the current one is traversed.
+    static_assert(B <= NT, "one staged Gaussian per thread and batch");
+    int32_t next_id = max_last > 0 ? a.ids[t.first + max(max_last - 1 - (int)threadIdx.x, 0)] : 0;
     for (int top = max_last; top > 0; top -= B) {
         __syncthreads();
-        for (int e = threadIdx.x; e < B; e += NT) {
+        if (threadIdx.x < B) {
+            const int e = threadIdx.x;
             const int p = top - 1 - e;
+            const int32_t g = next_id;
             if (p >= 0) {
-                const int32_t g = a.ids[t.first + p];
                 s_id[e] = g;
                 stage_gaussian<CH, PIX>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
             }
+            if (top > B) next_id = a.ids[t.first + max(p - B, 0)];
         }
         __syncthreads();
         const int cnt = min(B, top);
