@@ -1414,17 +1414,23 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
         uint64_t got[kChunkSteps];
 #pragma unroll
         for (int k = 0; k < kChunkSteps; ++k) got[k] = items[min(begin + k * 64 + lane, end - 1)];
+        // Corners in row or column 8 lie outside the summed 8x8 part and are
+        // not added; items starting at the group's first tile (common: the
+        // rectangles clipped by the group's edges) add their corner with one
+        // atomic per step instead of as many serialised ones on one word.
 #pragma unroll
         for (int k = 0; k < kChunkSteps; ++k) {
-            const int64_t i = begin + k * 64 + lane;
-            if (i < end) {
-                const uint32_t local = (uint32_t)(got[k] >> kGroupBits) & 0xFFFu;
-                const int lx0 = local & 7, lx1 = ((local >> 3) & 7) + 1, ly0 = (local >> 6) & 7,
-                          ly1 = ((local >> 9) & 7) + 1;
-                atomicAdd(&diff[ly0 * 9 + lx0], 1);
-                atomicAdd(&diff[ly0 * 9 + lx1], -1);
-                atomicAdd(&diff[ly1 * 9 + lx0], -1);
-                atomicAdd(&diff[ly1 * 9 + lx1], 1);
+            const bool in = begin + k * 64 + lane < end;
+            const uint32_t local = (uint32_t)(got[k] >> kGroupBits) & 0xFFFu;
+            const int lx0 = local & 7, lx1 = ((local >> 3) & 7) + 1, ly0 = (local >> 6) & 7,
+                      ly1 = ((local >> 9) & 7) + 1;
+            const uint64_t origin = __ballot(in && (lx0 | ly0) == 0);
+            if (origin && lane == (int)__builtin_ctzll(origin)) atomicAdd(&diff[0], (int)__popcll(origin));
+            if (in) {
+                if ((lx0 | ly0) != 0) atomicAdd(&diff[ly0 * 9 + lx0], 1);
+                if (lx1 < 8) atomicAdd(&diff[ly0 * 9 + lx1], -1);
+                if (ly1 < 8) atomicAdd(&diff[ly1 * 9 + lx0], -1);
+                if (lx1 < 8 && ly1 < 8) atomicAdd(&diff[ly1 * 9 + lx1], 1);
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
