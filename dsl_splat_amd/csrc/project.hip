@@ -75,7 +75,7 @@ GS3D_DEV M3 glm_rotation(const float* q) {
 struct CovParts {
     float t[3];
     float limx, limy;
-    M3 R, M, Sigma, J, W, Tm, X;
+    M3 Sigma, J, W, Tm, X;
 };
 
 // a / b, correctly rounded; with APPROX a times the hardware reciprocal of b
@@ -88,18 +88,10 @@ GS3D_DEV float quotient(float a, float b) {
         return a / b;
 }
 
-// gs3d/projection.py:37-86.  APPROX (the VJP's recomputation): the divisions
-// of t, J and nothing else are approximate -- the clamp limits stay exact,
-// and the VJP takes its clamp decisions from exact quotients of its own.
-template <bool APPROX = false>
-GS3D_DEV void screen_covariance(const float* pos, const float* q, const float* s, const float* V, int width,
-                                int height, float fx, float fy, CovParts& st, float* cov) {
-    st.limx = 1.3f * (float)width / (2.0f * fx);
-    st.limy = 1.3f * (float)height / (2.0f * fy);
-    st.t[0] = sel_clamp(quotient<APPROX>(pos[0], pos[2]), -st.limx, st.limx) * pos[2];
-    st.t[1] = sel_clamp(quotient<APPROX>(pos[1], pos[2]), -st.limy, st.limy) * pos[2];
-    st.t[2] = pos[2];
-    st.R = glm_rotation(q);
+// 3D covariance Sigma = M^T M with M = S R(q) (gs3d/projection.py:37-86):
+// the same for every view, so the kernels form it once per Gaussian.
+GS3D_DEV M3 covariance_3d(const float* q, const float* s) {
+    const M3 R = glm_rotation(q);
     M3 S;
 #pragma unroll
     for (int i = 0; i < 3; ++i)
@@ -108,8 +100,23 @@ GS3D_DEV void screen_covariance(const float* pos, const float* q, const float* s
     S.m[0][0] = s[0];
     S.m[1][1] = s[1];
     S.m[2][2] = s[2];
-    st.M = ref_matmul(S, st.R);
-    st.Sigma = ref_matmul(transpose3(st.M), st.M);
+    const M3 M = ref_matmul(S, R);
+    return ref_matmul(transpose3(M), M);
+}
+
+// gs3d/projection.py:37-86 for one view, from the Gaussian's Sigma.  APPROX
+// (the VJP's recomputation): the divisions of t, J and nothing else are
+// approximate -- the clamp limits stay exact, and the VJP takes its clamp
+// decisions from exact quotients of its own.
+template <bool APPROX = false>
+GS3D_DEV void screen_covariance(const float* pos, const M3& Sigma, const float* V, int width, int height, float fx,
+                                float fy, CovParts& st, float* cov) {
+    st.limx = 1.3f * (float)width / (2.0f * fx);
+    st.limy = 1.3f * (float)height / (2.0f * fy);
+    st.t[0] = sel_clamp(quotient<APPROX>(pos[0], pos[2]), -st.limx, st.limx) * pos[2];
+    st.t[1] = sel_clamp(quotient<APPROX>(pos[1], pos[2]), -st.limy, st.limy) * pos[2];
+    st.t[2] = pos[2];
+    st.Sigma = Sigma;
     const float* t = st.t;
     st.J.m[0][0] = quotient<APPROX>(fx, t[2]);
     st.J.m[0][1] = 0.0f;
@@ -152,7 +159,7 @@ struct Footprint {
 };
 
 // gs3d/projection.py:113-162 for one (Gaussian, view); false when culled.
-GS3D_DEV bool project_one(const float* mean, const float* q, const float* s, const float* V, const float* P,
+GS3D_DEV bool project_one(const float* mean, const M3& Sigma, const float* V, const float* P,
                           float fx, float fy, int width, int height, float near_plane, float far_plane,
                           float radius_clip, Footprint& f) {
     float t4[3];
@@ -161,7 +168,7 @@ GS3D_DEV bool project_one(const float* mean, const float* q, const float* s, con
     if (t4[2] <= near_plane || t4[2] >= far_plane) return false;
     CovParts st;
     float cov[3];
-    screen_covariance(t4, q, s, V, width, height, fx, fy, st, cov);
+    screen_covariance(t4, Sigma, V, width, height, fx, fy, st, cov);
     const float a = cov[0], b = cov[1], c = cov[2];
     const float det = a * c - b * b;
     if (det == 0.0f) return false;
@@ -372,9 +379,10 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(8)))
 #pragma unroll
     for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * i + k];
     const float opac = a.opacities[i];
+    const M3 Sigma = covariance_3d(q, s);
     auto one = [&](int v, const float* V, const float* P, float fx, float fy) {
         Footprint f;
-        const bool vis = project_one(mean, q, s, V, P, fx, fy, a.width, a.height, a.near_plane, a.far_plane,
+        const bool vis = project_one(mean, Sigma, V, P, fx, fy, a.width, a.height, a.near_plane, a.far_plane,
                                      a.radius_clip, f);
         const int64_t row = (int64_t)v * n + i;
         if (!vis) f = Footprint{{0.0f, 0.0f}, {0.0f, 0.0f, 0.0f}, 0, 0, 0.0f};
@@ -446,7 +454,7 @@ GS3D_DEV M3 zero3() {
     return z;
 }
 
-GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, const float* V, const float* P,
+GS3D_DEV void projection_vjp(const float* mean, const M3& Sigma, const float* V, const float* P,
                              int width, int height, float fx, float fy, const float* gc, const float* gk, VJP& g) {
     // Gradients are compared within a tolerance: products and sums here may
     // fuse (the recomputed forward quantities come from the shared helpers,
@@ -459,7 +467,7 @@ GS3D_DEV void projection_vjp(const float* mean, const float* q, const float* s, 
     // clamp decisions below keep exact quotients, as in the forward.
     CovParts st;
     float cov[3];
-    screen_covariance<true>(pos, q, s, V, width, height, fx, fy, st, cov);
+    screen_covariance<true>(pos, Sigma, V, width, height, fx, fy, st, cov);
     g.opacity = gk[3];
     // splatting/geometry.py:61-71.
     const float a = cov[0], b = cov[1], c = cov[2];
@@ -605,6 +613,7 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(4)))
         if (a.normalize_quats) qnorm = normalize_quat(q);
 #pragma unroll
         for (int k = 0; k < 3; ++k) s[k] = a.scales[3 * ic + k];
+        const M3 Sigma = covariance_3d(q, s);
         float gm[3] = {0, 0, 0}, gq[4] = {0, 0, 0, 0}, gs[3] = {0, 0, 0}, go = 0.0f;
         M3 gsigma = zero3();
         for (int v = 0; v < views; ++v) {
@@ -622,7 +631,7 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(4)))
             float2 screen = make_float2(0.0f, 0.0f);
             if (vis) {
                 screen = make_float2(gc[0], gc[1]);
-                projection_vjp(mean, q, s, a.view + 16 * v, a.projection + 16 * v, a.width, a.height,
+                projection_vjp(mean, Sigma, a.view + 16 * v, a.projection + 16 * v, a.width, a.height,
                                a.intrinsics[9 * v], a.intrinsics[9 * v + 4], gc, gk, g);
 #pragma unroll
                 for (int k = 0; k < 3; ++k) gm[k] += g.mean[k];
