@@ -1068,6 +1068,9 @@ __global__ __launch_bounds__(1024) void sum_i64_kernel(const int64_t* __restrict
 // output range, filled with stride 256 (coalesced), each item locating its
 // row by binary search over the rows' inclusive ends in LDS.
 // Item = Gaussian index << 32 | clipped rectangle << 20 | group id.
+constexpr int kEmitOwners = 2048;
+static_assert(kBinThreads <= 256, "owner map entries are bytes");
+
 template <bool PACKED>
 __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t* __restrict__ records,
                                                                  const int32_t* __restrict__ offsets, int64_t rows,
@@ -1078,6 +1081,7 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
     __shared__ int32_t s_gw[kBinThreads];
     __shared__ uint32_t s_gbase[kBinThreads];
     __shared__ uint32_t s_id[kBinThreads];
+    __shared__ uint8_t s_owner[kEmitOwners];
     const int64_t r0 = (int64_t)blockIdx.x * kBinThreads;
     const int cnt = (int)min((int64_t)kBinThreads, rows - r0);
     const int t = threadIdx.x;
@@ -1101,14 +1105,29 @@ __global__ __launch_bounds__(kBinThreads) void group_emit_kernel(const uint64_t*
     }
     __syncthreads();
     const int64_t E = min((int64_t)s_end[cnt - 1], limit);
+    // Blocks of at most kEmitOwners items look their rows up in an owner map
+    // that the rows fill (one byte per item); larger ones search.
+    const bool mapped = (int64_t)s_end[cnt - 1] - S <= kEmitOwners;
+    if (mapped) {
+        if (t < cnt) {
+            const int32_t from = (t > 0 ? s_end[t - 1] : (int32_t)S) - (int32_t)S, to = s_end[t] - (int32_t)S;
+            for (int32_t q = from; q < to; ++q) s_owner[q] = (uint8_t)t;
+        }
+        __syncthreads();
+    }
     for (int64_t p = S + t; p < E; p += kBinThreads) {
-        // First j with s_end[j] > p (p < s_end[cnt - 1], offsets are int32):
-        // a fixed 8-step search, every entry below lo ends at or before p.
-        const int32_t p32 = (int32_t)p;
         int lo = 0;
+        if (mapped) {
+            lo = s_owner[p - S];
+        } else {
+            // First j with s_end[j] > p (p < s_end[cnt - 1], offsets are
+            // int32): a fixed 8-step search, every entry below lo ends at or
+            // before p.
+            const int32_t p32 = (int32_t)p;
 #pragma unroll
-        for (int step = kBinThreads / 2; step > 0; step >>= 1)
-            if (lo + step <= cnt && s_end[lo + step - 1] <= p32) lo += step;
+            for (int step = kBinThreads / 2; step > 0; step >>= 1)
+                if (lo + step <= cnt && s_end[lo + step - 1] <= p32) lo += step;
+        }
         const int64_t start = lo > 0 ? s_end[lo - 1] : S;
         const int local = (int)(p - start);
         const int gw = s_gw[lo];
