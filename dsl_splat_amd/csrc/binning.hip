@@ -551,6 +551,7 @@ __global__ __launch_bounds__(256) void transpose_offsets_kernel(const int32_t* _
 template <class K, int RB, bool DROP = false>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
                 hipStream_t s, const int64_t* live = nullptr, int64_t* total = nullptr);
+inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStream_t s, int64_t* total);
 
 // tail_kind (1 or 2, 64-bit values only): the last pass also writes the
 // order tail (record_extent<tail_kind>).
@@ -615,7 +616,7 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
 // records (and, with a tail, zero group counts) to [*live, count).  The
 // result is in the first halves, as with run_sort.
 inline int run_order_sort(uint32_t* keys, uint64_t* values, int64_t count, void* scratch, int64_t* live,
-                          uint64_t filler, hipStream_t s, int tail_kind, OrderTail tail) {
+                          uint64_t filler, hipStream_t s, int tail_kind, OrderTail tail, bool first_counted) {
     SortScratch sc;
     sort_scratch_bytes(count, &sc, scratch);
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
@@ -626,7 +627,9 @@ inline int run_order_sort(uint32_t* keys, uint64_t* values, int64_t count, void*
     const dim3 grid((unsigned)tiles), block(kSortThreads);
     for (int shift = 0; shift < 32; shift += 8) {
         const bool first = shift == 0, last = shift == 24;
-        const int status = first ? sort_counts<uint32_t, 8, true>(kin, count, shift, 255u, 256, sc, s, nullptr, live)
+        const int status = first ? (first_counted ? scan_counts(count, 256, sc, s, live)
+                                                  : sort_counts<uint32_t, 8, true>(kin, count, shift, 255u, 256, sc, s,
+                                                                                   nullptr, live))
                                  : sort_counts<uint32_t, 8, false>(kin, count, shift, 255u, 256, sc, s, live, nullptr);
         if (status != GS3D_OK) return status;
         if (first) {
@@ -709,6 +712,16 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
     }
 }
 
+// Scan and transpose of a pass's [digit][tile] counts (already in sc.counts).
+inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStream_t s, int64_t* total) {
+    const int64_t tiles = (count + kSortTile - 1) / kSortTile;
+    const int status = run_scan<uint32_t, false>(sc.counts, tiles * digits, sc.scanned, total, sc.scan_scratch, s);
+    if (status != GS3D_OK) return status;
+    hipLaunchKernelGGL(transpose_offsets_kernel, dim3((unsigned)((tiles + 31) / 32), digits / 32), dim3(256), 0, s,
+                       sc.scanned, tiles, digits, sc.offsets);
+    return launch_status("radix sort counts");
+}
+
 // total (optional) receives the number of keys counted.
 template <class K, int RB, bool DROP>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
@@ -719,11 +732,7 @@ int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digi
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
     hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB, DROP>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
                        dim3(kSortThreads), 0, s, keys, count, shift, mask, sc.counts, tiles, digits, live);
-    const int status = run_scan<uint32_t, false>(sc.counts, tiles * digits, sc.scanned, total, sc.scan_scratch, s);
-    if (status != GS3D_OK) return status;
-    hipLaunchKernelGGL(transpose_offsets_kernel, dim3((unsigned)((tiles + 31) / 32), digits / 32), dim3(256), 0, s,
-                       sc.scanned, tiles, digits, sc.offsets);
-    return launch_status("radix sort counts");
+    return scan_counts(count, digits, sc, s, total);
 }
 
 // Start and end of every digit's run in the output of a one-pass sort: row
@@ -881,19 +890,23 @@ struct RowGeometry {
     int mode;
 };
 
-GS3D_DEV TileRect row_rect(const RowGeometry& g, int64_t row, int gx, int gy) {
+GS3D_DEV TileRect rect_of(int radius, float2 c, float4 k, int gx, int gy, int mode) {
     TileRect r{0, 0, 0, 0};
+    if (radius > 0) {
+        const int4 b = mode_rect(c, k, radius, gx, gy, mode);
+        if (b.z > b.x && b.w > b.y) r = TileRect{b.x, b.y, b.z, b.w};
+    }
+    return r;
+}
+
+GS3D_DEV TileRect row_rect(const RowGeometry& g, int64_t row, int gx, int gy) {
     // Centre and conic are loaded with the radius, not after it.
     const int radius = g.radii[row];
     const float2 c = reinterpret_cast<const float2*>(g.centers)[row];
     const float4 k = g.mode == GS3D_TILE_RADIUS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
                                                 : reinterpret_cast<const float4*>(g.conics)[row];
     asm volatile("" ::"v"(c.x), "v"(c.y), "v"(k.x), "v"(k.y), "v"(k.z), "v"(k.w));
-    if (radius > 0) {
-        const int4 b = mode_rect(c, k, radius, gx, gy, g.mode);
-        if (b.z > b.x && b.w > b.y) r = TileRect{b.x, b.y, b.z, b.w};
-    }
-    return r;
+    return rect_of(radius, c, k, gx, gy, g.mode);
 }
 
 template <bool PACKED>
@@ -954,41 +967,74 @@ GS3D_DEV void record_extent(uint64_t record, int32_t& groups, int64_t& area) {
     }
 }
 
-// Row order: depth-bit keys and records (coalesced reads of depth, centre
-// and radius).  Outside AccuTile, rows whose footprint touches no tile get
-// kDroppedKey instead of their depth bits: the depth order leaves them out.
-//
-// AccuTile (ACCU): the row's footprint and strips are computed here, once, in
-// row order; on grids of at most 256 x 256 tiles the record's high half
-// carries tiles << 12 | groups and footprints[row] the compact footprint, so
-// the depth-ordered passes neither gather nor recompute it.
+// Row order under AccuTile: depth-bit keys and records (coalesced reads of
+// depth, centre and radius).  The row's footprint and strips are computed
+// here, once, in row order; on grids of at most 256 x 256 tiles the record's
+// high half carries tiles << 12 | groups and footprints[row] the compact
+// footprint, so the depth-ordered passes neither gather nor recompute it.
 // tiles_out (optional) receives every row's tile count in the mode.
-template <bool PACKED, bool ACCU>
+template <bool PACKED>
 __global__ void row_records_kernel(const float* __restrict__ depths, RowGeometry g, int64_t rows, int gx, int gy,
                                    uint32_t* __restrict__ keys, uint64_t* __restrict__ records,
                                    int32_t* __restrict__ tiles_out, float4* __restrict__ footprints) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
-    uint32_t key = __float_as_uint(depths[i]);
     uint64_t rec = (uint64_t)(uint32_t)i;
-    if constexpr (ACCU) {
-        int groups = 0, tiles = 0;
-        const int radius = g.radii[i];
-        if (radius > 0) {
-            const Ellipse e = footprint(reinterpret_cast<const float2*>(g.centers)[i],
-                                        reinterpret_cast<const float4*>(g.conics)[i], radius, gx, gy);
-            accutile_groups(e, groups, tiles);
-            if constexpr (PACKED) {
-                float4 p0, p1;
-                pack_ellipse(e, p0, p1);
-                footprints[2 * i] = p0;
-                footprints[2 * i + 1] = p1;
-            }
+    int groups = 0, tiles = 0;
+    const int radius = g.radii[i];
+    if (radius > 0) {
+        const Ellipse e = footprint(reinterpret_cast<const float2*>(g.centers)[i],
+                                    reinterpret_cast<const float4*>(g.conics)[i], radius, gx, gy);
+        accutile_groups(e, groups, tiles);
+        if constexpr (PACKED) {
+            float4 p0, p1;
+            pack_ellipse(e, p0, p1);
+            footprints[2 * i] = p0;
+            footprints[2 * i + 1] = p1;
         }
-        if constexpr (PACKED) rec |= (uint64_t)(((uint32_t)tiles << 12) | (uint32_t)groups) << 32;
-        if (tiles_out) tiles_out[i] = tiles;
-    } else {
-        const TileRect r = row_rect(g, i, gx, gy);
+    }
+    if constexpr (PACKED) rec |= (uint64_t)(((uint32_t)tiles << 12) | (uint32_t)groups) << 32;
+    if (tiles_out) tiles_out[i] = tiles;
+    keys[i] = __float_as_uint(depths[i]);
+    records[i] = rec;
+}
+
+// Row order outside AccuTile: depth-bit keys and records, rows whose
+// footprint touches no tile keyed kDroppedKey (the depth order leaves them
+// out); record high halves as in the packed layout above.  One 2048-row sort
+// tile per block, which also counts the tile's key bytes 0-7 for the depth
+// order's first pass (dropped rows not counted): the [digit][tile] table that
+// pass's histogram would form, without reading the keys again.  Every load of
+// a thread's eight rows is issued first (clamped to the last row).
+template <bool PACKED>
+__global__ __launch_bounds__(kSortThreads) void row_records_counted_kernel(
+    const float* __restrict__ depths, RowGeometry g, int64_t rows, int gx, int gy, uint32_t* __restrict__ keys,
+    uint64_t* __restrict__ records, int32_t* __restrict__ tiles_out, uint32_t* __restrict__ counts, int64_t tiles) {
+    static_assert(kSortThreads == kRadix, "one digit per thread");
+    __shared__ uint32_t s_hist[kRadix];
+    s_hist[threadIdx.x] = 0u;
+    const int64_t tile = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int64_t base = tile * kSortTile + threadIdx.x;
+    float dep[kSortItems];
+    int rad[kSortItems];
+    float2 cen[kSortItems];
+    float4 con[kSortItems];
+#pragma unroll
+    for (int k = 0; k < kSortItems; ++k) {
+        const int64_t i = min(base + k * kSortThreads, rows - 1);
+        dep[k] = depths[i];
+        rad[k] = g.radii[i];
+        cen[k] = reinterpret_cast<const float2*>(g.centers)[i];
+        con[k] = g.mode == GS3D_TILE_RADIUS ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                                            : reinterpret_cast<const float4*>(g.conics)[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kSortItems; ++k) {
+        const int64_t i = base + k * kSortThreads;
+        if (i >= rows) continue;
+        const TileRect r = rect_of(rad[k], cen[k], con[k], gx, gy, g.mode);
+        uint64_t rec = (uint64_t)(uint32_t)i;
         if constexpr (PACKED) {
             const uint32_t p = r.x1 > r.x0 ? (uint32_t)r.x0 | ((uint32_t)r.y0 << 8) |
                                                  ((uint32_t)(r.x1 - 1) << 16) | ((uint32_t)(r.y1 - 1) << 24)
@@ -996,10 +1042,13 @@ __global__ void row_records_kernel(const float* __restrict__ depths, RowGeometry
             rec |= (uint64_t)p << 32;
         }
         if (tiles_out) tiles_out[i] = r.x1 > r.x0 ? (r.x1 - r.x0) * (r.y1 - r.y0) : 0;
-        if (!(r.x1 > r.x0)) key = kDroppedKey;
+        const uint32_t key = r.x1 > r.x0 ? __float_as_uint(dep[k]) : kDroppedKey;
+        keys[i] = key;
+        records[i] = rec;
+        if (key != kDroppedKey) atomicAdd(&s_hist[key & 255u], 1u);
     }
-    keys[i] = key;
-    records[i] = rec;
+    __syncthreads();
+    counts[(int64_t)threadIdx.x * tiles + tile] = s_hist[threadIdx.x];
 }
 
 // Group count of every row in depth order; the block's tile pair count goes
@@ -1965,17 +2014,26 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     float4* fp = reinterpret_cast<float4*>(a.footprints);
     const dim3 grid(gs3d::blocks_for(rows, 256)), block(256);
     if (accu && packed)
-        hipLaunchKernelGGL((gs3d::row_records_kernel<true, true>), grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy,
+        hipLaunchKernelGGL((gs3d::row_records_kernel<true>), grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy,
                            sc.keys, a.order, a.tiles_out, fp);
     else if (accu)
-        hipLaunchKernelGGL((gs3d::row_records_kernel<false, true>), grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy,
+        hipLaunchKernelGGL((gs3d::row_records_kernel<false>), grid, block, 0, s, a.depths, geo, rows, d.gx, d.gy,
                            sc.keys, a.order, a.tiles_out, fp);
-    else if (packed)
-        hipLaunchKernelGGL((gs3d::row_records_kernel<true, false>), grid, block, 0, s, a.depths, geo, rows, d.gx,
-                           d.gy, sc.keys, a.order, a.tiles_out, fp);
-    else
-        hipLaunchKernelGGL((gs3d::row_records_kernel<false, false>), grid, block, 0, s, a.depths, geo, rows, d.gx,
-                           d.gy, sc.keys, a.order, a.tiles_out, fp);
+    else {
+        // Outside AccuTile the records kernel also forms the depth order's
+        // first digit counts.
+        gs3d::SortScratch ss;
+        gs3d::sort_scratch_bytes(rows, &ss, sc.sort);
+        const int64_t tiles = (rows + gs3d::kSortTile - 1) / gs3d::kSortTile;
+        if (packed)
+            hipLaunchKernelGGL((gs3d::row_records_counted_kernel<true>), dim3((unsigned)tiles),
+                               dim3(gs3d::kSortThreads), 0, s, a.depths, geo, rows, d.gx, d.gy, sc.keys, a.order,
+                               a.tiles_out, ss.counts, tiles);
+        else
+            hipLaunchKernelGGL((gs3d::row_records_counted_kernel<false>), dim3((unsigned)tiles),
+                               dim3(gs3d::kSortThreads), 0, s, a.depths, geo, rows, d.gx, d.gy, sc.keys, a.order,
+                               a.tiles_out, ss.counts, tiles);
+    }
     // order holds 2*rows records: [0, rows) sorted result, [rows, 2rows) ping-pong.  With packed
     // records the last pass also writes each row's group count at its sorted position and the
     // blocks' tile-pair sums; otherwise order_counts_kernel computes them from the geometry.
@@ -1989,7 +2047,7 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     else
         status = gs3d::run_order_sort(sc.keys, a.order, rows, sc.sort, sc.live,
                                       packed ? (uint64_t)gs3d::kEmptyRect << 32 : 0u, s, tail_kind,
-                                      gs3d::OrderTail{sc.counts, sc.pairs});
+                                      gs3d::OrderTail{sc.counts, sc.pairs}, true);
     if (status != GS3D_OK) return status;
     int64_t pair_blocks = (rows + gs3d::kSortTile - 1) / gs3d::kSortTile;
     if (!packed) {
