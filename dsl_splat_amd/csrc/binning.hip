@@ -1002,7 +1002,7 @@ __global__ void row_records_kernel(const float* __restrict__ depths, RowGeometry
 // Row order outside AccuTile: depth-bit keys and records, rows whose
 // footprint touches no tile keyed kDroppedKey (the depth order leaves them
 // out); record high halves as in the packed layout above.  One 2048-row sort
-// tile per block, which also counts the tile's key bytes 0-7 for the depth
+// tile per block, which also counts the tile's keys by bits 0-7 for the depth
 // order's first pass (dropped rows not counted): the [digit][tile] table that
 // pass's histogram would form, without reading the keys again.  Every load of
 // a thread's eight rows is issued first (clamped to the last row).
