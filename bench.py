@@ -256,37 +256,48 @@ def kernel_timings(scene, frame):
     out = {}
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.no_grad():
-        # One launch at a time after a 2 GiB read that evicts the L2 and the
-        # Infinity Cache with clean lines: the kernel's inputs then come from
-        # HBM, as inside a step (back-to-back launches would find the 132 MB
-        # of parameters cached; a fill would leave dirty lines for the kernel
-        # to write back).  The read (~0.3 ms) outlasts the host's enqueueing
-        # of the launch, so no idle time falls between the events.  Without
-        # coefficients the call launches the projection kernel only.
-        launches = 10
+        # Back-to-back launches that rotate over three copies of the
+        # parameters (3 x 132 MB) and three sets of outputs (3 x 720 MB):
+        # every launch reads its inputs from HBM (the two launches in between
+        # wrote 1.4 GB, far more than the L2 and the Infinity Cache hold) and
+        # pays for writing back the dirty lines the previous launch left, as
+        # inside a training step.  Only the last launch's lines still in the
+        # caches at the end event go unpaid: about 1/20 of one launch's output
+        # at most.  Without coefficients the call launches the projection
+        # kernel only.
+        launches, copies = 20, 3
+        params = [tuple(t.clone() for t in (scene.means, scene.quats, scene.scales, scene.opacities))
+                  for _ in range(copies)]
+        project = lambda p: gproj.project_views(*p, scene.viewmats, full, scene.Ks, scene.width, scene.height, 0.2,
+                                                math.inf, 0.0, metadata=True, normalize_quats=True)
+        keep = [project(p) for p in params]
+        # A 2 GiB read ahead of the first launch keeps the device busy while
+        # the host enqueues the first launches, so no idle time falls
+        # between the events.
         flush = torch.ones(512 << 20, dtype=torch.float32, device=scene.means.device)
-        project = lambda: gproj.project_views(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats,
-                                              full, scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0,
-                                              metadata=True, normalize_quats=True)
-        project()
-        out["project_kernel"] = 0.0
-        for _ in range(launches):
-            flush.amax()
-            e0.record()
-            project()
-            e1.record()
-            torch.cuda.synchronize()
-            out["project_kernel"] += e0.elapsed_time(e1) / launches
+        torch.cuda.synchronize()
+        flush.amax()
+        e0.record()
+        for i in range(launches):
+            # project_views allocates its outputs; the caching allocator
+            # hands back the blocks freed copies launches earlier, so the
+            # output sets rotate as the parameter copies do.
+            keep[i % copies] = None
+            keep[i % copies] = project(params[i % copies])
+        e1.record()
+        torch.cuda.synchronize()
+        out["project_kernel"] = e0.elapsed_time(e1) / launches
+        del params, keep
         # A plain 2 GiB device copy on the same GPU: the bandwidth a
         # streaming kernel reaches here, beside the 8 TB/s peak.
         dst = torch.empty_like(flush)
         dst.copy_(flush)
         e0.record()
-        for _ in range(launches):
+        for _ in range(10):
             dst.copy_(flush)
         e1.record()
         torch.cuda.synchronize()
-        out["copy_gbps"] = 2 * flush.numel() * 4 / (e0.elapsed_time(e1) / launches * 1e-3) / 1e9
+        out["copy_gbps"] = 2 * flush.numel() * 4 / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
         del flush, dst
         # Contribution statistics (a masked count and a weighted sum over
         # per-view pixel maps) observed by the forward blend, against the
@@ -512,7 +523,9 @@ def main():
             "ms": round(kernel_ms, 4),
             "bytes": kernel_bytes,
             "note": "parameters read once for all views (44 B/G) and 60 B per (view, Gaussian) written; the "
-                    "colour kernel's bytes are in stages.project",
+                    "colour kernel's bytes are in stages.project. Time base: HIP events around 20 back-to-back "
+                    "launches rotating over 3 parameter copies and 3 output sets (inputs from HBM, each launch "
+                    "pays the previous one's write-back), averaged",
             "copy_gbps": round(kt["copy_gbps"], 1),
             "copy_note": "a 2 GiB device-to-device copy (read + write) timed on the same GPU, for context",
         },

@@ -594,6 +594,9 @@ __global__ __launch_bounds__(kProjBlock) __attribute__((amdgpu_waves_per_eu(4)))
     if constexpr (CAM) {
         for (int e = threadIdx.x; e < (kProjBlock / 64) * kMaxViewsCamLds * 24; e += kProjBlock)
             (&s_cam[0][0][0])[e] = 0.0f;
+        // The loop above zeroes other wavefronts' slices too: every zero must
+        // land before any wavefront's lane 63 adds into its slice.
+        __syncthreads();
     }
     for (int64_t base = (int64_t)blockIdx.x * kProjBlock; base < n; base += (int64_t)gridDim.x * kProjBlock) {
         const int64_t i = base + threadIdx.x;
