@@ -211,7 +211,7 @@ GS3D_DEV uint32_t strip_mask(float2 xy, float4 con, float cut, int x0, int y0) {
 
 // Stage one Gaussian's centre, conic, cutoff, strip mask and the channels
 // [c0, c0 + CH) of its channel vector (zero beyond D').
-template <int CH, int PIX>
+template <int CH, int PIX, bool LAUNDER = false>
 GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32_t g, int slot, int c0,
                              float2* s_xy, float4* s_con, float* s_cut, uint32_t* s_mask, float* s_feat) {
     const int view = t.view;
@@ -241,7 +241,15 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32
     s_con[slot] = con;
     const float cut = power_cutoff(con.w);
     s_cut[slot] = cut;
-    s_mask[slot] = strip_mask<PIX>(xy, con, cut, t.x0, t.y0);
+    int x0 = t.x0, y0 = t.y0;
+    if constexpr (LAUNDER) {
+        // The tile origin passes through an opaque scalar move, so that the
+        // strip edges' float conversions are redone here (a few VALU per
+        // staged Gaussian) instead of being hoisted out of the batch loop
+        // into VGPRs that stay live over the whole traversal.
+        asm volatile("" : "+s"(x0), "+s"(y0));
+    }
+    s_mask[slot] = strip_mask<PIX>(xy, con, cut, x0, y0);
     float* dst = s_feat + slot * CH;
 #pragma unroll
     for (int c = 0; c < CH; ++c) dst[c] = v[c];
@@ -287,43 +295,101 @@ GS3D_DEV Staged<CH> load_staged(int j, const float2* s_xy, const float4* s_con, 
 }
 
 // Contribution statistics of one accepted Gaussian (statistics.py:46-70,
-// observed at gs3d/render.py:109-115): for every request r, a masked count
-// adds the number of this wavefront's accepted pixels whose value is nonzero
-// (one ballot per pixel slot), a weighted sum adds value * alpha * T over
-// them (one wavefront reduction).  One lane issues each request's atomic, so
-// a wavefront adds one partial per (Gaussian, request) instead of one per
-// pixel; counts are exact, sums differ from per-pixel atomics only in the
-// order of the float additions (which atomics leave unspecified anyway).
-template <int PIX>
-GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, int view, int n, int32_t g, const bool (&acc)[PIX],
-                                 const float (&w)[PIX], const float (&val)[PIX][GS3D_MAX_STATISTICS], int lane) {
-    int count_row = 0, sum_row = 0;
+// observed at gs3d/render.py:109-115).  Each lane forms, for every request r
+// of the launch (RB, the request count rounded up to 1, 2, 4 or 8), its
+// pixels' part: the number of accepted pixels whose value is nonzero for a
+// masked count, the sum of value * alpha * T over them for a weighted sum.
+// A count request's pixel values are replaced by 0/1 masks when they are
+// loaded, so both kinds are one multiply-add per pixel: value times
+// (accepted ? alpha * T : 0) for a sum, mask times (accepted ? 1 : 0) for a
+// count.  That product form is exact only for finite values (a rejected
+// pixel's value times zero), so a wavefront with a non-finite value selects
+// each term instead (wave-uniform choice).  One wavefront sum covers all
+// requests together (permlane pairing and a DPP row butterfly, as in the
+// backward), and each lane that holds a request's total adds it with one
+// atomic to the row fixed for it at the start of the tile (StatLane).
+// Counts are exact (at most 64 * PIX per wavefront, summed in float32
+// without rounding); sums differ from per-pixel atomics only in the order of
+// the float additions, which atomics leave unspecified anyway.
+struct StatLane {
+    void* row;    // the lane's request row (view applied), or NULL
+    bool is_sum;  // row is a float sums row, else an int32 counts row
+};
+
+template <int RB>
+GS3D_DEV StatLane stat_lane(const gs3d_render_stats_args& st, int view, int n, int lane) {
+    StatLane l{nullptr, false};
+    int r = 0;
+    if constexpr (RB == 1) {
+        if (lane != 63) return l;
+    } else {
+        constexpr int rows = (RB + 3) / 4;
+        r = wave_sum_rows_value(lane);
+        if ((lane & 15) >= rows || r >= RB) return l;
+    }
+    if (r >= st.requests) return l;
+    // Row of request r among the requests of its kind.
+    const uint32_t before = st.sum_mask & ((1u << r) - 1u);
+    l.is_sum = (st.sum_mask >> r) & 1u;
+    if (l.is_sum)
+        l.row = st.sums + view * st.sums_view_stride + (int64_t)__builtin_popcount(before) * n;
+    else
+        l.row = st.counts + view * st.counts_view_stride + (int64_t)(r - __builtin_popcount(before)) * n;
+    return l;
+}
+
+// KINDS: the requests' kinds as a compile-time sum mask (bit r set: request
+// r is a weighted sum) for launches of one or two requests, -1 to read them
+// from st.sum_mask.
+template <int PIX, int RB, int KINDS>
+GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, const StatLane& dst, int32_t g,
+                                 const bool (&acc)[PIX], const float (&w)[PIX], const float (&val)[PIX][RB],
+                                 bool finite, int lane) {
+    float e[RB];
+    if (finite) {
+        float one[PIX];
 #pragma unroll
-    for (int r = 0; r < GS3D_MAX_STATISTICS; ++r) {
-        if (r >= st.requests) break;
-        if ((st.sum_mask >> r) & 1u) {
-            float s = 0.0f;
-            bool any = false;
+        for (int k = 0; k < PIX; ++k) one[k] = acc[k] ? 1.0f : 0.0f;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            // wave-uniform; a compile-time constant for KINDS >= 0
+            const bool is_sum = KINDS >= 0 ? ((KINDS >> r) & 1) != 0 : ((st.sum_mask >> r) & 1u) != 0;
+            float v = 0.0f;
+#pragma unroll
+            for (int k = 0; k < PIX; ++k) v = __builtin_fmaf(val[k][r], is_sum ? w[k] : one[k], v);
+            e[r] = v;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const bool is_sum = (st.sum_mask >> r) & 1u;
+            float v = 0.0f;
 #pragma unroll
             for (int k = 0; k < PIX; ++k) {
                 const bool hit = acc[k] && val[k][r] != 0.0f;
-                any = any || hit;
-                s += hit ? val[k][r] * w[k] : 0.0f;
+                v += hit ? (is_sum ? val[k][r] * w[k] : 1.0f) : 0.0f;
             }
-            if (__ballot(any)) {
-                s = wave_sum_to_lane63(s);
-                if (lane == 63)
-                    atomicAdd(st.sums + view * st.sums_view_stride + (int64_t)sum_row * n + g, s);
-            }
-            ++sum_row;
-        } else {
-            int c = 0;
-#pragma unroll
-            for (int k = 0; k < PIX; ++k) c += __popcll(__ballot(acc[k] && val[k][r] != 0.0f));
-            if (c > 0 && lane == 0)
-                atomicAdd(st.counts + view * st.counts_view_stride + (int64_t)count_row * n + g, c);
-            ++count_row;
+            e[r] = v;
         }
+    }
+    float total;
+    if constexpr (RB == 1) {
+        total = wave_sum_to_lane63(e[0]);
+    } else {
+        constexpr int rows = (RB + 3) / 4;
+        float sums[rows];
+        wave_sum_rows<RB>(e, sums);
+#pragma unroll
+        for (int q = 0; q < rows; ++q) asm volatile("" : "+v"(sums[q]));
+        total = sums[0];
+#pragma unroll
+        for (int q = 1; q < rows; ++q) total = ((lane & 15) == q) ? sums[q] : total;
+    }
+    if (dst.row && total != 0.0f) {
+        if (dst.is_sum)
+            atomicAdd(static_cast<float*>(dst.row) + g, total);
+        else
+            atomicAdd(static_cast<int*>(dst.row) + g, (int)total);
     }
 }
 
@@ -336,8 +402,13 @@ GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, int view, int
 // them (list entries up to and including the one that terminates the pixel,
 // the whole list otherwise), evaluated by this kernel (after strip culling,
 // while the pixel is live) and accepted (blended).
-template <int CH, int PIX, int MODE>
-__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 8 ? 6 : 1))) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st, int c0, unsigned long long* counts) {
+//
+// RB: statistics requests compiled in (MODE 1; the launch's request count
+// rounded up to 1, 2, 4 or 8), so that only their pixel values take
+// registers; KINDS: their kinds as a sum mask for one or two requests (the
+// observer then needs no per-request selects), -1 otherwise.
+template <int CH, int PIX, int MODE, int RB = 1, int KINDS = -1>
+__global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 4 ? 6 : CH <= 8 ? 5 : 1))) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st, int c0, unsigned long long* counts) {
     constexpr bool STATS = MODE == 1, COUNTS = MODE == 2;
     constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
@@ -353,7 +424,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     float fx[PIX], fy[PIX], T[PIX], color[PIX][CH];
     int px[PIX], py[PIX], last_contributor[PIX];
     bool done[PIX];
-    float val[PIX][STATS ? GS3D_MAX_STATISTICS : 1];
+    float val[PIX][STATS ? RB : 1];
     int visited[PIX];
     uint32_t evaluated = 0, accepted = 0;
 #pragma unroll
@@ -374,8 +445,11 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
             const float* pv = st.pixel_values + t.view * st.pixel_view_stride + (int64_t)py[k] * a.width + px[k];
             const int64_t plane = (int64_t)a.width * a.height;
 #pragma unroll
-            for (int r = 0; r < GS3D_MAX_STATISTICS; ++r)
-                val[k][r] = (r < st.requests && !done[k]) ? pv[r * plane] : 0.0f;
+            for (int r = 0; r < RB; ++r) {
+                const float v = (r < st.requests && !done[k]) ? pv[r * plane] : 0.0f;
+                // Count requests keep a 0/1 mask (see observe_statistics).
+                val[k][r] = ((st.sum_mask >> r) & 1u) ? v : (v != 0.0f ? 1.0f : 0.0f);
+            }
         }
     }
     // Each thread stages at most one Gaussian per batch (B <= NT); its index
@@ -383,6 +457,17 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     // into the list, so the load is unconditional).
     static_assert(B <= NT, "one staged Gaussian per thread and batch");
     int32_t next_id = t.last > t.first ? a.ids[min(t.first + (int)threadIdx.x, t.last - 1)] : 0;
+    StatLane stat_dst{nullptr, false};
+    bool stat_finite = true;
+    if constexpr (STATS) {
+        stat_dst = stat_lane<RB>(st, t.view, a.n, lane);
+        bool finite = true;
+#pragma unroll
+        for (int k = 0; k < PIX; ++k)
+#pragma unroll
+            for (int r = 0; r < RB; ++r) finite = finite && __builtin_fabsf(val[k][r]) <= 3.0e38f;
+        stat_finite = __ballot(!finite) == 0;
+    }
     for (int begin = t.first; begin < t.last; begin += B) {
         bool active = false;
 #pragma unroll
@@ -392,7 +477,9 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
             const int e = threadIdx.x;
             const int32_t g = next_id;
             if (begin + e < t.last) {
-                stage_gaussian<CH, PIX>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
+                // The 4-channel plain blend fits its registers without the
+                // tile-origin laundering (and is fastest so).
+                stage_gaussian<CH, PIX, (STATS || CH > 4)>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
                 if constexpr (STATS) s_id[e] = g;
             }
             if (begin + B < t.last) next_id = a.ids[min(begin + B + e, t.last - 1)];
@@ -449,7 +536,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                     bool hit = false;
 #pragma unroll
                     for (int k = 0; k < PIX; ++k) hit = hit || acc[k];
-                    if (__ballot(hit)) observe_statistics<PIX>(st, t.view, a.n, s_id[j], acc, wk, val, lane);
+                    if (__ballot(hit)) observe_statistics<PIX, RB, KINDS>(st, stat_dst, s_id[j], acc, wk, val, stat_finite, lane);
                 }
             };
             auto alive = [&]() {
@@ -463,9 +550,12 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 todo &= todo - 1;
                 return j;
             };
-            if constexpr (STATS || (CH > 16 && CH <= 36)) {
+            if constexpr ((STATS && (RB > 2 || CH > 4)) || (CH > 16 && CH <= 36)) {
                 // Loads at use: the pipelined form's extra registers would
-                // cost occupancy -- the statistics variant's, and for 36
+                // cost occupancy -- with statistics beyond two requests (their
+                // pixel values take 4 * PIX registers or more) or four
+                // channels (up to both, the pipelined form fits 80 VGPRs),
+                // and for 36
                 // channels a third wavefront per SIMD (148 VGPRs against 190
                 // with the next Gaussian's vector prefetched: 0.83 -> 0.72
                 // ms on the 32-feature workload).
@@ -858,7 +948,24 @@ int launch_fwd_pix(const gs3d_render_args& a, const gs3d_render_stats_args* st, 
                    unsigned blocks, int c0, hipStream_t s) {
     const dim3 grid(blocks), block(kTilePixels / PIX);
     if (st) {
-        hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1>), grid, block, 0, s, a, *st, c0, nullptr);
+        const uint32_t kinds = st->sum_mask;
+        if (st->requests <= 1) {
+            if (kinds & 1u)
+                hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1, 1, 1>), grid, block, 0, s, a, *st, c0, nullptr);
+            else
+                hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1, 1, 0>), grid, block, 0, s, a, *st, c0, nullptr);
+        } else if (st->requests <= 2) {
+            switch (kinds & 3u) {
+                case 0: hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1, 2, 0>), grid, block, 0, s, a, *st, c0, nullptr); break;
+                case 1: hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1, 2, 1>), grid, block, 0, s, a, *st, c0, nullptr); break;
+                case 2: hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1, 2, 2>), grid, block, 0, s, a, *st, c0, nullptr); break;
+                default: hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1, 2, 3>), grid, block, 0, s, a, *st, c0, nullptr); break;
+            }
+        } else if (st->requests <= 4)
+            hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1, 4>), grid, block, 0, s, a, *st, c0, nullptr);
+        else
+            hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 1, GS3D_MAX_STATISTICS>), grid, block, 0, s, a, *st, c0,
+                               nullptr);
         return launch_status("gs3d_render_fwd_stats");
     }
     const gs3d_render_stats_args none = {};

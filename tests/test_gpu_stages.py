@@ -273,6 +273,45 @@ def test_render_backward_parity(key, degree, absgrad):
         check_gradient("abs", rec[..., 6:8], ref["abs"], bound["abs"])
 
 
+@pytest.mark.parametrize("key", ["small_rgb", "wide_rgb"])
+def test_render_backward_non_finite_inputs(key):
+    # The backward's fast traversal adds a rejected pixel's terms with zero
+    # weights; whenever an operand may be non-finite it must skip them as the
+    # reference's loop does.  NaN features, a NaN upstream gradient and an
+    # infinite conic entry (staged after a finite forward, so the lists and
+    # transmittances are ordinary) must give the oracle's results: NaN exactly
+    # where the oracle has NaN, every other entry within the criterion.
+    scene = _scene(key)
+    _say(f"render bwd non-finite {key}")
+    quats, full, inverse, centers, st, bins = _frame(scene, None)
+    feats = scene.features
+    out = grender.render_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats, scene.width,
+                               scene.height)
+    up = torch.randn(out.stacked().shape, device=DEV)
+    visible = torch.nonzero(st.radii[0] > 0).flatten()
+    feats = feats.clone()
+    feats[visible[:3], 1] = float("nan")
+    conics = st.conics.clone()
+    conics[0, visible[3:5], 0] = float("inf")
+    up[0, scene.height // 2, scene.width // 3, 0] = float("nan")
+    record, gf, _ = grender.backward_views(bins["ranges"], bins["point_list"], st.centers, conics, feats,
+                                           out.transmittance, out.contributors, up, scene.width, scene.height,
+                                           absgrad=True)
+    ref, bound = _oracle_render_bwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]),
+                                    _np(st.centers), _np(conics), _np(feats), _np(out.transmittance),
+                                    _np(out.contributors), _np(up), absgrad=True)
+    rec = _np(record)
+    nans = 0
+    for name, got in (("centers", rec[..., 0:2]), ("conics", rec[..., 2:6]), ("abs", rec[..., 6:8]),
+                      ("features", _np(gf))):
+        nan_got, nan_ref = np.isnan(got), np.isnan(ref[name])
+        nans += int(nan_ref.sum())
+        np.testing.assert_array_equal(nan_got, nan_ref, err_msg=name)
+        keep = ~nan_ref
+        check_gradient(name, got[keep], ref[name][keep], np.broadcast_to(bound[name], ref[name].shape)[keep])
+    assert nans > 0
+
+
 # Blended-channel widths D' = features + extra + 1 covering every compiled
 # channel window: one window (D' <= 56: kernels of 4, 8, 16, 36 and 56
 # channels), the geometry window of 56 followed by feature windows (57-64,

@@ -69,6 +69,85 @@ def test_statistics_kernel_matches_oracle(key, degree):
     compare(f"stat_sums_{key}", _np(sums), ref_sums, rtol=1e-4, atol=1e-5 * float(np.abs(ref_sums).max()))
 
 
+def _bucket_maps(views, H, W, kinds, seed):
+    """Pixel values (views, R, H*W) for the given request kinds: 0/1 masks for
+    counts, N(0,1) weights with 20% zeros for sums."""
+    g = torch.Generator().manual_seed(seed)
+    maps = []
+    for kind in kinds:
+        if kind == 0:
+            maps.append((torch.rand((views, H, W), generator=g) < 0.4).float())
+        else:
+            w = torch.randn((views, H, W), generator=g)
+            w[torch.rand((views, H, W), generator=g) < 0.2] = 0.0
+            maps.append(w)
+    return torch.stack(maps, 1).reshape(views, len(kinds), H * W).contiguous().to(DEV)
+
+
+def _stats_against_oracle(scene, feats, st, bins, kinds, pv, nonfinite=False):
+    views, n = st.radii.shape
+    H, W = scene.height, scene.width
+    counts = torch.zeros((views, kinds.count(0), n), dtype=torch.int32, device=DEV)
+    sums = torch.zeros((views, kinds.count(1), n), dtype=torch.float32, device=DEV)
+    args = (bins["ranges"], bins["point_list"], st.centers, st.conics, feats, W, H)
+    out = grender.render_views(*args, statistics=PreparedStatistics(tuple(kinds), pv, counts, sums))
+    img, ft, ct, ref_counts, ref_sums = oracle.render_fwd_stats(
+        W, H, _np(bins["ranges"]), _np(bins["point_list"]), _np(st.centers), _np(st.conics), _np(feats),
+        tuple(kinds), _np(pv))
+    np.testing.assert_array_equal(_np(out.stacked()), img)
+    np.testing.assert_array_equal(_np(out.contributors), ct)
+    np.testing.assert_array_equal(_np(counts), ref_counts)
+    got = _np(sums)
+    if nonfinite:
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(ref_sums))
+        np.testing.assert_array_equal(np.isinf(got), np.isinf(ref_sums))
+        assert not np.isfinite(ref_sums).all()
+        keep = np.isfinite(ref_sums)
+        got, ref_sums = got[keep], ref_sums[keep]
+    if ref_sums.size:
+        compare(f"stat_sums_{len(kinds)}", got, ref_sums, rtol=1e-4,
+                atol=1e-5 * max(float(np.abs(ref_sums).max()), 1e-30))
+    return ref_counts, ref_sums
+
+
+# Request counts of every compiled bucket (1, 2, 4, 8), every combination of
+# kinds of one and two requests (compiled in), at one and two pixels per lane
+# and at 4 and 8 blended channels (4-channel launches of up to two requests
+# take the pipelined traversal; the others load at use).
+@pytest.mark.parametrize("key,channels,kinds", [
+    ("small_rgb", 3, (1,)), ("wide_rgb", 3, (1,)), ("wide_rgb", 3, (0,)), ("wide_rgb", 3, (0, 1)),
+    ("wide_rgb", 3, (1, 0)), ("wide_rgb", 3, (0, 0)), ("wide_rgb", 3, (1, 1)), ("wide_rgb", 3, (0, 1, 1)),
+    ("wide_rgb", 3, (1, 0, 1, 1, 0, 1, 0, 0)), ("wide_rgb", 6, (1,)), ("wide_rgb", 6, (0, 1)),
+    ("small_rgb", 6, (0, 1, 0, 1))])
+def test_statistics_request_buckets(key, channels, kinds):
+    scene = _scene(key)
+    _say(f"statistics buckets {key} D={channels} kinds={kinds}")
+    quats, full, inverse, centers, st, bins = _frame(scene, None)
+    n = st.radii.shape[1]
+    g = torch.Generator().manual_seed(5)
+    feats = scene.features if channels == 3 else torch.rand((n, channels), generator=g).to(DEV)
+    pv = _bucket_maps(st.radii.shape[0], scene.height, scene.width, kinds, 11)
+    ref_counts, ref_sums = _stats_against_oracle(scene, feats, st, bins, list(kinds), pv)
+    assert (ref_counts.sum() > 0) or (ref_sums != 0).any()
+
+
+@pytest.mark.parametrize("key", ["small_rgb", "wide_rgb"])
+def test_statistics_non_finite_weights(key):
+    # A weighted sum whose pixel weights hold NaN and +inf: the product form
+    # of the observer (value times a zero weight for rejected pixels) must not
+    # be used there; the oracle's sums, NaN and inf included, are reproduced.
+    scene = _scene(key)
+    _say(f"statistics non-finite weights {key}")
+    quats, full, inverse, centers, st, bins = _frame(scene, None)
+    views = st.radii.shape[0]
+    H, W = scene.height, scene.width
+    kinds = [0, 1]
+    pv = _bucket_maps(views, H, W, kinds, 13)
+    pv[0, 1, (H // 2) * W + W // 2] = float("nan")
+    pv[0, 1, (H // 3) * W + W // 4] = float("inf")
+    _stats_against_oracle(scene, scene.features, st, bins, kinds, pv, nonfinite=True)
+
+
 def _requests(views, H, W):
     g = torch.Generator().manual_seed(3)
     mask = (torch.rand((H, W), generator=g) < 0.5).to(DEV)
