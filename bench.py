@@ -39,6 +39,7 @@ HEADLINE = "sh3_1080p_4view"
 # Benchmark workloads in order (synthetic.make_scene names).
 WORKLOADS = ("small", "sh3_720p", "sh3_1080p_4view", "feat32", "pose_fanout")
 HBM_STAGES = ("project", "order", "bin", "project_bwd")
+FANOUT = "pose_fanout"  # 2M Gaussians, 5% of them large: the workload the tile modes are for
 
 
 def measured_traffic(workload, n):
@@ -321,6 +322,52 @@ def kernel_timings(scene, frame):
     return out
 
 
+def sort_pairs_timing(scene, frame, reps=5):
+    """The reference's own binning sequence on one camera's real tile pairs:
+    gs3d_sort_pairs_u64 (stable LSD radix sort of the (tile << 32 | depth
+    bits) keys with their Gaussian ids over bits [0, 32 + bit_length(T))) +
+    gs3d_tile_ranges, the entry points a caller of the reference's
+    primitives/tiling.py:67-100 binds.  The keys come from gs3d_emit_keys on
+    the first camera's projected rows; each repetition restores the unsorted
+    keys and zeroes the ranges outside the timed region."""
+    import torch
+    from dsl_splat_amd.primitives import tiling
+    from dsl_splat_amd.splatting import binning
+
+    st = frame["st"]
+    W, H = scene.width, scene.height
+    T = binning.tile_count(W, H, 1)
+    with torch.no_grad():
+        offsets, count = tiling.scan_counts(st.tile_counts[0])
+        keys, ids = binning.emit_keys(st.centers[0], st.radii[0], st.depths[0], offsets, count, W, H)
+        keys0, ids0 = keys[:count].clone(), ids[:count].clone()
+        ranges = torch.zeros((T, 2), dtype=torch.int32, device=keys.device)
+        end_bit = 32 + int(T).bit_length()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ms = []
+        for i in range(reps + 1):
+            keys[:count].copy_(keys0)
+            ids[:count].copy_(ids0)
+            ranges.zero_()
+            e0.record()
+            tiling.sort_pairs(keys, ids, count, end_bit)
+            tiling.identify_ranges(keys[:count], ranges)
+            e1.record()
+            torch.cuda.synchronize()
+            if i:
+                ms.append(e0.elapsed_time(e1))
+        passes = (end_bit + 7) // 8
+        nbytes = (24 * passes + 8) * count + 8 * T
+        t = statistics.median(ms)
+        gbps = nbytes / (t * 1e-3) / 1e9
+        del keys, ids, keys0, ids0
+    return dict(pairs=count, end_bit=end_bit, passes=passes, tiles=T, ms=round(t, 4), bytes=nbytes,
+                gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
+                note="gs3d_sort_pairs_u64 + gs3d_tile_ranges on camera 1's keys from gs3d_emit_keys (the "
+                     "reference's sort_tile_pairs); bytes (24 P + 8) M + 8 T, median of "
+                     f"{reps} repetitions")
+
+
 def cpu_baseline(scene, workload):
     """The C++ oracle (fwd+bwd, OpenMP on the host cores): the workload's
     first camera at full N and resolution, scaled by the camera count for
@@ -467,6 +514,8 @@ def main():
         modes[mode] = dict(ms=round(t["ms"], 3), pairs=int(f_m.meta["tiles_per_gauss"].sum()))
     log("[bench] kernel timings")
     kt = kernel_timings(scene, frame)
+    log("[bench] reference-convention pair sort")
+    sort_pairs = sort_pairs_timing(scene, frame)
     if args.copy_calibration_mib > 0:
         src = torch.ones(args.copy_calibration_mib << 18, device=device)
         dst = torch.empty_like(src)
@@ -481,7 +530,20 @@ def main():
         for wl in WORKLOADS:
             if wl == args.workload:
                 continue
-            entry, *_ = run_workload(wl, None, device, args.workload_steps, 2, cpu, min_timed_ms=50.0)
+            entry, _, _, wl_inputs, wl_forward = run_workload(wl, None, device, args.workload_steps, 2, cpu,
+                                                               min_timed_ms=50.0)
+            if wl == FANOUT and args.mode_steps > 0:
+                # The tile modes cut the pair count most where Gaussians fan
+                # out over many tiles.
+                modes_wl = {"radius": dict(ms=entry["ms"], pairs=int(wl_forward.meta["tiles_per_gauss"].sum()))}
+                for mode in ("snugbox", "accutile"):
+                    log(f"[bench] {wl} tile_mode={mode}: {entry['steps']} steps")
+                    f_m, b_m = step_fn(*wl_inputs, mode)
+                    t = time_steps(f_m, b_m, entry["steps"], 1, stage_events=True)
+                    modes_wl[mode] = dict(ms=round(t["ms"], 3), pairs=int(f_m.meta["tiles_per_gauss"].sum()),
+                                          stages={k: round(v, 4) for k, v in t["stages"].items()})
+                entry["tile_modes"] = modes_wl
+            del wl_inputs, wl_forward
             others[wl] = entry
             torch.cuda.empty_cache()
     # The roofline object is the projection forward kernel: HBM-bound, one
@@ -534,6 +596,7 @@ def main():
         "staged_ms": head["staged_ms"],
         "pairs": head["pairs"],
         "tile_modes": modes,
+        "sort_pairs": sort_pairs,
         "statistics": {"requests": "masked count + weighted sum, per-view maps",
                        "render_fwd_ms": round(kt["render_fwd_kernel"], 4),
                        "render_fwd_stats_ms": round(kt["render_fwd_stats_kernel"], 4)},

@@ -124,6 +124,7 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
         ranges, ids = launch_bin_rows(launch, group_pairs, count, early)
         bins = [ViewBins(0, cameras, ranges, ids)]
     else:
+        del early  # the per-group binning below allocates its own scratch
         bins = _bin_view_groups(state, width, height, tile_mode)
     profiling.mark("binned")
     return Frame(

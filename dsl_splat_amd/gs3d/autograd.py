@@ -13,6 +13,7 @@ sum to.  Gradients of means2d are the blend's centre gradients
 (screen_gradient_mode "projected_mean").
 """
 
+import os
 from dataclasses import dataclass
 from typing import Any
 
@@ -68,7 +69,12 @@ def _views(t, v0: int, v1: int, views: int, per_view_ndim: int):
 # One side stream per device clears the backward's accumulation buffers
 # (blend gradient record, colour and extra-channel gradients) while the
 # forward blend, which is bound by arithmetic, runs on the caller's stream.
+# The buffers then live from the forward to the backward: C*N*(6 or 8) + the
+# blended channels' C*N*D floats (0.43 GB at 3M Gaussians, 4 cameras, SH
+# colours).  GS3D_CLEAR_IN_BACKWARD=1 makes the backward allocate and clear
+# them instead, for callers bound by memory rather than time.
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+CLEAR_DURING_FORWARD = os.environ.get("GS3D_CLEAR_IN_BACKWARD", "0") != "1"
 
 
 @dataclass(slots=True)
@@ -134,7 +140,7 @@ class Rasterize(torch.autograd.Function):
         blended = st.colors if frame.sh_degree is not None else colors
         train = grad_enabled and any(ctx.needs_input_grad[:8])
         ctx.cleared = None
-        if train and len(frame.bins) == 1:
+        if train and len(frame.bins) == 1 and CLEAR_DURING_FORWARD:
             needs = ctx.needs_input_grad
             absgrad = absolute is not None and any(t is not None for t in absolute)
             views, n = st.centers.shape[0], st.centers.shape[1]

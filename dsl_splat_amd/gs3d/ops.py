@@ -113,22 +113,32 @@ class _Pixels(torch.autograd.Function):
                 None, None)
 
 
+# Per-Gaussian parameters of prepare_gaussians: (name, shape after N).  Their
+# validation order, exception types and messages are the reference's
+# (gs3d/ops.py:215-249), so a caller sees the same error first.
+_GAUSSIAN_PARAMETERS = (("means", (3,)), ("quats", (4,)), ("scales", (3,)), ("opacities", ()))
+
+
+def _leading_means(means) -> tuple[int, torch.device]:
+    """N and the device, fixed by the means."""
+    if isinstance(means, Tensor) and means.is_cuda and means.ndim == 2 and means.shape[1] == 3:
+        return len(means), means.device
+    raise ValueError("means must be CUDA float32 (N,3)")
+
+
 def prepare_gaussians(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tensor, camera: PinholeCamera, *,
                       radius_clip: float = 0.0, tile_mode: str = "radius") -> GaussianGeometry:
-    if not isinstance(means, Tensor) or not means.is_cuda or means.ndim != 2 or means.shape[1] != 3:
-        raise ValueError("means must be CUDA float32 (N,3)")
+    params = (means, quats, scales, opacities)
+    n, device = _leading_means(means)
     validate_tile_mode(tile_mode)
-    n, device = len(means), means.device
-    for name, value, shape in (("means", means, (n, 3)), ("quats", quats, (n, 4)), ("scales", scales, (n, 3)),
-                               ("opacities", opacities, (n,))):
-        check_tensor(name, value, device, shape)
-    view, full, intrinsics, config = prepare_camera(camera, radius_clip)
+    for (name, tail), value in zip(_GAUSSIAN_PARAMETERS, params):
+        check_tensor(name, value, device, (n, *tail))
+    view, full, intrinsics, camera_config = prepare_camera(camera, radius_clip)
     if view.device != device:
         raise ValueError("camera and Gaussians must use the same CUDA device")
-    config = replace(config, tile_mode=tile_mode)
-    centers, conics, radii, tiles, depths = _Project.apply(
-        means.contiguous(), quats.contiguous(), scales.contiguous(), opacities.contiguous(), view,
-        full, intrinsics, config, torch.is_grad_enabled())
+    config = replace(camera_config, tile_mode=tile_mode)
+    centers, conics, radii, tiles, depths = _Project.apply(*(t.contiguous() for t in params), view, full, intrinsics,
+                                                           config, torch.is_grad_enabled())
     return GaussianGeometry(centers, conics, radii, tiles, depths, config)
 
 
@@ -140,26 +150,35 @@ def bin_and_sort(geometry: GaussianGeometry) -> GaussianTiles:
     return GaussianTiles(bins["ranges"], bins["point_list"], geometry)
 
 
+def _pixel_rules(geometry: GaussianGeometry, tiles: GaussianTiles, features: Tensor, background: Tensor | None):
+    """rasterize_to_pixels' input checks as (violated?, exception) pairs, in
+    the reference's order (gs3d/ops.py:273-300): each is evaluated only once
+    the ones before it hold."""
+    n, device = len(geometry.radii), geometry.radii.device
+    yield (lambda: tiles._geometry is not geometry), ValueError("tiles must have been built from this geometry")
+    yield (lambda: check_tensor("features", features, device)), None
+    yield ((lambda: features.ndim != 2 or features.shape[0] != n or features.shape[1] <= 0),
+           ValueError("features must have shape (N,D), D>0"))
+    if background is not None:
+        yield (lambda: check_tensor("background", background, device, (features.shape[1],))), None
+        yield ((lambda: torch.is_grad_enabled() and background.requires_grad),
+               NotImplementedError("background gradients are not supported"))
+
+
 def rasterize_to_pixels(geometry: GaussianGeometry, tiles: GaussianTiles, features: Tensor,
                         background: Tensor | None = None, *,
                         statistics: Sequence[StatisticsRequest] = ()) -> PixelResult:
-    if tiles._geometry is not geometry:
-        raise ValueError("tiles must have been built from this geometry")
-    n, device = len(geometry.radii), geometry.radii.device
-    check_tensor("features", features, device)
-    if features.ndim != 2 or features.shape[0] != n or features.shape[1] <= 0:
-        raise ValueError("features must have shape (N,D), D>0")
-    channels = features.shape[1]
-    if background is not None:
-        check_tensor("background", background, device, (channels,))
-        if torch.is_grad_enabled() and background.requires_grad:
-            raise NotImplementedError("background gradients are not supported")
+    for violated, error in _pixel_rules(geometry, tiles, features, background):
+        # A rule without an exception raises its own (check_tensor).
+        if violated() and error is not None:
+            raise error
     config = geometry._config
-    prepared, outputs = (
-        prepare_statistics(statistics, batch_dims=(), batch_count=1, cameras=1, n=n, width=config.width,
-                           height=config.height, device=device)
-        if statistics else ([], {})
-    )
+    n = len(geometry.radii)
+    prepared, outputs = ([], {})
+    if statistics:
+        prepared, outputs = prepare_statistics(statistics, batch_dims=(), batch_count=1, cameras=1, n=n,
+                                               width=config.width, height=config.height,
+                                               device=geometry.radii.device)
     image, alpha = _Pixels.apply(geometry.centers, geometry.conics, features.contiguous(), geometry.radii,
                                  tiles.ranges, tiles.gaussian_ids, background, config,
                                  prepared[0] if statistics else None, torch.is_grad_enabled())

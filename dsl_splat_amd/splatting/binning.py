@@ -195,8 +195,9 @@ CAPACITY_HEADROOM = 1.125
 
 @dataclass(slots=True)
 class EarlyItems:
-    """Binning scratch holding the group items emitted with ``capacity``."""
-    scratch: Tensor
+    """Binning scratch holding the group items emitted with ``capacity``
+    (dropped, None, once a frame turns out to need more)."""
+    scratch: Tensor | None
     capacity: int
 
 
@@ -222,16 +223,21 @@ def emit_early(launch: BinLaunch) -> EarlyItems | None:
     return EarlyItems(scratch, capacity)
 
 
+# A stored capacity shrinks by this factor per frame towards the latest need,
+# so one unusually large frame does not oversize the early scratch of every
+# later frame of its shape.
+CAPACITY_DECAY = 0.9
+
+
 def _remember_capacity(launch: BinLaunch, group_pairs: int) -> None:
     if launch.args.tile_mode == abi.TILE_MODES["accutile"] or group_pairs <= 0:
         return
     key = _shape_key(launch)
     want = min(PAIR_LIMIT, int(group_pairs * CAPACITY_HEADROOM) + 1)
-    if _CAPACITY.get(key, 0) >= want:
-        return
-    if key not in _CAPACITY and len(_CAPACITY) >= _CAPACITY_SHAPES:
+    stored = _CAPACITY.get(key)
+    if stored is None and len(_CAPACITY) >= _CAPACITY_SHAPES:
         del _CAPACITY[next(iter(_CAPACITY))]
-    _CAPACITY[key] = want
+    _CAPACITY[key] = max(want, int(stored * CAPACITY_DECAY)) if stored else want
 
 
 @torch.no_grad()
@@ -248,6 +254,11 @@ def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int,
         native.call("gs3d_bin_emitted_rows", ctypes.byref(a), native.ptr(early.scratch), early.scratch.numel(),
                     native.stream(device))
     else:
+        if early is not None:
+            # Too small: release the early scratch before the full one is
+            # allocated (the allocator reuses it in stream order, after the
+            # early emission), so the two are never held together.
+            early.scratch = None
         scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, a.views, a.width, a.height,
                                         a.tile_mode), device)
         native.call("gs3d_bin_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))

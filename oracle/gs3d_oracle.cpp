@@ -1566,6 +1566,11 @@ static int render_fwd(const gs3d_render_args* a, const gs3d_render_stats_args* s
                     const float next_t = T * (1.0f - alpha);
                     if (next_t < 0.0001f) break;
                     gather_features(a, v, g, f.data());
+                    // gs3d/render.py:106-108 adds value * alpha * transmittance,
+                    // i.e. (v * alpha) * T; the kernels and this restatement
+                    // reassociate it as v * (alpha * T), one weight per pixel
+                    // shared by every channel (at most one rounding of the
+                    // product apart per term).
                     const float w = alpha * T;
                     for (int k = 0; k < D; ++k) color[k] = fmaf(f[k], w, color[k]);
                     if (st) observe(st, v, a->n, g, (int64_t)y * W + x, (int64_t)W * H, w);

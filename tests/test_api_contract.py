@@ -109,3 +109,33 @@ def test_pair_count_checks():
     assert binning.view_groups([1, 2, 3]) == [(0, 3)]
     with pytest.raises(OverflowError):
         binning.view_groups([1, limit + 1])
+
+
+def test_group_item_capacity_decays_after_a_large_frame():
+    # The early-emission capacity of a binning shape follows the latest frame
+    # with 12.5% headroom; after an unusually large frame it shrinks by 10% per
+    # frame instead of staying at the largest frame's size.
+    from types import SimpleNamespace
+
+    from dsl_splat_amd.splatting import binning
+
+    launch = SimpleNamespace(args=SimpleNamespace(tile_mode=0, n=10, views=1, width=16, height=16),
+                             ranges=torch.empty(0))
+    key = binning._shape_key(launch)
+    saved = dict(binning._CAPACITY)
+    binning._CAPACITY.clear()
+    try:
+        binning._remember_capacity(launch, 1000)
+        assert binning._CAPACITY[key] == 1126
+        binning._remember_capacity(launch, 100_000)
+        assert binning._CAPACITY[key] == 112_501
+        seen = []
+        for _ in range(60):
+            binning._remember_capacity(launch, 1000)
+            seen.append(binning._CAPACITY[key])
+        assert seen[0] == int(112_501 * 0.9)
+        assert all(b <= a for a, b in zip(seen, seen[1:]))
+        assert seen[-1] == 1126
+    finally:
+        binning._CAPACITY.clear()
+        binning._CAPACITY.update(saved)

@@ -334,3 +334,25 @@ def test_repeated_backward_and_interleaved_frames():
     leaves, sh = fresh()
     frame(leaves, sh, False)
     torch.cuda.synchronize()
+
+
+def test_clearing_in_backward_matches_clearing_during_forward(monkeypatch):
+    # With GS3D_CLEAR_IN_BACKWARD the blend VJP's accumulation buffers are
+    # allocated and zeroed by the backward instead of on a side stream during
+    # the forward: the same gradients (atomic order aside).
+    from dsl_splat_amd.gs3d import autograd
+
+    scene = synthetic.make_scene("sh3_1080p_4view", n=8000, width=288, height=240, seed=21).to(DEV)
+    print("clearing in backward vs during forward", flush=True)
+    grads = []
+    for during_forward in (True, False):
+        monkeypatch.setattr(autograd, "CLEAR_DURING_FORWARD", during_forward)
+        means = scene.means.clone().requires_grad_(True)
+        sh = scene.sh_coeffs.clone().requires_grad_(True)
+        res = gs3d.rasterize(means, scene.quats, scene.scales, scene.opacities, scene.viewmats, scene.Ks,
+                             scene.width, scene.height, sh_coeffs=sh, sh_degree=3, absgrad=True)
+        W = scene.loss_weights
+        ((res.features * W[..., :3]).sum() + (res.alpha * W[..., 3:]).sum()).backward()
+        grads.append((means.grad.cpu(), sh.grad.cpu(), res.meta["means2d"].absgrad.cpu()))
+    for a, b in zip(*grads):
+        torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-6)

@@ -67,6 +67,7 @@ def test_projection_bound_covers_float32_error(oracle_lib):
     view64 = np.zeros((4, 4))
     proj64 = np.zeros((4, 4))
     visible = 0
+    rel = {"means": [], "quats": [], "scales": []}
     for i in range(300):
         if out["radii"][0, i] <= 0:
             continue
@@ -79,8 +80,24 @@ def test_projection_bound_covers_float32_error(oracle_lib):
         for name, key in (("means", "mean"), ("quats", "quat"), ("scales", "scale")):
             err = np.abs(g32[name][i].astype(np.float64) - v[key])
             assert np.all(err <= bound[name][i]), (name, i, err, bound[name][i])
-            assert np.all(bound[name][i] <= 1e-2 * np.abs(v[key]).max() + 1e-30), (name, i)
+            live = np.abs(v[key]) > 0
+            rel[name] += list(_relative(bound[name][i][live], v[key][live]))
     assert visible > 100
+    # Not vacuous, per parameter (as for the blend): the mean gradients'
+    # bound has a median of ~2e-6 of the value and lies below 1e-4 for ~98%
+    # of the entries.  The quaternion and scale gradients come out of the
+    # covariance chain (Sigma -> M -> R -> q), whose differences of nearly
+    # equal products make the worst-case bound ~1000x the typical float32
+    # error (median ~2e-7 against bounds of ~1e-4 -- 3e-4); there a
+    # systematic relative error of 1e-3 still exceeds the bound for ~80% of
+    # the entries.  (Measured over seeds 1, 2, 3, 6: medians 1.8-1.9e-6,
+    # 2.5-2.8e-4 and 1.0-1.1e-4; shares below 1e-4 0.98, below 1e-3 0.81-0.84
+    # and 0.86-0.87.)
+    r = {k: np.array(v) for k, v in rel.items()}
+    assert np.median(r["means"]) < 1e-5 and np.mean(r["means"] < 1e-4) > 0.95
+    for name in ("quats", "scales"):
+        assert np.median(r[name]) < 5e-4, name
+        assert np.mean(r[name] < 1e-3) > 0.75, name
     # Camera gradients sum a few hundred per-Gaussian contributions that
     # largely cancel (each Gaussian's pull on the pose), so float32 moves
     # them by ~1e-3 of their largest entry and their bound is of that order.
