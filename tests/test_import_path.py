@@ -28,8 +28,21 @@ assert rasterization is dsl_splat_amd.gs3d.gsplat.rasterization
 assert PinholeCamera is dsl_splat_amd.cameras.PinholeCamera is dsl_splat.PinholeCamera
 assert MaskedContributionCount is dsl_splat_amd.statistics.MaskedContributionCount
 assert sort_tile_pairs is dsl_splat_amd.primitives.tiling.sort_tile_pairs
+import dsl_splat.gs3d.render, dsl_splat.gs3d.projection, dsl_splat.gs3d.binning, dsl_splat.gs3d.cameras
+import dsl_splat.gs3d.api, dsl_splat.gs3d.autograd
+import dsl_splat.splatting.binning, dsl_splat.splatting.cameras, dsl_splat.splatting.geometry
+import dsl_splat.runtime.gradients
+from dsl_splat.gs3d.binning import bin_and_sort as gs3d_bin_and_sort
+from dsl_splat.splatting.geometry import ProjectedGaussians
+from dsl_splat.runtime.gradients import AbsGradientTarget
+import dsl_splat_amd.gs3d.binning, dsl_splat_amd.splatting.geometry, dsl_splat_amd.runtime.gradients
+assert gs3d_bin_and_sort is dsl_splat_amd.gs3d.binning.bin_and_sort
+assert ProjectedGaussians is dsl_splat_amd.splatting.geometry.ProjectedGaussians
+assert AbsGradientTarget is dsl_splat_amd.runtime.gradients.AbsGradientTarget
 for name in ("gs3d.gsplat", "gs3d.ops", "cameras", "statistics", "training", "inputs", "primitives.tiling",
-             "primitives.spherical_harmonics"):
+             "primitives.spherical_harmonics", "gs3d.api", "gs3d.autograd", "gs3d.binning", "gs3d.cameras",
+             "gs3d.projection", "gs3d.render", "splatting.binning", "splatting.cameras", "splatting.geometry",
+             "runtime.gradients"):
     assert sys.modules["dsl_splat." + name] is sys.modules["dsl_splat_amd." + name], name
 print("ok")
 """
