@@ -154,6 +154,74 @@ __global__ __launch_bounds__(kScanThreads) void scan_down_kernel(const In* __res
     }
 }
 
+// Small scans in one workgroup: up to kSingleScanMax entries, tiles of
+// kSingleTile with a running carry.  One launch instead of two (three with
+// the radix sort's transpose, which it can write directly): at these sizes
+// every launch costs more than the work it does.  With rows > 0, `in` is a
+// [cols][rows] table (entry e = c * rows + r) and out[r * cols + c] receives
+// entry e's scan: the transposed layout the sort scatter reads.
+constexpr int kSingleThreads = 512;
+constexpr int kSingleItems = 16;
+constexpr int kSingleTile = kSingleThreads * kSingleItems;
+// Measured: at 1-2 tiles one launch of this kernel (4-5 us) replaces two or
+// three (3-5 us each); at 8 tiles it is slower than the grid-wide scan.
+constexpr int64_t kSingleScanMax = 2 * kSingleTile;
+
+template <class In, bool INCLUSIVE>
+__global__ __launch_bounds__(kSingleThreads) void scan_single_kernel(const In* __restrict__ in, int64_t n,
+                                                                     int32_t* __restrict__ out,
+                                                                     int64_t* __restrict__ total_out, int32_t rows,
+                                                                     int32_t cols) {
+    __shared__ int64_t s_wave[kSingleThreads / 64];
+    __shared__ int32_t s_tile[kSingleTile + kSingleTile / 16];
+    const int count = (int)n;  // n <= kSingleScanMax
+    int64_t carry = 0;
+    for (int base = 0; base < count; base += kSingleTile) {
+        int32_t raw[kSingleItems];
+#pragma unroll
+        for (int k = 0; k < kSingleItems; ++k) raw[k] = (int32_t)in[min(base + k * kSingleThreads + (int)threadIdx.x, count - 1)];
+#pragma unroll
+        for (int k = 0; k < kSingleItems; ++k) {
+            const int e = k * kSingleThreads + (int)threadIdx.x;
+            s_tile[scan_lds_index(e)] = base + e < count ? raw[k] : 0;
+        }
+        __syncthreads();
+        int32_t vals[kSingleItems];
+        int64_t sum = 0;
+#pragma unroll
+        for (int k = 0; k < kSingleItems; ++k) {
+            vals[k] = s_tile[scan_lds_index((int)threadIdx.x * kSingleItems + k)];
+            sum += vals[k];
+        }
+        int64_t tile_total;
+        int64_t run = block_exclusive_scan<kSingleThreads>(sum, s_wave, tile_total) + carry;
+#pragma unroll
+        for (int k = 0; k < kSingleItems; ++k) {
+            if (INCLUSIVE) run += vals[k];
+            s_tile[scan_lds_index((int)threadIdx.x * kSingleItems + k)] = (int32_t)run;
+            if (!INCLUSIVE) run += vals[k];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kSingleItems; ++k) {
+            const int e = k * kSingleThreads + (int)threadIdx.x;
+            const int idx = base + e;
+            if (idx < count) {
+                const int32_t v = s_tile[scan_lds_index(e)];
+                if (rows > 0) {
+                    const int c = idx / rows, r = idx - c * rows;
+                    out[(int64_t)r * cols + c] = v;
+                } else {
+                    out[idx] = v;
+                }
+            }
+        }
+        carry += tile_total;
+        __syncthreads();  // the next tile reuses s_tile
+    }
+    if (total_out && threadIdx.x == 0) *total_out = carry;
+}
+
 inline size_t scan_partials_bytes(int64_t n) {
     const int64_t tiles = (n + kScanTile - 1) / kScanTile;
     return (size_t)((tiles + 1) * sizeof(int64_t) + 255) & ~(size_t)255;
@@ -164,6 +232,11 @@ template <class In, bool INCLUSIVE>
 int run_scan(const In* in, int64_t n, int32_t* out, int64_t* total, void* scratch, hipStream_t stream) {
     const int64_t tiles = (n + kScanTile - 1) / kScanTile;
     if (tiles == 0) return GS3D_OK;  // callers handle empty inputs (total untouched)
+    if (n <= kSingleScanMax) {
+        hipLaunchKernelGGL((scan_single_kernel<In, INCLUSIVE>), dim3(1), dim3(kSingleThreads), 0, stream, in, n, out,
+                           total, 0, 0);
+        return launch_status("scan");
+    }
     int64_t* partials = reinterpret_cast<int64_t*>(scratch);
     hipLaunchKernelGGL((scan_reduce_kernel<In>), dim3((unsigned)((tiles + kReduceWaves - 1) / kReduceWaves)),
                        dim3(64 * kReduceWaves), 0, stream, in, n, tiles, partials);
@@ -715,6 +788,12 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
 // Scan and transpose of a pass's [digit][tile] counts (already in sc.counts).
 inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStream_t s, int64_t* total) {
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
+    if (tiles * digits <= kSingleScanMax) {
+        // Small table: scanned and written transposed by one workgroup.
+        hipLaunchKernelGGL((scan_single_kernel<uint32_t, false>), dim3(1), dim3(kSingleThreads), 0, s, sc.counts,
+                           tiles * digits, sc.offsets, total, (int32_t)tiles, (int32_t)digits);
+        return launch_status("radix sort counts");
+    }
     const int status = run_scan<uint32_t, false>(sc.counts, tiles * digits, sc.scanned, total, sc.scan_scratch, s);
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL(transpose_offsets_kernel, dim3((unsigned)((tiles + 31) / 32), digits / 32), dim3(256), 0, s,

@@ -131,7 +131,7 @@ def test_per_view_sh_projection():
     np.testing.assert_array_equal(_np(st.colors), ref["colors"])
 
 
-@pytest.mark.parametrize("n", [1, 1000, 4096, 4097, 300_001, 5_000_000])
+@pytest.mark.parametrize("n", [1, 1000, 4096, 4097, 12_000, 16_384, 16_385, 300_001, 5_000_000])
 def test_scan_bit_exact(n):
     _say(f"scan n={n}")
     g = torch.Generator().manual_seed(n)
