@@ -775,7 +775,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     // Gradient entry this lane adds after the wavefront sums (see
     // wave_sum_rows): entry k of Gaussian g lives at dst_base + g * dst_step.
     float* dst_base = nullptr;
-    int64_t dst_step = 0;
+    uint32_t dst_step = 0;  // row strides below 2^31 (checked on the host)
     float dst_scale = 1.0f;
     {
         const int k = wave_sum_rows_value(lane);
@@ -824,7 +824,10 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
             const int32_t g = next_id;
             if (p >= 0) {
                 s_id[e] = g;
-                stage_gaussian<CH, PIX>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
+                // Tile origin laundered (see stage_gaussian): 75 instead of
+                // 79 VGPRs, no spill with absolute gradients, 1.7% faster
+                // at 36 channels.
+                stage_gaussian<CH, PIX, true>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
             }
             if (top > B) next_id = a.ids[t.first + max(p - B, 0)];
         }
@@ -927,7 +930,10 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 float v = sums[0];
 #pragma unroll
                 for (int r = 1; r < R; ++r) v = (slot == r) ? sums[r] : v;
-                atomicAdd(dst_base + (int64_t)s_id[j] * dst_step, v * dst_scale);
+                // One 32 x 32 -> 64-bit multiply-add for the address (ids
+                // are non-negative, strides below 2^31): 1829 against 1865
+                // us for the 3M-Gaussian blend VJP.
+                atomicAdd(dst_base + (uint64_t)(uint32_t)s_id[j] * dst_step, v * dst_scale);
             }
           }
         }
@@ -1099,6 +1105,10 @@ extern "C" int gs3d_render_bwd(const gs3d_render_bwd_args* args, void* stream) {
     if (!a.final_t || !a.contributors || !b.grad_centers || !b.grad_conics) return GS3D_ERR_ARGUMENT;
     if (b.grad_centers_stride < 2 || b.grad_conics_stride < 4 || (b.abs_centers && b.abs_stride < 2))
         return GS3D_ERR_ARGUMENT;
+    // Gradient row strides feed 32-bit multipliers in the kernel.
+    for (int64_t stride : {b.grad_centers_stride, b.grad_conics_stride, b.abs_stride, b.grad_feat_stride,
+                           b.grad_extra_stride})
+        if (stride < 0 || stride > INT32_MAX) return GS3D_ERR_ARGUMENT;
     if ((b.upstream && b.upstream_stride < a.feat_channels) ||
         (b.upstream_extra && b.upstream_extra_stride < a.extra_channels) ||
         (b.upstream_alpha && b.upstream_alpha_stride < 1))

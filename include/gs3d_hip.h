@@ -430,7 +430,9 @@ int gs3d_render_fwd_stats(const gs3d_render_args* args, const gs3d_render_stats_
  * gradient pointer may be NULL except grad_centers/grad_conics.  The
  * upstream gradient arrives in the planes of the forward output, each with
  * its own pixel stride (floats between pixels, channels contiguous); a NULL
- * plane is a zero gradient.
+ * plane is a zero gradient.  The gradient row strides (grad_centers_stride,
+ * grad_conics_stride, abs_stride, grad_feat_stride, grad_extra_stride) must
+ * lie in [0, 2^31).
  * ---------------------------------------------------------------------- */
 typedef struct gs3d_render_bwd_args {
     gs3d_render_args fwd;        /* same inputs; image planes unused */

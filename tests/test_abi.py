@@ -84,6 +84,14 @@ def test_argument_errors_are_reported_without_launching():
     st.requests, st.sum_mask, st.sums = 2, 0b10, None
     assert lib.gs3d_render_fwd_stats(ctypes.byref(args), ctypes.byref(st), None) == abi.GS3D_ERR_ARGUMENT
     assert lib.gs3d_render_fwd_stats(ctypes.byref(args), None, None) == abi.GS3D_ERR_ARGUMENT
+    # The blend VJP's gradient row strides feed 32-bit multipliers: a stride
+    # of 2^31 or more is rejected before any launch.
+    bwd = abi.RenderBwdArgs()
+    bwd.fwd = args
+    bwd.fwd.final_t = bwd.fwd.contributors = ctypes.c_void_p(256)
+    bwd.grad_centers = bwd.grad_conics = ctypes.c_void_p(256)
+    bwd.grad_centers_stride, bwd.grad_conics_stride = 1 << 31, 4
+    assert lib.gs3d_render_bwd(ctypes.byref(bwd), None) == abi.GS3D_ERR_ARGUMENT
     # Zero-size work is a no-op.
     assert lib.gs3d_pair_tiles(None, 0, None, 0, None) == abi.GS3D_OK
     args = abi.BinArgs()
