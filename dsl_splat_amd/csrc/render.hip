@@ -209,11 +209,25 @@ GS3D_DEV uint32_t strip_mask(float2 xy, float4 con, float cut, int x0, int y0) {
     return m;
 }
 
+// One staged Gaussian in LDS: conic + opacity, centre, exponent cutoff and
+// the window's channels in one 16-byte-aligned record, so that the blend
+// loops read all of it from one LDS address (with immediate offsets) instead
+// of materialising one address per field from the scalar slot index.  The
+// strip masks stay in their own array: the wavefronts read them per lane.
+template <int CH>
+struct alignas(16) StagedRec {
+    float4 con;
+    float2 xy;
+    float cut;
+    float pad;
+    float f[CH];
+};
+
 // Stage one Gaussian's centre, conic, cutoff, strip mask and the channels
 // [c0, c0 + CH) of its channel vector (zero beyond D').
 template <int CH, int PIX, bool LAUNDER = false>
 GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32_t g, int slot, int c0,
-                             float2* s_xy, float4* s_con, float* s_cut, uint32_t* s_mask, float* s_feat) {
+                             StagedRec<CH>* s_g, uint32_t* s_mask) {
     const int view = t.view;
     const int64_t row = (int64_t)view * a.n + g;
     const float2 xy = reinterpret_cast<const float2*>(a.centers)[row];
@@ -237,10 +251,11 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32
             x = 1.0f;
         v[c] = x;
     }
-    s_xy[slot] = xy;
-    s_con[slot] = con;
+    StagedRec<CH>& rec = s_g[slot];
+    rec.con = con;
+    rec.xy = xy;
     const float cut = power_cutoff(con.w);
-    s_cut[slot] = cut;
+    rec.cut = cut;
     int x0 = t.x0, y0 = t.y0;
     if constexpr (LAUNDER) {
         // The tile origin passes through an opaque scalar move, so that the
@@ -250,9 +265,8 @@ GS3D_DEV void stage_gaussian(const gs3d_render_args& a, const TileInfo& t, int32
         asm volatile("" : "+s"(x0), "+s"(y0));
     }
     s_mask[slot] = strip_mask<PIX>(xy, con, cut, x0, y0);
-    float* dst = s_feat + slot * CH;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) dst[c] = v[c];
+    for (int c = 0; c < CH; ++c) rec.f[c] = v[c];
 }
 
 // 0.0f that the compiler cannot see through (a register written by an
@@ -283,14 +297,14 @@ struct Staged {
 };
 
 template <int CH>
-GS3D_DEV Staged<CH> load_staged(int j, const float2* s_xy, const float4* s_con, const float* s_cut,
-                                const float* s_feat) {
+GS3D_DEV Staged<CH> load_staged(int j, const StagedRec<CH>* s_g) {
+    const StagedRec<CH>& rec = s_g[j];
     Staged<CH> g;
-    g.xy = s_xy[j];
-    g.con = s_con[j];
-    g.cut = s_cut[j];
+    g.xy = rec.xy;
+    g.con = rec.con;
+    g.cut = rec.cut;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) g.f[c] = s_feat[j * CH + c];
+    for (int c = 0; c < CH; ++c) g.f[c] = rec.f[c];
     return g;
 }
 
@@ -412,11 +426,8 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     constexpr bool STATS = MODE == 1, COUNTS = MODE == 2;
     constexpr int NT = kTilePixels / PIX;
     constexpr int B = Batch<CH>::size;
-    __shared__ float2 s_xy[B];
-    __shared__ float4 s_con[B];
-    __shared__ float s_cut[B];
+    __shared__ StagedRec<CH> s_g[B];
     __shared__ uint32_t s_mask[B];
-    __shared__ float s_feat[B * CH];
     __shared__ int32_t s_id[STATS ? B : 1];
     const TileInfo t = tile_info(a);
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
@@ -479,7 +490,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
             if (begin + e < t.last) {
                 // The 4-channel plain blend fits its registers without the
                 // tile-origin laundering (and is fastest so).
-                stage_gaussian<CH, PIX, (STATS || CH > 4)>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
+                stage_gaussian<CH, PIX, (STATS || CH > 4)>(a, t, g, e, c0, s_g, s_mask);
                 if constexpr (STATS) s_id[e] = g;
             }
             if (begin + B < t.last) next_id = a.ids[min(begin + B + e, t.last - 1)];
@@ -565,13 +576,13 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                         break;
                     }
                     const int j = take();
-                    blend(load_staged<CH>(j, s_xy, s_con, s_cut, s_feat), j);
+                    blend(load_staged<CH>(j, s_g), j);
                 }
             } else {
                 // Unrolled by two: the next Gaussian is loaded into the other
                 // buffer before the current one is blended.
                 int ja = take(), jb = 0;
-                Staged<CH> ga = load_staged<CH>(ja, s_xy, s_con, s_cut, s_feat), gb;
+                Staged<CH> ga = load_staged<CH>(ja, s_g), gb;
                 while (true) {
                     if (!alive()) {
                         live = false;
@@ -580,7 +591,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                     bool more = todo != 0;
                     if (more) {
                         jb = take();
-                        gb = load_staged<CH>(jb, s_xy, s_con, s_cut, s_feat);
+                        gb = load_staged<CH>(jb, s_g);
                     }
                     blend(ga, ja);
                     if (!more) break;
@@ -591,7 +602,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                     more = todo != 0;
                     if (more) {
                         ja = take();
-                        ga = load_staged<CH>(ja, s_xy, s_con, s_cut, s_feat);
+                        ga = load_staged<CH>(ja, s_g);
                     }
                     blend(gb, jb);
                     if (!more) break;
@@ -682,12 +693,9 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     constexpr int NV = FB + CH;
     static_assert(NV <= 64, "one wavefront sum holds at most 64 gradient entries");
     constexpr int R = (NV + 3) / 4;
-    __shared__ float2 s_xy[B];
-    __shared__ float4 s_con[B];
-    __shared__ float s_cut[B];
+    __shared__ StagedRec<CH> s_g[B];
     __shared__ uint32_t s_mask[B];
     __shared__ int32_t s_id[B];
-    __shared__ float s_feat[B * CH];
     __shared__ int s_max_last;
     const gs3d_render_args& a = b.fwd;
     const TileInfo t = tile_info(a);
@@ -827,7 +835,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 // Tile origin laundered (see stage_gaussian): 75 instead of
                 // 79 VGPRs, no spill with absolute gradients, 1.7% faster
                 // at 36 channels.
-                stage_gaussian<CH, PIX, true>(a, t, g, e, c0, s_xy, s_con, s_cut, s_mask, s_feat);
+                stage_gaussian<CH, PIX, true>(a, t, g, e, c0, s_g, s_mask);
             }
             if (top > B) next_id = a.ids[t.first + max(p - B, 0)];
         }
@@ -844,10 +852,10 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
             const int pos = top - 1 - j;
             // Pixels outside the image have last contributor 0.
             if (__ballot(pos < lane_last) == 0) continue;
-            const float2 xy = s_xy[j];
-            const float4 con = s_con[j];
-            const float cut = s_cut[j];
-            const float* f = s_feat + j * CH;
+            const float2 xy = s_g[j].xy;
+            const float4 con = s_g[j].con;
+            const float cut = s_g[j].cut;
+            const float* f = s_g[j].f;
             // Accumulators start from an opaque zero: a literal zero would be
             // folded into each accumulator's first FMA, and every path that
             // skips a pixel would then re-materialise the zeros.  vals holds,
