@@ -595,10 +595,11 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                     }
                     blend(ga, ja);
                     if (!more) break;
-                    if (!alive()) {
-                        live = false;
-                        break;
-                    }
+                    // Liveness is checked once per two Gaussians: a Gaussian
+                    // blended after every pixel is done changes nothing (no
+                    // pixel accepts it), and the check costs VALU and scalar
+                    // work on every Gaussian (1091 -> 1067 us for the
+                    // 3M-Gaussian forward blend).
                     more = todo != 0;
                     if (more) {
                         ja = take();

@@ -274,6 +274,31 @@ def test_render_backward_parity(key, degree, absgrad):
 
 
 @pytest.mark.parametrize("key", ["small_rgb", "wide_rgb"])
+def test_render_forward_non_finite_features(key):
+    # The forward blend adds a rejected Gaussian's channels with a zero weight
+    # only when they are all finite; a Gaussian with a NaN or infinite channel
+    # is skipped by a select, as the reference's loop skips it.  The image
+    # equals the oracle's bit for bit, NaN and inf included.
+    scene = _scene(key)
+    _say(f"render fwd non-finite features {key}")
+    quats, full, inverse, centers, st, bins = _frame(scene, None)
+    visible = torch.nonzero(st.radii[0] > 0).flatten()
+    feats = scene.features.clone()
+    feats[visible[:3], 0] = float("nan")
+    feats[visible[3:5], 2] = float("inf")
+    feats[visible[5:7], 1] = -float("inf")
+    out = grender.render_views(bins["ranges"], bins["point_list"], st.centers, st.conics, feats, scene.width,
+                               scene.height)
+    img, ft, ct = oracle.render_fwd(scene.width, scene.height, _np(bins["ranges"]), _np(bins["point_list"]),
+                                    _np(st.centers), _np(st.conics), _np(feats))
+    got = _np(out.stacked())
+    assert not np.isfinite(img).all()
+    np.testing.assert_array_equal(got, img)
+    np.testing.assert_array_equal(_np(out.contributors), ct)
+    np.testing.assert_array_equal(_np(out.transmittance), ft)
+
+
+@pytest.mark.parametrize("key", ["small_rgb", "wide_rgb"])
 def test_render_backward_non_finite_inputs(key):
     # The backward's fast traversal adds a rejected pixel's terms with zero
     # weights; whenever an operand may be non-finite it must skip them as the
