@@ -184,7 +184,9 @@ def frame_info(scene):
         st = gproj.project_views(scene.means, scene.quats, scene.scales, scene.opacities, scene.viewmats, full,
                                  scene.Ks, scene.width, scene.height, 0.2, math.inf, 0.0, sh=sh, sh_degree=deg or 0,
                                  camera_centers=centers if deg else None, metadata=True, normalize_quats=True)
-        order, offsets, totals = binning.order_rows(st.centers, st.radii, st.depths, scene.width, scene.height)
+        key_bits = torch.zeros(1, dtype=torch.int32, device=st.radii.device)
+        order, offsets, totals = binning.order_rows(st.centers, st.radii, st.depths, scene.width, scene.height,
+                                                    key_bits_out=key_bits)
         group_pairs, count = totals.cpu().tolist()
         ranges, ids = binning.bin_rows(st.centers, st.radii, order, offsets, group_pairs, count, scene.width,
                                        scene.height)
@@ -196,7 +198,10 @@ def frame_info(scene):
     groups = views * (((scene.width + 15) // 16 + 7) // 8) * (((scene.height + 15) // 16 + 7) // 8)
     info = dict(pairs=count, group_pairs=group_pairs, groups=groups, tiles=tiles,
                 group_passes=1 if groups <= 1024 else math.ceil(int(groups - 1).bit_length() / 8),
-                rows=views * n, visible=int((st.radii > 0).sum()), blend_pairs=pairs)
+                rows=views * n, visible=int((st.radii > 0).sum()), blend_pairs=pairs,
+                # radix passes of the depth order in the timed steps (they sort
+                # the key bits the frame's kept rows need)
+                order_passes=binning.order_pass_count(max(9, int(key_bits.item()))))
     return info, dict(full=full, st=st, ranges=ranges, ids=ids, feats=feats)
 
 
@@ -214,10 +219,11 @@ def stage_bytes(scene, info):
         "project": n * 44 + sh_in + views * n * (60 + (12 if sh is not None else 0)),
         # keys and records (depth 4 + centre 8 + radius 4 in, key 4 + record 8 out); the first radix
         # pass reads every row's key for its histogram (4) and (key, record) (12) and writes the V
-        # rows that touch a tile (12); three more passes over those V rows (key 4 for the histogram,
-        # (key, record) 12 in and 12 out); group counts at the sorted positions (4) and filler
-        # records + zero counts after them ((R - V) x 12); inclusive scan of the counts (4 in, 4 out)
-        "order": R * (28 + 4 + 12 + 8) + V * (12 + 3 * 28 + 4) + (R - V) * 12,
+        # rows that touch a tile (12); the later passes (two or three, by the key bits the kept rows
+        # need) over those V rows (key 4 for the histogram, (key, record) 12 in and 12 out); group
+        # counts at the sorted positions (4) and filler records + zero counts after them
+        # ((R - V) x 12); inclusive scan of the counts (4 in, 4 out)
+        "order": R * (28 + 4 + 12 + 8) + V * (12 + (info["order_passes"] - 1) * 28 + 4) + (R - V) * 12,
         # items: records and offsets in (12 B/row), items out (8 B/item); group sort (keys read for the
         # histogram 8 + read and written 16 per pass; one 10-bit pass up to 1024 groups, whose digit
         # scan gives the group ranges, else 8-bit passes and a range search, 8 B/item); count and

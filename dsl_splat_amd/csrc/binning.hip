@@ -423,6 +423,10 @@ struct Culled {
     const int64_t* live;  // null: every key of [0, count) is sorted
     bool fill;
     uint64_t filler;
+    // Optional: digits are taken from key - *key_base (every key sorted is at
+    // least *key_base, so the order is unchanged and the difference may need
+    // fewer bits than the key).
+    const uint32_t* key_base = nullptr;
 };
 
 // VALS = false sorts keys alone: no value loads, stores or LDS staging, which
@@ -447,6 +451,8 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const int64_t tile = GS3D_SORT_XCD ? xcd_contiguous(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
     const int64_t tile_base = tile * kSortTile;
     const int64_t live = cull.live ? min(count, *cull.live) : count;
+    const K key_base = cull.key_base ? (K)*cull.key_base : K(0);
+    auto digit = [&](K k) { return digit_of((K)(k - key_base), shift, mask); };
     K key[kSortItems];
     V val[kSortItems];
     uint32_t rank[kSortItems];
@@ -479,7 +485,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     for (int k = 0; k < kSortItems; ++k) {
         rank[k] = 0;
         if (in[k]) {
-            const uint32_t d = digit_of(key[k], shift, mask);
+            const uint32_t d = digit(key[k]);
             uint64_t peers = __ballot(1);
             for (int b = 0; b < bits; ++b) {
                 const bool set = (d >> b) & 1u;
@@ -525,7 +531,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
 #pragma unroll
     for (int k = 0; k < kSortItems; ++k) {
         if (in[k]) {
-            const uint32_t d = digit_of(key[k], shift, mask);
+            const uint32_t d = digit(key[k]);
             const uint32_t pos = s_wcnt[wave][d] + rank[k];
             s_keys[pos] = key[k];
             if (VALS) s_vals[pos] = val[k];
@@ -538,7 +544,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
         const int p = j * kSortThreads + threadIdx.x;
         if (p < (int)block_total) {
             const K kk = s_keys[p];
-            const int64_t dst = (int64_t)s_gbase[digit_of(kk, shift, mask)] + p;
+            const int64_t dst = (int64_t)s_gbase[digit(kk)] + p;
             keys_out[dst] = kk;  // plain stores: digit runs start mid-line and the L2 merges them
             if (VALS) vals_out[dst] = s_vals[p];
             if constexpr (TAIL != 0) {
@@ -623,7 +629,8 @@ __global__ __launch_bounds__(256) void transpose_offsets_kernel(const int32_t* _
 // every key's digit below `digits`, a multiple of 32 up to 1 << RB).
 template <class K, int RB, bool DROP = false>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
-                hipStream_t s, const int64_t* live = nullptr, int64_t* total = nullptr);
+                hipStream_t s, const int64_t* live = nullptr, int64_t* total = nullptr,
+                const uint32_t* key_base = nullptr);
 inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStream_t s, int64_t* total);
 
 // tail_kind (1 or 2, 64-bit values only): the last pass also writes the
@@ -682,44 +689,102 @@ int run_sort(K* keys, V* values, int64_t count, int end_bit, void* scratch, hipS
     return launch_status("radix sort");
 }
 
+// Passes of a depth order over key bits [0, end_bit), 9 <= end_bit <= 32:
+// bits 0-7 first (the records kernel counts them), then 8-bit passes, the
+// last one widened to up to 10 bits, so 25 or 26 key bits take three passes
+// instead of four.  Returns the number of passes (2 to 4).
+inline int order_passes(int end_bit, int (&shift)[4], int (&width)[4]) {
+    int passes = 0, at = 0, rest = end_bit;
+    shift[passes] = at;
+    width[passes++] = 8;
+    at += 8;
+    rest -= 8;
+    while (rest > 10) {
+        shift[passes] = at;
+        width[passes++] = 8;
+        at += 8;
+        rest -= 8;
+    }
+    shift[passes] = at;
+    width[passes++] = rest;
+    return passes;
+}
+
+// Radix bits of the order's count tables (its widest pass).
+constexpr int kOrderRadixBits = 10;
+
 // The depth order of the rows that touch a tile group: 32-bit keys with
-// kDroppedKey for the others, 64-bit records, four 8-bit passes.  The first
-// pass leaves the dropped rows out and its digit scan counts the rest into
-// *live; the later passes sort [0, *live), and the last one writes `filler`
-// records (and, with a tail, zero group counts) to [*live, count).  The
-// result is in the first halves, as with run_sort.
+// kDroppedKey for the others, 64-bit records, the passes of order_passes
+// over bits [0, end_bit), the later ones of key - *key_base (key_base_kernel;
+// null: of the key; every kept key minus the base must be below 2^end_bit).
+// The first pass leaves the dropped rows out and its digit scan counts the rest
+// into *live; the later passes sort [0, *live), and the last one writes
+// `filler` records (and, with a tail, zero group counts) to [*live, count).
+// The input is in the halves [start_half * count, ...) of keys and values,
+// the half that leaves the result in the first halves after the passes:
+// start_half = passes & 1.  Scratch: sort_scratch_bytes(count, ...,
+// kOrderRadixBits).  tail_kind 0 or 1.
 inline int run_order_sort(uint32_t* keys, uint64_t* values, int64_t count, void* scratch, int64_t* live,
-                          uint64_t filler, hipStream_t s, int tail_kind, OrderTail tail, bool first_counted) {
+                          uint64_t filler, hipStream_t s, int tail_kind, OrderTail tail, bool first_counted,
+                          int end_bit, int start_half, const uint32_t* key_base) {
     SortScratch sc;
-    sort_scratch_bytes(count, &sc, scratch);
+    sort_scratch_bytes(count, &sc, scratch, kOrderRadixBits);
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
-    uint32_t* kin = keys;
-    uint64_t* vin = values;
-    uint32_t* kout = keys + count;
-    uint64_t* vout = values + count;
+    int shifts[4], widths[4];
+    const int passes = order_passes(end_bit, shifts, widths);
+    if (((passes + start_half) & 1) || tail_kind < 0 || tail_kind > 1) {
+        set_error("depth order: input half or tail kind does not fit the passes");
+        return GS3D_ERR_ARGUMENT;
+    }
+    uint32_t* kin = keys + start_half * count;
+    uint64_t* vin = values + start_half * count;
+    uint32_t* kout = keys + (1 - start_half) * count;
+    uint64_t* vout = values + (1 - start_half) * count;
     const dim3 grid((unsigned)tiles), block(kSortThreads);
-    for (int shift = 0; shift < 32; shift += 8) {
-        const bool first = shift == 0, last = shift == 24;
-        const int status = first ? (first_counted ? scan_counts(count, 256, sc, s, live)
-                                                  : sort_counts<uint32_t, 8, true>(kin, count, shift, 255u, 256, sc, s,
-                                                                                   nullptr, live))
-                                 : sort_counts<uint32_t, 8, false>(kin, count, shift, 255u, 256, sc, s, live, nullptr);
+    for (int p = 0; p < passes; ++p) {
+        const bool first = p == 0, last = p == passes - 1;
+        const int shift = shifts[p], bits = widths[p];
+        const uint32_t mask = (1u << bits) - 1u;
+        const bool wide = bits > 8;
+        const int digits = wide ? 1 << bits : 256;
+        int status;
+        if (first)
+            status = first_counted ? scan_counts(count, 256, sc, s, live)
+                                   : sort_counts<uint32_t, 8, true>(kin, count, shift, mask, 256, sc, s, nullptr, live);
+        else if (wide && bits == 9)
+            status = sort_counts<uint32_t, 9, false>(kin, count, shift, mask, digits, sc, s, live, nullptr, key_base);
+        else if (wide)
+            status = sort_counts<uint32_t, 10, false>(kin, count, shift, mask, digits, sc, s, live, nullptr, key_base);
+        else
+            status = sort_counts<uint32_t, 8, false>(kin, count, shift, mask, 256, sc, s, live, nullptr, key_base);
         if (status != GS3D_OK) return status;
         if (first) {
             hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 8, 0, true>), grid, block, 0, s, kin, vin,
-                               kout, vout, count, shift, 255u, 8, sc.offsets, tiles, 256, OrderTail{},
+                               kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, OrderTail{},
                                Culled{nullptr, false, 0});
         } else {
-            const Culled cull{live, last, filler};
-            if (last && tail_kind == 1)
+            const Culled cull{live, last, filler, key_base};
+            const OrderTail t = last && tail_kind != 0 ? tail : OrderTail{};
+            // Wide passes are compiled for their digit width (9 or 10 bits):
+            // LDS counters and per-thread digit loops sized for it.
+            if (wide && bits == 9 && last && tail_kind == 1)
+                hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 9, 1>), grid, block, 0, s, kin, vin,
+                                   kout, vout, count, shift, mask, bits, sc.offsets, tiles, digits, t, cull);
+            else if (wide && bits == 9)
+                hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 9, 0>), grid, block, 0, s, kin, vin,
+                                   kout, vout, count, shift, mask, bits, sc.offsets, tiles, digits, t, cull);
+            else if (wide && last && tail_kind == 1)
+                hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 10, 1>), grid, block, 0, s, kin, vin,
+                                   kout, vout, count, shift, mask, bits, sc.offsets, tiles, digits, t, cull);
+            else if (wide)
+                hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 10, 0>), grid, block, 0, s, kin, vin,
+                                   kout, vout, count, shift, mask, bits, sc.offsets, tiles, digits, t, cull);
+            else if (last && tail_kind == 1)
                 hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 8, 1>), grid, block, 0, s, kin, vin,
-                                   kout, vout, count, shift, 255u, 8, sc.offsets, tiles, 256, tail, cull);
-            else if (last && tail_kind == 2)
-                hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 8, 2>), grid, block, 0, s, kin, vin,
-                                   kout, vout, count, shift, 255u, 8, sc.offsets, tiles, 256, tail, cull);
+                                   kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, t, cull);
             else
                 hipLaunchKernelGGL((sort_scatter_kernel<uint32_t, uint64_t, true, 8, 0>), grid, block, 0, s, kin, vin,
-                                   kout, vout, count, shift, 255u, 8, sc.offsets, tiles, 256, OrderTail{}, cull);
+                                   kout, vout, count, shift, mask, bits, sc.offsets, tiles, 256, t, cull);
         }
         std::swap(kin, kout);
         std::swap(vin, vout);
@@ -738,8 +803,10 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
                                                                             int shift, uint32_t mask,
                                                                             uint32_t* __restrict__ counts,
                                                                             int64_t tiles, int digits,
-                                                                            const int64_t* __restrict__ live_count) {
+                                                                            const int64_t* __restrict__ live_count,
+                                                                            const uint32_t* __restrict__ key_base) {
     constexpr int R = 1 << RB, P = R + 1;
+    const K base_key = key_base ? (K)*key_base : K(0);
     __shared__ uint32_t s_hist[TPB * P];
     for (int e = threadIdx.x; e < TPB * P; e += kSortThreads) s_hist[e] = 0;
     __syncthreads();
@@ -764,7 +831,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
         for (int k = 0; k < kSortItems; ++k) {
             const int64_t idx = base + k * kSortThreads + threadIdx.x;
             const bool valid = idx < live && !(DROP && key[k] == (K)kDroppedKey);
-            const uint32_t d = digit_of(key[k], shift, mask);
+            const uint32_t d = digit_of((K)(key[k] - base_key), shift, mask);
             // A wavefront whose valid keys share one digit (high key bits:
             // exponents, view ids) adds them with one atomic instead of 64
             // serialised ones on the same LDS word.
@@ -804,13 +871,13 @@ inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStre
 // total (optional) receives the number of keys counted.
 template <class K, int RB, bool DROP>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
-                hipStream_t s, const int64_t* live, int64_t* total) {
+                hipStream_t s, const int64_t* live, int64_t* total, const uint32_t* key_base) {
     // Tiles per histogram block: runs of 16 words (whole 64-byte sectors) for
     // 8-bit digits; 8 for 10-bit digits, whose LDS histograms are 4x larger.
     constexpr int TPB = RB > 8 ? 8 : GS3D_HIST_TILES8;
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
     hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB, DROP>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
-                       dim3(kSortThreads), 0, s, keys, count, shift, mask, sc.counts, tiles, digits, live);
+                       dim3(kSortThreads), 0, s, keys, count, shift, mask, sc.counts, tiles, digits, live, key_base);
     return scan_counts(count, digits, sc, s, total);
 }
 
@@ -1083,15 +1150,23 @@ __global__ void row_records_kernel(const float* __restrict__ depths, RowGeometry
 // out); record high halves as in the packed layout above.  One 2048-row sort
 // tile per block, which also counts the tile's keys by bits 0-7 for the depth
 // order's first pass (dropped rows not counted): the [digit][tile] table that
-// pass's histogram would form, without reading the keys again.  Every load of
-// a thread's eight rows is issued first (clamped to the last row).
+// pass's histogram would form, without reading the keys again; and writes the
+// smallest and largest kept key of the tile to block_range[2 * tile + {0, 1}]
+// (0xFFFFFFFF, 0 when it keeps none).  Every load of a thread's eight rows is
+// issued first (clamped to the last row).
 template <bool PACKED>
 __global__ __launch_bounds__(kSortThreads) void row_records_counted_kernel(
     const float* __restrict__ depths, RowGeometry g, int64_t rows, int gx, int gy, uint32_t* __restrict__ keys,
-    uint64_t* __restrict__ records, int32_t* __restrict__ tiles_out, uint32_t* __restrict__ counts, int64_t tiles) {
+    uint64_t* __restrict__ records, int32_t* __restrict__ tiles_out, uint32_t* __restrict__ counts, int64_t tiles,
+    uint32_t* __restrict__ block_range) {
     static_assert(kSortThreads == kRadix, "one digit per thread");
     __shared__ uint32_t s_hist[kRadix];
+    __shared__ uint32_t s_range[2];
     s_hist[threadIdx.x] = 0u;
+    if (threadIdx.x == 0) {
+        s_range[0] = 0xFFFFFFFFu;
+        s_range[1] = 0u;
+    }
     const int64_t tile = xcd_contiguous(blockIdx.x, gridDim.x);
     const int64_t base = tile * kSortTile + threadIdx.x;
     float dep[kSortItems];
@@ -1108,6 +1183,7 @@ __global__ __launch_bounds__(kSortThreads) void row_records_counted_kernel(
                                             : reinterpret_cast<const float4*>(g.conics)[i];
     }
     __syncthreads();
+    uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
 #pragma unroll
     for (int k = 0; k < kSortItems; ++k) {
         const int64_t i = base + k * kSortThreads;
@@ -1124,10 +1200,27 @@ __global__ __launch_bounds__(kSortThreads) void row_records_counted_kernel(
         const uint32_t key = r.x1 > r.x0 ? __float_as_uint(dep[k]) : kDroppedKey;
         keys[i] = key;
         records[i] = rec;
-        if (key != kDroppedKey) atomicAdd(&s_hist[key & 255u], 1u);
+        if (key != kDroppedKey) {
+            atomicAdd(&s_hist[key & 255u], 1u);
+            kmin = min(kmin, key);
+            kmax = max(kmax, key);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o));
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+    }
+    if (lane_id() == 0) {
+        atomicMin(&s_range[0], kmin);
+        atomicMax(&s_range[1], kmax);
     }
     __syncthreads();
     counts[(int64_t)threadIdx.x * tiles + tile] = s_hist[threadIdx.x];
+    if (threadIdx.x == 0) {
+        block_range[2 * tile] = s_range[0];
+        block_range[2 * tile + 1] = s_range[1];
+    }
 }
 
 // Group count of every row in depth order; the block's tile pair count goes
@@ -1190,6 +1283,51 @@ __global__ __launch_bounds__(1024) void sum_i64_kernel(const int64_t* __restrict
     int64_t total;
     block_exclusive_scan<1024>(v, s_wave, total);
     if (threadIdx.x == 0) *out = total;
+}
+
+// Base of the depth order's later passes (one block): the smallest kept key
+// of all sort tiles (block_range pairs from row_records_counted_kernel) with
+// its low byte cleared.  Those passes take their digits from key - *base,
+// whose low byte is the key's own, so the first pass (counted on raw low
+// bytes) and the later ones sort the same numbers, and the differences may
+// need fewer bits than the keys (depths on both sides of a power of two).
+// key_bits (optional) receives the bits the largest difference needs, 0
+// without kept keys; without block_range (orders that sort raw 32-bit keys)
+// it receives 32 and *base is left alone.
+__global__ __launch_bounds__(1024) void key_base_kernel(const uint32_t* __restrict__ block_range, int64_t ranges,
+                                                        uint32_t* __restrict__ base, int32_t* __restrict__ key_bits) {
+    __shared__ uint32_t s_range[2];
+    if (!block_range) {
+        if (key_bits && threadIdx.x == 0) *key_bits = 32;
+        return;
+    }
+    if (threadIdx.x == 0) {
+        s_range[0] = 0xFFFFFFFFu;
+        s_range[1] = 0u;
+    }
+    __syncthreads();
+    uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+    for (int64_t i = threadIdx.x; i < ranges; i += 1024) {
+        kmin = min(kmin, block_range[2 * i]);
+        kmax = max(kmax, block_range[2 * i + 1]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o));
+        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+    }
+    if (lane_id() == 0) {
+        atomicMin(&s_range[0], kmin);
+        atomicMax(&s_range[1], kmax);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t lo = s_range[0], hi = s_range[1];
+        const bool any = lo <= hi;
+        const uint32_t b = any ? lo & ~255u : 0u;
+        *base = b;
+        if (key_bits) *key_bits = any ? 32 - __clz((int)(hi - b)) : 0;
+    }
 }
 
 // One block per 256 ordered rows; the block's items form one contiguous
@@ -1816,17 +1954,21 @@ struct OrderScratch {
     int32_t* counts;      // rows group counts
     int64_t* pairs;       // per-block tile pair counts
     int64_t* live;        // rows that the depth order keeps (outside AccuTile)
+    uint32_t* range;      // per sort tile: smallest and largest kept key
+    uint32_t* base;       // key base of the passes after the first (key_base_kernel)
     void* sort;
     void* scan;
 };
 
 inline size_t order_scratch_bytes(int64_t rows, OrderScratch* out, void* base) {
     const int64_t blocks = (rows + kBinThreads - 1) / kBinThreads;
+    const int64_t sort_tiles = (rows + kSortTile - 1) / kSortTile;
     const size_t a = align256((size_t)rows * 2 * sizeof(uint32_t));
     const size_t b = align256((size_t)rows * sizeof(int32_t));
     const size_t c = align256((size_t)blocks * sizeof(int64_t));
     const size_t l = align256(sizeof(int64_t));
-    const size_t e = align256(sort_scratch_bytes(rows, nullptr, nullptr));
+    const size_t r = align256((size_t)sort_tiles * 2 * sizeof(uint32_t));
+    const size_t e = align256(sort_scratch_bytes(rows, nullptr, nullptr, kOrderRadixBits));
     const size_t f = scan_partials_bytes(rows);
     if (out) {
         char* p = reinterpret_cast<char*>(base);
@@ -1834,10 +1976,12 @@ inline size_t order_scratch_bytes(int64_t rows, OrderScratch* out, void* base) {
         out->counts = reinterpret_cast<int32_t*>(p + a);
         out->pairs = reinterpret_cast<int64_t*>(p + a + b);
         out->live = reinterpret_cast<int64_t*>(p + a + b + c);
-        out->sort = p + a + b + c + l;
-        out->scan = p + a + b + c + l + e;
+        out->range = reinterpret_cast<uint32_t*>(p + a + b + c + l);
+        out->base = reinterpret_cast<uint32_t*>(p + a + b + c + l + r);
+        out->sort = p + a + b + c + l + r + l;
+        out->scan = p + a + b + c + l + r + l + e;
     }
-    return a + b + c + l + e + f;
+    return a + b + c + l + r + l + e + f;
 }
 
 // Scratch of gs3d_bin_rows.
@@ -2072,8 +2216,10 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0 || !a.totals) return GS3D_ERR_ARGUMENT;
     const int64_t rows = (int64_t)a.n * a.views;
     hipStream_t s = gs3d::as_stream(stream);
+    if (a.sort_bits < 0 || a.sort_bits > 32) return GS3D_ERR_ARGUMENT;
     if (rows == 0) {
         gs3d::fill_u32(reinterpret_cast<uint32_t*>(a.totals), 4, 0u, s);
+        if (a.key_bits_out) gs3d::fill_u32(reinterpret_cast<uint32_t*>(a.key_bits_out), 1, 0u, s);
         return gs3d::launch_status("gs3d_order_rows");
     }
     if (rows > INT32_MAX) return GS3D_ERR_OVERFLOW;
@@ -2089,6 +2235,12 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     const gs3d::RowGeometry geo{a.centers, a.conics, a.radii, a.tile_mode};
     const bool accu = a.tile_mode == GS3D_TILE_ACCUTILE;
     const bool packed = d.gx <= 256 && d.gy <= 256;
+    // Key bits the depth order sorts (at least 9: its first two passes).
+    const int end_bit = a.sort_bits == 0 ? 32 : (a.sort_bits < 9 ? 9 : a.sort_bits);
+    int shifts[4], widths[4];
+    // The records are written to the half that leaves the sorted result in
+    // the first half of keys and order after the passes.
+    const int start_half = accu ? 0 : gs3d::order_passes(end_bit, shifts, widths) & 1;
     if (accu && (!a.footprints || (reinterpret_cast<uintptr_t>(a.footprints) & 15))) return GS3D_ERR_ARGUMENT;
     float4* fp = reinterpret_cast<float4*>(a.footprints);
     const dim3 grid(gs3d::blocks_for(rows, 256)), block(256);
@@ -2102,17 +2254,24 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
         // Outside AccuTile the records kernel also forms the depth order's
         // first digit counts.
         gs3d::SortScratch ss;
-        gs3d::sort_scratch_bytes(rows, &ss, sc.sort);
+        gs3d::sort_scratch_bytes(rows, &ss, sc.sort, gs3d::kOrderRadixBits);
         const int64_t tiles = (rows + gs3d::kSortTile - 1) / gs3d::kSortTile;
+        uint32_t* keys_in = sc.keys + start_half * rows;
+        uint64_t* records_in = a.order + start_half * rows;
         if (packed)
             hipLaunchKernelGGL((gs3d::row_records_counted_kernel<true>), dim3((unsigned)tiles),
-                               dim3(gs3d::kSortThreads), 0, s, a.depths, geo, rows, d.gx, d.gy, sc.keys, a.order,
-                               a.tiles_out, ss.counts, tiles);
+                               dim3(gs3d::kSortThreads), 0, s, a.depths, geo, rows, d.gx, d.gy, keys_in, records_in,
+                               a.tiles_out, ss.counts, tiles, sc.range);
         else
             hipLaunchKernelGGL((gs3d::row_records_counted_kernel<false>), dim3((unsigned)tiles),
-                               dim3(gs3d::kSortThreads), 0, s, a.depths, geo, rows, d.gx, d.gy, sc.keys, a.order,
-                               a.tiles_out, ss.counts, tiles);
+                               dim3(gs3d::kSortThreads), 0, s, a.depths, geo, rows, d.gx, d.gy, keys_in, records_in,
+                               a.tiles_out, ss.counts, tiles, sc.range);
+        hipLaunchKernelGGL(gs3d::key_base_kernel, dim3(1), dim3(1024), 0, s, sc.range, tiles, sc.base,
+                           a.key_bits_out);
     }
+    if (accu && a.key_bits_out)
+        hipLaunchKernelGGL(gs3d::key_base_kernel, dim3(1), dim3(1024), 0, s, (const uint32_t*)nullptr, (int64_t)0,
+                           sc.base, a.key_bits_out);
     // order holds 2*rows records: [0, rows) sorted result, [rows, 2rows) ping-pong.  With packed
     // records the last pass also writes each row's group count at its sorted position and the
     // blocks' tile-pair sums; otherwise order_counts_kernel computes them from the geometry.
@@ -2126,7 +2285,7 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     else
         status = gs3d::run_order_sort(sc.keys, a.order, rows, sc.sort, sc.live,
                                       packed ? (uint64_t)gs3d::kEmptyRect << 32 : 0u, s, tail_kind,
-                                      gs3d::OrderTail{sc.counts, sc.pairs}, true);
+                                      gs3d::OrderTail{sc.counts, sc.pairs}, true, end_bit, start_half, sc.base);
     if (status != GS3D_OK) return status;
     int64_t pair_blocks = (rows + gs3d::kSortTile - 1) / gs3d::kSortTile;
     if (!packed) {

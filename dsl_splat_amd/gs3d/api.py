@@ -84,11 +84,13 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     """Camera rows, fused projection, depth order, one synchronisation, binning."""
     profiling.mark("start")
     with_centers = sh_degree is not None and sh_degree > 0
-    # One int64 status buffer read back once: [group pairs, tile pairs] and
-    # then the cameras' int32 status codes.
+    # One int64 status buffer read back once: [group pairs, tile pairs], the
+    # depth keys' bit count (int32 in the low half of the third word) and then
+    # the cameras' int32 status codes.
     cameras = viewmats.numel() // 16
-    status = torch.empty(2 + (cameras + 1) // 2, dtype=torch.int64, device=viewmats.device)
-    camera_status = status[2:].view(torch.int32)[:cameras]
+    status = torch.empty(3 + (cameras + 1) // 2, dtype=torch.int64, device=viewmats.device)
+    key_bits = status[2:3].view(torch.int32)[:1]
+    camera_status = status[3:].view(torch.int32)[:cameras]
     full, inverse, centers, _ = launch_prepare(viewmats, Ks, width, height, with_centers, errors=camera_status)
     state = project_views(
         means, quats, scales, opacities, viewmats, full, Ks, width, height, near, far, radius_clip,
@@ -98,11 +100,15 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     profiling.mark("projected")
     # The depth ordering computes every row's footprint in the chosen mode
     # once; it also leaves the mode's tile counts in state.tile_counts (the
-    # projection counted radius squares).
+    # projection counted radius squares).  It sorts the depth-key bits that
+    # the last frame of this shape needed; the frame's own need comes back
+    # with the totals.
+    shape = (status.device.index, state.radii.shape[-1], cameras, width, height, tile_mode)
+    sort_bits = binning.planned_sort_bits(shape)
     order, offsets, _ = order_rows(state.centers, state.radii, state.depths, width, height,
                                    conics=state.conics, tile_mode=tile_mode,
                                    tiles_out=None if tile_mode == "radius" else state.tile_counts,
-                                   totals=status[:2])
+                                   totals=status[:2], sort_bits=sort_bits, key_bits_out=key_bits)
     # Everything the binning launch needs besides the totals is prepared
     # while the device works on the depth order.
     launch = prepare_bin_rows(state.centers, state.radii, order, offsets, width, height, conics=state.conics,
@@ -118,8 +124,17 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     early = binning.emit_early(launch)
     copied.synchronize()
     profiling.mark("totals_read")
-    raise_camera_errors(host[2:].view(torch.int32)[:cameras].tolist())
+    raise_camera_errors(host[3:].view(torch.int32)[:cameras].tolist())
     group_pairs, count = host[:2].tolist()
+    if binning.remember_key_bits(shape, int(host[2:3].view(torch.int32)[0]), sort_bits):
+        # The depth keys now differ in more bits than were sorted: order
+        # again with enough (the totals do not depend on the order).
+        early = None
+        order, offsets, _ = order_rows(state.centers, state.radii, state.depths, width, height,
+                                       conics=state.conics, tile_mode=tile_mode,
+                                       sort_bits=binning.planned_sort_bits(shape))
+        launch = prepare_bin_rows(state.centers, state.radii, order, offsets, width, height,
+                                  conics=state.conics, tile_mode=tile_mode)
     if count <= binning.PAIR_LIMIT and group_pairs <= binning.PAIR_LIMIT:
         ranges, ids = launch_bin_rows(launch, group_pairs, count, early)
         bins = [ViewBins(0, cameras, ranges, ids)]

@@ -13,6 +13,7 @@ sum to.  Gradients of means2d are the blend's centre gradients
 (screen_gradient_mode "projected_mean").
 """
 
+import math
 import os
 from dataclasses import dataclass
 from typing import Any
@@ -72,9 +73,13 @@ def _views(t, v0: int, v1: int, views: int, per_view_ndim: int):
 # The buffers then live from the forward to the backward: C*N*(6 or 8) + the
 # blended channels' C*N*D floats (0.43 GB at 3M Gaussians, 4 cameras, SH
 # colours).  GS3D_CLEAR_IN_BACKWARD=1 makes the backward allocate and clear
-# them instead, for callers bound by memory rather than time.
+# them instead, for callers bound by memory rather than time.  Buffers below
+# CLEAR_DURING_FORWARD_MIN_FLOATS are always cleared in the backward: there
+# the side stream's host work (stream switch, wait, event: ~80 us per frame)
+# costs more than the device time that the overlap hides.
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
 CLEAR_DURING_FORWARD = os.environ.get("GS3D_CLEAR_IN_BACKWARD", "0") != "1"
+CLEAR_DURING_FORWARD_MIN_FLOATS = 1 << 24
 
 
 @dataclass(slots=True)
@@ -145,10 +150,11 @@ class Rasterize(torch.autograd.Function):
             absgrad = absolute is not None and any(t is not None for t in absolute)
             views, n = st.centers.shape[0], st.centers.shape[1]
             need_features = frame.sh_degree is not None or needs[4]
-            ctx.cleared = _clear_for_backward(
-                st.centers.device, (views, n, render.RECORD_ABS if absgrad else render.RECORD),
-                blended.shape if need_features and blended is not None else None,
-                extra_features.shape if needs[5] and extra_features is not None else None)
+            shapes = ((views, n, render.RECORD_ABS if absgrad else render.RECORD),
+                      blended.shape if need_features and blended is not None else None,
+                      extra_features.shape if needs[5] and extra_features is not None else None)
+            if sum(math.prod(s) for s in shapes if s is not None) >= CLEAR_DURING_FORWARD_MIN_FLOATS:
+                ctx.cleared = _clear_for_backward(st.centers.device, *shapes)
         if len(frame.bins) == 1:
             bins = frame.bins[0]
             output = render.render_views(

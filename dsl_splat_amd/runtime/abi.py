@@ -9,7 +9,7 @@ import ctypes
 c_float_p = ctypes.POINTER(ctypes.c_float)
 c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Tile modes (GS3D_TILE_*), named as the reference's TileMode literals.
 TILE_MODES = {"radius": 0, "snugbox": 1, "accutile": 2}
@@ -140,6 +140,8 @@ class OrderArgs(ctypes.Structure):
         ("tile_mode", ctypes.c_int32),
         ("tiles_out", _P),
         ("footprints", _P),
+        ("sort_bits", ctypes.c_int32),
+        ("key_bits_out", _P),
     ]
 
 

@@ -74,8 +74,17 @@ def query(name: str, *args) -> int:
     return int(getattr(load(), name)(*args))
 
 
+# torch's raw current-stream lookup (one C call) where this torch has it;
+# torch.cuda.current_stream builds a Stream object on every call (~6 us of
+# host time, several times per rasterize).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(device: torch.device) -> ctypes.c_void_p:
     """Handle of torch's current stream on ``device`` (the launch stream)."""
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return ctypes.c_void_p(_raw_stream(index))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 

@@ -84,7 +84,8 @@ def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tenso
 @torch.no_grad()
 def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, height: int, *,
                conics: Tensor | None = None, tile_mode="radius",
-               tiles_out: Tensor | None = None, totals: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+               tiles_out: Tensor | None = None, totals: Tensor | None = None,
+               sort_bits: int = 0, key_bits_out: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """Depth order of the (views, N) rows.
 
     Returns (ordered row records with 2*rows storage -- followed, for
@@ -92,7 +93,10 @@ def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, heigh
     group offsets, totals = [group pairs, tile pairs]), all left on the
     device.  ``tiles_out`` (int32, views*N), if given, receives every row's
     tile count in ``tile_mode``; ``totals`` (contiguous int64, 2), if given,
-    receives the totals."""
+    receives the totals.  ``sort_bits`` (0 = 32) sorts only the low depth-key
+    bits, valid when the kept rows' keys agree above them; ``key_bits_out``
+    (int32, 1), if given, receives the bits they need (the order must be
+    redone with at least that many when it exceeds ``sort_bits``)."""
     mode = _mode(tile_mode, conics)
     device = radii.device
     views, n = (1, radii.numel()) if radii.ndim == 1 else radii.shape
@@ -119,9 +123,61 @@ def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, heigh
         if tiles_out.dtype != torch.int32 or not tiles_out.is_contiguous() or tiles_out.numel() != rows:
             raise ValueError("tiles_out must be a contiguous int32 tensor with one entry per row")
         a.tiles_out = native.ptr(tiles_out)
+    if not 0 <= sort_bits <= 32:
+        raise ValueError("sort_bits must be in [0, 32]")
+    a.sort_bits = int(sort_bits)
+    if key_bits_out is not None:
+        if key_bits_out.dtype != torch.int32 or key_bits_out.numel() < 1:
+            raise ValueError("key_bits_out must be an int32 tensor of at least one entry")
+        a.key_bits_out = native.ptr(key_bits_out)
     scratch = _scratch(native.query("gs3d_order_rows_scratch_bytes", rows), device)
     native.call("gs3d_order_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
     return order, offsets, totals
+
+
+def order_pass_count(sort_bits: int) -> int:
+    """Radix passes of gs3d_order_rows for ``sort_bits`` (0 = 32): bits 0-7,
+    then 8-bit passes, the last one widened to up to 10 bits."""
+    end = 32 if sort_bits <= 0 else max(9, min(32, sort_bits))
+    passes, rest = 1, end - 8
+    while rest > 10:
+        passes, rest = passes + 1, rest - 8
+    return passes + 1
+
+
+def _pass_ceiling(bits: int) -> int:
+    """Most key bits sorted in as many passes as ``bits`` take (18, 26, 32)."""
+    passes = order_pass_count(bits)
+    return 32 if passes >= 4 else 8 + 8 * (passes - 2) + 10
+
+
+# Depth-key bits of earlier frames, per order shape (device, N, views,
+# width, height, tile mode): the next frame of the shape sorts only those
+# bits (three radix passes instead of four for 25 or 26 bits), and its own
+# key range, read with the totals, tells whether that was enough.
+_KEY_BITS: dict[tuple, int] = {}
+
+
+def planned_sort_bits(shape: tuple) -> int:
+    """Bits the next depth order of ``shape`` sorts (0 = all 32)."""
+    return _KEY_BITS.get(shape, 0)
+
+
+def remember_key_bits(shape: tuple, needed: int, sorted_bits: int) -> bool:
+    """Record the bits a frame's kept depth keys needed; True when the
+    frame's order sorted fewer (``sorted_bits``, 0 = 32) and must be redone.
+    After such a miss the plan takes the most bits of the needed pass count,
+    so a key range that keeps growing by a bit does not miss every frame."""
+    sorted_bits = 32 if sorted_bits <= 0 else max(9, sorted_bits)
+    needed = max(9, min(32, int(needed)))
+    miss = needed > sorted_bits
+    if shape not in _KEY_BITS and len(_KEY_BITS) >= _CAPACITY_SHAPES:
+        del _KEY_BITS[next(iter(_KEY_BITS))]
+    if miss:
+        _KEY_BITS[shape] = _pass_ceiling(needed)
+    elif order_pass_count(needed) < order_pass_count(sorted_bits) or shape not in _KEY_BITS:
+        _KEY_BITS[shape] = needed
+    return miss
 
 
 # Largest pair count one binning launch addresses: tile lists, ranges and

@@ -293,6 +293,17 @@ typedef struct gs3d_order_args {
     int32_t tile_mode;        /* GS3D_TILE_* */
     int32_t* tiles_out;       /* optional (views*N): every row's tile count in tile_mode */
     float* footprints;        /* ACCUTILE: (views*N,8) working footprints, 16-byte aligned, kept for gs3d_bin_rows */
+    /* Bits the order sorts, 0 (all 32) or 1..32 (values below 9 sort 9):
+     * the radix passes after the first take their digits from key - base,
+     * base = the smallest depth key (float bits) of the rows that touch a
+     * tile with its low byte cleared.  Fewer bits take fewer passes (up to
+     * 26 bits: three instead of four) and order the rows correctly only if
+     * every such key minus base is below 2^sort_bits, which key_bits_out
+     * reports after the call: an order whose key_bits_out exceeds the bits
+     * it sorted must be redone with at least that many.  Ignored (32) under
+     * GS3D_TILE_ACCUTILE. */
+    int32_t sort_bits;
+    int32_t* key_bits_out;    /* optional (1): bit length of (largest kept key - base), 0 without kept rows; 32 for ACCUTILE */
 } gs3d_order_args;
 
 size_t gs3d_order_rows_scratch_bytes(int64_t rows);

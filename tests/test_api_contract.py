@@ -139,3 +139,40 @@ def test_group_item_capacity_decays_after_a_large_frame():
     finally:
         binning._CAPACITY.clear()
         binning._CAPACITY.update(saved)
+
+
+def test_depth_order_pass_count_and_key_bit_plan():
+    # Passes of the depth order: bits 0-7, then 8-bit passes with the last
+    # one widened to up to 10 bits, i.e. two passes up to 18 key bits, three
+    # up to 26, four up to 32 (0 means 32; fewer than 9 bits still take two).
+    from dsl_splat_amd.splatting import binning
+
+    for bits in range(0, 33):
+        end = 32 if bits == 0 else max(bits, 9)
+        want = 2 if end <= 18 else 3 if end <= 26 else 4
+        assert binning.order_pass_count(bits) == want, bits
+    shape = ("test", 10, 1, 16, 16, "radius")
+    saved = dict(binning._KEY_BITS)
+    binning._KEY_BITS.clear()
+    try:
+        assert binning.planned_sort_bits(shape) == 0
+        # First frame sorts all 32 bits: never a miss; the plan is its need.
+        assert not binning.remember_key_bits(shape, 25, 0)
+        assert binning.planned_sort_bits(shape) == 25
+        # A smaller need in the same pass count keeps the plan.
+        assert not binning.remember_key_bits(shape, 20, 25)
+        assert binning.planned_sort_bits(shape) == 25
+        # A larger need is a miss; the plan takes the most bits of its passes.
+        assert binning.remember_key_bits(shape, 26, 25)
+        assert binning.planned_sort_bits(shape) == 26
+        assert binning.remember_key_bits(shape, 27, 26)
+        assert binning.planned_sort_bits(shape) == 32
+        # Fewer passes suffice again: the plan shrinks to the need.
+        assert not binning.remember_key_bits(shape, 16, 32)
+        assert binning.planned_sort_bits(shape) == 16
+        # All kept keys equal (0 bits) still sort the two passes' 9 bits.
+        assert not binning.remember_key_bits(shape, 0, 16)
+        assert binning.order_pass_count(binning.planned_sort_bits(shape)) == 2
+    finally:
+        binning._KEY_BITS.clear()
+        binning._KEY_BITS.update(saved)

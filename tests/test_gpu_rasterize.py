@@ -285,12 +285,17 @@ def test_packed_metadata_several_cameras_and_batches():
                 atol=1e-5 * max(1.0, float(np.abs(want).max())))
 
 
-def test_repeated_backward_and_interleaved_frames():
+@pytest.mark.parametrize("side_stream", [True, False])
+def test_repeated_backward_and_interleaved_frames(monkeypatch, side_stream):
     # The blend VJP accumulates into buffers cleared on a second stream
-    # during the forward blend: a second backward of the same graph
+    # during the forward blend (large frames; forced here) or by the
+    # backward (small frames): a second backward of the same graph
     # (retain_graph) must use fresh buffers (gradients add up to twice one
     # backward), and two frames whose forwards run before either backward
     # must keep their own buffers.
+    from dsl_splat_amd.gs3d import autograd
+
+    monkeypatch.setattr(autograd, "CLEAR_DURING_FORWARD_MIN_FLOATS", 0 if side_stream else 1 << 62)
     scene = synthetic.make_scene("sh3_720p", n=4000, width=128, height=96, seed=17).to(DEV)
     print("repeated backward, interleaved frames", flush=True)
     W = scene.loss_weights
@@ -347,6 +352,7 @@ def test_clearing_in_backward_matches_clearing_during_forward(monkeypatch):
     grads = []
     for during_forward in (True, False):
         monkeypatch.setattr(autograd, "CLEAR_DURING_FORWARD", during_forward)
+        monkeypatch.setattr(autograd, "CLEAR_DURING_FORWARD_MIN_FLOATS", 0)
         means = scene.means.clone().requires_grad_(True)
         sh = scene.sh_coeffs.clone().requires_grad_(True)
         res = gs3d.rasterize(means, scene.quats, scene.scales, scene.opacities, scene.viewmats, scene.Ks,

@@ -690,3 +690,96 @@ def test_blend_pair_counts_match_the_reference_loop(key, degree):
                                                   _np(feats))
     assert (got["visited"], got["accepted"]) == (visited, accepted)
     assert accepted <= got["evaluated"] <= visited and accepted > 0
+
+
+def _kept_key_bits(order, rows, depths):
+    """Bit length of (largest key - smallest key with its low byte cleared)
+    over the depth keys of the rows that the order kept (records before the
+    fillers, packed rectangles)."""
+    rec = _np(order[:rows]).view(np.uint64)
+    kept = (rec >> np.uint64(32)) != np.uint64(0xFF)
+    keys = _np(depths).ravel().view(np.uint32)[(rec[kept] & np.uint64(0xFFFFFFFF)).astype(np.int64)]
+    if keys.size == 0:
+        return 0
+    return (int(keys.max()) - (int(keys.min()) & ~255)).bit_length()
+
+
+@pytest.mark.parametrize("lo,hi,width", [
+    (1.7, 8.3, 640),      # 25 bits of key - base across 2.0: passes of 8, 8 and 9 bits
+    (2.1, 40.0, 640),     # 26 bits: 8, 8, 10
+    (2.1, 3.9, 640),      # 23 bits: 8, 8, 7
+    (2.0, 2.06, 640),     # 18 bits: 8, 10
+    (2.0, 2.01, 640),     # 16 bits: 8, 8
+    (0.05, 30.0, 640),    # 27 bits: four passes
+    (2.5, 2.5, 640),      # one distinct depth: the key's low byte, sorted as 9 bits
+    (1.7, 8.3, 4200),     # 263 tiles across: unpacked records
+])
+def test_depth_order_sorts_only_the_key_bits_in_use(lo, hi, width):
+    # gs3d_order_rows with sort_bits = the bits the kept rows' depth keys
+    # need (as key_bits_out reports them) gives exactly the 32-bit order:
+    # records, group offsets and totals; key_bits_out equals the bit length
+    # of the largest kept key minus the smallest with its low byte cleared.
+    _say(f"depth order key bits [{lo}, {hi}] width {width}")
+    g = torch.Generator().manual_seed(7)
+    views, n, height = 3, 30_000, 480
+    centers = (torch.rand((views, n, 2), generator=g) * torch.tensor([width * 1.2, height * 1.2])
+               - torch.tensor([width * 0.1, height * 0.1]))
+    radii = torch.randint(1, 30, (views, n), generator=g, dtype=torch.int32)
+    radii[:, 3::11] = 0
+    depths = lo + (hi - lo) * torch.rand((views, n), generator=g)
+    depths[:, ::5] = depths[:, 1::5][:, : depths[:, ::5].shape[1]]  # ties
+    centers, radii, depths = centers.to(DEV), radii.to(DEV), depths.to(DEV)
+    rows = views * n
+    bits = torch.full((1,), -1, dtype=torch.int32, device=DEV)
+    ref_order, ref_offsets, ref_totals = binning.order_rows(centers, radii, depths, width, height, key_bits_out=bits)
+    need = int(bits.item())
+    packed = (width + 15) // 16 <= 256
+    if packed:
+        assert need == _kept_key_bits(ref_order, rows, depths)
+    plans = {max(need, 9)} | ({26} if need <= 26 else set())
+    for sort_bits in sorted(plans):
+        bits2 = torch.full((1,), -1, dtype=torch.int32, device=DEV)
+        order, offsets, totals = binning.order_rows(centers, radii, depths, width, height, sort_bits=sort_bits,
+                                                    key_bits_out=bits2)
+        assert int(bits2.item()) == need
+        np.testing.assert_array_equal(_np(order[:rows]), _np(ref_order[:rows]))
+        np.testing.assert_array_equal(_np(offsets), _np(ref_offsets))
+        np.testing.assert_array_equal(_np(totals), _np(ref_totals))
+
+
+def test_rasterize_redoes_the_depth_order_when_the_key_bits_grow(monkeypatch):
+    # Frames of one shape sort the key bits the previous frame needed; a
+    # frame whose depths need more is ordered again, and every frame's
+    # output equals a frame rendered with no plan (all 32 bits).
+    scene = _scene("sh3_720p")
+    _say("rasterize, depth-order plan and a miss")
+    binning._KEY_BITS.clear()
+    calls = []
+    real_call = native.call
+    monkeypatch.setattr(native, "call", lambda name, *a: (calls.append(name), real_call(name, *a))[1])
+
+    def frame(viewmats):
+        calls.clear()
+        out = gs3d.rasterize(scene.means, scene.quats, scene.scales, scene.opacities, viewmats, scene.Ks,
+                             scene.width, scene.height, sh_coeffs=scene.sh_coeffs, sh_degree=3)
+        return out, calls.count("gs3d_order_rows")
+
+    near = scene.viewmats.clone()
+    near[..., 2, 3] -= 2.0  # camera 2 units closer: depths from ~0.5, more key bits than the 24 of "far"
+    outputs = {}
+    for name, vm in (("far", scene.viewmats), ("near", near)):
+        binning._KEY_BITS.clear()
+        outputs[name], orders = frame(vm)
+        assert orders == 1
+    binning._KEY_BITS.clear()
+    first, orders = frame(scene.viewmats)
+    plan = binning._KEY_BITS[next(iter(binning._KEY_BITS))]
+    assert orders == 1 and plan <= 26, plan
+    again, orders = frame(scene.viewmats)
+    assert orders == 1
+    closer, orders = frame(near)
+    assert orders == 2  # the plan missed: ordered again with enough bits
+    for got, want in ((first, outputs["far"]), (again, outputs["far"]), (closer, outputs["near"])):
+        assert torch.equal(got.features, want.features)
+        assert torch.equal(got.alpha, want.alpha)
+    binning._KEY_BITS.clear()
