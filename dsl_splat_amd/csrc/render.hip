@@ -320,43 +320,51 @@ GS3D_DEV Staged<CH> load_staged(int j, const StagedRec<CH>* s_g) {
 // pixel's value times zero), so a wavefront with a non-finite value selects
 // each term instead (wave-uniform choice).  One wavefront sum covers all
 // requests together (permlane pairing and a DPP row butterfly, as in the
-// backward), and each lane that holds a request's total adds it with one
-// atomic to the row fixed for it at the start of the tile (StatLane).
-// Counts are exact (at most 64 * PIX per wavefront, summed in float32
-// without rounding); sums differ from per-pixel atomics only in the order of
-// the float additions, which atomics leave unspecified anyway.
-struct StatLane {
-    void* row;    // the lane's request row (view applied), or NULL
-    bool is_sum;  // row is a float sums row, else an int32 counts row
-};
-
+// backward), and each lane that holds a request's total (stat_lane) adds it
+// to the Gaussian's LDS slot, where the tile's wavefronts meet; once every
+// wavefront is past the batch, the thread that staged the Gaussian adds the
+// slot's nonzero totals to the request rows with one global atomic each
+// (flush_statistics): half the global atomics of one per wavefront.
+// Counts are exact (at most 256 per tile, summed in float32 without
+// rounding); sums differ from per-pixel atomics only in the order of the
+// float additions, which atomics leave unspecified anyway.
 template <int RB>
-GS3D_DEV StatLane stat_lane(const gs3d_render_stats_args& st, int view, int n, int lane) {
-    StatLane l{nullptr, false};
+GS3D_DEV int stat_lane(const gs3d_render_stats_args& st, int lane) {
     int r = 0;
     if constexpr (RB == 1) {
-        if (lane != 63) return l;
+        if (lane != 63) return -1;
     } else {
         constexpr int rows = (RB + 3) / 4;
         r = wave_sum_rows_value(lane);
-        if ((lane & 15) >= rows || r >= RB) return l;
+        if ((lane & 15) >= rows || r >= RB) return -1;
     }
-    if (r >= st.requests) return l;
-    // Row of request r among the requests of its kind.
-    const uint32_t before = st.sum_mask & ((1u << r) - 1u);
-    l.is_sum = (st.sum_mask >> r) & 1u;
-    if (l.is_sum)
-        l.row = st.sums + view * st.sums_view_stride + (int64_t)__builtin_popcount(before) * n;
-    else
-        l.row = st.counts + view * st.counts_view_stride + (int64_t)(r - __builtin_popcount(before)) * n;
-    return l;
+    return r < st.requests ? r : -1;
+}
+
+// Adds a staged Gaussian's per-request totals (slot[r]) to the request rows
+// of view `view` (each row among the rows of its kind) and clears the slot.
+template <int RB>
+GS3D_DEV void flush_statistics(const gs3d_render_stats_args& st, int view, int n, int32_t g, float* slot) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        if (r >= st.requests) break;
+        const float v = slot[r];
+        slot[r] = 0.0f;
+        if (v == 0.0f) continue;
+        const uint32_t before = st.sum_mask & ((1u << r) - 1u);
+        if ((st.sum_mask >> r) & 1u)
+            atomicAdd(st.sums + view * st.sums_view_stride + (int64_t)__builtin_popcount(before) * n + g, v);
+        else
+            atomicAdd(st.counts + view * st.counts_view_stride + (int64_t)(r - __builtin_popcount(before)) * n + g,
+                      (int)v);
+    }
 }
 
 // KINDS: the requests' kinds as a compile-time sum mask (bit r set: request
 // r is a weighted sum) for launches of one or two requests, -1 to read them
 // from st.sum_mask.
 template <int PIX, int RB, int KINDS>
-GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, const StatLane& dst, int32_t g,
+GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, int dst_r, float* slot,
                                  const bool (&acc)[PIX], const float (&w)[PIX], const float (&val)[PIX][RB],
                                  bool finite, int lane) {
     float e[RB];
@@ -399,12 +407,7 @@ GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, const StatLan
 #pragma unroll
         for (int q = 1; q < rows; ++q) total = ((lane & 15) == q) ? sums[q] : total;
     }
-    if (dst.row && total != 0.0f) {
-        if (dst.is_sum)
-            atomicAdd(static_cast<float*>(dst.row) + g, total);
-        else
-            atomicAdd(static_cast<int*>(dst.row) + g, (int)total);
-    }
+    if (dst_r >= 0 && total != 0.0f) atomicAdd(slot + dst_r, total);  // LDS
 }
 
 // Up to 8 channels the kernel is held to 80 VGPRs (6 wavefronts per SIMD
@@ -428,10 +431,13 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     constexpr int B = Batch<CH>::size;
     __shared__ StagedRec<CH> s_g[B];
     __shared__ uint32_t s_mask[B];
-    __shared__ int32_t s_id[STATS ? B : 1];
+    // Per staged Gaussian: the tile's totals of every statistics request.
+    __shared__ float s_stat[STATS ? B * RB : 1];
     const TileInfo t = tile_info(a);
     const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
     const int lane = lane_id(), wave = threadIdx.x >> 6;
+    if constexpr (STATS)
+        for (int e = threadIdx.x; e < B * RB; e += NT) s_stat[e] = 0.0f;
     float fx[PIX], fy[PIX], T[PIX], color[PIX][CH];
     int px[PIX], py[PIX], last_contributor[PIX];
     bool done[PIX];
@@ -468,10 +474,19 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     // into the list, so the load is unconditional).
     static_assert(B <= NT, "one staged Gaussian per thread and batch");
     int32_t next_id = t.last > t.first ? a.ids[min(t.first + (int)threadIdx.x, t.last - 1)] : 0;
-    StatLane stat_dst{nullptr, false};
+    int stat_r = -1;
     bool stat_finite = true;
+    // The Gaussian this thread staged for the batch being blended, whose
+    // statistics slot it flushes (-1: none).
+    int32_t flush_id = -1;
+    auto flush = [&]() {
+        if constexpr (STATS) {
+            if (flush_id >= 0) flush_statistics<RB>(st, t.view, a.n, flush_id, &s_stat[threadIdx.x * RB]);
+            flush_id = -1;
+        }
+    };
     if constexpr (STATS) {
-        stat_dst = stat_lane<RB>(st, t.view, a.n, lane);
+        stat_r = stat_lane<RB>(st, lane);
         bool finite = true;
 #pragma unroll
         for (int k = 0; k < PIX; ++k)
@@ -483,7 +498,9 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
         bool active = false;
 #pragma unroll
         for (int k = 0; k < PIX; ++k) active = active || !done[k];
-        if (__syncthreads_count(active) == 0) break;
+        const int active_threads = __syncthreads_count(active);
+        flush();  // every wavefront is past the previous batch
+        if (active_threads == 0) break;
         if (threadIdx.x < B) {
             const int e = threadIdx.x;
             const int32_t g = next_id;
@@ -491,7 +508,7 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 // The 4-channel plain blend fits its registers without the
                 // tile-origin laundering (and is fastest so).
                 stage_gaussian<CH, PIX, (STATS || CH > 4)>(a, t, g, e, c0, s_g, s_mask);
-                if constexpr (STATS) s_id[e] = g;
+                if constexpr (STATS) flush_id = g;
             }
             if (begin + B < t.last) next_id = a.ids[min(begin + B + e, t.last - 1)];
         }
@@ -547,7 +564,8 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                     bool hit = false;
 #pragma unroll
                     for (int k = 0; k < PIX; ++k) hit = hit || acc[k];
-                    if (__ballot(hit)) observe_statistics<PIX, RB, KINDS>(st, stat_dst, s_id[j], acc, wk, val, stat_finite, lane);
+                    if (__ballot(hit))
+                        observe_statistics<PIX, RB, KINDS>(st, stat_r, &s_stat[j * RB], acc, wk, val, stat_finite, lane);
                 }
             };
             auto alive = [&]() {
@@ -610,6 +628,11 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 }
             }
         }
+    }
+    if constexpr (STATS) {
+        // The last batch, when the loop ran to the end of the list.
+        __syncthreads();
+        flush();
     }
     const float* bg = a.background ? a.background + t.view * a.background_view_stride : nullptr;
     const int F = a.feat_channels, E = a.extra_channels;
