@@ -39,6 +39,7 @@ HEADLINE = "sh3_1080p_4view"
 # Benchmark workloads in order (synthetic.make_scene names).
 WORKLOADS = ("small", "sh3_720p", "sh3_1080p_4view", "feat32", "pose_fanout")
 HBM_STAGES = ("project", "order", "bin", "project_bwd")
+WARM_MS = 300.0  # warm-up of the other workloads, in milliseconds of steps
 FANOUT = "pose_fanout"  # 2M Gaussians, 5% of them large: the workload the tile modes are for
 
 
@@ -462,7 +463,10 @@ def run_workload(workload, n, device, steps, warmup, cpu, tile_mode="radius", mi
     if min_timed_ms > 0:
         probe = time_steps(forward, backward, 2, warmup)
         steps = max(steps, min(100, math.ceil(min_timed_ms / max(probe["ms"], 1e-3))))
-        warmup = 1
+        # Short steps reach their steady rate only after a few hundred
+        # milliseconds of back-to-back steps (clocks ramp up): warm up for
+        # about that long, as a training loop would have.
+        warmup = max(1, min(400, math.ceil(WARM_MS / max(probe["ms"], 1e-3))))
     log(f"[bench] {workload}: {warmup} warm-up + {steps} timed steps")
     clean = time_steps(forward, backward, steps, warmup)
     staged = time_steps(forward, backward, steps, 1, stage_events=True)
