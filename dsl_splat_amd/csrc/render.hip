@@ -438,6 +438,17 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     const int lane = lane_id(), wave = threadIdx.x >> 6;
     if constexpr (STATS)
         for (int e = threadIdx.x; e < B * RB; e += NT) s_stat[e] = 0.0f;
+    if (c0 == 0 && a.zero_out) {
+        // The blend VJP's accumulation buffers, cleared by the first
+        // window's launch: the stores drain while the blend computes.
+        typedef float zero4 __attribute__((ext_vector_type(4)));
+        const int64_t n4 = a.zero_count >> 2;
+        zero4* z = reinterpret_cast<zero4*>(a.zero_out);
+        const int64_t step = (int64_t)gridDim.x * NT;
+        for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n4; i += step)
+            __builtin_nontemporal_store(zero4{0.0f, 0.0f, 0.0f, 0.0f}, z + i);
+        if (blockIdx.x == 0 && threadIdx.x < (a.zero_count & 3)) a.zero_out[(n4 << 2) + threadIdx.x] = 0.0f;
+    }
     float fx[PIX], fy[PIX], T[PIX], color[PIX][CH];
     int px[PIX], py[PIX], last_contributor[PIX];
     bool done[PIX];
@@ -1084,6 +1095,8 @@ int render_fwd(const gs3d_render_args* args, const gs3d_render_stats_args* st, u
     const gs3d_render_args& a = *args;
     int status = check_render_args(a);
     if (status != GS3D_OK) return status;
+    if (a.zero_count < 0 || (a.zero_count > 0 && (!a.zero_out || (reinterpret_cast<uintptr_t>(a.zero_out) & 15))))
+        return GS3D_ERR_ARGUMENT;
     if (a.views == 0) return GS3D_OK;
     if ((a.feat_channels > 0 && !a.image) || (a.extra_channels > 0 && !a.image_extra) ||
         (a.one_tail && !a.image_alpha) || !a.final_t || !a.contributors)

@@ -67,51 +67,37 @@ def _views(t, v0: int, v1: int, views: int, per_view_ndim: int):
     return t[v0:v1]
 
 
-# One side stream per device clears the backward's accumulation buffers
-# (blend gradient record, colour and extra-channel gradients) while the
-# forward blend, which is bound by arithmetic, runs on the caller's stream.
+# The backward's accumulation buffers (blend gradient record, colour and
+# extra-channel gradients) are views of one allocation that the forward blend
+# launch clears while it blends (its arithmetic leaves HBM idle; a separate
+# fill kernel per buffer cost ~55 us per step at 3M Gaussians, 4 cameras).
 # The buffers then live from the forward to the backward: C*N*(6 or 8) + the
 # blended channels' C*N*D floats (0.43 GB at 3M Gaussians, 4 cameras, SH
 # colours).  GS3D_CLEAR_IN_BACKWARD=1 makes the backward allocate and clear
-# them instead, for callers bound by memory rather than time.  Buffers below
-# CLEAR_DURING_FORWARD_MIN_FLOATS are always cleared in the backward: there
-# the side stream's host work (stream switch, wait, event: ~80 us per frame)
-# costs more than the device time that the overlap hides.
-_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+# them instead, for callers bound by memory rather than time.
 CLEAR_DURING_FORWARD = os.environ.get("GS3D_CLEAR_IN_BACKWARD", "0") != "1"
-CLEAR_DURING_FORWARD_MIN_FLOATS = 1 << 24
 
 
 @dataclass(slots=True)
 class ClearedBuffers:
-    """Zeroed accumulation targets of the blend VJP, ready once ``done``."""
+    """Accumulation targets of the blend VJP, zeroed by the forward blend."""
 
     record: Tensor
     features: Tensor | None
     extra: Tensor | None
-    done: torch.cuda.Event
 
 
-def _clear_for_backward(device: torch.device, record_shape, feature_shape, extra_shape) -> ClearedBuffers:
-    main = torch.cuda.current_stream(device)
-    side = _SIDE_STREAMS.get(device.index)
-    if side is None:
-        side = _SIDE_STREAMS[device.index] = torch.cuda.Stream(device=device)
-    f32 = dict(dtype=torch.float32, device=device)
-    bufs = [None if shape is None else torch.empty(shape, **f32) for shape in (record_shape, feature_shape, extra_shape)]
-    # The side stream starts after everything enqueued so far (the memory may
-    # have served earlier work on the caller's stream), not after the blend.
-    side.wait_stream(main)
-    with torch.cuda.stream(side):
-        for b in bufs:
-            if b is not None:
-                b.zero_()
-    for b in bufs:
-        if b is not None:
-            b.record_stream(side)
-    done = torch.cuda.Event()
-    done.record(side)
-    return ClearedBuffers(*bufs, done)
+def _buffers_for_backward(device: torch.device, shapes) -> tuple[ClearedBuffers, Tensor]:
+    """(record, features, extra) as views of one float32 allocation, each
+    starting on a 16-byte boundary, and that allocation (which the forward
+    blend clears)."""
+    offsets, total = [], 0
+    for shape in shapes:
+        offsets.append(total)
+        total += 0 if shape is None else (math.prod(shape) + 3) // 4 * 4
+    flat = torch.empty(max(total, 4), dtype=torch.float32, device=device)
+    views = [None if shape is None else flat[o:o + math.prod(shape)].view(shape) for shape, o in zip(shapes, offsets)]
+    return ClearedBuffers(*views), flat
 
 
 def _statistics_views(statistics, v0: int, v1: int):
@@ -145,6 +131,7 @@ class Rasterize(torch.autograd.Function):
         blended = st.colors if frame.sh_degree is not None else colors
         train = grad_enabled and any(ctx.needs_input_grad[:8])
         ctx.cleared = None
+        zero = None
         if train and len(frame.bins) == 1 and CLEAR_DURING_FORWARD:
             needs = ctx.needs_input_grad
             absgrad = absolute is not None and any(t is not None for t in absolute)
@@ -153,13 +140,13 @@ class Rasterize(torch.autograd.Function):
             shapes = ((views, n, render.RECORD_ABS if absgrad else render.RECORD),
                       blended.shape if need_features and blended is not None else None,
                       extra_features.shape if needs[5] and extra_features is not None else None)
-            if sum(math.prod(s) for s in shapes if s is not None) >= CLEAR_DURING_FORWARD_MIN_FLOATS:
-                ctx.cleared = _clear_for_backward(st.centers.device, *shapes)
+            ctx.cleared, zero = _buffers_for_backward(st.centers.device, shapes)
         if len(frame.bins) == 1:
             bins = frame.bins[0]
             output = render.render_views(
                 bins.ranges, bins.ids, st.centers, st.conics, blended, frame.width, frame.height,
                 extra=extra_features, background=frame.background, one_tail=True, statistics=statistics,
+                zero=zero,
             )
         else:
             views = st.centers.shape[0]
@@ -209,10 +196,7 @@ class Rasterize(torch.autograd.Function):
         blend_args = dict(one_tail=True, absgrad=absgrad, need_features=sh or needs[4], need_extra=needs[5])
         if len(frame.bins) == 1:
             bins = frame.bins[0]
-            cleared = ctx.cleared
-            if cleared is not None:
-                torch.cuda.current_stream(st.centers.device).wait_event(cleared.done)
-                ctx.cleared = None
+            cleared, ctx.cleared = ctx.cleared, None
             record, grad_blended, grad_extra = render.backward_views(
                 bins.ranges, bins.ids, st.centers, st.conics, blended, final_t, contributors, upstream,
                 frame.width, frame.height, extra=extra, background=frame.background, cleared=cleared, **blend_args,

@@ -118,9 +118,11 @@ def _stats_args(statistics, views: int, n: int, width: int, height: int, keep: l
 @torch.no_grad()
 def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, features: Tensor,
                  width: int, height: int, *, extra: Tensor | None = None, background: Tensor | None = None,
-                 one_tail: bool = True, statistics=None) -> RenderedPixels:
+                 one_tail: bool = True, statistics=None, zero: Tensor | None = None) -> RenderedPixels:
     """Blend all views; with a PreparedStatistics, its counts and sums
-    accumulate the contribution statistics of the same launch."""
+    accumulate the contribution statistics of the same launch.  ``zero`` (a
+    contiguous float32 tensor, 16-byte aligned), if given, is cleared by the
+    launch while it blends."""
     views, n = centers.shape[0], centers.shape[1]
     device = centers.device
     keep = []
@@ -137,6 +139,10 @@ def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, f
     a.image, a.final_t, a.contributors = (native.ptr(out.features), native.ptr(out.transmittance),
                                           native.ptr(out.contributors))
     a.image_extra, a.image_alpha = native.ptr(out.extra), native.ptr(out.alpha)
+    if zero is not None:
+        if zero.dtype != torch.float32 or not zero.is_contiguous() or zero.device != device:
+            raise ValueError("zero must be a contiguous float32 tensor on the rendering device")
+        a.zero_out, a.zero_count = native.ptr(zero), zero.numel()
     if statistics is not None and len(statistics.key):
         st = _stats_args(statistics, views, n, width, height, keep)
         native.call("gs3d_render_fwd_stats", ctypes.byref(a), ctypes.byref(st), native.stream(device))

@@ -9,7 +9,7 @@ import ctypes
 c_float_p = ctypes.POINTER(ctypes.c_float)
 c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # Tile modes (GS3D_TILE_*), named as the reference's TileMode literals.
 TILE_MODES = {"radius": 0, "snugbox": 1, "accutile": 2}
@@ -191,6 +191,8 @@ class RenderArgs(ctypes.Structure):
         ("image_alpha", _P),
         ("final_t", _P),
         ("contributors", _P),
+        ("zero_out", _P),
+        ("zero_count", ctypes.c_int64),
     ]
 
 

@@ -393,6 +393,12 @@ typedef struct gs3d_render_args {
     float* image_alpha;        /* (views,H,W); NULL unless one_tail */
     float* final_t;            /* (views,H,W) */
     int32_t* contributors;     /* (views,H,W) */
+    /* Optional, forward launches only: zero_count floats from zero_out
+     * (16-byte aligned) are set to zero by the launch, while its blend
+     * runs -- the accumulation buffers of a later gs3d_render_bwd, cleared
+     * without a fill kernel of their own.  NULL / 0: nothing is cleared. */
+    float* zero_out;
+    int64_t zero_count;
 } gs3d_render_args;
 
 int gs3d_render_fwd(const gs3d_render_args* args, void* stream);

@@ -285,17 +285,16 @@ def test_packed_metadata_several_cameras_and_batches():
                 atol=1e-5 * max(1.0, float(np.abs(want).max())))
 
 
-@pytest.mark.parametrize("side_stream", [True, False])
-def test_repeated_backward_and_interleaved_frames(monkeypatch, side_stream):
-    # The blend VJP accumulates into buffers cleared on a second stream
-    # during the forward blend (large frames; forced here) or by the
-    # backward (small frames): a second backward of the same graph
-    # (retain_graph) must use fresh buffers (gradients add up to twice one
-    # backward), and two frames whose forwards run before either backward
-    # must keep their own buffers.
+@pytest.mark.parametrize("during_forward", [True, False])
+def test_repeated_backward_and_interleaved_frames(monkeypatch, during_forward):
+    # The blend VJP accumulates into buffers that the forward blend launch
+    # clears (or, with GS3D_CLEAR_IN_BACKWARD, the backward): a second
+    # backward of the same graph (retain_graph) must use fresh buffers
+    # (gradients add up to twice one backward), and two frames whose
+    # forwards run before either backward must keep their own buffers.
     from dsl_splat_amd.gs3d import autograd
 
-    monkeypatch.setattr(autograd, "CLEAR_DURING_FORWARD_MIN_FLOATS", 0 if side_stream else 1 << 62)
+    monkeypatch.setattr(autograd, "CLEAR_DURING_FORWARD", during_forward)
     scene = synthetic.make_scene("sh3_720p", n=4000, width=128, height=96, seed=17).to(DEV)
     print("repeated backward, interleaved frames", flush=True)
     W = scene.loss_weights
@@ -343,8 +342,8 @@ def test_repeated_backward_and_interleaved_frames(monkeypatch, side_stream):
 
 def test_clearing_in_backward_matches_clearing_during_forward(monkeypatch):
     # With GS3D_CLEAR_IN_BACKWARD the blend VJP's accumulation buffers are
-    # allocated and zeroed by the backward instead of on a side stream during
-    # the forward: the same gradients (atomic order aside).
+    # allocated and zeroed by the backward instead of by the forward blend
+    # launch: the same gradients (atomic order aside).
     from dsl_splat_amd.gs3d import autograd
 
     scene = synthetic.make_scene("sh3_1080p_4view", n=8000, width=288, height=240, seed=21).to(DEV)
@@ -352,7 +351,6 @@ def test_clearing_in_backward_matches_clearing_during_forward(monkeypatch):
     grads = []
     for during_forward in (True, False):
         monkeypatch.setattr(autograd, "CLEAR_DURING_FORWARD", during_forward)
-        monkeypatch.setattr(autograd, "CLEAR_DURING_FORWARD_MIN_FLOATS", 0)
         means = scene.means.clone().requires_grad_(True)
         sh = scene.sh_coeffs.clone().requires_grad_(True)
         res = gs3d.rasterize(means, scene.quats, scene.scales, scene.opacities, scene.viewmats, scene.Ks,

@@ -783,3 +783,23 @@ def test_rasterize_redoes_the_depth_order_when_the_key_bits_grow(monkeypatch):
         assert torch.equal(got.features, want.features)
         assert torch.equal(got.alpha, want.alpha)
     binning._KEY_BITS.clear()
+
+
+@pytest.mark.parametrize("count", [0, 1, 3, 4, 1001, 262_147])
+def test_forward_blend_clears_the_given_buffer(count):
+    # render_views(zero=...) clears every float of the buffer (float4 body
+    # and scalar tail) and blends exactly as without it.
+    scene = _scene("wide_sh3_4view")
+    _say(f"forward blend clears {count} floats")
+    quats, full, inverse, centers, errors, st = _project(scene, 3)
+    bins = binning.bin_and_sort(st.centers, st.radii, st.tile_counts, st.depths, scene.width, scene.height)
+    args = (bins["ranges"], bins["point_list"], st.centers, st.conics, st.colors, scene.width, scene.height)
+    ref = grender.render_views(*args)
+    buf = torch.full((count + 8,), float("nan"), device=DEV)
+    zero = buf[4:4 + count]  # 16-byte aligned view, NaN guards on both sides
+    out = grender.render_views(*args, zero=zero)
+    torch.cuda.synchronize()
+    assert torch.equal(out.features, ref.features) and torch.equal(out.alpha, ref.alpha)
+    assert torch.equal(out.contributors, ref.contributors)
+    assert bool((zero == 0).all())
+    assert bool(buf[:4].isnan().all()) and bool(buf[4 + count:].isnan().all())
