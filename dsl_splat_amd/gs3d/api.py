@@ -15,6 +15,7 @@ strips (splatting/intersections.py).
 
 from dataclasses import dataclass, field
 import math
+import threading
 from numbers import Integral
 from typing import Any, Sequence
 
@@ -78,6 +79,22 @@ def _sh_degree(features, sh_coeffs, sh_degree) -> int | None:
     return sh_degree
 
 
+# Pinned host buffers the per-frame status word is copied into, one per
+# thread and size: a frame waits for its copy before it returns, so the next
+# frame of the thread may reuse the buffer.
+_PINNED = threading.local()
+
+
+def _pinned_status(numel: int) -> Tensor:
+    cache = getattr(_PINNED, "buffers", None)
+    if cache is None:
+        cache = _PINNED.buffers = {}
+    buf = cache.get(numel)
+    if buf is None:
+        buf = cache[numel] = torch.empty(numel, dtype=torch.int64, pin_memory=True)
+    return buf
+
+
 @torch.no_grad()
 def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height, near, far, radius_clip,
                    sh, sh_degree, background, tile_mode="radius") -> Frame:
@@ -116,10 +133,13 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     # The totals are copied to pinned host memory right after the depth
     # order; with a group-item capacity from an earlier frame of this shape,
     # the device then emits the group items while the host waits for them.
-    host = torch.empty(status.shape, dtype=status.dtype, pin_memory=True)
+    host = _pinned_status(status.numel())
     host.copy_(status, non_blocking=True)
     copied = torch.cuda.Event()
-    copied.record(torch.cuda.current_stream(status.device))
+    if status.device.index == torch.cuda.current_device():
+        copied.record()  # the current stream, as torch.cuda.current_stream() would give it
+    else:
+        copied.record(torch.cuda.current_stream(status.device))
     profiling.mark("ordered")
     early = binning.emit_early(launch)
     copied.synchronize()

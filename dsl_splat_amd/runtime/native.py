@@ -88,11 +88,14 @@ def stream(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def ptr(tensor: torch.Tensor | None, offset_elems: int = 0) -> ctypes.c_void_p | None:
-    """Device address of a tensor's first element (plus an element offset)."""
+def ptr(tensor: torch.Tensor | None, offset_elems: int = 0) -> int | None:
+    """Device address of a tensor's first element (plus an element offset),
+    as the integer that ctypes passes for a ``void*`` argument or field."""
     if tensor is None:
         return None
-    return ctypes.c_void_p(tensor.data_ptr() + offset_elems * tensor.element_size())
+    if offset_elems:
+        return tensor.data_ptr() + offset_elems * tensor.element_size()
+    return tensor.data_ptr()
 
 
 def require_device(tensor: torch.Tensor) -> None:
