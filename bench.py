@@ -244,6 +244,8 @@ def stage_report(stages, by, info):
         if k in by:
             gbps = by[k] / (ms * 1e-3) / 1e9
             entry.update(bytes=by[k], gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4))
+        if k == "order":
+            entry["radix_passes"] = info["order_passes"]
         if k in ("render_fwd", "render_bwd"):
             p = info["blend_pairs"]
             entry.update(visited_pairs_per_us=round(p["visited"] / (ms * 1e3), 1),
