@@ -27,6 +27,7 @@ from .. import profiling
 from .projection import project_views
 from ..cameras import validate_camera_options
 from ..inputs import batch_item, normalize_inputs
+from ..runtime import native
 from ..splatting import binning
 from ..splatting.binning import launch_bin_rows, order_rows, prepare_bin_rows, validate_tile_mode
 from ..splatting.cameras import launch_prepare, raise_camera_errors
@@ -95,7 +96,7 @@ def _pinned_status(numel: int) -> Tensor:
     return buf
 
 
-@torch.no_grad()
+@native.no_grad
 def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height, near, far, radius_clip,
                    sh, sh_degree, background, tile_mode="radius") -> Frame:
     """Camera rows, fused projection, depth order, one synchronisation, binning."""

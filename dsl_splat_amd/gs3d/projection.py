@@ -47,7 +47,7 @@ def _sh_layout(sh: Tensor, views: int) -> tuple[Tensor, int, int]:
     return sh, 0, sh.shape[1]
 
 
-@torch.no_grad()
+@native.no_grad
 def project_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tensor, view: Tensor,
                   projection: Tensor, intrinsics: Tensor, width: int, height: int, near: float, far: float,
                   radius_clip: float, *, sh: Tensor | None = None, sh_degree: int = 0,
@@ -105,7 +105,7 @@ def project_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tenso
 CAMERA_GRADIENT_GROUP = 16
 
 
-@torch.no_grad()
+@native.no_grad
 def backward_views(means: Tensor, quats: Tensor, scales: Tensor, opacities: Tensor, view: Tensor,
                    projection: Tensor, intrinsics: Tensor, width: int, height: int, radii: Tensor,
                    grad_centers: Tensor, grad_conics: Tensor, needs: tuple[bool, ...], *,

@@ -115,7 +115,7 @@ def _stats_args(statistics, views: int, n: int, width: int, height: int, keep: l
     return st
 
 
-@torch.no_grad()
+@native.no_grad
 def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, features: Tensor,
                  width: int, height: int, *, extra: Tensor | None = None, background: Tensor | None = None,
                  one_tail: bool = True, statistics=None, zero: Tensor | None = None) -> RenderedPixels:
@@ -151,7 +151,7 @@ def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, f
     return out
 
 
-@torch.no_grad()
+@native.no_grad
 def backward_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, features: Tensor,
                    final_t: Tensor, contributors: Tensor, upstream, width: int, height: int, *,
                    extra: Tensor | None = None, background: Tensor | None = None, one_tail: bool = True,
@@ -211,7 +211,7 @@ def backward_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor,
     return record, grad_features, grad_extra
 
 
-@torch.no_grad()
+@native.no_grad
 def pair_counts(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, features: Tensor, width: int,
                 height: int, *, extra: Tensor | None = None, background: Tensor | None = None,
                 one_tail: bool = True) -> dict[str, int]:

@@ -31,7 +31,7 @@ def _scratch(nbytes: int, device) -> Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-@torch.no_grad()
+@native.no_grad
 def scan_device(counts: Tensor) -> tuple[Tensor, Tensor]:
     """Inclusive int32 offsets and the int64 total, both left on the device."""
     counts = counts.contiguous().view(-1)
@@ -54,7 +54,7 @@ def scan_counts(counts: Tensor, stream=None) -> tuple[Tensor, int]:
     return offsets, count
 
 
-@torch.no_grad()
+@native.no_grad
 def sort_pairs(keys: Tensor, ids: Tensor, count: int, end_bit: int) -> None:
     """Stable LSD radix sort of keys[:count]/ids[:count] in place (2*count storage)."""
     if count <= 0:
@@ -66,7 +66,7 @@ def sort_pairs(keys: Tensor, ids: Tensor, count: int, end_bit: int) -> None:
                 native.ptr(scratch), scratch.numel(), native.stream(keys.device))
 
 
-@torch.no_grad()
+@native.no_grad
 def identify_ranges(sorted_keys: Tensor, ranges: Tensor) -> None:
     count = sorted_keys.numel()
     if count:

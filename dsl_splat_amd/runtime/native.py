@@ -9,6 +9,7 @@ no HIP device, the call raises.
 """
 
 import ctypes
+import functools
 import os
 import threading
 
@@ -96,6 +97,21 @@ def ptr(tensor: torch.Tensor | None, offset_elems: int = 0) -> int | None:
     if offset_elems:
         return tensor.data_ptr() + offset_elems * tensor.element_size()
     return tensor.data_ptr()
+
+
+def no_grad(fn):
+    """torch.no_grad() as a decorator that costs nothing when gradients are
+    already off (the launch wrappers call one another; torch's decorator
+    enters a fresh context manager on every call)."""
+
+    @functools.wraps(fn)
+    def wrapper(*args, **kwargs):
+        if not torch.is_grad_enabled():
+            return fn(*args, **kwargs)
+        with torch.no_grad():
+            return fn(*args, **kwargs)
+
+    return wrapper
 
 
 def require_device(tensor: torch.Tensor) -> None:

@@ -41,7 +41,7 @@ def tile_count(width: int, height: int, views: int = 1) -> int:
     return views * ((width + 15) // 16) * ((height + 15) // 16)
 
 
-@torch.no_grad()
+@native.no_grad
 def emit_keys(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, count: int, width: int,
               height: int, *, conics: Tensor | None = None, tile_mode="radius") -> tuple[Tensor, Tensor]:
     """Keys/ids (2*count storage each) of the (views, N) rows' tile pairs."""
@@ -66,7 +66,7 @@ def emit_keys(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, c
     return keys, ids
 
 
-@torch.no_grad()
+@native.no_grad
 def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tensor, count: int, width: int,
                   height: int, *, conics: Tensor | None = None, tile_mode="radius") -> TileBins:
     """Emit keys for (views, N) rows given inclusive offsets and their total,
@@ -81,7 +81,7 @@ def emit_and_sort(centers: Tensor, radii: Tensor, depths: Tensor, offsets: Tenso
     return dict(point_list=ids[:count], ranges=ranges, point_list_keys=keys[:count], point_offsets=offsets)
 
 
-@torch.no_grad()
+@native.no_grad
 def order_rows(centers: Tensor, radii: Tensor, depths: Tensor, width: int, height: int, *,
                conics: Tensor | None = None, tile_mode="radius",
                tiles_out: Tensor | None = None, totals: Tensor | None = None,
@@ -217,7 +217,7 @@ class BinLaunch:
     inputs: tuple
 
 
-@torch.no_grad()
+@native.no_grad
 def prepare_bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, width: int, height: int, *,
                      conics: Tensor | None = None, tile_mode="radius") -> BinLaunch:
     mode = _mode(tile_mode, conics)
@@ -262,7 +262,7 @@ def _shape_key(launch: BinLaunch) -> tuple:
     return (launch.ranges.device.index, a.n, a.views, a.width, a.height, a.tile_mode)
 
 
-@torch.no_grad()
+@native.no_grad
 def emit_early(launch: BinLaunch) -> EarlyItems | None:
     """Enqueue the emission of group items before the totals are known, when
     an earlier frame of the same shape gave a capacity; None otherwise."""
@@ -296,7 +296,7 @@ def _remember_capacity(launch: BinLaunch, group_pairs: int) -> None:
     _CAPACITY[key] = max(want, int(stored * CAPACITY_DECAY)) if stored else want
 
 
-@torch.no_grad()
+@native.no_grad
 def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int,
                     early: EarlyItems | None = None) -> tuple[Tensor, Tensor]:
     """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs);
@@ -332,7 +332,7 @@ def bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, gro
     return launch_bin_rows(launch, group_pairs, tile_pairs)
 
 
-@torch.no_grad()
+@native.no_grad
 def pair_tiles(ranges: Tensor, count: int) -> Tensor:
     """Global tile id of every listed pair (uint32 values in int32 storage)."""
     tiles = torch.empty(count, dtype=torch.int32, device=ranges.device)
@@ -342,7 +342,7 @@ def pair_tiles(ranges: Tensor, count: int) -> Tensor:
     return tiles
 
 
-@torch.no_grad()
+@native.no_grad
 def expand_keys(sorted_tiles: Tensor, ids: Tensor, count: int, depths: Tensor, width: int, height: int) -> Tensor:
     """The reference's 64-bit keys (tile << 32 | depth bits) of sorted pairs."""
     n = depths.shape[-1]
@@ -354,7 +354,7 @@ def expand_keys(sorted_tiles: Tensor, ids: Tensor, count: int, depths: Tensor, w
     return keys
 
 
-@torch.no_grad()
+@native.no_grad
 def finish_binning(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, group_pairs: int,
                    tile_pairs: int, depths: Tensor, width: int, height: int, *, with_keys: bool = False,
                    conics: Tensor | None = None, tile_mode="radius") -> TileBins:
@@ -368,7 +368,7 @@ def finish_binning(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tenso
     return bins
 
 
-@torch.no_grad()
+@native.no_grad
 def bin_and_sort(centers: Tensor, radii: Tensor, tile_counts: Tensor, depths: Tensor, width: int, height: int,
                  bindings=None, *, conics: Tensor | None = None, tile_mode="radius",
                  with_keys: bool = False) -> TileBins:

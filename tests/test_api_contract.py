@@ -176,3 +176,24 @@ def test_depth_order_pass_count_and_key_bit_plan():
     finally:
         binning._KEY_BITS.clear()
         binning._KEY_BITS.update(saved)
+
+
+def test_launch_wrappers_run_without_gradients():
+    # native.no_grad turns gradients off inside the wrapped call (and only
+    # there), also when the caller already has them off.
+    from dsl_splat_amd.runtime import native
+
+    seen = []
+
+    @native.no_grad
+    def probe(x):
+        seen.append(torch.is_grad_enabled())
+        return x * 2
+
+    x = torch.ones(2, requires_grad=True)
+    y = probe(x)
+    assert seen == [False] and not y.requires_grad and torch.is_grad_enabled()
+    with torch.no_grad():
+        probe(x)
+    assert seen == [False, False] and torch.is_grad_enabled()
+    assert probe.__name__ == "probe"
