@@ -803,3 +803,34 @@ def test_forward_blend_clears_the_given_buffer(count):
     assert torch.equal(out.contributors, ref.contributors)
     assert bool((zero == 0).all())
     assert bool(buf[:4].isnan().all()) and bool(buf[4 + count:].isnan().all())
+
+
+def test_depth_order_plan_over_a_moving_camera():
+    # Frames of one shape whose depth ranges shrink and grow (the camera
+    # moves along its axis): every frame, planned from the one before, equals
+    # the same frame rendered with no plan, gradients included.
+    scene = _scene("sh3_720p")
+    _say("depth-order plan over a moving camera")
+    binning._KEY_BITS.clear()
+
+    def frame(viewmats, plan):
+        if not plan:
+            saved = dict(binning._KEY_BITS)
+            binning._KEY_BITS.clear()
+        means = scene.means.clone().requires_grad_(True)
+        out = gs3d.rasterize(means, scene.quats, scene.scales, scene.opacities, viewmats, scene.Ks,
+                             scene.width, scene.height, sh_coeffs=scene.sh_coeffs, sh_degree=3)
+        (out.features.sum() + out.alpha.sum()).backward()
+        if not plan:
+            binning._KEY_BITS.clear()
+            binning._KEY_BITS.update(saved)
+        return out.features, out.alpha, means.grad
+
+    for shift in (0.0, -1.5, 0.0, 3.0, 40.0, 0.5, -2.0, -2.0):
+        vm = scene.viewmats.clone()
+        vm[..., 2, 3] += shift
+        got = frame(vm, True)
+        want = frame(vm, False)
+        assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+        torch.testing.assert_close(got[2], want[2], rtol=1e-4, atol=1e-6 * float(want[2].abs().max().clamp(min=1.0)))
+    binning._KEY_BITS.clear()
