@@ -1656,13 +1656,19 @@ __global__ void chunk_group_kernel(const int32_t* __restrict__ chunk_base, int g
 // start as the scalar offset, and the buffer's range check stands in for the
 // id_limit test.  Tiles are walked in two halves so that each membership
 // test reads one 32-bit word of the item's mask.
-template <bool WRITE, bool MASKS, bool BUF = false>
+//
+// LISTS (write pass): 0 whole lists; 1 each tile's first list_cap(caps[t])
+// entries; 2 a redo pass, the whole lists of the tiles flagged in redo
+// (redo_count of them).
+template <bool WRITE, bool MASKS, bool BUF = false, int LISTS = 0>
 __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     const uint64_t* __restrict__ items, const uint64_t* __restrict__ masks, const int32_t* __restrict__ granges,
     const int32_t* __restrict__ chunk_base,
     const int32_t* __restrict__ chunk_group, int groups, int64_t max_chunks, GridDims d,
     uint32_t* __restrict__ counts, const int32_t* __restrict__ scanned, const int32_t* __restrict__ tile_start,
-    int32_t* __restrict__ ids, int64_t id_limit) {
+    int32_t* __restrict__ ids, int64_t id_limit, const int32_t* __restrict__ caps, const int32_t* __restrict__ redo,
+    const int32_t* __restrict__ redo_count) {
+    static_assert(LISTS == 0 || WRITE, "caps and redo flags are write-pass arguments");
     // A chunk's run for one tile, then one slot per lane that rejected items
     // are written to (so the writes need neither a branch nor an exec mask).
     __shared__ int32_t s_run[WRITE && BUF ? kBinWaves : 1][WRITE && BUF ? kChunk + 64 : 1];
@@ -1670,231 +1676,266 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     constexpr bool RECT_COUNT = !WRITE && !MASKS;
     __shared__ int32_t s_diff[RECT_COUNT ? kBinWaves : 1][RECT_COUNT ? 96 : 1];
     const int lane = lane_id();
-    const int64_t block = xcd_contiguous(blockIdx.x, gridDim.x);
-    const int64_t u = block * kBinWaves + (threadIdx.x >> 6);
-    if (u >= max_chunks) return;
-    if (u >= chunk_base[groups]) {
-        // Chunks beyond the last group's: their counts (the tail of the
-        // scanned table) are zero.
-        if constexpr (!WRITE) counts[u * 64 + lane] = 0u;
-        return;
-    }
-    if constexpr (RECT_COUNT) {
-        // Counts of a chunk of rectangle items: each item adds its
-        // rectangle's four corners to a difference grid; the 2D prefix sum of
-        // the grid at tile t is the number of items covering t.
-        int32_t* diff = s_diff[threadIdx.x >> 6];
+    // One chunk of items per wavefront.  A redo pass (LISTS 2) walks the
+    // chunks over a small grid and leaves at once when no tile is flagged.
+    auto pass = [&](const int64_t u) {
+        if (u >= max_chunks) return;
+        if (u >= chunk_base[groups]) {
+            // Chunks beyond the last group's: their counts (the tail of the
+            // scanned table) are zero.
+            if constexpr (!WRITE) counts[u * 64 + lane] = 0u;
+            return;
+        }
+        if constexpr (RECT_COUNT) {
+            // Counts of a chunk of rectangle items: each item adds its
+            // rectangle's four corners to a difference grid; the 2D prefix sum of
+            // the grid at tile t is the number of items covering t.
+            int32_t* diff = s_diff[threadIdx.x >> 6];
+            const int g = chunk_group[u];
+            const int32_t cb = chunk_base[g];
+            const int32_t q = chunk_base[g + 1] - cb;
+            const int32_t s = (int32_t)(u - cb);
+            const int64_t begin = (int64_t)granges[2 * g] + (int64_t)s * kChunk;
+            const int64_t end = min(begin + kChunk, (int64_t)granges[2 * g + 1]);
+            for (int e = lane; e < 96; e += 64) diff[e] = 0;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // All loads first, from clamped addresses (begin < end): a guarded
+            // load would be a branch that waits for its data.
+            uint64_t got[kChunkSteps];
+#pragma unroll
+            for (int k = 0; k < kChunkSteps; ++k) got[k] = items[min(begin + k * 64 + lane, end - 1)];
+            // Corners in row or column 8 lie outside the summed 8x8 part and are
+            // not added; items starting at the group's first tile (common: the
+            // rectangles clipped by the group's edges) add their corner with one
+            // atomic per step instead of as many serialised ones on one word.
+#pragma unroll
+            for (int k = 0; k < kChunkSteps; ++k) {
+                const bool in = begin + k * 64 + lane < end;
+                const uint32_t local = (uint32_t)(got[k] >> kGroupBits) & 0xFFFu;
+                const int lx0 = local & 7, lx1 = ((local >> 3) & 7) + 1, ly0 = (local >> 6) & 7,
+                          ly1 = ((local >> 9) & 7) + 1;
+                const uint64_t origin = __ballot(in && (lx0 | ly0) == 0);
+                if (origin && lane == (int)__builtin_ctzll(origin)) atomicAdd(&diff[0], (int)__popcll(origin));
+                if (in) {
+                    if ((lx0 | ly0) != 0) atomicAdd(&diff[ly0 * 9 + lx0], 1);
+                    if (lx1 < 8) atomicAdd(&diff[ly0 * 9 + lx1], -1);
+                    if (ly1 < 8) atomicAdd(&diff[ly1 * 9 + lx0], -1);
+                    if (lx1 < 8 && ly1 < 8) atomicAdd(&diff[ly1 * 9 + lx1], 1);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // Inclusive 2D prefix sum of the grid's 8x8 corner: along each row of
+            // 8 lanes, then down the columns (lanes 8 apart).
+            const int tx = lane & 7;
+            int32_t c = diff[(lane >> 3) * 9 + tx];
+#pragma unroll
+            for (int d = 1; d < 8; d <<= 1) {
+                const int32_t u = __shfl_up(c, d, 8);
+                if (tx >= d) c += u;
+            }
+#pragma unroll
+            for (int d = 8; d < 64; d <<= 1) {
+                const int32_t u = __shfl_up(c, d, 64);
+                if (lane >= d) c += u;
+            }
+            counts[(int64_t)cb * 64 + (int64_t)lane * q + s] = (uint32_t)c;
+            return;
+        }
+        int32_t* const run_lds = s_run[WRITE && BUF ? threadIdx.x >> 6 : 0];
         const int g = chunk_group[u];
         const int32_t cb = chunk_base[g];
         const int32_t q = chunk_base[g + 1] - cb;
         const int32_t s = (int32_t)(u - cb);
         const int64_t begin = (int64_t)granges[2 * g] + (int64_t)s * kChunk;
         const int64_t end = min(begin + kChunk, (int64_t)granges[2 * g + 1]);
-        for (int e = lane; e < 96; e += 64) diff[e] = 0;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // All loads first, from clamped addresses (begin < end): a guarded
-        // load would be a branch that waits for its data.
+        const int64_t slot = (int64_t)cb * 64 + (int64_t)lane * q;  // entry (g, lane, 0)
+        // Write pass: lane t's tile starts this chunk's run at init and keeps its
+        // first `limit` ids.  With caps, a tile keeps the first list_cap(caps[t])
+        // entries of its list; a redo pass writes only the flagged tiles, in
+        // full.  Chunks that no tile needs return before loading their items.
+        uint32_t init = 0, limit = 0xFFFFFFFFu;
+        uint64_t want_tiles = ~0ull;
+        if constexpr (WRITE) {
+            const int view = g / d.gpv, rem = g - view * d.gpv;
+            const int Y = rem / d.sgx, X = rem - Y * d.sgx;
+            const int ty = (Y << kGroupShift) + (lane >> 3), tx = (X << kGroupShift) + (lane & 7);
+            const bool inside = ty < d.gy && tx < d.gx;
+            const int64_t gt = (int64_t)view * d.tpv + ty * d.gx + tx;
+            // A redo pass reads its flags before anything else: most chunks have
+            // no flagged tile.
+            bool want = inside && (LISTS != 2 || redo[gt] != 0);
+            if (LISTS == 2 && __ballot(want) == 0) return;
+            if (inside) {
+                const uint32_t rel = (uint32_t)(scanned[slot + s] - scanned[slot]);
+                init = (uint32_t)tile_start[gt] + rel;
+                if constexpr (LISTS == 1) {
+                    const uint32_t cap = list_cap(caps[gt]);
+                    want = rel < cap;
+                    limit = want ? cap - rel : 0u;
+                }
+            }
+            if constexpr (LISTS != 0) {
+                want_tiles = __ballot(want);
+                if (want_tiles == 0) return;
+            }
+        }
+        uint64_t mask[kChunkSteps];
+        int32_t id[kChunkSteps];
+        uint64_t any = 0;
+        // All loads first, from clamped addresses (begin < end), then the lanes
+        // beyond the chunk's end are cleared.
         uint64_t got[kChunkSteps];
 #pragma unroll
-        for (int k = 0; k < kChunkSteps; ++k) got[k] = items[min(begin + k * 64 + lane, end - 1)];
-        // Corners in row or column 8 lie outside the summed 8x8 part and are
-        // not added; items starting at the group's first tile (common: the
-        // rectangles clipped by the group's edges) add their corner with one
-        // atomic per step instead of as many serialised ones on one word.
+        for (int k = 0; k < kChunkSteps; ++k) {
+            const int64_t i = min(begin + k * 64 + lane, end - 1);
+            got[k] = items[i];
+            if constexpr (MASKS) mask[k] = masks[i];
+        }
 #pragma unroll
         for (int k = 0; k < kChunkSteps; ++k) {
             const bool in = begin + k * 64 + lane < end;
-            const uint32_t local = (uint32_t)(got[k] >> kGroupBits) & 0xFFFu;
-            const int lx0 = local & 7, lx1 = ((local >> 3) & 7) + 1, ly0 = (local >> 6) & 7,
-                      ly1 = ((local >> 9) & 7) + 1;
-            const uint64_t origin = __ballot(in && (lx0 | ly0) == 0);
-            if (origin && lane == (int)__builtin_ctzll(origin)) atomicAdd(&diff[0], (int)__popcll(origin));
-            if (in) {
-                if ((lx0 | ly0) != 0) atomicAdd(&diff[ly0 * 9 + lx0], 1);
-                if (lx1 < 8) atomicAdd(&diff[ly0 * 9 + lx1], -1);
-                if (ly1 < 8) atomicAdd(&diff[ly1 * 9 + lx0], -1);
-                if (lx1 < 8 && ly1 < 8) atomicAdd(&diff[ly1 * 9 + lx1], 1);
-            }
+            if constexpr (!MASKS) mask[k] = group_tile_mask((uint32_t)(got[k] >> kGroupBits) & 0xFFFu);
+            if (!in) mask[k] = 0;
+            id[k] = in ? (int32_t)(got[k] >> 32) : 0;
+            any |= mask[k];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // Inclusive 2D prefix sum of the grid's 8x8 corner: along each row of
-        // 8 lanes, then down the columns (lanes 8 apart).
-        const int tx = lane & 7;
-        int32_t c = diff[(lane >> 3) * 9 + tx];
+        uint32_t mine = 0;
+        const uint64_t todo_all = LISTS != 0 ? wave_or64(any) & want_tiles : wave_or64(any);
+        // (unused unless WRITE && BUF)
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc(ids, (short)0, (int)(uint32_t)(BUF ? id_limit * 4 : 0), 0x00020000);
+        auto walk = [&](auto half) {
+            constexpr int H = decltype(half)::value;
+            uint32_t todo = (uint32_t)(todo_all >> (32 * H));
+            while (todo) {
+                const int tb = __builtin_ctz(todo);
+                todo &= todo - 1;
+                const int t = 32 * H + tb;
+                const uint32_t bit = 1u << tb;
+                const uint32_t start = WRITE ? (uint32_t)__builtin_amdgcn_readlane((int)init, t) : 0u;
+                const uint32_t lim = LISTS == 1 ? (uint32_t)__builtin_amdgcn_readlane((int)limit, t) : 0xFFFFFFFFu;
+                uint32_t run = WRITE && BUF ? 0u : start;
 #pragma unroll
-        for (int d = 1; d < 8; d <<= 1) {
-            const int32_t u = __shfl_up(c, d, 8);
-            if (tx >= d) c += u;
-        }
-#pragma unroll
-        for (int d = 8; d < 64; d <<= 1) {
-            const int32_t u = __shfl_up(c, d, 64);
-            if (lane >= d) c += u;
-        }
-        counts[(int64_t)cb * 64 + (int64_t)lane * q + s] = (uint32_t)c;
-        return;
-    }
-    int32_t* const run_lds = s_run[WRITE && BUF ? threadIdx.x >> 6 : 0];
-    const int g = chunk_group[u];
-    const int32_t cb = chunk_base[g];
-    const int32_t q = chunk_base[g + 1] - cb;
-    const int32_t s = (int32_t)(u - cb);
-    const int64_t begin = (int64_t)granges[2 * g] + (int64_t)s * kChunk;
-    const int64_t end = min(begin + kChunk, (int64_t)granges[2 * g + 1]);
-    const int64_t slot = (int64_t)cb * 64 + (int64_t)lane * q;  // entry (g, lane, 0)
-    uint64_t mask[kChunkSteps];
-    int32_t id[kChunkSteps];
-    uint64_t any = 0;
-    // All loads first, from clamped addresses (begin < end), then the lanes
-    // beyond the chunk's end are cleared.
-    uint64_t got[kChunkSteps];
-#pragma unroll
-    for (int k = 0; k < kChunkSteps; ++k) {
-        const int64_t i = min(begin + k * 64 + lane, end - 1);
-        got[k] = items[i];
-        if constexpr (MASKS) mask[k] = masks[i];
-    }
-#pragma unroll
-    for (int k = 0; k < kChunkSteps; ++k) {
-        const bool in = begin + k * 64 + lane < end;
-        if constexpr (!MASKS) mask[k] = group_tile_mask((uint32_t)(got[k] >> kGroupBits) & 0xFFFu);
-        if (!in) mask[k] = 0;
-        id[k] = in ? (int32_t)(got[k] >> 32) : 0;
-        any |= mask[k];
-    }
-    uint32_t init = 0;
-    if constexpr (WRITE) {
-        const int view = g / d.gpv, rem = g - view * d.gpv;
-        const int Y = rem / d.sgx, X = rem - Y * d.sgx;
-        const int ty = (Y << kGroupShift) + (lane >> 3), tx = (X << kGroupShift) + (lane & 7);
-        if (ty < d.gy && tx < d.gx)
-            init = (uint32_t)(tile_start[(int64_t)view * d.tpv + ty * d.gx + tx] + (scanned[slot + s] - scanned[slot]));
-    }
-    uint32_t mine = 0;
-    const uint64_t todo_all = wave_or64(any);
-    // (unused unless WRITE && BUF)
-    const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(ids, (short)0, (int)(uint32_t)(BUF ? id_limit * 4 : 0), 0x00020000);
-    auto walk = [&](auto half) {
-        constexpr int H = decltype(half)::value;
-        uint32_t todo = (uint32_t)(todo_all >> (32 * H));
-        while (todo) {
-            const int tb = __builtin_ctz(todo);
-            todo &= todo - 1;
-            const int t = 32 * H + tb;
-            const uint32_t bit = 1u << tb;
-            const uint32_t start = WRITE ? (uint32_t)__builtin_amdgcn_readlane((int)init, t) : 0u;
-            uint32_t run = WRITE && BUF ? 0u : start;
-#pragma unroll
-            for (int k = 0; k < kChunkSteps; ++k) {
-                const uint32_t word = H ? (uint32_t)(mask[k] >> 32) : (uint32_t)mask[k];
-                const bool has = (word & bit) != 0u;
-                const uint64_t b = __ballot(has);
+                for (int k = 0; k < kChunkSteps; ++k) {
+                    const uint32_t word = H ? (uint32_t)(mask[k] >> 32) : (uint32_t)mask[k];
+                    const bool has = (word & bit) != 0u;
+                    const uint64_t b = __ballot(has);
+                    if constexpr (WRITE && BUF) {
+                        const uint32_t rank =
+                            __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+                        run_lds[has ? run + rank : (uint32_t)(kChunk + lane)] = id[k];
+                        run += (uint32_t)__popcll(b);
+                    } else if (b) {
+                        if constexpr (WRITE) {
+                            if (has) {
+                                const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
+                                    (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+                                const int64_t pos = (int64_t)run + rank;
+                                if (pos < id_limit && (uint32_t)(pos - start) < lim)
+                                    ids[pos] = id[k];  // plain: short runs per tile, merged in L2
+                            }
+                        }
+                        run += (uint32_t)__popcll(b);
+                    }
+                }
                 if constexpr (WRITE && BUF) {
+                    // The run is complete in LDS: store it with consecutive lanes.
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    const uint32_t keep = min(run, lim);
+                    for (uint32_t e = (uint32_t)lane; e < keep; e += 64)
+                        __builtin_amdgcn_raw_buffer_store_b32(run_lds[e], rsrc, (int)(e * 4u), (int)(start * 4u), 0);
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                }
+                if (lane == t) mine = run;
+            }
+        };
+        // Buffered write: the tiles of each half are visited from the highest bit
+        // down and every step's mask word is shifted left as the walk proceeds, so
+        // one add of the word to itself both advances it and yields the tile's
+        // membership bit as its carry (the carry mask is the ballot).  Each step
+        // then costs the carry add, the two-part lane count, one address and one
+        // select; non-members write to their own slot beyond the run.
+        auto walk_buf = [&](auto half) {
+            constexpr int H = decltype(half)::value;
+            static_assert(kChunk % 128 == 0, "store loop reads two 64-word rows below kChunk");
+            uint32_t todo = (uint32_t)(todo_all >> (32 * H));
+            uint32_t w[kChunkSteps];
+#pragma unroll
+            for (int k = 0; k < kChunkSteps; ++k) w[k] = (uint32_t)(mask[k] >> (32 * H));
+            using lds_i32 = __attribute__((address_space(3))) int32_t;
+            // LDS byte addresses: the slice's first word (wave-uniform) and this
+            // lane's spare slot.
+            const uint32_t slice_word =
+                (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(uintptr_t)(lds_i32*)run_lds >> 2));
+            const uint32_t spare = (slice_word + (uint32_t)(kChunk + lane)) << 2;
+            int top = 31;  // bit of the original word now at bit 31 of w[]
+            while (todo) {
+                const int tb = 31 - __builtin_clz(todo);
+                todo ^= 1u << tb;
+                const int sh = top - tb;
+                if (sh != 0) {
+#pragma unroll
+                    for (int k = 0; k < kChunkSteps; ++k) w[k] <<= sh;
+                }
+                top = tb - 1;
+                const int t = 32 * H + tb;
+                const uint32_t start = (uint32_t)__builtin_amdgcn_readlane((int)init, t);
+                const uint32_t lim = LISTS == 1 ? (uint32_t)__builtin_amdgcn_readlane((int)limit, t) : 0xFFFFFFFFu;
+                uint32_t end_word = slice_word;  // LDS word after the run so far
+#pragma unroll
+                for (int k = 0; k < kChunkSteps; ++k) {
+                    // b = carry mask of w + w: lanes whose item covers tile t.
+                    uint32_t next;
+                    uint64_t b;
+                    asm volatile("v_add_co_u32_e64 %0, %1, %2, %2" : "=v"(next), "=s"(b) : "v"(w[k]));
+                    w[k] = next;
                     const uint32_t rank =
                         __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-                    run_lds[has ? run + rank : (uint32_t)(kChunk + lane)] = id[k];
-                    run += (uint32_t)__popcll(b);
-                } else if (b) {
-                    if constexpr (WRITE) {
-                        if (has) {
-                            const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
-                                (uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-                            const int64_t pos = (int64_t)run + rank;
-                            if (pos < id_limit) ids[pos] = id[k];  // plain: short runs per tile, merged in L2
-                        }
-                    }
-                    run += (uint32_t)__popcll(b);
+                    const uint32_t member = (rank + end_word) << 2;
+                    uint32_t at;
+                    asm volatile("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(at) : "v"(spare), "v"(member), "s"(b));
+                    *(lds_i32*)(uintptr_t)at = id[k];
+                    end_word += (uint32_t)__popcll(b);
                 }
-            }
-            if constexpr (WRITE && BUF) {
-                // The run is complete in LDS: store it with consecutive lanes.
+                const uint32_t run = min(end_word - slice_word, lim);  // ids this chunk keeps for tile t
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
-                for (uint32_t e = (uint32_t)lane; e < run; e += 64)
-                    __builtin_amdgcn_raw_buffer_store_b32(run_lds[e], rsrc, (int)(e * 4u), (int)(start * 4u), 0);
+                // Two LDS reads in flight per lane before the stores: a run holds
+                // at most kChunk ids, so e0 <= kChunk - 128 and both reads stay in
+                // the slice (words past the run are read but not stored).
+                for (uint32_t e0 = 0; e0 < run; e0 += 128) {
+                    const uint32_t e1 = e0 + (uint32_t)lane, e2 = e1 + 64u;
+                    int32_t v1 = run_lds[e1], v2 = run_lds[e2];
+                    asm volatile("" : "+v"(v1), "+v"(v2));  // both reads issued before either store
+                    if (e1 < run) __builtin_amdgcn_raw_buffer_store_b32(v1, rsrc, (int)(e1 * 4u), (int)(start * 4u), 0);
+                    if (e2 < run) __builtin_amdgcn_raw_buffer_store_b32(v2, rsrc, (int)(e2 * 4u), (int)(start * 4u), 0);
+                }
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
             }
-            if (lane == t) mine = run;
+        };
+        if constexpr (WRITE && BUF) {
+            walk_buf(std::integral_constant<int, 0>{});
+            walk_buf(std::integral_constant<int, 1>{});
+        } else {
+            walk(std::integral_constant<int, 0>{});
+            walk(std::integral_constant<int, 1>{});
         }
+        if constexpr (!WRITE) counts[slot + s] = mine;
     };
-    // Buffered write: the tiles of each half are visited from the highest bit
-    // down and every step's mask word is shifted left as the walk proceeds, so
-    // one add of the word to itself both advances it and yields the tile's
-    // membership bit as its carry (the carry mask is the ballot).  Each step
-    // then costs the carry add, the two-part lane count, one address and one
-    // select; non-members write to their own slot beyond the run.
-    auto walk_buf = [&](auto half) {
-        constexpr int H = decltype(half)::value;
-        static_assert(kChunk % 128 == 0, "store loop reads two 64-word rows below kChunk");
-        uint32_t todo = (uint32_t)(todo_all >> (32 * H));
-        uint32_t w[kChunkSteps];
-#pragma unroll
-        for (int k = 0; k < kChunkSteps; ++k) w[k] = (uint32_t)(mask[k] >> (32 * H));
-        using lds_i32 = __attribute__((address_space(3))) int32_t;
-        // LDS byte addresses: the slice's first word (wave-uniform) and this
-        // lane's spare slot.
-        const uint32_t slice_word =
-            (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(uintptr_t)(lds_i32*)run_lds >> 2));
-        const uint32_t spare = (slice_word + (uint32_t)(kChunk + lane)) << 2;
-        int top = 31;  // bit of the original word now at bit 31 of w[]
-        while (todo) {
-            const int tb = 31 - __builtin_clz(todo);
-            todo ^= 1u << tb;
-            const int sh = top - tb;
-            if (sh != 0) {
-#pragma unroll
-                for (int k = 0; k < kChunkSteps; ++k) w[k] <<= sh;
-            }
-            top = tb - 1;
-            const int t = 32 * H + tb;
-            const uint32_t start = (uint32_t)__builtin_amdgcn_readlane((int)init, t);
-            uint32_t end_word = slice_word;  // LDS word after the run so far
-#pragma unroll
-            for (int k = 0; k < kChunkSteps; ++k) {
-                // b = carry mask of w + w: lanes whose item covers tile t.
-                uint32_t next;
-                uint64_t b;
-                asm volatile("v_add_co_u32_e64 %0, %1, %2, %2" : "=v"(next), "=s"(b) : "v"(w[k]));
-                w[k] = next;
-                const uint32_t rank =
-                    __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-                const uint32_t member = (rank + end_word) << 2;
-                uint32_t at;
-                asm volatile("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(at) : "v"(spare), "v"(member), "s"(b));
-                *(lds_i32*)(uintptr_t)at = id[k];
-                end_word += (uint32_t)__popcll(b);
-            }
-            const uint32_t run = end_word - slice_word;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            // Two LDS reads in flight per lane before the stores: a run holds
-            // at most kChunk ids, so e0 <= kChunk - 128 and both reads stay in
-            // the slice (words past the run are read but not stored).
-            for (uint32_t e0 = 0; e0 < run; e0 += 128) {
-                const uint32_t e1 = e0 + (uint32_t)lane, e2 = e1 + 64u;
-                int32_t v1 = run_lds[e1], v2 = run_lds[e2];
-                asm volatile("" : "+v"(v1), "+v"(v2));  // both reads issued before either store
-                if (e1 < run) __builtin_amdgcn_raw_buffer_store_b32(v1, rsrc, (int)(e1 * 4u), (int)(start * 4u), 0);
-                if (e2 < run) __builtin_amdgcn_raw_buffer_store_b32(v2, rsrc, (int)(e2 * 4u), (int)(start * 4u), 0);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-        }
-    };
-    if constexpr (WRITE && BUF) {
-        walk_buf(std::integral_constant<int, 0>{});
-        walk_buf(std::integral_constant<int, 1>{});
+    if constexpr (LISTS == 2) {
+        if (*redo_count == 0) return;
+        const int64_t waves = (int64_t)gridDim.x * kBinWaves;
+        for (int64_t u = (int64_t)blockIdx.x * kBinWaves + (threadIdx.x >> 6); u < max_chunks; u += waves) pass(u);
     } else {
-        walk(std::integral_constant<int, 0>{});
-        walk(std::integral_constant<int, 1>{});
+        pass(xcd_contiguous(blockIdx.x, gridDim.x) * kBinWaves + (threadIdx.x >> 6));
     }
-    if constexpr (!WRITE) counts[slot + s] = mine;
 }
 
 // Pairs of every global tile: sum over its group's chunks.
@@ -2331,6 +2372,9 @@ inline void emit_group_items(const gs3d_bin_args& a, const GridDims& d, int64_t 
 
 // gs3d_bin_rows; with `emitted` the group items are already in the scratch
 // (gs3d_emit_group_items with a capacity of at least group_pairs).
+int write_pass(const gs3d_bin_args& a, const BinScratch& sc, const uint64_t* items, int64_t groups, int64_t chunks,
+               const GridDims& d, const int32_t* caps, const int32_t* redo, const int32_t* redo_count, hipStream_t s);
+
 int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream, bool emitted) {
     if (!args) return GS3D_ERR_ARGUMENT;
     const gs3d_bin_args& a = *args;
@@ -2402,11 +2446,13 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
     if (accu)
         hipLaunchKernelGGL((gs3d::group_pass_kernel<false, true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,
                            sc.masks, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts,
-                           (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0);
+                           (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0,
+                           (const int32_t*)nullptr, (const int32_t*)nullptr, (const int32_t*)nullptr);
     else
         hipLaunchKernelGGL((gs3d::group_pass_kernel<false, false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,
                            (const uint64_t*)nullptr, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d,
-                           sc.counts, (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0);
+                           sc.counts, (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0,
+                           (const int32_t*)nullptr, (const int32_t*)nullptr, (const int32_t*)nullptr);
     status = gs3d::run_scan<uint32_t, false>(sc.counts, 64 * chunks, sc.scanned, nullptr, sc.scan, s);
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL(gs3d::tile_totals_kernel, dim3(gs3d::blocks_for(tiles, 256)), dim3(256), 0, s, sc.chunk_base,
@@ -2415,12 +2461,30 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL(gs3d::tile_ranges_from_totals_kernel, dim3(gs3d::blocks_for(tiles, 256)), dim3(256), 0, s,
                        sc.totals, sc.starts, tiles, a.ranges);
+    return write_pass(a, sc, items, groups, chunks, d, a.caps, nullptr, nullptr, s);
+}
+
+// The id-write pass over binning state left in the scratch by bin_rows (the
+// sorted group items at `items`, group ranges, chunk tables, scanned counts,
+// tile starts): every tile's list, the first list_cap(caps[t]) entries of it
+// with caps, only the tiles flagged in redo (whole lists; redo_count of
+// them) with redo.
+constexpr unsigned kRedoPassGrid = 1024;
+
+template <int LISTS>
+void launch_write_pass(const gs3d_bin_args& a, const BinScratch& sc, const uint64_t* items, int64_t groups,
+                       int64_t chunks, const GridDims& d, const int32_t* caps, const int32_t* redo,
+                       const int32_t* redo_count, hipStream_t s) {
+    const bool accu = a.tile_mode == GS3D_TILE_ACCUTILE;
+    const unsigned blocks = (unsigned)blocks_for(chunks, kBinWaves);
+    const dim3 pass_grid(LISTS == 2 ? min(blocks, kRedoPassGrid) : blocks);
     // Buffer stores address the id list with 32-bit byte offsets.
     const bool buf = a.tile_pairs <= (int64_t)(0xFFFFFFFFu / 4);
 #define GS3D_WRITE_PASS(M, B)                                                                                      \
-    hipLaunchKernelGGL((gs3d::group_pass_kernel<true, M, B>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,     \
+    hipLaunchKernelGGL((group_pass_kernel<true, M, B, LISTS>), pass_grid, dim3(kBinThreads), 0, s, items,          \
                        M ? (const uint64_t*)sc.masks : nullptr, sc.granges, sc.chunk_base, sc.chunk_group,        \
-                       (int)groups, chunks, d, sc.counts, sc.scanned, sc.starts, a.ids, a.tile_pairs)
+                       (int)groups, chunks, d, sc.counts, sc.scanned, sc.starts, a.ids, a.tile_pairs, caps, redo, \
+                       redo_count)
     if (accu) {
         if (buf)
             GS3D_WRITE_PASS(true, true);
@@ -2433,13 +2497,50 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
             GS3D_WRITE_PASS(false, false);
     }
 #undef GS3D_WRITE_PASS
-    return gs3d::launch_status("gs3d_bin_rows");
+}
+
+int write_pass(const gs3d_bin_args& a, const BinScratch& sc, const uint64_t* items, int64_t groups, int64_t chunks,
+               const GridDims& d, const int32_t* caps, const int32_t* redo, const int32_t* redo_count, hipStream_t s) {
+    if (redo)
+        launch_write_pass<2>(a, sc, items, groups, chunks, d, nullptr, redo, redo_count, s);
+    else if (caps)
+        launch_write_pass<1>(a, sc, items, groups, chunks, d, caps, nullptr, nullptr, s);
+    else
+        launch_write_pass<0>(a, sc, items, groups, chunks, d, nullptr, nullptr, nullptr, s);
+    return launch_status("gs3d_bin_rows");
 }
 
 }  // namespace gs3d
 
 extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream) {
     return gs3d::bin_rows(args, scratch, scratch_bytes, stream, false);
+}
+
+extern "C" int gs3d_bin_redo(const gs3d_bin_args* args, const int32_t* redo, const int32_t* redo_list,
+                             void* scratch, size_t scratch_bytes, void* stream) {
+    if (!args || !redo || !redo_list) return GS3D_ERR_ARGUMENT;
+    const gs3d_bin_args& a = *args;
+    if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0 || a.group_pairs < 0 || a.tile_pairs < 0)
+        return GS3D_ERR_ARGUMENT;
+    const gs3d::GridDims d = gs3d::grid_dims(a.width, a.height);
+    const int64_t rows = (int64_t)a.n * a.views;
+    const int64_t groups = (int64_t)a.views * d.gpv, tiles = (int64_t)a.views * d.tpv;
+    if (tiles == 0 || a.group_pairs == 0 || a.tile_pairs == 0 || rows == 0) return GS3D_OK;
+    if (rows > INT32_MAX || a.group_pairs > INT32_MAX || a.tile_pairs > INT32_MAX) return GS3D_ERR_OVERFLOW;
+    if (groups >= (int64_t)1 << gs3d::kGroupBits || d.gx >= 0xFFFF || d.gy >= 0xFFFF) return GS3D_ERR_UNSUPPORTED;
+    if (!a.ids || !scratch) return GS3D_ERR_ARGUMENT;
+    if (scratch_bytes < gs3d_bin_rows_scratch_bytes(a.group_pairs, a.views, a.width, a.height, a.tile_mode))
+        return GS3D_ERR_SCRATCH;
+    const bool accu = a.tile_mode == GS3D_TILE_ACCUTILE;
+    gs3d::BinScratch sc;
+    gs3d::bin_scratch_bytes(a.group_pairs, groups, tiles, accu, &sc, scratch);
+    const int64_t S = a.group_pairs;
+    const int group_bits = gs3d::bit_length(groups - 1 > 0 ? groups - 1 : 1);
+    // Where bin_rows left the sorted items: the second half after the
+    // one-pass group sort, the first otherwise.
+    const uint64_t* items = !accu && group_bits <= gs3d::kOnePassBits ? sc.items + S : sc.items;
+    return gs3d::write_pass(a, sc, items, groups, gs3d::max_chunks_of(S, groups), d, nullptr, redo, redo_list,
+                            gs3d::as_stream(stream));
 }
 
 extern "C" int gs3d_emit_group_items(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream) {

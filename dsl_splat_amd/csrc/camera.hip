@@ -46,14 +46,34 @@ __device__ float inverse44(const float* m, float* inv) {
     return m[0] * inv[0] + m[1] * inv[4] + m[2] * inv[8] + m[3] * inv[12];
 }
 
+// A 64-bit key of one camera's view matrix and intrinsics: each value
+// rounded to 12 mantissa bits (so a pose that moves by a small optimiser
+// step keeps its key), signed zeros merged, the words mixed by
+// multiply-xorshift rounds.  Equal cameras get equal keys; distinct cameras
+// share one only by a collision, which costs the caller no more than a stale
+// hint.
+__device__ uint64_t camera_key(const float* V, const float* K) {
+    uint64_t h = 0x243F6A8885A308D3ull;
+    auto mix = [&](float v) {
+        uint32_t w = __float_as_uint(v);
+        w = (w & 0x7FFFFFFFu) == 0u ? 0u : (w + 0x400u) & ~0x7FFu;
+        h = (h ^ w) * 0xD6E8FEB86659FD93ull;
+        h ^= h >> 32;
+    };
+    for (int e = 0; e < 16; ++e) mix(V[e]);
+    for (int e = 0; e < 9; ++e) mix(K[e]);
+    return h;
+}
+
 __global__ void camera_prepare_kernel(const float* __restrict__ views, const float* __restrict__ Ks, int count,
                                       int width, int height, int with_centers, float* __restrict__ full,
                                       float* __restrict__ inverse, float* __restrict__ centers,
-                                      int32_t* __restrict__ errors) {
+                                      int32_t* __restrict__ errors, uint64_t* __restrict__ keys) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
     const float* K = Ks + 9 * i;
     const float* V = views + 16 * i;
+    if (keys) keys[i] = camera_key(V, K);
     bool finite = true;
     for (int e = 0; e < 9; ++e) finite = finite && finite_f(K[e]);
     int error = 0;
@@ -122,16 +142,24 @@ __global__ void camera_backward_kernel(const float* __restrict__ Ks, const float
 
 }  // namespace gs3d
 
-extern "C" int gs3d_camera_prepare(const float* views, const float* Ks, int32_t count, int32_t width,
-                                   int32_t height, int32_t with_centers, float* full, float* inverse,
-                                   float* centers, int32_t* errors, void* stream) {
+extern "C" int gs3d_camera_prepare_keyed(const float* views, const float* Ks, int32_t count, int32_t width,
+                                         int32_t height, int32_t with_centers, float* full, float* inverse,
+                                         float* centers, int32_t* errors, uint64_t* keys, void* stream) {
     if (count < 0 || width <= 0 || height <= 0) return GS3D_ERR_ARGUMENT;
     if (count == 0) return GS3D_OK;
     if (!views || !Ks || !full || !errors || (with_centers && (!inverse || !centers))) return GS3D_ERR_ARGUMENT;
+    if (reinterpret_cast<uintptr_t>(keys) & 7) return GS3D_ERR_ARGUMENT;
     hipLaunchKernelGGL(gs3d::camera_prepare_kernel, dim3(gs3d::blocks_for(count, 64)), dim3(64), 0,
                        gs3d::as_stream(stream), views, Ks, count, width, height, with_centers, full, inverse,
-                       centers, errors);
+                       centers, errors, keys);
     return gs3d::launch_status("gs3d_camera_prepare");
+}
+
+extern "C" int gs3d_camera_prepare(const float* views, const float* Ks, int32_t count, int32_t width,
+                                   int32_t height, int32_t with_centers, float* full, float* inverse,
+                                   float* centers, int32_t* errors, void* stream) {
+    return gs3d_camera_prepare_keyed(views, Ks, count, width, height, with_centers, full, inverse, centers, errors,
+                                     nullptr, stream);
 }
 
 extern "C" int gs3d_camera_backward(const float* Ks, const float* grad_full, int32_t width, int32_t height,

@@ -224,6 +224,14 @@ GS3D_DEV int wave_sum_rows_value(int lane) {
 
 GS3D_DEV int lane_id() { return __lane_id(); }
 
+// Length of a tile's list that the id-write pass writes and the forward
+// blend reads when the tile's previous frame stopped after `stop` entries
+// (all its pixels terminated by then); a negative stop (the tile needed its
+// whole list) gives no cap.
+GS3D_DEV uint32_t list_cap(int32_t stop) {
+    return stop < 0 ? 0xFFFFFFFFu : (uint32_t)stop + ((uint32_t)stop >> 2) + 128u;
+}
+
 // ---------------------------------------------------------------------------
 // Tile rectangle of a projected Gaussian, splatting/geometry.py:22-30
 // (truncating conversions, then clamping to the tile grid).

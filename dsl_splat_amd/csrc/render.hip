@@ -97,7 +97,7 @@ GS3D_DEV void pixel_of(int t, int k, int& x, int& y) {
 }
 
 struct TileInfo {
-    int view, x0, y0, first, last;
+    int view, x0, y0, first, last, tile;
 };
 
 // Workgroups go to the 8 XCDs in turn; within every run of 8 * GS3D_TILE_CHUNK
@@ -116,10 +116,9 @@ GS3D_DEV int tile_of_block(int b, int blocks) {
     return run * R + (w & 7) * C + (w >> 3);
 }
 
-GS3D_DEV TileInfo tile_info(const gs3d_render_args& a) {
+GS3D_DEV TileInfo tile_info(const gs3d_render_args& a, int tile) {
     const int gx = (a.width + kTile - 1) / kTile, gy = (a.height + kTile - 1) / kTile;
     const int per_view = gx * gy;
-    const int tile = tile_of_block(blockIdx.x, gridDim.x);
     TileInfo t;
     t.view = tile / per_view;
     const int local = tile - t.view * per_view;
@@ -128,8 +127,11 @@ GS3D_DEV TileInfo tile_info(const gs3d_render_args& a) {
     t.y0 = ty * kTile;
     t.first = a.ranges[2 * (int64_t)tile];
     t.last = a.ranges[2 * (int64_t)tile + 1];
+    t.tile = tile;
     return t;
 }
+
+GS3D_DEV TileInfo tile_info(const gs3d_render_args& a) { return tile_info(a, tile_of_block(blockIdx.x, gridDim.x)); }
 
 // Lowest power at which opacity o can still give alpha >= 1/255 (see the
 // file comment); +inf rejects everything (o <= 0), -inf rejects nothing.
@@ -424,7 +426,13 @@ GS3D_DEV void observe_statistics(const gs3d_render_stats_args& st, int dst_r, fl
 // rounded up to 1, 2, 4 or 8), so that only their pixel values take
 // registers; KINDS: their kinds as a sum mask for one or two requests (the
 // observer then needs no per-request selects), -1 otherwise.
-template <int CH, int PIX, int MODE, int RB = 1, int KINDS = -1>
+//
+// LISTS (MODE 0): 0 whole lists; 1 lists capped by gs3d_render_args.caps
+// and/or stops reported (stop_out, redo flags); 2 a redo launch
+// (gs3d_render_args.redo_pass), whose workgroups walk the tiles listed by the
+// capped launch.  Only the instantiations that use them carry the stop
+// tracking and the loop.
+template <int CH, int PIX, int MODE, int RB = 1, int KINDS = -1, int LISTS = 0>
 __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_eu(CH <= 4 ? 6 : CH <= 8 ? 5 : 1))) void render_fwd_kernel(gs3d_render_args a, gs3d_render_stats_args st, int c0, unsigned long long* counts) {
     constexpr bool STATS = MODE == 1, COUNTS = MODE == 2;
     constexpr int NT = kTilePixels / PIX;
@@ -433,257 +441,309 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     __shared__ uint32_t s_mask[B];
     // Per staged Gaussian: the tile's totals of every statistics request.
     __shared__ float s_stat[STATS ? B * RB : 1];
-    const TileInfo t = tile_info(a);
-    const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
-    const int lane = lane_id(), wave = threadIdx.x >> 6;
-    if constexpr (STATS)
-        for (int e = threadIdx.x; e < B * RB; e += NT) s_stat[e] = 0.0f;
-    if (c0 == 0 && a.zero_out) {
-        // The blend VJP's accumulation buffers, cleared by the first
-        // window's launch: the stores drain while the blend computes.
-        typedef float zero4 __attribute__((ext_vector_type(4)));
-        const int64_t n4 = a.zero_count >> 2;
-        zero4* z = reinterpret_cast<zero4*>(a.zero_out);
-        const int64_t step = (int64_t)gridDim.x * NT;
-        for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n4; i += step)
-            __builtin_nontemporal_store(zero4{0.0f, 0.0f, 0.0f, 0.0f}, z + i);
-        if (blockIdx.x == 0 && threadIdx.x < (a.zero_count & 3)) a.zero_out[(n4 << 2) + threadIdx.x] = 0.0f;
-    }
-    float fx[PIX], fy[PIX], T[PIX], color[PIX][CH];
-    int px[PIX], py[PIX], last_contributor[PIX];
-    bool done[PIX];
-    float val[PIX][STATS ? RB : 1];
-    int visited[PIX];
-    uint32_t evaluated = 0, accepted = 0;
-#pragma unroll
-    for (int k = 0; k < PIX; ++k) {
-        int lx, ly;
-        pixel_of<PIX>(threadIdx.x, k, lx, ly);
-        px[k] = t.x0 + lx;
-        py[k] = t.y0 + ly;
-        fx[k] = (float)px[k];
-        fy[k] = (float)py[k];
-        done[k] = !(px[k] < a.width && py[k] < a.height);
-        visited[k] = done[k] ? 0 : t.last - t.first;  // the whole list unless the pixel terminates
-        T[k] = 1.0f;
-        last_contributor[k] = 0;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) color[k][c] = 0.0f;
-        if constexpr (STATS) {
-            const float* pv = st.pixel_values + t.view * st.pixel_view_stride + (int64_t)py[k] * a.width + px[k];
-            const int64_t plane = (int64_t)a.width * a.height;
-#pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                const float v = (r < st.requests && !done[k]) ? pv[r * plane] : 0.0f;
-                // Count requests keep a 0/1 mask (see observe_statistics).
-                val[k][r] = ((st.sum_mask >> r) & 1u) ? v : (v != 0.0f ? 1.0f : 0.0f);
+    static_assert(LISTS == 0 || MODE == 0, "capped lists neither count pairs nor total statistics");
+    // The blend of one tile: a normal launch blends the tile of its
+    // workgroup, a redo launch walks the tiles that the capped launch listed.
+    auto blend = [&](const TileInfo t) {
+        // With caps the tile's list is read up to list_cap of its previous stop
+        // (the id-write pass wrote that far); a redo reads whole lists.
+        int last = t.last;
+        bool capped = false;
+        if constexpr (LISTS == 1) {
+            if (a.caps) {
+                const uint32_t cap = list_cap(a.caps[t.tile]);
+                if ((uint32_t)(t.last - t.first) > cap) {
+                    last = t.first + (int)cap;
+                    capped = true;
+                }
             }
         }
-    }
-    // Each thread stages at most one Gaussian per batch (B <= NT); its index
-    // for the next batch is loaded while the current batch blends (clamped
-    // into the list, so the load is unconditional).
-    static_assert(B <= NT, "one staged Gaussian per thread and batch");
-    int32_t next_id = t.last > t.first ? a.ids[min(t.first + (int)threadIdx.x, t.last - 1)] : 0;
-    int stat_r = -1;
-    bool stat_finite = true;
-    // The Gaussian this thread staged for the batch being blended, whose
-    // statistics slot it flushes (-1: none).
-    int32_t flush_id = -1;
-    auto flush = [&]() {
+        const int D = a.feat_channels + a.extra_channels + (a.one_tail ? 1 : 0);
+        const int lane = lane_id(), wave = threadIdx.x >> 6;
+        if constexpr (STATS)
+            for (int e = threadIdx.x; e < B * RB; e += NT) s_stat[e] = 0.0f;
+        if (c0 == 0 && a.zero_out) {
+            // The blend VJP's accumulation buffers, cleared by the first
+            // window's launch: the stores drain while the blend computes.
+            typedef float zero4 __attribute__((ext_vector_type(4)));
+            const int64_t n4 = a.zero_count >> 2;
+            zero4* z = reinterpret_cast<zero4*>(a.zero_out);
+            const int64_t step = (int64_t)gridDim.x * NT;
+            for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n4; i += step)
+                __builtin_nontemporal_store(zero4{0.0f, 0.0f, 0.0f, 0.0f}, z + i);
+            if (blockIdx.x == 0 && threadIdx.x < (a.zero_count & 3)) a.zero_out[(n4 << 2) + threadIdx.x] = 0.0f;
+        }
+        float fx[PIX], fy[PIX], T[PIX], color[PIX][CH];
+        int px[PIX], py[PIX], last_contributor[PIX];
+        bool done[PIX];
+        float val[PIX][STATS ? RB : 1];
+        int visited[PIX];
+        uint32_t evaluated = 0, accepted = 0;
+#pragma unroll
+        for (int k = 0; k < PIX; ++k) {
+            int lx, ly;
+            pixel_of<PIX>(threadIdx.x, k, lx, ly);
+            px[k] = t.x0 + lx;
+            py[k] = t.y0 + ly;
+            fx[k] = (float)px[k];
+            fy[k] = (float)py[k];
+            done[k] = !(px[k] < a.width && py[k] < a.height);
+            visited[k] = done[k] ? 0 : last - t.first;  // the whole list unless the pixel terminates
+            T[k] = 1.0f;
+            last_contributor[k] = 0;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) color[k][c] = 0.0f;
+            if constexpr (STATS) {
+                const float* pv = st.pixel_values + t.view * st.pixel_view_stride + (int64_t)py[k] * a.width + px[k];
+                const int64_t plane = (int64_t)a.width * a.height;
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    const float v = (r < st.requests && !done[k]) ? pv[r * plane] : 0.0f;
+                    // Count requests keep a 0/1 mask (see observe_statistics).
+                    val[k][r] = ((st.sum_mask >> r) & 1u) ? v : (v != 0.0f ? 1.0f : 0.0f);
+                }
+            }
+        }
+        // Each thread stages at most one Gaussian per batch (B <= NT); its index
+        // for the next batch is loaded while the current batch blends (clamped
+        // into the list, so the load is unconditional).
+        static_assert(B <= NT, "one staged Gaussian per thread and batch");
+        int32_t next_id = last > t.first ? a.ids[min(t.first + (int)threadIdx.x, last - 1)] : 0;
+        int stat_r = -1;
+        bool stat_finite = true;
+        // The Gaussian this thread staged for the batch being blended, whose
+        // statistics slot it flushes (-1: none).
+        int32_t flush_id = -1;
+        auto flush = [&]() {
+            if constexpr (STATS) {
+                if (flush_id >= 0) flush_statistics<RB>(st, t.view, a.n, flush_id, &s_stat[threadIdx.x * RB]);
+                flush_id = -1;
+            }
+        };
         if constexpr (STATS) {
-            if (flush_id >= 0) flush_statistics<RB>(st, t.view, a.n, flush_id, &s_stat[threadIdx.x * RB]);
-            flush_id = -1;
+            stat_r = stat_lane<RB>(st, lane);
+            bool finite = true;
+#pragma unroll
+            for (int k = 0; k < PIX; ++k)
+#pragma unroll
+                for (int r = 0; r < RB; ++r) finite = finite && __builtin_fabsf(val[k][r]) <= 3.0e38f;
+            stat_finite = __ballot(!finite) == 0;
+        }
+        int stop = -1;  // list entries read before every pixel terminated (-1: never)
+        for (int begin = t.first; begin < last; begin += B) {
+            bool active = false;
+#pragma unroll
+            for (int k = 0; k < PIX; ++k) active = active || !done[k];
+            const int active_threads = __syncthreads_count(active);
+            flush();  // every wavefront is past the previous batch
+            if (active_threads == 0) {
+                stop = begin - t.first;
+                break;
+            }
+            if (threadIdx.x < B) {
+                const int e = threadIdx.x;
+                const int32_t g = next_id;
+                if (begin + e < last) {
+                    // The 4-channel plain blend fits its registers without the
+                    // tile-origin laundering (and is fastest so).
+                    stage_gaussian<CH, PIX, (STATS || CH > 4)>(a, t, g, e, c0, s_g, s_mask);
+                    if constexpr (STATS) flush_id = g;
+                }
+                if (begin + B < last) next_id = a.ids[min(begin + B + e, last - 1)];
+            }
+            __syncthreads();
+            const int cnt = min(B, last - begin);
+            bool live = true;
+            for (int c0 = 0; c0 < cnt && live; c0 += 64) {
+                // This wavefront's Gaussians of the next 64, in list order.
+                uint64_t todo = __ballot(c0 + lane < cnt && ((s_mask[min(c0 + lane, B - 1)] >> wave) & 1u));
+                if (!todo) continue;
+                // Blend one Gaussian (batch slot j) into this lane's pixels.
+                auto blend = [&](const Staged<CH>& g, int j) {
+                    const int contributor = begin - t.first + j + 1;  // list position, 1-based
+                    bool acc[PIX];
+                    float wk[PIX];
+                    // Branch-free per pixel except for the exponential: a
+                    // divergent branch per test costs more in exec-mask work than
+                    // the selects it replaces (the wavefront issues the tail
+                    // whenever any lane needs it).  Updates are selected, not
+                    // multiplied by zero, so non-finite features of a rejected
+                    // Gaussian cannot reach the pixel.
+#pragma unroll
+                    for (int k = 0; k < PIX; ++k) {
+                        const float dx = g.xy.x - fx[k], dy = g.xy.y - fy[k];
+                        const float power = blend_power(g.con.x, g.con.y, g.con.z, dx, dy);
+                        if constexpr (COUNTS) evaluated += done[k] ? 0u : 1u;
+                        const bool in = !done[k] && power <= 0.0f && power >= g.cut;
+                        float e = 0.0f;
+                        if (in) e = blend_exp(power);
+                        const float alpha = in ? sel_min(0.99f, g.con.w * e) : 0.0f;
+                        const bool take = alpha >= 1.0f / 255.0f;
+                        const float next_t = T[k] * (1.0f - alpha);
+                        const bool term = take && next_t < 0.0001f;
+                        const bool upd = take && !term;
+                        if constexpr (COUNTS) {
+                            visited[k] = term ? contributor : visited[k];
+                            accepted += upd ? 1u : 0u;
+                        }
+                        done[k] = done[k] || term;
+                        const float w = alpha * T[k];
+#pragma unroll
+                        for (int c = 0; c < CH; ++c) {
+                            const float nc = __builtin_fmaf(g.f[c], w, color[k][c]);
+                            color[k][c] = upd ? nc : color[k][c];
+                        }
+                        T[k] = upd ? next_t : T[k];
+                        last_contributor[k] = upd ? contributor : last_contributor[k];
+                        acc[k] = upd;
+                        wk[k] = upd ? w : 0.0f;
+                    }
+
+                    if constexpr (STATS) {
+                        bool hit = false;
+#pragma unroll
+                        for (int k = 0; k < PIX; ++k) hit = hit || acc[k];
+                        if (__ballot(hit))
+                            observe_statistics<PIX, RB, KINDS>(st, stat_r, &s_stat[j * RB], acc, wk, val, stat_finite, lane);
+                    }
+                };
+                auto alive = [&]() {
+                    bool any = false;
+#pragma unroll
+                    for (int k = 0; k < PIX; ++k) any = any || !done[k];
+                    return __ballot(any) != 0;
+                };
+                auto take = [&]() {
+                    const int j = c0 + __builtin_ctzll(todo);
+                    todo &= todo - 1;
+                    return j;
+                };
+                if constexpr ((STATS && (RB > 2 || CH > 4)) || (CH > 16 && CH <= 36)) {
+                    // Loads at use: the pipelined form's extra registers would
+                    // cost occupancy -- with statistics beyond two requests (their
+                    // pixel values take 4 * PIX registers or more) or four
+                    // channels (up to both, the pipelined form fits 80 VGPRs),
+                    // and for 36
+                    // channels a third wavefront per SIMD (148 VGPRs against 190
+                    // with the next Gaussian's vector prefetched: 0.83 -> 0.72
+                    // ms on the 32-feature workload).
+                    while (todo) {
+                        if (!alive()) {
+                            live = false;
+                            break;
+                        }
+                        const int j = take();
+                        blend(load_staged<CH>(j, s_g), j);
+                    }
+                } else {
+                    // Unrolled by two: the next Gaussian is loaded into the other
+                    // buffer before the current one is blended.
+                    int ja = take(), jb = 0;
+                    Staged<CH> ga = load_staged<CH>(ja, s_g), gb;
+                    while (true) {
+                        if (!alive()) {
+                            live = false;
+                            break;
+                        }
+                        bool more = todo != 0;
+                        if (more) {
+                            jb = take();
+                            gb = load_staged<CH>(jb, s_g);
+                        }
+                        blend(ga, ja);
+                        if (!more) break;
+                        // Liveness is checked once per two Gaussians: a Gaussian
+                        // blended after every pixel is done changes nothing (no
+                        // pixel accepts it), and the check costs VALU and scalar
+                        // work on every Gaussian (1091 -> 1067 us for the
+                        // 3M-Gaussian forward blend).
+                        more = todo != 0;
+                        if (more) {
+                            ja = take();
+                            ga = load_staged<CH>(ja, s_g);
+                        }
+                        blend(gb, jb);
+                        if (!more) break;
+                    }
+                }
+            }
+        }
+        if constexpr (STATS) {
+            // The last batch, when the loop ran to the end of the list.
+            __syncthreads();
+            flush();
+        }
+        if constexpr (LISTS != 0) {
+            if (stop < 0) {
+                // The loop ran to the end of the list it had: all of it read.
+                bool active = false;
+#pragma unroll
+                for (int k = 0; k < PIX; ++k) active = active || !done[k];
+                if (__syncthreads_count(active) == 0) stop = last - t.first;
+            }
+            if (threadIdx.x == 0 && c0 == 0) {
+                // A capped tile with pixels still live needs its whole list:
+                // flagged and listed for a redo (its outputs here are
+                // incomplete).
+                if (LISTS == 1 && a.redo) {
+                    const bool redo = capped && stop < 0;
+                    a.redo[t.tile] = redo ? 1 : 0;
+                    if (redo) a.redo_list[1 + atomicAdd(a.redo_list, 1)] = t.tile;
+                }
+                if (a.stop_out) a.stop_out[t.tile] = stop;
+            }
+        }
+        const float* bg = a.background ? a.background + t.view * a.background_view_stride : nullptr;
+        const int F = a.feat_channels, E = a.extra_channels;
+#pragma unroll
+        for (int k = 0; k < PIX; ++k) {
+            if (!(px[k] < a.width && py[k] < a.height)) continue;
+            const int64_t pix = ((int64_t)t.view * a.height + py[k]) * a.width + px[k];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int gc = c0 + c;
+                if (gc >= D) continue;
+                const float v = __builtin_fmaf(T[k], (bg && gc < F) ? bg[gc] : 0.0f, color[k][c]);
+                if (gc < F)
+                    a.image[pix * F + gc] = v;
+                else if (gc < F + E)
+                    a.image_extra[pix * E + (gc - F)] = v;
+                else
+                    a.image_alpha[pix] = v;
+            }
+            if (c0 == 0) {
+                a.final_t[pix] = T[k];
+                a.contributors[pix] = last_contributor[k];
+            }
+        }
+        if constexpr (COUNTS) {
+            uint64_t v = 0;
+#pragma unroll
+            for (int k = 0; k < PIX; ++k) v += (uint64_t)visited[k];
+            uint64_t e = evaluated, c = accepted;
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) {
+                v += (uint64_t)__shfl_xor((long long)v, d, 64);
+                e += (uint64_t)__shfl_xor((long long)e, d, 64);
+                c += (uint64_t)__shfl_xor((long long)c, d, 64);
+            }
+            if (lane == 0) {
+                atomicAdd(counts, (unsigned long long)v);
+                atomicAdd(counts + 1, (unsigned long long)e);
+                atomicAdd(counts + 2, (unsigned long long)c);
+            }
         }
     };
-    if constexpr (STATS) {
-        stat_r = stat_lane<RB>(st, lane);
-        bool finite = true;
-#pragma unroll
-        for (int k = 0; k < PIX; ++k)
-#pragma unroll
-            for (int r = 0; r < RB; ++r) finite = finite && __builtin_fabsf(val[k][r]) <= 3.0e38f;
-        stat_finite = __ballot(!finite) == 0;
-    }
-    for (int begin = t.first; begin < t.last; begin += B) {
-        bool active = false;
-#pragma unroll
-        for (int k = 0; k < PIX; ++k) active = active || !done[k];
-        const int active_threads = __syncthreads_count(active);
-        flush();  // every wavefront is past the previous batch
-        if (active_threads == 0) break;
-        if (threadIdx.x < B) {
-            const int e = threadIdx.x;
-            const int32_t g = next_id;
-            if (begin + e < t.last) {
-                // The 4-channel plain blend fits its registers without the
-                // tile-origin laundering (and is fastest so).
-                stage_gaussian<CH, PIX, (STATS || CH > 4)>(a, t, g, e, c0, s_g, s_mask);
-                if constexpr (STATS) flush_id = g;
-            }
-            if (begin + B < t.last) next_id = a.ids[min(begin + B + e, t.last - 1)];
+    if constexpr (LISTS == 2) {
+        // redo_list[0] tiles from redo_list[1], over a grid smaller than the
+        // frame's; the next tile reuses the staging LDS.
+        const int items = a.redo_list[0];
+        for (int item = blockIdx.x; item < items; item += gridDim.x) {
+            blend(tile_info(a, a.redo_list[1 + item]));
+            __syncthreads();
         }
-        __syncthreads();
-        const int cnt = min(B, t.last - begin);
-        bool live = true;
-        for (int c0 = 0; c0 < cnt && live; c0 += 64) {
-            // This wavefront's Gaussians of the next 64, in list order.
-            uint64_t todo = __ballot(c0 + lane < cnt && ((s_mask[min(c0 + lane, B - 1)] >> wave) & 1u));
-            if (!todo) continue;
-            // Blend one Gaussian (batch slot j) into this lane's pixels.
-            auto blend = [&](const Staged<CH>& g, int j) {
-                const int contributor = begin - t.first + j + 1;  // list position, 1-based
-                bool acc[PIX];
-                float wk[PIX];
-                // Branch-free per pixel except for the exponential: a
-                // divergent branch per test costs more in exec-mask work than
-                // the selects it replaces (the wavefront issues the tail
-                // whenever any lane needs it).  Updates are selected, not
-                // multiplied by zero, so non-finite features of a rejected
-                // Gaussian cannot reach the pixel.
-#pragma unroll
-                for (int k = 0; k < PIX; ++k) {
-                    const float dx = g.xy.x - fx[k], dy = g.xy.y - fy[k];
-                    const float power = blend_power(g.con.x, g.con.y, g.con.z, dx, dy);
-                    if constexpr (COUNTS) evaluated += done[k] ? 0u : 1u;
-                    const bool in = !done[k] && power <= 0.0f && power >= g.cut;
-                    float e = 0.0f;
-                    if (in) e = blend_exp(power);
-                    const float alpha = in ? sel_min(0.99f, g.con.w * e) : 0.0f;
-                    const bool take = alpha >= 1.0f / 255.0f;
-                    const float next_t = T[k] * (1.0f - alpha);
-                    const bool term = take && next_t < 0.0001f;
-                    const bool upd = take && !term;
-                    if constexpr (COUNTS) {
-                        visited[k] = term ? contributor : visited[k];
-                        accepted += upd ? 1u : 0u;
-                    }
-                    done[k] = done[k] || term;
-                    const float w = alpha * T[k];
-#pragma unroll
-                    for (int c = 0; c < CH; ++c) {
-                        const float nc = __builtin_fmaf(g.f[c], w, color[k][c]);
-                        color[k][c] = upd ? nc : color[k][c];
-                    }
-                    T[k] = upd ? next_t : T[k];
-                    last_contributor[k] = upd ? contributor : last_contributor[k];
-                    acc[k] = upd;
-                    wk[k] = upd ? w : 0.0f;
-                }
-
-                if constexpr (STATS) {
-                    bool hit = false;
-#pragma unroll
-                    for (int k = 0; k < PIX; ++k) hit = hit || acc[k];
-                    if (__ballot(hit))
-                        observe_statistics<PIX, RB, KINDS>(st, stat_r, &s_stat[j * RB], acc, wk, val, stat_finite, lane);
-                }
-            };
-            auto alive = [&]() {
-                bool any = false;
-#pragma unroll
-                for (int k = 0; k < PIX; ++k) any = any || !done[k];
-                return __ballot(any) != 0;
-            };
-            auto take = [&]() {
-                const int j = c0 + __builtin_ctzll(todo);
-                todo &= todo - 1;
-                return j;
-            };
-            if constexpr ((STATS && (RB > 2 || CH > 4)) || (CH > 16 && CH <= 36)) {
-                // Loads at use: the pipelined form's extra registers would
-                // cost occupancy -- with statistics beyond two requests (their
-                // pixel values take 4 * PIX registers or more) or four
-                // channels (up to both, the pipelined form fits 80 VGPRs),
-                // and for 36
-                // channels a third wavefront per SIMD (148 VGPRs against 190
-                // with the next Gaussian's vector prefetched: 0.83 -> 0.72
-                // ms on the 32-feature workload).
-                while (todo) {
-                    if (!alive()) {
-                        live = false;
-                        break;
-                    }
-                    const int j = take();
-                    blend(load_staged<CH>(j, s_g), j);
-                }
-            } else {
-                // Unrolled by two: the next Gaussian is loaded into the other
-                // buffer before the current one is blended.
-                int ja = take(), jb = 0;
-                Staged<CH> ga = load_staged<CH>(ja, s_g), gb;
-                while (true) {
-                    if (!alive()) {
-                        live = false;
-                        break;
-                    }
-                    bool more = todo != 0;
-                    if (more) {
-                        jb = take();
-                        gb = load_staged<CH>(jb, s_g);
-                    }
-                    blend(ga, ja);
-                    if (!more) break;
-                    // Liveness is checked once per two Gaussians: a Gaussian
-                    // blended after every pixel is done changes nothing (no
-                    // pixel accepts it), and the check costs VALU and scalar
-                    // work on every Gaussian (1091 -> 1067 us for the
-                    // 3M-Gaussian forward blend).
-                    more = todo != 0;
-                    if (more) {
-                        ja = take();
-                        ga = load_staged<CH>(ja, s_g);
-                    }
-                    blend(gb, jb);
-                    if (!more) break;
-                }
-            }
-        }
-    }
-    if constexpr (STATS) {
-        // The last batch, when the loop ran to the end of the list.
-        __syncthreads();
-        flush();
-    }
-    const float* bg = a.background ? a.background + t.view * a.background_view_stride : nullptr;
-    const int F = a.feat_channels, E = a.extra_channels;
-#pragma unroll
-    for (int k = 0; k < PIX; ++k) {
-        if (!(px[k] < a.width && py[k] < a.height)) continue;
-        const int64_t pix = ((int64_t)t.view * a.height + py[k]) * a.width + px[k];
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int gc = c0 + c;
-            if (gc >= D) continue;
-            const float v = __builtin_fmaf(T[k], (bg && gc < F) ? bg[gc] : 0.0f, color[k][c]);
-            if (gc < F)
-                a.image[pix * F + gc] = v;
-            else if (gc < F + E)
-                a.image_extra[pix * E + (gc - F)] = v;
-            else
-                a.image_alpha[pix] = v;
-        }
-        if (c0 == 0) {
-            a.final_t[pix] = T[k];
-            a.contributors[pix] = last_contributor[k];
-        }
-    }
-    if constexpr (COUNTS) {
-        uint64_t v = 0;
-#pragma unroll
-        for (int k = 0; k < PIX; ++k) v += (uint64_t)visited[k];
-        uint64_t e = evaluated, c = accepted;
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) {
-            v += (uint64_t)__shfl_xor((long long)v, d, 64);
-            e += (uint64_t)__shfl_xor((long long)e, d, 64);
-            c += (uint64_t)__shfl_xor((long long)c, d, 64);
-        }
-        if (lane == 0) {
-            atomicAdd(counts, (unsigned long long)v);
-            atomicAdd(counts + 1, (unsigned long long)e);
-            atomicAdd(counts + 2, (unsigned long long)c);
-        }
+    } else {
+        blend(tile_info(a));
     }
 }
 
@@ -991,6 +1051,8 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
 #define GS3D_SMALL_GRID 1024
 #endif
 constexpr unsigned kSmallGrid = GS3D_SMALL_GRID;
+// Workgroups of a redo launch (gs3d_render_args.redo_pass).
+constexpr unsigned kRedoGrid = 512;
 
 template <int CH, int PIX>
 int launch_fwd_pix(const gs3d_render_args& a, const gs3d_render_stats_args* st, unsigned long long* counts,
@@ -1018,6 +1080,16 @@ int launch_fwd_pix(const gs3d_render_args& a, const gs3d_render_stats_args* st, 
         return launch_status("gs3d_render_fwd_stats");
     }
     const gs3d_render_stats_args none = {};
+    if (a.redo_pass) {
+        // The workgroups walk the listed tiles (usually none).
+        hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 0, 1, -1, 2>), dim3(min(blocks, kRedoGrid)), block, 0, s, a,
+                           none, c0, nullptr);
+        return launch_status("gs3d_render_fwd");
+    }
+    if (a.caps || a.stop_out) {
+        hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 0, 1, -1, 1>), grid, block, 0, s, a, none, c0, nullptr);
+        return launch_status("gs3d_render_fwd");
+    }
     if (counts) {
         hipLaunchKernelGGL((render_fwd_kernel<CH, PIX, 2>), grid, block, 0, s, a, none, c0, counts);
         return launch_status("gs3d_render_pair_counts");
@@ -1097,6 +1169,12 @@ int render_fwd(const gs3d_render_args* args, const gs3d_render_stats_args* st, u
     if (status != GS3D_OK) return status;
     if (a.zero_count < 0 || (a.zero_count > 0 && (!a.zero_out || (reinterpret_cast<uintptr_t>(a.zero_out) & 15))))
         return GS3D_ERR_ARGUMENT;
+    // Capped lists: overflowing tiles must be reported; a redo launch skips
+    // tiles, so it cannot clear a buffer, count pairs or total statistics
+    // (nor can a capped launch, whose redone tiles would total twice).
+    if (a.caps && !a.redo_pass && (!a.redo || !a.redo_list)) return GS3D_ERR_ARGUMENT;
+    if (a.redo_pass && (!a.redo_list || a.zero_out)) return GS3D_ERR_ARGUMENT;
+    if ((a.caps || a.redo_pass || a.stop_out) && (st || counts)) return GS3D_ERR_ARGUMENT;
     if (a.views == 0) return GS3D_OK;
     if ((a.feat_channels > 0 && !a.image) || (a.extra_channels > 0 && !a.image_extra) ||
         (a.one_tail && !a.image_alpha) || !a.final_t || !a.contributors)

@@ -22,6 +22,7 @@ from typing import Any, Sequence
 import torch
 from torch import Tensor
 
+from . import lists as tile_lists
 from .autograd import Frame, Rasterize, ViewBins
 from .. import profiling
 from .projection import project_views
@@ -98,18 +99,21 @@ def _pinned_status(numel: int) -> Tensor:
 
 @native.no_grad
 def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height, near, far, radius_clip,
-                   sh, sh_degree, background, tile_mode="radius") -> Frame:
-    """Camera rows, fused projection, depth order, one synchronisation, binning."""
+                   sh, sh_degree, background, tile_mode="radius", capped=True) -> Frame:
+    """Camera rows, fused projection, depth order, one synchronisation, binning
+    (with ``capped``, of lists capped by the cameras' earlier stops)."""
     profiling.mark("start")
     with_centers = sh_degree is not None and sh_degree > 0
     # One int64 status buffer read back once: [group pairs, tile pairs], the
-    # depth keys' bit count (int32 in the low half of the third word) and then
-    # the cameras' int32 status codes.
+    # depth keys' bit count (int32 in the low half of the third word), the
+    # cameras' 64-bit keys and then their int32 status codes.
     cameras = viewmats.numel() // 16
-    status = torch.empty(3 + (cameras + 1) // 2, dtype=torch.int64, device=viewmats.device)
+    status = torch.empty(3 + cameras + (cameras + 1) // 2, dtype=torch.int64, device=viewmats.device)
     key_bits = status[2:3].view(torch.int32)[:1]
-    camera_status = status[3:].view(torch.int32)[:cameras]
-    full, inverse, centers, _ = launch_prepare(viewmats, Ks, width, height, with_centers, errors=camera_status)
+    camera_keys = status[3:3 + cameras]
+    camera_status = status[3 + cameras:].view(torch.int32)[:cameras]
+    full, inverse, centers, _ = launch_prepare(viewmats, Ks, width, height, with_centers, errors=camera_status,
+                                               keys=camera_keys)
     state = project_views(
         means, quats, scales, opacities, viewmats, full, Ks, width, height, near, far, radius_clip,
         sh=sh if sh_degree is not None else None, sh_degree=sh_degree or 0,
@@ -145,7 +149,7 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     early = binning.emit_early(launch)
     copied.synchronize()
     profiling.mark("totals_read")
-    raise_camera_errors(host[3:].view(torch.int32)[:cameras].tolist())
+    raise_camera_errors(host[3 + cameras:].view(torch.int32)[:cameras].tolist())
     group_pairs, count = host[:2].tolist()
     if binning.remember_key_bits(shape, int(host[2:3].view(torch.int32)[0]), sort_bits):
         # The depth keys now differ in more bits than were sorted: order
@@ -156,8 +160,15 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
                                        sort_bits=binning.planned_sort_bits(shape))
         launch = prepare_bin_rows(state.centers, state.radii, order, offsets, width, height,
                                   conics=state.conics, tile_mode=tile_mode)
+    lists = None
     if count <= binning.PAIR_LIMIT and group_pairs <= binning.PAIR_LIMIT:
-        ranges, ids = launch_bin_rows(launch, group_pairs, count, early)
+        if capped:
+            lists = tile_lists.plan(status.device, width, height, tile_mode, host[3:3 + cameras].tolist(), count,
+                                    launch.ranges.shape[0] // max(cameras, 1))
+        caps = lists.caps if lists is not None else None
+        ranges, ids = launch_bin_rows(launch, group_pairs, count, early, caps=caps)
+        if caps is not None:
+            lists.launch = launch
         bins = [ViewBins(0, cameras, ranges, ids)]
     else:
         del early  # the per-group binning below allocates its own scratch
@@ -165,7 +176,7 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     profiling.mark("binned")
     return Frame(
         width, height, Ks.detach(), full, inverse if with_centers else None, centers if with_centers else None,
-        state, bins, count, sh_degree, background,
+        state, bins, count, sh_degree, background, lists,
     )
 
 
@@ -242,6 +253,7 @@ def rasterize(
             batch_item(layout.viewmats, b), batch_item(layout.Ks, b), width, height, near_plane, far_plane,
             radius_clip, colors if sh_degree is not None else None, sh_degree,
             None if layout.backgrounds is None else batch_item(layout.backgrounds, b), tile_mode,
+            capped=not statistics,  # a redone tile would total its statistics twice
         )
         frames.append(frame)
         st = frame.state

@@ -22,7 +22,7 @@ import torch
 from torch import Tensor
 from torch.autograd.function import once_differentiable
 
-from . import projection, render
+from . import lists as tile_lists, projection, render
 from .. import profiling
 from ..runtime.gradients import AbsGradientTarget
 from ..splatting.cameras import camera_backward
@@ -57,6 +57,7 @@ class Frame:
     pair_count: int
     sh_degree: int | None
     background: Tensor | None  # (C, D) or None
+    lists: "tile_lists.CappedLists | None" = None  # capped lists (one bins entry only), until blended
 
 
 def _views(t, v0: int, v1: int, views: int, per_view_ndim: int):
@@ -143,11 +144,14 @@ class Rasterize(torch.autograd.Function):
             ctx.cleared, zero = _buffers_for_backward(st.centers.device, shapes)
         if len(frame.bins) == 1:
             bins = frame.bins[0]
+            lists, frame.lists = frame.lists, None
             output = render.render_views(
                 bins.ranges, bins.ids, st.centers, st.conics, blended, frame.width, frame.height,
                 extra=extra_features, background=frame.background, one_tail=True, statistics=statistics,
-                zero=zero,
+                zero=zero, lists=lists,
             )
+            if lists is not None:
+                tile_lists.remember(lists)
         else:
             views = st.centers.shape[0]
             parts = []

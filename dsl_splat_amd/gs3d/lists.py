@@ -1,0 +1,147 @@
+"""Capped tile lists: each camera's tile stops carried from one frame of that
+camera to the next.
+
+A tile's blend stops reading its depth-ordered list once every pixel of the
+tile has terminated (transmittance below 1e-4, gs3d/render.py:107-169 of the
+reference), usually after a small part of the list.  The blend reports that
+position per tile (its stop), and the next frame of the same camera (same
+64-bit key of view matrix and intrinsics, gs3d_camera_prepare_keyed; same
+image size and tile mode) writes each tile's list only up to its cap,
+stop + stop/4 + 128 entries.  The blend reads no further; a tile whose pixels
+are still live at its cap is flagged, and after the blend gs3d_bin_redo
+writes the whole lists of the flagged tiles and a second blend launch
+renders only those tiles again, from their first entry.  Images,
+transmittance, contributor counts and gradients are therefore those of
+whole lists whatever the caps were; a stale cap costs only the redo.
+
+The first frame of a camera writes whole lists (no stops known), and so do
+frames with statistics, frames binned per camera group and frames of fewer
+than MIN_PAIRS tile pairs or MIN_PAIRS_PER_TILE pairs per tile: a capped
+frame launches three more kernels (the count's clearing, gs3d_bin_redo, the
+redo blend; ~14 us on MI355X when no tile overflows), which only long lists
+repay (measured: 4M-pair 720p frames of ~2100 pairs per tile lose ~12 us,
+1080p frames of ~5200 pairs per tile gain ~190 us).  GS3D_LIST_CAPS=0 turns
+the caps off.
+"""
+
+from collections import OrderedDict
+from dataclasses import dataclass
+import os
+import threading
+
+import torch
+from torch import Tensor
+
+from ..runtime import native
+from ..splatting import binning
+
+ENABLED = os.environ.get("GS3D_LIST_CAPS", "1") != "0"
+# Frames with fewer tile pairs, or fewer per tile, write whole lists.
+MIN_PAIRS = 1 << 22
+MIN_PAIRS_PER_TILE = 4096
+# The stop cache keeps at most this many bytes of stop rows (one int32 per
+# tile per camera, 32 KB per 1920x1080 camera), dropping the least recently
+# rendered cameras first.
+CACHE_BYTES = 64 << 20
+
+_LOCK = threading.Lock()
+# (device index, width, height, tile mode, camera key) -> (stops of the
+# frame that rendered the camera last, its row in them, the stream its blend
+# ran on).  Stops are used on that stream only: the binning and the blend
+# of a frame must read equal caps, which a blend still writing them on
+# another stream would not guarantee.
+_STOPS: "OrderedDict[tuple, tuple[Tensor, int, int]]" = OrderedDict()
+_BYTES = 0
+
+
+@dataclass(slots=True)
+class CappedLists:
+    """Caps and outputs of one frame's capped lists.
+
+    caps: (views*tiles) int32 caps of the binning and blend, None when no
+    camera of the frame was seen before (whole lists; the stops are still
+    measured).  stops: (views, tiles) int32 that the blend fills.  With
+    caps, redo: (views*tiles) int32 overflow flags, and redo_list:
+    (1 + views*tiles) int32, the count of flagged tiles (zeroed here) and
+    the tiles.  launch: the binning launch that gs3d_bin_redo repeats for
+    the flagged tiles."""
+
+    keys: list
+    shape: tuple
+    stream: int
+    caps: Tensor | None
+    stops: Tensor
+    redo: Tensor | None = None
+    redo_list: Tensor | None = None
+    launch: binning.BinLaunch | None = None
+
+    def rewrite(self) -> None:
+        """Whole lists for the tiles the capped blend flagged."""
+        binning.redo_bin_rows(self.launch, self.redo, self.redo_list)
+        self.launch = None
+
+
+def clear() -> None:
+    """Forget every camera's stops."""
+    global _BYTES
+    with _LOCK:
+        _STOPS.clear()
+        _BYTES = 0
+
+
+def plan(device: torch.device, width: int, height: int, tile_mode: str, keys: list, tile_pairs: int,
+         tiles_per_view: int) -> CappedLists | None:
+    """The frame's caps from the stop cache; None when the frame writes whole
+    lists without measuring stops (caps off or a small frame)."""
+    if not ENABLED or not keys or tile_pairs < max(MIN_PAIRS, MIN_PAIRS_PER_TILE * len(keys) * tiles_per_view):
+        return None
+    shape = (device.index, width, height, tile_mode)
+    stream = native.stream(device).value or 0
+    views = len(keys)
+    with _LOCK:
+        rows = []
+        for k in keys:
+            row = _STOPS.get(shape + (k,))
+            if row is not None:
+                _STOPS.move_to_end(shape + (k,))
+                if row[2] != stream:
+                    row = None
+            rows.append(row)
+    count = views * tiles_per_view
+    caps = None
+    if all(r is not None for r in rows) and all(r[0] is rows[0][0] and r[1] == i for i, r in enumerate(rows)) \
+            and rows[0][0].shape[0] == views:
+        caps = rows[0][0].view(-1)  # the same cameras in the same order as their last frame
+    elif any(r is not None for r in rows):
+        caps = torch.full((views, tiles_per_view), -1, dtype=torch.int32, device=device)
+        for i, r in enumerate(rows):
+            if r is not None:
+                caps[i].copy_(r[0][r[1]])
+        caps = caps.view(-1)
+    if caps is None:
+        return CappedLists(list(keys), shape, stream, None,
+                           torch.empty((views, tiles_per_view), dtype=torch.int32, device=device))
+    # stops | redo flags | count of flagged tiles, flagged tiles
+    buffer = torch.empty(3 * count + 1, dtype=torch.int32, device=device)
+    redo_list = buffer[2 * count:]
+    redo_list[:1].zero_()
+    return CappedLists(list(keys), shape, stream, caps, buffer[:count].view(views, tiles_per_view),
+                       buffer[count:2 * count], redo_list)
+
+
+def remember(lists: CappedLists) -> None:
+    """Store the stops of a blend that has been enqueued: later frames of
+    these cameras read them in stream order."""
+    global _BYTES
+    row_bytes = lists.stops.shape[1] * 4
+    with _LOCK:
+        for i, k in enumerate(lists.keys):
+            key = lists.shape + (k,)
+            if key in _STOPS:
+                _BYTES -= row_bytes
+                del _STOPS[key]
+            _STOPS[key] = (lists.stops, i, lists.stream)
+            _BYTES += row_bytes
+        while _BYTES > CACHE_BYTES and _STOPS:
+            _, (t, _, _) = _STOPS.popitem(last=False)
+            _BYTES -= t.shape[1] * 4

@@ -118,11 +118,14 @@ def _stats_args(statistics, views: int, n: int, width: int, height: int, keep: l
 @native.no_grad
 def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, features: Tensor,
                  width: int, height: int, *, extra: Tensor | None = None, background: Tensor | None = None,
-                 one_tail: bool = True, statistics=None, zero: Tensor | None = None) -> RenderedPixels:
+                 one_tail: bool = True, statistics=None, zero: Tensor | None = None, lists=None) -> RenderedPixels:
     """Blend all views; with a PreparedStatistics, its counts and sums
     accumulate the contribution statistics of the same launch.  ``zero`` (a
     contiguous float32 tensor, 16-byte aligned), if given, is cleared by the
-    launch while it blends."""
+    launch while it blends.  ``lists`` (a CappedLists of the frame whose
+    ``ids`` were written up to ``lists.caps``) receives each tile's stop; with
+    caps, the tiles the blend flags get their whole lists (lists.rewrite())
+    and a second launch blends them again into the same outputs."""
     views, n = centers.shape[0], centers.shape[1]
     device = centers.device
     keep = []
@@ -143,10 +146,26 @@ def render_views(ranges: Tensor, ids: Tensor, centers: Tensor, conics: Tensor, f
         if zero.dtype != torch.float32 or not zero.is_contiguous() or zero.device != device:
             raise ValueError("zero must be a contiguous float32 tensor on the rendering device")
         a.zero_out, a.zero_count = native.ptr(zero), zero.numel()
+    capped = lists is not None and lists.caps is not None
+    if lists is not None:
+        tiles = ranges.shape[0]
+        if lists.stops.numel() != tiles or (capped and (lists.caps.numel() != tiles or lists.redo.numel() != tiles
+                                                        or lists.redo_list.numel() != tiles + 1)):
+            raise ValueError("the capped lists do not match the frame's tiles")
+        a.stop_out = native.ptr(lists.stops)
+        if capped:
+            a.caps, a.redo, a.redo_list = native.ptr(lists.caps), native.ptr(lists.redo), native.ptr(lists.redo_list)
     if statistics is not None and len(statistics.key):
+        if capped:
+            raise ValueError("statistics need whole tile lists")
         st = _stats_args(statistics, views, n, width, height, keep)
         native.call("gs3d_render_fwd_stats", ctypes.byref(a), ctypes.byref(st), native.stream(device))
     else:
+        native.call("gs3d_render_fwd", ctypes.byref(a), native.stream(device))
+    if capped:
+        lists.rewrite()
+        a.caps, a.redo, a.redo_pass = None, None, 1
+        a.zero_out, a.zero_count = None, 0
         native.call("gs3d_render_fwd", ctypes.byref(a), native.stream(device))
     return out
 

@@ -9,7 +9,7 @@ import ctypes
 c_float_p = ctypes.POINTER(ctypes.c_float)
 c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # Tile modes (GS3D_TILE_*), named as the reference's TileMode literals.
 TILE_MODES = {"radius": 0, "snugbox": 1, "accutile": 2}
@@ -162,6 +162,7 @@ class BinArgs(ctypes.Structure):
         ("conics", _P),
         ("tile_mode", ctypes.c_int32),
         ("footprints", _P),
+        ("caps", _P),
     ]
 
 
@@ -193,6 +194,11 @@ class RenderArgs(ctypes.Structure):
         ("contributors", _P),
         ("zero_out", _P),
         ("zero_count", ctypes.c_int64),
+        ("caps", _P),
+        ("stop_out", _P),
+        ("redo", _P),
+        ("redo_list", _P),
+        ("redo_pass", ctypes.c_int32),
     ]
 
 
@@ -260,6 +266,10 @@ FUNCTIONS = {
         ctypes.c_int,
         [_P, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P],
     ),
+    "gs3d_camera_prepare_keyed": (
+        ctypes.c_int,
+        [_P, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P],
+    ),
     "gs3d_camera_backward": (
         ctypes.c_int,
         [_P, _P, _I32, _I32, _P, _P, _I32, _P, _P],
@@ -286,6 +296,7 @@ FUNCTIONS = {
     "gs3d_bin_rows": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
     "gs3d_emit_group_items": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
     "gs3d_bin_emitted_rows": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
+    "gs3d_bin_redo": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _P, _P, _SZ, _P]),
     "gs3d_pair_tiles": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
     "gs3d_sort_pairs_u32": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),
     "gs3d_expand_keys": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _I32, _P, _P]),

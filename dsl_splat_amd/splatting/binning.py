@@ -211,10 +211,13 @@ def view_groups(pairs_per_view: list[int]) -> list[tuple[int, int]]:
 class BinLaunch:
     """Arguments of gs3d_bin_rows that do not depend on the totals, built
     while the device still works on the depth order; ``inputs`` keeps the
-    tensors behind the pointers alive."""
+    tensors behind the pointers alive.  After a launch with caps, ``caps``
+    and ``scratch`` hold what gs3d_bin_redo reads."""
     args: abi.BinArgs
     ranges: Tensor
     inputs: tuple
+    caps: Tensor | None = None
+    scratch: Tensor | None = None
 
 
 @native.no_grad
@@ -298,17 +301,26 @@ def _remember_capacity(launch: BinLaunch, group_pairs: int) -> None:
 
 @native.no_grad
 def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int,
-                    early: EarlyItems | None = None) -> tuple[Tensor, Tensor]:
+                    early: EarlyItems | None = None, caps: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs);
-    ``early`` (from emit_early) is used when its capacity holds every item."""
+    ``early`` (from emit_early) is used when its capacity holds every item.
+    With ``caps`` (views*tiles int32, see gs3d_bin_args.caps) each tile's
+    list is written only up to its cap, and the launch keeps the binning
+    scratch for redo_bin_rows."""
     check_pair_counts(group_pairs, tile_pairs)
     a, device = launch.args, launch.ranges.device
     ids = torch.empty(tile_pairs, dtype=torch.int32, device=device)
     a.group_pairs, a.tile_pairs = group_pairs, tile_pairs
     a.ids = native.ptr(ids)
+    if caps is not None:
+        if caps.dtype != torch.int32 or not caps.is_contiguous() or caps.numel() != launch.ranges.shape[0]:
+            raise ValueError("caps must be a contiguous int32 tensor with one entry per tile")
+        launch.caps = caps
+        a.caps = native.ptr(caps)
     if early is not None and group_pairs <= early.capacity:
         native.call("gs3d_bin_emitted_rows", ctypes.byref(a), native.ptr(early.scratch), early.scratch.numel(),
                     native.stream(device))
+        scratch = early.scratch
     else:
         if early is not None:
             # Too small: release the early scratch before the full one is
@@ -318,8 +330,23 @@ def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int,
         scratch = _scratch(native.query("gs3d_bin_rows_scratch_bytes", group_pairs, a.views, a.width, a.height,
                                         a.tile_mode), device)
         native.call("gs3d_bin_rows", ctypes.byref(a), native.ptr(scratch), scratch.numel(), native.stream(device))
+    if caps is not None:
+        launch.scratch = scratch
     _remember_capacity(launch, group_pairs)
     return launch.ranges, ids
+
+
+@native.no_grad
+def redo_bin_rows(launch: BinLaunch, redo: Tensor, redo_list: Tensor) -> None:
+    """Write the whole lists of the tiles flagged in ``redo`` (views*tiles
+    int32, from a capped blend, whose ``redo_list`` starts with their count)
+    after a launch_bin_rows with caps, then release the binning scratch."""
+    if launch.scratch is None:
+        raise RuntimeError("redo_bin_rows needs a launch_bin_rows with caps before it")
+    device = launch.ranges.device
+    native.call("gs3d_bin_redo", ctypes.byref(launch.args), native.ptr(redo), native.ptr(redo_list),
+                native.ptr(launch.scratch), launch.scratch.numel(), native.stream(device))
+    launch.scratch = None
 
 
 def bin_rows(centers: Tensor, radii: Tensor, order: Tensor, offsets: Tensor, group_pairs: int, tile_pairs: int,

@@ -58,6 +58,17 @@ int gs3d_camera_prepare(const float* views, const float* Ks, int32_t count,
                         float* full, float* inverse, float* centers,
                         int32_t* errors, void* stream);
 
+/* gs3d_camera_prepare that also writes keys (count uint64, 8-byte aligned;
+ * NULL: none): a 64-bit key of each camera's view matrix and intrinsics,
+ * with each value rounded to 12 mantissa bits, so that equal cameras (and
+ * poses an optimiser step apart) share a key.  No counterpart in the
+ * reference: the rasterizer uses the keys to find the tile-list caps that
+ * an earlier frame of the same camera measured (gs3d_render_args.caps). */
+int gs3d_camera_prepare_keyed(const float* views, const float* Ks, int32_t count,
+                              int32_t width, int32_t height, int32_t with_centers,
+                              float* full, float* inverse, float* centers,
+                              int32_t* errors, uint64_t* keys, void* stream);
+
 /* Replaces splatting/camera_kernels.py:69-106 (backward_kernel), launched from
  * splatting/cameras.py:98-114.  grad_full and/or grad_centers may be NULL.
  * Writes grad_views (count,4,4) (overwritten, not accumulated). */
@@ -322,6 +333,13 @@ typedef struct gs3d_bin_args {
     const float* conics;           /* (views,N,4), as given to gs3d_order_rows */
     int32_t tile_mode;             /* the tile_mode given to gs3d_order_rows */
     const float* footprints;       /* ACCUTILE: the footprints gs3d_order_rows wrote */
+    /* Optional (views*tiles): per tile, the number of list entries an earlier
+     * frame's forward blend read (gs3d_render_args.stop_out), negative for
+     * "the whole list".  Each tile's list is then written only up to
+     * stop + stop/4 + 128 entries (ranges stay whole); a forward blend given
+     * the same caps reads no further and flags the tiles that needed more,
+     * whose whole lists gs3d_bin_redo then writes.  NULL: whole lists. */
+    const int32_t* caps;
 } gs3d_bin_args;
 
 size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t width, int32_t height,
@@ -342,6 +360,15 @@ int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes
  * Same reference counterpart as gs3d_bin_rows (splatting/binning.py:16-117). */
 int gs3d_emit_group_items(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream);
 int gs3d_bin_emitted_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream);
+
+/* No counterpart in the reference (the reference writes whole lists): after
+ * gs3d_bin_rows / gs3d_bin_emitted_rows with caps, and with the same
+ * arguments and untouched scratch, writes the whole lists of the tiles whose
+ * redo flag (views*tiles int32, from gs3d_render_args.redo) is nonzero.
+ * redo_list is the capped blend's gs3d_render_args.redo_list: with its count
+ * zero the launch ends without reading the binning state. */
+int gs3d_bin_redo(const gs3d_bin_args* args, const int32_t* redo, const int32_t* redo_list,
+                  void* scratch, size_t scratch_bytes, void* stream);
 
 /* Global tile id of every listed pair: tiles[p] = t for p in ranges[t]. */
 int gs3d_pair_tiles(const int32_t* ranges, int64_t tile_count, uint32_t* tiles, int64_t count,
@@ -399,6 +426,25 @@ typedef struct gs3d_render_args {
      * without a fill kernel of their own.  NULL / 0: nothing is cleared. */
     float* zero_out;
     int64_t zero_count;
+    /* Optional, gs3d_render_fwd only -- not with statistics or pair counts
+     * (no counterpart in the reference): caps as gs3d_bin_args.caps -- each tile's list is read no further than
+     * the capped id-write pass wrote it.  Required with caps: redo
+     * (views*tiles int32) receives 1 for the tiles that still had live
+     * pixels there while their lists are longer (their outputs are then
+     * incomplete), 0 for the others, and redo_list (1 + views*tiles int32,
+     * redo_list[0] zero before the launch) receives their count in [0] and
+     * the tiles from [1], in no particular order.  stop_out (views*tiles
+     * int32) receives, per tile, the list entries read before every pixel
+     * terminated (-1: the whole list did not suffice), the caps of a later
+     * frame.  redo_pass = 1: a redo launch -- only the tiles in redo_list are
+     * blended, with whole lists (after gs3d_bin_redo), into the same outputs
+     * (stop_out, if given, receives their stops); caps and redo are ignored
+     * and the other tiles are untouched. */
+    const int32_t* caps;
+    int32_t* stop_out;
+    int32_t* redo;
+    int32_t* redo_list;
+    int32_t redo_pass;
 } gs3d_render_args;
 
 int gs3d_render_fwd(const gs3d_render_args* args, void* stream);

@@ -34,7 +34,10 @@ def build(force: bool = False) -> str:
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
-        if not os.path.exists(_LIB_PATH):
+        # The default build is brought up to date first: a library built
+        # against an older include/gs3d_hip.h would read the argument structs
+        # with their old layout.
+        if not os.environ.get("ORACLE_LIBRARY") or not os.path.exists(_LIB_PATH):
             build()
         _lib = ctypes.CDLL(_LIB_PATH)
         P = ctypes.c_void_p

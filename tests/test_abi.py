@@ -84,6 +84,36 @@ def test_argument_errors_are_reported_without_launching():
     st.requests, st.sum_mask, st.sums = 2, 0b10, None
     assert lib.gs3d_render_fwd_stats(ctypes.byref(args), ctypes.byref(st), None) == abi.GS3D_ERR_ARGUMENT
     assert lib.gs3d_render_fwd_stats(ctypes.byref(args), None, None) == abi.GS3D_ERR_ARGUMENT
+    # Capped lists: a capped blend must be given its overflow flags; a redo
+    # blend (which skips tiles) can neither clear a buffer nor total
+    # statistics, and neither can a capped one.
+    args.final_t = args.contributors = args.image = args.image_alpha = ctypes.c_void_p(256)
+    args.caps = ctypes.c_void_p(256)
+    assert lib.gs3d_render_fwd(ctypes.byref(args), None) == abi.GS3D_ERR_ARGUMENT
+    args.redo = ctypes.c_void_p(256)
+    assert lib.gs3d_render_fwd(ctypes.byref(args), None) == abi.GS3D_ERR_ARGUMENT  # no redo_list
+    st.requests, st.sum_mask, st.sums = 1, 0b1, ctypes.c_void_p(256)
+    args.redo_list = ctypes.c_void_p(256)
+    assert lib.gs3d_render_fwd_stats(ctypes.byref(args), ctypes.byref(st), None) == abi.GS3D_ERR_ARGUMENT
+    args.caps = args.redo = None
+    args.redo_pass = 1
+    args.zero_out, args.zero_count = ctypes.c_void_p(256), 4
+    assert lib.gs3d_render_fwd(ctypes.byref(args), None) == abi.GS3D_ERR_ARGUMENT
+    args.zero_out, args.zero_count = None, 0
+    assert lib.gs3d_render_fwd_stats(ctypes.byref(args), ctypes.byref(st), None) == abi.GS3D_ERR_ARGUMENT
+    assert lib.gs3d_render_pair_counts(ctypes.byref(args), ctypes.c_void_p(256), None) == abi.GS3D_ERR_ARGUMENT
+    args.redo_pass, args.stop_out = 0, ctypes.c_void_p(256)
+    assert lib.gs3d_render_fwd_stats(ctypes.byref(args), ctypes.byref(st), None) == abi.GS3D_ERR_ARGUMENT
+    assert lib.gs3d_render_pair_counts(ctypes.byref(args), ctypes.c_void_p(256), None) == abi.GS3D_ERR_ARGUMENT
+    args.redo_pass, args.stop_out = 1, None
+    args.redo_list = None
+    assert lib.gs3d_render_fwd(ctypes.byref(args), None) == abi.GS3D_ERR_ARGUMENT
+    args.redo_pass = 0
+    args.final_t = args.contributors = args.image = args.image_alpha = None
+    # Camera keys are 8-byte aligned.
+    p = ctypes.c_void_p(256)
+    assert lib.gs3d_camera_prepare_keyed(p, p, 1, 10, 10, 0, p, None, None, p, ctypes.c_void_p(260),
+                                         None) == abi.GS3D_ERR_ARGUMENT
     # The blend VJP's gradient row strides feed 32-bit multipliers: a stride
     # of 2^31 or more is rejected before any launch.
     bwd = abi.RenderBwdArgs()
@@ -99,6 +129,15 @@ def test_argument_errors_are_reported_without_launching():
     args.group_pairs, args.tile_pairs = 1 << 31, 5
     args.ranges = ctypes.c_void_p(256)
     assert lib.gs3d_bin_rows(ctypes.byref(args), None, 0, None) == abi.GS3D_ERR_OVERFLOW
+    p = ctypes.c_void_p(256)
+    assert lib.gs3d_bin_redo(ctypes.byref(args), p, p, None, 0, None) == abi.GS3D_ERR_OVERFLOW
+    assert lib.gs3d_bin_redo(ctypes.byref(args), None, p, None, 0, None) == abi.GS3D_ERR_ARGUMENT
+    assert lib.gs3d_bin_redo(ctypes.byref(args), p, None, None, 0, None) == abi.GS3D_ERR_ARGUMENT
+    assert lib.gs3d_bin_redo(None, p, p, None, 0, None) == abi.GS3D_ERR_ARGUMENT
+    args.group_pairs = 5
+    assert lib.gs3d_bin_redo(ctypes.byref(args), p, p, p, 1, None) == abi.GS3D_ERR_ARGUMENT  # no ids
+    args.ids = p
+    assert lib.gs3d_bin_redo(ctypes.byref(args), p, p, p, 1, None) == abi.GS3D_ERR_SCRATCH
     with pytest.raises(native.NativeLibraryError, match="invalid argument"):
         native.call("gs3d_scan_i32", None, -1, None, None, None, 0, None)
     # The allocation-free sort rejects counts beyond its static scratch before

@@ -197,3 +197,35 @@ def test_launch_wrappers_run_without_gradients():
         probe(x)
     assert seen == [False, False] and torch.is_grad_enabled()
     assert probe.__name__ == "probe"
+
+
+def test_capped_list_stop_cache_keeps_recent_cameras(monkeypatch):
+    # The stop cache (one int32 row per tile and camera) drops the least
+    # recently rendered cameras beyond its byte limit; a camera rendered
+    # again moves to the back, and its row is the latest frame's.
+    from dsl_splat_amd.gs3d import lists as tile_lists
+
+    tile_lists.clear()
+    tiles = 1000
+    monkeypatch.setattr(tile_lists, "CACHE_BYTES", 10 * tiles * 4)
+    try:
+        frames = []
+        for f in range(6):
+            stops = torch.full((2, tiles), f, dtype=torch.int32)
+            lists = tile_lists.CappedLists([f * 2, f * 2 + 1], (None, 64, 48, "radius"), 7, None, stops, None)
+            tile_lists.remember(lists)
+            frames.append(stops)
+        assert tile_lists._BYTES == 10 * tiles * 4
+        shape = (None, 64, 48, "radius")
+        assert sorted(k[-1] for k in tile_lists._STOPS) == list(range(2, 12))
+        again = torch.full((1, tiles), 99, dtype=torch.int32)
+        tile_lists.remember(tile_lists.CappedLists([2], shape, 7, None, again, None))
+        assert tile_lists._BYTES == 10 * tiles * 4
+        assert next(reversed(tile_lists._STOPS))[-1] == 2
+        stops, row, stream = tile_lists._STOPS[shape + (2,)]
+        assert stops is again and row == 0 and stream == 7
+        tile_lists.remember(tile_lists.CappedLists([100], shape, 7, None, again, None))
+        assert shape + (3,) not in tile_lists._STOPS and shape + (2,) in tile_lists._STOPS
+    finally:
+        tile_lists.clear()
+    assert tile_lists._BYTES == 0 and not tile_lists._STOPS
