@@ -174,7 +174,7 @@ def frame_info(scene):
     rasterizer makes) for the byte accounting, and the blend's pair counts
     from the counting forward pass (outside any timed region)."""
     import torch
-    from dsl_splat_amd.gs3d import projection as gproj, render as grender
+    from dsl_splat_amd.gs3d import lists as tile_lists, projection as gproj, render as grender
     from dsl_splat_amd.splatting import binning, cameras
 
     deg, sh = scene.sh_degree, scene.sh_coeffs
@@ -194,15 +194,28 @@ def frame_info(scene):
         feats = st.colors if sh is not None else scene.features
         pairs = grender.pair_counts(ranges, ids, st.centers, st.conics, feats, scene.width, scene.height,
                                     extra=scene.extra_features)
+        tiles = binning.tile_count(scene.width, scene.height, views)
+        capped = {}
+        if tile_lists.applies(count, tiles):
+            # The steady-state frames of the timed steps write lists capped
+            # by the same cameras' stops: the ids they keep, and the group
+            # items their write pass reads.
+            stops = torch.empty((views, tiles // views), dtype=torch.int32, device=st.radii.device)
+            grender.render_views(ranges, ids, st.centers, st.conics, feats, scene.width, scene.height,
+                                 extra=scene.extra_features, lists=tile_lists.CappedLists([], (), 0, None, stops))
+            launch = binning.prepare_bin_rows(st.centers, st.radii, order, offsets, scene.width, scene.height)
+            binning.launch_bin_rows(launch, group_pairs, count, caps=stops.view(-1))
+            capped = dict(items_loaded=binning.capped_items_loaded(launch),
+                          ids_written=int(tile_lists.capped_lengths(stops, ranges[:, 1] - ranges[:, 0]).sum()))
+            del launch
         torch.cuda.synchronize()
-    tiles = binning.tile_count(scene.width, scene.height, views)
     groups = views * (((scene.width + 15) // 16 + 7) // 8) * (((scene.height + 15) // 16 + 7) // 8)
     info = dict(pairs=count, group_pairs=group_pairs, groups=groups, tiles=tiles,
                 group_passes=1 if groups <= 1024 else math.ceil(int(groups - 1).bit_length() / 8),
                 rows=views * n, visible=int((st.radii > 0).sum()), blend_pairs=pairs,
                 # radix passes of the depth order in the timed steps (they sort
                 # the key bits the frame's kept rows need)
-                order_passes=binning.order_pass_count(max(9, int(key_bits.item()))))
+                order_passes=binning.order_pass_count(max(9, int(key_bits.item()))), capped=capped)
     return info, dict(full=full, st=st, ranges=ranges, ids=ids, feats=feats)
 
 
@@ -210,6 +223,7 @@ def stage_bytes(scene, info):
     """Algorithmic bytes of every HBM-bound stage: what its kernels must read
     and write once each."""
     M, S, T, R, V = info["pairs"], info["group_pairs"], info["tiles"], info["rows"], info["visible"]
+    cap = info["capped"]
     sh = scene.sh_coeffs
     views, n = scene.viewmats.shape[0], len(scene.means)
     K = 0 if sh is None else sh.shape[-2]
@@ -227,10 +241,12 @@ def stage_bytes(scene, info):
         "order": R * (28 + 4 + 12 + 8) + V * (12 + (info["order_passes"] - 1) * 28 + 4) + (R - V) * 12,
         # items: records and offsets in (12 B/row), items out (8 B/item); group sort (keys read for the
         # histogram 8 + read and written 16 per pass; one 10-bit pass up to 1024 groups, whose digit
-        # scan gives the group ranges, else 8-bit passes and a range search, 8 B/item); count and
-        # write passes read items (2 x 8 B); ids out (4 B/pair); tile totals/starts/ranges (16 B/tile)
-        "bin": R * 12 + S * (8 + 24 * info["group_passes"] + (16 if info["group_passes"] == 1 else 24))
-               + M * 4 + T * 16,
+        # scan gives the group ranges, else 8-bit passes and a range search, 8 B/item); the count pass
+        # reads the items (8 B); the write pass reads the items of the chunks it needs (8 B; all of
+        # them for whole lists) and writes the ids it keeps (4 B/pair; all pairs for whole lists);
+        # tile totals/starts/ranges (16 B/tile), and the caps (4 B/tile) for capped lists
+        "bin": R * 12 + S * (8 + 24 * info["group_passes"] + (8 if info["group_passes"] == 1 else 16))
+               + cap.get("items_loaded", S) * 8 + cap.get("ids_written", M) * 4 + T * (20 if cap else 16),
         # params 44 + SH 4K*3 in, per view radii 4 + centre/conic grads 24 (+ colour grads 12) in;
         # grads 44 + SH out
         "project_bwd": n * 88 + 2 * sh_in + views * n * (28 + (12 if sh is not None else 0)),
@@ -491,6 +507,7 @@ def run_workload(workload, n, device, steps, warmup, cpu, tile_mode="radius", mi
                             "totals_read)"},
         pairs=dict(tile_pairs=info["pairs"], group_items=info["group_pairs"], visible_rows=info["visible"],
                    rows=info["rows"], **info["blend_pairs"]),
+        capped_lists=info["capped"] or None,
     )
     torch.cuda.synchronize()
     if cpu:
@@ -607,6 +624,7 @@ def main():
         "stages_1_3": head["stages_1_3"],
         "staged_ms": head["staged_ms"],
         "pairs": head["pairs"],
+        "capped_lists": head["capped_lists"],
         "tile_modes": modes,
         "sort_pairs": sort_pairs,
         "statistics": {"requests": "masked count + weighted sum, per-view maps",

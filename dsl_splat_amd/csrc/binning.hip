@@ -1659,7 +1659,8 @@ __global__ void chunk_group_kernel(const int32_t* __restrict__ chunk_base, int g
 //
 // LISTS (write pass): 0 whole lists; 1 each tile's first list_cap(caps[t])
 // entries; 2 a redo pass, the whole lists of the tiles flagged in redo
-// (redo_count of them).
+// (redo_count of them); 3 no pass, only the number of group items mode 1
+// would load, added to *loaded.
 template <bool WRITE, bool MASKS, bool BUF = false, int LISTS = 0>
 __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     const uint64_t* __restrict__ items, const uint64_t* __restrict__ masks, const int32_t* __restrict__ granges,
@@ -1667,7 +1668,8 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     const int32_t* __restrict__ chunk_group, int groups, int64_t max_chunks, GridDims d,
     uint32_t* __restrict__ counts, const int32_t* __restrict__ scanned, const int32_t* __restrict__ tile_start,
     int32_t* __restrict__ ids, int64_t id_limit, const int32_t* __restrict__ caps, const int32_t* __restrict__ redo,
-    const int32_t* __restrict__ redo_count) {
+    const int32_t* __restrict__ redo_count, const int32_t* __restrict__ totals,
+    unsigned long long* __restrict__ loaded) {
     static_assert(LISTS == 0 || WRITE, "caps and redo flags are write-pass arguments");
     // A chunk's run for one tile, then one slot per lane that rejected items
     // are written to (so the writes need neither a branch nor an exec mask).
@@ -1772,14 +1774,20 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
             if (inside) {
                 const uint32_t rel = (uint32_t)(scanned[slot + s] - scanned[slot]);
                 init = (uint32_t)tile_start[gt] + rel;
-                if constexpr (LISTS == 1) {
+                if constexpr (LISTS == 1 || LISTS == 3) {
+                    // Wanted while the tile has entries left below its cap
+                    // (a tile whose list ends first stops wanting chunks).
                     const uint32_t cap = list_cap(caps[gt]);
-                    want = rel < cap;
+                    want = rel < min(cap, (uint32_t)totals[gt]);
                     limit = want ? cap - rel : 0u;
                 }
             }
             if constexpr (LISTS != 0) {
                 want_tiles = __ballot(want);
+                if constexpr (LISTS == 3) {
+                    if (lane == 0 && want_tiles) atomicAdd(loaded, (unsigned long long)(end - begin));
+                    return;
+                }
                 if (want_tiles == 0) return;
             }
         }
@@ -2447,12 +2455,14 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
         hipLaunchKernelGGL((gs3d::group_pass_kernel<false, true>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,
                            sc.masks, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts,
                            (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0,
-                           (const int32_t*)nullptr, (const int32_t*)nullptr, (const int32_t*)nullptr);
+                           (const int32_t*)nullptr, (const int32_t*)nullptr, (const int32_t*)nullptr,
+                           (const int32_t*)nullptr, (unsigned long long*)nullptr);
     else
         hipLaunchKernelGGL((gs3d::group_pass_kernel<false, false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,
                            (const uint64_t*)nullptr, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d,
                            sc.counts, (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0,
-                           (const int32_t*)nullptr, (const int32_t*)nullptr, (const int32_t*)nullptr);
+                           (const int32_t*)nullptr, (const int32_t*)nullptr, (const int32_t*)nullptr,
+                           (const int32_t*)nullptr, (unsigned long long*)nullptr);
     status = gs3d::run_scan<uint32_t, false>(sc.counts, 64 * chunks, sc.scanned, nullptr, sc.scan, s);
     if (status != GS3D_OK) return status;
     hipLaunchKernelGGL(gs3d::tile_totals_kernel, dim3(gs3d::blocks_for(tiles, 256)), dim3(256), 0, s, sc.chunk_base,
@@ -2474,7 +2484,7 @@ constexpr unsigned kRedoPassGrid = 1024;
 template <int LISTS>
 void launch_write_pass(const gs3d_bin_args& a, const BinScratch& sc, const uint64_t* items, int64_t groups,
                        int64_t chunks, const GridDims& d, const int32_t* caps, const int32_t* redo,
-                       const int32_t* redo_count, hipStream_t s) {
+                       const int32_t* redo_count, hipStream_t s, unsigned long long* loaded = nullptr) {
     const bool accu = a.tile_mode == GS3D_TILE_ACCUTILE;
     const unsigned blocks = (unsigned)blocks_for(chunks, kBinWaves);
     const dim3 pass_grid(LISTS == 2 ? min(blocks, kRedoPassGrid) : blocks);
@@ -2484,7 +2494,7 @@ void launch_write_pass(const gs3d_bin_args& a, const BinScratch& sc, const uint6
     hipLaunchKernelGGL((group_pass_kernel<true, M, B, LISTS>), pass_grid, dim3(kBinThreads), 0, s, items,          \
                        M ? (const uint64_t*)sc.masks : nullptr, sc.granges, sc.chunk_base, sc.chunk_group,        \
                        (int)groups, chunks, d, sc.counts, sc.scanned, sc.starts, a.ids, a.tile_pairs, caps, redo, \
-                       redo_count)
+                       redo_count, sc.totals, loaded)
     if (accu) {
         if (buf)
             GS3D_WRITE_PASS(true, true);
@@ -2516,31 +2526,68 @@ extern "C" int gs3d_bin_rows(const gs3d_bin_args* args, void* scratch, size_t sc
     return gs3d::bin_rows(args, scratch, scratch_bytes, stream, false);
 }
 
-extern "C" int gs3d_bin_redo(const gs3d_bin_args* args, const int32_t* redo, const int32_t* redo_list,
-                             void* scratch, size_t scratch_bytes, void* stream) {
-    if (!args || !redo || !redo_list) return GS3D_ERR_ARGUMENT;
-    const gs3d_bin_args& a = *args;
+namespace gs3d {
+
+// The binning state that gs3d_bin_rows / gs3d_bin_emitted_rows left in the
+// scratch, for passes that follow them with the same arguments.
+struct BinState {
+    BinScratch sc;
+    const uint64_t* items;  // the sorted group items
+    int64_t groups, chunks;
+    GridDims d;
+};
+
+// GS3D_OK with *state filled, 1 when the frame has no pairs (nothing to
+// do), or an error status.
+int bin_state(const gs3d_bin_args& a, void* scratch, size_t scratch_bytes, BinState* state) {
     if (a.n < 0 || a.views < 0 || a.width <= 0 || a.height <= 0 || a.group_pairs < 0 || a.tile_pairs < 0)
         return GS3D_ERR_ARGUMENT;
-    const gs3d::GridDims d = gs3d::grid_dims(a.width, a.height);
+    const GridDims d = grid_dims(a.width, a.height);
     const int64_t rows = (int64_t)a.n * a.views;
     const int64_t groups = (int64_t)a.views * d.gpv, tiles = (int64_t)a.views * d.tpv;
-    if (tiles == 0 || a.group_pairs == 0 || a.tile_pairs == 0 || rows == 0) return GS3D_OK;
+    if (tiles == 0 || a.group_pairs == 0 || a.tile_pairs == 0 || rows == 0) return 1;
     if (rows > INT32_MAX || a.group_pairs > INT32_MAX || a.tile_pairs > INT32_MAX) return GS3D_ERR_OVERFLOW;
-    if (groups >= (int64_t)1 << gs3d::kGroupBits || d.gx >= 0xFFFF || d.gy >= 0xFFFF) return GS3D_ERR_UNSUPPORTED;
+    if (groups >= (int64_t)1 << kGroupBits || d.gx >= 0xFFFF || d.gy >= 0xFFFF) return GS3D_ERR_UNSUPPORTED;
     if (!a.ids || !scratch) return GS3D_ERR_ARGUMENT;
     if (scratch_bytes < gs3d_bin_rows_scratch_bytes(a.group_pairs, a.views, a.width, a.height, a.tile_mode))
         return GS3D_ERR_SCRATCH;
     const bool accu = a.tile_mode == GS3D_TILE_ACCUTILE;
-    gs3d::BinScratch sc;
-    gs3d::bin_scratch_bytes(a.group_pairs, groups, tiles, accu, &sc, scratch);
+    bin_scratch_bytes(a.group_pairs, groups, tiles, accu, &state->sc, scratch);
     const int64_t S = a.group_pairs;
-    const int group_bits = gs3d::bit_length(groups - 1 > 0 ? groups - 1 : 1);
+    const int group_bits = bit_length(groups - 1 > 0 ? groups - 1 : 1);
     // Where bin_rows left the sorted items: the second half after the
     // one-pass group sort, the first otherwise.
-    const uint64_t* items = !accu && group_bits <= gs3d::kOnePassBits ? sc.items + S : sc.items;
-    return gs3d::write_pass(a, sc, items, groups, gs3d::max_chunks_of(S, groups), d, nullptr, redo, redo_list,
+    state->items = !accu && group_bits <= kOnePassBits ? state->sc.items + S : state->sc.items;
+    state->groups = groups;
+    state->chunks = max_chunks_of(S, groups);
+    state->d = d;
+    return GS3D_OK;
+}
+
+}  // namespace gs3d
+
+extern "C" int gs3d_bin_redo(const gs3d_bin_args* args, const int32_t* redo, const int32_t* redo_list,
+                             void* scratch, size_t scratch_bytes, void* stream) {
+    if (!args || !redo || !redo_list) return GS3D_ERR_ARGUMENT;
+    gs3d::BinState st;
+    const int status = gs3d::bin_state(*args, scratch, scratch_bytes, &st);
+    if (status != GS3D_OK) return status == 1 ? GS3D_OK : status;
+    return gs3d::write_pass(*args, st.sc, st.items, st.groups, st.chunks, st.d, nullptr, redo, redo_list,
                             gs3d::as_stream(stream));
+}
+
+extern "C" int gs3d_bin_capped_items(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes,
+                                     uint64_t* items_loaded, void* stream) {
+    if (!args || !args->caps || !items_loaded || (reinterpret_cast<uintptr_t>(items_loaded) & 7))
+        return GS3D_ERR_ARGUMENT;
+    gs3d::BinState st;
+    hipStream_t s = gs3d::as_stream(stream);
+    gs3d::fill_u32(reinterpret_cast<uint32_t*>(items_loaded), 2, 0u, s);
+    const int status = gs3d::bin_state(*args, scratch, scratch_bytes, &st);
+    if (status != GS3D_OK) return status == 1 ? gs3d::launch_status("gs3d_bin_capped_items") : status;
+    gs3d::launch_write_pass<3>(*args, st.sc, st.items, st.groups, st.chunks, st.d, args->caps, nullptr, nullptr, s,
+                               reinterpret_cast<unsigned long long*>(items_loaded));
+    return gs3d::launch_status("gs3d_bin_capped_items");
 }
 
 extern "C" int gs3d_emit_group_items(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, void* stream) {

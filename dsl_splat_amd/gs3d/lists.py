@@ -81,6 +81,20 @@ class CappedLists:
         self.launch = None
 
 
+def applies(tile_pairs: int, tiles: int) -> bool:
+    """Whether a frame of ``tile_pairs`` pairs over ``tiles`` tiles (all
+    cameras) caps its lists once its cameras have stops."""
+    return ENABLED and tiles > 0 and tile_pairs >= max(MIN_PAIRS, MIN_PAIRS_PER_TILE * tiles)
+
+
+def capped_lengths(stops: Tensor, lengths: Tensor) -> Tensor:
+    """Entries of each tile's list that a capped id-write pass keeps: the
+    list length, or stop + stop/4 + 128 when that is shorter (int64)."""
+    s = stops.reshape(-1).to(torch.int64)
+    n = lengths.reshape(-1).to(torch.int64)
+    return torch.where(s < 0, n, torch.minimum(n, s + s // 4 + 128))
+
+
 def clear() -> None:
     """Forget every camera's stops."""
     global _BYTES
@@ -93,7 +107,7 @@ def plan(device: torch.device, width: int, height: int, tile_mode: str, keys: li
          tiles_per_view: int) -> CappedLists | None:
     """The frame's caps from the stop cache; None when the frame writes whole
     lists without measuring stops (caps off or a small frame)."""
-    if not ENABLED or not keys or tile_pairs < max(MIN_PAIRS, MIN_PAIRS_PER_TILE * len(keys) * tiles_per_view):
+    if not keys or not applies(tile_pairs, len(keys) * tiles_per_view):
         return None
     shape = (device.index, width, height, tile_mode)
     stream = native.stream(device).value or 0

@@ -297,6 +297,7 @@ FUNCTIONS = {
     "gs3d_emit_group_items": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
     "gs3d_bin_emitted_rows": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P]),
     "gs3d_bin_redo": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _P, _P, _SZ, _P]),
+    "gs3d_bin_capped_items": (ctypes.c_int, [ctypes.POINTER(BinArgs), _P, _SZ, _P, _P]),
     "gs3d_pair_tiles": (ctypes.c_int, [_P, _I64, _P, _I64, _P]),
     "gs3d_sort_pairs_u32": (ctypes.c_int, [_P, _P, _I64, _I32, _P, _SZ, _P]),
     "gs3d_expand_keys": (ctypes.c_int, [_P, _P, _I64, _P, _I32, _I32, _P, _P]),

@@ -337,6 +337,20 @@ def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int,
 
 
 @native.no_grad
+def capped_items_loaded(launch: BinLaunch) -> int:
+    """Group items the capped id-write pass of ``launch`` (a launch_bin_rows
+    with caps, before redo_bin_rows) read (gs3d_bin_capped_items);
+    synchronises."""
+    if launch.scratch is None or launch.caps is None:
+        raise RuntimeError("capped_items_loaded needs a launch_bin_rows with caps before it")
+    device = launch.ranges.device
+    out = torch.empty(1, dtype=torch.int64, device=device)
+    native.call("gs3d_bin_capped_items", ctypes.byref(launch.args), native.ptr(launch.scratch),
+                launch.scratch.numel(), native.ptr(out), native.stream(device))
+    return int(out.item())
+
+
+@native.no_grad
 def redo_bin_rows(launch: BinLaunch, redo: Tensor, redo_list: Tensor) -> None:
     """Write the whole lists of the tiles flagged in ``redo`` (views*tiles
     int32, from a capped blend, whose ``redo_list`` starts with their count)

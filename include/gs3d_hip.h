@@ -370,6 +370,14 @@ int gs3d_bin_emitted_rows(const gs3d_bin_args* args, void* scratch, size_t scrat
 int gs3d_bin_redo(const gs3d_bin_args* args, const int32_t* redo, const int32_t* redo_list,
                   void* scratch, size_t scratch_bytes, void* stream);
 
+/* Measurement aid, no counterpart in the reference: after gs3d_bin_rows with
+ * the same arguments (caps required) and untouched scratch, writes to
+ * *items_loaded (one uint64, 8-byte aligned) the number of group items the
+ * capped id-write pass reads -- those of every chunk that some tile of its
+ * group still needed -- without repeating the pass. */
+int gs3d_bin_capped_items(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes,
+                          uint64_t* items_loaded, void* stream);
+
 /* Global tile id of every listed pair: tiles[p] = t for p in ranges[t]. */
 int gs3d_pair_tiles(const int32_t* ranges, int64_t tile_count, uint32_t* tiles, int64_t count,
                     void* stream);

@@ -65,6 +65,43 @@ def _project(scene, degree):
         sh_degree=degree or 0, camera_centers=centers if with_centers else None, metadata=True)
 
 
+def _capped_items(ranges, ids, depths, caps, width, height):
+    """Group items the capped id-write pass must read, from the whole lists.
+
+    A group's items are the rows that touch any of its 8x8 tiles (radius
+    mode: a row's tile square meets the group exactly where it covers
+    tiles), in depth order (ties by row).  The pass reads, per group, every
+    512-item chunk that starts at or before the item holding some tile's
+    min(L, cap)-th entry; returns that count and the group item total."""
+    V, N = depths.shape
+    gx, gy = (width + 15) // 16, (height + 15) // 16
+    sgx, sgy = (gx + 7) // 8, (gy + 7) // 8
+    tpv, gpv = gx * gy, sgx * sgy
+    T = V * tpv
+    lengths = ranges[:, 1] - ranges[:, 0]
+    t = np.arange(T)
+    local = t % tpv
+    group = (t // tpv) * gpv + (local // gx // 8) * sgx + (local % gx) // 8
+    # depth rank of every (view, row), ties by row
+    rank = np.empty(V * N, np.int64)
+    for v in range(V):
+        o = np.lexsort((np.arange(N), depths[v]))
+        rank[v * N + o] = np.arange(N)
+    tile_of = np.repeat(t, lengths)
+    key = group[tile_of].astype(np.int64) * (V * N) + rank[(tile_of // tpv) * N + ids]
+    items = np.unique(key)
+    item_group = items // (V * N)
+    group_start = np.searchsorted(item_group, np.arange(V * gpv))
+    pos = np.searchsorted(items, key) - group_start[group[tile_of]]
+    k = np.minimum(lengths, caps)
+    need = np.zeros(V * gpv, np.int64)
+    has = k > 0
+    last_pos = pos[(ranges[:, 0] + k - 1)[has]]
+    np.maximum.at(need, group[has], last_pos // 512 + 1)
+    size = np.bincount(item_group, minlength=V * gpv)
+    return int(np.minimum(need * 512, size).sum()), len(items)
+
+
 class _PoisonedTorch:
     """torch, except that new int32 tensors start filled with -1 (so an id
     the write pass should have written and did not shows up)."""
@@ -137,6 +174,16 @@ def test_capped_write_pass_writes_each_tile_prefix(key, monkeypatch):
         assert (got[~written] == -1).all(), "ids written beyond a tile's cap"
 
     check(pos < keep_len[tile_of])
+    # The items the capped pass read: every chunk (kChunk = 512 consecutive
+    # items of a group) that some tile of the group still needed, i.e. that
+    # starts before the tile's min(L, cap)-th entry.  With every cap at
+    # infinity that is every item.
+    loaded = binning.capped_items_loaded(launch)
+    assert 0 < loaded <= S
+    if mode == "radius":
+        want_loaded, group_items = _capped_items(ranges_np, want, _np(st.depths), _cap(stops), W, H)
+        assert group_items == S
+        assert loaded == want_loaded
     flags = (rng.random(tiles) < 0.3).astype(np.int32)
     listed = np.concatenate([[flags.sum()], np.flatnonzero(flags), np.zeros(tiles - flags.sum())]).astype(np.int32)
     flags_t, listed_t = torch.from_numpy(flags).to(DEV), torch.from_numpy(listed).to(DEV)
