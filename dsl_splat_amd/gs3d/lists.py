@@ -16,11 +16,11 @@ whole lists whatever the caps were; a stale cap costs only the redo.
 
 The first frame of a camera writes whole lists (no stops known), and so do
 frames with statistics, frames binned per camera group and frames of fewer
-than MIN_PAIRS tile pairs or MIN_PAIRS_PER_TILE pairs per tile: a capped
-frame launches three more kernels (the count's clearing, gs3d_bin_redo, the
-redo blend; ~14 us on MI355X when no tile overflows), which only long lists
-repay (measured: 4M-pair 720p frames of ~2100 pairs per tile lose ~12 us,
-1080p frames of ~5200 pairs per tile gain ~190 us).  GS3D_LIST_CAPS=0 turns
+than MIN_PAIRS tile pairs: a capped frame launches three more kernels (the
+count's clearing, gs3d_bin_redo, the redo blend; ~13 us on MI355X when no
+tile overflows) and does ~20 us more host work, which only a long id-write
+pass repays (measured per step: 20.8M-pair frames lose 30-50 us, frames of
+93M-171M pairs gain 100-170 us in every tile mode).  GS3D_LIST_CAPS=0 turns
 the caps off.
 """
 
@@ -36,9 +36,8 @@ from ..runtime import native
 from ..splatting import binning
 
 ENABLED = os.environ.get("GS3D_LIST_CAPS", "1") != "0"
-# Frames with fewer tile pairs, or fewer per tile, write whole lists.
-MIN_PAIRS = 1 << 22
-MIN_PAIRS_PER_TILE = 4096
+# Frames with fewer tile pairs write whole lists.
+MIN_PAIRS = 48 << 20
 # The stop cache keeps at most this many bytes of stop rows (one int32 per
 # tile per camera, 32 KB per 1920x1080 camera), dropping the least recently
 # rendered cameras first.
@@ -84,7 +83,7 @@ class CappedLists:
 def applies(tile_pairs: int, tiles: int) -> bool:
     """Whether a frame of ``tile_pairs`` pairs over ``tiles`` tiles (all
     cameras) caps its lists once its cameras have stops."""
-    return ENABLED and tiles > 0 and tile_pairs >= max(MIN_PAIRS, MIN_PAIRS_PER_TILE * tiles)
+    return ENABLED and tiles > 0 and tile_pairs >= MIN_PAIRS
 
 
 def capped_lengths(stops: Tensor, lengths: Tensor) -> Tensor:

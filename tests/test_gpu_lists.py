@@ -291,7 +291,6 @@ def test_capped_lists_match_whole_lists(key, monkeypatch):
     real_remember = tile_lists.remember
     monkeypatch.setattr(tile_lists, "remember", lambda lists: (seen.append(lists), real_remember(lists))[1])
     monkeypatch.setattr(tile_lists, "MIN_PAIRS", 0)
-    monkeypatch.setattr(tile_lists, "MIN_PAIRS_PER_TILE", 0)
     ranges = []
     real_bin = api.launch_bin_rows
     monkeypatch.setattr(api, "launch_bin_rows", lambda *a, **k: (lambda r: (ranges.append(r[0]), r)[1])(
@@ -342,7 +341,6 @@ def test_capped_lists_follow_the_cameras(monkeypatch):
     real_remember = tile_lists.remember
     monkeypatch.setattr(tile_lists, "remember", lambda lists: (seen.append(lists), real_remember(lists))[1])
     monkeypatch.setattr(tile_lists, "MIN_PAIRS", 0)
-    monkeypatch.setattr(tile_lists, "MIN_PAIRS_PER_TILE", 0)
     tile_lists.clear()
     try:
         perm = torch.tensor([3, 1, 0, 2], device=DEV)
