@@ -99,9 +99,10 @@ def _pinned_status(numel: int) -> Tensor:
 
 @native.no_grad
 def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height, near, far, radius_clip,
-                   sh, sh_degree, background, tile_mode="radius", capped=True) -> Frame:
+                   sh, sh_degree, background, tile_mode="radius", capped=True, slot=0) -> Frame:
     """Camera rows, fused projection, depth order, one synchronisation, binning
-    (with ``capped``, of lists capped by the cameras' earlier stops)."""
+    (with ``capped``, of lists capped by the cameras' earlier stops; ``slot``:
+    the batch item, whose stops are kept apart from the other items')."""
     profiling.mark("start")
     with_centers = sh_degree is not None and sh_degree > 0
     # One int64 status buffer read back once: [group pairs, tile pairs], the
@@ -164,7 +165,7 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
     if count <= binning.PAIR_LIMIT and group_pairs <= binning.PAIR_LIMIT:
         if capped:
             lists = tile_lists.plan(status.device, width, height, tile_mode, host[3:3 + cameras].tolist(), count,
-                                    launch.ranges.shape[0] // max(cameras, 1))
+                                    launch.ranges.shape[0] // max(cameras, 1), slot=slot)
         caps = lists.caps if lists is not None else None
         ranges, ids = launch_bin_rows(launch, group_pairs, count, early, caps=caps)
         if caps is not None:
@@ -254,6 +255,7 @@ def rasterize(
             radius_clip, colors if sh_degree is not None else None, sh_degree,
             None if layout.backgrounds is None else batch_item(layout.backgrounds, b), tile_mode,
             capped=not statistics,  # a redone tile would total its statistics twice
+            slot=b,
         )
         frames.append(frame)
         st = frame.state

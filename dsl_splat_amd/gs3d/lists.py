@@ -44,7 +44,7 @@ MIN_PAIRS = 48 << 20
 CACHE_BYTES = 64 << 20
 
 _LOCK = threading.Lock()
-# (device index, width, height, tile mode, camera key) -> (stops of the
+# (device index, width, height, tile mode, batch slot, camera key) -> (stops of the
 # frame that rendered the camera last, its row in them, the stream its blend
 # ran on).  Stops are used on that stream only: the binning and the blend
 # of a frame must read equal caps, which a blend still writing them on
@@ -103,12 +103,15 @@ def clear() -> None:
 
 
 def plan(device: torch.device, width: int, height: int, tile_mode: str, keys: list, tile_pairs: int,
-         tiles_per_view: int) -> CappedLists | None:
+         tiles_per_view: int, slot: int = 0) -> CappedLists | None:
     """The frame's caps from the stop cache; None when the frame writes whole
-    lists without measuring stops (caps off or a small frame)."""
+    lists without measuring stops (caps off or a small frame).  ``slot``
+    tells apart the frames of one call that render different Gaussians (the
+    items of a batched call), so that each finds its own stops even when
+    they share a camera."""
     if not keys or not applies(tile_pairs, len(keys) * tiles_per_view):
         return None
-    shape = (device.index, width, height, tile_mode)
+    shape = (device.index, width, height, tile_mode, slot)
     stream = native.stream(device).value or 0
     views = len(keys)
     with _LOCK:

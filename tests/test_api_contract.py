@@ -212,11 +212,11 @@ def test_capped_list_stop_cache_keeps_recent_cameras(monkeypatch):
         frames = []
         for f in range(6):
             stops = torch.full((2, tiles), f, dtype=torch.int32)
-            lists = tile_lists.CappedLists([f * 2, f * 2 + 1], (None, 64, 48, "radius"), 7, None, stops, None)
+            lists = tile_lists.CappedLists([f * 2, f * 2 + 1], (None, 64, 48, "radius", 0), 7, None, stops, None)
             tile_lists.remember(lists)
             frames.append(stops)
         assert tile_lists._BYTES == 10 * tiles * 4
-        shape = (None, 64, 48, "radius")
+        shape = (None, 64, 48, "radius", 0)
         assert sorted(k[-1] for k in tile_lists._STOPS) == list(range(2, 12))
         again = torch.full((1, tiles), 99, dtype=torch.int32)
         tile_lists.remember(tile_lists.CappedLists([2], shape, 7, None, again, None))

@@ -396,3 +396,39 @@ def test_camera_keys():
     cameras.launch_prepare(torch.cat([zero, negzero]), Ks[:1].repeat(2, 1, 1), scene.width, scene.height, False,
                            keys=kz)
     assert kz[0] == kz[1]
+
+
+def test_batch_items_sharing_cameras_keep_their_own_stops(monkeypatch):
+    # Two batch items render different Gaussians through the same cameras:
+    # each finds its own stops on the next call (no overflow), and the images
+    # equal those of whole lists.
+    a = _dense("sh3_1080p_4view", 40000, 160, 96, 47, **DENSE)
+    b = _dense("sh3_1080p_4view", 40000, 160, 96, 48, **DENSE)
+    stack = lambda name: torch.stack([getattr(a, name), getattr(b, name)])  # noqa: E731
+    args = [stack(k) for k in ("means", "quats", "scales", "opacities")]
+    viewmats = torch.stack([a.viewmats, a.viewmats])
+    Ks = torch.stack([a.Ks, a.Ks])
+    sh = stack("sh_coeffs")
+    seen = []
+    real_remember = tile_lists.remember
+    monkeypatch.setattr(tile_lists, "remember", lambda lists: (seen.append(lists), real_remember(lists))[1])
+    monkeypatch.setattr(tile_lists, "MIN_PAIRS", 0)
+    tile_lists.clear()
+    try:
+        run = lambda: gs3d.rasterize(*args, viewmats, Ks, a.width, a.height, sh_coeffs=sh,  # noqa: E731
+                                     sh_degree=3)
+        monkeypatch.setattr(tile_lists, "ENABLED", False)
+        want = run()
+        monkeypatch.setattr(tile_lists, "ENABLED", True)
+        _say("batched items sharing cameras: first call, then one with caps")
+        run()
+        first = seen[-2:]
+        got = run()
+        second = seen[-2:]
+        for i in range(2):
+            assert second[i].caps is not None and int(second[i].redo.sum()) == 0
+            assert torch.equal(second[i].caps.view_as(second[i].stops), first[i].stops)
+        assert not torch.equal(first[0].stops, first[1].stops)
+        assert torch.equal(got.features, want.features) and torch.equal(got.alpha, want.alpha)
+    finally:
+        tile_lists.clear()
