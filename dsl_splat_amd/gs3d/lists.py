@@ -129,11 +129,9 @@ def plan(device: torch.device, width: int, height: int, tile_mode: str, keys: li
             and rows[0][0].shape[0] == views:
         caps = rows[0][0].view(-1)  # the same cameras in the same order as their last frame
     elif any(r is not None for r in rows):
-        caps = torch.full((views, tiles_per_view), -1, dtype=torch.int32, device=device)
-        for i, r in enumerate(rows):
-            if r is not None:
-                caps[i].copy_(r[0][r[1]])
-        caps = caps.view(-1)
+        # One gather launch; cameras without stops read whole lists (-1).
+        whole = torch.full((tiles_per_view,), -1, dtype=torch.int32, device=device) if None in rows else None
+        caps = torch.stack([whole if r is None else r[0][r[1]] for r in rows]).view(-1)
     if caps is None:
         return CappedLists(list(keys), shape, stream, None,
                            torch.empty((views, tiles_per_view), dtype=torch.int32, device=device))
