@@ -893,16 +893,61 @@ __global__ void digit_ranges_kernel(const int32_t* __restrict__ offsets, int64_t
     ranges[2 * d + 1] = end;
 }
 
+// Everything the group passes need from a one-pass group sort, in one
+// workgroup (groups <= 1024): each group's range of sorted items (row 0 of
+// the transposed offsets holds every digit's start), chunk_base (exclusive
+// scan of the groups' chunk counts, the chunk total at [groups]) and the
+// group of every chunk.  One launch instead of three latency-bound ones.
+constexpr int kChunkSteps = 8;  // items per lane of a group chunk (4 and 16 measured slower)
+constexpr int kChunk = 64 * kChunkSteps;  // items of a group ranked by one wavefront
+constexpr int kLayoutThreads = 1024;
+
+__global__ __launch_bounds__(kLayoutThreads) void group_layout_kernel(const int32_t* __restrict__ offsets,
+                                                                      int64_t count, int digits, int groups,
+                                                                      int32_t* __restrict__ ranges,
+                                                                      int32_t* __restrict__ chunk_base,
+                                                                      int32_t* __restrict__ chunk_group) {
+    __shared__ int32_t s_wave[kLayoutThreads / 64];
+    __shared__ int32_t s_base[kLayoutThreads + 1];
+    const int g = threadIdx.x;
+    int32_t q = 0;
+    if (g < groups) {
+        const int32_t start = offsets[g];
+        const int32_t end = g + 1 < digits ? offsets[g + 1] : (int32_t)count;
+        ranges[2 * g] = start;
+        ranges[2 * g + 1] = end;
+        q = (end - start + kChunk - 1) / kChunk;
+    }
+    int32_t total;
+    const int32_t ex = block_exclusive_scan<kLayoutThreads>(q, s_wave, total);
+    if (g < groups) {
+        chunk_base[g] = ex;
+        s_base[g] = ex;
+    }
+    if (g == 0) {
+        chunk_base[groups] = total;
+        s_base[groups] = total;
+    }
+    __syncthreads();
+    // Wavefront w writes the chunk entries of groups w, w + 16, ...
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    for (int h = wave; h < groups; h += kLayoutThreads / 64) {
+        const int32_t end = s_base[h + 1];
+        for (int32_t u = s_base[h] + lane; u < end; u += 64) chunk_group[u] = h;
+    }
+}
+
 // Stable keys-only sort of keys[0:count) on bits [0, end_bit), end_bit <=
 // kOnePassBits, in one 10-bit pass: the result is written to
 // keys[count:2count) and ranges[2d], ranges[2d + 1] (d < ranges_count)
-// receive the run of key value d.  Scratch as sort_scratch_bytes(count, ...,
-// kOnePassBits).
+// receive the run of key value d.  With chunk_base, the group layout of
+// group_layout_kernel is written too (ranges_count groups, at most 1024).
+// Scratch as sort_scratch_bytes(count, ..., kOnePassBits).
 constexpr int kOnePassBits = 10;
 
 template <class K>
 int run_sort_once(K* keys, int64_t count, int end_bit, void* scratch, int ranges_count, int32_t* ranges,
-                  hipStream_t s) {
+                  hipStream_t s, int32_t* chunk_base = nullptr, int32_t* chunk_group = nullptr) {
     constexpr int RB = kOnePassBits;
     SortScratch sc;
     sort_scratch_bytes(count, &sc, scratch, RB);
@@ -916,8 +961,12 @@ int run_sort_once(K* keys, int64_t count, int end_bit, void* scratch, int ranges
     hipLaunchKernelGGL((sort_scatter_kernel<K, int32_t, false, RB>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
                        keys, (const int32_t*)nullptr, keys + count, (int32_t*)nullptr, count, 0, mask, end_bit,
                        sc.offsets, tiles, digits, OrderTail{}, Culled{});
-    hipLaunchKernelGGL(digit_ranges_kernel, dim3((unsigned)((ranges_count + 255) / 256)), dim3(256), 0, s,
-                       sc.offsets, count, digits, ranges_count, ranges);
+    if (chunk_base)
+        hipLaunchKernelGGL(group_layout_kernel, dim3(1), dim3(kLayoutThreads), 0, s, sc.offsets, count, digits,
+                           ranges_count, ranges, chunk_base, chunk_group);
+    else
+        hipLaunchKernelGGL(digit_ranges_kernel, dim3((unsigned)((ranges_count + 255) / 256)), dim3(256), 0, s,
+                           sc.offsets, count, digits, ranges_count, ranges);
     return launch_status("one-pass radix sort");
 }
 
@@ -968,8 +1017,6 @@ __global__ void tile_ranges_kernel(const K* __restrict__ keys, int64_t count, in
 constexpr int kGroupShift = 3;  // groups of 8x8 tiles: one wavefront lane per tile
 constexpr int kGroupBits = 20;  // group id field (low bits) of an item
 constexpr uint32_t kGroupMask = (1u << kGroupBits) - 1u;
-constexpr int kChunkSteps = 8;  // items per lane of a chunk (4 and 16 measured slower)
-constexpr int kChunk = 64 * kChunkSteps;  // items ranked by one wavefront
 constexpr int kBinThreads = 256;
 constexpr int kBinWaves = kBinThreads / 64;
 
@@ -1946,12 +1993,9 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     }
 }
 
-// Pairs of every global tile: sum over its group's chunks.
-__global__ void tile_totals_kernel(const int32_t* __restrict__ chunk_base, const uint32_t* __restrict__ counts,
-                                   const int32_t* __restrict__ scanned, GridDims d, int64_t tiles,
-                                   int32_t* __restrict__ totals) {
-    const int64_t tile = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (tile >= tiles) return;
+// Pairs of global tile `tile`: the sum over its group's chunks.
+GS3D_DEV int32_t tile_total(const int32_t* __restrict__ chunk_base, const uint32_t* __restrict__ counts,
+                            const int32_t* __restrict__ scanned, const GridDims& d, int64_t tile) {
     const int view = (int)(tile / d.tpv);
     const int r = (int)(tile - (int64_t)view * d.tpv);
     const int ty = r / d.gx, tx = r - ty * d.gx;
@@ -1959,13 +2003,18 @@ __global__ void tile_totals_kernel(const int32_t* __restrict__ chunk_base, const
     const int t = ((ty & 7) << 3) + (tx & 7);
     const int32_t cb = chunk_base[g];
     const int32_t q = chunk_base[g + 1] - cb;
-    int32_t total = 0;
-    if (q > 0) {
-        const int64_t first = (int64_t)cb * 64 + (int64_t)t * q;
-        const int64_t last = first + q - 1;
-        total = scanned[last] + (int32_t)counts[last] - scanned[first];
-    }
-    totals[tile] = total;
+    if (q <= 0) return 0;
+    const int64_t first = (int64_t)cb * 64 + (int64_t)t * q;
+    const int64_t last = first + q - 1;
+    return scanned[last] + (int32_t)counts[last] - scanned[first];
+}
+
+__global__ void tile_totals_kernel(const int32_t* __restrict__ chunk_base, const uint32_t* __restrict__ counts,
+                                   const int32_t* __restrict__ scanned, GridDims d, int64_t tiles,
+                                   int32_t* __restrict__ totals) {
+    const int64_t tile = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tile >= tiles) return;
+    totals[tile] = tile_total(chunk_base, counts, scanned, d, tile);
 }
 
 __global__ void tile_ranges_from_totals_kernel(const int32_t* __restrict__ totals, const int32_t* __restrict__ starts,
@@ -2432,8 +2481,10 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
     } else {
         if (!emitted) gs3d::emit_group_items(a, d, S, sc.items, s);
         if (group_bits <= gs3d::kOnePassBits) {
-            // One 10-bit pass; its digit scan gives the group ranges.
-            status = gs3d::run_sort_once<uint64_t>(sc.items, S, group_bits, sc.sort, (int)groups, sc.granges, s);
+            // One 10-bit pass; its digit scan gives the group ranges, and the
+            // chunk layout follows in the same workgroup.
+            status = gs3d::run_sort_once<uint64_t>(sc.items, S, group_bits, sc.sort, (int)groups, sc.granges, s,
+                                                   sc.chunk_base, sc.chunk_group);
             items = sc.items + S;
         } else {
             status = gs3d::run_sort<uint64_t, int32_t>(sc.items, nullptr, S, group_bits, sc.sort, s);
@@ -2444,10 +2495,11 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
         gs3d::fill_u32(reinterpret_cast<uint32_t*>(sc.granges), 2 * groups, 0u, s);
         hipLaunchKernelGGL(gs3d::tile_ranges_kernel<uint64_t>, dim3(gs3d::blocks_for(S, 256)), dim3(256), 0, s, items,
                            S, 0, gs3d::kGroupMask, sc.granges, groups);
+        hipLaunchKernelGGL(gs3d::chunk_base_kernel, dim3(1), dim3(1024), 0, s, sc.granges, (int)groups,
+                           sc.chunk_base);
+        hipLaunchKernelGGL(gs3d::chunk_group_kernel, dim3(gs3d::blocks_for(chunks, 256)), dim3(256), 0, s,
+                           sc.chunk_base, (int)groups, chunks, sc.chunk_group);
     }
-    hipLaunchKernelGGL(gs3d::chunk_base_kernel, dim3(1), dim3(1024), 0, s, sc.granges, (int)groups, sc.chunk_base);
-    hipLaunchKernelGGL(gs3d::chunk_group_kernel, dim3(gs3d::blocks_for(chunks, 256)), dim3(256), 0, s,
-                       sc.chunk_base, (int)groups, chunks, sc.chunk_group);
     // The count pass writes every entry of the 64 * chunks table (zeros for
     // chunks beyond the groups' own).
     const dim3 pass_grid(gs3d::blocks_for(chunks, gs3d::kBinWaves));
@@ -2465,6 +2517,9 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
                            (const int32_t*)nullptr, (unsigned long long*)nullptr);
     status = gs3d::run_scan<uint32_t, false>(sc.counts, 64 * chunks, sc.scanned, nullptr, sc.scan, s);
     if (status != GS3D_OK) return status;
+    // (One workgroup computing totals, starts and ranges of up to 16K tiles
+    // took 23-44 us against ~10 us for these three launches: each tile's
+    // total is a chain of dependent loads.)
     hipLaunchKernelGGL(gs3d::tile_totals_kernel, dim3(gs3d::blocks_for(tiles, 256)), dim3(256), 0, s, sc.chunk_base,
                        sc.counts, sc.scanned, d, tiles, sc.totals);
     status = gs3d::run_scan<int32_t, false>(sc.totals, tiles, sc.starts, nullptr, sc.scan, s);
