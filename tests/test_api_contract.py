@@ -229,3 +229,24 @@ def test_capped_list_stop_cache_keeps_recent_cameras(monkeypatch):
     finally:
         tile_lists.clear()
     assert tile_lists._BYTES == 0 and not tile_lists._STOPS
+
+
+def test_capped_list_lengths_and_gate(monkeypatch):
+    # capped_lengths keeps min(L, stop + stop/4 + 128) entries per tile (the
+    # whole list for stop -1), the cap the id-write pass and the blend use;
+    # frames below MIN_PAIRS tile pairs write whole lists.
+    from dsl_splat_amd.gs3d import lists as tile_lists
+
+    stops = torch.tensor([-1, 0, 7, 100, 4000, 4000], dtype=torch.int32)
+    lengths = torch.tensor([50, 1000, 100, 10, 6000, 4999], dtype=torch.int32)
+    want = [50, 128, 100, 10, 5128, 4999]
+    assert tile_lists.capped_lengths(stops, lengths).tolist() == want
+    # stop + stop/4 + 128 for the largest stop a list of 2^31 - 1 entries can report stays exact in int64
+    big = torch.tensor([2**31 - 2], dtype=torch.int32)
+    assert tile_lists.capped_lengths(big, torch.tensor([2**31 - 1], dtype=torch.int32)).tolist() == [2**31 - 1]
+    monkeypatch.setattr(tile_lists, "ENABLED", True)
+    assert tile_lists.applies(tile_lists.MIN_PAIRS, 1000)
+    assert not tile_lists.applies(tile_lists.MIN_PAIRS - 1, 1000)
+    assert not tile_lists.applies(tile_lists.MIN_PAIRS, 0)
+    monkeypatch.setattr(tile_lists, "ENABLED", False)
+    assert not tile_lists.applies(tile_lists.MIN_PAIRS, 1000)
