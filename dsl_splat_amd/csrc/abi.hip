@@ -21,6 +21,6 @@ int launch_status(const char* where) {
 
 }  // namespace gs3d
 
-extern "C" int gs3d_abi_version(void) { return 9; }
+extern "C" int gs3d_abi_version(void) { return 10; }
 
 extern "C" const char* gs3d_last_error(void) { return gs3d::g_last_error; }

@@ -1716,7 +1716,10 @@ __global__ __launch_bounds__(kBinThreads) void group_pass_kernel(
     uint32_t* __restrict__ counts, const int32_t* __restrict__ scanned, const int32_t* __restrict__ tile_start,
     int32_t* __restrict__ ids, int64_t id_limit, const int32_t* __restrict__ caps, const int32_t* __restrict__ redo,
     const int32_t* __restrict__ redo_count, const int32_t* __restrict__ totals,
-    unsigned long long* __restrict__ loaded) {
+    unsigned long long* __restrict__ loaded, int32_t* __restrict__ clear_count) {
+    // A capped pass clears the overflow count of the blend that follows.
+    if constexpr (LISTS == 1)
+        if (clear_count && blockIdx.x == 0 && threadIdx.x == 0) *clear_count = 0;
     static_assert(LISTS == 0 || WRITE, "caps and redo flags are write-pass arguments");
     // A chunk's run for one tile, then one slot per lane that rejected items
     // are written to (so the writes need neither a branch nor an exec mask).
@@ -2450,6 +2453,7 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
     hipStream_t s = gs3d::as_stream(stream);
     if (a.group_pairs == 0 || a.tile_pairs == 0 || rows == 0) {
         gs3d::fill_u32(reinterpret_cast<uint32_t*>(a.ranges), 2 * tiles, 0u, s);
+        if (a.caps && a.redo_list) gs3d::fill_u32(reinterpret_cast<uint32_t*>(a.redo_list), 1, 0u, s);
         return gs3d::launch_status("gs3d_bin_rows");
     }
     if (!a.centers || !a.radii || !a.order || !a.group_offsets || !a.ids || !scratch) return GS3D_ERR_ARGUMENT;
@@ -2508,13 +2512,13 @@ int bin_rows(const gs3d_bin_args* args, void* scratch, size_t scratch_bytes, voi
                            sc.masks, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d, sc.counts,
                            (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0,
                            (const int32_t*)nullptr, (const int32_t*)nullptr, (const int32_t*)nullptr,
-                           (const int32_t*)nullptr, (unsigned long long*)nullptr);
+                           (const int32_t*)nullptr, (unsigned long long*)nullptr, (int32_t*)nullptr);
     else
         hipLaunchKernelGGL((gs3d::group_pass_kernel<false, false>), pass_grid, dim3(gs3d::kBinThreads), 0, s, items,
                            (const uint64_t*)nullptr, sc.granges, sc.chunk_base, sc.chunk_group, (int)groups, chunks, d,
                            sc.counts, (const int32_t*)nullptr, (const int32_t*)nullptr, (int32_t*)nullptr, (int64_t)0,
                            (const int32_t*)nullptr, (const int32_t*)nullptr, (const int32_t*)nullptr,
-                           (const int32_t*)nullptr, (unsigned long long*)nullptr);
+                           (const int32_t*)nullptr, (unsigned long long*)nullptr, (int32_t*)nullptr);
     status = gs3d::run_scan<uint32_t, false>(sc.counts, 64 * chunks, sc.scanned, nullptr, sc.scan, s);
     if (status != GS3D_OK) return status;
     // (One workgroup computing totals, starts and ranges of up to 16K tiles
@@ -2549,7 +2553,7 @@ void launch_write_pass(const gs3d_bin_args& a, const BinScratch& sc, const uint6
     hipLaunchKernelGGL((group_pass_kernel<true, M, B, LISTS>), pass_grid, dim3(kBinThreads), 0, s, items,          \
                        M ? (const uint64_t*)sc.masks : nullptr, sc.granges, sc.chunk_base, sc.chunk_group,        \
                        (int)groups, chunks, d, sc.counts, sc.scanned, sc.starts, a.ids, a.tile_pairs, caps, redo, \
-                       redo_count, sc.totals, loaded)
+                       redo_count, sc.totals, loaded, LISTS == 1 ? a.redo_list : nullptr)
     if (accu) {
         if (buf)
             GS3D_WRITE_PASS(true, true);

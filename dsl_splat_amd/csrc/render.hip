@@ -688,7 +688,12 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
                 if (LISTS == 1 && a.redo) {
                     const bool redo = capped && stop < 0;
                     a.redo[t.tile] = redo ? 1 : 0;
-                    if (redo) a.redo_list[1 + atomicAdd(a.redo_list, 1)] = t.tile;
+                    if (redo) {
+                        // The list holds one slot per tile (a count left
+                        // uncleared cannot send the store out of it).
+                        const int slot = atomicAdd(a.redo_list, 1);
+                        if ((unsigned)slot < (unsigned)gridDim.x) a.redo_list[1 + slot] = t.tile;
+                    }
                 }
                 if (a.stop_out) a.stop_out[t.tile] = stop;
             }
@@ -736,10 +741,14 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
     };
     if constexpr (LISTS == 2) {
         // redo_list[0] tiles from redo_list[1], over a grid smaller than the
-        // frame's; the next tile reuses the staging LDS.
-        const int items = a.redo_list[0];
+        // frame's; the next tile reuses the staging LDS.  Counts and tile
+        // indices beyond the frame's tiles are ignored.
+        const int tiles = a.views * ((a.width + kTile - 1) / kTile) * ((a.height + kTile - 1) / kTile);
+        const int items = min(a.redo_list[0], tiles);
         for (int item = blockIdx.x; item < items; item += gridDim.x) {
-            blend(tile_info(a, a.redo_list[1 + item]));
+            const int tile = a.redo_list[1 + item];
+            if ((unsigned)tile >= (unsigned)tiles) continue;  // uniform: one value per workgroup
+            blend(tile_info(a, tile));
             __syncthreads();
         }
     } else {

@@ -167,7 +167,8 @@ def _prepare_frame(means, quats, scales, opacities, viewmats, Ks, width, height,
             lists = tile_lists.plan(status.device, width, height, tile_mode, host[3:3 + cameras].tolist(), count,
                                     launch.ranges.shape[0] // max(cameras, 1), slot=slot)
         caps = lists.caps if lists is not None else None
-        ranges, ids = launch_bin_rows(launch, group_pairs, count, early, caps=caps)
+        ranges, ids = launch_bin_rows(launch, group_pairs, count, early, caps=caps,
+                                      redo_list=lists.redo_list if caps is not None else None)
         if caps is not None:
             lists.launch = launch
         bins = [ViewBins(0, cameras, ranges, ids)]

@@ -61,8 +61,8 @@ class CappedLists:
     camera of the frame was seen before (whole lists; the stops are still
     measured).  stops: (views, tiles) int32 that the blend fills.  With
     caps, redo: (views*tiles) int32 overflow flags, and redo_list:
-    (1 + views*tiles) int32, the count of flagged tiles (zeroed here) and
-    the tiles.  launch: the binning launch that gs3d_bin_redo repeats for
+    (1 + views*tiles) int32, the count of flagged tiles (zeroed by the
+    capped binning it is given to) and the tiles.  launch: the binning launch that gs3d_bin_redo repeats for
     the flagged tiles."""
 
     keys: list
@@ -125,9 +125,10 @@ def plan(device: torch.device, width: int, height: int, tile_mode: str, keys: li
             rows.append(row)
     count = views * tiles_per_view
     caps = None
-    if all(r is not None for r in rows) and all(r[0] is rows[0][0] and r[1] == i for i, r in enumerate(rows)) \
-            and rows[0][0].shape[0] == views:
-        caps = rows[0][0].view(-1)  # the same cameras in the same order as their last frame
+    first = rows[0]
+    if first is not None and first[0].shape[0] == views and all(
+            r is not None and r[0] is first[0] and r[1] == i for i, r in enumerate(rows)):
+        caps = first[0].view(-1)  # the same cameras in the same order as their last frame
     elif any(r is not None for r in rows):
         # One gather launch; cameras without stops read whole lists (-1).
         whole = torch.full((tiles_per_view,), -1, dtype=torch.int32, device=device) if None in rows else None
@@ -135,12 +136,11 @@ def plan(device: torch.device, width: int, height: int, tile_mode: str, keys: li
     if caps is None:
         return CappedLists(list(keys), shape, stream, None,
                            torch.empty((views, tiles_per_view), dtype=torch.int32, device=device))
-    # stops | redo flags | count of flagged tiles, flagged tiles
+    # stops | redo flags | count of flagged tiles (cleared by the capped
+    # id-write pass, gs3d_bin_args.redo_list), flagged tiles
     buffer = torch.empty(3 * count + 1, dtype=torch.int32, device=device)
-    redo_list = buffer[2 * count:]
-    redo_list[:1].zero_()
     return CappedLists(list(keys), shape, stream, caps, buffer[:count].view(views, tiles_per_view),
-                       buffer[count:2 * count], redo_list)
+                       buffer[count:2 * count], buffer[2 * count:])
 
 
 def remember(lists: CappedLists) -> None:

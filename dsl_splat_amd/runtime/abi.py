@@ -9,7 +9,7 @@ import ctypes
 c_float_p = ctypes.POINTER(ctypes.c_float)
 c_int32_p = ctypes.POINTER(ctypes.c_int32)
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # Tile modes (GS3D_TILE_*), named as the reference's TileMode literals.
 TILE_MODES = {"radius": 0, "snugbox": 1, "accutile": 2}
@@ -163,6 +163,7 @@ class BinArgs(ctypes.Structure):
         ("tile_mode", ctypes.c_int32),
         ("footprints", _P),
         ("caps", _P),
+        ("redo_list", _P),
     ]
 
 

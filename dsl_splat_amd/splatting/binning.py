@@ -301,12 +301,14 @@ def _remember_capacity(launch: BinLaunch, group_pairs: int) -> None:
 
 @native.no_grad
 def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int,
-                    early: EarlyItems | None = None, caps: Tensor | None = None) -> tuple[Tensor, Tensor]:
+                    early: EarlyItems | None = None, caps: Tensor | None = None,
+                    redo_list: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """Ranges (views*tiles, 2) and the tile-ordered Gaussian ids (tile_pairs);
     ``early`` (from emit_early) is used when its capacity holds every item.
     With ``caps`` (views*tiles int32, see gs3d_bin_args.caps) each tile's
-    list is written only up to its cap, and the launch keeps the binning
-    scratch for redo_bin_rows."""
+    list is written only up to its cap, the first entry of ``redo_list`` (the
+    overflow count of the blend that follows) is zeroed, and the launch keeps
+    the binning scratch for redo_bin_rows."""
     check_pair_counts(group_pairs, tile_pairs)
     a, device = launch.args, launch.ranges.device
     ids = torch.empty(tile_pairs, dtype=torch.int32, device=device)
@@ -317,6 +319,7 @@ def launch_bin_rows(launch: BinLaunch, group_pairs: int, tile_pairs: int,
             raise ValueError("caps must be a contiguous int32 tensor with one entry per tile")
         launch.caps = caps
         a.caps = native.ptr(caps)
+        a.redo_list = native.ptr(redo_list)
     if early is not None and group_pairs <= early.capacity:
         native.call("gs3d_bin_emitted_rows", ctypes.byref(a), native.ptr(early.scratch), early.scratch.numel(),
                     native.stream(device))

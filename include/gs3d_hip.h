@@ -340,6 +340,10 @@ typedef struct gs3d_bin_args {
      * the same caps reads no further and flags the tiles that needed more,
      * whose whole lists gs3d_bin_redo then writes.  NULL: whole lists. */
     const int32_t* caps;
+    /* Optional, with caps: redo_list[0] is set to zero by the id-write pass
+     * -- the count that the capped blend then fills (gs3d_render_args.
+     * redo_list), so the caller needs no clearing of its own. */
+    int32_t* redo_list;
 } gs3d_bin_args;
 
 size_t gs3d_bin_rows_scratch_bytes(int64_t group_pairs, int32_t views, int32_t width, int32_t height,
@@ -440,7 +444,8 @@ typedef struct gs3d_render_args {
      * (views*tiles int32) receives 1 for the tiles that still had live
      * pixels there while their lists are longer (their outputs are then
      * incomplete), 0 for the others, and redo_list (1 + views*tiles int32,
-     * redo_list[0] zero before the launch) receives their count in [0] and
+     * redo_list[0] zero before the launch, e.g. by gs3d_bin_rows given the
+     * same redo_list) receives their count in [0] and
      * the tiles from [1], in no particular order.  stop_out (views*tiles
      * int32) receives, per tile, the list entries read before every pixel
      * terminated (-1: the whole list did not suffice), the caps of a later

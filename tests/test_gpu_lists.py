@@ -161,8 +161,10 @@ def test_capped_write_pass_writes_each_tile_prefix(key, monkeypatch):
             binning._CAPACITY.pop(shape, None)
         assert got_early is not None
     caps = torch.from_numpy(stops).to(DEV)
-    ranges, ids = binning.launch_bin_rows(launch, S, M, got_early, caps=caps)
+    redo_list = torch.full((tiles + 1,), 77, dtype=torch.int32, device=DEV)
+    ranges, ids = binning.launch_bin_rows(launch, S, M, got_early, caps=caps, redo_list=redo_list)
     assert launch.scratch is not None
+    assert int(redo_list[0]) == 0 and bool((redo_list[1:] == 77).all())  # the count only
     np.testing.assert_array_equal(_np(ranges), _np(ref_ranges))
     tile_of = np.repeat(np.arange(tiles), lengths)
     pos = np.arange(M) - np.repeat(ranges_np[:, 0], lengths)
