@@ -16,10 +16,9 @@ whole lists whatever the caps were; a stale cap costs only the redo.
 
 The first frame of a camera writes whole lists (no stops known), and so do
 frames with statistics, frames binned per camera group and frames of fewer
-than MIN_PAIRS tile pairs: a capped frame launches three more kernels (the
-count's clearing, gs3d_bin_redo, the redo blend; ~13 us on MI355X when no
-tile overflows) and does ~20 us more host work, which only a long id-write
-pass repays (measured per step: 20.8M-pair frames lose 30-50 us, frames of
+than MIN_PAIRS tile pairs: a capped frame launches two more kernels
+(gs3d_bin_redo and the redo blend; ~9 us on MI355X when no tile overflows)
+and does ~15 us more host work, which only a long id-write pass repays (measured per step: 20.8M-pair frames lose 30-50 us, frames of
 93M-171M pairs gain 100-170 us in every tile mode).  GS3D_LIST_CAPS=0 turns
 the caps off.
 """
