@@ -13,7 +13,7 @@ reference's Warp kernel modules (``gs3d/frame.py``, ``*/math.py``,
 ``*/metadata.py``, ``*/camera_kernels.py``, ``splatting/intersections.py``,
 ``runtime/dispatch.py``) have no Python counterpart: the HIP library does
 their work behind the same entry points.  The reference's other methods (its
-root exports, aaa, geer, pgsr, rade, strategy) are not part of this build.
+root exports, aaa, geer, pgsr, rade, strategy) are not part of dsl_splat_amd.
 """
 
 import importlib

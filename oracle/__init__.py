@@ -1,7 +1,7 @@
 """NumPy front end of the CPU oracle (liboracle_gs3d.so).
 
 TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg, always as the checker.  The product package
+bench.py's cpu_baseline leg, always to test results.  The product package
 dsl_splat_amd never imports this module.
 
 Each function takes NumPy arrays (converted to contiguous float32/int32),

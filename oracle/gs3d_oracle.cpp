@@ -1,5 +1,5 @@
 // gs3d_oracle.cpp — CPU restatement of the original-3DGS (gs3d) path of
-// YukiNagato/dsl_splat, used ONLY as the checker for the HIP kernels.
+// YukiNagato/dsl_splat, used ONLY to test the HIP kernels' results.
 //
 // TEST INFRASTRUCTURE.  Only tests/, __graft_entry__.smoke() and bench.py's
 // cpu_baseline leg load this library.  The product (dsl_splat_amd) never

@@ -1,4 +1,4 @@
-"""The reference's import path (dsl_splat.gs3d ...) resolves to this build's
+"""The reference's import path (dsl_splat.gs3d ...) resolves to dsl_splat_amd's
 modules when dsl_splat_amd/compat is on sys.path (checked in a fresh
 interpreter, so nothing here is imported from the test process)."""
 
