@@ -434,3 +434,32 @@ def test_batch_items_sharing_cameras_keep_their_own_stops(monkeypatch):
         assert torch.equal(got.features, want.features) and torch.equal(got.alpha, want.alpha)
     finally:
         tile_lists.clear()
+
+
+def test_capped_lists_on_empty_and_partly_empty_frames(monkeypatch):
+    # With caps on for every frame size: a frame whose Gaussians are all
+    # behind the cameras (no tile pairs), then one where only one camera sees
+    # any, each rendered twice (the second time with the first's stops), equal
+    # the same frames rendered with whole lists.
+    scene = _dense("sh3_1080p_4view", 20000, 160, 96, 49, **DENSE)
+    monkeypatch.setattr(tile_lists, "MIN_PAIRS", 0)
+    hidden = scene.means.clone()
+    hidden[:, 2] = -1000.0
+    views = scene.viewmats.clone()
+    views[1:, :3, 3] += torch.tensor([0.0, 0.0, 1000.0], device=DEV)  # cameras 1-3 far beyond everything
+    cases = {"all culled": (hidden, scene.viewmats), "three cameras empty": (scene.means, views)}
+    tile_lists.clear()
+    try:
+        for name, (means, vm) in cases.items():
+            _say(f"capped lists, {name}")
+            run = lambda: gs3d.rasterize(means, scene.quats, scene.scales, scene.opacities, vm, scene.Ks,  # noqa
+                                         scene.width, scene.height, sh_coeffs=scene.sh_coeffs, sh_degree=3)
+            monkeypatch.setattr(tile_lists, "ENABLED", False)
+            want = run()
+            monkeypatch.setattr(tile_lists, "ENABLED", True)
+            for _ in range(2):
+                got = run()
+                assert torch.equal(got.features, want.features) and torch.equal(got.alpha, want.alpha)
+            torch.cuda.synchronize()
+    finally:
+        tile_lists.clear()
