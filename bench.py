@@ -497,6 +497,16 @@ def run_workload(workload, n, device, steps, warmup, cpu, tile_mode="radius", mi
     clean = time_steps(forward, backward, steps, warmup)
     staged = time_steps(forward, backward, steps, 1, stage_events=True)
     info, frame = frame_info(scene)
+    if info["capped"]:
+        # The same steps writing whole lists: what a camera's first frame
+        # costs, and the step without capped lists.
+        from dsl_splat_amd.gs3d import lists as tile_lists
+
+        enabled, tile_lists.ENABLED = tile_lists.ENABLED, False
+        try:
+            info["capped"]["ms_whole_lists"] = round(time_steps(forward, backward, steps, 1)["ms"], 3)
+        finally:
+            tile_lists.ENABLED = enabled
     by = stage_bytes(scene, info)
     stages = stage_report(staged["stages"], by, info)
     hbm = [k for k in ("project", "order", "bin") if k in stages]
