@@ -581,47 +581,163 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
 // stable LSD pass places the keys, so its flat exclusive scan gives every
 // tile's offset for every digit), written by histogram blocks of several
 // consecutive tiles (runs of words instead of one scattered word per digit).
-// The scanned table is transposed to [tile][digit] so that each scatter
-// block reads its offsets as one contiguous row.
+// The scan is written transposed, [tile][digit], so that each scatter block
+// reads its offsets as one contiguous row.
 struct SortScratch {
     uint32_t* counts;     // [R][tiles]
-    int32_t* scanned;     // [R][tiles]
-    int32_t* offsets;     // [tiles][R], the transpose of scanned
-    void* scan_scratch;   // scan partials for R*tiles entries
+    int32_t* offsets;     // [tiles][R], the exclusive scan of counts in digit-major order
+    int32_t* scan;        // the digit scan's segment prefixes [R][segments] and row totals [R]
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+constexpr int kSegTiles = 128;  // tiles per segment of the digit scan
+
 inline size_t sort_scratch_bytes(int64_t count, SortScratch* out, void* base, int radix_bits = 8) {
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
-    const int64_t entries = tiles << radix_bits;
-    const size_t a = align256((size_t)entries * 4);
-    const size_t c = scan_partials_bytes(entries);
+    const int64_t segs = (tiles + kSegTiles - 1) / kSegTiles;
+    const size_t a = align256((size_t)(tiles << radix_bits) * 4);
+    const size_t b = align256((size_t)((segs + 1) << radix_bits) * 4);
     if (out) {
         char* p = reinterpret_cast<char*>(base);
         out->counts = reinterpret_cast<uint32_t*>(p);
-        out->scanned = reinterpret_cast<int32_t*>(p + a);
-        out->offsets = reinterpret_cast<int32_t*>(p + 2 * a);
-        out->scan_scratch = p + 3 * a;
+        out->offsets = reinterpret_cast<int32_t*>(p + a);
+        out->scan = reinterpret_cast<int32_t*>(p + 2 * a);
     }
-    return 3 * a + c;
+    return 2 * a + b;
 }
 
-// offsets[t][d] = scanned[d][t] through 32x32 LDS tiles (coalesced both ways).
-__global__ __launch_bounds__(256) void transpose_offsets_kernel(const int32_t* __restrict__ scanned, int64_t tiles,
-                                                                int digits, int32_t* __restrict__ offsets) {
-    __shared__ int32_t s[32][33];
-    const int64_t t0 = (int64_t)blockIdx.x * 32;
-    const int d0 = blockIdx.y * 32;
-    const int x = threadIdx.x & 31, y = threadIdx.x >> 5;
-    for (int r = y; r < 32; r += 8) {
-        const int64_t t = t0 + x;
-        if (t < tiles) s[r][x] = scanned[(int64_t)(d0 + r) * tiles + t];
+// Digit scan of a sort pass in two launches.  The exclusive scan of the
+// digit-major count table counts[d][t] is written transposed, as the
+// offsets[t][d] the scatter reads (each tile's base for every digit):
+//   digit_rows_kernel: one workgroup per digit row adds up the row in
+//     segments of kSegTiles tiles and writes each segment's exclusive prefix
+//     within the row (seg_prefix[d][segment]) and the row's total;
+//   digit_offsets_kernel: one workgroup per kSegDigits digits x kSegTiles
+//     tiles scans its block in LDS from the totals of the rows above and the
+//     segment prefixes, and writes it transposed (128-byte rows).
+// No workgroup waits for another and the scanned table is never stored
+// digit-major.
+constexpr int kSegDigits = 32;
+constexpr int kRowThreads = 256;
+
+// Each wavefront owns ITEMS / 2 consecutive segments of a chunk of
+// kRowThreads * ITEMS tiles (every load a run of 64 words); a lane adds its
+// two words of a segment before the wave sum.  Small workgroups keep every
+// row of the table resident at once (up to 1024 rows), and ITEMS (chosen
+// from the row length) puts a whole row in one chunk up to 12288 tiles.
+template <int ITEMS>
+__global__ __launch_bounds__(kRowThreads) void digit_rows_kernel(const uint32_t* __restrict__ counts, int tiles,
+                                                                 int segs, int32_t* __restrict__ seg_prefix,
+                                                                 int32_t* __restrict__ row_totals) {
+    static_assert(ITEMS % 2 == 0, "two words of a segment per lane");
+    constexpr int kChunkTiles = kRowThreads * ITEMS;
+    constexpr int kChunkSegs = kChunkTiles / kSegTiles;
+    constexpr int kWaveSegs = ITEMS / 2;
+    __shared__ uint32_t s_seg[kChunkSegs];
+    const int d = blockIdx.x;
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    const uint32_t* row = counts + (int64_t)d * tiles;
+    int64_t carry = 0;  // wave 0: the row's sum before this chunk
+    for (int c0 = 0; c0 < tiles; c0 += kChunkTiles) {
+        const int w0 = c0 + wave * (ITEMS * 64) + lane;
+        uint32_t v[ITEMS];
+#pragma unroll
+        for (int m = 0; m < ITEMS; ++m) v[m] = row[min(w0 + m * 64, tiles - 1)];
+#pragma unroll
+        for (int m = 0; m < ITEMS; ++m)
+            if (w0 + m * 64 >= tiles) v[m] = 0;
+#pragma unroll
+        for (int s = 0; s < kWaveSegs; ++s) {
+            const uint32_t sum = wave_sum_u32_to_lane63(v[2 * s] + v[2 * s + 1]);
+            if (lane == 63) s_seg[wave * kWaveSegs + s] = sum;
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int g = 0; g < (kChunkSegs + 63) / 64; ++g) {
+                const int j = g * 64 + lane;
+                const uint32_t s = j < kChunkSegs ? s_seg[j] : 0u;
+                const uint32_t inc = wave_inclusive_scan(s);
+                const int seg = c0 / kSegTiles + j;
+                if (j < kChunkSegs && seg < segs)
+                    seg_prefix[(int64_t)d * segs + seg] = (int32_t)(carry + (int64_t)(inc - s));
+                carry += (int64_t)__shfl(inc, 63, 64);
+            }
+        }
+        __syncthreads();  // the next chunk reuses s_seg
+    }
+    if (threadIdx.x == 0) row_totals[d] = (int32_t)carry;
+}
+
+template <int ITEMS>
+void launch_digit_rows(int per_thread, int digits, const uint32_t* counts, int tiles, int segs, int32_t* seg_prefix,
+                       int32_t* row_totals, hipStream_t s) {
+    if constexpr (ITEMS < 48) {
+        if (per_thread > ITEMS)
+            return launch_digit_rows<ITEMS + 8>(per_thread, digits, counts, tiles, segs, seg_prefix, row_totals, s);
+    }
+    hipLaunchKernelGGL(digit_rows_kernel<ITEMS>, dim3((unsigned)digits), dim3(kRowThreads), 0, s, counts, tiles, segs,
+                       seg_prefix, row_totals);
+}
+
+// grid (segments, digits / kSegDigits); total_out (optional) receives the
+// sum of the table.
+__global__ __launch_bounds__(256) void digit_offsets_kernel(const uint32_t* __restrict__ counts, int64_t tiles,
+                                                            int digits, const int32_t* __restrict__ seg_prefix,
+                                                            const int32_t* __restrict__ row_totals,
+                                                            int32_t* __restrict__ offsets,
+                                                            int64_t* __restrict__ total_out) {
+    static_assert(kSegTiles == 128 && kSegDigits == 32, "the thread mapping below");
+    __shared__ int32_t s_block[kSegDigits][kSegTiles + 1];
+    __shared__ int32_t s_row[kSegDigits];
+    __shared__ int64_t s_wave[4];
+    const int64_t segs = gridDim.x, seg = blockIdx.x;
+    const int64_t t0 = seg * kSegTiles;
+    const int d0 = blockIdx.y * kSegDigits;
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    // Every load is issued before the first wait: the block's rows (lanes
+    // 0-31 of wave 0: total and segment prefix of row d0 + lane), its counts
+    // (entry k * 256 + thread is row 2k + thread / 128 of the block, column
+    // thread % 128) and the totals of the rows above it.
+    int64_t rt = 0;
+    int32_t sp = 0;
+    if (wave == 0 && lane < kSegDigits) {
+        rt = row_totals[d0 + lane];
+        sp = seg_prefix[(int64_t)(d0 + lane) * segs + seg];
+    }
+    const int col = threadIdx.x & (kSegTiles - 1), half = threadIdx.x >> 7;
+    const int64_t t = t0 + col;
+    uint32_t raw[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) raw[k] = counts[(int64_t)(d0 + 2 * k + half) * tiles + min(t, tiles - 1)];
+    int64_t above = 0;
+    for (int j = threadIdx.x; j < d0; j += 256) above += row_totals[j];
+    int64_t base;
+    block_exclusive_scan<256>(above, s_wave, base);
+    if (wave == 0) {
+        const int64_t inc = wave_inclusive_scan(rt);
+        if (lane < kSegDigits) s_row[lane] = (int32_t)(base + inc - rt + sp);
+        if (total_out && seg == 0 && blockIdx.y == gridDim.y - 1 && lane == kSegDigits - 1) *total_out = base + inc;
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) s_block[2 * k + half][col] = t < tiles ? (int32_t)raw[k] : 0;
+    __syncthreads();
+    // Each wavefront scans 8 rows, two consecutive entries per lane.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = wave * 8 + i;
+        const int32_t a = s_block[r][2 * lane], b = s_block[r][2 * lane + 1];
+        const int32_t ex = s_row[r] + wave_inclusive_scan(a + b) - (a + b);
+        s_block[r][2 * lane] = ex;
+        s_block[r][2 * lane + 1] = ex + a;
     }
     __syncthreads();
-    for (int r = y; r < 32; r += 8) {
-        const int64_t t = t0 + r;
-        if (t < tiles) offsets[t * digits + d0 + x] = s[x][r];
+    const int dd = threadIdx.x & (kSegDigits - 1);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int c = (threadIdx.x >> 5) + 8 * k;
+        if (t0 + c < tiles) offsets[(t0 + c) * digits + d0 + dd] = s_block[dd][c];
     }
 }
 
@@ -861,10 +977,15 @@ inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStre
                            tiles * digits, sc.offsets, total, (int32_t)tiles, (int32_t)digits);
         return launch_status("radix sort counts");
     }
-    const int status = run_scan<uint32_t, false>(sc.counts, tiles * digits, sc.scanned, total, sc.scan_scratch, s);
-    if (status != GS3D_OK) return status;
-    hipLaunchKernelGGL(transpose_offsets_kernel, dim3((unsigned)((tiles + 31) / 32), digits / 32), dim3(256), 0, s,
-                       sc.scanned, tiles, digits, sc.offsets);
+    const int64_t segs = (tiles + kSegTiles - 1) / kSegTiles;
+    int32_t* seg_prefix = sc.scan;
+    int32_t* row_totals = sc.scan + segs * digits;
+    // The fewest words a thread (a multiple of 8, at most 48) that cover a
+    // row in one chunk; longer rows loop over chunks of 48.
+    launch_digit_rows<8>((int)((tiles + kRowThreads - 1) / kRowThreads), digits, sc.counts, (int)tiles, (int)segs,
+                         seg_prefix, row_totals, s);
+    hipLaunchKernelGGL(digit_offsets_kernel, dim3((unsigned)segs, digits / kSegDigits), dim3(256), 0, s, sc.counts,
+                       tiles, digits, seg_prefix, row_totals, sc.offsets, total);
     return launch_status("radix sort counts");
 }
 

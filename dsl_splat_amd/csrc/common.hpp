@@ -152,6 +152,22 @@ GS3D_DEV float wave_sum_to_lane63(float v) {
     return v;
 }
 
+// The same wave sum of 32-bit integers (the radix sort's digit counts).
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+GS3D_DEV uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+
+GS3D_DEV uint32_t wave_sum_u32_to_lane63(uint32_t v) {
+    v += dpp_u<0xB1>(v);
+    v += dpp_u<0x4E>(v);
+    v += dpp_u<0x124>(v);
+    v += dpp_u<0x128>(v);
+    v += dpp_u<0x142, 0xA>(v);
+    v += dpp_u<0x143, 0xC>(v);
+    return v;
+}
+
 // Wave sum broadcast as a wave-uniform value.
 GS3D_DEV float wave_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(v)), 63));

@@ -248,7 +248,7 @@ int gs3d_sort_pairs_u64(uint64_t* keys, int32_t* values, int64_t count,
  * Same arguments and result as gs3d_sort_pairs_u64 without the scratch
  * buffer: the scratch is a static device array of GS3D_STATIC_SCRATCH_BYTES
  * per GPU (128 MiB, held until the process ends), so count is limited to
- * gs3d_sort_scratch_bytes(count) <= GS3D_STATIC_SCRATCH_BYTES (about 268M
+ * gs3d_sort_scratch_bytes(count) <= GS3D_STATIC_SCRATCH_BYTES (133,693,440
  * pairs); larger counts return GS3D_ERR_SCRATCH.  The stream must belong to
  * the current device.  The call allocates nothing, but every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (other streams or

@@ -144,6 +144,9 @@ def test_argument_errors_are_reported_without_launching():
     # touching a device (the pointers are never dereferenced).
     big = 300_000_000
     assert native.query("gs3d_sort_scratch_bytes", big) > abi.STATIC_SCRATCH_BYTES
+    # The documented limit of the static scratch.
+    assert native.query("gs3d_sort_scratch_bytes", 133_693_440) <= abi.STATIC_SCRATCH_BYTES
+    assert native.query("gs3d_sort_scratch_bytes", 133_693_441) > abi.STATIC_SCRATCH_BYTES
     assert lib.gs3d_sort_pairs_u64_static(ctypes.c_void_p(256), ctypes.c_void_p(256), big, 45,
                                           None) == abi.GS3D_ERR_SCRATCH
     assert b"GS3D_STATIC_SCRATCH_BYTES" in lib.gs3d_last_error()

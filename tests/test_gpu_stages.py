@@ -617,8 +617,12 @@ def test_rasterize_reuses_the_group_item_capacity():
 
 
 @pytest.mark.parametrize("count,end_bit", [(2, 13), (4097, 15), (1_000_003, 16), (5_000_000, 32), (3, 11),
-                                           (4097, 9), (1_000_003, 10), (70_001, 11), (2048, 11)])
+                                           (4097, 9), (1_000_003, 10), (70_001, 11), (2048, 11),
+                                           (14_000_000, 24), (30_000_000, 20)])
 def test_u32_radix_sort_stable(count, end_bit):
+    # The digit scan's row pass takes 8-48 words a thread by the number of
+    # 2048-key tiles per digit row: 1M keys 8, 5M 16, 14M 32, and 30M keys
+    # (14,649 tiles) two chunks of 48.
     _say(f"u32 sort count={count} end_bit={end_bit}")
     rng = np.random.default_rng(count + 1)
     keys = rng.integers(0, 1 << end_bit, size=count, dtype=np.uint64).astype(np.uint32)
