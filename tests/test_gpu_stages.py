@@ -34,14 +34,15 @@ def _say(*args):
     print(*args, flush=True)
 
 
-# Frames of fewer than 1024 tiles (all views) blend at one pixel per lane,
-# larger ones at two: the "wide" scenes cover the two-pixel kernels.
+# Frames of fewer than 4096 tiles (all views) blend at one pixel per lane,
+# larger ones at two: the "wide" scenes (4320 tiles) cover the two-pixel
+# kernels.
 SCENES = {
     "small_rgb": dict(name="small", n=4000, width=128, height=96, seed=1),
     "sh3_4view": dict(name="sh3_1080p_4view", n=6000, width=160, height=96, seed=2),
     "sh3_720p": dict(name="sh3_720p", n=5000, width=200, height=120, seed=3),
-    "wide_rgb": dict(name="small", n=16000, width=576, height=480, seed=11),
-    "wide_sh3_4view": dict(name="sh3_1080p_4view", n=12000, width=288, height=240, seed=12),
+    "wide_rgb": dict(name="small", n=16000, width=1152, height=960, seed=11),
+    "wide_sh3_4view": dict(name="sh3_1080p_4view", n=12000, width=576, height=480, seed=12),
 }
 
 
@@ -209,7 +210,7 @@ def test_render_forward_bit_exact(key, degree, extra, bg):
     assert ct.max() > 0
 
 
-@pytest.mark.parametrize("n,width,height", [(3000, 136, 100), (12000, 576, 480)])
+@pytest.mark.parametrize("n,width,height", [(3000, 136, 100), (12000, 1152, 960)])
 def test_render_culling_edge_cases(n, width, height):
     # Needle-shaped Gaussians at every orientation and opacities straddling
     # the 1/255 threshold: the per-wavefront strip culling must not change a
