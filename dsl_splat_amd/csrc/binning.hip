@@ -56,6 +56,36 @@ GS3D_DEV T block_exclusive_scan(T v, T* s_wave, T& total) {
     return before + inc - v;
 }
 
+// A sum of int64 values that a scan's first launch adds up beside its own
+// work (in one more workgroup, or in its single workgroup before the scan),
+// so that a sum too small to fill the GPU costs no launch of its own.
+struct SideSum {
+    const int64_t* values = nullptr;
+    int64_t count = 0;
+    int64_t* out = nullptr;
+};
+
+// *side.out = sum of side.values[0, count), by the whole block of B threads;
+// eight loads per thread in flight at a time.
+template <int B>
+GS3D_DEV void side_sum(const SideSum& side, int64_t* s_wave) {
+    constexpr int U = 8;
+    int64_t v = 0;
+    for (int64_t i0 = threadIdx.x; i0 < side.count; i0 += (int64_t)B * U) {
+        int64_t x[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + (int64_t)u * B;
+            x[u] = i < side.count ? side.values[i] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) v += x[u];
+    }
+    int64_t total;
+    block_exclusive_scan<B>(v, s_wave, total);
+    if (threadIdx.x == 0) *side.out = total;
+}
+
 // ---------------------------------------------------------------------------
 // Scan (reduce-then-scan over 4096-element tiles).
 // ---------------------------------------------------------------------------
@@ -65,7 +95,13 @@ constexpr int kReduceWaves = 4;
 template <class In>
 __global__ __launch_bounds__(64 * kReduceWaves) void scan_reduce_kernel(const In* __restrict__ in, int64_t n,
                                                                         int64_t tiles,
-                                                                        int64_t* __restrict__ partials) {
+                                                                        int64_t* __restrict__ partials,
+                                                                        SideSum side) {
+    if (side.values && blockIdx.x == gridDim.x - 1) {  // the extra workgroup
+        __shared__ int64_t s_wave[kReduceWaves];
+        side_sum<64 * kReduceWaves>(side, s_wave);
+        return;
+    }
     const int lane = lane_id();
     const int64_t tile = (int64_t)blockIdx.x * kReduceWaves + (threadIdx.x >> 6);
     if (tile >= tiles) return;
@@ -171,9 +207,10 @@ template <class In, bool INCLUSIVE>
 __global__ __launch_bounds__(kSingleThreads) void scan_single_kernel(const In* __restrict__ in, int64_t n,
                                                                      int32_t* __restrict__ out,
                                                                      int64_t* __restrict__ total_out, int32_t rows,
-                                                                     int32_t cols) {
+                                                                     int32_t cols, SideSum side) {
     __shared__ int64_t s_wave[kSingleThreads / 64];
     __shared__ int32_t s_tile[kSingleTile + kSingleTile / 16];
+    if (side.values) side_sum<kSingleThreads>(side, s_wave);
     const int count = (int)n;  // n <= kSingleScanMax
     int64_t carry = 0;
     for (int base = 0; base < count; base += kSingleTile) {
@@ -227,19 +264,22 @@ inline size_t scan_partials_bytes(int64_t n) {
     return (size_t)((tiles + 1) * sizeof(int64_t) + 255) & ~(size_t)255;
 }
 
-// Scratch layout: [tile totals (tiles int64)].
+// Scratch layout: [tile totals (tiles int64)].  side (optional): a sum the
+// first launch also computes.
 template <class In, bool INCLUSIVE>
-int run_scan(const In* in, int64_t n, int32_t* out, int64_t* total, void* scratch, hipStream_t stream) {
+int run_scan(const In* in, int64_t n, int32_t* out, int64_t* total, void* scratch, hipStream_t stream,
+             SideSum side = SideSum{}) {
     const int64_t tiles = (n + kScanTile - 1) / kScanTile;
-    if (tiles == 0) return GS3D_OK;  // callers handle empty inputs (total untouched)
+    if (tiles == 0 && !side.values) return GS3D_OK;  // callers handle empty inputs (total untouched)
     if (n <= kSingleScanMax) {
         hipLaunchKernelGGL((scan_single_kernel<In, INCLUSIVE>), dim3(1), dim3(kSingleThreads), 0, stream, in, n, out,
-                           total, 0, 0);
+                           n > 0 ? total : nullptr, 0, 0, side);
         return launch_status("scan");
     }
     int64_t* partials = reinterpret_cast<int64_t*>(scratch);
-    hipLaunchKernelGGL((scan_reduce_kernel<In>), dim3((unsigned)((tiles + kReduceWaves - 1) / kReduceWaves)),
-                       dim3(64 * kReduceWaves), 0, stream, in, n, tiles, partials);
+    const unsigned reduce_blocks = (unsigned)((tiles + kReduceWaves - 1) / kReduceWaves) + (side.values ? 1u : 0u);
+    hipLaunchKernelGGL((scan_reduce_kernel<In>), dim3(reduce_blocks), dim3(64 * kReduceWaves), 0, stream, in, n,
+                       tiles, partials, side);
     hipLaunchKernelGGL((scan_down_kernel<In, INCLUSIVE>), dim3((unsigned)tiles), dim3(kScanThreads), 0, stream, in, n,
                        partials, out, total);
     return launch_status("scan");
@@ -974,7 +1014,7 @@ inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStre
     if (tiles * digits <= kSingleScanMax) {
         // Small table: scanned and written transposed by one workgroup.
         hipLaunchKernelGGL((scan_single_kernel<uint32_t, false>), dim3(1), dim3(kSingleThreads), 0, s, sc.counts,
-                           tiles * digits, sc.offsets, total, (int32_t)tiles, (int32_t)digits);
+                           tiles * digits, sc.offsets, total, (int32_t)tiles, (int32_t)digits, SideSum{});
         return launch_status("radix sort counts");
     }
     const int64_t segs = (tiles + kSegTiles - 1) / kSegTiles;
@@ -1429,28 +1469,6 @@ __global__ __launch_bounds__(kBinThreads) void order_counts_kernel(const uint64_
     int64_t total;
     block_exclusive_scan<kBinThreads>(area, s_wave, total);
     if (threadIdx.x == 0) block_pairs[blockIdx.x] = total;
-}
-
-// *out = sum of values[0, count) (one block).  Eight loads per thread are in
-// flight at a time: the kernel is latency-bound (tens of thousands of values).
-__global__ __launch_bounds__(1024) void sum_i64_kernel(const int64_t* __restrict__ values, int64_t count,
-                                                       int64_t* __restrict__ out) {
-    __shared__ int64_t s_wave[1024 / 64];
-    constexpr int U = 8;
-    int64_t v = 0;
-    for (int64_t i0 = threadIdx.x; i0 < count; i0 += 1024 * U) {
-        int64_t x[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t i = i0 + (int64_t)u * 1024;
-            x[u] = i < count ? values[i] : 0;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) v += x[u];
-    }
-    int64_t total;
-    block_exclusive_scan<1024>(v, s_wave, total);
-    if (threadIdx.x == 0) *out = total;
 }
 
 // Base of the depth order's later passes (one block): the smallest kept key
@@ -2520,8 +2538,9 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
                                d.gx, d.gy, sc.counts, sc.pairs, (const int64_t*)sc.live);
         pair_blocks = cgrid.x;
     }
-    hipLaunchKernelGGL(gs3d::sum_i64_kernel, dim3(1), dim3(1024), 0, s, sc.pairs, pair_blocks, a.totals + 1);
-    status = gs3d::run_scan<int32_t, true>(sc.counts, rows, a.group_offsets, a.totals, sc.scan, s);
+    // The blocks' tile-pair sums are added up by the group-count scan's first launch.
+    status = gs3d::run_scan<int32_t, true>(sc.counts, rows, a.group_offsets, a.totals, sc.scan, s,
+                                           gs3d::SideSum{sc.pairs, pair_blocks, a.totals + 1});
     if (status != GS3D_OK) return status;
     return gs3d::launch_status("gs3d_order_rows");
 }
