@@ -43,6 +43,9 @@ SCENES = {
     "sh3_720p": dict(name="sh3_720p", n=5000, width=200, height=120, seed=3),
     "wide_rgb": dict(name="small", n=16000, width=1152, height=960, seed=11),
     "wide_sh3_4view": dict(name="sh3_1080p_4view", n=12000, width=576, height=480, seed=12),
+    # 4 tile groups and ~1.5M group items: the group sort's 32 digit rows
+    # over more than 512 sort tiles take the two-launch digit scan.
+    "dense_small": dict(name="small", n=1_500_000, width=256, height=256, seed=21),
 }
 
 
@@ -497,7 +500,8 @@ def test_projection_per_view_sh_parity(degree):
     check_gradient("camera_centers", _np(res["camera_centers"]), ref["camera_centers"], bound["camera_centers"])
 
 
-@pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3), ("sh3_720p", 0)])
+@pytest.mark.parametrize("key,degree", [("small_rgb", None), ("sh3_4view", 3), ("sh3_720p", 0),
+                                        ("dense_small", None)])
 def test_grouped_binning_matches_reference_order(key, degree):
     # The production binning (depth-ordered rows, 8x8-tile groups, ballot
     # ranking) must give exactly the reference's ids, ranges and 64-bit keys
@@ -518,6 +522,13 @@ def test_grouped_binning_matches_reference_order(key, degree):
     np.testing.assert_array_equal(_np(bins["point_list"]), sv)
     np.testing.assert_array_equal(_np(bins["point_list_keys"]).view(np.uint64), sk)
     np.testing.assert_array_equal(_np(bins["ranges"]), oracle.tile_ranges(sk, T))
+    if key == "dense_small":
+        # Group items = distinct (Gaussian, 8x8-tile group) of the pairs:
+        # more than 512 sort tiles of 2048 items.
+        gx = (scene.width + 15) // 16
+        tile = (sk >> np.uint64(32)).astype(np.int64)
+        group = (tile // gx >> 3) * 64 + (tile % gx >> 3)
+        assert np.unique(sv.astype(np.int64) * 4096 + group).size > 512 * 2048
 
 
 @pytest.mark.parametrize("views,n,W,H,spread", [
