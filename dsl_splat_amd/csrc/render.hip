@@ -1056,8 +1056,8 @@ __global__ __launch_bounds__(kTilePixels / PIX) __attribute__((amdgpu_waves_per_
 // at one pixel per lane: four wavefronts per tile instead of two, so that a
 // small frame still spreads over the SIMDs.  Each tile's list is walked
 // serially; at two pixels per lane a few thousand tiles make little more than
-// one round of wavefronts (6 per SIMD, 6144 on the chip), and the longest
-// lists set the time (500K Gaussians at 1280x720, 3600 tiles: a step 0.93 ->
+// one full set of resident wavefronts (6 per SIMD, 6144 on the chip), and the
+// longest lists set the time (500K Gaussians at 1280x720, 3600 tiles: a step 0.93 ->
 // 0.87 ms at one pixel per lane; 1920x1080, 8160 tiles: 1.31 -> 1.64 ms).
 #ifndef GS3D_SMALL_GRID
 #define GS3D_SMALL_GRID 4096
