@@ -470,15 +470,16 @@ struct Culled {
 };
 
 // VALS = false sorts keys alone: no value loads, stores or LDS staging, which
-// leaves room for one more block per CU.
-template <class K, class V, bool VALS, int RB = 8, int TAIL = 0, bool DROP = false>
+// leaves room for one more block per CU.  R: the digits the LDS counters hold
+// (every key's digit is below it; fewer than 1 << RB when the keys are known
+// to stay below R, which leaves more LDS for resident blocks).
+template <class K, class V, bool VALS, int RB = 8, int TAIL = 0, bool DROP = false, int R = 1 << RB>
 __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
     const K* __restrict__ keys_in, const V* __restrict__ vals_in, K* __restrict__ keys_out,
     V* __restrict__ vals_out, int64_t count, int shift, uint32_t mask, int bits,
     const int32_t* __restrict__ offsets, int64_t tiles, int digits, OrderTail tail, Culled cull) {
     static_assert(TAIL == 0 || (VALS && sizeof(V) == 8), "the order tail reads 64-bit records");
-    constexpr int R = 1 << RB;
-    static_assert(R % kSortThreads == 0, "whole digits per thread");
+    static_assert(R % kSortThreads == 0 && R <= (1 << RB), "whole digits per thread");
     __shared__ K s_keys[kSortTile];
     __shared__ V s_vals[VALS ? kSortTile : 1];
     __shared__ uint32_t s_wcnt[kSortThreads / 64][R];
@@ -782,8 +783,8 @@ __global__ __launch_bounds__(256) void digit_offsets_kernel(const uint32_t* __re
 }
 
 // Histogram and scan of one sort pass (digits of `bits` bits at `shift`;
-// every key's digit below `digits`, a multiple of 32 up to 1 << RB).
-template <class K, int RB, bool DROP = false>
+// every key's digit below `digits`, a multiple of 32 up to R).
+template <class K, int RB, bool DROP = false, int R = 1 << RB>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
                 hipStream_t s, const int64_t* live = nullptr, int64_t* total = nullptr,
                 const uint32_t* key_base = nullptr);
@@ -953,15 +954,17 @@ inline int run_order_sort(uint32_t* keys, uint64_t* values, int64_t count, void*
 // words instead of one scattered word per digit.  One LDS histogram per tile
 // (pitch R + 1: the transposed read is conflict-free).
 // DROP and live as in sort_scatter_kernel (tiles at or beyond live count
-// nothing, and their columns are written as zeros).
-template <class K, int RB, int TPB, bool DROP = false>
+// nothing, and their columns are written as zeros).  R as in
+// sort_scatter_kernel.
+template <class K, int RB, int TPB, bool DROP = false, int R = 1 << RB>
 __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(const K* __restrict__ keys, int64_t count,
                                                                             int shift, uint32_t mask,
                                                                             uint32_t* __restrict__ counts,
                                                                             int64_t tiles, int digits,
                                                                             const int64_t* __restrict__ live_count,
                                                                             const uint32_t* __restrict__ key_base) {
-    constexpr int R = 1 << RB, P = R + 1;
+    static_assert(R <= (1 << RB), "digits of RB bits");
+    constexpr int P = R + 1;
     const K base_key = key_base ? (K)*key_base : K(0);
     __shared__ uint32_t s_hist[TPB * P];
     for (int e = threadIdx.x; e < TPB * P; e += kSortThreads) s_hist[e] = 0;
@@ -1030,14 +1033,14 @@ inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStre
 }
 
 // total (optional) receives the number of keys counted.
-template <class K, int RB, bool DROP>
+template <class K, int RB, bool DROP, int R>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
                 hipStream_t s, const int64_t* live, int64_t* total, const uint32_t* key_base) {
     // Tiles per histogram block: runs of 16 words (whole 64-byte sectors) for
     // 8-bit digits; 8 for 10-bit digits, whose LDS histograms are 4x larger.
     constexpr int TPB = RB > 8 ? 8 : GS3D_HIST_TILES8;
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
-    hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB, DROP>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
+    hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB, DROP, R>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
                        dim3(kSortThreads), 0, s, keys, count, shift, mask, sc.counts, tiles, digits, live, key_base);
     return scan_counts(count, digits, sc, s, total);
 }
@@ -1117,11 +1120,20 @@ int run_sort_once(K* keys, int64_t count, int end_bit, void* scratch, int ranges
     // Only the digits of the key range are counted, scanned and transposed
     // (the keys are below ranges_count).
     const int digits = min(1 << RB, (ranges_count + 31) & ~31);
-    const int status = sort_counts<K, RB>(keys, count, 0, mask, digits, sc, s);
+    // Up to 768 key values the histogram and scatter keep 768 LDS counters
+    // per row instead of 1024 (the keys are below ranges_count <= digits).
+    auto sort_pass = [&](auto counters) -> int {
+        constexpr int R = decltype(counters)::value;
+        const int status = sort_counts<K, RB, false, R>(keys, count, 0, mask, digits, sc, s);
+        if (status != GS3D_OK) return status;
+        hipLaunchKernelGGL((sort_scatter_kernel<K, int32_t, false, RB, 0, false, R>), dim3((unsigned)tiles),
+                           dim3(kSortThreads), 0, s, keys, (const int32_t*)nullptr, keys + count, (int32_t*)nullptr,
+                           count, 0, mask, end_bit, sc.offsets, tiles, digits, OrderTail{}, Culled{});
+        return GS3D_OK;
+    };
+    const int status = digits <= 768 ? sort_pass(std::integral_constant<int, 768>{})
+                                     : sort_pass(std::integral_constant<int, 1 << RB>{});
     if (status != GS3D_OK) return status;
-    hipLaunchKernelGGL((sort_scatter_kernel<K, int32_t, false, RB>), dim3((unsigned)tiles), dim3(kSortThreads), 0, s,
-                       keys, (const int32_t*)nullptr, keys + count, (int32_t*)nullptr, count, 0, mask, end_bit,
-                       sc.offsets, tiles, digits, OrderTail{}, Culled{});
     if (chunk_base)
         hipLaunchKernelGGL(group_layout_kernel, dim3(1), dim3(kLayoutThreads), 0, s, sc.offsets, count, digits,
                            ranges_count, ranges, chunk_base, chunk_group);

@@ -535,6 +535,8 @@ def test_grouped_binning_matches_reference_order(key, degree):
     (2, 3000, 200, 120, 1.0),      # partial groups at the right/bottom edges, several chunks per group
     (1, 40000, 128, 128, 0.15),    # crowded corner: long group lists, many 512-item chunks
     (70, 400, 160, 160, 1.0),      # 280 groups: one 10-bit pass, ranges from its digit scan
+    (12, 200, 1024, 1024, 1.0),    # 768 groups: the most the group sort's 768-counter kernels take
+    (13, 200, 1024, 1024, 1.0),    # 832 groups: 1024 counters per digit row
     (16, 200, 1024, 1024, 1.0),    # 1024 groups: the largest one-pass group sort
     (41, 150, 640, 640, 1.0),      # 1025 groups: two 8-bit passes and a range search
     (130, 250, 400, 400, 1.0),     # 2080 groups: 12-bit group keys
