@@ -444,9 +444,10 @@ GS3D_DEV uint32_t digit_of(K key, int shift, uint32_t mask) { return (uint32_t)(
 // Outputs of the depth order's last pass (TAIL != 0): the group count of
 // every record at its sorted position and each block's tile-pair sum, taken
 // from the packed record (TAIL 1: tile rectangle, TAIL 2: AccuTile
-// tiles << 12 | groups).
+// tiles << 12 | groups).  The counts are 16-bit: a packed rectangle spans at
+// most 32 x 32 groups and an AccuTile record holds fewer than 4096.
 struct OrderTail {
-    int32_t* group_counts;
+    uint16_t* group_counts;
     int64_t* block_pairs;
 };
 template <int TAIL>
@@ -592,7 +593,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
                 int32_t groups;
                 int64_t area;
                 record_extent<TAIL>((uint64_t)s_vals[p], groups, area);
-                tail.group_counts[dst] = groups;
+                tail.group_counts[dst] = (uint16_t)groups;
                 area_sum += area;
             }
         }
@@ -2530,14 +2531,17 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
     // Outside AccuTile the rows that touch no tile are left out of the sort; their places at
     // the end hold filler records (row 0, no rectangle) with no groups.
     const int tail_kind = packed ? (accu ? 2 : 1) : 0;
+    // The last pass writes 16-bit group counts (packed records); order_counts_kernel
+    // writes 32-bit ones.
+    uint16_t* const counts16 = reinterpret_cast<uint16_t*>(sc.counts);
     int status;
     if (accu)
         status = gs3d::run_sort<uint32_t, uint64_t>(sc.keys, a.order, rows, 32, sc.sort, s, tail_kind,
-                                                    gs3d::OrderTail{sc.counts, sc.pairs});
+                                                    gs3d::OrderTail{counts16, sc.pairs});
     else
         status = gs3d::run_order_sort(sc.keys, a.order, rows, sc.sort, sc.live,
                                       packed ? (uint64_t)gs3d::kEmptyRect << 32 : 0u, s, tail_kind,
-                                      gs3d::OrderTail{sc.counts, sc.pairs}, true, end_bit, start_half, sc.base);
+                                      gs3d::OrderTail{counts16, sc.pairs}, true, end_bit, start_half, sc.base);
     if (status != GS3D_OK) return status;
     int64_t pair_blocks = (rows + gs3d::kSortTile - 1) / gs3d::kSortTile;
     if (!packed) {
@@ -2551,8 +2555,9 @@ extern "C" int gs3d_order_rows(const gs3d_order_args* args, void* scratch, size_
         pair_blocks = cgrid.x;
     }
     // The blocks' tile-pair sums are added up by the group-count scan's first launch.
-    status = gs3d::run_scan<int32_t, true>(sc.counts, rows, a.group_offsets, a.totals, sc.scan, s,
-                                           gs3d::SideSum{sc.pairs, pair_blocks, a.totals + 1});
+    const gs3d::SideSum pair_sum{sc.pairs, pair_blocks, a.totals + 1};
+    status = packed ? gs3d::run_scan<uint16_t, true>(counts16, rows, a.group_offsets, a.totals, sc.scan, s, pair_sum)
+                    : gs3d::run_scan<int32_t, true>(sc.counts, rows, a.group_offsets, a.totals, sc.scan, s, pair_sum);
     if (status != GS3D_OK) return status;
     return gs3d::launch_status("gs3d_order_rows");
 }
