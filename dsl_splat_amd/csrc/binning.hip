@@ -626,7 +626,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(
 // The scan is written transposed, [tile][digit], so that each scatter block
 // reads its offsets as one contiguous row.
 struct SortScratch {
-    uint32_t* counts;     // [R][tiles]
+    uint16_t* counts;     // [R][tiles], each at most kSortTile (its region keeps room for 32-bit words)
     int32_t* offsets;     // [tiles][R], the exclusive scan of counts in digit-major order
     int32_t* scan;        // the digit scan's segment prefixes [R][segments] and row totals [R]
 };
@@ -642,7 +642,7 @@ inline size_t sort_scratch_bytes(int64_t count, SortScratch* out, void* base, in
     const size_t b = align256((size_t)((segs + 1) << radix_bits) * 4);
     if (out) {
         char* p = reinterpret_cast<char*>(base);
-        out->counts = reinterpret_cast<uint32_t*>(p);
+        out->counts = reinterpret_cast<uint16_t*>(p);
         out->offsets = reinterpret_cast<int32_t*>(p + a);
         out->scan = reinterpret_cast<int32_t*>(p + 2 * a);
     }
@@ -669,7 +669,7 @@ constexpr int kRowThreads = 256;
 // row of the table resident at once (up to 1024 rows), and ITEMS (chosen
 // from the row length) puts a whole row in one chunk up to 12288 tiles.
 template <int ITEMS>
-__global__ __launch_bounds__(kRowThreads) void digit_rows_kernel(const uint32_t* __restrict__ counts, int tiles,
+__global__ __launch_bounds__(kRowThreads) void digit_rows_kernel(const uint16_t* __restrict__ counts, int tiles,
                                                                  int segs, int32_t* __restrict__ seg_prefix,
                                                                  int32_t* __restrict__ row_totals) {
     static_assert(ITEMS % 2 == 0, "two words of a segment per lane");
@@ -679,7 +679,7 @@ __global__ __launch_bounds__(kRowThreads) void digit_rows_kernel(const uint32_t*
     __shared__ uint32_t s_seg[kChunkSegs];
     const int d = blockIdx.x;
     const int lane = lane_id(), wave = threadIdx.x >> 6;
-    const uint32_t* row = counts + (int64_t)d * tiles;
+    const uint16_t* row = counts + (int64_t)d * tiles;
     int64_t carry = 0;  // wave 0: the row's sum before this chunk
     for (int c0 = 0; c0 < tiles; c0 += kChunkTiles) {
         const int w0 = c0 + wave * (ITEMS * 64) + lane;
@@ -713,7 +713,7 @@ __global__ __launch_bounds__(kRowThreads) void digit_rows_kernel(const uint32_t*
 }
 
 template <int ITEMS>
-void launch_digit_rows(int per_thread, int digits, const uint32_t* counts, int tiles, int segs, int32_t* seg_prefix,
+void launch_digit_rows(int per_thread, int digits, const uint16_t* counts, int tiles, int segs, int32_t* seg_prefix,
                        int32_t* row_totals, hipStream_t s) {
     if constexpr (ITEMS < 48) {
         if (per_thread > ITEMS)
@@ -725,7 +725,7 @@ void launch_digit_rows(int per_thread, int digits, const uint32_t* counts, int t
 
 // grid (segments, digits / kSegDigits); total_out (optional) receives the
 // sum of the table.
-__global__ __launch_bounds__(256) void digit_offsets_kernel(const uint32_t* __restrict__ counts, int64_t tiles,
+__global__ __launch_bounds__(256) void digit_offsets_kernel(const uint16_t* __restrict__ counts, int64_t tiles,
                                                             int digits, const int32_t* __restrict__ seg_prefix,
                                                             const int32_t* __restrict__ row_totals,
                                                             int32_t* __restrict__ offsets,
@@ -952,7 +952,7 @@ inline int run_order_sort(uint32_t* keys, uint64_t* values, int64_t count, void*
 
 // Histogram of TPB consecutive sort tiles per block: each digit's TPB counts
 // are consecutive in the [digit][tile] layout, so a block writes runs of TPB
-// words instead of one scattered word per digit.  One LDS histogram per tile
+// 16-bit counts instead of one scattered count per digit.  One LDS histogram per tile
 // (pitch R + 1: the transposed read is conflict-free).
 // DROP and live as in sort_scatter_kernel (tiles at or beyond live count
 // nothing, and their columns are written as zeros).  R as in
@@ -960,7 +960,7 @@ inline int run_order_sort(uint32_t* keys, uint64_t* values, int64_t count, void*
 template <class K, int RB, int TPB, bool DROP = false, int R = 1 << RB>
 __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(const K* __restrict__ keys, int64_t count,
                                                                             int shift, uint32_t mask,
-                                                                            uint32_t* __restrict__ counts,
+                                                                            uint16_t* __restrict__ counts,
                                                                             int64_t tiles, int digits,
                                                                             const int64_t* __restrict__ live_count,
                                                                             const uint32_t* __restrict__ key_base) {
@@ -1008,7 +1008,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_histogram_tiles_kernel(cons
     for (int e = threadIdx.x; e < TPB * digits; e += kSortThreads) {
         const int d = e / TPB, tt = e - d * TPB;
         const int64_t t = t0 + tt;
-        if (t < tiles) counts[(int64_t)d * tiles + t] = s_hist[tt * P + d];  // runs of TPB words
+        if (t < tiles) counts[(int64_t)d * tiles + t] = (uint16_t)s_hist[tt * P + d];  // runs of TPB counts
     }
 }
 
@@ -1017,7 +1017,7 @@ inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStre
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
     if (tiles * digits <= kSingleScanMax) {
         // Small table: scanned and written transposed by one workgroup.
-        hipLaunchKernelGGL((scan_single_kernel<uint32_t, false>), dim3(1), dim3(kSingleThreads), 0, s, sc.counts,
+        hipLaunchKernelGGL((scan_single_kernel<uint16_t, false>), dim3(1), dim3(kSingleThreads), 0, s, sc.counts,
                            tiles * digits, sc.offsets, total, (int32_t)tiles, (int32_t)digits, SideSum{});
         return launch_status("radix sort counts");
     }
@@ -1037,8 +1037,8 @@ inline int scan_counts(int64_t count, int digits, const SortScratch& sc, hipStre
 template <class K, int RB, bool DROP, int R>
 int sort_counts(const K* keys, int64_t count, int shift, uint32_t mask, int digits, const SortScratch& sc,
                 hipStream_t s, const int64_t* live, int64_t* total, const uint32_t* key_base) {
-    // Tiles per histogram block: runs of 16 words (whole 64-byte sectors) for
-    // 8-bit digits; 8 for 10-bit digits, whose LDS histograms are 4x larger.
+    // Tiles per histogram block (the length of each digit's run of counts):
+    // GS3D_HIST_TILES8 for 8-bit digits, 8 for wider ones.
     constexpr int TPB = RB > 8 ? 8 : GS3D_HIST_TILES8;
     const int64_t tiles = (count + kSortTile - 1) / kSortTile;
     hipLaunchKernelGGL((sort_histogram_tiles_kernel<K, RB, TPB, DROP, R>), dim3((unsigned)((tiles + TPB - 1) / TPB)),
@@ -1378,7 +1378,7 @@ __global__ void row_records_kernel(const float* __restrict__ depths, RowGeometry
 template <bool PACKED>
 __global__ __launch_bounds__(kSortThreads) void row_records_counted_kernel(
     const float* __restrict__ depths, RowGeometry g, int64_t rows, int gx, int gy, uint32_t* __restrict__ keys,
-    uint64_t* __restrict__ records, int32_t* __restrict__ tiles_out, uint32_t* __restrict__ counts, int64_t tiles,
+    uint64_t* __restrict__ records, int32_t* __restrict__ tiles_out, uint16_t* __restrict__ counts, int64_t tiles,
     uint32_t* __restrict__ block_range) {
     static_assert(kSortThreads == kRadix, "one digit per thread");
     __shared__ uint32_t s_hist[kRadix];
@@ -1437,7 +1437,7 @@ __global__ __launch_bounds__(kSortThreads) void row_records_counted_kernel(
         atomicMax(&s_range[1], kmax);
     }
     __syncthreads();
-    counts[(int64_t)threadIdx.x * tiles + tile] = s_hist[threadIdx.x];
+    counts[(int64_t)threadIdx.x * tiles + tile] = (uint16_t)s_hist[threadIdx.x];
     if (threadIdx.x == 0) {
         block_range[2 * tile] = s_range[0];
         block_range[2 * tile + 1] = s_range[1];
